@@ -1,0 +1,157 @@
+"""Throughput of the anchored transport score, forward + backward, on one MI355X.
+
+Workload: 1M synthetic events on a 640x480 sensor over 100 ms (50 line segments + 30% noise), a smooth random
+dense flow grid 2x480x640 (max 200 px/s), AnchoredExact with h = sigma (default 1 px), tau = 20 ms (0.2 of the
+window), cut = 3, 16 slices, every event an anchor, dequantisation jitter, smoothed anchors, exposure
+correction; backward to the flow grid.  One step = one full loss evaluation + backward, inputs resident in
+HBM.  Prints one JSON line (rank 0, N = 1) with events/s, the dominant kernel's roofline and the CPU baseline
+(the oracle's OpenMP restatement of the reference CPU path on this host's cores).
+
+    python bench.py [--steps K] [--warmup W] [--sigma S] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+VALU_PEAK = 256 * 4 * 16 * 2.4e9      # fp32 lane-slots/s (non-packed): 256 CUs x 4 SIMD x 16 lanes x 2.4 GHz
+SLOTS_FWD, SLOTS_BWD = 14, 16          # VALU lane-slots per contributing pair (forward, backward)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--sigma", type=float, default=1.0)
+    ap.add_argument("--events", type=int, default=1_000_000)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=25.0, help="seconds of CPU baseline work, at most")
+    return ap.parse_args()
+
+
+def workload(n_events, device):
+    from x_amd import synth
+    from x_amd.core import EventPacket
+    from x_amd.motion import DenseLinearFlow
+    win = synth.dense_flow_window(seed=0, n=n_events)
+    ev = EventPacket.from_window(win, device)
+    grid = win.motion["grid"]
+    motion = DenseLinearFlow(1, win.height, win.width, grid=grid.shape[-2:], init=torch.as_tensor(grid)).to(device)
+    return win, ev, motion
+
+
+def cpu_baseline(win, sigma, budget):
+    """Oracle (OpenMP restatement of the reference CPU loops + NumPy plan) on the same workload: the full
+    anchored score forward + backward, timed once after a warm-up on a subset."""
+    import oracle as O
+    H, W = win.height, win.width
+    rng = np.random.default_rng(0)
+    xs = (win.xy + rng.uniform(-0.5, 0.5, win.xy.shape)).astype(np.float32)
+    xa = (xs + sigma * rng.standard_normal(xs.shape)).astype(np.float32)
+    grid = win.motion["grid"]
+
+    def run(n):
+        sl = slice(0, n)
+        v, idx, wts = O.dense_velocity(grid, xs[sl], win.b[sl], H, W)
+        anchors = np.arange(n)
+        p = O.build_pair_plan(xs[sl], win.t[sl], v, win.b[sl], 1, H, W, anchors, sigma, 0.2, 3.0, 16,
+                              anchor_xy=xa[sl])
+        S = O.ats_pair_fwd(p, sigma, 0.2, 3.0)
+        wc = O.window_counts(win.t[sl], win.b[sl], anchors, 0.2)
+        vis = O.visible_fraction_dense(grid, xa[sl], win.t[sl], win.b[sl], win.t[sl], win.b[sl], 1, H, W, 0.2)
+        _, gS, _ = O.anchored_epilogue(S, wc, sigma, H, W, vis=vis)
+        gv = O.ats_pair_bwd(gS, p, sigma, 0.2, 3.0, n)
+        O.sample_grid_bwd(gv, idx, wts, grid.shape)
+
+    run(min(win.n, 50_000))
+    n = win.n
+    t0 = time.perf_counter()
+    run(n)
+    dt = time.perf_counter() - t0
+    if dt > budget:      # keep the baseline bounded: time a prefix of the (time-sorted) window instead
+        n = max(int(win.n * budget / dt / 2), 10_000)
+        t0 = time.perf_counter()
+        run(n)
+        dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "events/s", "cores": O.num_threads(), "kind": "port",
+            "sample": f"anchored score fwd+bwd on the first {n} events of the same window "
+                      f"(time-sorted prefix), one timed run after a 50k-event warm-up, {dt:.2f} s"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for {a.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        sys.exit(2)
+    from x_amd.objectives import AnchoredExact
+    from x_amd.ops import _ext
+    from x_amd.ops import functional as F
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    win, ev, motion = workload(a.events, dev)
+    obj = AnchoredExact(h=a.sigma, tau=0.2, cut=3.0, n_slices=16, n_anchors=None, seed=0, rng="device")
+
+    def step():
+        motion.grid.grad = None
+        out = obj(ev, motion)
+        out["loss"].backward()
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    kernels = ["atl_ats_pair_fwd", "atl_ats_pair_bwd"]
+    rec = _ext.time_kernels(kernels)
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    _ext.time_kernels(())
+    ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1 in rec[k]])) for k in kernels}
+    # contributing pairs K = sum_i n_i of one step (counted outside the timed region)
+    with torch.no_grad():
+        g = torch.Generator(device=dev).manual_seed(1)
+        xs = ev.xy + (torch.rand(ev.xy.shape, generator=g, device=dev) - 0.5)
+        xa = xs + a.sigma * torch.randn(xs.shape, generator=g, device=dev)
+        v = motion.velocity(xs, ev.t, ev.b)
+        plan = F.build_pair_plan(xs, ev.t, v, ev.b, 1, ev.height, ev.width, torch.arange(ev.n, device=dev), a.sigma,
+                                 0.2, 3.0, 16, anchor_xy=xa)
+        K = int(F.pair_counts(plan, a.sigma, 0.2, 3.0).sum())
+    dom = max(kernels, key=lambda k: ms[k])
+    slots = SLOTS_FWD if dom.endswith("fwd") else SLOTS_BWD
+    achieved = K * slots / (ms[dom] * 1e-3)
+    value = ev.n * a.steps / dt
+    line = {
+        "metric": "events/s for anchored-score fwd+bwd @1M events 640x480; % HBM/VALU roofline",
+        "value": value, "unit": "events/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": 1e3 * dt / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"anchored score fwd+bwd, {ev.n} events, 640x480, dense flow 2x480x640, "
+                               f"h={a.sigma}, tau=0.2, cut=3, S=16, all anchors",
+                   "events": ev.n, "sensor": [640, 480], "sigma": a.sigma, "tau": 0.2, "slices": 16,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "valu", "kernel": dom, "achieved": achieved / 1e12, "peak": VALU_PEAK / 1e12,
+                     "unit": "Tslot/s", "frac": achieved / VALU_PEAK, "traffic": None,
+                     "pairs": K, "slots_per_pair": slots, "kernel_ms": ms[dom]},
+        "kernel_ms": ms,
+        "pairs_per_anchor": K / ev.n,
+    }
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(win, a.sigma, a.cpu_budget)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

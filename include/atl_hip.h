@@ -1,0 +1,140 @@
+/* C-ABI of libatl_hip.so: the MI355X (gfx950) event-transport hot path of atl.
+ *
+ * Replaces the reference's pybind module (csrc/atl_cpu.cpp:299-329, declarations csrc/atl_ops.h:18-75) as the
+ * boundary under atl/ops/functional.py.  Conventions for every entry point:
+ *   - plain device pointers, sizes and a hipStream_t; kernels are launched asynchronously on that stream;
+ *   - layouts as csrc/atl_ops.h:3-14: pos (N,2) f32 [x, y], w (N) f32, b (N) int64, img (B,H,W) f32,
+ *     all contiguous;
+ *   - outputs are caller-allocated; outputs documented as "accumulated" must be zero-filled by the caller
+ *     (the reference allocates them with torch::zeros, csrc/atl_cpu.cpp:41,154,229);
+ *   - return 0 on success, non-zero on a rejected argument or launch error; atl_last_error() returns the
+ *     message (per host thread).
+ * Nothing here allocates device memory; scratch buffers are passed in by the caller.
+ */
+#ifndef ATL_HIP_H_
+#define ATL_HIP_H_
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#define ATL_HIP_ABI_VERSION 1
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+const char* atl_last_error(void);
+int atl_abi_version(void);
+
+/* ---------------------------------------------------------------- splat / gather (csrc/atl_ops.h:20-29) */
+
+/* splat_bilinear_fwd (csrc/atl_ops.h:20, csrc/atl_cpu.cpp:38-56): img[b,y,x] += w * bilinear(pos).
+ * img (B,H,W) accumulated. */
+int atl_splat_bilinear_fwd(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B, int64_t H,
+                           int64_t W, float* img, hipStream_t stream);
+/* splat_bilinear_bwd (csrc/atl_ops.h:21, csrc/atl_cpu.cpp:58-76): gpos (N,2), gw (N) written. */
+int atl_splat_bilinear_bwd(const float* gimg, const float* pos, const float* w, const int64_t* b, int64_t N,
+                           int64_t B, int64_t H, int64_t W, float* gpos, float* gw, hipStream_t stream);
+/* splat_gauss_fwd (csrc/atl_ops.h:23-24, csrc/atl_cpu.cpp:79-104): truncated Gaussian of radius R around
+ * round(pos), normalised by 2 pi sigma^2.  img accumulated. */
+int atl_splat_gauss_fwd(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B, int64_t H,
+                        int64_t W, double sigma, int64_t R, float* img, hipStream_t stream);
+/* splat_gauss_bwd (csrc/atl_ops.h:25-26, csrc/atl_cpu.cpp:106-131): gpos, gw written. */
+int atl_splat_gauss_bwd(const float* gimg, const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B,
+                        int64_t H, int64_t W, double sigma, int64_t R, float* gpos, float* gw, hipStream_t stream);
+/* gather_bilinear_fwd (csrc/atl_ops.h:28, csrc/atl_cpu.cpp:134-149): out (N) written, zero padding. */
+int atl_gather_bilinear_fwd(const float* img, const float* pos, const int64_t* b, int64_t N, int64_t B, int64_t H,
+                            int64_t W, float* out, hipStream_t stream);
+/* gather_bilinear_bwd (csrc/atl_ops.h:29, csrc/atl_cpu.cpp:151-172): gimg (B,H,W) accumulated, gpos written. */
+int atl_gather_bilinear_bwd(const float* gval, const float* img, const float* pos, const int64_t* b, int64_t N,
+                            int64_t B, int64_t H, int64_t W, float* gimg, float* gpos, hipStream_t stream);
+/* voxel_grid (csrc/atl_ops.h:49-50, csrc/atl_cpu.cpp:256-286): vox (B,C,H,W) accumulated. */
+int atl_voxel_grid(const float* pos, const float* t, const float* p, const int64_t* b, int64_t N, int64_t B,
+                   int64_t C, int64_t H, int64_t W, float* vox, hipStream_t stream);
+
+/* ---------------------------------------------------------------- flow-grid sampling */
+
+/* DenseLinearFlow.field + sample_grid (atl/motion/parametric.py:212-216, 235-251): out (N,C) written, bilinear
+ * border-clamped sample of field (B,C,Hg,Wg).  With img_h, img_w > 0 the positions are image pixels mapped by
+ * g = x / max(W-1, 1) * (Wg-1); with img_h = img_w = 0 they are grid coordinates. */
+int atl_sample_grid_fwd(const float* field, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                        const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* out, hipStream_t stream);
+/* Adjoint of atl_sample_grid_fwd w.r.t. the field (the index_put accumulate of parametric.py:247-251 under
+ * autograd): gfield (B,C,Hg,Wg) accumulated. */
+int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                        const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gfield,
+                        hipStream_t stream);
+
+/* ---------------------------------------------------------------- pair plan (atl/ops/functional.py:132-178) */
+
+/* Reductions behind the plan geometry (functional.py:139,144-145): stats (5 ints, ordered-int encoding of
+ * floats: i >= 0 ? bits = i : bits = i ^ 0x7fffffff) = [max ||v|| as sqrt(fma(vy,vy,vx*vx)), min xa.x,
+ * min xa.y, min -xa.x, min -xa.y]. */
+int atl_plan_stats(const float* v, int64_t N, const float* xa, int64_t M, int* stats, hipStream_t stream);
+/* Per-cell entry counts of the (source, slice) pairs, functional.py:150-167: counts (B*S*GH*GW) int32
+ * accumulated.  ox, oy, cell, tau are the host doubles of functional.py:139-149 (rounded to fp32 inside). */
+int atl_plan_count(const float* x, const float* t, const float* v, const int64_t* b, int64_t N, int64_t B,
+                   double ox, double oy, double cell, double tau, int64_t S, int64_t GH, int64_t GW, int* counts,
+                   hipStream_t stream);
+/* start (n+1) int64 = [0, cumsum(counts)] (functional.py:168); work holds atl_scan_work_size(n) int64. */
+int atl_scan_counts(const int* counts, int64_t n, int64_t* start, int64_t* work, hipStream_t stream);
+int64_t atl_scan_work_size(int64_t n);
+int atl_fill_i32(int* p, int64_t n, int value, hipStream_t stream);
+/* Scatter of the plan entries into CSR order (functional.py:163-165, 176): cursor (ncell) zero-filled.
+ * Entry order inside one cell is unspecified, as with the reference's torch.argsort. */
+int atl_plan_fill(const float* x, const float* t, const float* v, const int64_t* b, int64_t N, int64_t B,
+                  double ox, double oy, double cell, double tau, int64_t S, int64_t GH, int64_t GW,
+                  const int64_t* start, int* cursor, float* src_y, float* src_v, float* src_t, int64_t* src_id,
+                  hipStream_t stream);
+/* Anchor fields of the plan (functional.py:169-177): anc_x (M,2), anc_t (M), anc_cell (M,3), anc_id (M).
+ * anchor_xy may be null (positions x[anchors]). */
+int atl_plan_anchors(const float* x, const float* t, const int64_t* b, const int64_t* anchors,
+                     const float* anchor_xy, int64_t M, int64_t N, double ox, double oy, double cell, int64_t S,
+                     int64_t GH, int64_t GW, float* anc_x, float* anc_t, int64_t* anc_cell, int64_t* anc_id,
+                     hipStream_t stream);
+
+/* ---------------------------------------------------------------- pair sums over a reference-layout plan */
+
+/* ats_pair_fwd (csrc/atl_ops.h:31-42, csrc/atl_cpu.cpp:203-222): out (M) written.  E = number of plan
+ * entries, ncell = B*S*GH*GW (cell_start has ncell+1 entries).  count (M) int32 receives n_i, the number of
+ * visited pairs of each anchor, when non-null (not output by the reference). */
+int atl_ats_pair_fwd(const float* src_y, const float* src_v, const float* src_t, const int64_t* src_id,
+                     const int64_t* cell_start, int64_t E, int64_t ncell, const float* anc_x, const float* anc_t,
+                     const int64_t* anc_cell, const int64_t* anc_id, int64_t M, const float* slice_c, int64_t S,
+                     int64_t GH, int64_t GW, double h, double tau, double cut, float* out, int* count,
+                     hipStream_t stream);
+/* ats_pair_bwd (csrc/atl_ops.h:43-47, csrc/atl_cpu.cpp:224-253): gv (N,2) accumulated. */
+int atl_ats_pair_bwd(const float* gS, const float* src_y, const float* src_v, const float* src_t,
+                     const int64_t* src_id, const int64_t* cell_start, int64_t E, int64_t ncell, const float* anc_x,
+                     const float* anc_t, const int64_t* anc_cell, const int64_t* anc_id, int64_t M,
+                     const float* slice_c, int64_t S, int64_t GH, int64_t GW, double h, double tau, double cut,
+                     int64_t N, float* gv, hipStream_t stream);
+
+/* ---------------------------------------------------------------- anchored-score pieces */
+
+/* window_counts (atl/ops/functional.py:210-217): out (M) written.  Requires keys b*4 + t ascending in event
+ * order (the EventPacket invariant, atl/core/events.py:11-12); atl_check_sorted tests it (flag = 1 if not). */
+int atl_window_counts(const float* t, const int64_t* b, int64_t N, const int64_t* idx, int64_t M, double tau,
+                      float* out, hipStream_t stream);
+int atl_check_sorted(const float* t, const int64_t* b, int64_t N, int* flag, hipStream_t stream);
+/* Per-batch event counts in n_check time bins (atl/objectives/ats.py:39-41): counts (B, n_check) f32
+ * accumulated. */
+int atl_bin_counts(const float* t, const int64_t* b, int64_t N, int64_t B, int64_t n_check, float* counts,
+                   hipStream_t stream);
+/* visible_fraction for linear motion (atl/objectives/ats.py:31-50): anchors xa (M,2) with velocities va (M,2)
+ * transported to the bin centres (n_check floats), out (M) written. */
+int atl_visible_fraction(const float* xa, const float* va, const float* ta, const int64_t* ba, int64_t M,
+                         const float* counts, const float* centres, int64_t B, int64_t n_check, double tau,
+                         int64_t H, int64_t W, float* out, hipStream_t stream);
+/* Log-score epilogue (atl/objectives/ats.py:92-96): ls = log(eps + S / D), D = max(wc,1) * vis * 2 pi h^2
+ * (vis may be null); q = eps + S/D and D are saved for atl_anchored_epilogue_bwd: gS = (g / q) / D. */
+int atl_anchored_epilogue_fwd(const float* S, const float* wc, const float* vis, int64_t M, double h,
+                              double eps, float* ls, float* q, float* D, hipStream_t stream);
+int atl_anchored_epilogue_bwd(const float* g, const float* q, const float* D, int64_t M, float* gS,
+                              hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATL_HIP_H_ */

@@ -1,0 +1,259 @@
+"""HIP kernels against the oracle on identical seeded inputs (the reference's tests/test_ops.py, on the GPU).
+
+Bars: integer outputs (cell bins, keys, CSR offsets, neighbour counts, window counts) bit-exact; values
+computed in the same fp32 order bit-exact where no atomics reorder sums; forward values within 1e-5
+relative; gradients within 1e-4 relative (to the largest magnitude, as gradient sums cancel)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from tests.conftest import rand_events
+from x_amd import synth
+from x_amd.ops import functional as F
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+F32 = np.float32
+
+
+def T(a, dev=DEV):
+    return torch.as_tensor(np.ascontiguousarray(a), device=dev)
+
+
+def N(t):
+    return t.detach().cpu().numpy()
+
+
+def close_rel(got, want, rel, floor=0.0):
+    """|got - want| <= rel * max(|want|) elementwise (plus an absolute floor)."""
+    scale = max(float(np.abs(want).max()), 1e-30)
+    err = float(np.abs(got.astype(np.float64) - want.astype(np.float64)).max()) if want.size else 0.0
+    assert err <= rel * scale + floor, f"max err {err:.3e} vs scale {scale:.3e} (rel {err / scale:.2e})"
+
+
+# ------------------------------------------------------------------------------------------- splat / gather
+@pytest.mark.parametrize("kernel", ["bilinear", "gauss"])
+def test_splat_matches_oracle(kernel):
+    pos, w, b, _ = rand_events(n=5000, seed=0)
+    B, H, W = 2, 20, 24
+    p = T(pos).requires_grad_(True)
+    wt = T(w).requires_grad_(True)
+    out = F.splat(p, wt, T(b), B, H, W, kernel=kernel, sigma=1.3)
+    if kernel == "bilinear":
+        ref = O.splat_bilinear_fwd(pos, w, b, B, H, W)
+    else:
+        ref = O.splat_gauss_fwd(pos, w, b, B, H, W, 1.3, int(math.ceil(3 * 1.3)))
+    close_rel(N(out), ref, 1e-5)
+    g = np.random.default_rng(1).standard_normal(ref.shape).astype(F32)
+    (out * T(g)).sum().backward()
+    if kernel == "bilinear":
+        gp, gw = O.splat_bilinear_bwd(g, pos, w, b)
+        assert np.array_equal(N(wt.grad), gw) and np.array_equal(N(p.grad), gp)   # same fp32 order, no atomics
+    else:
+        gp, gw = O.splat_gauss_bwd(g, pos, w, b, 1.3, 4)
+        close_rel(N(wt.grad), gw, 1e-5)
+        close_rel(N(p.grad), gp, 1e-4)
+
+
+def test_gather_matches_oracle():
+    pos, _, b, _ = rand_events(n=5000, seed=2)
+    img = np.random.default_rng(3).standard_normal((2, 20, 24)).astype(F32)
+    ti = T(img).requires_grad_(True)
+    tp = T(pos).requires_grad_(True)
+    out = F.gather(ti, tp, T(b))
+    assert np.array_equal(N(out), O.gather_bilinear_fwd(img, pos, b))
+    g = np.random.default_rng(4).standard_normal(5000).astype(F32)
+    out.backward(T(g))
+    gimg, gp = O.gather_bilinear_bwd(g, img, pos, b)
+    assert np.array_equal(N(tp.grad), gp)
+    close_rel(N(ti.grad), gimg, 1e-5)
+
+
+def test_voxel_matches_oracle():
+    pos, _, b, t = rand_events(n=5000, seed=5)
+    p = np.where(np.random.default_rng(6).random(5000) > 0.5, 1.0, -1.0).astype(F32)
+    got = F.voxel_grid(T(pos), T(t), T(p), T(b), 2, 5, 20, 24, normalize=None)
+    close_rel(N(got), O.voxel_grid(pos, t, p, b, 2, 5, 20, 24), 1e-5)
+
+
+def test_plumbing_translation_splat_gather_fwd_bwd():
+    """100k events at 240x180, translation (2.0, -1.25) px/window: warp to t_ref = 0, splat, gather back."""
+    win = synth.plumbing_translation(seed=0)
+    th = win.motion["theta"]
+    xy = win.xy + th[None, :] * (F32(0.0) - win.t)[:, None]
+    xy = xy.astype(F32)
+    w = np.ones(win.n, F32)
+    b = win.b
+    tp = T(xy).requires_grad_(True)
+    img = F.splat(tp, T(w), T(b), 1, 180, 240)
+    ref_img = O.splat_bilinear_fwd(xy, w, b, 1, 180, 240)
+    close_rel(N(img), ref_img, 1e-5)
+    val = F.gather(img, tp, T(b))
+    close_rel(N(val), O.gather_bilinear_fwd(ref_img, xy, b), 1e-5)
+    val.sum().backward()
+    # d(sum gather(splat(pos), pos))/dpos = gather-pos-grad(1) + splat-pos-grad(gather-img-grad(1))
+    gimg, gp1 = O.gather_bilinear_bwd(np.ones(win.n, F32), ref_img, xy, b)
+    gp2, _ = O.splat_bilinear_bwd(gimg, xy, w, b)
+    close_rel(N(tp.grad), gp1 + gp2, 1e-4)
+
+
+# ------------------------------------------------------------------------------------------- flow grid
+def test_sample_grid_matches_oracle():
+    win = synth.small_window(seed=7, n=3000, B=2)
+    grid = win.motion["grid"]
+    H, W = win.height, win.width
+    tg = T(grid).requires_grad_(True)
+    v = F.sample_grid_hip(tg, T(win.xy), T(win.b), img_hw=(H, W))
+    want, idx, wts = O.dense_velocity(grid, win.xy, win.b, H, W)
+    assert np.array_equal(N(v), want)
+    g = np.random.default_rng(8).standard_normal(want.shape).astype(F32)
+    v.backward(T(g))
+    close_rel(N(tg.grad), O.sample_grid_bwd(g, idx, wts, grid.shape), 1e-5)
+
+
+# ------------------------------------------------------------------------------------------- pair plan + sums
+def _pair_case(seed=0, n=6000, B=2, H=40, W=48, h=1.0):
+    win = synth.small_window(seed=seed, n=n // B, H=H, W=W, B=B)
+    v, _, _ = O.dense_velocity(win.motion["grid"], win.xy, win.b, H, W)
+    rng = np.random.default_rng(seed + 100)
+    xs = (win.xy + rng.uniform(-0.5, 0.5, win.xy.shape)).astype(F32)
+    anchors = np.arange(win.n)
+    xa = (xs + h * rng.standard_normal(xs.shape)).astype(F32)
+    return win, xs, v, anchors, xa
+
+
+def _cellwise_sorted(keys, ids):
+    order = np.lexsort((ids, keys))
+    return keys[order], ids[order], order
+
+
+@pytest.mark.parametrize("tau,S,h", [(0.2, 16, 1.0), (1.0, 8, 1.5), (0.05, 4, 0.5)])
+def test_plan_bit_exact(tau, S, h):
+    win, xs, v, anchors, xa = _pair_case(seed=1, h=h)
+    p = O.build_pair_plan(xs, win.t, v, win.b, 2, 40, 48, anchors, h, tau, 3.0, S, anchor_xy=xa)
+    q = F.build_pair_plan(T(xs), T(win.t), T(v), T(win.b), 2, 40, 48, T(anchors), h, tau, 3.0, S, anchor_xy=T(xa))
+    assert (q.GH, q.GW, q.S) == (p["GH"], p["GW"], p["S"])
+    assert q.geometry["cell"] == p["geometry"]["cell"] and q.geometry["ox"] == p["geometry"]["ox"]
+    assert np.array_equal(N(q.cell_start), p["cell_start"])
+    # entries: same (key, source) multiset, same slice-centre positions
+    cs = N(q.cell_start)
+    qkey = np.repeat(np.arange(cs.shape[0] - 1), np.diff(cs))
+    k1, i1, o1 = _cellwise_sorted(qkey, N(q.src_id))
+    k2, i2, o2 = _cellwise_sorted(p["key"], p["src_id"])
+    assert np.array_equal(k1, k2) and np.array_equal(i1, i2)
+    assert np.array_equal(N(q.src_y)[o1], p["src_y"][o2])
+    assert np.array_equal(N(q.src_v)[o1], p["src_v"][o2])
+    assert np.array_equal(N(q.src_t)[o1], p["src_t"][o2])
+    for f in ("anc_x", "anc_t", "anc_cell", "anc_id", "slice_c"):
+        assert np.array_equal(N(getattr(q, f)), p[f]), f
+
+
+@pytest.mark.parametrize("tau,S,h", [(0.2, 16, 1.0), (1.0, 8, 1.5), (0.05, 4, 0.5)])
+def test_pair_sums_match_oracle(tau, S, h):
+    win, xs, v, anchors, xa = _pair_case(seed=2, h=h)
+    p = O.build_pair_plan(xs, win.t, v, win.b, 2, 40, 48, anchors, h, tau, 3.0, S, anchor_xy=xa)
+    want, wcnt = O.ats_pair_fwd(p, h, tau, 3.0, with_counts=True)
+    tv = T(v).requires_grad_(True)
+    q = F.build_pair_plan(T(xs), T(win.t), tv, T(win.b), 2, 40, 48, T(anchors), h, tau, 3.0, S, anchor_xy=T(xa))
+    Sg = F._ATSPair.apply(tv, q, h, tau, 3.0)
+    assert np.array_equal(N(F.pair_counts(q, h, tau, 3.0)), wcnt)
+    close_rel(N(Sg), want, 1e-5)
+    assert np.allclose(N(Sg), want, rtol=1e-5, atol=1e-6)
+    gS = np.random.default_rng(3).standard_normal(len(anchors)).astype(F32)
+    Sg.backward(T(gS))
+    close_rel(N(tv.grad), O.ats_pair_bwd(gS, p, h, tau, 3.0, win.n), 1e-4)
+
+
+def test_ats_pair_sums_api_matches_bruteforce():
+    """Reference test_ats_pair_matches_bruteforce (tests/test_ops.py:62-77) on the device: plan + kernel vs the
+    O(MN) brute force, values and gradients."""
+    pos, _, b, t = rand_events(n=600, seed=3)
+    rng = np.random.default_rng(1)
+    v = (rng.standard_normal((600, 2)) * 6).astype(F32)
+    anchors = np.arange(0, 600, 3)
+    for tau, S in [(1.0, 8), (0.2, 16), (0.05, 4)]:
+        tv = T(v).requires_grad_(True)
+        s_ext = F.ats_pair_sums(T(pos), T(t), tv, T(b), 2, 20, 24, T(anchors), 1.5, tau, cut=3.0, n_slices=S)
+        Sb, _, grad = O.pair_sums_fp64(pos, t, v, b, anchors, 1.5, tau, 3.0)
+        assert np.allclose(N(s_ext), Sb, atol=1e-4, rtol=1e-4)
+        gS = rng.standard_normal(len(anchors)).astype(F32)
+        s_ext.backward(T(gS))
+        assert np.allclose(N(tv.grad), grad(gS), atol=1e-4, rtol=1e-3)
+
+
+# ------------------------------------------------------------------------------------------- anchored pieces
+def test_window_counts_bit_exact():
+    _, _, b, t = rand_events(n=20000, B=3, seed=4)
+    idx = np.arange(0, 20000, 3)
+    for tau in (0.01, 0.2, 1.0):
+        got = F.window_counts(T(t), T(b), T(idx), tau)
+        assert np.array_equal(N(got), O.window_counts(t, b, idx, tau))
+    got = F.window_counts(T(np.array([0.0, 0.1, 0.2, 0.9, 0.0, 0.5], F32)), T(np.array([0, 0, 0, 0, 1, 1])),
+                          T(np.arange(6)), 0.15)
+    assert N(got).tolist() == [1, 2, 1, 0, 0, 0]
+    perm = np.random.default_rng(5).permutation(20000)          # unsorted input is sorted first
+    got = F.window_counts(T(t[perm]), T(b[perm]), T(idx), 0.2)
+    assert np.array_equal(N(got), O.window_counts(t[perm], b[perm], idx, 0.2))
+
+
+def test_visible_fraction_bit_exact():
+    win, xs, v, anchors, xa = _pair_case(seed=6)
+    grid = win.motion["grid"]
+    va, _, _ = O.dense_velocity(grid, xa, win.b[anchors], 40, 48)
+    got = F.visible_fraction_linear(T(xa), T(va), T(win.t[anchors]), T(win.b[anchors]), T(win.t), T(win.b), 2, 40,
+                                    48, 0.2)
+    want = O.visible_fraction_dense(grid, xa, win.t[anchors], win.b[anchors], win.t, win.b, 2, 40, 48, 0.2)
+    assert np.array_equal(N(got), want)
+
+
+def test_anchored_exact_end_to_end():
+    """AnchoredExact (dense linear flow) log scores and flow-grid gradient vs the oracle pipeline."""
+    from x_amd.core import EventPacket
+    from x_amd.motion import DenseLinearFlow
+    from x_amd.objectives import AnchoredExact
+    win = synth.small_window(seed=8, n=4000, B=2)
+    H, W = win.height, win.width
+    ev = EventPacket.from_window(win, DEV)
+    grid = win.motion["grid"]
+    m = DenseLinearFlow(2, H, W, grid=grid.shape[-2:], init=torch.as_tensor(grid)).to(DEV)
+    obj = AnchoredExact(h=1.0, tau=0.2, n_anchors=None, seed=0, n_slices=16)
+    ls, anchors = obj.log_scores(ev, m)
+    (-ls.mean()).backward()
+    # oracle: same draws (CPU generator, same order), then the plan, pair sums, counts, visibility, epilogue
+    g = torch.Generator().manual_seed(0)
+    xs = win.xy + (torch.rand(win.xy.shape, generator=g).numpy() - F32(0.5))
+    xa = xs + F32(1.0) * torch.randn(xs.shape, generator=g).numpy()
+    v, idx, wts = O.dense_velocity(grid, xs, win.b, H, W)
+    p = O.build_pair_plan(xs, win.t, v, win.b, 2, H, W, np.arange(win.n), 1.0, 0.2, 3.0, 16, anchor_xy=xa)
+    Sv = O.ats_pair_fwd(p, 1.0, 0.2, 3.0)
+    wc = O.window_counts(win.t, win.b, np.arange(win.n), 0.2)
+    vis = O.visible_fraction_dense(grid, xa, win.t, win.b, win.t, win.b, 2, H, W, 0.2)
+    want, gS, _ = O.anchored_epilogue(Sv, wc, 1.0, H, W, vis=vis)
+    close_rel(N(ls), want, 1e-5)
+    gv = O.ats_pair_bwd(gS, p, 1.0, 0.2, 3.0, win.n)
+    ggrid = O.sample_grid_bwd(gv, idx, wts, grid.shape)
+    close_rel(N(m.grid.grad), ggrid, 1e-4)
+
+
+# ------------------------------------------------------------------------------------------- full size
+def test_full_size_splat_gather_properties():
+    """1M events at 640x480 (dense flow, warp to t_ref = 0.5): mass conservation of the splat and the adjoint
+    identities <splat(w), G> = <w, gather(G)> and splat_bwd.gw = gather_fwd at the same positions."""
+    win = synth.dense_flow_window(seed=0)
+    grid = T(win.motion["grid"])
+    xy, t, b = T(win.xy), T(win.t), T(win.b)
+    v = F.sample_grid_hip(grid, xy, b, img_hw=(480, 640))
+    pos = xy + v * (0.5 - t)[:, None]
+    inside = ((pos[:, 0] >= 0) & (pos[:, 0] <= 639) & (pos[:, 1] >= 0) & (pos[:, 1] <= 479)).float()
+    img = F.splat(pos, inside, b, 1, 480, 640)
+    assert abs(float(img.double().sum()) - float(inside.double().sum())) < 1e-6 * win.n + 1.0
+    G = torch.randn(1, 480, 640, device=DEV)
+    val = F.gather(G, pos, b)
+    lhs = float((img.double() * G.double()).sum())
+    rhs = float((inside.double() * val.double()).sum())
+    assert abs(lhs - rhs) < 1e-4 * (abs(lhs) + float(inside.sum()))
+    _, gw = F.get_ext().splat_bilinear_bwd(G.contiguous(), pos.contiguous(), inside.contiguous(), b)
+    assert torch.equal(gw, val)

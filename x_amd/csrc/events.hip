@@ -1,0 +1,408 @@
+// Event <-> image kernels for gfx950: bilinear splat / gather (fwd + bwd), truncated-Gaussian splat
+// (fwd + bwd), trilinear voxel grid, and the border-clamped flow-grid sampler of DenseLinearFlow (fwd + bwd).
+//
+// Semantics follow the reference's CPU loops (csrc/atl_cpu.cpp, cited per kernel); float expressions are
+// evaluated in the same order and this file is compiled with -ffp-contract=off, so corner indices and
+// weights are bit-identical to the reference's fp32 arithmetic.  Outputs that accumulate (splatted images,
+// image gradients, grid gradients) are accumulated into caller-zeroed buffers with hardware float atomics.
+#include "common.h"
+#include "../../include/atl_hip.h"
+
+#include <cmath>
+
+using namespace atlhip;
+
+namespace {
+
+// In-image corners of floor(x), floor(y): csrc/atl_cpu.cpp:17-33.  f(pixel offset, c, dc/dx, dc/dy).
+// The float range test before the integer conversion rejects NaN and coordinates too large for int.
+template <typename F>
+__device__ __forceinline__ void for_corners(float x, float y, int H, int W, F&& f) {
+  const float fx = floorf(x), fy = floorf(y);
+  if (!(fx >= -1.f && fx <= (float)(W - 1) && fy >= -1.f && fy <= (float)(H - 1))) return;
+  const int x0 = (int)fx, y0 = (int)fy;
+  const float ax = x - fx, ay = y - fy;
+  const float wx0 = 1.f - ax, wy0 = 1.f - ay;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int yy = y0 + j;
+    if (yy < 0 || yy >= H) continue;
+    const float wy = j ? ay : wy0;
+    const float dwy = j ? 1.f : -1.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int xx = x0 + i;
+      if (xx < 0 || xx >= W) continue;
+      const float wx = i ? ax : wx0;
+      const float dwx = i ? 1.f : -1.f;
+      f(yy * W + xx, wx * wy, dwx * wy, wx * dwy);
+    }
+  }
+}
+
+__device__ __forceinline__ bool batch_ok(int64_t b, int64_t B) { return b >= 0 && b < B; }
+
+// csrc/atl_cpu.cpp:38-56
+__global__ void __launch_bounds__(kBlock) k_splat_bilinear_fwd(const float2* __restrict__ pos,
+                                                               const float* __restrict__ w,
+                                                               const int64_t* __restrict__ bidx, int64_t N, int64_t B,
+                                                               int H, int W, float* __restrict__ img) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const float wn = w[n];
+  const int64_t b = bidx[n];
+  if (wn == 0.f || !batch_ok(b, B)) return;
+  float* base = img + b * (int64_t)H * W;
+  const float2 p = pos[n];
+  for_corners(p.x, p.y, H, W, [&](int off, float c, float, float) { atomicAdd(base + off, wn * c); });
+}
+
+// csrc/atl_cpu.cpp:58-76
+__global__ void __launch_bounds__(kBlock) k_splat_bilinear_bwd(const float* __restrict__ gimg,
+                                                               const float2* __restrict__ pos,
+                                                               const float* __restrict__ w,
+                                                               const int64_t* __restrict__ bidx, int64_t N, int64_t B,
+                                                               int H, int W, float2* __restrict__ gpos,
+                                                               float* __restrict__ gw) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  float sx = 0.f, sy = 0.f, sw = 0.f;
+  if (batch_ok(b, B)) {
+    const float* base = gimg + b * (int64_t)H * W;
+    const float2 p = pos[n];
+    for_corners(p.x, p.y, H, W, [&](int off, float c, float dcx, float dcy) {
+      const float g = base[off];
+      sw += g * c;
+      sx += g * dcx;
+      sy += g * dcy;
+    });
+  }
+  const float wn = w[n];
+  gw[n] = sw;
+  gpos[n] = make_float2(wn * sx, wn * sy);
+}
+
+// csrc/atl_cpu.cpp:134-149
+__global__ void __launch_bounds__(kBlock) k_gather_bilinear_fwd(const float* __restrict__ img,
+                                                                const float2* __restrict__ pos,
+                                                                const int64_t* __restrict__ bidx, int64_t N,
+                                                                int64_t B, int H, int W, float* __restrict__ out) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  float s = 0.f;
+  if (batch_ok(b, B)) {
+    const float* base = img + b * (int64_t)H * W;
+    const float2 p = pos[n];
+    for_corners(p.x, p.y, H, W, [&](int off, float c, float, float) { s += c * base[off]; });
+  }
+  out[n] = s;
+}
+
+// csrc/atl_cpu.cpp:151-172
+__global__ void __launch_bounds__(kBlock) k_gather_bilinear_bwd(const float* __restrict__ gval,
+                                                                const float* __restrict__ img,
+                                                                const float2* __restrict__ pos,
+                                                                const int64_t* __restrict__ bidx, int64_t N,
+                                                                int64_t B, int H, int W, float* __restrict__ gimg,
+                                                                float2* __restrict__ gpos) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  const float g = gval[n];
+  float sx = 0.f, sy = 0.f;
+  if (batch_ok(b, B)) {
+    const int64_t plane = b * (int64_t)H * W;
+    const float2 p = pos[n];
+    for_corners(p.x, p.y, H, W, [&](int off, float c, float dcx, float dcy) {
+      const float v = img[plane + off];
+      sx += dcx * v;
+      sy += dcy * v;
+      if (g != 0.f) atomicAdd(gimg + plane + off, g * c);
+    });
+  }
+  gpos[n] = make_float2(g * sx, g * sy);
+}
+
+// Truncated Gaussian around (lround(x), lround(y)), csrc/atl_cpu.cpp:79-104.
+__global__ void __launch_bounds__(kBlock) k_splat_gauss_fwd(const float2* __restrict__ pos,
+                                                            const float* __restrict__ w,
+                                                            const int64_t* __restrict__ bidx, int64_t N, int64_t B,
+                                                            int H, int W, float inv2s2, float norm, int R,
+                                                            float* __restrict__ img) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const float wn = w[n] * norm;
+  const int64_t b = bidx[n];
+  if (wn == 0.f || !batch_ok(b, B)) return;
+  const float2 p = pos[n];
+  const float rx = roundf(p.x), ry = roundf(p.y);
+  if (!(rx >= (float)(-R) && rx <= (float)(W - 1 + R) && ry >= (float)(-R) && ry <= (float)(H - 1 + R))) return;
+  const int cx = (int)rx, cy = (int)ry;
+  float* base = img + b * (int64_t)H * W;
+  const int ylo = max(cy - R, 0), yhi = min(cy + R, H - 1);
+  const int xlo = max(cx - R, 0), xhi = min(cx + R, W - 1);
+  for (int yy = ylo; yy <= yhi; ++yy) {
+    const float dy = (float)yy - p.y;
+    for (int xx = xlo; xx <= xhi; ++xx) {
+      const float dx = (float)xx - p.x;
+      atomicAdd(base + yy * W + xx, wn * expf(-(dx * dx + dy * dy) * inv2s2));
+    }
+  }
+}
+
+// csrc/atl_cpu.cpp:106-131
+__global__ void __launch_bounds__(kBlock) k_splat_gauss_bwd(const float* __restrict__ gimg,
+                                                            const float2* __restrict__ pos,
+                                                            const float* __restrict__ w,
+                                                            const int64_t* __restrict__ bidx, int64_t N, int64_t B,
+                                                            int H, int W, float inv2s2, float norm, float s2, int R,
+                                                            float2* __restrict__ gpos, float* __restrict__ gw) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  const float2 p = pos[n];
+  float sw = 0.f, sx = 0.f, sy = 0.f;
+  const float rx = roundf(p.x), ry = roundf(p.y);
+  if (batch_ok(b, B) &&
+      rx >= (float)(-R) && rx <= (float)(W - 1 + R) && ry >= (float)(-R) && ry <= (float)(H - 1 + R)) {
+    const int cx = (int)rx, cy = (int)ry;
+    const float* base = gimg + b * (int64_t)H * W;
+    const int ylo = max(cy - R, 0), yhi = min(cy + R, H - 1);
+    const int xlo = max(cx - R, 0), xhi = min(cx + R, W - 1);
+    for (int yy = ylo; yy <= yhi; ++yy) {
+      const float dy = (float)yy - p.y;
+      for (int xx = xlo; xx <= xhi; ++xx) {
+        const float dx = (float)xx - p.x;
+        const float gk = norm * expf(-(dx * dx + dy * dy) * inv2s2) * base[yy * W + xx];
+        sw += gk;
+        sx += gk * dx / s2;
+        sy += gk * dy / s2;
+      }
+    }
+  }
+  const float wn = w[n];
+  gw[n] = sw;
+  gpos[n] = make_float2(wn * sx, wn * sy);
+}
+
+// Trilinear polarity voting, csrc/atl_cpu.cpp:256-286.
+__global__ void __launch_bounds__(kBlock) k_voxel_grid(const float2* __restrict__ pos, const float* __restrict__ t,
+                                                       const float* __restrict__ pol,
+                                                       const int64_t* __restrict__ bidx, int64_t N, int64_t B, int C,
+                                                       int H, int W, float* __restrict__ vox) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  if (!batch_ok(b, B)) return;
+  const float2 p = pos[n];
+  const float tn = t[n] * (float)(C - 1);
+  const float fx = floorf(p.x), fy = floorf(p.y), ft = floorf(tn);
+  if (!(fx >= -1.f && fx <= (float)(W - 1) && fy >= -1.f && fy <= (float)(H - 1) && ft >= -1.f &&
+        ft <= (float)(C - 1)))
+    return;
+  const int x0 = (int)fx, y0 = (int)fy, t0 = (int)ft;
+  const float pn = pol[n];
+  for (int dt = 0; dt < 2; ++dt) {
+    const int tt = t0 + dt;
+    if (tt < 0 || tt >= C) continue;
+    const float wt = 1.f - fabsf((float)tt - tn);
+    for (int dy = 0; dy < 2; ++dy) {
+      const int yy = y0 + dy;
+      if (yy < 0 || yy >= H) continue;
+      const float wy = 1.f - fabsf((float)yy - p.y);
+      for (int dx = 0; dx < 2; ++dx) {
+        const int xx = x0 + dx;
+        if (xx < 0 || xx >= W) continue;
+        const float wx = 1.f - fabsf((float)xx - p.x);
+        atomicAdd(vox + ((b * C + tt) * (int64_t)H + yy) * W + xx, pn * wt * wy * wx);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------- flow grid
+// DenseLinearFlow.field + sample_grid (atl/motion/parametric.py:212-216, 235-251): grid coordinates
+// gx = x / sx * (Wg - 1) with sx = max(W - 1, 1) (when `scale` is set; raw grid coordinates otherwise),
+// border clamp, corners (y0, x0) .. (y1, x1) with x0 <= Wg - 2, fixed sum order c00 + c01 + c10 + c11.
+struct GridCorners {
+  int o00, o01, o10, o11;      // offsets inside one (Hg, Wg) plane
+  float w00, w01, w10, w11;
+};
+
+__device__ __forceinline__ GridCorners grid_corners(float x, float y, int Hg, int Wg, float sxw, float syh,
+                                                    bool scale) {
+  float gx = x, gy = y;
+  if (scale) {
+    gx = x / sxw * (float)(Wg - 1);
+    gy = y / syh * (float)(Hg - 1);
+  }
+  gx = fminf(fmaxf(gx, 0.f), (float)(Wg - 1));   // clamp(0, Wg-1); NaN stays NaN as in torch.clamp
+  gy = fminf(fmaxf(gy, 0.f), (float)(Hg - 1));
+  if (gx != gx) gx = 0.f;
+  if (gy != gy) gy = 0.f;
+  const float x0 = fminf(floorf(gx), (float)max(Wg - 2, 0));
+  const float y0 = fminf(floorf(gy), (float)max(Hg - 2, 0));
+  const float ax = gx - x0, ay = gy - y0;
+  const int ix0 = (int)x0, iy0 = (int)y0;
+  const int ix1 = min(ix0 + 1, Wg - 1), iy1 = min(iy0 + 1, Hg - 1);
+  GridCorners c;
+  c.o00 = iy0 * Wg + ix0;
+  c.o01 = iy0 * Wg + ix1;
+  c.o10 = iy1 * Wg + ix0;
+  c.o11 = iy1 * Wg + ix1;
+  c.w00 = (1.f - ax) * (1.f - ay);
+  c.w01 = ax * (1.f - ay);
+  c.w10 = (1.f - ax) * ay;
+  c.w11 = ax * ay;
+  return c;
+}
+
+__global__ void __launch_bounds__(kBlock) k_sample_grid_fwd(const float* __restrict__ field, int64_t B, int C,
+                                                            int Hg, int Wg, const float2* __restrict__ pos,
+                                                            const int64_t* __restrict__ bidx, int64_t N, float sxw,
+                                                            float syh, int scale, float* __restrict__ out) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  float* o = out + n * C;
+  if (!batch_ok(b, B)) {
+    for (int c = 0; c < C; ++c) o[c] = 0.f;
+    return;
+  }
+  const float2 p = pos[n];
+  const GridCorners g = grid_corners(p.x, p.y, Hg, Wg, sxw, syh, scale != 0);
+  const int64_t plane = (int64_t)Hg * Wg;
+  const float* f = field + b * C * plane;
+  for (int c = 0; c < C; ++c) {
+    const float* fc = f + c * plane;
+    float v = fc[g.o00] * g.w00;
+    v = v + fc[g.o01] * g.w01;
+    v = v + fc[g.o10] * g.w10;
+    v = v + fc[g.o11] * g.w11;
+    o[c] = v;
+  }
+}
+
+__global__ void __launch_bounds__(kBlock) k_sample_grid_bwd(const float* __restrict__ gout, int64_t B, int C,
+                                                            int Hg, int Wg, const float2* __restrict__ pos,
+                                                            const int64_t* __restrict__ bidx, int64_t N, float sxw,
+                                                            float syh, int scale, float* __restrict__ gfield) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  if (!batch_ok(b, B)) return;
+  const float2 p = pos[n];
+  const GridCorners g = grid_corners(p.x, p.y, Hg, Wg, sxw, syh, scale != 0);
+  const int64_t plane = (int64_t)Hg * Wg;
+  float* f = gfield + b * C * plane;
+  for (int c = 0; c < C; ++c) {
+    const float go = gout[n * C + c];
+    if (go == 0.f) continue;
+    float* fc = f + c * plane;
+    atomicAdd(fc + g.o00, go * g.w00);
+    atomicAdd(fc + g.o01, go * g.w01);
+    atomicAdd(fc + g.o10, go * g.w10);
+    atomicAdd(fc + g.o11, go * g.w11);
+  }
+}
+
+bool dims_ok(int64_t H, int64_t W) { return H > 0 && W > 0 && H * W < (int64_t)1 << 31; }
+
+}  // namespace
+
+// ================================================================================================ C-ABI
+extern "C" {
+
+int atl_splat_bilinear_fwd(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B, int64_t H,
+                           int64_t W, float* img, hipStream_t stream) {
+  if (N < 0 || B < 0 || !dims_ok(H, W)) { set_error("splat_bilinear_fwd: bad sizes N=%lld B=%lld H=%lld W=%lld", (long long)N, (long long)B, (long long)H, (long long)W); return 1; }
+  if (N == 0 || B == 0) return 0;
+  hipLaunchKernelGGL(k_splat_bilinear_fwd, dim3(grid_for(N)), dim3(kBlock), 0, stream, (const float2*)pos, w, b, N,
+                     B, (int)H, (int)W, img);
+  return check_launch("splat_bilinear_fwd");
+}
+
+int atl_splat_bilinear_bwd(const float* gimg, const float* pos, const float* w, const int64_t* b, int64_t N,
+                           int64_t B, int64_t H, int64_t W, float* gpos, float* gw, hipStream_t stream) {
+  if (N < 0 || B < 0 || !dims_ok(H, W)) { set_error("splat_bilinear_bwd: bad sizes"); return 1; }
+  if (N == 0) return 0;
+  hipLaunchKernelGGL(k_splat_bilinear_bwd, dim3(grid_for(N)), dim3(kBlock), 0, stream, gimg, (const float2*)pos, w,
+                     b, N, B, (int)H, (int)W, (float2*)gpos, gw);
+  return check_launch("splat_bilinear_bwd");
+}
+
+int atl_splat_gauss_fwd(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B, int64_t H,
+                        int64_t W, double sigma, int64_t R, float* img, hipStream_t stream) {
+  if (N < 0 || B < 0 || !dims_ok(H, W) || R < 0 || R > 4096 || !(sigma > 0)) { set_error("splat_gauss_fwd: bad arguments (sigma=%g R=%lld)", sigma, (long long)R); return 1; }
+  if (N == 0 || B == 0) return 0;
+  const float s2 = (float)(sigma * sigma);
+  const float inv2s2 = 1.f / (2.f * s2), norm = 1.f / (2.f * (float)M_PI * s2);
+  hipLaunchKernelGGL(k_splat_gauss_fwd, dim3(grid_for(N)), dim3(kBlock), 0, stream, (const float2*)pos, w, b, N, B,
+                     (int)H, (int)W, inv2s2, norm, (int)R, img);
+  return check_launch("splat_gauss_fwd");
+}
+
+int atl_splat_gauss_bwd(const float* gimg, const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B,
+                        int64_t H, int64_t W, double sigma, int64_t R, float* gpos, float* gw, hipStream_t stream) {
+  if (N < 0 || B < 0 || !dims_ok(H, W) || R < 0 || R > 4096 || !(sigma > 0)) { set_error("splat_gauss_bwd: bad arguments"); return 1; }
+  if (N == 0) return 0;
+  const float s2 = (float)(sigma * sigma);
+  const float inv2s2 = 1.f / (2.f * s2), norm = 1.f / (2.f * (float)M_PI * s2);
+  hipLaunchKernelGGL(k_splat_gauss_bwd, dim3(grid_for(N)), dim3(kBlock), 0, stream, gimg, (const float2*)pos, w, b,
+                     N, B, (int)H, (int)W, inv2s2, norm, s2, (int)R, (float2*)gpos, gw);
+  return check_launch("splat_gauss_bwd");
+}
+
+int atl_gather_bilinear_fwd(const float* img, const float* pos, const int64_t* b, int64_t N, int64_t B, int64_t H,
+                            int64_t W, float* out, hipStream_t stream) {
+  if (N < 0 || B < 0 || !dims_ok(H, W)) { set_error("gather_bilinear_fwd: bad sizes"); return 1; }
+  if (N == 0) return 0;
+  hipLaunchKernelGGL(k_gather_bilinear_fwd, dim3(grid_for(N)), dim3(kBlock), 0, stream, img, (const float2*)pos, b,
+                     N, B, (int)H, (int)W, out);
+  return check_launch("gather_bilinear_fwd");
+}
+
+int atl_gather_bilinear_bwd(const float* gval, const float* img, const float* pos, const int64_t* b, int64_t N,
+                            int64_t B, int64_t H, int64_t W, float* gimg, float* gpos, hipStream_t stream) {
+  if (N < 0 || B < 0 || !dims_ok(H, W)) { set_error("gather_bilinear_bwd: bad sizes"); return 1; }
+  if (N == 0) return 0;
+  hipLaunchKernelGGL(k_gather_bilinear_bwd, dim3(grid_for(N)), dim3(kBlock), 0, stream, gval, img,
+                     (const float2*)pos, b, N, B, (int)H, (int)W, gimg, (float2*)gpos);
+  return check_launch("gather_bilinear_bwd");
+}
+
+int atl_voxel_grid(const float* pos, const float* t, const float* p, const int64_t* b, int64_t N, int64_t B,
+                   int64_t C, int64_t H, int64_t W, float* vox, hipStream_t stream) {
+  if (N < 0 || B < 0 || C < 1 || !dims_ok(H, W) || C * H * W >= (int64_t)1 << 31) { set_error("voxel_grid: bad sizes"); return 1; }
+  if (N == 0 || B == 0) return 0;
+  hipLaunchKernelGGL(k_voxel_grid, dim3(grid_for(N)), dim3(kBlock), 0, stream, (const float2*)pos, t, p, b, N, B,
+                     (int)C, (int)H, (int)W, vox);
+  return check_launch("voxel_grid");
+}
+
+int atl_sample_grid_fwd(const float* field, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                        const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* out, hipStream_t stream) {
+  if (N < 0 || B < 0 || C < 1 || Hg < 1 || Wg < 1 || !dims_ok(Hg, Wg)) { set_error("sample_grid_fwd: bad sizes"); return 1; }
+  if (N == 0) return 0;
+  const int scale = img_h > 0 && img_w > 0;
+  const float sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1), syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
+  hipLaunchKernelGGL(k_sample_grid_fwd, dim3(grid_for(N)), dim3(kBlock), 0, stream, field, B, (int)C, (int)Hg,
+                     (int)Wg, (const float2*)pos, b, N, sxw, syh, scale, out);
+  return check_launch("sample_grid_fwd");
+}
+
+int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                        const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gfield,
+                        hipStream_t stream) {
+  if (N < 0 || B < 0 || C < 1 || Hg < 1 || Wg < 1 || !dims_ok(Hg, Wg)) { set_error("sample_grid_bwd: bad sizes"); return 1; }
+  if (N == 0) return 0;
+  const int scale = img_h > 0 && img_w > 0;
+  const float sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1), syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
+  hipLaunchKernelGGL(k_sample_grid_bwd, dim3(grid_for(N)), dim3(kBlock), 0, stream, gout, B, (int)C, (int)Hg,
+                     (int)Wg, (const float2*)pos, b, N, sxw, syh, scale, gfield);
+  return check_launch("sample_grid_bwd");
+}
+
+}  // extern "C"

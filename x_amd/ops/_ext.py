@@ -1,0 +1,285 @@
+"""Loader of the HIP library (libatl_hip.so) behind the atl ops API.
+
+Replaces the reference's JIT-built pybind module (atl/ops/_ext.py:16-50, csrc/atl_cpu.cpp:299-329) with a
+ctypes binding of the C-ABI declared in include/atl_hip.h.  ``get_ext()`` returns an object with the same
+method names, argument order and return values as the pybind module (plus ``with_cuda = True``), so
+atl/ops/functional.py-style callers work unchanged.  The HIP library handles device tensors only:
+
+* device tensors always go to the HIP kernels; if the library is missing, ``get_ext()`` raises (no silent
+  fallback);
+* CPU tensors are not supported by the library (``ext_supports`` is False for them) and the ops use the
+  pure-torch semantics in :mod:`x_amd.ops.reference`, as the reference does without its extension.
+
+The library is built in-tree by ``python x_amd/csrc/build.py`` (or ``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(os.environ.get("ATL_HIP_LIB", Path(__file__).resolve().parents[1] / "csrc" / "libatl_hip.so"))
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int64
+_D = ctypes.c_double
+_C = ctypes.c_int
+
+# name -> argtypes (all return int status unless listed in _RESTYPE)
+_SIGS = {
+    "atl_splat_bilinear_fwd": [_P, _P, _P, _I, _I, _I, _I, _P, _P],
+    "atl_splat_bilinear_bwd": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P],
+    "atl_splat_gauss_fwd": [_P, _P, _P, _I, _I, _I, _I, _D, _I, _P, _P],
+    "atl_splat_gauss_bwd": [_P, _P, _P, _P, _I, _I, _I, _I, _D, _I, _P, _P, _P],
+    "atl_gather_bilinear_fwd": [_P, _P, _P, _I, _I, _I, _I, _P, _P],
+    "atl_gather_bilinear_bwd": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P],
+    "atl_voxel_grid": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P],
+    "atl_sample_grid_fwd": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
+    "atl_sample_grid_bwd": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
+    "atl_plan_stats": [_P, _I, _P, _I, _P, _P],
+    "atl_plan_count": [_P, _P, _P, _P, _I, _I, _D, _D, _D, _D, _I, _I, _I, _P, _P],
+    "atl_scan_counts": [_P, _I, _P, _P, _P],
+    "atl_scan_work_size": [_I],
+    "atl_fill_i32": [_P, _I, _C, _P],
+    "atl_plan_fill": [_P, _P, _P, _P, _I, _I, _D, _D, _D, _D, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
+    "atl_plan_anchors": [_P, _P, _P, _P, _P, _I, _I, _D, _D, _D, _I, _I, _I, _P, _P, _P, _P, _P],
+    "atl_ats_pair_fwd": [_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _D, _D, _D, _P, _P, _P],
+    "atl_ats_pair_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _D, _D, _D, _I, _P,
+                         _P],
+    "atl_window_counts": [_P, _P, _I, _P, _I, _D, _P, _P],
+    "atl_check_sorted": [_P, _P, _I, _P, _P],
+    "atl_bin_counts": [_P, _P, _I, _I, _I, _P, _P],
+    "atl_visible_fraction": [_P, _P, _P, _P, _I, _P, _P, _I, _I, _D, _I, _I, _P, _P],
+    "atl_anchored_epilogue_fwd": [_P, _P, _P, _I, _D, _D, _P, _P, _P, _P],
+    "atl_anchored_epilogue_bwd": [_P, _P, _P, _I, _P, _P],
+    "atl_fast_plan_bins": [_P, _P, _P, _P, _I, _I, _D, _D, _D, _D, _I, _I, _I, _P, _P, _P],
+    "atl_fast_plan_fill": [_P, _P, _P, _P, _I, _I, _D, _D, _D, _D, _I, _I, _I, _P, _P, _P, _P, _P],
+    "atl_fast_anchor_bins": [_P, _P, _P, _P, _I, _D, _D, _D, _D, _I, _I, _I, _P, _P],
+    "atl_fast_anchor_fill": [_P, _P, _P, _P, _P, _I, _D, _D, _D, _D, _I, _I, _I, _P, _P, _P, _P],
+    "atl_fast_pair_fwd": [_P, _P, _P, _I, _P, _P, _I, _P, _I, _D, _D, _D, _D, _D, _D, _I, _I, _I, _I, _P, _P, _P],
+    "atl_fast_pair_bwd": [_P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _D, _D, _D, _D, _D, _D, _D, _I, _I, _I,
+                          _I, _P, _P],
+}
+_RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
+
+_LIB = None
+
+
+class HipLibraryError(RuntimeError):
+    """The HIP library is missing, or one of its entry points rejected its arguments."""
+
+
+def load_library():
+    """ctypes handle of libatl_hip.so (raises HipLibraryError if it is not built)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise HipLibraryError(f"{LIB_PATH} is not built: run `python x_amd/csrc/build.py` "
+                              "(x_amd runs device tensors on its HIP kernels only)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, args in _SIGS.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            continue
+        fn.argtypes = args
+        fn.restype = _RESTYPE.get(name, ctypes.c_int)
+    for name, rt in _RESTYPE.items():
+        getattr(lib, name).restype = rt
+    lib.atl_last_error.argtypes = []
+    _LIB = lib
+    return lib
+
+
+def exported_symbols():
+    return sorted(_SIGS) + ["atl_last_error", "atl_abi_version"]
+
+
+_TIMED = {}          # entry point -> list of (start, end) events, while kernel timing is on
+
+
+def time_kernels(names) -> dict:
+    """Bracket every later call of the named entry points with events on the caller's current stream (the
+    stream the kernels run on); returns the live {name: [(start, end), ...]} record.  ``time_kernels(())``
+    turns timing off."""
+    _TIMED.clear()
+    for n in names:
+        _TIMED[n] = []
+    return _TIMED
+
+
+def call(name: str, *args):
+    """Invoke a C-ABI entry point; raise HipLibraryError with the library's message on failure."""
+    lib = load_library()
+    rec = _TIMED.get(name)
+    if rec is not None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        rc = getattr(lib, name)(*args)
+        e1.record()
+        rec.append((e0, e1))
+    else:
+        rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.atl_last_error().decode(errors="replace")
+        raise HipLibraryError(f"{name}: {msg}")
+    return rc
+
+
+def ptr(t: torch.Tensor | None):
+    return ctypes.c_void_p(0) if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, dev: torch.device, shape=None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device != dev:
+        raise ValueError(f"{name} must be on {dev}, got {t.device}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None:
+        for k, s in enumerate(shape):
+            if s is not None and (t.dim() <= k or t.shape[k] != s):
+                raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {shape}")
+    return t
+
+
+F32, I64 = torch.float32, torch.int64
+
+
+class HipOps:
+    """Same surface as the reference's extension module (csrc/atl_cpu.cpp:299-329), on HIP device tensors."""
+    with_cuda = True
+
+    # -------------------------------------------------------------------------------- splat / gather
+    def splat_bilinear_fwd(self, pos, w, b, B, H, W):
+        dev = pos.device
+        N = pos.shape[0]
+        _need(pos, "pos", F32, dev, (N, 2)); _need(w, "w", F32, dev, (N,)); _need(b, "b", I64, dev, (N,))
+        img = torch.zeros(int(B), int(H), int(W), device=dev, dtype=F32)
+        with torch.cuda.device(dev):
+            call("atl_splat_bilinear_fwd", ptr(pos), ptr(w), ptr(b), N, int(B), int(H), int(W), ptr(img),
+                 stream_of(pos))
+        return img
+
+    def splat_bilinear_bwd(self, gimg, pos, w, b):
+        dev = pos.device
+        N = pos.shape[0]
+        _need(gimg, "gimg", F32, dev); _need(pos, "pos", F32, dev, (N, 2)); _need(w, "w", F32, dev, (N,))
+        _need(b, "b", I64, dev, (N,))
+        B, H, W = gimg.shape
+        gpos = torch.empty_like(pos); gw = torch.empty_like(w)
+        with torch.cuda.device(dev):
+            call("atl_splat_bilinear_bwd", ptr(gimg), ptr(pos), ptr(w), ptr(b), N, B, H, W, ptr(gpos), ptr(gw),
+                 stream_of(pos))
+        return [gpos, gw]
+
+    def splat_gauss_fwd(self, pos, w, b, B, H, W, sigma, radius):
+        dev = pos.device
+        N = pos.shape[0]
+        _need(pos, "pos", F32, dev, (N, 2)); _need(w, "w", F32, dev, (N,)); _need(b, "b", I64, dev, (N,))
+        img = torch.zeros(int(B), int(H), int(W), device=dev, dtype=F32)
+        with torch.cuda.device(dev):
+            call("atl_splat_gauss_fwd", ptr(pos), ptr(w), ptr(b), N, int(B), int(H), int(W), float(sigma),
+                 int(radius), ptr(img), stream_of(pos))
+        return img
+
+    def splat_gauss_bwd(self, gimg, pos, w, b, sigma, radius):
+        dev = pos.device
+        N = pos.shape[0]
+        _need(gimg, "gimg", F32, dev); _need(pos, "pos", F32, dev, (N, 2)); _need(w, "w", F32, dev, (N,))
+        _need(b, "b", I64, dev, (N,))
+        B, H, W = gimg.shape
+        gpos = torch.empty_like(pos); gw = torch.empty_like(w)
+        with torch.cuda.device(dev):
+            call("atl_splat_gauss_bwd", ptr(gimg), ptr(pos), ptr(w), ptr(b), N, B, H, W, float(sigma), int(radius),
+                 ptr(gpos), ptr(gw), stream_of(pos))
+        return [gpos, gw]
+
+    def gather_bilinear_fwd(self, img, pos, b):
+        dev = pos.device
+        N = pos.shape[0]
+        _need(img, "img", F32, dev); _need(pos, "pos", F32, dev, (N, 2)); _need(b, "b", I64, dev, (N,))
+        B, H, W = img.shape
+        out = torch.empty(N, device=dev, dtype=F32)
+        with torch.cuda.device(dev):
+            call("atl_gather_bilinear_fwd", ptr(img), ptr(pos), ptr(b), N, B, H, W, ptr(out), stream_of(pos))
+        return out
+
+    def gather_bilinear_bwd(self, gval, img, pos, b):
+        dev = pos.device
+        N = pos.shape[0]
+        _need(gval, "gval", F32, dev, (N,)); _need(img, "img", F32, dev); _need(pos, "pos", F32, dev, (N, 2))
+        _need(b, "b", I64, dev, (N,))
+        B, H, W = img.shape
+        gimg = torch.zeros_like(img); gpos = torch.empty_like(pos)
+        with torch.cuda.device(dev):
+            call("atl_gather_bilinear_bwd", ptr(gval), ptr(img), ptr(pos), ptr(b), N, B, H, W, ptr(gimg), ptr(gpos),
+                 stream_of(pos))
+        return [gimg, gpos]
+
+    def voxel_grid(self, pos, t, p, b, B, C, H, W):
+        dev = pos.device
+        N = pos.shape[0]
+        _need(pos, "pos", F32, dev, (N, 2)); _need(t, "t", F32, dev, (N,)); _need(p, "p", F32, dev, (N,))
+        _need(b, "b", I64, dev, (N,))
+        vox = torch.zeros(int(B), int(C), int(H), int(W), device=dev, dtype=F32)
+        with torch.cuda.device(dev):
+            call("atl_voxel_grid", ptr(pos), ptr(t), ptr(p), ptr(b), N, int(B), int(C), int(H), int(W), ptr(vox),
+                 stream_of(pos))
+        return vox
+
+    # -------------------------------------------------------------------------------- pair sums
+    def _pair_args(self, sy, sv, st, sid, cs, ax, at, ac, aid, sc):
+        dev = ax.device
+        E, M = st.shape[0], ax.shape[0]
+        _need(sy, "src_y", F32, dev, (E, 2)); _need(sv, "src_v", F32, dev, (E, 2)); _need(st, "src_t", F32, dev)
+        _need(sid, "src_id", I64, dev, (E,)); _need(cs, "cell_start", I64, dev)
+        _need(ax, "anc_x", F32, dev, (M, 2)); _need(at, "anc_t", F32, dev, (M,)); _need(ac, "anc_cell", I64, dev,
+                                                                                         (M, 3))
+        _need(aid, "anc_id", I64, dev, (M,)); _need(sc, "slice_c", F32, dev)
+        return E, M, cs.shape[0] - 1
+
+    def ats_pair_fwd(self, sy, sv, st, sid, cs, ax, at, ac, aid, sc, S, GH, GW, h, tau, cut, count=None):
+        E, M, ncell = self._pair_args(sy, sv, st, sid, cs, ax, at, ac, aid, sc)
+        out = torch.empty(M, device=ax.device, dtype=F32)
+        with torch.cuda.device(ax.device):
+            call("atl_ats_pair_fwd", ptr(sy), ptr(sv), ptr(st), ptr(sid), ptr(cs), E, ncell, ptr(ax), ptr(at),
+                 ptr(ac), ptr(aid), M, ptr(sc), int(S), int(GH), int(GW), float(h), float(tau), float(cut), ptr(out),
+                 ptr(count), stream_of(ax))
+        return out
+
+    def ats_pair_bwd(self, g, sy, sv, st, sid, cs, ax, at, ac, aid, sc, S, GH, GW, h, tau, cut, N):
+        E, M, ncell = self._pair_args(sy, sv, st, sid, cs, ax, at, ac, aid, sc)
+        _need(g, "gS", F32, ax.device, (M,))
+        gv = torch.zeros(int(N), 2, device=ax.device, dtype=F32)
+        with torch.cuda.device(ax.device):
+            call("atl_ats_pair_bwd", ptr(g), ptr(sy), ptr(sv), ptr(st), ptr(sid), ptr(cs), E, ncell, ptr(ax),
+                 ptr(at), ptr(ac), ptr(aid), M, ptr(sc), int(S), int(GH), int(GW), float(h), float(tau), float(cut),
+                 int(N), ptr(gv), stream_of(ax))
+        return gv
+
+
+_OPS = None
+
+
+def get_ext() -> HipOps:
+    """The HIP ops object (raises HipLibraryError if libatl_hip.so is not built)."""
+    global _OPS
+    if _OPS is None:
+        load_library()
+        _OPS = HipOps()
+    return _OPS
+
+
+def ext_supports(t: torch.Tensor) -> bool:
+    """True for device tensors: they always run on the HIP library (which must then be built)."""
+    return bool(t.is_cuda)

@@ -1,0 +1,480 @@
+"""Differentiable event-transport ops on MI355X HIP kernels (same API as atl/ops/functional.py).
+
+* :func:`splat`          events -> image (bilinear vote or truncated Gaussian); grads to positions and weights
+* :func:`gather`         bilinear sample of an image at event positions; grads to image and positions
+* :func:`ats_pair_sums`  exact anchored leave-one-out Gaussian sums for per-event velocities; grad to v
+* :func:`build_pair_plan`, :class:`PairPlan`  the spatial hash behind the pair sums (built on the device)
+* :func:`window_counts`  per-anchor number of same-batch events within +-tau
+* :func:`voxel_grid`     trilinear polarity voting (no grad)
+* :func:`sample_grid`    bilinear border-clamped lookup in a (B, C, Hg, Wg) field; grad to the field
+
+Device tensors run on the HIP library (libatl_hip.so) through the C-ABI; CPU tensors use the pure-torch
+semantics of :mod:`x_amd.ops.reference`, as the reference does without its extension.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import reference as ref
+from ._ext import F32, I64, call, ext_supports, get_ext, load_library, ptr, stream_of
+
+
+def _f32(t):
+    return t.contiguous().float()
+
+
+# ------------------------------------------------------------------------------------------- splat
+class _SplatBilinear(torch.autograd.Function):
+    """atl/ops/functional.py:24-35."""
+
+    @staticmethod
+    def forward(ctx, pos, w, b, B, H, W):
+        pos, w, b = _f32(pos), _f32(w), b.contiguous().long()
+        ctx.save_for_backward(pos, w, b)
+        return get_ext().splat_bilinear_fwd(pos, w, b, B, H, W)
+
+    @staticmethod
+    def backward(ctx, g):
+        pos, w, b = ctx.saved_tensors
+        gp, gw = get_ext().splat_bilinear_bwd(g.contiguous().float(), pos, w, b)
+        return gp, gw, None, None, None, None
+
+
+class _SplatGauss(torch.autograd.Function):
+    """atl/ops/functional.py:38-50."""
+
+    @staticmethod
+    def forward(ctx, pos, w, b, B, H, W, sigma, radius):
+        pos, w, b = _f32(pos), _f32(w), b.contiguous().long()
+        ctx.save_for_backward(pos, w, b)
+        ctx.sigma, ctx.radius = sigma, radius
+        return get_ext().splat_gauss_fwd(pos, w, b, B, H, W, sigma, radius)
+
+    @staticmethod
+    def backward(ctx, g):
+        pos, w, b = ctx.saved_tensors
+        gp, gw = get_ext().splat_gauss_bwd(g.contiguous().float(), pos, w, b, ctx.sigma, ctx.radius)
+        return gp, gw, None, None, None, None, None, None
+
+
+def splat(pos: torch.Tensor, w: torch.Tensor, b: torch.Tensor, B: int, H: int, W: int,
+          kernel: str = "bilinear", sigma: float = 1.0, radius: int | None = None) -> torch.Tensor:
+    """Accumulate weighted events into a (B, H, W) image (atl/ops/functional.py:53-65)."""
+    if kernel == "bilinear":
+        if ext_supports(pos):
+            return _SplatBilinear.apply(pos, w, b, B, H, W)
+        return ref.splat_bilinear(pos, w, b, B, H, W)
+    if kernel == "gauss":
+        radius = int(math.ceil(3 * sigma)) if radius is None else radius
+        if ext_supports(pos):
+            return _SplatGauss.apply(pos, w, b, B, H, W, float(sigma), int(radius))
+        return ref.splat_gauss(pos, w, b, B, H, W, sigma, radius)
+    raise ValueError(kernel)
+
+
+# ------------------------------------------------------------------------------------------- gather
+class _Gather(torch.autograd.Function):
+    """atl/ops/functional.py:69-80."""
+
+    @staticmethod
+    def forward(ctx, img, pos, b):
+        img, pos, b = _f32(img), _f32(pos), b.contiguous().long()
+        ctx.save_for_backward(img, pos, b)
+        return get_ext().gather_bilinear_fwd(img, pos, b)
+
+    @staticmethod
+    def backward(ctx, g):
+        img, pos, b = ctx.saved_tensors
+        gi, gp = get_ext().gather_bilinear_bwd(g.contiguous().float(), img, pos, b)
+        return gi, gp, None
+
+
+def gather(img: torch.Tensor, pos: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Bilinear sample of a (B, H, W) image at event positions (zero outside); differentiable in both."""
+    if ext_supports(pos):
+        return _Gather.apply(img, pos, b)
+    return ref.gather_bilinear(img, pos, b)
+
+
+# ------------------------------------------------------------------------------------------- blur
+def gaussian_kernel1d(sigma: float, device, dtype=torch.float32):
+    """Normalised 1-D Gaussian kernel of radius ceil(3 sigma) (atl/ops/functional.py:91-96)."""
+    r = max(int(math.ceil(3 * sigma)), 1)
+    x = torch.arange(-r, r + 1, device=device, dtype=dtype)
+    k = torch.exp(-x * x / (2 * sigma * sigma))
+    return k / k.sum()
+
+
+def blur(img: torch.Tensor, sigma: float) -> torch.Tensor:
+    """Separable Gaussian blur of a (B, H, W) or (B, C, H, W) image, zero padding (functional.py:99-110)."""
+    if sigma <= 0:
+        return img
+    squeeze = img.dim() == 3
+    x = img[:, None] if squeeze else img
+    C = x.shape[1]
+    k = gaussian_kernel1d(sigma, img.device, img.dtype)
+    r = (k.numel() - 1) // 2
+    x = torch.nn.functional.conv2d(x, k.view(1, 1, 1, -1).expand(C, 1, 1, -1), padding=(0, r), groups=C)
+    x = torch.nn.functional.conv2d(x, k.view(1, 1, -1, 1).expand(C, 1, -1, 1), padding=(r, 0), groups=C)
+    return x[:, 0] if squeeze else x
+
+
+# ------------------------------------------------------------------------------------------- flow grid
+class _SampleGrid(torch.autograd.Function):
+    """Bilinear border-clamped lookup of a (B, C, Hg, Wg) field (atl/motion/parametric.py:235-251)."""
+
+    @staticmethod
+    def forward(ctx, fld, pos, b, img_h, img_w):
+        fld, pos, b = _f32(fld), _f32(pos), b.contiguous().long()
+        B, C, Hg, Wg = fld.shape
+        N = pos.shape[0]
+        out = torch.empty(N, C, device=pos.device, dtype=F32)
+        with torch.cuda.device(pos.device):
+            call("atl_sample_grid_fwd", ptr(fld), B, C, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w),
+                 ptr(out), stream_of(pos))
+        ctx.save_for_backward(pos, b)
+        ctx.shape, ctx.img = (B, C, Hg, Wg), (int(img_h), int(img_w))
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        pos, b = ctx.saved_tensors
+        B, C, Hg, Wg = ctx.shape
+        gf = torch.zeros(B, C, Hg, Wg, device=pos.device, dtype=F32)
+        g = g.contiguous().float()
+        with torch.cuda.device(pos.device):
+            call("atl_sample_grid_bwd", ptr(g), B, C, Hg, Wg, ptr(pos), ptr(b), pos.shape[0], ctx.img[0], ctx.img[1],
+                 ptr(gf), stream_of(pos))
+        return gf, None, None, None, None
+
+
+def sample_grid_hip(fld: torch.Tensor, pos: torch.Tensor, b: torch.Tensor, img_hw=(0, 0)) -> torch.Tensor:
+    """HIP flow lookup: ``pos`` are grid coordinates, or image pixels mapped by x / max(W-1, 1) * (Wg-1)
+    when ``img_hw`` = (H, W) is given (DenseLinearFlow.field).  Differentiable w.r.t. the field only."""
+    if pos.requires_grad:
+        raise NotImplementedError("the HIP flow lookup differentiates w.r.t. the field only (positions are data)")
+    get_ext()
+    return _SampleGrid.apply(fld, pos, b, img_hw[0], img_hw[1])
+
+
+# ------------------------------------------------------------------------------------------- anchored pairs
+@dataclass
+class PairPlan:
+    """Spatial hash for :func:`ats_pair_sums`: (source, slice) entries sorted by (batch, slice, cell)
+    (atl/ops/functional.py:114-130)."""
+    src_y: torch.Tensor
+    src_v: torch.Tensor
+    src_t: torch.Tensor
+    src_id: torch.Tensor
+    cell_start: torch.Tensor
+    anc_x: torch.Tensor
+    anc_t: torch.Tensor
+    anc_cell: torch.Tensor
+    anc_id: torch.Tensor
+    slice_c: torch.Tensor
+    S: int
+    GH: int
+    GW: int
+    geometry: dict = field(default_factory=dict)
+
+
+def decode_ordered(st: np.ndarray) -> np.ndarray:
+    """Floats from the order-preserving int encoding used by the device reductions."""
+    st = st.astype(np.int32)
+    return np.where(st >= 0, st, st ^ np.int32(0x7FFFFFFF)).astype(np.int32).view(np.float32)
+
+
+def plan_stats(v: torch.Tensor, xa: torch.Tensor):
+    """(vmax, min x, min y, max x, max y) of the plan geometry from one device reduction (one host sync)."""
+    dev = v.device
+    stats = torch.empty(5, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        call("atl_plan_stats", ptr(v), v.shape[0], ptr(xa), xa.shape[0], ptr(stats), stream_of(v))
+    f = decode_ordered(stats.cpu().numpy())
+    return float(f[0]), float(f[1]), float(f[2]), -float(f[3]), -float(f[4])
+
+
+def plan_geometry(vmax: float, bbox, M: int, h, tau, cut, S, W, H):
+    """Grid geometry in Python doubles exactly as atl/ops/functional.py:135-149."""
+    delta = 1.0 / S
+    cell = max(cut * h + vmax * delta / 2 + 1e-3, 1.0)
+    if M:
+        ox, oy = bbox[0] - cell, bbox[1] - cell
+        ex, ey = bbox[2] + cell, bbox[3] + cell
+    else:
+        ox, oy, ex, ey = -cell, -cell, W + cell, H + cell
+    GW = int(math.ceil((ex - ox) / cell)) + 1
+    GH = int(math.ceil((ey - oy) / cell)) + 1
+    return dict(delta=delta, cell=cell, ox=ox, oy=oy, ex=ex, ey=ey, GW=GW, GH=GH, vmax=vmax)
+
+
+def _scan(counts: torch.Tensor) -> torch.Tensor:
+    n = counts.shape[0]
+    lib_work = int(load_library().atl_scan_work_size(n))
+    start = torch.empty(n + 1, dtype=I64, device=counts.device)
+    work = torch.empty(max(lib_work, 1), dtype=I64, device=counts.device)
+    call("atl_scan_counts", ptr(counts), n, ptr(start), ptr(work), stream_of(counts))
+    return start
+
+
+def _build_pair_plan_hip(x, t, v, b, B, H, W, anchors, h, tau, cut, n_slices, anchor_xy):
+    dev = x.device
+    S = int(n_slices)
+    delta = 1.0 / S
+    x, t, vd = _f32(x), _f32(t), _f32(v.detach())
+    b, anchors = b.contiguous().long(), anchors.contiguous().long()
+    N, M = t.shape[0], anchors.shape[0]
+    xa_all = _f32(x[anchors] if anchor_xy is None else anchor_xy.detach())
+    with torch.cuda.device(dev):
+        vmax, *bbox = plan_stats(vd, xa_all)
+        geo = plan_geometry(vmax if N else 0.0, bbox, M, h, tau, cut, S, W, H)
+        GW, GH, cell, ox, oy = geo["GW"], geo["GH"], geo["cell"], geo["ox"], geo["oy"]
+        ncell = B * S * GH * GW
+        if ncell >= 2 ** 31:
+            raise ValueError(f"pair plan grid too large ({ncell} cells)")
+        st = stream_of(x)
+        counts = torch.zeros(ncell, dtype=torch.int32, device=dev)
+        call("atl_plan_count", ptr(x), ptr(t), ptr(vd), ptr(b), N, B, ox, oy, cell, float(tau), S, GH, GW,
+             ptr(counts), st)
+        cell_start = _scan(counts)
+        E = int(cell_start[-1])
+        src_y = torch.empty(E, 2, dtype=F32, device=dev)
+        src_v = torch.empty(E, 2, dtype=F32, device=dev)
+        src_t = torch.empty(E, dtype=F32, device=dev)
+        src_id = torch.empty(E, dtype=I64, device=dev)
+        counts.zero_()
+        call("atl_plan_fill", ptr(x), ptr(t), ptr(vd), ptr(b), N, B, ox, oy, cell, float(tau), S, GH, GW,
+             ptr(cell_start), ptr(counts), ptr(src_y), ptr(src_v), ptr(src_t), ptr(src_id), st)
+        anc_x = torch.empty(M, 2, dtype=F32, device=dev)
+        anc_t = torch.empty(M, dtype=F32, device=dev)
+        anc_cell = torch.empty(M, 3, dtype=I64, device=dev)
+        anc_id = torch.empty(M, dtype=I64, device=dev)
+        call("atl_plan_anchors", ptr(x), ptr(t), ptr(b), ptr(anchors),
+             ptr(None if anchor_xy is None else xa_all), M, N, ox, oy, cell, S, GH, GW, ptr(anc_x), ptr(anc_t),
+             ptr(anc_cell), ptr(anc_id), st)
+        slice_c = (torch.arange(S, device=dev, dtype=F32) + 0.5) * delta
+    return PairPlan(src_y, src_v, src_t, src_id, cell_start, anc_x, anc_t, anc_cell, anc_id, slice_c, S, GH, GW,
+                    geo)
+
+
+def _build_pair_plan_torch(x, t, v, b, B, H, W, anchors, h, tau, cut, n_slices, anchor_xy):
+    """CPU tensors: the plan from torch ops, same arithmetic as atl/ops/functional.py:132-178."""
+    dev = x.device
+    S = int(n_slices)
+    delta = 1.0 / S
+    with torch.no_grad():
+        vd = v.detach().float()
+        vmax = float(vd.norm(dim=1).max()) if vd.numel() else 0.0
+        xa = (x[anchors] if anchor_xy is None else anchor_xy).float()
+        bbox = (float(xa[:, 0].min()), float(xa[:, 1].min()), float(xa[:, 0].max()), float(xa[:, 1].max())) \
+            if xa.numel() else (0.0, 0.0, 0.0, 0.0)
+        geo = plan_geometry(vmax, bbox, xa.shape[0], h, tau, cut, S, W, H)
+        GW, GH, cell, ox, oy = geo["GW"], geo["GH"], geo["cell"], geo["ox"], geo["oy"]
+        s_lo = torch.ceil((t - tau - delta / 2) / delta - 0.5).clamp(0, S - 1).long()
+        s_hi = torch.floor((t + tau + delta / 2) / delta - 0.5).clamp(0, S - 1).long()
+        cnt = (s_hi - s_lo + 1).clamp(min=0)
+        rep = torch.repeat_interleave(torch.arange(t.numel(), device=dev), cnt)
+        first = torch.cumsum(cnt, 0) - cnt
+        s = s_lo[rep] + (torch.arange(rep.numel(), device=dev) - first[rep])
+        cs_all = (torch.arange(S, device=dev, dtype=torch.float32) + 0.5) * delta
+        y = x[rep].float() + vd[rep] * (cs_all[s] - t[rep])[:, None]
+        cx = torch.floor((y[:, 0] - ox) / cell).long()
+        cy = torch.floor((y[:, 1] - oy) / cell).long()
+        keep = (cx >= 0) & (cx < GW) & (cy >= 0) & (cy < GH)
+        rep, s, y, cx, cy = rep[keep], s[keep], y[keep], cx[keep], cy[keep]
+        key = ((b[rep] * S + s) * GH + cy) * GW + cx
+        order = torch.argsort(key, stable=True)
+        key, rep, y = key[order], rep[order], y[order]
+        counts = torch.bincount(key, minlength=B * S * GH * GW)
+        cell_start = torch.cat([counts.new_zeros(1), torch.cumsum(counts, 0)]).long()
+        ta = t[anchors]
+        sa = torch.clamp(torch.floor(ta / delta), 0, S - 1).long()
+        acx = torch.floor((xa[:, 0] - ox) / cell).long().clamp(0, GW - 1)
+        acy = torch.floor((xa[:, 1] - oy) / cell).long().clamp(0, GH - 1)
+        anc_cell = torch.stack([b[anchors] * S + sa, acx, acy], 1).contiguous()
+    return PairPlan(y.contiguous(), vd[rep].contiguous(), t[rep].float().contiguous(), rep.contiguous(), cell_start,
+                    xa.contiguous(), ta.float().contiguous(), anc_cell, anchors.long().contiguous(),
+                    cs_all.contiguous(), S, GH, GW, geo)
+
+
+def build_pair_plan(x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, anchor_xy=None) -> PairPlan:
+    """Spatial hash of (source, slice) pairs sorted by (batch, slice, cell) (atl/ops/functional.py:132-178).
+
+    On device tensors the plan is built by HIP kernels (count, scan, scatter) with the reference's fp32
+    arithmetic, so slice ranges, cell bins, keys and ``cell_start`` are bit-identical to the reference's CPU
+    plan.  ``vmax`` is max ||v|| evaluated as sqrt(fma(vy, vy, vx * vx)), the rounding of torch's CPU vector
+    norm on AVX2/AVX-512 hosts.  Entry order within one cell is unspecified, as with ``torch.argsort``."""
+    with torch.no_grad():
+        if x.is_cuda:
+            get_ext()
+            return _build_pair_plan_hip(x, t, v, b, B, H, W, anchors, h, tau, cut, n_slices, anchor_xy)
+        return _build_pair_plan_torch(x, t, v, b, B, H, W, anchors, h, tau, cut, n_slices, anchor_xy)
+
+
+class _ATSPair(torch.autograd.Function):
+    """atl/ops/functional.py:181-196: forward over a plan; gradient to the per-event velocities only."""
+
+    @staticmethod
+    def forward(ctx, v, plan: PairPlan, h, tau, cut):
+        e = get_ext()
+        ctx.plan, ctx.args, ctx.n = plan, (float(h), float(tau), float(cut)), v.shape[0]
+        p = plan
+        return e.ats_pair_fwd(p.src_y, p.src_v, p.src_t, p.src_id, p.cell_start, p.anc_x, p.anc_t, p.anc_cell,
+                              p.anc_id, p.slice_c, p.S, p.GH, p.GW, *ctx.args)
+
+    @staticmethod
+    def backward(ctx, g):
+        p = ctx.plan
+        gv = get_ext().ats_pair_bwd(g.contiguous().float(), p.src_y, p.src_v, p.src_t, p.src_id, p.cell_start,
+                                    p.anc_x, p.anc_t, p.anc_cell, p.anc_id, p.slice_c, p.S, p.GH, p.GW,
+                                    *ctx.args, ctx.n)
+        return gv, None, None, None, None
+
+
+def ats_pair_sums(x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, force_ref=False, anchor_xy=None):
+    """S_i = sum_{j != i} 1[|t_i - t_j| <= tau] exp(-|x_i - x_j - v_j (t_i - t_j)|^2 / 2h^2) for anchors i
+    (atl/ops/functional.py:199-207).  ``x`` are raw event positions, ``v`` per-event velocities in px per
+    window; the gradient flows to ``v`` only."""
+    if force_ref or not ext_supports(x):
+        return ref.ats_pair_sums(x.float(), t.float(), v.float(), b, anchors, h, tau, cut, anchor_xy=anchor_xy)
+    plan = build_pair_plan(x, t, v, b, B, H, W, anchors, h, tau, cut, n_slices, anchor_xy=anchor_xy)
+    return _ATSPair.apply(v.float(), plan, h, tau, cut)
+
+
+def pair_counts(plan: PairPlan, h, tau, cut) -> torch.Tensor:
+    """n_i: number of contributing pairs of every anchor of a device plan (instrumented forward)."""
+    p = plan
+    cnt = torch.zeros(p.anc_x.shape[0], dtype=torch.int32, device=p.anc_x.device)
+    get_ext().ats_pair_fwd(p.src_y, p.src_v, p.src_t, p.src_id, p.cell_start, p.anc_x, p.anc_t, p.anc_cell,
+                           p.anc_id, p.slice_c, p.S, p.GH, p.GW, h, tau, cut, count=cnt)
+    return cnt
+
+
+# ------------------------------------------------------------------------------------------- window counts
+def events_sorted(t: torch.Tensor, b: torch.Tensor) -> bool:
+    """True if the keys b*4 + t ascend in event order (device check, one host sync)."""
+    t, b = _f32(t), b.contiguous().long()
+    flag = torch.empty(1, dtype=torch.int32, device=t.device)
+    with torch.cuda.device(t.device):
+        call("atl_check_sorted", ptr(t), ptr(b), t.shape[0], ptr(flag), stream_of(t))
+    return int(flag.item()) == 0
+
+
+def window_counts(t: torch.Tensor, b: torch.Tensor, idx: torch.Tensor, tau: float,
+                  assume_sorted: Optional[bool] = None) -> torch.Tensor:
+    """#{j != i, same batch, |t_j - t_i| <= tau} for i in idx (atl/ops/functional.py:210-217).
+
+    Device path: binary searches over the float64 keys b*4 + t in event order, which the EventPacket
+    invariant (sorted by (b, t)) keeps ascending; ``assume_sorted=None`` verifies that first, an unsorted
+    input is sorted (by key) before the search."""
+    if not t.is_cuda:
+        key = b.double() * 4.0 + t.double()
+        ks, _ = torch.sort(key)
+        ki = key[idx]
+        lo = torch.searchsorted(ks, ki - tau, right=False)
+        hi = torch.searchsorted(ks, ki + tau, right=True)
+        return (hi - lo - 1).clamp(min=0).to(t.dtype)
+    get_ext()
+    t, b, idx = _f32(t), b.contiguous().long(), idx.contiguous().long()
+    if assume_sorted is None:
+        assume_sorted = events_sorted(t, b)
+    if not assume_sorted:
+        key = b.double() * 4.0 + t.double()
+        order = torch.argsort(key, stable=True)
+        inv = torch.empty_like(order)
+        inv[order] = torch.arange(order.numel(), device=order.device)
+        t, b, idx = t[order].contiguous(), b[order].contiguous(), inv[idx].contiguous()
+    out = torch.empty(idx.shape[0], dtype=F32, device=t.device)
+    with torch.cuda.device(t.device):
+        call("atl_window_counts", ptr(t), ptr(b), t.shape[0], ptr(idx), idx.shape[0], float(tau), ptr(out),
+             stream_of(t))
+    return out
+
+
+# ------------------------------------------------------------------------------------------- exposure
+_CENTRES = {}
+
+
+def bin_centres(n_check: int, device) -> torch.Tensor:
+    """0.5 (e_k + e_{k+1}) of linspace(0, 1, n_check + 1) in fp32 (atl/objectives/ats.py:37-38)."""
+    key = (int(n_check), str(device))
+    c = _CENTRES.get(key)
+    if c is None:
+        edges = torch.linspace(0, 1, n_check + 1)
+        c = (0.5 * (edges[:-1] + edges[1:])).to(device)
+        _CENTRES[key] = c
+    return c
+
+
+def visible_fraction_linear(xa, va, ta, ba, t_all, b_all, B, H, W, tau, n_check=16):
+    """Exposure correction of atl/objectives/ats.py:31-50 for motion linear at the event: anchors (xa, ta, ba)
+    with velocities ``va`` transported to the n_check bin centres.  No grad."""
+    dev = xa.device
+    xa, va, ta, ba = _f32(xa), _f32(va), _f32(ta), ba.contiguous().long()
+    t_all, b_all = _f32(t_all), b_all.contiguous().long()
+    counts = torch.zeros(B, n_check, dtype=F32, device=dev)
+    out = torch.empty(ta.shape[0], dtype=F32, device=dev)
+    centres = bin_centres(n_check, dev)
+    with torch.cuda.device(dev):
+        st = stream_of(xa)
+        call("atl_bin_counts", ptr(t_all), ptr(b_all), t_all.shape[0], B, n_check, ptr(counts), st)
+        call("atl_visible_fraction", ptr(xa), ptr(va), ptr(ta), ptr(ba), ta.shape[0], ptr(counts), ptr(centres), B,
+             n_check, float(tau), int(H), int(W), ptr(out), st)
+    return out
+
+
+class _AnchoredEpilogue(torch.autograd.Function):
+    """log(eps + S / (Wn 2 pi h^2)) with Wn = max(count, 1) * vis (atl/objectives/ats.py:92-96)."""
+
+    @staticmethod
+    def forward(ctx, S, wc, vis, h, eps):
+        S, wc = _f32(S), _f32(wc)
+        vis = None if vis is None else _f32(vis)
+        M = S.shape[0]
+        ls, q, D = (torch.empty(M, dtype=F32, device=S.device) for _ in range(3))
+        with torch.cuda.device(S.device):
+            call("atl_anchored_epilogue_fwd", ptr(S), ptr(wc), ptr(vis), M, float(h), float(eps), ptr(ls), ptr(q),
+                 ptr(D), stream_of(S))
+        ctx.save_for_backward(q, D)
+        return ls
+
+    @staticmethod
+    def backward(ctx, g):
+        q, D = ctx.saved_tensors
+        gS = torch.empty_like(q)
+        g = g.contiguous().float()
+        with torch.cuda.device(q.device):
+            call("atl_anchored_epilogue_bwd", ptr(g), ptr(q), ptr(D), q.shape[0], ptr(gS), stream_of(q))
+        return gS, None, None, None, None
+
+
+def anchored_log_scores(S, wc, vis, h, eps):
+    """Device log-score epilogue (gradient to S only)."""
+    get_ext()
+    return _AnchoredEpilogue.apply(S, wc, vis, h, eps)
+
+
+# ------------------------------------------------------------------------------------------- voxel grid
+def voxel_grid(pos, t, p, b, B, C, H, W, normalize: str | None = "mean_std") -> torch.Tensor:
+    """Trilinear polarity voxel grid (B, C, H, W), optionally normalised (atl/ops/functional.py:221-238)."""
+    with torch.no_grad():
+        if ext_supports(pos):
+            vox = get_ext().voxel_grid(_f32(pos), _f32(t), _f32(p), b.contiguous().long(), B, C, H, W)
+        else:
+            vox = ref.voxel_grid(pos.float(), t.float(), p.float(), b, B, C, H, W)
+        if normalize == "mean_std":
+            for k in range(B):
+                vk = vox[k]
+                nz = vk != 0
+                if nz.any():
+                    m, s = vk[nz].mean(), vk[nz].std()
+                    vk[nz] = (vk[nz] - m) / s if s > 0 else vk[nz] - m
+        elif normalize == "max":
+            mx = vox.abs().amax(dim=(1, 2, 3), keepdim=True).clamp(min=1e-9)
+            vox = vox / mx
+    return vox
