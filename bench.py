@@ -111,7 +111,7 @@ def main():
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
-    kernels = ["atl_ats_pair_fwd", "atl_ats_pair_bwd"]
+    kernels = ["atl_fast_pair_fwd", "atl_fast_pair_bwd"]
     rec = _ext.time_kernels(kernels)
     t0 = time.perf_counter()
     for _ in range(a.steps):
@@ -126,9 +126,9 @@ def main():
         xs = ev.xy + (torch.rand(ev.xy.shape, generator=g, device=dev) - 0.5)
         xa = xs + a.sigma * torch.randn(xs.shape, generator=g, device=dev)
         v = motion.velocity(xs, ev.t, ev.b)
-        plan = F.build_pair_plan(xs, ev.t, v, ev.b, 1, ev.height, ev.width, torch.arange(ev.n, device=dev), a.sigma,
-                                 0.2, 3.0, 16, anchor_xy=xa)
-        K = int(F.pair_counts(plan, a.sigma, 0.2, 3.0).sum())
+        plan = F.FastPairPlan(xs, ev.t, v, ev.b, 1, ev.height, ev.width, torch.arange(ev.n, device=dev), a.sigma,
+                              0.2, 3.0, 16, anchor_xy=xa)
+        K = int(plan.counts().sum())
     dom = max(kernels, key=lambda k: ms[k])
     slots = SLOTS_FWD if dom.endswith("fwd") else SLOTS_BWD
     achieved = K * slots / (ms[dom] * 1e-3)

@@ -110,6 +110,41 @@ int atl_ats_pair_bwd(const float* gS, const float* src_y, const float* src_v, co
                      const float* slice_c, int64_t S, int64_t GH, int64_t GW, double h, double tau, double cut,
                      int64_t N, float* gv, hipStream_t stream);
 
+/* ---------------------------------------------------------------- fused pair sums (no host synchronisation)
+ *
+ * The same S_i and dS/dv as atl_ats_pair_fwd/bwd over the reference plan (functional.py:181-207:
+ * build_pair_plan + ats_pair_fwd / ats_pair_bwd), built and evaluated without a host round trip:
+ * the reference's (source, slice) entries and the anchors are binned into a fixed fine-cell grid clamped
+ * around the sensor, the forward gathers per anchor and the backward gathers per entry (no per-pair
+ * atomics).  The contributing pairs, and so every per-anchor neighbour count, are the reference's.
+ *
+ * Usage: atl_fast_geometry_init (host only, fills the struct, including ws_bytes) -> allocate ws_bytes
+ * of device memory -> atl_fast_plan -> atl_fast_pair_fwd -> atl_fast_pair_bwd (any number of times while
+ * the workspace is kept).  Inputs: x (N,2) raw source positions, t (N), v (N,2) velocities, b (N) int64;
+ * anchors (M) int64 event indices, anchor_xy (M,2) anchor positions or null (x[anchors]). */
+typedef struct atl_fast_geometry {
+  int32_t version;                      /* ATL_HIP_ABI_VERSION once initialised */
+  int32_t reserved;
+  int64_t N, M, B, H, W, S;
+  double h, tau, cut;
+  float gx0, gy0, gx1, gy1, cell;       /* clamp box and fine cell size (pixels) */
+  float reserved_f;
+  int64_t GW, GH, ncell, max_span, ecap;
+  int64_t ws_bytes;
+  int64_t off_params, off_cnt, off_start, off_part, off_erank, off_arank, off_esv, off_eti, off_ekey, off_arec,
+      off_aid, off_akey, off_gss;
+} atl_fast_geometry;
+
+int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W, int64_t S, double h, double tau,
+                           double cut, atl_fast_geometry* geo);
+/* Plan: entries and anchors binned and sorted by (batch, slice, cell) in ws. */
+int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, const float* v, const int64_t* b,
+                  const int64_t* anchors, const float* anchor_xy, void* ws, int64_t ws_bytes, hipStream_t stream);
+/* out (M) written for every valid anchor (zero-fill it first); count (M) int32 receives n_i when non-null. */
+int atl_fast_pair_fwd(const atl_fast_geometry* geo, const void* ws, float* out, int* count, hipStream_t stream);
+/* gv (N,2) accumulated (zero-fill it first). */
+int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, float* gv, hipStream_t stream);
+
 /* ---------------------------------------------------------------- anchored-score pieces */
 
 /* window_counts (atl/ops/functional.py:210-217): out (M) written.  Requires keys b*4 + t ascending in event

@@ -1,0 +1,72 @@
+// Device-wide exclusive scan of int32 counts (three launches: per-tile totals, one-block scan of the
+// totals, per-tile rescan), shared by the plan builders.  Tiles are kScanTile = 2048 counts.
+#pragma once
+#include "common.h"
+
+namespace atlhip {
+
+constexpr int kScanItems = 8;
+constexpr int kScanTile = kBlock * kScanItems;
+
+inline int64_t scan_tiles(int64_t n) { return (n + kScanTile - 1) / kScanTile; }
+
+__global__ void __launch_bounds__(kBlock) k_scan32_reduce(const int* __restrict__ in, int64_t n,
+                                                          int* __restrict__ part) {
+  __shared__ int lds[kBlock / kWave + 1];
+  const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+  int s = 0;
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k)
+    if (base + k < n) s += in[base + k];
+  int total;
+  block_exclusive_scan<kBlock>(s, lds, total);
+  if (threadIdx.x == 0) part[blockIdx.x] = total;
+}
+
+// Exclusive scan of the tile totals in place (one block); part[nparts] receives the grand total.
+__global__ void __launch_bounds__(kBlock) k_scan32_parts(int* __restrict__ part, int64_t nparts) {
+  __shared__ int lds[kBlock / kWave + 1];
+  int carry = 0;
+  for (int64_t base = 0; base < nparts; base += kBlock) {
+    const int64_t i = base + threadIdx.x;
+    const int v = i < nparts ? part[i] : 0;
+    int total;
+    const int excl = block_exclusive_scan<kBlock>(v, lds, total);
+    if (i < nparts) part[i] = carry + excl;
+    carry += total;
+  }
+  if (threadIdx.x == 0) part[nparts] = carry;
+}
+
+// out[i + 1] = sum(in[0..i]), out[0] = 0.
+__global__ void __launch_bounds__(kBlock) k_scan32_write(const int* __restrict__ in, int64_t n,
+                                                         const int* __restrict__ part, int* __restrict__ out) {
+  __shared__ int lds[kBlock / kWave + 1];
+  const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+  int vals[kScanItems];
+  int s = 0;
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    vals[k] = base + k < n ? in[base + k] : 0;
+    s += vals[k];
+  }
+  int total;
+  const int excl = block_exclusive_scan<kBlock>(s, lds, total);
+  int run = part[blockIdx.x] + excl;
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    run += vals[k];
+    if (base + k < n) out[base + k + 1] = run;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) out[0] = 0;
+}
+
+// Launches the three passes; `part` holds scan_tiles(n) + 1 ints.  n >= 1.
+inline void scan32(const int* in, int64_t n, int* part, int* out, hipStream_t stream) {
+  const int64_t tiles = scan_tiles(n);
+  hipLaunchKernelGGL(k_scan32_reduce, dim3((unsigned)tiles), dim3(kBlock), 0, stream, in, n, part);
+  hipLaunchKernelGGL(k_scan32_parts, dim3(1), dim3(kBlock), 0, stream, part, tiles);
+  hipLaunchKernelGGL(k_scan32_write, dim3((unsigned)tiles), dim3(kBlock), 0, stream, in, n, (const int*)part, out);
+}
+
+}  // namespace atlhip

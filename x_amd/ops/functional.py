@@ -13,6 +13,7 @@ semantics of :mod:`x_amd.ops.reference`, as the reference does without its exten
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass, field
 from typing import Optional
@@ -21,7 +22,7 @@ import numpy as np
 import torch
 
 from . import reference as ref
-from ._ext import F32, I64, call, ext_supports, get_ext, load_library, ptr, stream_of
+from ._ext import F32, I64, FastGeometry, HipLibraryError, call, ext_supports, get_ext, load_library, ptr, stream_of
 
 
 def _f32(t):
@@ -336,14 +337,79 @@ class _ATSPair(torch.autograd.Function):
         return gv, None, None, None, None
 
 
+class FastPairPlan:
+    """Device workspace of the fused pair-sum path (include/atl_hip.h, atl_fast_*): the reference's (source,
+    slice) entries and the anchors binned on a fixed fine-cell grid, built without a host synchronisation.
+    Holds its inputs alive for as long as it is used."""
+
+    def __init__(self, x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, anchor_xy=None):
+        dev = x.device
+        self.x, self.t, self.v = _f32(x), _f32(t), _f32(v.detach())
+        self.b, self.anchors = b.contiguous().long(), anchors.contiguous().long()
+        self.anchor_xy = None if anchor_xy is None else _f32(anchor_xy.detach())
+        N, M = self.t.shape[0], self.anchors.shape[0]
+        if self.x.shape != (N, 2) or self.v.shape != (N, 2) or self.b.shape != (N,):
+            raise ValueError("x, v must be (N, 2) and t, b (N,)")
+        if self.anchor_xy is not None and self.anchor_xy.shape != (M, 2):
+            raise ValueError("anchor_xy must be (M, 2)")
+        self.N, self.M, self.device = N, M, dev
+        self.geo = FastGeometry()
+        lib = load_library()
+        if lib.atl_fast_geometry_init(N, M, int(B), int(H), int(W), int(n_slices), float(h), float(tau), float(cut),
+                                      ctypes.byref(self.geo)) != 0:
+            raise HipLibraryError("atl_fast_geometry_init: " + lib.atl_last_error().decode(errors="replace"))
+        self.ws = torch.empty(int(self.geo.ws_bytes), dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            call("atl_fast_plan", ctypes.byref(self.geo), ptr(self.x), ptr(self.t), ptr(self.v), ptr(self.b),
+                 ptr(self.anchors), ptr(self.anchor_xy), ptr(self.ws), int(self.geo.ws_bytes), stream_of(self.x))
+
+    def forward(self, count: Optional[torch.Tensor] = None) -> torch.Tensor:
+        out = torch.zeros(self.M, dtype=F32, device=self.device)
+        with torch.cuda.device(self.device):
+            call("atl_fast_pair_fwd", ctypes.byref(self.geo), ptr(self.ws), ptr(out), ptr(count), stream_of(out))
+        return out
+
+    def backward(self, gS: torch.Tensor) -> torch.Tensor:
+        gS = _f32(gS)
+        if gS.shape != (self.M,):
+            raise ValueError(f"gS has shape {tuple(gS.shape)}, expected ({self.M},)")
+        gv = torch.zeros(self.N, 2, dtype=F32, device=self.device)
+        with torch.cuda.device(self.device):
+            call("atl_fast_pair_bwd", ctypes.byref(self.geo), ptr(self.ws), ptr(gS), ptr(gv), stream_of(gv))
+        return gv
+
+    def counts(self) -> torch.Tensor:
+        """n_i: number of contributing pairs of every anchor (bit-identical to the reference's visits)."""
+        cnt = torch.zeros(self.M, dtype=torch.int32, device=self.device)
+        self.forward(count=cnt)
+        return cnt
+
+
+class _ATSPairFast(torch.autograd.Function):
+    """atl/ops/functional.py:181-196 on the fused path: plan and forward in one go, gradient to v only."""
+
+    @staticmethod
+    def forward(ctx, v, x, t, b, anchors, anchor_xy, B, H, W, h, tau, cut, n_slices):
+        plan = FastPairPlan(x, t, v, b, B, H, W, anchors, h, tau, cut, n_slices, anchor_xy)
+        ctx.plan = plan
+        return plan.forward()
+
+    @staticmethod
+    def backward(ctx, g):
+        gv = ctx.plan.backward(g)
+        return gv, None, None, None, None, None, None, None, None, None, None, None, None
+
+
 def ats_pair_sums(x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, force_ref=False, anchor_xy=None):
     """S_i = sum_{j != i} 1[|t_i - t_j| <= tau] exp(-|x_i - x_j - v_j (t_i - t_j)|^2 / 2h^2) for anchors i
     (atl/ops/functional.py:199-207).  ``x`` are raw event positions, ``v`` per-event velocities in px per
-    window; the gradient flows to ``v`` only."""
+    window; the gradient flows to ``v`` only.  Device tensors run the fused HIP path (same contributing pairs
+    as the reference's plan + kernel, no host synchronisation)."""
     if force_ref or not ext_supports(x):
         return ref.ats_pair_sums(x.float(), t.float(), v.float(), b, anchors, h, tau, cut, anchor_xy=anchor_xy)
-    plan = build_pair_plan(x, t, v, b, B, H, W, anchors, h, tau, cut, n_slices, anchor_xy=anchor_xy)
-    return _ATSPair.apply(v.float(), plan, h, tau, cut)
+    get_ext()
+    return _ATSPairFast.apply(v.float(), x.detach(), t.detach(), b, anchors, anchor_xy, int(B), int(H), int(W),
+                              float(h), float(tau), float(cut), int(n_slices))
 
 
 def pair_counts(plan: PairPlan, h, tau, cut) -> torch.Tensor:
