@@ -65,6 +65,17 @@ int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int
                         const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gfield,
                         hipStream_t stream);
 
+/* The same adjoint as a gather (deterministic, no atomics): atl_grid_plan sorts the positions by their base
+ * corner into a workspace of atl_grid_plan_bytes(B, Hg, Wg, N) bytes (-1 if the sizes are unsupported);
+ * atl_sample_grid_bwd_planned then sums, per grid node, the weighted gout of the positions around it.
+ * gfield accumulated; C <= 4.  The positions and img_h, img_w must be the ones the plan was built from. */
+int64_t atl_grid_plan_bytes(int64_t B, int64_t Hg, int64_t Wg, int64_t N);
+int atl_grid_plan(int64_t B, int64_t Hg, int64_t Wg, const float* pos, const int64_t* b, int64_t N, int64_t img_h,
+                  int64_t img_w, void* ws, int64_t ws_bytes, hipStream_t stream);
+int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                                int64_t N, int64_t img_h, int64_t img_w, const void* ws, float* gfield,
+                                hipStream_t stream);
+
 /* ---------------------------------------------------------------- pair plan (atl/ops/functional.py:132-178) */
 
 /* Reductions behind the plan geometry (functional.py:139,144-145): stats (5 ints, ordered-int encoding of
@@ -129,10 +140,10 @@ typedef struct atl_fast_geometry {
   double h, tau, cut;
   float gx0, gy0, gx1, gy1, cell;       /* clamp box and fine cell size (pixels) */
   float reserved_f;
-  int64_t GW, GH, ncell, max_span, ecap;
-  int64_t ws_bytes;
-  int64_t off_params, off_cnt, off_start, off_part, off_erank, off_arank, off_esv, off_eti, off_ekey, off_arec,
-      off_aid, off_akey, off_gss;
+  int64_t GW, GH, ncell, ncell_pad, max_span, ecap;
+  int64_t ws_bytes;                     /* workspace layout (byte offsets) */
+  int64_t off_params, off_cnt, off_boff, off_part, off_start, off_tkey, off_trec, off_esv, off_eti, off_ekey,
+      off_arec, off_aid, off_akey, off_gss, off_srec, off_sid, off_skey;
 } atl_fast_geometry;
 
 int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W, int64_t S, double h, double tau,

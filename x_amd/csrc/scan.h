@@ -4,6 +4,7 @@
 #include "common.h"
 
 namespace atlhip {
+namespace {   // one private copy per translation unit that includes this header
 
 constexpr int kScanItems = 8;
 constexpr int kScanTile = kBlock * kScanItems;
@@ -69,4 +70,5 @@ inline void scan32(const int* in, int64_t n, int* part, int* out, hipStream_t st
   hipLaunchKernelGGL(k_scan32_write, dim3((unsigned)tiles), dim3(kBlock), 0, stream, in, n, (const int*)part, out);
 }
 
+}  // namespace
 }  // namespace atlhip

@@ -25,7 +25,8 @@ def visible_fraction(motion, xa, ta, ba, ev: EventPacket, tau: float, n_check: i
     """Fraction of the sources within +-tau of each anchor recorded while the anchor's scene content was inside
     the field of view (atl/objectives/ats.py:31-50)."""
     if xa.is_cuda and getattr(motion, "linear_at_event", False):
-        va = motion.velocity(xa, ta, ba).detach()
+        with torch.no_grad():
+            va = motion.velocity(xa, ta, ba)
         return visible_fraction_linear(xa, va, ta, ba, ev.t, ev.b, ev.batch_size, ev.height, ev.width, tau, n_check)
     edges = torch.linspace(0, 1, n_check + 1, device=ev.device)
     centres = 0.5 * (edges[:-1] + edges[1:])

@@ -54,12 +54,15 @@ _SIGS = {
     "atl_visible_fraction": [_P, _P, _P, _P, _I, _P, _P, _I, _I, _D, _I, _I, _P, _P],
     "atl_anchored_epilogue_fwd": [_P, _P, _P, _I, _D, _D, _P, _P, _P, _P],
     "atl_anchored_epilogue_bwd": [_P, _P, _P, _I, _P, _P],
+    "atl_grid_plan_bytes": [_I, _I, _I, _I],
+    "atl_grid_plan": [_I, _I, _I, _P, _P, _I, _I, _I, _P, _I, _P],
+    "atl_sample_grid_bwd_planned": [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _P],
     "atl_fast_geometry_init": [_I, _I, _I, _I, _I, _I, _D, _D, _D, _P],
     "atl_fast_plan": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P],
     "atl_fast_pair_fwd": [_P, _P, _P, _P, _P],
     "atl_fast_pair_bwd": [_P, _P, _P, _P, _P],
 }
-_RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
+_RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.c_int64, "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):
     """Mirror of ``atl_fast_geometry`` (include/atl_hip.h): sizes, grid and workspace layout of the fused
@@ -68,10 +71,10 @@ class FastGeometry(ctypes.Structure):
                 [(n, ctypes.c_int64) for n in ("N", "M", "B", "H", "W", "S")] +
                 [(n, ctypes.c_double) for n in ("h", "tau", "cut")] +
                 [(n, ctypes.c_float) for n in ("gx0", "gy0", "gx1", "gy1", "cell", "reserved_f")] +
-                [(n, ctypes.c_int64) for n in ("GW", "GH", "ncell", "max_span", "ecap", "ws_bytes", "off_params",
-                                               "off_cnt", "off_start", "off_part", "off_erank", "off_arank",
-                                               "off_esv", "off_eti", "off_ekey", "off_arec", "off_aid", "off_akey",
-                                               "off_gss")])
+                [(n, ctypes.c_int64) for n in ("GW", "GH", "ncell", "ncell_pad", "max_span", "ecap", "ws_bytes",
+                                               "off_params", "off_cnt", "off_boff", "off_part", "off_start",
+                                               "off_tkey", "off_trec", "off_esv", "off_eti", "off_ekey", "off_arec",
+                                               "off_aid", "off_akey", "off_gss", "off_srec", "off_sid", "off_skey")])
 
 
 _LIB = None

@@ -127,17 +127,28 @@ def blur(img: torch.Tensor, sigma: float) -> torch.Tensor:
 
 # ------------------------------------------------------------------------------------------- flow grid
 class _SampleGrid(torch.autograd.Function):
-    """Bilinear border-clamped lookup of a (B, C, Hg, Wg) field (atl/motion/parametric.py:235-251)."""
+    """Bilinear border-clamped lookup of a (B, C, Hg, Wg) field (atl/motion/parametric.py:235-251).
+
+    When the field needs a gradient, the forward also sorts the positions by their base corner (a device
+    plan), so that the backward is a per-node gather instead of scattered atomic adds."""
 
     @staticmethod
-    def forward(ctx, fld, pos, b, img_h, img_w):
+    def forward(ctx, fld, pos, b, img_h, img_w, plan):
         fld, pos, b = _f32(fld), _f32(pos), b.contiguous().long()
         B, C, Hg, Wg = fld.shape
         N = pos.shape[0]
         out = torch.empty(N, C, device=pos.device, dtype=F32)
+        ctx.plan = None
         with torch.cuda.device(pos.device):
+            st = stream_of(pos)
             call("atl_sample_grid_fwd", ptr(fld), B, C, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w),
-                 ptr(out), stream_of(pos))
+                 ptr(out), st)
+            if plan and C <= 4:
+                nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N))
+                if nbytes >= 0:
+                    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=pos.device)
+                    call("atl_grid_plan", B, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w), ptr(ws), nbytes, st)
+                    ctx.plan = ws
         ctx.save_for_backward(pos, b)
         ctx.shape, ctx.img = (B, C, Hg, Wg), (int(img_h), int(img_w))
         return out
@@ -149,9 +160,13 @@ class _SampleGrid(torch.autograd.Function):
         gf = torch.zeros(B, C, Hg, Wg, device=pos.device, dtype=F32)
         g = g.contiguous().float()
         with torch.cuda.device(pos.device):
-            call("atl_sample_grid_bwd", ptr(g), B, C, Hg, Wg, ptr(pos), ptr(b), pos.shape[0], ctx.img[0], ctx.img[1],
-                 ptr(gf), stream_of(pos))
-        return gf, None, None, None, None
+            if ctx.plan is not None:
+                call("atl_sample_grid_bwd_planned", ptr(g), B, C, Hg, Wg, ptr(pos), pos.shape[0], ctx.img[0],
+                     ctx.img[1], ptr(ctx.plan), ptr(gf), stream_of(pos))
+            else:
+                call("atl_sample_grid_bwd", ptr(g), B, C, Hg, Wg, ptr(pos), ptr(b), pos.shape[0], ctx.img[0],
+                     ctx.img[1], ptr(gf), stream_of(pos))
+        return gf, None, None, None, None, None
 
 
 def sample_grid_hip(fld: torch.Tensor, pos: torch.Tensor, b: torch.Tensor, img_hw=(0, 0)) -> torch.Tensor:
@@ -160,7 +175,8 @@ def sample_grid_hip(fld: torch.Tensor, pos: torch.Tensor, b: torch.Tensor, img_h
     if pos.requires_grad:
         raise NotImplementedError("the HIP flow lookup differentiates w.r.t. the field only (positions are data)")
     get_ext()
-    return _SampleGrid.apply(fld, pos, b, img_hw[0], img_hw[1])
+    plan = fld.requires_grad and torch.is_grad_enabled()     # sort the positions for a gather backward
+    return _SampleGrid.apply(fld, pos, b, img_hw[0], img_hw[1], plan)
 
 
 # ------------------------------------------------------------------------------------------- anchored pairs
