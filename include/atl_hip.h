@@ -135,15 +135,14 @@ int atl_ats_pair_bwd(const float* gS, const float* src_y, const float* src_v, co
  * anchors (M) int64 event indices, anchor_xy (M,2) anchor positions or null (x[anchors]). */
 typedef struct atl_fast_geometry {
   int32_t version;                      /* ATL_HIP_ABI_VERSION once initialised */
-  int32_t reserved;
+  int32_t bucket_shift;                 /* log2 of the cell keys per sort bucket */
   int64_t N, M, B, H, W, S;
   double h, tau, cut;
   float gx0, gy0, gx1, gy1, cell;       /* clamp box and fine cell size (pixels) */
   float reserved_f;
   int64_t GW, GH, ncell, ncell_pad, max_span, ecap;
   int64_t ws_bytes;                     /* workspace layout (byte offsets) */
-  int64_t off_params, off_cnt, off_boff, off_part, off_start, off_tkey, off_trec, off_esv, off_eti, off_ekey,
-      off_arec, off_aid, off_akey, off_gss, off_srec, off_sid, off_skey;
+  int64_t off_params, off_cnt, off_boff, off_part, off_start, off_trec, off_erec, off_arec, off_srec;
 } atl_fast_geometry;
 
 int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W, int64_t S, double h, double tau,

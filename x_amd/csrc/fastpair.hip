@@ -34,12 +34,17 @@ using namespace atlhip;
 
 namespace {
 
-constexpr int kBucketShift = 12;                   // 4096 keys per bucket (two LDS arrays of 16 KB in pass 2)
-constexpr int kBucketKeys = 1 << kBucketShift;
-constexpr int kSortBlock = 512;                    // pass-2 workgroup
-constexpr int kSrcPerBlock = 1024;                 // pass-1 sources per block
-constexpr int kAncPerBlock = 4096;                 // pass-1 anchors per block
-constexpr int kUnroll = 4;                         // candidates per walk step (record arrays padded by this)
+// Buckets hold 2^bshift keys, bshift the smallest of kMinBucketShift.. that keeps the bucket count within
+// kMaxBuckets (the pass-1 LDS histogram).  Small buckets keep pass 2 balanced (two LDS arrays of 4 KB each).
+constexpr int kMinBucketShift = 10;
+constexpr int kMaxBucketShift = 13;
+constexpr int kMaxBuckets = 16384;
+constexpr int kSortBlock = 256;                    // pass-2 workgroup
+constexpr int kP1Block = 512;                      // pass-1 workgroup
+constexpr int kSrcPerBlock = 4096;                 // pass-1 sources per block (8 per thread)
+constexpr int kAncPerBlock = 8192;                 // pass-1 anchors per block (16 per thread)
+constexpr int kUnroll = 2;                         // candidates per walk step (record arrays padded by this)
+
 constexpr int kXcd = 8;                            // XCDs: consecutive workgroups go round-robin over them
 
 // Fixed geometry shared by every kernel (host-computed, passed by value).
@@ -52,7 +57,8 @@ struct FGeo {
   int ncell_pad;               // ncell rounded up to whole buckets: anchor keys start here, source keys at 2x
   int MS;                      // max slices per source
   int nblk_e, nblk_a;          // pass-1 blocks over sources, over anchors
-  int nbuckets;                // 3 * ncell_pad / kBucketKeys
+  int nbuckets;                // 3 * ncell_pad >> bshift
+  int bshift;                  // log2 of the keys per bucket
   float tau, half_delta, delta;
   float r2max, kexp, invh2;    // (cut*cut)*h*h, -log2(e)/(2 h h), 1/(h h)
   float cuth;                  // cut * h
@@ -65,11 +71,15 @@ struct FParams {
   int pad[6];
 };
 
-// Sort record: entries (y.x, y.y, v.x, v.y) + (t bits, j); anchors (x, y, t, at) + (a, m);
-// sources (x, y, v.x, v.y) + (t bits, j).
+// One 32-byte record per sorted item, written with a single scattered line (separate arrays would cost one
+// scattered cache line each, and scattered lines are what the sort pays for):
+//   entries  f = (y.x, y.y, v.x, v.y) at the slice centre, i = (t bits, source id, key, 0)
+//   anchors  f = (x, y, t, at),                            i = (event id, input position, key, gS bits)
+//   sources  f = (x, y, v.x, v.y),                         i = (t bits, source id, key, 0)
+// key is the cell key within the item's own key space (the tmp records carry the combined key).
 struct Rec {
   float4 f;
-  int2 i;
+  int4 i;
 };
 
 __device__ __forceinline__ float ordered_to_float(int i) { return __int_as_float(i >= 0 ? i : i ^ 0x7fffffff); }
@@ -166,7 +176,7 @@ __device__ __forceinline__ bool anchor_rec(int64_t m, const float2* x, const flo
   const int cx = cell_of(xa.x, G.gx0, G.gx1, G.cf, G.GW), cy = cell_of(xa.y, G.gy0, G.gy1, G.cf, G.GH);
   key = G.ncell_pad + ((((int)ba * G.S + s) * G.GH + cy) * G.GW + cx);
   rec.f = make_float4(xa.x, xa.y, ta, ta - slice_centre(s, G.delta));
-  rec.i = make_int2((int)a, (int)m);
+  rec.i = make_int4((int)a, (int)m, key, 0);
   return true;
 }
 
@@ -218,51 +228,61 @@ __global__ void __launch_bounds__(kBlock) k_fast_stats(const float2* __restrict_
 
 // Pass 1.  Blocks [0, nblk_e) cover kSrcPerBlock sources each (their entries and one source record keyed
 // by the cell of the own-slice entry), blocks [nblk_e, nblk_e + nblk_a) kAncPerBlock anchors each.
-// SCATTER = false: per-block bucket histogram into cnt[bucket * nblk + block].  SCATTER = true: each record
-// goes to cnt[bucket * nblk + block] (now the scanned offsets) + its LDS rank within (block, bucket).
+// SCATTER = false: per-block bucket histogram into cnt[bucket * nblk + block].  SCATTER = true: the block's
+// scanned offsets cnt[bucket * nblk + block] are loaded into LDS once, and each record takes its slot there.
 template <bool SCATTER>
-__global__ void __launch_bounds__(kBlock) k_sort_pass1(const float2* __restrict__ x, const float* __restrict__ t,
+__global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restrict__ x, const float* __restrict__ t,
                                                        const float2* __restrict__ v, const int64_t* __restrict__ b,
                                                        int64_t N, const int64_t* __restrict__ anchors,
                                                        const float2* __restrict__ anchor_xy, int64_t M, FGeo G,
-                                                       int* __restrict__ cnt, int* __restrict__ tkey,
-                                                       Rec* __restrict__ trec) {
+                                                       int* __restrict__ cnt, Rec* __restrict__ trec) {
   extern __shared__ int hist[];
   const int nblk = G.nblk_e + G.nblk_a;
-  for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) hist[i] = 0;
-  __syncthreads();
   const int blk = blockIdx.x;
+  for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) hist[i] = SCATTER ? cnt[i * nblk + blk] : 0;
+  __syncthreads();
   auto emit = [&](int key, const Rec& r) {
-    const int bucket = key >> kBucketShift;
+    const int bucket = key >> G.bshift;
     if (!SCATTER) {
       atomicAdd(hist + bucket, 1);
     } else {
-      const int pos = cnt[bucket * nblk + blk] + atomicAdd(hist + bucket, 1);
-      tkey[pos] = key;
-      trec[pos] = r;
+      trec[atomicAdd(hist + bucket, 1)] = r;
     }
   };
   if (blk < G.nblk_e) {
+    constexpr int per = kSrcPerBlock / kP1Block;
     const int64_t j0 = (int64_t)blk * kSrcPerBlock;
-    const int64_t j1 = j0 + kSrcPerBlock < N ? j0 + kSrcPerBlock : N;
-    for (int64_t j = j0 + threadIdx.x; j < j1; j += blockDim.x) {
-      const int64_t bj = b[j];
-      if (bj < 0 || bj >= G.B) continue;
-      const float tj = t[j];
-      const float2 xj = x[j], vj = v[j];
+    float2 xj[per], vj[per];
+    float tj[per];
+    int64_t bj[per];
+#pragma unroll
+    for (int u = 0; u < per; ++u) {              // all loads of the thread's sources first
+      const int64_t j = j0 + u * kP1Block + threadIdx.x;
+      bj[u] = j < N ? b[j] : -1;
+      if (j < N) {
+        tj[u] = t[j];
+        xj[u] = x[j];
+        vj[u] = v[j];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < per; ++u) {
+      const int64_t j = j0 + u * kP1Block + threadIdx.x;
+      if (bj[u] < 0 || bj[u] >= G.B) continue;
       int lo, hi;
-      slice_range(tj, G, lo, hi);
-      const int own = min(max((int)fminf(fmaxf(floorf(tj / G.delta), 0.f), (float)(G.S - 1)), lo), hi);
+      slice_range(tj[u], G, lo, hi);
+      const int own = min(max((int)fminf(fmaxf(floorf(tj[u] / G.delta), 0.f), (float)(G.S - 1)), lo), hi);
       for (int s = lo; s <= hi; ++s) {
         Rec r;
         float yx, yy;
-        const int key = entry_key(xj, vj, tj, (int)bj, s, G, yx, yy);
-        r.f = make_float4(yx, yy, vj.x, vj.y);
-        r.i = make_int2(__float_as_int(tj), (int)j);
+        const int key = entry_key(xj[u], vj[u], tj[u], (int)bj[u], s, G, yx, yy);
+        r.f = make_float4(yx, yy, vj[u].x, vj[u].y);
+        r.i = make_int4(__float_as_int(tj[u]), (int)j, key, 0);
         emit(key, r);
         if (s == own) {
-          r.f = make_float4(xj.x, xj.y, vj.x, vj.y);
-          emit(2 * G.ncell_pad + key, r);
+          r.f = make_float4(xj[u].x, xj[u].y, vj[u].x, vj[u].y);
+          r.i.z = 2 * G.ncell_pad + key;
+          emit(r.i.z, r);
         }
       }
     }
@@ -283,14 +303,14 @@ __global__ void __launch_bounds__(kBlock) k_sort_pass1(const float2* __restrict_
 
 // Pass 2: workgroup `bucket` sorts its records by cell.  start[key] (combined key space, 3 * ncell_pad + 1
 // offsets) receives the CSR; entry records land at [0, E), anchor records at [0, Mv) and source records at
-// [0, Nv) of their own arrays.
-__global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict__ boff, const int* __restrict__ tkey,
-                                                           const Rec* __restrict__ trec, FGeo G,
-                                                           int* __restrict__ start, float4* __restrict__ esv,
-                                                           int2* __restrict__ eti, int* __restrict__ ekey,
-                                                           float4* __restrict__ arec, int2* __restrict__ aid,
-                                                           int* __restrict__ akey, float4* __restrict__ srec,
-                                                           int2* __restrict__ sid, int* __restrict__ skey) {
+// [0, Nv) of their own arrays.  Every thread handles kSortItems records per round, all loads issued first.
+constexpr int kSortItems = 8;
+
+template <int SHIFT>
+__global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict__ boff, const Rec* __restrict__ trec,
+                                                           FGeo G, int* __restrict__ start, Rec* __restrict__ erec,
+                                                           Rec* __restrict__ arec, Rec* __restrict__ srec) {
+  constexpr int kBucketKeys = 1 << SHIFT;
   __shared__ int cnt[kBucketKeys];
   __shared__ int cur[kBucketKeys];
   __shared__ int wsum[kSortBlock / kWave + 1];
@@ -298,14 +318,25 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
   const int bucket = blockIdx.x;
   const int lo = boff[bucket * nblk];
   const int hi = boff[(bucket + 1) * nblk];        // boff has nbuckets * nblk + 1 entries (total last)
-  const int bpk = G.ncell_pad >> kBucketShift;     // buckets per key space
+  const int bpk = G.ncell_pad >> SHIFT;            // buckets per key space
   const int E = boff[bpk * nblk], EA = boff[2 * bpk * nblk];
+  const int4* tki = (const int4*)trec;             // int half of record p: tki[2 * p + 1]
   for (int i = threadIdx.x; i < kBucketKeys; i += kSortBlock) {
     cnt[i] = 0;
     cur[i] = 0;
   }
   __syncthreads();
-  for (int p = lo + threadIdx.x; p < hi; p += kSortBlock) atomicAdd(cnt + (tkey[p] & (kBucketKeys - 1)), 1);
+  for (int base = lo; base < hi; base += kSortBlock * kSortItems) {
+    int key[kSortItems];
+#pragma unroll
+    for (int u = 0; u < kSortItems; ++u) {
+      const int p = base + u * kSortBlock + threadIdx.x;
+      key[u] = p < hi ? tki[2 * p + 1].z : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kSortItems; ++u)
+      if (key[u] >= 0) atomicAdd(cnt + (key[u] & (kBucketKeys - 1)), 1);
+  }
   __syncthreads();
   constexpr int per = kBucketKeys / kSortBlock;
   int vals[per];
@@ -317,7 +348,7 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
   }
   int total;
   int run = block_exclusive_scan<kSortBlock>(s, wsum, total);
-  const int base_key = bucket << kBucketShift;
+  const int base_key = bucket << SHIFT;
 #pragma unroll
   for (int k = 0; k < per; ++k) {
     const int i = threadIdx.x * per + k;
@@ -328,38 +359,35 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
   if (bucket == G.nbuckets - 1 && threadIdx.x == 0) start[3 * G.ncell_pad] = hi;
   __syncthreads();
   const int space = bucket / bpk;                  // 0 entries, 1 anchors, 2 sources
-  for (int p = lo + threadIdx.x; p < hi; p += kSortBlock) {
-    const int key = tkey[p];
-    const int kk = key & (kBucketKeys - 1);
-    const int pos = lo + cnt[kk] + atomicAdd(cur + kk, 1);
-    const Rec r = trec[p];
-    if (space == 0) {
-      esv[pos] = r.f;
-      eti[pos] = r.i;
-      ekey[pos] = key;
-    } else if (space == 1) {
-      arec[pos - E] = r.f;
-      aid[pos - E] = r.i;
-      akey[pos - E] = key - G.ncell_pad;
-    } else {
-      srec[pos - EA] = r.f;
-      sid[pos - EA] = r.i;
-      skey[pos - EA] = key - 2 * G.ncell_pad;
+  const int off = space == 0 ? 0 : (space == 1 ? E : EA);
+  Rec* out = space == 0 ? erec : (space == 1 ? arec : srec);
+  const int kbase = space * G.ncell_pad;
+  for (int base = lo; base < hi; base += kSortBlock * kSortItems) {
+    Rec r[kSortItems];
+    bool live[kSortItems];
+#pragma unroll
+    for (int u = 0; u < kSortItems; ++u) {
+      const int p = base + u * kSortBlock + threadIdx.x;
+      live[u] = p < hi;
+      if (live[u]) r[u] = trec[p];
+    }
+#pragma unroll
+    for (int u = 0; u < kSortItems; ++u) {
+      if (live[u]) {
+        const int kk = r[u].i.z & (kBucketKeys - 1);
+        const int pos = lo + cnt[kk] + atomicAdd(cur + kk, 1) - off;
+        r[u].i.z -= kbase;
+        out[pos] = r[u];
+      }
     }
   }
 }
 
 // ------------------------------------------------------------------------------------------ pair walks
 struct FPlan {
-  const float4* esv;           // entries: (y.x, y.y, v.x, v.y) at the slice centre
-  const int2* eti;             // entries: (t bits, source id)
-  const int* ekey;
-  const float4* arec;          // anchors: (x, y, t, at)
-  const int2* aid;             // anchors: (event id, input position)
-  const int* akey;
-  const float4* srec;          // sources: (x, y, v.x, v.y) in own-slice cell order
-  const int2* sid;             // sources: (t bits, source id)
-  const int* skey;             // own-slice entry key
+  const Rec* erec;             // entries in cell order
+  Rec* arec;                   // anchors in cell order (the backward stores gS in i.w)
+  const Rec* srec;             // sources in own-slice cell order
   const int* start;            // 3*ncell_pad + 1: entry cells, anchor cells (offset by E), source cells
   const FParams* P;
 };
@@ -529,9 +557,10 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
   R2 = unif(R2);
   const bool have = lane < n;
   const int q = wbase + min(lane, n - 1);
-  const float4 A = p.arec[q];
-  const int2 ai = p.aid[q];
-  const int key = p.akey[q];
+  const Rec AR = p.arec[q];
+  const float4 A = AR.f;
+  const int4 ai = AR.i;
+  const int key = ai.z;
   const int plane_cells = G.GH * G.GW;
   float mine = 0.f;
   int mine_n = 0;
@@ -563,8 +592,9 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
       }
       group_walk(p.start, 0, g * plane_cells, x0, x0 + G.cf, y0, y0 + G.cf, R, R2, G, [&](int pos) {
         const uint32_t k = (uint32_t)max(pos, 0);
-        const int2 ti = ld(p.eti, k);
-        const float4 e = ld(p.esv, k);
+        const Rec er = ld(p.erec, k);
+        const float4 e = er.f;
+        const int4 ti = er.i;
         const float ts = __int_as_float(ti.x);
 #pragma unroll
         for (int a = 0; a < kGroup; ++a) {
@@ -596,20 +626,18 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
   }
 }
 
-// gS in anchor (cell) order.
-__global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int M, const float* __restrict__ gS,
-                                                           float* __restrict__ gss) {
+// gS of every anchor into its record (i.w), for the backward's candidate loads.
+__global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int M, const float* __restrict__ gS) {
   const int q = blockIdx.x * blockDim.x + threadIdx.x;
   const int Mv = p.start[2 * G.ncell_pad] - p.start[G.ncell_pad];
   if (q >= Mv || q >= M) return;
-  gss[q] = gS[p.aid[q].y];
+  p.arec[q].i.w = __float_as_int(gS[p.arec[q].i.y]);
 }
 
 // Backward: every source (one lane each, own-slice cell order) sums, over the anchors of each slice of its
 // range within R of its slice-centre position, gS_i * k * dt / h^2 * r (csrc/atl_cpu.cpp:240-248);
 // gv[j] += the total (each source once: no atomics).
-__global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, const float* __restrict__ gss,
-                                                     float2* __restrict__ gv) {
+__global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, float2* __restrict__ gv) {
   const int lb = xcd_block((N + kBlock - 1) / kBlock);
   if (lb < 0) return;
   const int lane = threadIdx.x & (kWave - 1);
@@ -626,9 +654,10 @@ __global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, con
   R2 = unif(R2);
   const bool have = lane < n;
   const int q = wbase + min(lane, n - 1);
-  const float4 sr = p.srec[q];
-  const int2 si = p.sid[q];
-  const int key = p.skey[q];
+  const Rec SR = p.srec[q];
+  const float4 sr = SR.f;
+  const int4 si = SR.i;
+  const int key = si.z;
   const float tj = __int_as_float(si.x);
   int lo_l, hi_l;
   slice_range(tj, G, lo_l, hi_l);
@@ -644,22 +673,16 @@ __global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, con
       sv.w = sr.w;
       const float qx = clampf(sv.x, G.gx0, G.gx1), qy = clampf(sv.y, G.gy0, G.gy1);
       walk(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, nr, G, [&](int k, int e) {
-        int2 aidk[kUnroll];
-        float4 A[kUnroll];
-        float gs[kUnroll];
+        Rec ar[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          aidk[u] = ld(p.aid, (uint32_t)(k + u));
-          A[u] = ld(p.arec, (uint32_t)(k + u));
-          gs[u] = ld(gss, (uint32_t)(k + u));
-        }
+        for (int u = 0; u < kUnroll; ++u) ar[u] = ld((const Rec*)p.arec, (uint32_t)(k + u));
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
           float dt, rx, ry, d2;
-          const bool ok = pair_test(aidk[u].x, si.y, A[u].z, tj, A[u].x, A[u].y, A[u].w, sv, G, dt, rx, ry, d2) &
-                          (k + u < e);
+          const float4 A = ar[u].f;
+          const bool ok = pair_test(ar[u].i.x, si.y, A.z, tj, A.x, A.y, A.w, sv, G, dt, rx, ry, d2) & (k + u < e);
           const float kern = __builtin_amdgcn_exp2f(d2 * G.kexp);
-          const float f = gs[u] * kern * dt * G.invh2;
+          const float f = __int_as_float(ar[u].i.w) * kern * dt * G.invh2;
           mgx = ok ? fmaf(f, rx, mgx) : mgx;
           mgy = ok ? fmaf(f, ry, mgy) : mgy;
         }
@@ -684,7 +707,9 @@ bool make_geo(const atl_fast_geometry* geo, FGeo& G) {
   G.ncell = (int)geo->ncell; G.ncell_pad = (int)geo->ncell_pad; G.MS = (int)geo->max_span;
   G.nblk_e = (int)((geo->N + kSrcPerBlock - 1) / kSrcPerBlock);
   G.nblk_a = (int)((geo->M + kAncPerBlock - 1) / kAncPerBlock);
-  G.nbuckets = (int)(3 * geo->ncell_pad / kBucketKeys);
+  G.bshift = geo->bucket_shift;
+  if (G.bshift < kMinBucketShift || G.bshift > kMaxBucketShift) return false;
+  G.nbuckets = (int)((3 * geo->ncell_pad) >> G.bshift);
   const double delta = 1.0 / (double)geo->S;
   G.tau = (float)geo->tau;
   G.half_delta = (float)(delta / 2);
@@ -703,15 +728,9 @@ T* at_off(void* ws, int64_t off) { return (T*)((char*)ws + off); }
 
 FPlan make_plan(void* ws, const atl_fast_geometry* geo) {
   FPlan p;
-  p.esv = at_off<float4>(ws, geo->off_esv);
-  p.eti = at_off<int2>(ws, geo->off_eti);
-  p.ekey = at_off<int>(ws, geo->off_ekey);
-  p.arec = at_off<float4>(ws, geo->off_arec);
-  p.aid = at_off<int2>(ws, geo->off_aid);
-  p.akey = at_off<int>(ws, geo->off_akey);
-  p.srec = at_off<float4>(ws, geo->off_srec);
-  p.sid = at_off<int2>(ws, geo->off_sid);
-  p.skey = at_off<int>(ws, geo->off_skey);
+  p.erec = at_off<Rec>(ws, geo->off_erec);
+  p.arec = at_off<Rec>(ws, geo->off_arec);
+  p.srec = at_off<Rec>(ws, geo->off_srec);
   p.start = at_off<int>(ws, geo->off_start);
   p.P = at_off<FParams>(ws, geo->off_params);
   return p;
@@ -755,13 +774,20 @@ int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W
   if (ms > S) ms = S;
   g.max_span = ms;
   const double ecap = (double)N * (double)ms;
-  const double ncell_pad = std::ceil(ncell / kBucketKeys) * kBucketKeys;
-  const double nbuckets = 3 * ncell_pad / kBucketKeys;
+  int shift = kMinBucketShift;
+  double ncell_pad = 0, nbuckets = 0;
+  for (; shift <= kMaxBucketShift; ++shift) {
+    const double keys = std::ldexp(1.0, shift);
+    ncell_pad = std::ceil(ncell / keys) * keys;
+    nbuckets = 3 * ncell_pad / keys;
+    if (nbuckets <= kMaxBuckets) break;
+  }
   const double nblk = std::ceil((double)N / kSrcPerBlock) + std::ceil((double)M / kAncPerBlock);
-  if (3 * ncell_pad + 1 >= 2.0e9 || ecap + M + N >= 2.0e9 || nbuckets > 16384 || nbuckets * nblk + 1 >= 2.0e9) {
+  if (3 * ncell_pad + 1 >= 2.0e9 || ecap + M + N >= 2.0e9 || nbuckets > kMaxBuckets || nbuckets * nblk + 1 >= 2.0e9) {
     set_error("fast_geometry_init: problem too large for the 32-bit plan (cells %.0f, entries %.0f)", ncell, ecap);
     return 1;
   }
+  g.bucket_shift = shift;
   g.ncell = (int64_t)ncell;
   g.ncell_pad = (int64_t)ncell_pad;
   g.ecap = (int64_t)ecap;
@@ -773,19 +799,11 @@ int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W
   g.off_boff = off;    off += align256((nbh + 1) * 4);
   g.off_part = off;    off += align256((scan_tiles(nbh > 0 ? nbh : 1) + 1) * 4);
   g.off_start = off;   off += align256((3 * g.ncell_pad + 1) * 4);
-  g.off_tkey = off;    off += align256(ntmp * 4);
   g.off_trec = off;    off += align256(ntmp * (int64_t)sizeof(Rec));
   // the walks read up to kUnroll - 1 records past a range end: entry and anchor arrays carry that padding
-  g.off_esv = off;     off += align256((g.ecap + kUnroll) * 16);
-  g.off_eti = off;     off += align256((g.ecap + kUnroll) * 8);
-  g.off_ekey = off;    off += align256(g.ecap * 4);
-  g.off_arec = off;    off += align256((M + kUnroll) * 16);
-  g.off_aid = off;     off += align256((M + kUnroll) * 8);
-  g.off_akey = off;    off += align256(M * 4);
-  g.off_gss = off;     off += align256((M + kUnroll) * 4);
-  g.off_srec = off;    off += align256(N * 16);
-  g.off_sid = off;     off += align256(N * 8);
-  g.off_skey = off;    off += align256(N * 4);
+  g.off_erec = off;    off += align256((g.ecap + kUnroll) * (int64_t)sizeof(Rec));
+  g.off_arec = off;    off += align256((M + kUnroll) * (int64_t)sizeof(Rec));
+  g.off_srec = off;    off += align256(N * (int64_t)sizeof(Rec));
   g.ws_bytes = off;
   *geo = g;
   return 0;
@@ -802,7 +820,6 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
   int* cnt = at_off<int>(ws, geo->off_cnt);
   int* boff = at_off<int>(ws, geo->off_boff);
   int* part = at_off<int>(ws, geo->off_part);
-  int* tkey = at_off<int>(ws, geo->off_tkey);
   Rec* trec = at_off<Rec>(ws, geo->off_trec);
   const int nblk = G.nblk_e + G.nblk_a;
   const int64_t nbh = (int64_t)G.nbuckets * nblk;
@@ -816,20 +833,19 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
   }
   const size_t lds = (size_t)G.nbuckets * sizeof(int);
   if (nblk > 0) {
-    hipLaunchKernelGGL(k_sort_pass1<false>, dim3(nblk), dim3(kBlock), lds, stream, (const float2*)x, t,
-                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, (int*)nullptr,
-                       (Rec*)nullptr);
+    hipLaunchKernelGGL(k_sort_pass1<false>, dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
+                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, (Rec*)nullptr);
     scan32(cnt, nbh, part, boff, stream);
-    hipLaunchKernelGGL(k_sort_pass1<true>, dim3(nblk), dim3(kBlock), lds, stream, (const float2*)x, t,
-                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, boff, tkey, trec);
+    hipLaunchKernelGGL(k_sort_pass1<true>, dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
+                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, boff, trec);
   } else {
     hipLaunchKernelGGL(k_fill_zero, dim3(1), dim3(64), 0, stream, boff, (int64_t)1);
   }
-  hipLaunchKernelGGL(k_sort_pass2, dim3(G.nbuckets), dim3(kSortBlock), 0, stream, (const int*)boff,
-                     (const int*)tkey, (const Rec*)trec, G, at_off<int>(ws, geo->off_start),
-                     at_off<float4>(ws, geo->off_esv), at_off<int2>(ws, geo->off_eti), at_off<int>(ws, geo->off_ekey),
-                     at_off<float4>(ws, geo->off_arec), at_off<int2>(ws, geo->off_aid), at_off<int>(ws, geo->off_akey),
-                     at_off<float4>(ws, geo->off_srec), at_off<int2>(ws, geo->off_sid), at_off<int>(ws, geo->off_skey));
+  auto pass2 = G.bshift == 10 ? k_sort_pass2<10> : G.bshift == 11 ? k_sort_pass2<11>
+             : G.bshift == 12 ? k_sort_pass2<12> : k_sort_pass2<13>;
+  hipLaunchKernelGGL(pass2, dim3(G.nbuckets), dim3(kSortBlock), 0, stream, (const int*)boff,
+                     (const Rec*)trec, G, at_off<int>(ws, geo->off_start), at_off<Rec>(ws, geo->off_erec),
+                     at_off<Rec>(ws, geo->off_arec), at_off<Rec>(ws, geo->off_srec));
   return check_launch("fast_plan");
 }
 
@@ -853,10 +869,9 @@ int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, f
   if (!ws || (geo->M > 0 && (!gS || !gv))) { set_error("fast_pair_bwd: null argument"); return 1; }
   if (geo->M == 0 || geo->N == 0) return 0;
   const FPlan p = make_plan(ws, geo);
-  float* gss = at_off<float>(ws, geo->off_gss);
-  hipLaunchKernelGGL(k_fast_gather_gs, dim3(grid_for(geo->M)), dim3(kBlock), 0, stream, p, G, (int)geo->M, gS, gss);
+  hipLaunchKernelGGL(k_fast_gather_gs, dim3(grid_for(geo->M)), dim3(kBlock), 0, stream, p, G, (int)geo->M, gS);
   hipLaunchKernelGGL(k_fast_bwd, dim3(xcd_grid((geo->N + kBlock - 1) / kBlock)), dim3(kBlock), 0, stream, p, G,
-                     (int)geo->N, (const float*)gss, (float2*)gv);
+                     (int)geo->N, (float2*)gv);
   return check_launch("fast_pair_bwd");
 }
 

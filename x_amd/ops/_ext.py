@@ -67,14 +67,13 @@ _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.
 class FastGeometry(ctypes.Structure):
     """Mirror of ``atl_fast_geometry`` (include/atl_hip.h): sizes, grid and workspace layout of the fused
     pair-sum path, filled by ``atl_fast_geometry_init``."""
-    _fields_ = ([("version", ctypes.c_int32), ("reserved", ctypes.c_int32)] +
+    _fields_ = ([("version", ctypes.c_int32), ("bucket_shift", ctypes.c_int32)] +
                 [(n, ctypes.c_int64) for n in ("N", "M", "B", "H", "W", "S")] +
                 [(n, ctypes.c_double) for n in ("h", "tau", "cut")] +
                 [(n, ctypes.c_float) for n in ("gx0", "gy0", "gx1", "gy1", "cell", "reserved_f")] +
                 [(n, ctypes.c_int64) for n in ("GW", "GH", "ncell", "ncell_pad", "max_span", "ecap", "ws_bytes",
                                                "off_params", "off_cnt", "off_boff", "off_part", "off_start",
-                                               "off_tkey", "off_trec", "off_esv", "off_eti", "off_ekey", "off_arec",
-                                               "off_aid", "off_akey", "off_gss", "off_srec", "off_sid", "off_skey")])
+                                               "off_trec", "off_erec", "off_arec", "off_srec")])
 
 
 _LIB = None
