@@ -73,6 +73,15 @@ def test_fast_anchor_subsets_and_raw_positions():
     check_against_oracle(xs, win.t, v, win.b, 2, 40, 48, every3, None, 1.0, 0.2, 16)
 
 
+def test_fast_duplicate_anchors():
+    """An event listed twice among the anchors: both records skip exactly their own event (leave-one-out by id,
+    the backward's fallback from the own-record position test)."""
+    win, xs, v, xa = _case(seed=15)
+    anchors = np.concatenate([np.arange(0, win.n, 2), np.arange(0, win.n, 6)])
+    check_against_oracle(xs, win.t, v, win.b, 2, 40, 48, anchors, None, 1.0, 0.2, 16)
+    check_against_oracle(xs, win.t, v, win.b, 2, 40, 48, anchors, xa[anchors], 1.0, 0.2, 16)
+
+
 def test_fast_reference_test_shape():
     """tests/test_ops.py:62-77 shape: n=600, B=2, 20x24, positions in [-2, W+2), v = 6 N(0,1), h=1.5."""
     pos, _, b, t = rand_events(n=600, seed=3)

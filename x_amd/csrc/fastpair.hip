@@ -1,6 +1,7 @@
 // Fused anchored pair sums on gfx950: the reference's (source, slice) entries and the anchors binned into
-// one fixed, clamped fine-cell grid per slice, then a gather-form forward (one lane per anchor) and a
-// source-centric backward (one lane per entry), both walking a disc-pruned neighbourhood of fine cells.
+// one fixed, clamped fine-cell grid per slice, then a gather-form forward (the anchors of one cell share a
+// wave, whose lanes take the candidate entries of their neighbourhood) and a source-centric backward (one
+// lane per source, walking the anchors around all of its slices), both over disc-pruned rows of fine cells.
 //
 // What is kept identical to the reference (csrc/atl_cpu.cpp:176-253, atl/ops/functional.py:150-177):
 //   * the slice range of every source and its slice-centre position y = x + v (c_s - t), op for op in fp32;
@@ -17,9 +18,10 @@
 // max|at| are reduced on the device, so the whole path runs without a host synchronisation.
 //
 // The plan is a two-level counting sort with no per-item global atomics (scattered global atomics run at
-// ~25 G/s on MI355X, against ~450 G/s for coalesced traffic): pass 1 histograms 8192-key buckets in LDS per
-// block and scatters full records into bucket order; pass 2 gives every bucket one workgroup that sorts it
-// by cell with an LDS histogram and writes the cell offsets and the final records.  Entries and anchors
+// ~25 G/s on MI355X, against ~450 G/s for coalesced traffic): pass 1 histograms buckets of 1024 keys (more
+// for very fine grids) in LDS per block and scatters full records into bucket order; pass 2 gives every
+// bucket one workgroup that sorts it by cell with an LDS histogram and writes the cell offsets and the final
+// records.  Entries and anchors
 // share one key space (anchor keys offset by the padded cell count), so both sorts run in the same
 // launches.  The same sort also orders the sources by the cell of their own-slice position, and the
 // backward gives each source one lane that walks the anchors of all its slices: the gradient of a source
@@ -51,6 +53,7 @@ constexpr int kXcd = 8;                            // XCDs: consecutive workgrou
 struct FGeo {
   float gx0, gy0, gx1, gy1;    // clamp box; cell (0, 0) starts at (gx0, gy0)
   float cf;                    // fine cell size
+  float icf;                   // 1 / cf (fp32), for the walks' conservative cell lookups
   int GW, GH, S;
   int64_t B;
   int ncell;                   // B * S * GH * GW
@@ -68,7 +71,8 @@ struct FGeo {
 struct FParams {
   int vmax;                    // max ||v|| over sources
   int atmax;                   // max |t_a - c_s| over anchors
-  int pad[6];
+  int dup;                     // non-zero if an event occurs more than once among the anchors
+  int pad[5];
 };
 
 // One 32-byte record per sorted item, written with a single scattered line (separate arrays would cost one
@@ -84,20 +88,17 @@ struct Rec {
 
 __device__ __forceinline__ float ordered_to_float(int i) { return __int_as_float(i >= 0 ? i : i ^ 0x7fffffff); }
 
-// Search radius and neighbourhood half-width (in cells) from the device reductions.
-__device__ __forceinline__ void search_radius(const FParams* P, const FGeo& G, float& R, float& R2, int& nr) {
+// Search radius from the device reductions: every contributing pair lies within R of its query (cut*h and
+// the largest displacement v*at, each with relative slack, plus 0.01 px for fp32 rounding of positions).
+__device__ __forceinline__ void search_radius(const FParams* P, const FGeo& G, float& R, float& R2) {
   const float vmax = ordered_to_float(P->vmax), atmax = ordered_to_float(P->atmax);
   R = G.cuth * 1.000001f + vmax * atmax * 1.000001f + 0.01f;
-  const int lim = max(G.GW, G.GH);
   if (!(R < 1e30f)) {          // inf / NaN velocities: walk the whole slice
     R = 1e30f;
     R2 = 1e30f;
-    nr = lim;
     return;
   }
   R2 = R * R;
-  const float c = ceilf(R / G.cf);
-  nr = c < (float)lim ? (int)c : lim;
 }
 
 __device__ __forceinline__ int cell_of(float p, float lo, float hi, float cf, int n) {
@@ -107,6 +108,16 @@ __device__ __forceinline__ int cell_of(float p, float lo, float hi, float cf, in
 }
 
 __device__ __forceinline__ float clampf(float p, float lo, float hi) { return fminf(fmaxf(p, lo), hi); }
+
+// Cell of a walk bound (a query position -/+ a search half-width), by a multiplication with 1/cf instead of
+// the binning's division.  The two can differ only where the quotient lies within a few ulps (< 1e-4 cells)
+// of an integer; R carries 0.01 px (> 6e-3 cells) of slack beyond the largest distance a contributing pair
+// can have in fp32, so every cell that holds a contributing item is still inside [c(lo - w), c(lo + w)].
+__device__ __forceinline__ int cell_walk(float p, float lo, float hi, float icf, int n) {
+  const float c = fminf(fmaxf(p, lo), hi);          // NaN -> lo
+  const int i = (int)floorf((c - lo) * icf);
+  return min(max(i, 0), n - 1);
+}
 
 // Element i of an array through a 32-bit byte offset from a uniform base (lets the compiler use the
 // scalar-base + vector-offset addressing form instead of per-lane 64-bit address arithmetic).
@@ -146,8 +157,8 @@ __device__ __forceinline__ bool row_span(int r, float qx, float qy, float R, flo
   const float gap = fmaxf(0.f, fmaxf(row_lo - qy, qy - row_hi));
   if (gap > R) return false;
   const float w = sqrtf(fmaxf(R2 - gap * gap, 0.f));
-  c0 = cell_of(qx - w, G.gx0, G.gx1, G.cf, G.GW);
-  c1 = cell_of(qx + w, G.gx0, G.gx1, G.cf, G.GW);
+  c0 = cell_walk(qx - w, G.gx0, G.gx1, G.icf, G.GW);
+  c1 = cell_walk(qx + w, G.gx0, G.gx1, G.icf, G.GW);
   return true;
 }
 
@@ -184,6 +195,11 @@ __device__ __forceinline__ bool anchor_rec(int64_t m, const float2* x, const flo
 __global__ void __launch_bounds__(kBlock) k_fill_zero(int* __restrict__ p, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0;
+}
+
+__global__ void __launch_bounds__(kBlock) k_fill_i32(int* __restrict__ p, int64_t n, int v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
 }
 
 // vmax over velocities, max |at| over anchors: block maxima, then one atomic max per block (ordered ints;
@@ -309,7 +325,8 @@ constexpr int kSortItems = 8;
 template <int SHIFT>
 __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict__ boff, const Rec* __restrict__ trec,
                                                            FGeo G, int* __restrict__ start, Rec* __restrict__ erec,
-                                                           Rec* __restrict__ arec, Rec* __restrict__ srec) {
+                                                           Rec* __restrict__ arec, Rec* __restrict__ srec,
+                                                           int* __restrict__ self) {
   constexpr int kBucketKeys = 1 << SHIFT;
   __shared__ int cnt[kBucketKeys];
   __shared__ int cur[kBucketKeys];
@@ -378,6 +395,7 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
         const int pos = lo + cnt[kk] + atomicAdd(cur + kk, 1) - off;
         r[u].i.z -= kbase;
         out[pos] = r[u];
+        if (space == 1) self[r[u].i.x] = pos;     // the anchor's event id -> its record
       }
     }
   }
@@ -386,19 +404,13 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
 // ------------------------------------------------------------------------------------------ pair walks
 struct FPlan {
   const Rec* erec;             // entries in cell order
-  Rec* arec;                   // anchors in cell order (the backward stores gS in i.w)
+  const Rec* arec;             // anchors in cell order
   const Rec* srec;             // sources in own-slice cell order
+  float4* brec;                // anchors in cell order for the backward: (x, y, t, gS)
+  int* self;                   // per event: position of its own anchor record, -1 if it is no anchor
   const int* start;            // 3*ncell_pad + 1: entry cells, anchor cells (offset by E), source cells
-  const FParams* P;
+  FParams* P;
 };
-
-__device__ __forceinline__ void split_key(int key, const FGeo& G, int& g, int& cy, int& cx) {
-  const int plane = G.GH * G.GW;
-  g = key / plane;
-  const int r = key - g * plane;
-  cy = r / G.GW;
-  cx = r - cy * G.GW;
-}
 
 // One candidate pair, predicated: the reference's three tests (csrc/atl_cpu.cpp:187-197) in its fp32 order,
 // written as "not rejected" so that NaN distances count as visits exactly as there.
@@ -478,9 +490,8 @@ __device__ __forceinline__ float rdlanef(float v, int l) {
 // caller).  cstart offsets minus `base`.
 template <typename Visit>
 __device__ __forceinline__ void walk(const int* __restrict__ cstart, int base, int plane, float qx, float qy, float R,
-                                     float R2, int nr, const FGeo& G, Visit&& visit) {
-  const int cy = cell_of(qy, G.gy0, G.gy1, G.cf, G.GH);
-  const int rlo = max(cy - nr, 0), rhi = min(cy + nr, G.GH - 1);
+                                     float R2, const FGeo& G, Visit&& visit) {
+  const int rlo = cell_walk(qy - R, G.gy0, G.gy1, G.icf, G.GH), rhi = cell_walk(qy + R, G.gy0, G.gy1, G.icf, G.GH);
   for (int r = rlo; r <= rhi; ++r) {
     int c0, c1;
     if (!row_span(r, qx, qy, R, R2, G, c0, c1)) continue;
@@ -493,12 +504,17 @@ __device__ __forceinline__ void walk(const int* __restrict__ cstart, int base, i
 // Group walk: the candidates of the cells of plane `plane` that meet the R-neighbourhood of the box
 // [x0, x1] x [y0, y1], 64 per chunk: chunk(pos) with pos the lane's candidate index (-1 if idle).  Row
 // spans are fetched one row per lane and prefix-summed across the wave.  All arguments wave-uniform.
+// Up to kRowTable rows (the usual case: R / cf < 3) the row starts and offsets are read into scalars once
+// and every chunk maps its lanes with one compare and select per row; taller neighbourhoods take the
+// general loop.
+constexpr int kRowTable = 8;
+
 template <typename Chunk>
 __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int base, int plane, float x0, float x1,
                                            float y0, float y1, float R, float R2, const FGeo& G, Chunk&& chunk) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int rlo = uni(cell_of(y0 - R, G.gy0, G.gy1, G.cf, G.GH));
-  const int rhi = uni(cell_of(y1 + R, G.gy0, G.gy1, G.cf, G.GH));
+  const int rlo = uni(cell_walk(y0 - R, G.gy0, G.gy1, G.icf, G.GH));
+  const int rhi = uni(cell_walk(y1 + R, G.gy0, G.gy1, G.icf, G.GH));
   for (int rb = rlo; rb <= rhi; rb += kWave) {
     const int r = rb + lane;
     int s0 = 0, len = 0;
@@ -507,8 +523,8 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
       const float gap = fmaxf(0.f, fmaxf(row_lo - y1, y0 - row_hi));
       if (gap <= R) {
         const float w = sqrtf(fmaxf(R2 - gap * gap, 0.f));
-        const int c0 = cell_of(x0 - w, G.gx0, G.gx1, G.cf, G.GW);
-        const int c1 = cell_of(x1 + w, G.gx0, G.gx1, G.cf, G.GW);
+        const int c0 = cell_walk(x0 - w, G.gx0, G.gx1, G.icf, G.GW);
+        const int c1 = cell_walk(x1 + w, G.gx0, G.gx1, G.icf, G.GW);
         const int rowk = plane + r * G.GW;
         s0 = cstart[rowk + c0] - base;
         len = cstart[rowk + c1 + 1] - base - s0;
@@ -518,6 +534,23 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
     const int excl = incl - len;
     const int total = rdlane(incl, kWave - 1);
     const int nrb = min(kWave, rhi - rb + 1);   // rows of this batch
+    if (nrb <= kRowTable) {
+      // lanes >= nrb hold len 0 and excl = total, so their entries never match a valid index
+      int ex[kRowTable], of[kRowTable];
+#pragma unroll
+      for (int k = 0; k < kRowTable; ++k) {
+        ex[k] = rdlane(excl, k);
+        of[k] = rdlane(s0 - excl, k);
+      }
+      for (int c0 = 0; c0 < total; c0 += kWave) {
+        const int idx = c0 + lane;
+        int off = of[0];
+#pragma unroll
+        for (int k = 1; k < kRowTable; ++k) off = idx >= ex[k] ? of[k] : off;   // last row starting <= idx
+        chunk(idx < total ? idx + off : -1);
+      }
+      continue;
+    }
     int j = 0;                                  // first row that the current chunk may touch
     for (int c0 = 0; c0 < total; c0 += kWave) {
       const int idx = c0 + lane;
@@ -532,6 +565,53 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
         ++j;
       }
       chunk(pos);
+    }
+  }
+}
+
+// One pass of a group walk for WD wave-uniform anchors read from lanes src0 .. src0 + na - 1 (slots past na
+// repeat the last anchor and are discarded): lane `dst` of the wave receives anchor src0 + a's sum (and
+// count) in mine (mine_n).
+template <int WD, bool COUNT>
+__device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plane, float x0, float y0, float R,
+                                         float R2, const float4& A, const int4& ai, int src0, int na, int lane,
+                                         float& mine, int& mine_n) {
+  float ax[WD], ay[WD], ta[WD], at[WD], acc[WD];
+  int id[WD], cnt[WD];
+#pragma unroll
+  for (int a = 0; a < WD; ++a) {
+    const int src = src0 + min(a, na - 1);
+    ax[a] = rdlanef(A.x, src);
+    ay[a] = rdlanef(A.y, src);
+    ta[a] = rdlanef(A.z, src);
+    at[a] = rdlanef(A.w, src);
+    id[a] = rdlane(ai.x, src);
+    acc[a] = 0.f;
+    cnt[a] = 0;
+  }
+  group_walk(p.start, 0, plane, x0, x0 + G.cf, y0, y0 + G.cf, R, R2, G, [&](int pos) {
+    const Rec er = ld(p.erec, (uint32_t)max(pos, 0));
+    const float4 e = er.f;
+    const int4 ti = er.i;
+    const float ts = __int_as_float(ti.x);
+#pragma unroll
+    for (int a = 0; a < WD; ++a) {
+      float dt, rx, ry, d2;
+      const bool ok = pair_test(id[a], ti.y, ta[a], ts, ax[a], ay[a], at[a], e, G, dt, rx, ry, d2) & (pos >= 0);
+      const float kern = __builtin_amdgcn_exp2f(d2 * G.kexp);
+      acc[a] += ok ? kern : 0.f;
+      if (COUNT) cnt[a] += ok ? 1 : 0;
+    }
+  });
+#pragma unroll
+  for (int a = 0; a < WD; ++a) {
+    if (a < na) {
+      const float sa = wave_sum_f(acc[a]);
+      if (lane == src0 + a) mine = sa;
+      if (COUNT) {
+        const int ca = wave_sum_i(cnt[a]);
+        if (lane == src0 + a) mine_n = ca;
+      }
     }
   }
 }
@@ -551,8 +631,7 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
   if (wbase >= Mv) return;
   const int n = min(kWave, Mv - wbase);
   float R, R2;
-  int nr;
-  search_radius(p.P, G, R, R2, nr);
+  search_radius(p.P, G, R, R2);
   R = unif(R);
   R2 = unif(R2);
   const bool have = lane < n;
@@ -577,47 +656,15 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
     const float x0 = G.gx0 + (float)cx * G.cf, y0 = G.gy0 + (float)cy * G.cf;
     for (int a0 = 0; a0 < gsize; a0 += kGroup) {
       const int na = min(kGroup, gsize - a0);
-      float ax[kGroup], ay[kGroup], ta[kGroup], at[kGroup], acc[kGroup];
-      int id[kGroup], cnt[kGroup];
-#pragma unroll
-      for (int a = 0; a < kGroup; ++a) {
-        const int src = i + a0 + min(a, na - 1);
-        ax[a] = rdlanef(A.x, src);
-        ay[a] = rdlanef(A.y, src);
-        ta[a] = rdlanef(A.z, src);
-        at[a] = rdlanef(A.w, src);
-        id[a] = rdlane(ai.x, src);
-        acc[a] = 0.f;
-        cnt[a] = 0;
-      }
-      group_walk(p.start, 0, g * plane_cells, x0, x0 + G.cf, y0, y0 + G.cf, R, R2, G, [&](int pos) {
-        const uint32_t k = (uint32_t)max(pos, 0);
-        const Rec er = ld(p.erec, k);
-        const float4 e = er.f;
-        const int4 ti = er.i;
-        const float ts = __int_as_float(ti.x);
-#pragma unroll
-        for (int a = 0; a < kGroup; ++a) {
-          if (a < na) {
-            float dt, rx, ry, d2;
-            const bool ok = pair_test(id[a], ti.y, ta[a], ts, ax[a], ay[a], at[a], e, G, dt, rx, ry, d2) & (pos >= 0);
-            const float kern = __builtin_amdgcn_exp2f(d2 * G.kexp);
-            acc[a] += ok ? kern : 0.f;
-            if (COUNT) cnt[a] += ok ? 1 : 0;
-          }
-        }
-      });
-#pragma unroll
-      for (int a = 0; a < kGroup; ++a) {
-        if (a < na) {
-          const float sa = wave_sum_f(acc[a]);
-          if (lane == i + a0 + a) mine = sa;
-          if (COUNT) {
-            const int ca = wave_sum_i(cnt[a]);
-            if (lane == i + a0 + a) mine_n = ca;
-          }
-        }
-      }
+      const int plane = g * plane_cells;
+      if (na == 1)
+        fwd_pass<1, COUNT>(p, G, plane, x0, y0, R, R2, A, ai, i + a0, na, lane, mine, mine_n);
+      else if (na == 2)
+        fwd_pass<2, COUNT>(p, G, plane, x0, y0, R, R2, A, ai, i + a0, na, lane, mine, mine_n);
+      else if (na <= 4)
+        fwd_pass<4, COUNT>(p, G, plane, x0, y0, R, R2, A, ai, i + a0, na, lane, mine, mine_n);
+      else
+        fwd_pass<kGroup, COUNT>(p, G, plane, x0, y0, R, R2, A, ai, i + a0, na, lane, mine, mine_n);
     }
   }
   if (have) {
@@ -626,12 +673,65 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
   }
 }
 
-// gS of every anchor into its record (i.w), for the backward's candidate loads.
+// Backward records of the anchors in cell order, brec[q] = (x, y, t, gS): one 16-byte load per candidate in
+// the backward's per-lane walks (the anchor's at = t - c_s is recomputed there with the same fp32 operation).
+// Also checks that no event occurs twice among the anchors (self[id] then names only one of the records).
 __global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int M, const float* __restrict__ gS) {
   const int q = blockIdx.x * blockDim.x + threadIdx.x;
   const int Mv = p.start[2 * G.ncell_pad] - p.start[G.ncell_pad];
   if (q >= Mv || q >= M) return;
-  p.arec[q].i.w = __float_as_int(gS[p.arec[q].i.y]);
+  const Rec r = p.arec[q];
+  p.brec[q] = make_float4(r.f.x, r.f.y, r.f.z, gS[r.i.y]);
+  if (p.self[r.i.x] != q) p.P->dup = 1;
+}
+
+// One source's walk over the anchors of every slice of its range (csrc/atl_cpu.cpp:240-248): returns
+// sum_i gS_i * k * dt / h^2 * r.  The leave-one-out test compares the candidate's record position with the
+// position of the source's own anchor record (sp); with DUP (an event repeated among the anchors) it
+// compares event ids instead, as the reference does.
+template <bool DUP>
+__device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, float R, float R2, float4 sr, int sid,
+                                             float tj, int key, int sp) {
+  const int plane_cells = G.GH * G.GW;
+  const int* astart = p.start + G.ncell_pad;
+  const int E = uni(p.start[G.ncell_pad]);
+  const int* aid = (const int*)p.arec + 4;         // event id of record k: aid[8 * k]
+  int lo_l, hi_l;
+  slice_range(tj, G, lo_l, hi_l);
+  const int bj = key / (G.S * plane_cells);
+  float mgx = 0.f, mgy = 0.f;
+  for (int s = lo_l; s <= hi_l; ++s) {
+    float4 sv;
+    entry_key(make_float2(sr.x, sr.y), make_float2(sr.z, sr.w), tj, bj, s, G, sv.x, sv.y);
+    sv.z = sr.z;
+    sv.w = sr.w;
+    const float cs = slice_centre(s, G.delta);
+    const float qx = clampf(sv.x, G.gx0, G.gx1), qy = clampf(sv.y, G.gy0, G.gy1);
+    walk(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, [&](int k, int e) {
+      float4 A[kUnroll];
+      int id[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        A[u] = ld((const float4*)p.brec, (uint32_t)(k + u));
+        if (DUP) id[u] = ld(aid, 8u * (uint32_t)(k + u));
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const float at = A[u].z - cs;
+        const float dt = A[u].z - tj;
+        const float rx = A[u].x - (sv.x + sv.z * at);
+        const float ry = A[u].y - (sv.y + sv.w * at);
+        const float d2 = rx * rx + ry * ry;
+        const bool other = DUP ? id[u] != sid : k + u != sp;
+        const bool ok = other & !(fabsf(dt) > G.tau) & !(d2 > G.r2max) & (k + u < e);
+        const float kern = __builtin_amdgcn_exp2f(d2 * G.kexp);
+        const float f = A[u].w * kern * dt * G.invh2;
+        mgx = ok ? fmaf(f, rx, mgx) : mgx;
+        mgy = ok ? fmaf(f, ry, mgy) : mgy;
+      }
+    });
+  }
+  return make_float2(mgx, mgy);
 }
 
 // Backward: every source (one lane each, own-slice cell order) sums, over the anchors of each slice of its
@@ -642,59 +742,25 @@ __global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, flo
   if (lb < 0) return;
   const int lane = threadIdx.x & (kWave - 1);
   const int wbase = lb * kBlock + (threadIdx.x & ~(kWave - 1));
-  const int E = uni(p.start[G.ncell_pad]);
   const int EA = uni(p.start[2 * G.ncell_pad]);
   const int Nv = uni(p.start[3 * G.ncell_pad]) - EA;
   if (wbase >= Nv) return;
   const int n = min(kWave, Nv - wbase);
   float R, R2;
-  int nr;
-  search_radius(p.P, G, R, R2, nr);
+  search_radius(p.P, G, R, R2);
   R = unif(R);
   R2 = unif(R2);
-  const bool have = lane < n;
-  const int q = wbase + min(lane, n - 1);
-  const Rec SR = p.srec[q];
-  const float4 sr = SR.f;
+  if (lane >= n) return;
+  const Rec SR = p.srec[wbase + lane];
   const int4 si = SR.i;
-  const int key = si.z;
   const float tj = __int_as_float(si.x);
-  int lo_l, hi_l;
-  slice_range(tj, G, lo_l, hi_l);
-  const int* astart = p.start + G.ncell_pad;
-  const int plane_cells = G.GH * G.GW;
-  float mgx = 0.f, mgy = 0.f;
-  if (have) {
-    const int bj = key / (G.S * plane_cells);
-    for (int s = lo_l; s <= hi_l; ++s) {
-      float4 sv;
-      entry_key(make_float2(sr.x, sr.y), make_float2(sr.z, sr.w), tj, bj, s, G, sv.x, sv.y);
-      sv.z = sr.z;
-      sv.w = sr.w;
-      const float qx = clampf(sv.x, G.gx0, G.gx1), qy = clampf(sv.y, G.gy0, G.gy1);
-      walk(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, nr, G, [&](int k, int e) {
-        Rec ar[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) ar[u] = ld((const Rec*)p.arec, (uint32_t)(k + u));
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          float dt, rx, ry, d2;
-          const float4 A = ar[u].f;
-          const bool ok = pair_test(ar[u].i.x, si.y, A.z, tj, A.x, A.y, A.w, sv, G, dt, rx, ry, d2) & (k + u < e);
-          const float kern = __builtin_amdgcn_exp2f(d2 * G.kexp);
-          const float f = __int_as_float(ar[u].i.w) * kern * dt * G.invh2;
-          mgx = ok ? fmaf(f, rx, mgx) : mgx;
-          mgy = ok ? fmaf(f, ry, mgy) : mgy;
-        }
-      });
-    }
-  }
-  if (have) {
-    float2 o = gv[si.y];
-    o.x += mgx;
-    o.y += mgy;
-    gv[si.y] = o;
-  }
+  const int sp = p.self[si.y];
+  const float2 m = uni(p.P->dup) ? bwd_source<true>(p, G, R, R2, SR.f, si.y, tj, si.z, sp)
+                                 : bwd_source<false>(p, G, R, R2, SR.f, si.y, tj, si.z, sp);
+  float2 o = gv[si.y];
+  o.x += m.x;
+  o.y += m.y;
+  gv[si.y] = o;
 }
 
 // ------------------------------------------------------------------------------------------ host side
@@ -703,6 +769,7 @@ int64_t align256(int64_t n) { return (n + 255) & ~(int64_t)255; }
 bool make_geo(const atl_fast_geometry* geo, FGeo& G) {
   if (!geo || geo->version != ATL_HIP_ABI_VERSION) return false;
   G.gx0 = geo->gx0; G.gy0 = geo->gy0; G.gx1 = geo->gx1; G.gy1 = geo->gy1; G.cf = geo->cell;
+  G.icf = 1.f / G.cf;
   G.GW = (int)geo->GW; G.GH = (int)geo->GH; G.S = (int)geo->S; G.B = geo->B;
   G.ncell = (int)geo->ncell; G.ncell_pad = (int)geo->ncell_pad; G.MS = (int)geo->max_span;
   G.nblk_e = (int)((geo->N + kSrcPerBlock - 1) / kSrcPerBlock);
@@ -731,6 +798,8 @@ FPlan make_plan(void* ws, const atl_fast_geometry* geo) {
   p.erec = at_off<Rec>(ws, geo->off_erec);
   p.arec = at_off<Rec>(ws, geo->off_arec);
   p.srec = at_off<Rec>(ws, geo->off_srec);
+  p.brec = at_off<float4>(ws, geo->off_brec);
+  p.self = at_off<int>(ws, geo->off_self);
   p.start = at_off<int>(ws, geo->off_start);
   p.P = at_off<FParams>(ws, geo->off_params);
   return p;
@@ -804,6 +873,8 @@ int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W
   g.off_erec = off;    off += align256((g.ecap + kUnroll) * (int64_t)sizeof(Rec));
   g.off_arec = off;    off += align256((M + kUnroll) * (int64_t)sizeof(Rec));
   g.off_srec = off;    off += align256(N * (int64_t)sizeof(Rec));
+  g.off_brec = off;    off += align256((M + kUnroll) * (int64_t)sizeof(float4));
+  g.off_self = off;    off += align256(N * (int64_t)sizeof(int));
   g.ws_bytes = off;
   *geo = g;
   return 0;
@@ -841,11 +912,13 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
   } else {
     hipLaunchKernelGGL(k_fill_zero, dim3(1), dim3(64), 0, stream, boff, (int64_t)1);
   }
+  if (N > 0)
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(N)), dim3(kBlock), 0, stream, at_off<int>(ws, geo->off_self), N, -1);
   auto pass2 = G.bshift == 10 ? k_sort_pass2<10> : G.bshift == 11 ? k_sort_pass2<11>
              : G.bshift == 12 ? k_sort_pass2<12> : k_sort_pass2<13>;
   hipLaunchKernelGGL(pass2, dim3(G.nbuckets), dim3(kSortBlock), 0, stream, (const int*)boff,
                      (const Rec*)trec, G, at_off<int>(ws, geo->off_start), at_off<Rec>(ws, geo->off_erec),
-                     at_off<Rec>(ws, geo->off_arec), at_off<Rec>(ws, geo->off_srec));
+                     at_off<Rec>(ws, geo->off_arec), at_off<Rec>(ws, geo->off_srec), at_off<int>(ws, geo->off_self));
   return check_launch("fast_plan");
 }
 
