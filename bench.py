@@ -8,12 +8,23 @@ HBM.  Prints one JSON line (rank 0, N = 1) with events/s, the dominant kernel's 
 (the oracle's OpenMP restatement of the reference CPU path on this host's cores).
 
     python bench.py [--steps K] [--warmup W] [--sigma S] [--no-cpu]
+
+Two helpers for the rocprofv3 summaries under profiles/ (no GPU work beyond what they name):
+
+    python bench.py --calibrate-copy MB        # a plain f32 copy of MB MiB (read MB, write MB), 5 times
+    python bench.py --summarize DIR... --out FILE --title T --command C [--copy-mb MB]
+        # kernel table from *_kernel_stats.csv and per-dispatch counter means from *_counter_collection.csv;
+        # with --copy-mb, FETCH_SIZE / WRITE_SIZE are scaled by what they read for the calibration copy, and
+        # the per-launch HBM bytes of every kernel are recorded for bench.py's roofline "traffic"
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -25,7 +36,11 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 VALU_PEAK = 256 * 4 * 16 * 2.4e9      # fp32 lane-slots/s (non-packed): 256 CUs x 4 SIMD x 16 lanes x 2.4 GHz
+FP32_PEAK = 157.3e12                   # fp32 FLOP/s (packed FMA), MI355X
 SLOTS_FWD, SLOTS_BWD = 14, 16          # VALU lane-slots per contributing pair (forward, backward)
+FLOPS_FWD, FLOPS_BWD = 13, 19          # fp32 flops per contributing pair (FMA = 2, exp = 1)
+KERNEL_OF = {"atl_fast_pair_fwd": "k_fast_fwd<false>", "atl_fast_pair_bwd": "k_fast_bwd"}
+COUNTERS = ROOT / "profiles" / "anchored_score_1M_640x480_counters.md"
 
 
 def parse():
@@ -37,7 +52,93 @@ def parse():
     ap.add_argument("--events", type=int, default=1_000_000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=25.0, help="seconds of CPU baseline work, at most")
+    ap.add_argument("--calibrate-copy", type=float, default=0.0, metavar="MB")
+    ap.add_argument("--summarize", nargs="+", metavar="DIR")
+    ap.add_argument("--out")
+    ap.add_argument("--title", default="rocprofv3 summary")
+    ap.add_argument("--command", default="")
+    ap.add_argument("--copy-mb", type=float, default=0.0)
     return ap.parse_args()
+
+
+# ------------------------------------------------------------------------------------------- profiles
+def _short(name):
+    n = name.replace("(anonymous namespace)::", "").replace("void ", "")
+    if n.startswith("at::native"):
+        m = re.search(r"at::native::(?:\(anonymous namespace\)::)?(\w+)<[^<]*?(?:at::native::)?(\w+Functor\w*|\w+_kernel\w*)?",
+                      n)
+        return "torch " + n.split("<")[0].replace("at::native::", "") + (" " + m.group(2) if m and m.group(2) else "")
+    return n.split("(")[0]
+
+
+def summarize(dirs, out, title, command, copy_mb):
+    """Markdown summary of rocprofv3 csv output (kernel stats and counters), with the per-launch HBM traffic
+    of every kernel when a calibration copy of copy_mb MiB is among the counter runs."""
+    lines = [f"# {title}", "", "Command (repo root, on the MI355X):", "", f"    {command}", ""]
+    for f in sorted(sum((glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True) for d in dirs), [])):
+        rows = list(csv.DictReader(open(f)))
+        lines += ["| kernel | calls | avg us | total share |", "|---|---|---|---|"]
+        for r in rows[:24]:
+            lines.append(f"| {_short(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                         f"{float(r['Percentage']):.1f}% |")
+        lines.append("")
+    agg = {}
+    for f in sorted(sum((glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True) for d in dirs),
+                        [])):
+        for r in csv.DictReader(open(f)):
+            k = "calibration copy (torch.neg)" if "neg_kernel" in r["Kernel_Name"] else _short(r["Kernel_Name"])
+            agg.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    traffic = {}
+    if agg:
+        scale = {}
+        if copy_mb > 0:
+            want_kib = copy_mb * 1024.0
+            for k, cs in agg.items():
+                if k.startswith("calibration copy"):
+                    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+                        if c in cs:
+                            scale[c] = want_kib / (sum(cs[c]) / len(cs[c]))
+            lines += [f"Calibration: a plain copy of {copy_mb:g} MiB (torch.neg, f32) reads FETCH_SIZE = "
+                      f"{want_kib / scale.get('FETCH_SIZE', float('nan')):.0f} and WRITE_SIZE = "
+                      f"{want_kib / scale.get('WRITE_SIZE', float('nan')):.0f} (KiB per dispatch) for "
+                      f"{want_kib:.0f} KiB moved each way: scale factors {scale.get('FETCH_SIZE', float('nan')):.3f}"
+                      f" and {scale.get('WRITE_SIZE', float('nan')):.3f}.", ""]
+        lines += ["| kernel | counter | mean per dispatch | dispatches |", "|---|---|---|---|"]
+        for k in sorted(agg):
+            for c in sorted(agg[k]):
+                v = agg[k][c]
+                lines.append(f"| {k} | {c} | {sum(v) / len(v):.6g} | {len(v)} |")
+            if "FETCH_SIZE" in agg[k] and "WRITE_SIZE" in agg[k] and len(scale) == 2:
+                fetch = sum(agg[k]["FETCH_SIZE"]) / len(agg[k]["FETCH_SIZE"]) * scale["FETCH_SIZE"]
+                write = sum(agg[k]["WRITE_SIZE"]) / len(agg[k]["WRITE_SIZE"]) * scale["WRITE_SIZE"]
+                traffic[k] = (fetch + write) * 1024.0
+        lines.append("")
+    if traffic:
+        lines += ["HBM traffic per launch (calibrated FETCH_SIZE + WRITE_SIZE):", ""]
+        lines += [f"- {k}: {v / 1e6:.1f} MB" for k, v in sorted(traffic.items())]
+        lines += ["", f"<!-- traffic: {json.dumps(traffic)} -->"]
+    text = "\n".join(lines) + "\n"
+    if out:
+        Path(out).write_text(text)
+    print(text)
+
+
+def recorded_traffic(kernel):
+    """Calibrated HBM bytes per launch of `kernel` from the committed counter summary, or None."""
+    if not COUNTERS.exists():
+        return None
+    m = re.search(r"<!-- traffic: (\{.*\}) -->", COUNTERS.read_text())
+    return json.loads(m.group(1)).get(kernel) if m else None
+
+
+def calibrate_copy(mb):
+    n = int(mb * 2 ** 20 / 4)
+    src = torch.randn(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_copy_mib": mb, "elements": n}), flush=True)
 
 
 def workload(n_events, device):
@@ -91,6 +192,12 @@ def cpu_baseline(win, sigma, budget):
 
 def main():
     a = parse()
+    if a.summarize:
+        summarize(a.summarize, a.out, a.title, a.command, a.copy_mb)
+        return
+    if a.calibrate_copy > 0:
+        calibrate_copy(a.calibrate_copy)
+        return
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
@@ -130,8 +237,10 @@ def main():
                               0.2, 3.0, 16, anchor_xy=xa)
         K = int(plan.counts().sum())
     dom = max(kernels, key=lambda k: ms[k])
-    slots = SLOTS_FWD if dom.endswith("fwd") else SLOTS_BWD
+    fwd = dom.endswith("fwd")
+    slots = SLOTS_FWD if fwd else SLOTS_BWD
     achieved = K * slots / (ms[dom] * 1e-3)
+    flops = K * (FLOPS_FWD if fwd else FLOPS_BWD) / (ms[dom] * 1e-3)
     value = ev.n * a.steps / dt
     line = {
         "metric": "events/s for anchored-score fwd+bwd @1M events 640x480; % HBM/VALU roofline",
@@ -143,8 +252,10 @@ def main():
                    "events": ev.n, "sensor": [640, 480], "sigma": a.sigma, "tau": 0.2, "slices": 16,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "valu", "kernel": dom, "achieved": achieved / 1e12, "peak": VALU_PEAK / 1e12,
-                     "unit": "Tslot/s", "frac": achieved / VALU_PEAK, "traffic": None,
-                     "pairs": K, "slots_per_pair": slots, "kernel_ms": ms[dom]},
+                     "unit": "Tslot/s", "frac": achieved / VALU_PEAK, "traffic": recorded_traffic(KERNEL_OF[dom]),
+                     "pairs": K, "slots_per_pair": slots, "kernel_ms": ms[dom],
+                     "flop_view": {"achieved": flops / 1e12, "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
+                                   "frac": flops / FP32_PEAK}},
         "kernel_ms": ms,
         "pairs_per_anchor": K / ev.n,
     }

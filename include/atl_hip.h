@@ -142,8 +142,8 @@ typedef struct atl_fast_geometry {
   float reserved_f;
   int64_t GW, GH, ncell, ncell_pad, max_span, ecap;
   int64_t ws_bytes;                     /* workspace layout (byte offsets) */
-  int64_t off_params, off_cnt, off_boff, off_part, off_start, off_trec, off_erec, off_arec, off_srec, off_brec,
-      off_self;
+  int64_t off_params, off_cnt, off_boff, off_part, off_start, off_trec, off_epos, off_etim, off_eself, off_arec,
+      off_srec, off_brec, off_self;
 } atl_fast_geometry;
 
 int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W, int64_t S, double h, double tau,

@@ -156,7 +156,7 @@ __device__ __forceinline__ bool row_span(int r, float qx, float qy, float R, flo
   const float row_hi = row_lo + G.cf;
   const float gap = fmaxf(0.f, fmaxf(row_lo - qy, qy - row_hi));
   if (gap > R) return false;
-  const float w = sqrtf(fmaxf(R2 - gap * gap, 0.f));
+  const float w = __builtin_amdgcn_sqrtf(fmaxf(R2 - gap * gap, 0.f));   // ~1 ulp: far inside the slack
   c0 = cell_walk(qx - w, G.gx0, G.gx1, G.icf, G.GW);
   c1 = cell_walk(qx + w, G.gx0, G.gx1, G.icf, G.GW);
   return true;
@@ -183,7 +183,7 @@ __device__ __forceinline__ bool anchor_rec(int64_t m, const float2* x, const flo
   if (ba < 0 || ba >= G.B) return false;
   const float ta = t[a];
   const float2 xa = anchor_xy ? anchor_xy[m] : x[a];
-  const int s = (int)fminf(fmaxf(floorf(ta / G.delta), 0.f), (float)(G.S - 1));
+  const int s = (int)fminf(fmaxf(floorf(ta / G.delta), 0.f), (float)(G.S - 1));   // = anchor_slice(ta, G)
   const int cx = cell_of(xa.x, G.gx0, G.gx1, G.cf, G.GW), cy = cell_of(xa.y, G.gy0, G.gy1, G.cf, G.GH);
   key = G.ncell_pad + ((((int)ba * G.S + s) * G.GH + cy) * G.GW + cx);
   rec.f = make_float4(xa.x, xa.y, ta, ta - slice_centre(s, G.delta));
@@ -202,57 +202,22 @@ __global__ void __launch_bounds__(kBlock) k_fill_i32(int* __restrict__ p, int64_
   if (i < n) p[i] = v;
 }
 
-// vmax over velocities, max |at| over anchors: block maxima, then one atomic max per block (ordered ints;
-// params zeroed beforehand).
-__global__ void __launch_bounds__(kBlock) k_fast_stats(const float2* __restrict__ v, const int64_t* __restrict__ b,
-                                                       int64_t N, const float* __restrict__ t,
-                                                       const int64_t* __restrict__ anchors, int64_t M, FGeo G,
-                                                       FParams* __restrict__ P) {
-  __shared__ int red[2][kBlock / kWave];
-  int vm = 0, am = 0;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < N; j += stride) {
-    const int64_t bj = b[j];
-    if (bj < 0 || bj >= G.B) continue;
-    const float2 q = v[j];
-    vm = max(vm, float_to_ordered(sqrtf(q.x * q.x + q.y * q.y)));
-  }
-  for (int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; m < M; m += stride) {
-    const int64_t a = anchors[m];
-    if (a < 0 || a >= N) continue;
-    const float ta = t[a];
-    const float fs = fminf(fmaxf(floorf(ta / G.delta), 0.f), (float)(G.S - 1));
-    am = max(am, float_to_ordered(fabsf(ta - slice_centre((int)fs, G.delta))));
-  }
-  vm = wave_max_i(vm);
-  am = wave_max_i(am);
-  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-  if (lane == 0) {
-    red[0][wid] = vm;
-    red[1][wid] = am;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < kBlock / kWave; ++w) {
-      vm = max(vm, red[0][w]);
-      am = max(am, red[1][w]);
-    }
-    if (vm > 0) atomicMax(&P->vmax, vm);
-    if (am > 0) atomicMax(&P->atmax, am);
-  }
-}
-
 // Pass 1.  Blocks [0, nblk_e) cover kSrcPerBlock sources each (their entries and one source record keyed
 // by the cell of the own-slice entry), blocks [nblk_e, nblk_e + nblk_a) kAncPerBlock anchors each.
-// SCATTER = false: per-block bucket histogram into cnt[bucket * nblk + block].  SCATTER = true: the block's
-// scanned offsets cnt[bucket * nblk + block] are loaded into LDS once, and each record takes its slot there.
+// SCATTER = false: per-block bucket histogram into cnt[bucket * nblk + block], and the reductions behind the
+// search radius: vmax over the sources' velocities and max |at| over the anchors (block maxima, one atomic max
+// per block into P, zeroed beforehand; ordered-int encodings of non-negative floats).  SCATTER = true: the
+// block's scanned offsets cnt[bucket * nblk + block] are loaded into LDS once, and each record takes its slot.
 template <bool SCATTER>
 __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restrict__ x, const float* __restrict__ t,
                                                        const float2* __restrict__ v, const int64_t* __restrict__ b,
                                                        int64_t N, const int64_t* __restrict__ anchors,
                                                        const float2* __restrict__ anchor_xy, int64_t M, FGeo G,
-                                                       int* __restrict__ cnt, Rec* __restrict__ trec) {
+                                                       int* __restrict__ cnt, Rec* __restrict__ trec,
+                                                       FParams* __restrict__ P) {
   extern __shared__ int hist[];
+  __shared__ int red[kP1Block / kWave];
+  int vm = 0;                                    // this thread's max ||v|| (sources) or max |at| (anchors)
   const int nblk = G.nblk_e + G.nblk_a;
   const int blk = blockIdx.x;
   for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) hist[i] = SCATTER ? cnt[i * nblk + blk] : 0;
@@ -285,6 +250,7 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
     for (int u = 0; u < per; ++u) {
       const int64_t j = j0 + u * kP1Block + threadIdx.x;
       if (bj[u] < 0 || bj[u] >= G.B) continue;
+      if (!SCATTER) vm = max(vm, float_to_ordered(sqrtf(vj[u].x * vj[u].x + vj[u].y * vj[u].y)));
       int lo, hi;
       slice_range(tj[u], G, lo, hi);
       const int own = min(max((int)fminf(fmaxf(floorf(tj[u] / G.delta), 0.f), (float)(G.S - 1)), lo), hi);
@@ -308,12 +274,21 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
     for (int64_t m = m0 + threadIdx.x; m < m1; m += blockDim.x) {
       int key;
       Rec r;
-      if (anchor_rec(m, x, t, b, anchors, anchor_xy, N, G, key, r)) emit(key, r);
+      if (anchor_rec(m, x, t, b, anchors, anchor_xy, N, G, key, r)) {
+        emit(key, r);
+        if (!SCATTER) vm = max(vm, float_to_ordered(fabsf(r.f.w)));
+      }
     }
   }
   if (!SCATTER) {
+    vm = wave_max_i(vm);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = vm;
     __syncthreads();
     for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) cnt[i * nblk + blk] = hist[i];
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < kP1Block / kWave; ++w) vm = max(vm, red[w]);
+      if (vm > 0) atomicMax(blk < G.nblk_e ? &P->vmax : &P->atmax, vm);
+    }
   }
 }
 
@@ -322,11 +297,27 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
 // [0, Nv) of their own arrays.  Every thread handles kSortItems records per round, all loads issued first.
 constexpr int kSortItems = 8;
 
+// Where pass 2 puts the sorted items.  Entries are split into their positions and velocities (16 B) and
+// times (4 B), which is all the forward reads; the leave-one-out test there compares record positions, with
+// eself[j] the position of event j's entry in its own anchor slice.
+struct SortOut {
+  int* start;
+  float4* epos;                // entries: (y.x, y.y, v.x, v.y)
+  float* etim;                 // entries: t
+  int* eself;                  // per event: its entry in slice floor(t / delta), -1 if none
+  Rec* arec;                   // anchors
+  Rec* srec;                   // sources
+  int* self;                   // per event: its anchor record, -1 if none
+};
+
+__device__ __forceinline__ int anchor_slice(float t, const FGeo& G) {
+  return (int)fminf(fmaxf(floorf(t / G.delta), 0.f), (float)(G.S - 1));
+}
+
 template <int SHIFT>
 __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict__ boff, const Rec* __restrict__ trec,
-                                                           FGeo G, int* __restrict__ start, Rec* __restrict__ erec,
-                                                           Rec* __restrict__ arec, Rec* __restrict__ srec,
-                                                           int* __restrict__ self) {
+                                                           FGeo G, SortOut o) {
+  int* __restrict__ start = o.start;
   constexpr int kBucketKeys = 1 << SHIFT;
   __shared__ int cnt[kBucketKeys];
   __shared__ int cur[kBucketKeys];
@@ -343,16 +334,31 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
     cur[i] = 0;
   }
   __syncthreads();
-  for (int base = lo; base < hi; base += kSortBlock * kSortItems) {
-    int key[kSortItems];
+  // A bucket of at most kSortBlock * kSortItems records (the common case) is read once and kept in registers
+  // from the count to the scatter; larger buckets count from the keys and read the records again.
+  const bool one = hi - lo <= kSortBlock * kSortItems;
+  Rec r1[kSortItems];
+  if (one) {
 #pragma unroll
     for (int u = 0; u < kSortItems; ++u) {
-      const int p = base + u * kSortBlock + threadIdx.x;
-      key[u] = p < hi ? tki[2 * p + 1].z : -1;
+      const int p = lo + u * kSortBlock + threadIdx.x;
+      if (p < hi) r1[u] = trec[p];
     }
 #pragma unroll
     for (int u = 0; u < kSortItems; ++u)
-      if (key[u] >= 0) atomicAdd(cnt + (key[u] & (kBucketKeys - 1)), 1);
+      if (lo + u * kSortBlock + (int)threadIdx.x < hi) atomicAdd(cnt + (r1[u].i.z & (kBucketKeys - 1)), 1);
+  } else {
+    for (int base = lo; base < hi; base += kSortBlock * kSortItems) {
+      int key[kSortItems];
+#pragma unroll
+      for (int u = 0; u < kSortItems; ++u) {
+        const int p = base + u * kSortBlock + threadIdx.x;
+        key[u] = p < hi ? tki[2 * p + 1].z : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < kSortItems; ++u)
+        if (key[u] >= 0) atomicAdd(cnt + (key[u] & (kBucketKeys - 1)), 1);
+    }
   }
   __syncthreads();
   constexpr int per = kBucketKeys / kSortBlock;
@@ -377,8 +383,29 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
   __syncthreads();
   const int space = bucket / bpk;                  // 0 entries, 1 anchors, 2 sources
   const int off = space == 0 ? 0 : (space == 1 ? E : EA);
-  Rec* out = space == 0 ? erec : (space == 1 ? arec : srec);
+  Rec* out = space == 1 ? o.arec : o.srec;
   const int kbase = space * G.ncell_pad;
+  const int plane_cells = G.GH * G.GW;
+  auto place = [&](Rec r) {
+    const int kk = r.i.z & (kBucketKeys - 1);
+    const int pos = lo + cnt[kk] + atomicAdd(cur + kk, 1) - off;
+    r.i.z -= kbase;
+    if (space == 0) {
+      o.epos[pos] = r.f;
+      const float tj = __int_as_float(r.i.x);
+      o.etim[pos] = tj;
+      if ((r.i.z / plane_cells) % G.S == anchor_slice(tj, G)) o.eself[r.i.y] = pos;
+    } else {
+      out[pos] = r;
+      if (space == 1) o.self[r.i.x] = pos;       // the anchor's event id -> its record
+    }
+  };
+  if (one) {
+#pragma unroll
+    for (int u = 0; u < kSortItems; ++u)
+      if (lo + u * kSortBlock + (int)threadIdx.x < hi) place(r1[u]);
+    return;
+  }
   for (int base = lo; base < hi; base += kSortBlock * kSortItems) {
     Rec r[kSortItems];
     bool live[kSortItems];
@@ -389,31 +416,28 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
       if (live[u]) r[u] = trec[p];
     }
 #pragma unroll
-    for (int u = 0; u < kSortItems; ++u) {
-      if (live[u]) {
-        const int kk = r[u].i.z & (kBucketKeys - 1);
-        const int pos = lo + cnt[kk] + atomicAdd(cur + kk, 1) - off;
-        r[u].i.z -= kbase;
-        out[pos] = r[u];
-        if (space == 1) self[r[u].i.x] = pos;     // the anchor's event id -> its record
-      }
-    }
+    for (int u = 0; u < kSortItems; ++u)
+      if (live[u]) place(r[u]);
   }
 }
 
 // ------------------------------------------------------------------------------------------ pair walks
 struct FPlan {
-  const Rec* erec;             // entries in cell order
+  const float4* epos;          // entries in cell order: (y.x, y.y, v.x, v.y)
+  const float* etim;           // entries in cell order: t
+  const int* eself;            // per event: position of its own-slice entry, -1 if none
   const Rec* arec;             // anchors in cell order
   const Rec* srec;             // sources in own-slice cell order
-  float4* brec;                // anchors in cell order for the backward: (x, y, t, gS)
+  float4* brec;                // anchors in cell order for the backward: (x, y, t, gS / h^2)
   int* self;                   // per event: position of its own anchor record, -1 if it is no anchor
   const int* start;            // 3*ncell_pad + 1: entry cells, anchor cells (offset by E), source cells
   FParams* P;
 };
 
 // One candidate pair, predicated: the reference's three tests (csrc/atl_cpu.cpp:187-197) in its fp32 order,
-// written as "not rejected" so that NaN distances count as visits exactly as there.
+// written as "not rejected" so that NaN distances count as visits exactly as there.  The leave-one-out test
+// compares id_a and id_s: the anchor event's own entry position and the candidate's position (one entry per
+// source and slice, so this is the reference's id test).
 __device__ __forceinline__ bool pair_test(int id_a, int id_s, float ta, float ts, float ax, float ay, float at,
                                           const float4& e, const FGeo& G, float& dt, float& rx, float& ry,
                                           float& d2) {
@@ -522,7 +546,7 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
       const float row_lo = G.gy0 + (float)r * G.cf, row_hi = row_lo + G.cf;
       const float gap = fmaxf(0.f, fmaxf(row_lo - y1, y0 - row_hi));
       if (gap <= R) {
-        const float w = sqrtf(fmaxf(R2 - gap * gap, 0.f));
+        const float w = __builtin_amdgcn_sqrtf(fmaxf(R2 - gap * gap, 0.f));   // ~1 ulp: far inside the slack
         const int c0 = cell_walk(x0 - w, G.gx0, G.gx1, G.icf, G.GW);
         const int c1 = cell_walk(x1 + w, G.gx0, G.gx1, G.icf, G.GW);
         const int rowk = plane + r * G.GW;
@@ -570,11 +594,11 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
 }
 
 // One pass of a group walk for WD wave-uniform anchors read from lanes src0 .. src0 + na - 1 (slots past na
-// repeat the last anchor and are discarded): lane `dst` of the wave receives anchor src0 + a's sum (and
-// count) in mine (mine_n).
+// repeat the last anchor and are discarded): lane src0 + a receives anchor a's sum (and count) in mine
+// (mine_n).  es is each anchor lane's own entry position: the leave-one-out test skips that candidate.
 template <int WD, bool COUNT>
 __device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plane, float x0, float y0, float R,
-                                         float R2, const float4& A, const int4& ai, int src0, int na, int lane,
+                                         float R2, const float4& A, int es, int src0, int na, int lane,
                                          float& mine, int& mine_n) {
   float ax[WD], ay[WD], ta[WD], at[WD], acc[WD];
   int id[WD], cnt[WD];
@@ -585,19 +609,18 @@ __device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plan
     ay[a] = rdlanef(A.y, src);
     ta[a] = rdlanef(A.z, src);
     at[a] = rdlanef(A.w, src);
-    id[a] = rdlane(ai.x, src);
+    id[a] = rdlane(es, src);
     acc[a] = 0.f;
     cnt[a] = 0;
   }
   group_walk(p.start, 0, plane, x0, x0 + G.cf, y0, y0 + G.cf, R, R2, G, [&](int pos) {
-    const Rec er = ld(p.erec, (uint32_t)max(pos, 0));
-    const float4 e = er.f;
-    const int4 ti = er.i;
-    const float ts = __int_as_float(ti.x);
+    const uint32_t k = (uint32_t)max(pos, 0);
+    const float4 e = ld(p.epos, k);
+    const float ts = ld(p.etim, k);
 #pragma unroll
     for (int a = 0; a < WD; ++a) {
       float dt, rx, ry, d2;
-      const bool ok = pair_test(id[a], ti.y, ta[a], ts, ax[a], ay[a], at[a], e, G, dt, rx, ry, d2) & (pos >= 0);
+      const bool ok = pair_test(id[a], pos, ta[a], ts, ax[a], ay[a], at[a], e, G, dt, rx, ry, d2) & (pos >= 0);
       const float kern = __builtin_amdgcn_exp2f(d2 * G.kexp);
       acc[a] += ok ? kern : 0.f;
       if (COUNT) cnt[a] += ok ? 1 : 0;
@@ -640,6 +663,7 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
   const float4 A = AR.f;
   const int4 ai = AR.i;
   const int key = ai.z;
+  const int es = p.eself[ai.x];                  // the anchor event's own entry in this slice, -1 if none
   const int plane_cells = G.GH * G.GW;
   float mine = 0.f;
   int mine_n = 0;
@@ -658,13 +682,13 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
       const int na = min(kGroup, gsize - a0);
       const int plane = g * plane_cells;
       if (na == 1)
-        fwd_pass<1, COUNT>(p, G, plane, x0, y0, R, R2, A, ai, i + a0, na, lane, mine, mine_n);
+        fwd_pass<1, COUNT>(p, G, plane, x0, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
       else if (na == 2)
-        fwd_pass<2, COUNT>(p, G, plane, x0, y0, R, R2, A, ai, i + a0, na, lane, mine, mine_n);
+        fwd_pass<2, COUNT>(p, G, plane, x0, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
       else if (na <= 4)
-        fwd_pass<4, COUNT>(p, G, plane, x0, y0, R, R2, A, ai, i + a0, na, lane, mine, mine_n);
+        fwd_pass<4, COUNT>(p, G, plane, x0, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
       else
-        fwd_pass<kGroup, COUNT>(p, G, plane, x0, y0, R, R2, A, ai, i + a0, na, lane, mine, mine_n);
+        fwd_pass<kGroup, COUNT>(p, G, plane, x0, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
     }
   }
   if (have) {
@@ -673,7 +697,7 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
   }
 }
 
-// Backward records of the anchors in cell order, brec[q] = (x, y, t, gS): one 16-byte load per candidate in
+// Backward records of the anchors in cell order, brec[q] = (x, y, t, gS / h^2): one 16-byte load per candidate in
 // the backward's per-lane walks (the anchor's at = t - c_s is recomputed there with the same fp32 operation).
 // Also checks that no event occurs twice among the anchors (self[id] then names only one of the records).
 __global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int M, const float* __restrict__ gS) {
@@ -681,7 +705,7 @@ __global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int 
   const int Mv = p.start[2 * G.ncell_pad] - p.start[G.ncell_pad];
   if (q >= Mv || q >= M) return;
   const Rec r = p.arec[q];
-  p.brec[q] = make_float4(r.f.x, r.f.y, r.f.z, gS[r.i.y]);
+  p.brec[q] = make_float4(r.f.x, r.f.y, r.f.z, gS[r.i.y] * G.invh2);
   if (p.self[r.i.x] != q) p.P->dup = 1;
 }
 
@@ -725,7 +749,7 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
         const bool other = DUP ? id[u] != sid : k + u != sp;
         const bool ok = other & !(fabsf(dt) > G.tau) & !(d2 > G.r2max) & (k + u < e);
         const float kern = __builtin_amdgcn_exp2f(d2 * G.kexp);
-        const float f = A[u].w * kern * dt * G.invh2;
+        const float f = A[u].w * kern * dt;           // A.w = gS / h^2
         mgx = ok ? fmaf(f, rx, mgx) : mgx;
         mgy = ok ? fmaf(f, ry, mgy) : mgy;
       }
@@ -795,7 +819,9 @@ T* at_off(void* ws, int64_t off) { return (T*)((char*)ws + off); }
 
 FPlan make_plan(void* ws, const atl_fast_geometry* geo) {
   FPlan p;
-  p.erec = at_off<Rec>(ws, geo->off_erec);
+  p.epos = at_off<float4>(ws, geo->off_epos);
+  p.etim = at_off<float>(ws, geo->off_etim);
+  p.eself = at_off<int>(ws, geo->off_eself);
   p.arec = at_off<Rec>(ws, geo->off_arec);
   p.srec = at_off<Rec>(ws, geo->off_srec);
   p.brec = at_off<float4>(ws, geo->off_brec);
@@ -870,7 +896,9 @@ int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W
   g.off_start = off;   off += align256((3 * g.ncell_pad + 1) * 4);
   g.off_trec = off;    off += align256(ntmp * (int64_t)sizeof(Rec));
   // the walks read up to kUnroll - 1 records past a range end: entry and anchor arrays carry that padding
-  g.off_erec = off;    off += align256((g.ecap + kUnroll) * (int64_t)sizeof(Rec));
+  g.off_epos = off;    off += align256((g.ecap + kUnroll) * (int64_t)sizeof(float4));
+  g.off_etim = off;    off += align256((g.ecap + kUnroll) * (int64_t)sizeof(float));
+  g.off_eself = off;   off += align256(N * (int64_t)sizeof(int));
   g.off_arec = off;    off += align256((M + kUnroll) * (int64_t)sizeof(Rec));
   g.off_srec = off;    off += align256(N * (int64_t)sizeof(Rec));
   g.off_brec = off;    off += align256((M + kUnroll) * (int64_t)sizeof(float4));
@@ -895,30 +923,29 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
   const int nblk = G.nblk_e + G.nblk_a;
   const int64_t nbh = (int64_t)G.nbuckets * nblk;
   hipLaunchKernelGGL(k_fill_zero, dim3(1), dim3(64), 0, stream, (int*)P, (int64_t)(sizeof(FParams) / 4));
-  const int64_t n = N > M ? N : M;
-  if (n > 0) {
-    unsigned grid = grid_for(n);
-    if (grid > 512) grid = 512;
-    hipLaunchKernelGGL(k_fast_stats, dim3(grid), dim3(kBlock), 0, stream, (const float2*)v, b, N, t, anchors, M, G,
-                       P);
-  }
   const size_t lds = (size_t)G.nbuckets * sizeof(int);
   if (nblk > 0) {
     hipLaunchKernelGGL(k_sort_pass1<false>, dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
-                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, (Rec*)nullptr);
+                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, (Rec*)nullptr, P);
     scan32(cnt, nbh, part, boff, stream);
     hipLaunchKernelGGL(k_sort_pass1<true>, dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
-                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, boff, trec);
+                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, boff, trec, (FParams*)nullptr);
   } else {
     hipLaunchKernelGGL(k_fill_zero, dim3(1), dim3(64), 0, stream, boff, (int64_t)1);
   }
-  if (N > 0)
+  if (N > 0) {
     hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(N)), dim3(kBlock), 0, stream, at_off<int>(ws, geo->off_self), N, -1);
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(N)), dim3(kBlock), 0, stream, at_off<int>(ws, geo->off_eself), N,
+                       -1);
+  }
   auto pass2 = G.bshift == 10 ? k_sort_pass2<10> : G.bshift == 11 ? k_sort_pass2<11>
              : G.bshift == 12 ? k_sort_pass2<12> : k_sort_pass2<13>;
   hipLaunchKernelGGL(pass2, dim3(G.nbuckets), dim3(kSortBlock), 0, stream, (const int*)boff,
-                     (const Rec*)trec, G, at_off<int>(ws, geo->off_start), at_off<Rec>(ws, geo->off_erec),
-                     at_off<Rec>(ws, geo->off_arec), at_off<Rec>(ws, geo->off_srec), at_off<int>(ws, geo->off_self));
+                     (const Rec*)trec, G,
+                     SortOut{at_off<int>(ws, geo->off_start), at_off<float4>(ws, geo->off_epos),
+                             at_off<float>(ws, geo->off_etim), at_off<int>(ws, geo->off_eself),
+                             at_off<Rec>(ws, geo->off_arec), at_off<Rec>(ws, geo->off_srec),
+                             at_off<int>(ws, geo->off_self)});
   return check_launch("fast_plan");
 }
 

@@ -73,7 +73,8 @@ class FastGeometry(ctypes.Structure):
                 [(n, ctypes.c_float) for n in ("gx0", "gy0", "gx1", "gy1", "cell", "reserved_f")] +
                 [(n, ctypes.c_int64) for n in ("GW", "GH", "ncell", "ncell_pad", "max_span", "ecap", "ws_bytes",
                                                "off_params", "off_cnt", "off_boff", "off_part", "off_start",
-                                               "off_trec", "off_erec", "off_arec", "off_srec", "off_brec", "off_self")])
+                                               "off_trec", "off_epos", "off_etim", "off_eself", "off_arec", "off_srec", "off_brec",
+                                               "off_self")])
 
 
 _LIB = None
