@@ -9,6 +9,13 @@ HBM.  Prints one JSON line (rank 0, N = 1) with events/s, the dominant kernel's 
 
     python bench.py [--steps K] [--warmup W] [--sigma S] [--no-cpu]
 
+Other workloads (parity-test configurations, not the headline metric), same output contract:
+
+    python bench.py --workload iwe             # 1M events 640x480, dense flow: warp to t = 0.5, bilinear IWE
+                                               # (inside mask), gather of the IWE at the warped events,
+                                               # loss = sum, backward to the flow grid
+    python bench.py --workload iwe-plumbing    # the same on 100k events 240x180, constant flow (2, -1.25)
+
 Two helpers for the rocprofv3 summaries under profiles/ (no GPU work beyond what they name):
 
     python bench.py --calibrate-copy MB        # a plain f32 copy of MB MiB (read MB, write MB), 5 times
@@ -46,6 +53,7 @@ COUNTERS = ROOT / "profiles" / "anchored_score_1M_640x480_counters.md"
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--workload", default="anchored", choices=["anchored", "iwe", "iwe-plumbing"])
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--sigma", type=float, default=1.0)
@@ -190,6 +198,123 @@ def cpu_baseline(win, sigma, budget):
                       f"(time-sorted prefix), one timed run after a 50k-event warm-up, {dt:.2f} s"}
 
 
+# ----------------------------------------------------------------------------------------- IWE workloads
+# Algorithmic HBM bytes of each entry point: per event (positions 8, batch 8, weights or values 4, outputs)
+# plus the image or flow grid once.
+IWE_BYTES = {
+    "atl_splat_bilinear_fwd": lambda n, hw, g: 20 * n + 4 * hw,
+    "atl_splat_bilinear_bwd": lambda n, hw, g: 32 * n + 4 * hw,
+    "atl_gather_bilinear_fwd": lambda n, hw, g: 20 * n + 4 * hw,
+    "atl_gather_bilinear_bwd": lambda n, hw, g: 28 * n + 8 * hw,
+    "atl_sample_grid_fwd": lambda n, hw, g: 24 * n + 4 * g,
+    "atl_sample_grid_bwd_planned": lambda n, hw, g: 16 * n + 8 * g,
+}
+
+
+def iwe_workload(kind, dev):
+    from x_amd import synth
+    from x_amd.core import EventPacket
+    from x_amd.motion import DenseLinearFlow, Translation
+    if kind == "iwe":
+        win = synth.dense_flow_window(seed=0)
+        grid = win.motion["grid"]
+        motion = DenseLinearFlow(1, win.height, win.width, grid=grid.shape[-2:], init=torch.as_tensor(grid))
+        desc = (f"IWE splat+gather fwd+bwd, {win.n} events, 640x480, dense flow 2x480x640 (max 20 px/window), "
+                f"warp to t=0.5, bilinear, inside mask, loss = sum of gathered IWE, grad to the flow grid")
+    else:
+        win = synth.plumbing_translation(seed=0)
+        motion = Translation(1, win.height, win.width, init=torch.as_tensor(win.motion["theta"])[None])
+        desc = (f"IWE splat+gather fwd+bwd, {win.n} events, 240x180, translation (2.0, -1.25) px/window, "
+                f"warp to t=0, bilinear, inside mask, loss = sum of gathered IWE, grad to theta")
+    return win, EventPacket.from_window(win, dev), motion.to(dev), desc
+
+
+def iwe_cpu_baseline(win, t_ref, budget):
+    """Oracle on the host: NumPy warp (+ flow lookup), OpenMP splat / gather forward and backward, flow-grid
+    adjoint; same loss as the GPU step."""
+    import oracle as O
+    H, W = win.height, win.width
+
+    def run(n):
+        sl = slice(0, n)
+        xy, t, b = win.xy[sl], win.t[sl], win.b[sl]
+        if win.motion["kind"] == "dense":
+            v, idx, wts = O.dense_velocity(win.motion["grid"], xy, b, H, W)
+        else:
+            v = np.broadcast_to(win.motion["theta"].astype(np.float32), xy.shape)
+        y = (xy + v * (np.float32(t_ref) - t)[:, None]).astype(np.float32)
+        w = ((y[:, 0] >= 0) & (y[:, 0] <= W - 1) & (y[:, 1] >= 0) & (y[:, 1] <= H - 1)).astype(np.float32)
+        img = O.splat_bilinear_fwd(y, w, b, 1, H, W)
+        O.gather_bilinear_fwd(img, y, b)
+        gimg, gp1 = O.gather_bilinear_bwd(np.ones(n, np.float32), img, y, b)
+        gp2, _ = O.splat_bilinear_bwd(gimg, y, w, b)
+        gv = (gp1 + gp2) * (np.float32(t_ref) - t)[:, None]
+        if win.motion["kind"] == "dense":
+            O.sample_grid_bwd(gv, idx, wts, win.motion["grid"].shape)
+        else:
+            gv.sum(0)
+
+    run(min(win.n, 50_000))
+    n = win.n
+    t0 = time.perf_counter()
+    run(n)
+    dt = time.perf_counter() - t0
+    if dt > budget:
+        n = max(int(win.n * budget / dt / 2), 10_000)
+        t0 = time.perf_counter()
+        run(n)
+        dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "events/s", "cores": O.num_threads(), "kind": "port",
+            "sample": f"IWE step on the first {n} events of the same window, one timed run after a 50k-event "
+                      f"warm-up, {dt:.2f} s"}
+
+
+def iwe_main(a, dev):
+    from x_amd.objectives.base import IWEConfig, make_iwe
+    from x_amd.ops import _ext, gather
+    win, ev, motion, desc = iwe_workload(a.workload, dev)
+    t_ref = 0.5 if a.workload == "iwe" else 0.0
+    cfg = IWEConfig(kernel="bilinear", sigma=0.0, mask_border=True)
+
+    def step():
+        for p in motion.parameters():
+            p.grad = None
+        y = motion.transport(ev.xy, ev.t, t_ref, ev.b)
+        img = make_iwe(ev, y, t_ref, cfg)
+        gather(img, y, ev.b).sum().backward()
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    kernels = list(IWE_BYTES)
+    rec = _ext.time_kernels(kernels)
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1 in rec[k]])) for k in kernels if rec[k]}
+    _ext.time_kernels(())
+    hw = ev.height * ev.width
+    g = 2 * hw if a.workload == "iwe" else 0
+    gbs = {k: IWE_BYTES[k](ev.n, hw, g) / (ms[k] * 1e-3) / 1e9 for k in ms}
+    dom = max(ms, key=lambda k: ms[k])
+    line = {
+        "metric": f"events/s for IWE splat+gather fwd+bwd @{ev.n} events {ev.width}x{ev.height}; % HBM roofline",
+        "value": ev.n * a.steps / dt, "unit": "events/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": 1e3 * dt / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": desc, "events": ev.n, "sensor": [ev.width, ev.height], "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": gbs[dom], "peak": 8000.0, "unit": "GB/s",
+                     "frac": gbs[dom] / 8000.0, "traffic": recorded_traffic(dom), "kernel_ms": ms[dom]},
+        "kernel_ms": ms,
+        "kernel_gbs": gbs,
+    }
+    if not a.no_cpu:
+        line["cpu_baseline"] = iwe_cpu_baseline(win, t_ref, a.cpu_budget)
+    print(json.dumps(line), flush=True)
+
+
 def main():
     a = parse()
     if a.summarize:
@@ -202,6 +327,11 @@ def main():
         print(f"bench.py measures one GPU only (asked for {a.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
         sys.exit(2)
+    if a.workload != "anchored":
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        iwe_main(a, dev)
+        return
     from x_amd.objectives import AnchoredExact
     from x_amd.ops import _ext
     from x_amd.ops import functional as F

@@ -48,6 +48,15 @@ int atl_gather_bilinear_fwd(const float* img, const float* pos, const int64_t* b
 /* gather_bilinear_bwd (csrc/atl_ops.h:29, csrc/atl_cpu.cpp:151-172): gimg (B,H,W) accumulated, gpos written. */
 int atl_gather_bilinear_bwd(const float* gval, const float* img, const float* pos, const int64_t* b, int64_t N,
                             int64_t B, int64_t H, int64_t W, float* gimg, float* gpos, hipStream_t stream);
+/* The same splat forward and gather backward with tile-binned LDS accumulation instead of one global atomic
+ * per corner (identical corner indices and weights; float sums in another order).  ws: a workspace of
+ * atl_tile_ws_bytes(N, B, H, W) bytes (-1: sizes unsupported, use the entry points above). */
+int64_t atl_tile_ws_bytes(int64_t N, int64_t B, int64_t H, int64_t W);
+int atl_splat_bilinear_fwd_ws(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B, int64_t H,
+                              int64_t W, float* img, void* ws, int64_t ws_bytes, hipStream_t stream);
+int atl_gather_bilinear_bwd_ws(const float* gval, const float* img, const float* pos, const int64_t* b, int64_t N,
+                               int64_t B, int64_t H, int64_t W, float* gimg, float* gpos, void* ws, int64_t ws_bytes,
+                               hipStream_t stream);
 /* voxel_grid (csrc/atl_ops.h:49-50, csrc/atl_cpu.cpp:256-286): vox (B,C,H,W) accumulated. */
 int atl_voxel_grid(const float* pos, const float* t, const float* p, const int64_t* b, int64_t N, int64_t B,
                    int64_t C, int64_t H, int64_t W, float* vox, hipStream_t stream);
@@ -65,10 +74,11 @@ int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int
                         const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gfield,
                         hipStream_t stream);
 
-/* The same adjoint as a gather (deterministic, no atomics): atl_grid_plan sorts the positions by their base
- * corner into a workspace of atl_grid_plan_bytes(B, Hg, Wg, N) bytes (-1 if the sizes are unsupported);
- * atl_sample_grid_bwd_planned then sums, per grid node, the weighted gout of the positions around it.
- * gfield accumulated; C <= 4.  The positions and img_h, img_w must be the ones the plan was built from. */
+/* The same adjoint through a tile plan: atl_grid_plan bins the positions by the 16x16 tile of their base
+ * grid node into a workspace of atl_grid_plan_bytes(B, Hg, Wg, N) bytes (-1 if the sizes are unsupported);
+ * atl_sample_grid_bwd_planned then accumulates gout tile by tile in LDS and adds each touched node once.
+ * gfield accumulated; C <= 4.  The positions and img_h, img_w must be the ones the plan was built from
+ * (the plan keeps its own copy of the positions; `pos` is not read). */
 int64_t atl_grid_plan_bytes(int64_t B, int64_t Hg, int64_t Wg, int64_t N);
 int atl_grid_plan(int64_t B, int64_t Hg, int64_t Wg, const float* pos, const int64_t* b, int64_t N, int64_t img_h,
                   int64_t img_w, void* ws, int64_t ws_bytes, hipStream_t stream);

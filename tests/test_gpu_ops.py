@@ -72,6 +72,31 @@ def test_gather_matches_oracle():
     close_rel(N(ti.grad), gimg, 1e-5)
 
 
+@pytest.mark.parametrize("B,H,W", [(1, 480, 640), (20, 480, 640), (60, 480, 640), (2, 3, 2)])
+def test_splat_gather_tile_paths(B, H, W):
+    """The tile-binned splat forward and gather backward (16-px tiles; 32-px tiles when 16-px ones would
+    exceed the binning histogram, B = 20; the per-corner atomic kernels beyond that, B = 60) against the
+    oracle: a crowded pixel, events on the borders and just outside them, zero and negative weights."""
+    print(f"tile paths B={B} {H}x{W}", flush=True)
+    rng = np.random.default_rng(B)
+    n = 60000
+    pos = np.stack([rng.uniform(-1.5, W + 0.5, n), rng.uniform(-1.5, H + 0.5, n)], 1).astype(F32)
+    pos[: n // 4] = np.array([min(W - 1, 7) + 0.25, min(H - 1, 5) + 0.5], F32)       # one crowded pixel
+    pos[n // 4: n // 4 + 100, 0] = F32(-1.0)                                           # base corner -1
+    pos[n // 4 + 100: n // 4 + 200, 1] = F32(H - 1)                                    # last row exactly
+    w = rng.standard_normal(n).astype(F32)
+    w[::17] = 0.0
+    b = rng.integers(0, B, n).astype(np.int64)
+    img = F.get_ext().splat_bilinear_fwd(T(pos), T(w), T(b), B, H, W)
+    close_rel(N(img), O.splat_bilinear_fwd(pos, w, b, B, H, W), 1e-5)
+    src = rng.standard_normal((B, H, W)).astype(F32)
+    g = rng.standard_normal(n).astype(F32)
+    gimg, gp = F.get_ext().gather_bilinear_bwd(T(g), T(src), T(pos), T(b))
+    want_img, want_p = O.gather_bilinear_bwd(g, src, pos, b)
+    assert np.array_equal(N(gp), want_p)
+    close_rel(N(gimg), want_img, 1e-5)
+
+
 def test_voxel_matches_oracle():
     pos, _, b, t = rand_events(n=5000, seed=5)
     p = np.where(np.random.default_rng(6).random(5000) > 0.5, 1.0, -1.0).astype(F32)
@@ -116,7 +141,7 @@ def test_sample_grid_matches_oracle():
 
 @pytest.mark.parametrize("Hg,Wg", [(1, 1), (2, 3), (5, 1), (1, 7), (17, 13)])
 def test_sample_grid_planned_backward_small_grids(Hg, Wg):
-    """The sorted-gather adjoint on degenerate and odd grids, positions inside and far outside (clamped)."""
+    """The tile-plan adjoint on degenerate and odd grids, positions inside and far outside (clamped)."""
     rng = np.random.default_rng(Hg * 100 + Wg)
     n = 3000
     pos = np.stack([rng.uniform(-5, Wg + 4, n), rng.uniform(-5, Hg + 4, n)], 1).astype(F32)
@@ -132,7 +157,7 @@ def test_sample_grid_planned_backward_small_grids(Hg, Wg):
 
 
 def test_sample_grid_planned_backward_full_size():
-    """1M events on a 2x480x640 grid: the plan-and-gather adjoint equals the atomic scatter adjoint."""
+    """1M events on a 2x480x640 grid: the tile-plan adjoint equals the per-event atomic adjoint."""
     win = synth.dense_flow_window(seed=0)
     grid = T(win.motion["grid"]).requires_grad_(True)
     xy, b = T(win.xy), T(win.b)

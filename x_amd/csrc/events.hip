@@ -315,191 +315,6 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd(const float* __restr
 
 bool dims_ok(int64_t H, int64_t W) { return H > 0 && W > 0 && H * W < (int64_t)1 << 31; }
 
-// ------------------------------------------------------------------------------------------- flow-grid plan
-// The adjoint of the flow lookup as a gather: positions sorted by their base corner (y0, x0) (two-level
-// counting sort: LDS bucket histograms per block, then one workgroup per bucket of 8192 corners), then one
-// thread per grid node sums the weighted output gradients of the positions in the four cells around it.
-// No atomics: scattered float atomics run at ~25 G/s here, and positions on event lines put many
-// contributions on the same nodes.
-constexpr int kGridShift = 13;
-constexpr int kGridKeys = 1 << kGridShift;
-constexpr int kGridPerBlock = 4096;
-constexpr int kGridSortBlock = 1024;
-
-struct GridPlanGeo {
-  int B, Hg, Wg, N, nblk, nb;
-  float sxw, syh;
-  int scale;
-};
-
-__device__ __forceinline__ bool grid_key(const float2* pos, const int64_t* bidx, int n, const GridPlanGeo& g,
-                                         int& key, float2& a) {
-  const int64_t b = bidx[n];
-  if (b < 0 || b >= g.B) return false;
-  const float2 p = pos[n];
-  const GridCorners c = grid_corners(p.x, p.y, g.Hg, g.Wg, g.sxw, g.syh, g.scale != 0);
-  key = (int)b * g.Hg * g.Wg + c.o00;
-  a = make_float2(c.w00, c.w01);       // weights are recomputed from (w00, w01, w10, w11) below
-  return true;
-}
-
-template <bool SCATTER>
-__global__ void __launch_bounds__(kBlock) k_grid_pass1(const float2* __restrict__ pos, const int64_t* __restrict__ bidx,
-                                                       GridPlanGeo g, int* __restrict__ cnt, int* __restrict__ tkey,
-                                                       int* __restrict__ tidx) {
-  extern __shared__ int hist[];
-  for (int i = threadIdx.x; i < g.nb; i += blockDim.x) hist[i] = 0;
-  __syncthreads();
-  const int n0 = blockIdx.x * kGridPerBlock, n1 = min(n0 + kGridPerBlock, g.N);
-  for (int n = n0 + threadIdx.x; n < n1; n += blockDim.x) {
-    int key;
-    float2 a;
-    if (!grid_key(pos, bidx, n, g, key, a)) continue;
-    const int bucket = key >> kGridShift;
-    if (!SCATTER) {
-      atomicAdd(hist + bucket, 1);
-    } else {
-      const int at = cnt[bucket * g.nblk + blockIdx.x] + atomicAdd(hist + bucket, 1);
-      tkey[at] = key;
-      tidx[at] = n;
-    }
-  }
-  if (!SCATTER) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < g.nb; i += blockDim.x) cnt[i * g.nblk + blockIdx.x] = hist[i];
-  }
-}
-
-// start (B*Hg*Wg rounded up to buckets, + 1) cell offsets; sidx (position index) in corner order.
-__global__ void __launch_bounds__(kGridSortBlock) k_grid_pass2(const int* __restrict__ boff,
-                                                               const int* __restrict__ tkey,
-                                                               const int* __restrict__ tidx, GridPlanGeo g,
-                                                               int* __restrict__ start, int* __restrict__ sidx) {
-  __shared__ int cnt[kGridKeys];
-  __shared__ int cur[kGridKeys];
-  __shared__ int wsum[kGridSortBlock / kWave + 1];
-  const int bucket = blockIdx.x;
-  const int lo = boff[bucket * g.nblk], hi = boff[(bucket + 1) * g.nblk];
-  for (int i = threadIdx.x; i < kGridKeys; i += kGridSortBlock) {
-    cnt[i] = 0;
-    cur[i] = 0;
-  }
-  __syncthreads();
-  for (int p = lo + threadIdx.x; p < hi; p += kGridSortBlock) atomicAdd(cnt + (tkey[p] & (kGridKeys - 1)), 1);
-  __syncthreads();
-  constexpr int per = kGridKeys / kGridSortBlock;
-  int vals[per];
-  int s = 0;
-#pragma unroll
-  for (int k = 0; k < per; ++k) {
-    vals[k] = cnt[threadIdx.x * per + k];
-    s += vals[k];
-  }
-  int total;
-  int run = block_exclusive_scan<kGridSortBlock>(s, wsum, total);
-#pragma unroll
-  for (int k = 0; k < per; ++k) {
-    const int i = threadIdx.x * per + k;
-    cnt[i] = run;
-    start[(bucket << kGridShift) + i] = lo + run;
-    run += vals[k];
-  }
-  if (bucket == g.nb - 1 && threadIdx.x == 0) start[g.nb << kGridShift] = hi;
-  __syncthreads();
-  for (int p = lo + threadIdx.x; p < hi; p += kGridSortBlock) {
-    const int kk = tkey[p] & (kGridKeys - 1);
-    sidx[lo + cnt[kk] + atomicAdd(cur + kk, 1)] = tidx[p];
-  }
-}
-
-// Four lanes per grid node (b, y, x), one for each of the cells (y-1..y, x-1..x) whose positions can have
-// the node as a corner: each sums gout[n, c] * weight over its cell (loads issued four positions at a
-// time), the quad adds its partial sums and its first lane adds them to gfield (the adjoint of
-// k_sample_grid_fwd).
-constexpr int kGatherUnroll = 4;
-__global__ void __launch_bounds__(kBlock) k_grid_gather(const float* __restrict__ gout, int C,
-                                                        const float2* __restrict__ pos, GridPlanGeo g,
-                                                        const int* __restrict__ start, const int* __restrict__ sidx,
-                                                        float* __restrict__ gfield) {
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int plane = g.Hg * g.Wg;
-  const int64_t nodes = (int64_t)g.B * plane;
-  const bool live = tid < 4 * nodes;                 // every lane of a quad has the same liveness
-  const int node = live ? (int)(tid >> 2) : 0;
-  const int q = (int)(tid & 3);
-  const int b = node / plane, o = node - b * plane;
-  const int y = o / g.Wg, x = o - y * g.Wg;
-  const int cy = y - 1 + (q >> 1), cx = x - 1 + (q & 1);
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  const int cmax = C < 4 ? C : 4;
-  if (live && cy >= 0 && cx >= 0) {
-    const int key = b * plane + cy * g.Wg + cx;
-    const int k0 = start[key], k1 = start[key + 1];
-    for (int k = k0; k < k1; k += kGatherUnroll) {
-      int n[kGatherUnroll];
-      float2 p[kGatherUnroll];
-#pragma unroll
-      for (int u = 0; u < kGatherUnroll; ++u) n[u] = sidx[min(k + u, k1 - 1)];
-#pragma unroll
-      for (int u = 0; u < kGatherUnroll; ++u) p[u] = pos[n[u]];
-#pragma unroll
-      for (int u = 0; u < kGatherUnroll; ++u) {
-        const GridCorners c = grid_corners(p[u].x, p[u].y, g.Hg, g.Wg, g.sxw, g.syh, g.scale != 0);
-        float w = 0.f;
-        if (c.o00 == o) w += c.w00;
-        if (c.o01 == o) w += c.w01;
-        if (c.o10 == o) w += c.w10;
-        if (c.o11 == o) w += c.w11;
-        if (k + u >= k1) w = 0.f;
-        for (int ch = 0; ch < cmax; ++ch) acc[ch] = fmaf(gout[(int64_t)n[u] * C + ch], w, acc[ch]);
-      }
-    }
-  }
-  for (int ch = 0; ch < 4; ++ch) {
-    acc[ch] += __shfl_xor(acc[ch], 1, kWave);
-    acc[ch] += __shfl_xor(acc[ch], 2, kWave);
-  }
-  if (live && q == 0)
-    for (int ch = 0; ch < cmax; ++ch) gfield[((int64_t)b * C + ch) * plane + o] += acc[ch];
-}
-
-GridPlanGeo grid_geo(int64_t B, int64_t Hg, int64_t Wg, int64_t N, int64_t img_h, int64_t img_w) {
-  GridPlanGeo g;
-  g.B = (int)B; g.Hg = (int)Hg; g.Wg = (int)Wg; g.N = (int)N;
-  g.nblk = (int)((N + kGridPerBlock - 1) / kGridPerBlock);
-  g.nb = (int)((B * Hg * Wg + kGridKeys - 1) / kGridKeys);
-  g.scale = img_h > 0 && img_w > 0;
-  g.sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1);
-  g.syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
-  return g;
-}
-
-struct GridPlanLayout {
-  int64_t cnt, boff, part, start, tkey, tidx, sidx, bytes;
-};
-
-int64_t align256(int64_t n) { return (n + 255) & ~(int64_t)255; }
-
-GridPlanLayout grid_layout(const GridPlanGeo& g) {
-  GridPlanLayout L;
-  const int64_t nbh = (int64_t)g.nb * g.nblk;
-  int64_t off = 0;
-  L.cnt = off;   off += align256(nbh * 4);
-  L.boff = off;  off += align256((nbh + 1) * 4);
-  L.part = off;  off += align256((scan_tiles(nbh > 0 ? nbh : 1) + 1) * 4);
-  L.start = off; off += align256(((int64_t)g.nb * kGridKeys + 1) * 4);
-  L.tkey = off;  off += align256((int64_t)g.N * 4);
-  L.tidx = off;  off += align256((int64_t)g.N * 4);
-  L.sidx = off;  off += align256((int64_t)g.N * 4);
-  L.bytes = off;
-  return L;
-}
-
-bool grid_plan_ok(int64_t B, int64_t Hg, int64_t Wg, int64_t N) {
-  return B >= 1 && Hg >= 1 && Wg >= 1 && N >= 0 && (double)B * Hg * Wg < 1.0e9 && N < ((int64_t)1 << 30) &&
-         (B * Hg * Wg + kGridKeys - 1) / kGridKeys <= 16384;
-}
-
 }  // namespace
 
 // ================================================================================================ C-ABI
@@ -593,50 +408,6 @@ int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int
   hipLaunchKernelGGL(k_sample_grid_bwd, dim3(grid_for(N)), dim3(kBlock), 0, stream, gout, B, (int)C, (int)Hg,
                      (int)Wg, (const float2*)pos, b, N, sxw, syh, scale, gfield);
   return check_launch("sample_grid_bwd");
-}
-
-int64_t atl_grid_plan_bytes(int64_t B, int64_t Hg, int64_t Wg, int64_t N) {
-  if (!grid_plan_ok(B, Hg, Wg, N)) return -1;
-  return grid_layout(grid_geo(B, Hg, Wg, N, 0, 0)).bytes;
-}
-
-int atl_grid_plan(int64_t B, int64_t Hg, int64_t Wg, const float* pos, const int64_t* b, int64_t N, int64_t img_h,
-                  int64_t img_w, void* ws, int64_t ws_bytes, hipStream_t stream) {
-  if (!grid_plan_ok(B, Hg, Wg, N)) { set_error("grid_plan: bad sizes B=%lld Hg=%lld Wg=%lld N=%lld", (long long)B, (long long)Hg, (long long)Wg, (long long)N); return 1; }
-  const GridPlanGeo g = grid_geo(B, Hg, Wg, N, img_h, img_w);
-  const GridPlanLayout L = grid_layout(g);
-  if (!ws || ws_bytes < L.bytes) { set_error("grid_plan: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
-  if (N > 0 && (!pos || !b)) { set_error("grid_plan: null input"); return 1; }
-  char* w = (char*)ws;
-  int* cnt = (int*)(w + L.cnt);
-  int* boff = (int*)(w + L.boff);
-  const int64_t nbh = (int64_t)g.nb * g.nblk;
-  const size_t lds = (size_t)g.nb * sizeof(int);
-  if (g.nblk > 0) {
-    hipLaunchKernelGGL(k_grid_pass1<false>, dim3(g.nblk), dim3(kBlock), lds, stream, (const float2*)pos, b, g, cnt,
-                       (int*)nullptr, (int*)nullptr);
-    scan32(cnt, nbh, (int*)(w + L.part), boff, stream);
-    hipLaunchKernelGGL(k_grid_pass1<true>, dim3(g.nblk), dim3(kBlock), lds, stream, (const float2*)pos, b, g, boff,
-                       (int*)(w + L.tkey), (int*)(w + L.tidx));
-  } else {
-    hipLaunchKernelGGL(k_fill_i32_ev, dim3(1), dim3(64), 0, stream, boff, 1);
-  }
-  hipLaunchKernelGGL(k_grid_pass2, dim3(g.nb), dim3(kGridSortBlock), 0, stream, (const int*)boff,
-                     (const int*)(w + L.tkey), (const int*)(w + L.tidx), g, (int*)(w + L.start), (int*)(w + L.sidx));
-  return check_launch("grid_plan");
-}
-
-int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
-                                int64_t N, int64_t img_h, int64_t img_w, const void* ws, float* gfield,
-                                hipStream_t stream) {
-  if (!grid_plan_ok(B, Hg, Wg, N) || C < 1 || C > 4) { set_error("sample_grid_bwd_planned: bad sizes (C <= 4)"); return 1; }
-  if (!ws || !gfield || (N > 0 && (!gout || !pos))) { set_error("sample_grid_bwd_planned: null argument"); return 1; }
-  const GridPlanGeo g = grid_geo(B, Hg, Wg, N, img_h, img_w);
-  const GridPlanLayout L = grid_layout(g);
-  const char* w = (const char*)ws;
-  hipLaunchKernelGGL(k_grid_gather, dim3(grid_for(4 * B * Hg * Wg)), dim3(kBlock), 0, stream, gout, (int)C,
-                     (const float2*)pos, g, (const int*)(w + L.start), (const int*)(w + L.sidx), gfield);
-  return check_launch("sample_grid_bwd_planned");
 }
 
 }  // extern "C"

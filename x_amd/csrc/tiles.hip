@@ -1,0 +1,461 @@
+// Tile-binned accumulation of per-event contributions into an image or a flow grid, without per-corner
+// global atomics: the bilinear splat forward (csrc/atl_cpu.cpp:38-56), the image gradient of the bilinear
+// gather (csrc/atl_cpu.cpp:151-172) and the adjoint of the flow-grid lookup (atl/motion/parametric.py:235-251).
+//
+// Device-wide float atomics are resolved in the memory fabric on this multi-XCD part and run at ~25 G/s when
+// scattered, and events concentrated on edges put many of them on the same pixels.  Here every call:
+//   1. bins the events by the 16x16 (or 32x32) tile of their base corner: an LDS histogram per block of 4096
+//      events, a device scan, and a scatter of 16-byte records (x, y, value, event index) into tile order;
+//   2. splits the tile-ordered records into equal ranges, one per workgroup, which adds the weighted
+//      contributions of each tile segment of its range into an LDS copy of the (T+1) x (T+1) pixels they can
+//      reach (corners reach one past the tile);
+//   3. flushes every non-zero LDS pixel with one global atomic add (neighbouring tiles share their border row
+//      and column, and a crowded tile spans several ranges, so the flush stays atomic; it costs at most
+//      (T+1)^2 atomics per tile segment).
+// Corner indices and weights are computed exactly as by the per-event kernels (same fp32 expressions), so the
+// set of touched pixels is identical; only the order of the float additions differs.
+#include "common.h"
+#include "scan.h"
+#include "../../include/atl_hip.h"
+
+#include <cmath>
+
+using namespace atlhip;
+
+namespace {
+
+constexpr int kTilePerBlock = 4096;              // binning: events per block
+constexpr int kTileBinBlock = 512;               // binning: threads per block (8 events each)
+constexpr int kTileMaxKeys = 16384;              // LDS histogram capacity (tiles over all batches)
+constexpr int kAccBlock = 256;                   // accumulation: threads per tile
+
+enum { kImage = 0, kGrid = 1 };
+
+struct TileGeo {
+  int B, H, W;               // image (kImage) or grid (kGrid) extent
+  int T;                     // tile edge
+  int TX, TY, nkeys;         // tiles per row and column, B * TY * TX
+  int N, nblk;
+  int mode;
+  int scale;                 // kGrid: positions are image pixels mapped by sxw, syh
+  float sxw, syh;
+};
+
+__device__ __forceinline__ bool batch_ok(int64_t b, int64_t B) { return b >= 0 && b < B; }
+
+// kImage: base corner (floor(x), floor(y)) and the in-image test of csrc/atl_cpu.cpp:17-33 (the corners
+// themselves are re-tested one by one when they are added).
+__device__ __forceinline__ bool image_base(float x, float y, int H, int W, int& x0, int& y0) {
+  const float fx = floorf(x), fy = floorf(y);
+  if (!(fx >= -1.f && fx <= (float)(W - 1) && fy >= -1.f && fy <= (float)(H - 1))) return false;
+  x0 = (int)fx;
+  y0 = (int)fy;
+  return true;
+}
+
+// kGrid: border-clamped grid corners of atl/motion/parametric.py:235-251 (x0 <= Wg - 2, x1 = min(x0 + 1, Wg - 1)).
+struct GridCell {
+  int x0, y0, x1, y1;
+  float ax, ay;
+};
+
+__device__ __forceinline__ GridCell grid_cell(float x, float y, int Hg, int Wg, float sxw, float syh, bool scale) {
+  float gx = x, gy = y;
+  if (scale) {
+    gx = x / sxw * (float)(Wg - 1);
+    gy = y / syh * (float)(Hg - 1);
+  }
+  gx = fminf(fmaxf(gx, 0.f), (float)(Wg - 1));
+  gy = fminf(fmaxf(gy, 0.f), (float)(Hg - 1));
+  if (gx != gx) gx = 0.f;
+  if (gy != gy) gy = 0.f;
+  const float fx0 = fminf(floorf(gx), (float)max(Wg - 2, 0));
+  const float fy0 = fminf(floorf(gy), (float)max(Hg - 2, 0));
+  GridCell c;
+  c.ax = gx - fx0;
+  c.ay = gy - fy0;
+  c.x0 = (int)fx0;
+  c.y0 = (int)fy0;
+  c.x1 = min(c.x0 + 1, Wg - 1);
+  c.y1 = min(c.y0 + 1, Hg - 1);
+  return c;
+}
+
+// Tile key of event n (-1: contributes nothing) and its LDS origin.
+template <int MODE>
+__device__ __forceinline__ int tile_key(float x, float y, int64_t b, const TileGeo& g) {
+  if (!batch_ok(b, g.B)) return -1;
+  int tx, ty;
+  if (MODE == kImage) {
+    int x0, y0;
+    if (!image_base(x, y, g.H, g.W, x0, y0)) return -1;
+    tx = (x0 + 1) / g.T;
+    ty = (y0 + 1) / g.T;
+  } else {
+    const GridCell c = grid_cell(x, y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
+    tx = c.x0 / g.T;
+    ty = c.y0 / g.T;
+  }
+  return ((int)b * g.TY + ty) * g.TX + tx;
+}
+
+// Binning.  SCATTER = false: per-block tile histogram into cnt[key * nblk + block].  SCATTER = true: the
+// block's scanned offsets are loaded into LDS and every event writes (x, y, value, index) to its slot.
+template <int MODE, bool SCATTER>
+__global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __restrict__ pos,
+                                                            const int64_t* __restrict__ bidx,
+                                                            const float* __restrict__ val, TileGeo g,
+                                                            int* __restrict__ cnt, float4* __restrict__ rec) {
+  extern __shared__ int hist[];
+  const int blk = blockIdx.x;
+  for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) hist[i] = SCATTER ? cnt[i * g.nblk + blk] : 0;
+  __syncthreads();
+  constexpr int per = kTilePerBlock / kTileBinBlock;
+  const int j0 = blk * kTilePerBlock;
+  float2 p[per];
+  int64_t bj[per];
+  float vj[per];
+#pragma unroll
+  for (int u = 0; u < per; ++u) {
+    const int j = j0 + u * kTileBinBlock + threadIdx.x;
+    bj[u] = j < g.N ? bidx[j] : -1;
+    vj[u] = 1.f;
+    if (j < g.N) {
+      p[u] = pos[j];
+      if (val) vj[u] = val[j];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < per; ++u) {
+    const int j = j0 + u * kTileBinBlock + threadIdx.x;
+    if (j >= g.N || vj[u] == 0.f) continue;      // a zero weight adds nothing (csrc/atl_cpu.cpp:44)
+    const int key = tile_key<MODE>(p[u].x, p[u].y, bj[u], g);
+    if (key < 0) continue;
+    const int slot = atomicAdd(hist + key, 1);
+    if (SCATTER) rec[slot] = make_float4(p[u].x, p[u].y, vj[u], __int_as_float(j));
+  }
+  if (!SCATTER) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) cnt[i * g.nblk + blk] = hist[i];
+  }
+}
+
+// Accumulation: workgroup w takes the records [w * kAccRange, (w + 1) * kAccRange) of the tile-ordered array
+// (so a crowded tile is shared by several workgroups and every workgroup has the same work), and for each
+// tile segment inside its range adds the contributions into LDS and flushes the non-zero pixels.
+// kImage, C = 1: value * bilinear corner weight into out (B, H, W), zero padding.
+// kGrid: gout[j * C + c] * corner weight into out (B, C, Hg, Wg).
+constexpr int kAccItems = 8;
+constexpr int kAccRange = kAccBlock * kAccItems;
+
+template <int MODE, int C, int T>
+__device__ __forceinline__ void accum_record(const float4& q, const float* __restrict__ gout, const TileGeo& g,
+                                             int ox, int oy, float* acc) {
+  constexpr int L = T + 1;
+  if (MODE == kImage) {
+    int x0, y0;
+    if (!image_base(q.x, q.y, g.H, g.W, x0, y0)) return;   // never taken: the binning applied this test
+    const float fx = (float)x0, fy = (float)y0;
+    const float ax = q.x - fx, ay = q.y - fy;
+    const float wx0 = 1.f - ax, wy0 = 1.f - ay;
+#pragma unroll
+    for (int jy = 0; jy < 2; ++jy) {
+      const int yy = y0 + jy;
+      if (yy < 0 || yy >= g.H) continue;
+      const float wy = jy ? ay : wy0;
+#pragma unroll
+      for (int ix = 0; ix < 2; ++ix) {
+        const int xx = x0 + ix;
+        if (xx < 0 || xx >= g.W) continue;
+        const float wx = ix ? ax : wx0;
+        const int ly = yy - oy, lx = xx - ox;
+        if ((unsigned)ly < (unsigned)L && (unsigned)lx < (unsigned)L) atomicAdd(acc + ly * L + lx, q.z * (wx * wy));
+      }
+    }
+  } else {
+    const GridCell c = grid_cell(q.x, q.y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
+    const int j = __float_as_int(q.w);
+    const float w00 = (1.f - c.ax) * (1.f - c.ay), w01 = c.ax * (1.f - c.ay);
+    const float w10 = (1.f - c.ax) * c.ay, w11 = c.ax * c.ay;
+    const int ly0 = c.y0 - oy, ly1 = c.y1 - oy, lx0 = c.x0 - ox, lx1 = c.x1 - ox;
+    if ((unsigned)ly0 >= (unsigned)L || (unsigned)ly1 >= (unsigned)L || (unsigned)lx0 >= (unsigned)L ||
+        (unsigned)lx1 >= (unsigned)L)
+      return;                                                // never taken: the binning chose this tile
+    const int i00 = ly0 * L + lx0, i01 = ly0 * L + lx1, i10 = ly1 * L + lx0, i11 = ly1 * L + lx1;
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch) {
+      const float go = gout[(int64_t)j * C + ch];
+      float* a = acc + ch * L * L;
+      atomicAdd(a + i00, go * w00);
+      atomicAdd(a + i01, go * w01);
+      atomicAdd(a + i10, go * w10);
+      atomicAdd(a + i11, go * w11);
+    }
+  }
+}
+
+template <int MODE, int C, int T>
+__global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict__ boff,
+                                                          const float4* __restrict__ rec,
+                                                          const float* __restrict__ gout, TileGeo g,
+                                                          float* __restrict__ out) {
+  constexpr int L = T + 1;
+  __shared__ float acc[C * L * L];
+  __shared__ int ts[kAccBlock + 1];                       // starts of the tiles first .. first + kAccBlock
+  __shared__ int found, found2;
+  const int total = boff[g.nkeys * g.nblk];
+  const int r0 = blockIdx.x * kAccRange;
+  if (r0 >= total) return;
+  const int r1 = min(r0 + kAccRange, total);
+  auto tstart = [&](int k) { return boff[min(k, g.nkeys) * g.nblk]; };   // tile k's first record; nkeys: total
+  // the last tile starting at or before r0, in two parallel rounds (coarse stride, then within the stride)
+  const int step = (g.nkeys + kAccBlock - 1) / kAccBlock;
+  if (threadIdx.x == 0) {
+    found = 0;
+    found2 = 0;
+  }
+  __syncthreads();
+  {
+    const int k = threadIdx.x * step;
+    if (k < g.nkeys && tstart(k) <= r0) atomicMax(&found, k);
+  }
+  __syncthreads();
+  const int coarse = found;
+  {
+    const int k = coarse + (int)threadIdx.x;
+    if (threadIdx.x < step && k < g.nkeys && tstart(k) <= r0) atomicMax(&found2, k);
+  }
+  __syncthreads();
+  const int64_t pl = (int64_t)g.H * g.W;
+  const int plane = g.TY * g.TX;
+  for (int base = max(coarse, found2); base < g.nkeys; base += kAccBlock) {
+    for (int i = threadIdx.x; i <= kAccBlock; i += kAccBlock) ts[i] = tstart(base + i);
+    __syncthreads();
+    bool done = false;
+    for (int i = 0; i < kAccBlock && base + i < g.nkeys; ++i) {
+      const int key = base + i;
+      const int s0 = max(r0, ts[i]), s1 = min(r1, ts[i + 1]);
+      if (s0 >= r1) {
+        done = true;
+        break;
+      }
+      if (s0 >= s1) continue;                             // empty tile
+      for (int a = threadIdx.x; a < C * L * L; a += kAccBlock) acc[a] = 0.f;
+      __syncthreads();
+      const int b = key / plane, r = key - b * plane;
+      const int ty = r / g.TX, tx = r - ty * g.TX;
+      const int ox = MODE == kImage ? tx * T - 1 : tx * T;   // pixel of LDS column 0
+      const int oy = MODE == kImage ? ty * T - 1 : ty * T;
+      float4 q[kAccItems];
+#pragma unroll
+      for (int u = 0; u < kAccItems; ++u) {
+        const int k = s0 + u * kAccBlock + threadIdx.x;
+        if (k < s1) q[u] = rec[k];
+      }
+#pragma unroll
+      for (int u = 0; u < kAccItems; ++u)
+        if (s0 + u * kAccBlock + (int)threadIdx.x < s1) accum_record<MODE, C, T>(q[u], gout, g, ox, oy, acc);
+      __syncthreads();
+      for (int a = threadIdx.x; a < L * L; a += kAccBlock) {
+        const int py = oy + a / L, px = ox + a % L;
+        if (py < 0 || py >= g.H || px < 0 || px >= g.W) continue;
+#pragma unroll
+        for (int ch = 0; ch < C; ++ch) {
+          const float v = acc[ch * L * L + a];
+          if (v != 0.f) atomicAdd(out + ((int64_t)b * C + ch) * pl + (int64_t)py * g.W + px, v);
+        }
+      }
+      __syncthreads();
+    }
+    if (done) break;
+    __syncthreads();                                      // ts is reloaded
+  }
+}
+
+// gpos of the bilinear gather backward (csrc/atl_cpu.cpp:151-172, the position half): per event, no atomics.
+__global__ void __launch_bounds__(kBlock) k_gather_bwd_pos(const float* __restrict__ gval,
+                                                           const float* __restrict__ img,
+                                                           const float2* __restrict__ pos,
+                                                           const int64_t* __restrict__ bidx, int64_t N, int64_t B,
+                                                           int H, int W, float2* __restrict__ gpos) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  const float gn = gval[n];
+  float sx = 0.f, sy = 0.f;
+  int x0, y0;
+  const float2 p = pos[n];
+  if (batch_ok(b, B) && image_base(p.x, p.y, H, W, x0, y0)) {
+    const float* base = img + b * (int64_t)H * W;
+    const float ax = p.x - (float)x0, ay = p.y - (float)y0;
+    const float wx0 = 1.f - ax, wy0 = 1.f - ay;
+#pragma unroll
+    for (int jy = 0; jy < 2; ++jy) {
+      const int yy = y0 + jy;
+      if (yy < 0 || yy >= H) continue;
+      const float wy = jy ? ay : wy0;
+      const float dwy = jy ? 1.f : -1.f;
+#pragma unroll
+      for (int ix = 0; ix < 2; ++ix) {
+        const int xx = x0 + ix;
+        if (xx < 0 || xx >= W) continue;
+        const float wx = ix ? ax : wx0;
+        const float dwx = ix ? 1.f : -1.f;
+        const float v = base[yy * W + xx];
+        sx += (dwx * wy) * v;
+        sy += (wx * dwy) * v;
+      }
+    }
+  }
+  gpos[n] = make_float2(gn * sx, gn * sy);
+}
+
+int64_t align256(int64_t n) { return (n + 255) & ~(int64_t)255; }
+
+// Geometry: the smallest tile edge (16 or 32) whose tile count fits the LDS histogram; false if none does.
+bool tile_geo(int mode, int64_t B, int64_t H, int64_t W, int64_t N, int64_t img_h, int64_t img_w, TileGeo& g) {
+  if (B < 1 || H < 1 || W < 1 || N < 0 || N >= ((int64_t)1 << 30) || (double)B * H * W >= 2.0e9) return false;
+  for (int T : {16, 32}) {
+    const int64_t tx = (W + 1 + T - 1) / T, ty = (H + 1 + T - 1) / T;
+    if (B * tx * ty <= kTileMaxKeys) {
+      g.B = (int)B; g.H = (int)H; g.W = (int)W; g.T = T;
+      g.TX = (int)tx; g.TY = (int)ty; g.nkeys = (int)(B * tx * ty);
+      g.N = (int)N;
+      g.nblk = (int)((N + kTilePerBlock - 1) / kTilePerBlock);
+      g.mode = mode;
+      g.scale = img_h > 0 && img_w > 0;
+      g.sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1);
+      g.syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
+      return (double)g.nkeys * g.nblk + 1 < 2.0e9;
+    }
+  }
+  return false;
+}
+
+struct TileLayout {
+  int64_t cnt, boff, part, rec, bytes;
+};
+
+TileLayout tile_layout(const TileGeo& g) {
+  TileLayout L;
+  const int64_t nbh = (int64_t)g.nkeys * g.nblk;
+  int64_t off = 0;
+  L.cnt = off;  off += align256(nbh * 4);
+  L.boff = off; off += align256((nbh + 1) * 4);
+  L.part = off; off += align256((scan_tiles(nbh > 0 ? nbh : 1) + 1) * 4);
+  L.rec = off;  off += align256((int64_t)g.N * 16);
+  L.bytes = off;
+  return L;
+}
+
+__global__ void k_tile_zero1(int* p) { p[0] = 0; }
+
+template <int MODE>
+void tile_bin(const TileGeo& g, const TileLayout& L, void* ws, const float* pos, const int64_t* b, const float* val,
+              hipStream_t stream) {
+  char* w = (char*)ws;
+  int* cnt = (int*)(w + L.cnt);
+  int* boff = (int*)(w + L.boff);
+  if (g.nblk == 0) {
+    hipLaunchKernelGGL(k_tile_zero1, dim3(1), dim3(1), 0, stream, boff);
+    return;
+  }
+  const size_t lds = (size_t)g.nkeys * sizeof(int);
+  hipLaunchKernelGGL((k_tile_bin<MODE, false>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
+                     b, val, g, cnt, (float4*)nullptr);
+  scan32(cnt, (int64_t)g.nkeys * g.nblk, (int*)(w + L.part), boff, stream);
+  hipLaunchKernelGGL((k_tile_bin<MODE, true>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
+                     b, val, g, boff, (float4*)(w + L.rec));
+}
+
+template <int MODE, int C>
+void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const float* gout, float* out,
+                hipStream_t stream) {
+  if (g.nblk == 0) return;
+  const char* w = (const char*)ws;
+  const unsigned grid = (unsigned)((g.N + kAccRange - 1) / kAccRange);   // records <= N
+  if (g.T == 16)
+    hipLaunchKernelGGL((k_tile_accum<MODE, C, 16>), dim3(grid), dim3(kAccBlock), 0, stream,
+                       (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, out);
+  else
+    hipLaunchKernelGGL((k_tile_accum<MODE, C, 32>), dim3(grid), dim3(kAccBlock), 0, stream,
+                       (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, out);
+}
+
+}  // namespace
+
+// ================================================================================================ C-ABI
+extern "C" {
+
+int64_t atl_tile_ws_bytes(int64_t N, int64_t B, int64_t H, int64_t W) {
+  TileGeo g;
+  if (!tile_geo(kImage, B, H, W, N, 0, 0, g)) return -1;
+  return tile_layout(g).bytes;
+}
+
+int atl_splat_bilinear_fwd_ws(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B, int64_t H,
+                              int64_t W, float* img, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  if (N == 0 || B == 0) return 0;
+  TileGeo g;
+  if (!tile_geo(kImage, B, H, W, N, 0, 0, g)) { set_error("splat_bilinear_fwd_ws: unsupported sizes N=%lld B=%lld H=%lld W=%lld", (long long)N, (long long)B, (long long)H, (long long)W); return 1; }
+  const TileLayout L = tile_layout(g);
+  if (!ws || ws_bytes < L.bytes) { set_error("splat_bilinear_fwd_ws: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
+  if (!pos || !w || !b || !img) { set_error("splat_bilinear_fwd_ws: null argument"); return 1; }
+  tile_bin<kImage>(g, L, ws, pos, b, w, stream);
+  tile_accum<kImage, 1>(g, L, ws, nullptr, img, stream);
+  return check_launch("splat_bilinear_fwd_ws");
+}
+
+int atl_gather_bilinear_bwd_ws(const float* gval, const float* img, const float* pos, const int64_t* b, int64_t N,
+                               int64_t B, int64_t H, int64_t W, float* gimg, float* gpos, void* ws, int64_t ws_bytes,
+                               hipStream_t stream) {
+  if (N == 0) return 0;
+  TileGeo g;
+  if (!tile_geo(kImage, B, H, W, N, 0, 0, g)) { set_error("gather_bilinear_bwd_ws: unsupported sizes"); return 1; }
+  const TileLayout L = tile_layout(g);
+  if (!ws || ws_bytes < L.bytes) { set_error("gather_bilinear_bwd_ws: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
+  if (!gval || !img || !pos || !b || !gimg || !gpos) { set_error("gather_bilinear_bwd_ws: null argument"); return 1; }
+  hipLaunchKernelGGL(k_gather_bwd_pos, dim3(grid_for(N)), dim3(kBlock), 0, stream, gval, img, (const float2*)pos, b,
+                     N, B, (int)H, (int)W, (float2*)gpos);
+  tile_bin<kImage>(g, L, ws, pos, b, gval, stream);
+  tile_accum<kImage, 1>(g, L, ws, nullptr, gimg, stream);
+  return check_launch("gather_bilinear_bwd_ws");
+}
+
+// Flow-grid adjoint through a tile plan: atl_grid_plan bins the positions once (in the forward), and
+// atl_sample_grid_bwd_planned accumulates gout into gfield tile by tile.
+int64_t atl_grid_plan_bytes(int64_t B, int64_t Hg, int64_t Wg, int64_t N) {
+  TileGeo g;
+  if (!tile_geo(kGrid, B, Hg, Wg, N, 0, 0, g)) return -1;
+  return tile_layout(g).bytes;
+}
+
+int atl_grid_plan(int64_t B, int64_t Hg, int64_t Wg, const float* pos, const int64_t* b, int64_t N, int64_t img_h,
+                  int64_t img_w, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  TileGeo g;
+  if (!tile_geo(kGrid, B, Hg, Wg, N, img_h, img_w, g)) { set_error("grid_plan: bad sizes B=%lld Hg=%lld Wg=%lld N=%lld", (long long)B, (long long)Hg, (long long)Wg, (long long)N); return 1; }
+  const TileLayout L = tile_layout(g);
+  if (!ws || ws_bytes < L.bytes) { set_error("grid_plan: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
+  if (N > 0 && (!pos || !b)) { set_error("grid_plan: null input"); return 1; }
+  tile_bin<kGrid>(g, L, ws, pos, b, nullptr, stream);
+  return check_launch("grid_plan");
+}
+
+int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                                int64_t N, int64_t img_h, int64_t img_w, const void* ws, float* gfield,
+                                hipStream_t stream) {
+  TileGeo g;
+  if (!tile_geo(kGrid, B, Hg, Wg, N, img_h, img_w, g) || C < 1 || C > 4) { set_error("sample_grid_bwd_planned: bad sizes (C <= 4)"); return 1; }
+  if (!ws || !gfield || (N > 0 && !gout)) { set_error("sample_grid_bwd_planned: null argument"); return 1; }
+  (void)pos;                                     // the plan's records carry the positions
+  const TileLayout L = tile_layout(g);
+  switch (C) {
+    case 1: tile_accum<kGrid, 1>(g, L, ws, gout, gfield, stream); break;
+    case 2: tile_accum<kGrid, 2>(g, L, ws, gout, gfield, stream); break;
+    case 3: tile_accum<kGrid, 3>(g, L, ws, gout, gfield, stream); break;
+    default: tile_accum<kGrid, 4>(g, L, ws, gout, gfield, stream); break;
+  }
+  return check_launch("sample_grid_bwd_planned");
+}
+
+}  // extern "C"

@@ -55,6 +55,9 @@ _SIGS = {
     "atl_anchored_epilogue_fwd": [_P, _P, _P, _I, _D, _D, _P, _P, _P, _P],
     "atl_anchored_epilogue_bwd": [_P, _P, _P, _I, _P, _P],
     "atl_grid_plan_bytes": [_I, _I, _I, _I],
+    "atl_tile_ws_bytes": [_I, _I, _I, _I],
+    "atl_splat_bilinear_fwd_ws": [_P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P],
+    "atl_gather_bilinear_bwd_ws": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P],
     "atl_grid_plan": [_I, _I, _I, _P, _P, _I, _I, _I, _P, _I, _P],
     "atl_sample_grid_bwd_planned": [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _P],
     "atl_fast_geometry_init": [_I, _I, _I, _I, _I, _I, _D, _D, _D, _P],
@@ -62,7 +65,8 @@ _SIGS = {
     "atl_fast_pair_fwd": [_P, _P, _P, _P, _P],
     "atl_fast_pair_bwd": [_P, _P, _P, _P, _P],
 }
-_RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.c_int64, "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
+_RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.c_int64,
+            "atl_tile_ws_bytes": ctypes.c_int64, "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):
     """Mirror of ``atl_fast_geometry`` (include/atl_hip.h): sizes, grid and workspace layout of the fused
@@ -178,9 +182,15 @@ class HipOps:
         N = pos.shape[0]
         _need(pos, "pos", F32, dev, (N, 2)); _need(w, "w", F32, dev, (N,)); _need(b, "b", I64, dev, (N,))
         img = torch.zeros(int(B), int(H), int(W), device=dev, dtype=F32)
+        nbytes = load_library().atl_tile_ws_bytes(N, int(B), int(H), int(W)) if N > 0 and int(B) > 0 else -1
         with torch.cuda.device(dev):
-            call("atl_splat_bilinear_fwd", ptr(pos), ptr(w), ptr(b), N, int(B), int(H), int(W), ptr(img),
-                 stream_of(pos))
+            if nbytes >= 0:          # tile-binned LDS accumulation
+                ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+                call("atl_splat_bilinear_fwd_ws", ptr(pos), ptr(w), ptr(b), N, int(B), int(H), int(W), ptr(img),
+                     ptr(ws), nbytes, stream_of(pos))
+            else:                    # too many tiles for the binning: one atomic per corner
+                call("atl_splat_bilinear_fwd", ptr(pos), ptr(w), ptr(b), N, int(B), int(H), int(W), ptr(img),
+                     stream_of(pos))
         return img
 
     def splat_bilinear_bwd(self, gimg, pos, w, b):
@@ -234,9 +244,15 @@ class HipOps:
         _need(b, "b", I64, dev, (N,))
         B, H, W = img.shape
         gimg = torch.zeros_like(img); gpos = torch.empty_like(pos)
+        nbytes = load_library().atl_tile_ws_bytes(N, B, H, W) if N > 0 and B > 0 else -1
         with torch.cuda.device(dev):
-            call("atl_gather_bilinear_bwd", ptr(gval), ptr(img), ptr(pos), ptr(b), N, B, H, W, ptr(gimg), ptr(gpos),
-                 stream_of(pos))
+            if nbytes >= 0:          # tile-binned LDS accumulation of gimg
+                ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+                call("atl_gather_bilinear_bwd_ws", ptr(gval), ptr(img), ptr(pos), ptr(b), N, B, H, W, ptr(gimg),
+                     ptr(gpos), ptr(ws), nbytes, stream_of(pos))
+            else:
+                call("atl_gather_bilinear_bwd", ptr(gval), ptr(img), ptr(pos), ptr(b), N, B, H, W, ptr(gimg),
+                     ptr(gpos), stream_of(pos))
         return [gimg, gpos]
 
     def voxel_grid(self, pos, t, p, b, B, C, H, W):
