@@ -45,7 +45,7 @@ constexpr int kSortBlock = 256;                    // pass-2 workgroup
 constexpr int kP1Block = 512;                      // pass-1 workgroup
 constexpr int kSrcPerBlock = 4096;                 // pass-1 sources per block (8 per thread)
 constexpr int kAncPerBlock = 8192;                 // pass-1 anchors per block (16 per thread)
-constexpr int kUnroll = 2;                         // candidates per walk step (record arrays padded by this)
+constexpr int kUnroll = 4;                         // candidates per walk step (record arrays padded by this)
 
 constexpr int kXcd = 8;                            // XCDs: consecutive workgroups go round-robin over them
 
@@ -449,14 +449,16 @@ __device__ __forceinline__ bool pair_test(int id_a, int id_s, float ta, float ts
 }
 
 // ------------------------------------------------------------------------------------------ walks
-// Queries come in cell order, 64 to a wave.  Forward: the anchors of one cell form a group; the group's
-// anchors are wave-uniform and the lanes take 64 candidates of the group's common neighbourhood at a time
+// Queries come in cell order, 64 to a wave.  Forward: the anchors of up to kGroupCells consecutive cells of
+// one row form a group; the group's anchors are wave-uniform and the lanes take 64 candidates of the group's
+// common neighbourhood at a time
 // (coalesced loads, each candidate read once for the whole group); every anchor's sum is reduced across
 // the wave after its last chunk.  A walk with one lane per anchor reads a different cache line in every
 // lane, and that is what bounds it.  Backward: one lane per source walks its own neighbourhoods (sources'
 // per-slice positions differ, so a group shares less there than it costs to set up).
 
 constexpr int kGroup = 8;                          // queries evaluated per pass over a group's candidates
+constexpr int kGroupCells = 3;                     // a forward group spans up to this many cells of one row
 
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ float unif(float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); }
@@ -597,8 +599,8 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
 // repeat the last anchor and are discarded): lane src0 + a receives anchor a's sum (and count) in mine
 // (mine_n).  es is each anchor lane's own entry position: the leave-one-out test skips that candidate.
 template <int WD, bool COUNT>
-__device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plane, float x0, float y0, float R,
-                                         float R2, const float4& A, int es, int src0, int na, int lane,
+__device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plane, float x0, float x1, float y0,
+                                         float R, float R2, const float4& A, int es, int src0, int na, int lane,
                                          float& mine, int& mine_n) {
   float ax[WD], ay[WD], ta[WD], at[WD], acc[WD];
   int id[WD], cnt[WD];
@@ -613,7 +615,7 @@ __device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plan
     acc[a] = 0.f;
     cnt[a] = 0;
   }
-  group_walk(p.start, 0, plane, x0, x0 + G.cf, y0, y0 + G.cf, R, R2, G, [&](int pos) {
+  group_walk(p.start, 0, plane, x0, x1, y0, y0 + G.cf, R, R2, G, [&](int pos) {
     const uint32_t k = (uint32_t)max(pos, 0);
     const float4 e = ld(p.epos, k);
     const float ts = ld(p.etim, k);
@@ -671,24 +673,28 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
   while (todo) {
     const int i = __ffsll((unsigned long long)todo) - 1;
     const int gkey = rdlane(key, i);
-    const uint64_t gmask = __ballot(have && key == gkey);
-    todo &= ~gmask;
-    const int gsize = __popcll(gmask);           // lanes i .. i + gsize - 1 (cell order)
     const int g = gkey / plane_cells;
     const int rem = gkey - g * plane_cells;
     const int cy = rem / G.GW, cx = rem - cy * G.GW;
-    const float x0 = G.gx0 + (float)cx * G.cf, y0 = G.gy0 + (float)cy * G.cf;
+    // the group: anchors of up to kGroupCells consecutive cells of one row (lanes i .. i + gsize - 1)
+    const int span = min(kGroupCells, G.GW - cx);
+    const uint64_t gmask = __ballot(have && key >= gkey && key - gkey < span) & todo;
+    todo &= ~gmask;
+    const int gsize = __popcll(gmask);
+    const int last_cx = cx + (rdlane(key, i + gsize - 1) - gkey);
+    const float x0 = G.gx0 + (float)cx * G.cf, x1 = G.gx0 + (float)(last_cx + 1) * G.cf;
+    const float y0 = G.gy0 + (float)cy * G.cf;
+    const int plane = g * plane_cells;
     for (int a0 = 0; a0 < gsize; a0 += kGroup) {
       const int na = min(kGroup, gsize - a0);
-      const int plane = g * plane_cells;
       if (na == 1)
-        fwd_pass<1, COUNT>(p, G, plane, x0, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<1, COUNT>(p, G, plane, x0, x1, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
       else if (na == 2)
-        fwd_pass<2, COUNT>(p, G, plane, x0, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<2, COUNT>(p, G, plane, x0, x1, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
       else if (na <= 4)
-        fwd_pass<4, COUNT>(p, G, plane, x0, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<4, COUNT>(p, G, plane, x0, x1, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
       else
-        fwd_pass<kGroup, COUNT>(p, G, plane, x0, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<kGroup, COUNT>(p, G, plane, x0, x1, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
     }
   }
   if (have) {

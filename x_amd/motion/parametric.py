@@ -43,12 +43,22 @@ class VectorFieldMotion(Motion):
         return xy + self.field(xy, b) * dt[:, None]
 
 
+def per_event(theta: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """theta[b] (per-event copy of the per-batch parameters).  Its gradient is a sum over the events of each
+    batch item: with one item an expand (the backward is one reduction), otherwise index_select (index_add in
+    the backward); advanced indexing would instead backpropagate through an accumulating index_put, which
+    serialises over the repeated indices."""
+    if theta.shape[0] == 1:
+        return theta.expand(b.shape[0], theta.shape[1])
+    return theta.index_select(0, b)
+
+
 class Translation(VectorFieldMotion):
     """v = (tx, ty) (atl/motion/parametric.py:87-97)."""
     n_params = 2
 
     def field(self, xy, b):
-        return self.theta[b]
+        return per_event(self.theta, b)
 
 
 class Sim2(VectorFieldMotion):
@@ -56,7 +66,7 @@ class Sim2(VectorFieldMotion):
     n_params = 4
 
     def field(self, xy, b):
-        th = self.theta[b]
+        th = per_event(self.theta, b)
         d = xy - self.c.to(xy)
         vx = th[:, 0] + (th[:, 2] * d[:, 0] - th[:, 3] * d[:, 1])
         vy = th[:, 1] + (th[:, 3] * d[:, 0] + th[:, 2] * d[:, 1])
