@@ -15,6 +15,8 @@ Other workloads (parity-test configurations, not the headline metric), same outp
                                                # (inside mask), gather of the IWE at the warped events,
                                                # loss = sum, backward to the flow grid
     python bench.py --workload iwe-plumbing    # the same on 100k events 240x180, constant flow (2, -1.25)
+    python bench.py --workload anchored-blobs  # contention stress: the anchored score on 4M events, 90% in 5
+                                               # Gaussian blobs (sigma 8 px), Sim2 flow (0, 0, 0.1, 0.1)
 
 Two helpers for the rocprofv3 summaries under profiles/ (no GPU work beyond what they name):
 
@@ -53,11 +55,11 @@ COUNTERS = ROOT / "profiles" / "anchored_score_1M_640x480_counters.md"
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", default="anchored", choices=["anchored", "iwe", "iwe-plumbing"])
+    ap.add_argument("--workload", default="anchored", choices=["anchored", "anchored-blobs", "iwe", "iwe-plumbing"])
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--sigma", type=float, default=1.0)
-    ap.add_argument("--events", type=int, default=1_000_000)
+    ap.add_argument("--events", type=int, default=0, help="events of the anchored workloads (default 1M; 4M blobs)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=25.0, help="seconds of CPU baseline work, at most")
     ap.add_argument("--calibrate-copy", type=float, default=0.0, metavar="MB")
@@ -149,15 +151,50 @@ def calibrate_copy(mb):
     print(json.dumps({"calibration_copy_mib": mb, "elements": n}), flush=True)
 
 
-def workload(n_events, device):
+def workload(kind, n_events, device):
     from x_amd import synth
     from x_amd.core import EventPacket
-    from x_amd.motion import DenseLinearFlow
-    win = synth.dense_flow_window(seed=0, n=n_events)
-    ev = EventPacket.from_window(win, device)
-    grid = win.motion["grid"]
-    motion = DenseLinearFlow(1, win.height, win.width, grid=grid.shape[-2:], init=torch.as_tensor(grid)).to(device)
-    return win, ev, motion
+    from x_amd.motion import DenseLinearFlow, Sim2
+    if kind == "anchored-blobs":
+        win = synth.blob_window(seed=0, n=n_events)
+        motion = Sim2(1, win.height, win.width, init=torch.as_tensor(win.motion["theta"])[None])
+        desc = (f"anchored score fwd+bwd, {win.n} events, 640x480, 90% in 5 Gaussian blobs (sigma 8 px) + 10% "
+                f"noise, Sim2 flow (0, 0, 0.1, 0.1) per window")
+    else:
+        win = synth.dense_flow_window(seed=0, n=n_events)
+        grid = win.motion["grid"]
+        motion = DenseLinearFlow(1, win.height, win.width, grid=grid.shape[-2:], init=torch.as_tensor(grid))
+        desc = f"anchored score fwd+bwd, {win.n} events, 640x480, dense flow 2x480x640"
+    return win, EventPacket.from_window(win, device), motion.to(device), desc
+
+
+def _velocity_np(win, xy, b):
+    """The window's motion field at xy (NumPy, fp32 op order of the motion models) and, for a dense grid,
+    the flow-lookup indices and weights."""
+    import oracle as O
+    if win.motion["kind"] == "dense":
+        return O.dense_velocity(win.motion["grid"], xy, b, win.height, win.width)
+    th = win.motion["theta"].astype(np.float32)
+    c = np.array([(win.width - 1) / 2.0, (win.height - 1) / 2.0], np.float32)
+    d = (xy - c).astype(np.float32)
+    vx = th[0] + (th[2] * d[:, 0] - th[3] * d[:, 1])
+    vy = th[1] + (th[3] * d[:, 0] + th[2] * d[:, 1])
+    return np.stack([vx, vy], 1).astype(np.float32), None, None
+
+
+def _bounded_run(run, n_all, budget):
+    """Time prefixes of the (time-sorted) window of 20k, 40k, 80k, ... events until one takes more than a
+    quarter of the budget or covers the whole window; the work per event grows with the prefix (a short prefix
+    truncates the +-tau neighbourhoods), at most quadratically, so the last run stays within the budget.
+    Returns (events, seconds, events of the previous run)."""
+    n, prev = min(n_all, 20_000), 0
+    while True:
+        t0 = time.perf_counter()
+        run(n)
+        dt = time.perf_counter() - t0
+        if dt > budget / 4 or n >= n_all:
+            return n, dt, prev
+        prev, n = n, min(n_all, 2 * n)
 
 
 def cpu_baseline(win, sigma, budget):
@@ -168,34 +205,29 @@ def cpu_baseline(win, sigma, budget):
     rng = np.random.default_rng(0)
     xs = (win.xy + rng.uniform(-0.5, 0.5, win.xy.shape)).astype(np.float32)
     xa = (xs + sigma * rng.standard_normal(xs.shape)).astype(np.float32)
-    grid = win.motion["grid"]
+    dense = win.motion["kind"] == "dense"
 
     def run(n):
         sl = slice(0, n)
-        v, idx, wts = O.dense_velocity(grid, xs[sl], win.b[sl], H, W)
+        v, idx, wts = _velocity_np(win, xs[sl], win.b[sl])
         anchors = np.arange(n)
         p = O.build_pair_plan(xs[sl], win.t[sl], v, win.b[sl], 1, H, W, anchors, sigma, 0.2, 3.0, 16,
                               anchor_xy=xa[sl])
         S = O.ats_pair_fwd(p, sigma, 0.2, 3.0)
         wc = O.window_counts(win.t[sl], win.b[sl], anchors, 0.2)
-        vis = O.visible_fraction_dense(grid, xa[sl], win.t[sl], win.b[sl], win.t[sl], win.b[sl], 1, H, W, 0.2)
+        vis = (O.visible_fraction_dense(win.motion["grid"], xa[sl], win.t[sl], win.b[sl], win.t[sl], win.b[sl], 1,
+                                        H, W, 0.2) if dense else None)
         _, gS, _ = O.anchored_epilogue(S, wc, sigma, H, W, vis=vis)
         gv = O.ats_pair_bwd(gS, p, sigma, 0.2, 3.0, n)
-        O.sample_grid_bwd(gv, idx, wts, grid.shape)
+        if dense:
+            O.sample_grid_bwd(gv, idx, wts, win.motion["grid"].shape)
 
-    run(min(win.n, 50_000))
-    n = win.n
-    t0 = time.perf_counter()
-    run(n)
-    dt = time.perf_counter() - t0
-    if dt > budget:      # keep the baseline bounded: time a prefix of the (time-sorted) window instead
-        n = max(int(win.n * budget / dt / 2), 10_000)
-        t0 = time.perf_counter()
-        run(n)
-        dt = time.perf_counter() - t0
+    n, dt, _ = _bounded_run(run, win.n, budget)
     return {"value": n / dt, "unit": "events/s", "cores": O.num_threads(), "kind": "port",
-            "sample": f"anchored score fwd+bwd on the first {n} events of the same window "
-                      f"(time-sorted prefix), one timed run after a 50k-event warm-up, {dt:.2f} s"}
+            "sample": (f"anchored score fwd+bwd on the whole window, {dt:.2f} s" if n == win.n else
+                       f"anchored score fwd+bwd on the first {n} events of the same window (time-sorted prefix, "
+                       f"the largest of a doubling series that fits the budget; it truncates the +-tau "
+                       f"neighbourhoods near its end), {dt:.2f} s")}
 
 
 # ----------------------------------------------------------------------------------------- IWE workloads
@@ -254,19 +286,11 @@ def iwe_cpu_baseline(win, t_ref, budget):
         else:
             gv.sum(0)
 
-    run(min(win.n, 50_000))
-    n = win.n
-    t0 = time.perf_counter()
-    run(n)
-    dt = time.perf_counter() - t0
-    if dt > budget:
-        n = max(int(win.n * budget / dt / 2), 10_000)
-        t0 = time.perf_counter()
-        run(n)
-        dt = time.perf_counter() - t0
+    n, dt, _ = _bounded_run(run, win.n, budget)
     return {"value": n / dt, "unit": "events/s", "cores": O.num_threads(), "kind": "port",
-            "sample": f"IWE step on the first {n} events of the same window, one timed run after a 50k-event "
-                      f"warm-up, {dt:.2f} s"}
+            "sample": (f"IWE step on the whole window, {dt:.2f} s" if n == win.n else
+                       f"IWE step on the first {n} events of the same window (time-sorted prefix, the largest of "
+                       f"a doubling series that fits the budget), {dt:.2f} s")}
 
 
 def iwe_main(a, dev):
@@ -327,7 +351,7 @@ def main():
         print(f"bench.py measures one GPU only (asked for {a.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
         sys.exit(2)
-    if a.workload != "anchored":
+    if a.workload.startswith("iwe"):
         dev = torch.device("cuda:0")
         torch.cuda.set_device(dev)
         iwe_main(a, dev)
@@ -337,11 +361,13 @@ def main():
     from x_amd.ops import functional as F
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    win, ev, motion = workload(a.events, dev)
+    n_events = a.events if a.events else (4_000_000 if a.workload == "anchored-blobs" else 1_000_000)
+    win, ev, motion, desc = workload(a.workload, n_events, dev)
     obj = AnchoredExact(h=a.sigma, tau=0.2, cut=3.0, n_slices=16, n_anchors=None, seed=0, rng="device")
 
     def step():
-        motion.grid.grad = None
+        for prm in motion.parameters():
+            prm.grad = None
         out = obj(ev, motion)
         out["loss"].backward()
 
@@ -373,12 +399,13 @@ def main():
     flops = K * (FLOPS_FWD if fwd else FLOPS_BWD) / (ms[dom] * 1e-3)
     value = ev.n * a.steps / dt
     line = {
-        "metric": "events/s for anchored-score fwd+bwd @1M events 640x480; % HBM/VALU roofline",
+        "metric": ("events/s for anchored-score fwd+bwd @1M events 640x480; % HBM/VALU roofline"
+                   if a.workload == "anchored" else
+                   f"events/s for anchored-score fwd+bwd @{ev.n} events 640x480 blobs; % VALU roofline"),
         "value": value, "unit": "events/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": 1e3 * dt / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"anchored score fwd+bwd, {ev.n} events, 640x480, dense flow 2x480x640, "
-                               f"h={a.sigma}, tau=0.2, cut=3, S=16, all anchors",
+        "config": {"workload": f"{desc}, h={a.sigma}, tau=0.2, cut=3, S=16, all anchors",
                    "events": ev.n, "sensor": [640, 480], "sigma": a.sigma, "tau": 0.2, "slices": 16,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "valu", "kernel": dom, "achieved": achieved / 1e12, "peak": VALU_PEAK / 1e12,

@@ -181,3 +181,34 @@ def test_fast_full_size_matches_reference_layout(h):
     gv_ref = N(e.ats_pair_bwd(gS, p.src_y, p.src_v, p.src_t, p.src_id, p.cell_start, p.anc_x, p.anc_t, p.anc_cell,
                               p.anc_id, p.slice_c, p.S, p.GH, p.GW, h, 0.2, 3.0, win.n))
     close_rel(N(plan.backward(gS)), gv_ref, 1e-4)
+
+
+def test_fast_blob_contention_matches_reference_layout():
+    """Contention stress shape: 4M events, 90% in 5 Gaussian blobs (sigma 8 px), Sim2 flow (0, 0, 0.1, 0.1),
+    h = 1, a random 40k-anchor subset: fused path against the reference-layout device plan and kernels
+    (counts bit-exact, sums within 1e-5, gradients within 1e-4)."""
+    print("blob contention, 4M events", flush=True)
+    win = synth.blob_window(seed=0)
+    rng = np.random.default_rng(0)
+    xs = (win.xy + rng.uniform(-0.5, 0.5, win.xy.shape)).astype(F32)
+    th = win.motion["theta"].astype(F32)
+    c = np.array([(640 - 1) / 2.0, (480 - 1) / 2.0], F32)
+    d = (xs - c).astype(F32)
+    v = np.stack([th[0] + (th[2] * d[:, 0] - th[3] * d[:, 1]), th[1] + (th[3] * d[:, 0] + th[2] * d[:, 1])],
+                 1).astype(F32)
+    anchors = np.sort(rng.choice(win.n, 40_000, replace=False))
+    xa = (xs[anchors] + rng.standard_normal((len(anchors), 2))).astype(F32)
+    tx, tt, tv, tb, ta, txa = T(xs), T(win.t), T(v), T(win.b), T(anchors), T(xa)
+    ref_plan = F.build_pair_plan(tx, tt, tv, tb, 1, 480, 640, ta, 1.0, 0.2, 3.0, 16, anchor_xy=txa)
+    want_cnt = N(F.pair_counts(ref_plan, 1.0, 0.2, 3.0))
+    assert want_cnt.mean() > 1000                       # dense neighbourhoods
+    e = F.get_ext()
+    p = ref_plan
+    args = (p.src_y, p.src_v, p.src_t, p.src_id, p.cell_start, p.anc_x, p.anc_t, p.anc_cell, p.anc_id, p.slice_c,
+            p.S, p.GH, p.GW, 1.0, 0.2, 3.0)
+    want = N(e.ats_pair_fwd(*args))
+    plan = F.FastPairPlan(tx, tt, tv, tb, 1, 480, 640, ta, 1.0, 0.2, 3.0, 16, txa)
+    assert np.array_equal(N(plan.counts()), want_cnt)
+    assert np.allclose(N(plan.forward()), want, rtol=1e-5, atol=1e-6 * float(np.abs(want).max()))
+    gS = torch.randn(len(anchors), device=DEV, generator=torch.Generator(device=DEV).manual_seed(5))
+    close_rel(N(plan.backward(gS)), N(e.ats_pair_bwd(gS, *args, win.n)), 1e-4)
