@@ -21,10 +21,11 @@ Other workloads (parity-test configurations, not the headline metric), same outp
 Two helpers for the rocprofv3 summaries under profiles/ (no GPU work beyond what they name):
 
     python bench.py --calibrate-copy MB        # a plain f32 copy of MB MiB (read MB, write MB), 5 times
-    python bench.py --summarize DIR... --out FILE --title T --command C [--copy-mb MB]
+    python bench.py --summarize DIR... --out FILE --title T --command C [--calibration DIR... --copy-mb MB]
         # kernel table from *_kernel_stats.csv and per-dispatch counter means from *_counter_collection.csv;
-        # with --copy-mb, FETCH_SIZE / WRITE_SIZE are scaled by what they read for the calibration copy, and
-        # the per-launch HBM bytes of every kernel are recorded for bench.py's roofline "traffic"
+        # with a calibration, FETCH_SIZE / WRITE_SIZE are scaled by what they read for the copy of MB MiB in
+        # the calibration runs, and the per-launch HBM bytes of every kernel are recorded for the roofline
+        # "traffic" of bench.py
 """
 from __future__ import annotations
 
@@ -68,6 +69,8 @@ def parse():
     ap.add_argument("--title", default="rocprofv3 summary")
     ap.add_argument("--command", default="")
     ap.add_argument("--copy-mb", type=float, default=0.0)
+    ap.add_argument("--calibration", nargs="*", default=[], metavar="DIR",
+                    help="counter runs of --calibrate-copy (FETCH_SIZE, WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -81,7 +84,17 @@ def _short(name):
     return n.split("(")[0]
 
 
-def summarize(dirs, out, title, command, copy_mb):
+def _counters(dirs):
+    agg = {}
+    for f in sorted(sum((glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True) for d in dirs),
+                        [])):
+        for r in csv.DictReader(open(f)):
+            agg.setdefault(_short(r["Kernel_Name"]), {}).setdefault(r["Counter_Name"], []).append(
+                float(r["Counter_Value"]))
+    return agg
+
+
+def summarize(dirs, out, title, command, copy_mb, cal_dirs=()):
     """Markdown summary of rocprofv3 csv output (kernel stats and counters), with the per-launch HBM traffic
     of every kernel when a calibration copy of copy_mb MiB is among the counter runs."""
     lines = [f"# {title}", "", "Command (repo root, on the MI355X):", "", f"    {command}", ""]
@@ -92,22 +105,16 @@ def summarize(dirs, out, title, command, copy_mb):
             lines.append(f"| {_short(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
                          f"{float(r['Percentage']):.1f}% |")
         lines.append("")
-    agg = {}
-    for f in sorted(sum((glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True) for d in dirs),
-                        [])):
-        for r in csv.DictReader(open(f)):
-            k = "calibration copy (torch.neg)" if "neg_kernel" in r["Kernel_Name"] else _short(r["Kernel_Name"])
-            agg.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    agg = _counters(dirs)
     traffic = {}
     if agg:
         scale = {}
-        if copy_mb > 0:
+        if copy_mb > 0 and cal_dirs:
             want_kib = copy_mb * 1024.0
-            for k, cs in agg.items():
-                if k.startswith("calibration copy"):
-                    for c in ("FETCH_SIZE", "WRITE_SIZE"):
-                        if c in cs:
-                            scale[c] = want_kib / (sum(cs[c]) / len(cs[c]))
+            for cs in _counters(cal_dirs).values():      # the calibration runs hold only the copy kernel
+                for c in ("FETCH_SIZE", "WRITE_SIZE"):
+                    if c in cs:
+                        scale[c] = want_kib / (sum(cs[c]) / len(cs[c]))
             lines += [f"Calibration: a plain copy of {copy_mb:g} MiB (torch.neg, f32) reads FETCH_SIZE = "
                       f"{want_kib / scale.get('FETCH_SIZE', float('nan')):.0f} and WRITE_SIZE = "
                       f"{want_kib / scale.get('WRITE_SIZE', float('nan')):.0f} (KiB per dispatch) for "
@@ -342,7 +349,7 @@ def iwe_main(a, dev):
 def main():
     a = parse()
     if a.summarize:
-        summarize(a.summarize, a.out, a.title, a.command, a.copy_mb)
+        summarize(a.summarize, a.out, a.title, a.command, a.copy_mb, a.calibration)
         return
     if a.calibrate_copy > 0:
         calibrate_copy(a.calibrate_copy)
