@@ -527,17 +527,64 @@ __device__ __forceinline__ void walk(const int* __restrict__ cstart, int base, i
   }
 }
 
+// The same walk with the rows of the neighbourhood flattened: the spans of up to kRowTab rows are fetched at
+// once into this lane's column of an LDS table (tab[r * kBlock]), then the lane steps through them without
+// waiting for the other lanes at row ends (a wave's lanes have rows of different lengths; stepping row by row
+// in lockstep leaves most lanes idle).  Taller neighbourhoods take the row-by-row walk.
+constexpr int kRowTab = 8;
+
+template <typename Visit>
+__device__ __forceinline__ void walk_flat(const int* __restrict__ cstart, int base, int plane, float qx, float qy,
+                                          float R, float R2, const FGeo& G, int2* tab, Visit&& visit) {
+  const int rlo = cell_walk(qy - R, G.gy0, G.gy1, G.icf, G.GH), rhi = cell_walk(qy + R, G.gy0, G.gy1, G.icf, G.GH);
+  const int nrows = rhi - rlo + 1;
+  if (nrows > kRowTab) {
+    walk(cstart, base, plane, qx, qy, R, R2, G, visit);
+    return;
+  }
+  int kk[kRowTab], ee[kRowTab];
+#pragma unroll
+  for (int i = 0; i < kRowTab; ++i) {              // all span loads in flight together
+    kk[i] = base;
+    ee[i] = base;
+    int c0, c1;
+    if (i < nrows && row_span(rlo + i, qx, qy, R, R2, G, c0, c1)) {
+      const int rowk = plane + (rlo + i) * G.GW;
+      kk[i] = cstart[rowk + c0];
+      ee[i] = cstart[rowk + c1 + 1];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kRowTab; ++i) tab[i * kBlock] = make_int2(kk[i] - base, ee[i] - base);
+  int ri = 0;                                      // row of cur; nxt holds row ri + 1 (read one row ahead)
+  int2 cur = make_int2(kk[0] - base, ee[0] - base);
+  int2 nxt = make_int2(kk[1] - base, ee[1] - base);
+  while (true) {
+    if (cur.x >= cur.y) {
+      do {
+        cur = nxt;
+        ++ri;
+        nxt = ri + 1 < nrows ? tab[(ri + 1) * kBlock] : make_int2(0, 0);
+      } while (cur.x >= cur.y && ri < nrows - 1);
+      if (cur.x >= cur.y) break;
+    }
+    visit(cur.x, cur.y);
+    cur.x += kUnroll;
+  }
+}
+
 // Group walk: the candidates of the cells of plane `plane` that meet the R-neighbourhood of the box
-// [x0, x1] x [y0, y1], 64 per chunk: chunk(pos) with pos the lane's candidate index (-1 if idle).  Row
+// [x0, x1] x [y0, y1], 64 per chunk: use(load(pos), pos) with pos the lane's candidate index (-1 if idle).  Row
 // spans are fetched one row per lane and prefix-summed across the wave.  All arguments wave-uniform.
 // Up to kRowTable rows (the usual case: R / cf < 3) the row starts and offsets are read into scalars once
 // and every chunk maps its lanes with one compare and select per row; taller neighbourhoods take the
 // general loop.
 constexpr int kRowTable = 8;
 
-template <typename Chunk>
+template <typename Load, typename Use>
 __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int base, int plane, float x0, float x1,
-                                           float y0, float y1, float R, float R2, const FGeo& G, Chunk&& chunk) {
+                                           float y0, float y1, float R, float R2, const FGeo& G, Load&& load,
+                                           Use&& use) {
   const int lane = threadIdx.x & (kWave - 1);
   const int rlo = uni(cell_walk(y0 - R, G.gy0, G.gy1, G.icf, G.GH));
   const int rhi = uni(cell_walk(y1 + R, G.gy0, G.gy1, G.icf, G.GH));
@@ -556,10 +603,10 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
         len = cstart[rowk + c1 + 1] - base - s0;
       }
     }
+    const int nrb = min(kWave, rhi - rb + 1);   // rows of this batch
     const int incl = wave_incl_scan(len);
     const int excl = incl - len;
     const int total = rdlane(incl, kWave - 1);
-    const int nrb = min(kWave, rhi - rb + 1);   // rows of this batch
     if (nrb <= kRowTable) {
       // lanes >= nrb hold len 0 and excl = total, so their entries never match a valid index
       int ex[kRowTable], of[kRowTable];
@@ -568,12 +615,21 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
         ex[k] = rdlane(excl, k);
         of[k] = rdlane(s0 - excl, k);
       }
-      for (int c0 = 0; c0 < total; c0 += kWave) {
+      auto map = [&](int c0) {
         const int idx = c0 + lane;
         int off = of[0];
 #pragma unroll
         for (int k = 1; k < kRowTable; ++k) off = idx >= ex[k] ? of[k] : off;   // last row starting <= idx
-        chunk(idx < total ? idx + off : -1);
+        return idx < total ? idx + off : -1;
+      };
+      int pos = map(0);
+      auto cur = load(pos);
+      for (int c0 = 0; c0 < total; c0 += kWave) {  // the next chunk's candidates load while this one computes
+        const int pn = map(c0 + kWave);
+        auto nxt = load(pn);
+        use(cur, pos);
+        cur = nxt;
+        pos = pn;
       }
       continue;
     }
@@ -590,7 +646,7 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
         if (ej + lj > c0 + kWave) break;        // row continues into the next chunk
         ++j;
       }
-      chunk(pos);
+      use(load(pos), pos);
     }
   }
 }
@@ -615,10 +671,17 @@ __device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plan
     acc[a] = 0.f;
     cnt[a] = 0;
   }
-  group_walk(p.start, 0, plane, x0, x1, y0, y0 + G.cf, R, R2, G, [&](int pos) {
+  struct Cand {
+    float4 e;
+    float t;
+  };
+  auto load = [&](int pos) {
     const uint32_t k = (uint32_t)max(pos, 0);
-    const float4 e = ld(p.epos, k);
-    const float ts = ld(p.etim, k);
+    return Cand{ld(p.epos, k), ld(p.etim, k)};
+  };
+  group_walk(p.start, 0, plane, x0, x1, y0, y0 + G.cf, R, R2, G, load, [&](const Cand& c, int pos) {
+    const float4 e = c.e;
+    const float ts = c.t;
 #pragma unroll
     for (int a = 0; a < WD; ++a) {
       float dt, rx, ry, d2;
@@ -721,7 +784,7 @@ __global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int 
 // compares event ids instead, as the reference does.
 template <bool DUP>
 __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, float R, float R2, float4 sr, int sid,
-                                             float tj, int key, int sp) {
+                                             float tj, int key, int sp, int2* tab) {
   const int plane_cells = G.GH * G.GW;
   const int* astart = p.start + G.ncell_pad;
   const int E = uni(p.start[G.ncell_pad]);
@@ -737,7 +800,7 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
     sv.w = sr.w;
     const float cs = slice_centre(s, G.delta);
     const float qx = clampf(sv.x, G.gx0, G.gx1), qy = clampf(sv.y, G.gy0, G.gy1);
-    walk(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, [&](int k, int e) {
+    walk_flat(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, tab, [&](int k, int e) {
       float4 A[kUnroll];
       int id[kUnroll];
 #pragma unroll
@@ -768,6 +831,7 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
 // range within R of its slice-centre position, gS_i * k * dt / h^2 * r (csrc/atl_cpu.cpp:240-248);
 // gv[j] += the total (each source once: no atomics).
 __global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, float2* __restrict__ gv) {
+  __shared__ int2 tab[kRowTab * kBlock];           // per-lane row spans of the current slice (column threadIdx.x)
   const int lb = xcd_block((N + kBlock - 1) / kBlock);
   if (lb < 0) return;
   const int lane = threadIdx.x & (kWave - 1);
@@ -785,8 +849,9 @@ __global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, flo
   const int4 si = SR.i;
   const float tj = __int_as_float(si.x);
   const int sp = p.self[si.y];
-  const float2 m = uni(p.P->dup) ? bwd_source<true>(p, G, R, R2, SR.f, si.y, tj, si.z, sp)
-                                 : bwd_source<false>(p, G, R, R2, SR.f, si.y, tj, si.z, sp);
+  int2* mytab = tab + threadIdx.x;
+  const float2 m = uni(p.P->dup) ? bwd_source<true>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, mytab)
+                                 : bwd_source<false>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, mytab);
   float2 o = gv[si.y];
   o.x += m.x;
   o.y += m.y;
