@@ -17,6 +17,9 @@ Other workloads (parity-test configurations, not the headline metric), same outp
     python bench.py --workload iwe-plumbing    # the same on 100k events 240x180, constant flow (2, -1.25)
     python bench.py --workload anchored-blobs  # contention stress: the anchored score on 4M events, 90% in 5
                                                # Gaussian blobs (sigma 8 px), Sim2 flow (0, 0, 0.1, 0.1)
+    python bench.py --workload trajectories    # 4 windows x 500k events 640x480, degree-10 Bezier pixel
+                                               # trajectories, sliced anchored score (10 slices, sigma 1,
+                                               # tau 0.8), grad to the coefficient grid
 
 Two helpers for the rocprofv3 summaries under profiles/ (no GPU work beyond what they name):
 
@@ -56,7 +59,8 @@ COUNTERS = ROOT / "profiles" / "anchored_score_1M_640x480_counters.md"
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", default="anchored", choices=["anchored", "anchored-blobs", "iwe", "iwe-plumbing"])
+    ap.add_argument("--workload", default="anchored",
+                    choices=["anchored", "anchored-blobs", "iwe", "iwe-plumbing", "trajectories"])
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--sigma", type=float, default=1.0)
@@ -346,6 +350,96 @@ def iwe_main(a, dev):
     print(json.dumps(line), flush=True)
 
 
+# ----------------------------------------------------------------------------------- trajectories workload
+TRAJ_BYTES = {     # algorithmic bytes per entry point: per event, plus the field / image once (C channels)
+    "atl_sample_grid_fwd": lambda n, c, f, hw: (16 + 4 * c) * n + 4 * c * f,
+    "atl_sample_grid_bwd_planned": lambda n, c, f, hw: (16 + 4 * c) * n + 8 * c * f,
+    "atl_sample_grid_bwd_pos": lambda n, c, f, hw: (24 + 4 * c) * n + 4 * c * f,
+    "atl_splat_gauss_fwd": lambda n, c, f, hw: 20 * n + 4 * hw,
+    "atl_splat_gauss_bwd": lambda n, c, f, hw: 32 * n + 4 * hw,
+    "atl_gather_bilinear_fwd": lambda n, c, f, hw: 20 * n + 4 * hw,
+    "atl_gather_bilinear_bwd_ws": lambda n, c, f, hw: 28 * n + 8 * hw,
+}
+
+
+def trajectories_main(a, dev):
+    from x_amd import synth
+    from x_amd.core import EventPacket
+    from x_amd.motion import PixelTrajectories
+    from x_amd.objectives import AnchoredSliced
+    from x_amd.ops import _ext
+    win = synth.trajectory_windows(seed=0)
+    K = win.motion["K"]
+    ev = EventPacket.from_window(win, dev)
+    coeff = torch.tensor(win.motion["coeffs"], device=dev, requires_grad=True)
+    obj = AnchoredSliced(n_slices=10, sigma=1.0, tau=0.8, seed=0, rng="device")
+
+    def step():
+        coeff.grad = None
+        out = obj(ev, PixelTrajectories(coeff, K, "bezier"))
+        out["loss"].backward()
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    kernels = list(TRAJ_BYTES)
+    rec = _ext.time_kernels(kernels)
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1 in rec[k]])) for k in kernels if rec[k]}
+    calls = {k: len(rec[k]) / a.steps for k in kernels if rec[k]}
+    _ext.time_kernels(())
+    tot = {k: ms[k] * calls[k] for k in ms}
+    dom = max(tot, key=lambda k: tot[k])
+    # events per launch of the dominant entry point: sources of one slice (all within tau + delta/2) or anchors
+    n_launch = ev.n
+    gbs = TRAJ_BYTES[dom](n_launch, 2 * K, (win.height // 4) * (win.width // 4) * ev.batch_size,
+                          win.height * win.width * ev.batch_size) / (ms[dom] * 1e-3) / 1e9
+    line = {
+        "metric": f"events/s for sliced anchored score fwd+bwd @{ev.n} events ({ev.batch_size} windows) 640x480, "
+                  f"degree-{K} pixel trajectories; % HBM roofline",
+        "value": ev.n * a.steps / dt, "unit": "events/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": 1e3 * dt / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"AnchoredSliced(n_slices=10, sigma=1, tau=0.8) on {ev.batch_size} windows x "
+                               f"{ev.n // ev.batch_size} events, 640x480, PixelTrajectories(K={K}, bezier, tile 4, "
+                               f"6 fixed-point steps), grad to the (4, {2 * K}, 480, 640) coefficient grid",
+                   "events": ev.n, "windows": ev.batch_size, "sensor": [640, 480], "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": gbs, "peak": 8000.0, "unit": "GB/s",
+                     "frac": gbs / 8000.0, "traffic": recorded_traffic(dom), "kernel_ms": ms[dom],
+                     "events_per_launch": n_launch},
+        "kernel_ms": ms, "kernel_calls_per_step": calls, "kernel_ms_per_step": tot,
+    }
+    if not a.no_cpu:
+        line["cpu_baseline"] = trajectories_cpu_baseline(win, a.cpu_budget)
+    print(json.dumps(line), flush=True)
+
+
+def trajectories_cpu_baseline(win, budget):
+    """The same objective on the host's cores (PyTorch CPU ops: the package's CPU path) on a prefix of the
+    first window; forward + backward."""
+    from x_amd.core import EventPacket
+    from x_amd.motion import PixelTrajectories
+    from x_amd.objectives import AnchoredSliced
+    K = win.motion["K"]
+    coeff = torch.tensor(win.motion["coeffs"][:1], requires_grad=True)
+
+    def run(n):
+        sub = type(win)(xy=win.xy[:n], t=win.t[:n], p=win.p[:n], b=win.b[:n], height=win.height, width=win.width)
+        ev = EventPacket.from_window(sub, "cpu")
+        obj = AnchoredSliced(n_slices=10, sigma=1.0, tau=0.8, seed=0)
+        coeff.grad = None
+        obj(ev, PixelTrajectories(coeff, K, "bezier"))["loss"].backward()
+
+    n, dt, _ = _bounded_run(run, int((win.b == 0).sum()), budget)
+    return {"value": n / dt, "unit": "events/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"the same objective with PyTorch CPU ops on the first {n} events of window 0 (time-sorted "
+                      f"prefix, the largest of a doubling series that fits the budget), {dt:.2f} s"}
+
+
 def main():
     a = parse()
     if a.summarize:
@@ -358,10 +452,10 @@ def main():
         print(f"bench.py measures one GPU only (asked for {a.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
         sys.exit(2)
-    if a.workload.startswith("iwe"):
+    if a.workload.startswith("iwe") or a.workload == "trajectories":
         dev = torch.device("cuda:0")
         torch.cuda.set_device(dev)
-        iwe_main(a, dev)
+        (iwe_main if a.workload.startswith("iwe") else trajectories_main)(a, dev)
         return
     from x_amd.objectives import AnchoredExact
     from x_amd.ops import _ext

@@ -74,11 +74,16 @@ int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int
                         const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gfield,
                         hipStream_t stream);
 
+/* Gradient of atl_sample_grid_fwd w.r.t. the positions (the autograd of parametric.py:235-251 through its
+ * weights; zero where the border clamp is active): gpos (N,2) written. */
+int atl_sample_grid_bwd_pos(const float* gout, const float* field, int64_t B, int64_t C, int64_t Hg, int64_t Wg,
+                            const float* pos, const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gpos,
+                            hipStream_t stream);
 /* The same adjoint through a tile plan: atl_grid_plan bins the positions by the 16x16 tile of their base
  * grid node into a workspace of atl_grid_plan_bytes(B, Hg, Wg, N) bytes (-1 if the sizes are unsupported);
  * atl_sample_grid_bwd_planned then accumulates gout tile by tile in LDS and adds each touched node once.
- * gfield accumulated; C <= 4.  The positions and img_h, img_w must be the ones the plan was built from
- * (the plan keeps its own copy of the positions; `pos` is not read). */
+ * gfield accumulated; C <= 32 (C > 4 only where 16x16 tiles fit the binning).  The positions and img_h, img_w
+ * must be the ones the plan was built from (the plan keeps its own copy of the positions; `pos` is not read). */
 int64_t atl_grid_plan_bytes(int64_t B, int64_t Hg, int64_t Wg, int64_t N);
 int atl_grid_plan(int64_t B, int64_t Hg, int64_t Wg, const float* pos, const int64_t* b, int64_t N, int64_t img_h,
                   int64_t img_w, void* ws, int64_t ws_bytes, hipStream_t stream);

@@ -1,0 +1,119 @@
+"""Pixel trajectories and the sliced anchored score on the HIP path (the continuous-time workload).
+
+The trajectory model and the sliced score are host compositions (torch) of the HIP flow sampler (forward,
+field adjoint through the tile plan, position gradient), the Gaussian splat and the bilinear gather.  They run
+here on the device against the same composition on CPU tensors, where every op is plain PyTorch
+(x_amd/ops/reference.py); the kernels themselves are pinned to the oracle in test_gpu_ops.py.  Bars: values
+within 1e-5 relative, gradients within 1e-4 relative to the largest magnitude."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from x_amd import synth
+from x_amd.core import EventPacket
+from x_amd.motion import PixelTrajectories, sample_grid
+from x_amd.objectives import AnchoredSliced
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+F32 = np.float32
+
+
+def N(t):
+    return t.detach().cpu().numpy()
+
+
+def close_rel(got, want, rel):
+    scale = max(float(np.abs(want).max()), 1e-30)
+    err = float(np.abs(got.astype(np.float64) - want.astype(np.float64)).max())
+    assert err <= rel * scale, f"max err {err:.3e} vs scale {scale:.3e} (rel {err / scale:.2e})"
+
+
+@pytest.mark.parametrize("C,scale", [(2, False), (3, True), (20, False)])
+def test_sample_grid_position_and_field_gradients(C, scale):
+    """Flow sampler forward bit-exact vs the oracle; gradients w.r.t. the field (tile plan, C up to 32) and the
+    positions (zero where the border clamp is active) vs torch autograd of the same lookup on the CPU."""
+    print(f"sample_grid grads C={C} scale={scale}", flush=True)
+    rng = np.random.default_rng(C)
+    B, Hg, Wg, n = 2, 30, 40, 20000
+    H, W = (120, 160) if scale else (Hg, Wg)
+    pos = np.stack([rng.uniform(-3, W + 2, n), rng.uniform(-3, H + 2, n)], 1).astype(F32)
+    pos[:50] = np.round(pos[:50])                                       # integer corners
+    b = rng.integers(0, B, n).astype(np.int64)
+    fld = rng.standard_normal((B, C, Hg, Wg)).astype(F32)
+    g = rng.standard_normal((n, C)).astype(F32)
+    res = {}
+    for dev in ("cpu", DEV):
+        tf = torch.tensor(fld, device=dev, requires_grad=True)
+        tp = torch.tensor(pos, device=dev, requires_grad=True)
+        tb = torch.tensor(b, device=dev)
+        if scale:
+            gp = torch.stack([tp[:, 0] / max(W - 1, 1) * (Wg - 1), tp[:, 1] / max(H - 1, 1) * (Hg - 1)], 1)
+            out = sample_grid(tf, gp, tb) if dev == "cpu" else __import__("x_amd").ops.sample_grid_hip(
+                tf, tp, tb, img_hw=(H, W))
+        else:
+            out = sample_grid(tf, tp, tb)
+        (out * torch.tensor(g, device=dev)).sum().backward()
+        res[dev] = (N(out), N(tf.grad), N(tp.grad))
+    if not scale:
+        assert np.array_equal(res[DEV][0], O.sample_grid(fld, pos, b)[0])
+    close_rel(res[DEV][0], res["cpu"][0], 1e-5)
+    close_rel(res[DEV][1], res["cpu"][1], 1e-4)
+    close_rel(res[DEV][2], res["cpu"][2], 1e-4)
+
+
+@pytest.mark.parametrize("K,kind", [(1, "polynomial"), (3, "bezier"), (4, "polynomial")])
+def test_pixel_trajectories_device_matches_cpu(K, kind):
+    """Transport (fixed-point origin + displacement) values and coefficient gradients, device vs CPU."""
+    print(f"trajectories K={K} {kind}", flush=True)
+    win = synth.small_window(seed=K, n=3000, B=2)
+    rng = np.random.default_rng(K)
+    coeffs = synth.trajectory_coeffs(rng, 2, K, win.height, win.width, sigma_px=8.0, dmax=3.0)
+    w = rng.standard_normal((win.n, 2)).astype(F32)
+    res = {}
+    for dev in ("cpu", DEV):
+        ev = EventPacket.from_window(win, dev)
+        c = torch.tensor(coeffs, device=dev, requires_grad=True)
+        m = PixelTrajectories(c, K, kind)
+        y = m.transport(ev.xy, ev.t, 0.7, ev.b)
+        (y * torch.tensor(w, device=dev)).sum().backward()
+        res[dev] = (N(y), N(c.grad))
+    close_rel(res[DEV][0], res["cpu"][0], 1e-5)
+    close_rel(res[DEV][1], res["cpu"][1], 1e-4)
+
+
+def test_pixel_trajectories_linear_closed_form():
+    """Degree-1 polynomial trajectories with a constant coefficient field are the linear warp:
+    transport(x, t, t') = x + c (t' - t), velocity = c."""
+    win = synth.small_window(seed=3, n=2000, B=1)
+    ev = EventPacket.from_window(win, DEV)
+    c = torch.zeros(1, 2, win.height, win.width, device=DEV)
+    c[:, 0] = 1.5                                          # y coefficient
+    c[:, 1] = -2.25                                        # x coefficient
+    m = PixelTrajectories(c, 1)
+    y = N(m.transport(ev.xy, ev.t, 0.25, ev.b))
+    want = win.xy + np.array([-2.25, 1.5], F32) * (F32(0.25) - win.t)[:, None]
+    assert np.allclose(y, want, atol=1e-5)
+    assert np.allclose(N(m.velocity(ev.xy, ev.t, ev.b)), np.array([[-2.25, 1.5]], F32))
+
+
+@pytest.mark.parametrize("smooth", [True, False])
+def test_anchored_sliced_device_matches_cpu(smooth):
+    """The sliced anchored score (Gaussian splats, gathers, finite-difference log-det, leave-one-out terms,
+    exposure correction) on degree-3 Bezier trajectories: loss and coefficient gradient, device vs CPU, with the
+    same CPU-generated noise."""
+    print(f"anchored sliced smooth={smooth}", flush=True)
+    win = synth.small_window(seed=9, n=4000, B=2)
+    rng = np.random.default_rng(9)
+    coeffs = synth.trajectory_coeffs(rng, 2, 3, win.height, win.width, sigma_px=8.0, dmax=3.0)
+    res = {}
+    for dev in ("cpu", DEV):
+        ev = EventPacket.from_window(win, dev)
+        c = torch.tensor(coeffs, device=dev, requires_grad=True)
+        obj = AnchoredSliced(n_slices=6, sigma=1.0, tau=0.3, seed=0, smooth_anchors=smooth)
+        out = obj(ev, PixelTrajectories(c, 3, "bezier"))
+        out["loss"].backward()
+        res[dev] = (float(out["loss"]), N(c.grad))
+    assert abs(res[DEV][0] - res["cpu"][0]) <= 1e-5 * abs(res["cpu"][0])
+    close_rel(res[DEV][1], res["cpu"][1], 1e-4)

@@ -234,6 +234,7 @@ __global__ void __launch_bounds__(kBlock) k_voxel_grid(const float2* __restrict_
 struct GridCorners {
   int o00, o01, o10, o11;      // offsets inside one (Hg, Wg) plane
   float w00, w01, w10, w11;
+  float ax, ay;                // gx - x0, gy - y0
 };
 
 __device__ __forceinline__ GridCorners grid_corners(float x, float y, int Hg, int Wg, float sxw, float syh,
@@ -261,6 +262,8 @@ __device__ __forceinline__ GridCorners grid_corners(float x, float y, int Hg, in
   c.w01 = ax * (1.f - ay);
   c.w10 = (1.f - ax) * ay;
   c.w11 = ax * ay;
+  c.ax = ax;
+  c.ay = ay;
   return c;
 }
 
@@ -311,6 +314,47 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd(const float* __restr
     atomicAdd(fc + g.o10, go * g.w10);
     atomicAdd(fc + g.o11, go * g.w11);
   }
+}
+
+// Position gradient of the flow lookup (autograd of atl/motion/parametric.py:235-251 w.r.t. the positions):
+// d out / d gx = sum over corners of field * d w / d gx with ax = gx - x0 (x0 a constant), zero where the
+// border clamp is active (torch.clamp passes the gradient for min <= gx <= max), times (Wg - 1) / sx for
+// image-pixel positions.  gpos (N, 2) written.
+__global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos(const float* __restrict__ gout,
+                                                                const float* __restrict__ field, int64_t B, int C,
+                                                                int Hg, int Wg, const float2* __restrict__ pos,
+                                                                const int64_t* __restrict__ bidx, int64_t N,
+                                                                float sxw, float syh, int scale,
+                                                                float2* __restrict__ gpos) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  const float2 p = pos[n];
+  float sx = 0.f, sy = 0.f;
+  if (batch_ok(b, B)) {
+    float gx = p.x, gy = p.y, kx = 1.f, ky = 1.f;
+    if (scale) {
+      gx = p.x / sxw * (float)(Wg - 1);
+      gy = p.y / syh * (float)(Hg - 1);
+      kx = (float)(Wg - 1) / sxw;
+      ky = (float)(Hg - 1) / syh;
+    }
+    const bool inx = gx >= 0.f && gx <= (float)(Wg - 1), iny = gy >= 0.f && gy <= (float)(Hg - 1);
+    const GridCorners c = grid_corners(p.x, p.y, Hg, Wg, sxw, syh, scale != 0);
+    const float ax = c.ax, ay = c.ay;
+    const int64_t plane = (int64_t)Hg * Wg;
+    const float* f = field + b * C * plane;
+    for (int ch = 0; ch < C; ++ch) {
+      const float* fc = f + ch * plane;
+      const float f00 = fc[c.o00], f01 = fc[c.o01], f10 = fc[c.o10], f11 = fc[c.o11];
+      const float go = gout[n * C + ch];
+      sx += go * ((1.f - ay) * (f01 - f00) + ay * (f11 - f10));
+      sy += go * ((1.f - ax) * (f10 - f00) + ax * (f11 - f01));
+    }
+    sx = inx ? sx * kx : 0.f;
+    sy = iny ? sy * ky : 0.f;
+  }
+  gpos[n] = make_float2(sx, sy);
 }
 
 bool dims_ok(int64_t H, int64_t W) { return H > 0 && W > 0 && H * W < (int64_t)1 << 31; }
@@ -396,6 +440,18 @@ int atl_sample_grid_fwd(const float* field, int64_t B, int64_t C, int64_t Hg, in
   hipLaunchKernelGGL(k_sample_grid_fwd, dim3(grid_for(N)), dim3(kBlock), 0, stream, field, B, (int)C, (int)Hg,
                      (int)Wg, (const float2*)pos, b, N, sxw, syh, scale, out);
   return check_launch("sample_grid_fwd");
+}
+
+int atl_sample_grid_bwd_pos(const float* gout, const float* field, int64_t B, int64_t C, int64_t Hg, int64_t Wg,
+                            const float* pos, const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gpos,
+                            hipStream_t stream) {
+  if (N < 0 || B < 0 || C < 1 || Hg < 1 || Wg < 1 || !dims_ok(Hg, Wg)) { set_error("sample_grid_bwd_pos: bad sizes"); return 1; }
+  if (N == 0) return 0;
+  const int scale = img_h > 0 && img_w > 0;
+  const float sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1), syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
+  hipLaunchKernelGGL(k_sample_grid_bwd_pos, dim3(grid_for(N)), dim3(kBlock), 0, stream, gout, field, B, (int)C,
+                     (int)Hg, (int)Wg, (const float2*)pos, b, N, sxw, syh, scale, (float2*)gpos);
+  return check_launch("sample_grid_bwd_pos");
 }
 
 int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,

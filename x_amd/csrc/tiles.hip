@@ -28,6 +28,7 @@ constexpr int kTilePerBlock = 4096;              // binning: events per block
 constexpr int kTileBinBlock = 512;               // binning: threads per block (8 events each)
 constexpr int kTileMaxKeys = 16384;              // LDS histogram capacity (tiles over all batches)
 constexpr int kAccBlock = 256;                   // accumulation: threads per tile
+constexpr int kMaxChannels = 32;                 // field channels of the tile adjoint (LDS: C x 17 x 17 floats)
 
 enum { kImage = 0, kGrid = 1 };
 
@@ -37,6 +38,7 @@ struct TileGeo {
   int TX, TY, nkeys;         // tiles per row and column, B * TY * TX
   int N, nblk;
   int mode;
+  int C;                     // kGrid: channels of the field
   int scale;                 // kGrid: positions are image pixels mapped by sxw, syh
   float sxw, syh;
 };
@@ -151,6 +153,7 @@ constexpr int kAccRange = kAccBlock * kAccItems;
 template <int MODE, int C, int T>
 __device__ __forceinline__ void accum_record(const float4& q, const float* __restrict__ gout, const TileGeo& g,
                                              int ox, int oy, float* acc) {
+  const int nc = C > 0 ? C : g.C;                  // C = 0: the field's channel count at run time
   constexpr int L = T + 1;
   if (MODE == kImage) {
     int x0, y0;
@@ -183,8 +186,9 @@ __device__ __forceinline__ void accum_record(const float4& q, const float* __res
       return;                                                // never taken: the binning chose this tile
     const int i00 = ly0 * L + lx0, i01 = ly0 * L + lx1, i10 = ly1 * L + lx0, i11 = ly1 * L + lx1;
 #pragma unroll
-    for (int ch = 0; ch < C; ++ch) {
-      const float go = gout[(int64_t)j * C + ch];
+    for (int ch = 0; ch < (C > 0 ? C : kMaxChannels); ++ch) {
+      if (C == 0 && ch >= nc) break;
+      const float go = gout[(int64_t)j * nc + ch];
       float* a = acc + ch * L * L;
       atomicAdd(a + i00, go * w00);
       atomicAdd(a + i01, go * w01);
@@ -200,7 +204,8 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict_
                                                           const float* __restrict__ gout, TileGeo g,
                                                           float* __restrict__ out) {
   constexpr int L = T + 1;
-  __shared__ float acc[C * L * L];
+  extern __shared__ float acc[];                  // nc * L * L floats
+  const int nc = C > 0 ? C : g.C;
   __shared__ int ts[kAccBlock + 1];                       // starts of the tiles first .. first + kAccBlock
   __shared__ int found, found2;
   const int total = boff[g.nkeys * g.nblk];
@@ -240,7 +245,7 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict_
         break;
       }
       if (s0 >= s1) continue;                             // empty tile
-      for (int a = threadIdx.x; a < C * L * L; a += kAccBlock) acc[a] = 0.f;
+      for (int a = threadIdx.x; a < nc * L * L; a += kAccBlock) acc[a] = 0.f;
       __syncthreads();
       const int b = key / plane, r = key - b * plane;
       const int ty = r / g.TX, tx = r - ty * g.TX;
@@ -259,10 +264,9 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict_
       for (int a = threadIdx.x; a < L * L; a += kAccBlock) {
         const int py = oy + a / L, px = ox + a % L;
         if (py < 0 || py >= g.H || px < 0 || px >= g.W) continue;
-#pragma unroll
-        for (int ch = 0; ch < C; ++ch) {
+        for (int ch = 0; ch < nc; ++ch) {
           const float v = acc[ch * L * L + a];
-          if (v != 0.f) atomicAdd(out + ((int64_t)b * C + ch) * pl + (int64_t)py * g.W + px, v);
+          if (v != 0.f) atomicAdd(out + ((int64_t)b * nc + ch) * pl + (int64_t)py * g.W + px, v);
         }
       }
       __syncthreads();
@@ -323,6 +327,7 @@ bool tile_geo(int mode, int64_t B, int64_t H, int64_t W, int64_t N, int64_t img_
       g.N = (int)N;
       g.nblk = (int)((N + kTilePerBlock - 1) / kTilePerBlock);
       g.mode = mode;
+      g.C = 1;
       g.scale = img_h > 0 && img_w > 0;
       g.sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1);
       g.syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
@@ -374,11 +379,12 @@ void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const flo
   if (g.nblk == 0) return;
   const char* w = (const char*)ws;
   const unsigned grid = (unsigned)((g.N + kAccRange - 1) / kAccRange);   // records <= N
+  const int nc = C > 0 ? C : g.C;
   if (g.T == 16)
-    hipLaunchKernelGGL((k_tile_accum<MODE, C, 16>), dim3(grid), dim3(kAccBlock), 0, stream,
+    hipLaunchKernelGGL((k_tile_accum<MODE, C, 16>), dim3(grid), dim3(kAccBlock), (size_t)nc * 17 * 17 * 4, stream,
                        (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, out);
   else
-    hipLaunchKernelGGL((k_tile_accum<MODE, C, 32>), dim3(grid), dim3(kAccBlock), 0, stream,
+    hipLaunchKernelGGL((k_tile_accum<MODE, C, 32>), dim3(grid), dim3(kAccBlock), (size_t)nc * 33 * 33 * 4, stream,
                        (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, out);
 }
 
@@ -445,7 +451,8 @@ int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t
                                 int64_t N, int64_t img_h, int64_t img_w, const void* ws, float* gfield,
                                 hipStream_t stream) {
   TileGeo g;
-  if (!tile_geo(kGrid, B, Hg, Wg, N, img_h, img_w, g) || C < 1 || C > 4) { set_error("sample_grid_bwd_planned: bad sizes (C <= 4)"); return 1; }
+  if (!tile_geo(kGrid, B, Hg, Wg, N, img_h, img_w, g) || C < 1 || C > kMaxChannels || (C > 4 && g.T != 16)) { set_error("sample_grid_bwd_planned: bad sizes (C <= 4, or C <= 32 on grids of at most 16384 16x16 tiles)"); return 1; }
+  g.C = (int)C;
   if (!ws || !gfield || (N > 0 && !gout)) { set_error("sample_grid_bwd_planned: null argument"); return 1; }
   (void)pos;                                     // the plan's records carry the positions
   const TileLayout L = tile_layout(g);
@@ -453,7 +460,8 @@ int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t
     case 1: tile_accum<kGrid, 1>(g, L, ws, gout, gfield, stream); break;
     case 2: tile_accum<kGrid, 2>(g, L, ws, gout, gfield, stream); break;
     case 3: tile_accum<kGrid, 3>(g, L, ws, gout, gfield, stream); break;
-    default: tile_accum<kGrid, 4>(g, L, ws, gout, gfield, stream); break;
+    case 4: tile_accum<kGrid, 4>(g, L, ws, gout, gfield, stream); break;
+    default: tile_accum<kGrid, 0>(g, L, ws, gout, gfield, stream); break;
   }
   return check_launch("sample_grid_bwd_planned");
 }

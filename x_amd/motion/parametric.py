@@ -92,7 +92,7 @@ class DenseLinearFlow(VectorFieldMotion):
 
     def field(self, xy, b):
         Hg, Wg = self.grid.shape[-2:]
-        if xy.is_cuda and not xy.requires_grad:
+        if xy.is_cuda:
             return sample_grid_hip(self.grid, xy, b, img_hw=(self.H, self.W))
         gx = xy[:, 0] / max(self.W - 1, 1) * (Wg - 1)
         gy = xy[:, 1] / max(self.H - 1, 1) * (Hg - 1)
@@ -101,8 +101,8 @@ class DenseLinearFlow(VectorFieldMotion):
 
 def sample_grid(field: torch.Tensor, gpos: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """Bilinear, border-clamped sample of a (B, C, Hg, Wg) field at grid coordinates (N, 2), returns (N, C)
-    (atl/motion/parametric.py:235-251).  Device tensors with data positions use the HIP sampler."""
-    if gpos.is_cuda and not gpos.requires_grad:
+    (atl/motion/parametric.py:235-251).  Device tensors use the HIP sampler."""
+    if gpos.is_cuda:
         return sample_grid_hip(field, gpos, b)
     B, C, Hg, Wg = field.shape
     gx = gpos[:, 0].clamp(0, Wg - 1)

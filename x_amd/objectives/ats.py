@@ -1,4 +1,4 @@
-"""Anchored transport score (atl/objectives/ats.py:1-105).
+"""Anchored transport score (atl/objectives/ats.py:1-200).
 
     S(theta) = mean_i log(eps + rho_{-i}(x_i)),
     rho_{-i}(x) = (1 / W_i) sum_{j != i, |t_i - t_j| <= tau} K_h(x - (x_j + v_j (t_i - t_j)))
@@ -7,6 +7,11 @@ Every raw event (anchor) is scored by the Gaussian density of all other events t
 timestamp, with leave-one-out, dequantisation jitter of the sources, smoothed anchors and an exposure
 correction.  On device the whole chain runs on HIP kernels: flow lookup, pair sums, window counts,
 visible fraction and the log-score epilogue.
+
+* :class:`AnchoredExact`: exact pair sums, for motion that is linear at the event.
+* :class:`AnchoredSliced`: any motion (e.g. pixel trajectories).  The anchors of time slice s are scored
+  against a Gaussian splat of all sources transported to the slice centre c_s, at the anchors moved from their
+  own time to c_s, plus the exact log|det| of that small step.
 """
 from __future__ import annotations
 
@@ -16,7 +21,7 @@ from typing import Optional
 import torch
 
 from ..core.events import EventPacket
-from ..ops import anchored_log_scores, ats_pair_sums, visible_fraction_linear, window_counts
+from ..ops import anchored_log_scores, ats_pair_sums, gather, splat, visible_fraction_linear, window_counts
 from .base import Objective
 
 
@@ -116,4 +121,129 @@ class AnchoredExact(Objective):
     def __call__(self, ev, motion):
         ls, _ = self.log_scores(ev, motion)
         s = ls.mean()
+        return {"loss": -s, "score": s.detach()}
+
+
+def _noise_from(gen, dgen_holder, rng, seed, shape, like, kind):
+    """Dequantisation / smoothing noise: from a CPU generator as the reference draws it (``rng="cpu"``), or
+    drawn on the device (``"device"``: no host round trip, other numbers for the same seed)."""
+    f = torch.rand if kind == "uniform" else torch.randn
+    if rng == "device" and like.is_cuda:
+        if dgen_holder[0] is None:
+            dgen_holder[0] = torch.Generator(device=like.device)
+            dgen_holder[0].manual_seed(seed if seed is not None else torch.seed())
+        return f(shape, generator=dgen_holder[0], device=like.device, dtype=like.dtype)
+    return f(shape, generator=gen).to(like)
+
+
+def _splat_value_at(a: torch.Tensor, y: torch.Tensor, sigma: float, H: int, W: int, truncate: bool) -> torch.Tensor:
+    """Bilinear look-up at ``a`` of one event's own Gaussian splat centred at ``y`` (normalised by 2 pi sigma^2;
+    with ``truncate``, zero beyond the splat's radius ceil(3 sigma) around round(y), as the splat kernel)."""
+    R = int(math.ceil(3 * sigma))
+    x0, y0 = torch.floor(a[:, 0]), torch.floor(a[:, 1])
+    ax, ay = a[:, 0] - x0, a[:, 1] - y0
+    cx, cy = torch.round(y[:, 0]), torch.round(y[:, 1])
+    norm = 1.0 / (2 * math.pi * sigma * sigma)
+    s = torch.zeros_like(ax)
+    for dy, wy in ((0, 1 - ay), (1, ay)):
+        for dx, wx in ((0, 1 - ax), (1, ax)):
+            px, py = x0 + dx, y0 + dy
+            ok = (px >= 0) & (px < W) & (py >= 0) & (py < H)
+            if truncate:
+                ok = ok & ((px - cx).abs() <= R) & ((py - cy).abs() <= R)
+            d2 = (px - y[:, 0]) ** 2 + (py - y[:, 1]) ** 2
+            s = s + wx * wy * ok.to(a.dtype) * norm * torch.exp(-d2 / (2 * sigma * sigma))
+    return s
+
+
+def cross_term(a, y, sigma, H, W):
+    """The anchor's own source copy at y, seen from the moved anchor a (atl/objectives/ats.py:186-202)."""
+    return _splat_value_at(a, y, sigma, H, W, truncate=True)
+
+
+def self_term(y, sigma, H, W):
+    """An event's own splat at its own position (atl/objectives/cmax.py:125-137)."""
+    return _splat_value_at(y, y, sigma, H, W, truncate=False)
+
+
+class AnchoredSliced(Objective):
+    """Anchored transport score for any motion model (atl/objectives/ats.py:108-183): per time slice, a
+    Gaussian splat of the sources transported to the slice centre, looked up at the anchors moved to it, with
+    the log|det| of the move, leave-one-out by subtracting the anchor's own splat, and the exposure correction.
+    Same constructor, plus ``rng`` as in :class:`AnchoredExact`."""
+    name = "ats_sliced"
+    reference_frame = False
+
+    def __init__(self, n_slices: int = 10, slices_per_step: Optional[int] = None, sigma: float = 1.0,
+                 tau: float = 1.0, eps_frac: float = 1e-2, n_anchors_per_slice: Optional[int] = None,
+                 logdet: bool = True, seed: Optional[int] = None, smooth_anchors: bool = True,
+                 dequantize: bool = True, visibility: bool = True, rng: str = "cpu"):
+        self.S, self.sps, self.sigma, self.tau, self.eps_frac = n_slices, slices_per_step, sigma, tau, eps_frac
+        self.nap, self.logdet = n_anchors_per_slice, logdet
+        self.smooth_anchors, self.dequantize, self.visibility = smooth_anchors, dequantize, visibility
+        self.seed, self.rng = seed, rng
+        self.gen = torch.Generator().manual_seed(seed) if seed is not None else None
+        self._dgen = [None]
+
+    def log_scores(self, ev: EventPacket, motion, anchor_mask: Optional[torch.Tensor] = None,
+                   source_mask: Optional[torch.Tensor] = None):
+        """Per-anchor log predictive densities over the scored slices, and the anchor indices."""
+        S = self.S
+        delta = 1.0 / S
+        slice_of = torch.clamp(torch.floor(ev.t / delta), 0, S - 1).long()
+        slices = list(range(S))
+        if self.sps is not None and self.sps < S:
+            slices = torch.randperm(S, generator=self.gen)[: self.sps].tolist()
+        eps = self.eps_frac / (ev.height * ev.width)
+        noise = lambda shape, like, kind: _noise_from(self.gen, self._dgen, self.rng, self.seed, shape, like, kind)
+        xs = ev.xy
+        if self.dequantize:
+            xs = xs + (noise(xs.shape, xs, "uniform") - 0.5)
+        xsm = xs + self.sigma * noise(xs.shape, xs, "normal") if self.smooth_anchors else xs
+        scores, picked = [], []
+        for s in slices:
+            c = (s + 0.5) * delta
+            src = (ev.t - c).abs() <= self.tau + delta / 2
+            if source_mask is not None:
+                src = src & source_mask
+            anc = slice_of == s
+            if anchor_mask is not None:
+                anc = anc & anchor_mask
+            ai = torch.nonzero(anc).squeeze(1)
+            if ai.numel() == 0:
+                continue
+            if self.nap is not None and ai.numel() > self.nap:
+                ai = ai[torch.randperm(ai.numel(), generator=self.gen)[: self.nap].to(ai.device)]
+            si = torch.nonzero(src).squeeze(1)
+            y = motion.transport(xs[si], ev.t[si], c, ev.b[si])
+            img = splat(y, torch.ones_like(ev.t[si]), ev.b[si], ev.batch_size, ev.height, ev.width, kernel="gauss",
+                        sigma=self.sigma)
+            if self.logdet:
+                a, ld = motion.transport_logdet(xsm[ai], ev.t[ai], c, ev.b[ai])
+            else:
+                a, ld = motion.transport(xsm[ai], ev.t[ai], c, ev.b[ai]), 0.0
+            val = gather(img, a, ev.b[ai])
+            in_src = src[ai].to(val.dtype)
+            if self.smooth_anchors:           # the anchor's own source copy sits at transport(xs_i)
+                y_own = motion.transport(xs[ai], ev.t[ai], c, ev.b[ai])
+                own = in_src * cross_term(a, y_own, self.sigma, ev.height, ev.width)
+            else:
+                own = in_src * self_term(a, self.sigma, ev.height, ev.width)
+            nsrc = torch.bincount(ev.b[si], minlength=ev.batch_size).to(val.dtype)[ev.b[ai]] - in_src
+            if self.visibility:
+                nsrc = nsrc * visible_fraction(motion, xsm[ai].detach(), ev.t[ai], ev.b[ai], ev, self.tau)
+            rho = (val - own).clamp(min=0) / nsrc.clamp(min=1)
+            scores.append(torch.log(eps + rho) + ld)
+            picked.append(ai)
+        if not scores:
+            z = ev.t.new_zeros(0)
+            return z, z.long()
+        return torch.cat(scores), torch.cat(picked)
+
+    def set_bandwidth(self, h: float):
+        self.sigma = float(h)
+
+    def __call__(self, ev, motion):
+        ls, _ = self.log_scores(ev, motion)
+        s = ls.mean() if ls.numel() else ev.t.new_zeros(())
         return {"loss": -s, "score": s.detach()}

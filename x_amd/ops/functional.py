@@ -126,11 +126,17 @@ def blur(img: torch.Tensor, sigma: float) -> torch.Tensor:
 
 
 # ------------------------------------------------------------------------------------------- flow grid
+def _tile_plan_ok(B, C, Hg, Wg):
+    """The tile adjoint takes C <= 4 channels, or up to 32 where 16x16 tiles fit its 16384-bin binning."""
+    return C <= 4 or (C <= 32 and B * ((Wg + 16) // 16) * ((Hg + 16) // 16) <= 16384)
+
+
 class _SampleGrid(torch.autograd.Function):
     """Bilinear border-clamped lookup of a (B, C, Hg, Wg) field (atl/motion/parametric.py:235-251).
 
-    When the field needs a gradient, the forward also sorts the positions by their base corner (a device
-    plan), so that the backward is a per-node gather instead of scattered atomic adds."""
+    When the field needs a gradient, the forward also bins the positions by the tile of their base corner (a
+    device plan), so that the backward accumulates tile by tile in LDS instead of scattered atomic adds.  The
+    positions' gradient (through the interpolation weights) is a per-event gather."""
 
     @staticmethod
     def forward(ctx, fld, pos, b, img_h, img_w, plan):
@@ -143,37 +149,42 @@ class _SampleGrid(torch.autograd.Function):
             st = stream_of(pos)
             call("atl_sample_grid_fwd", ptr(fld), B, C, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w),
                  ptr(out), st)
-            if plan and C <= 4:
+            if plan and _tile_plan_ok(B, C, Hg, Wg):
                 nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N))
                 if nbytes >= 0:
                     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=pos.device)
                     call("atl_grid_plan", B, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w), ptr(ws), nbytes, st)
                     ctx.plan = ws
-        ctx.save_for_backward(pos, b)
+        ctx.save_for_backward(pos, b, fld)
         ctx.shape, ctx.img = (B, C, Hg, Wg), (int(img_h), int(img_w))
         return out
 
     @staticmethod
     def backward(ctx, g):
-        pos, b = ctx.saved_tensors
+        pos, b, fld = ctx.saved_tensors
         B, C, Hg, Wg = ctx.shape
-        gf = torch.zeros(B, C, Hg, Wg, device=pos.device, dtype=F32)
         g = g.contiguous().float()
+        gf = gp = None
         with torch.cuda.device(pos.device):
-            if ctx.plan is not None:
-                call("atl_sample_grid_bwd_planned", ptr(g), B, C, Hg, Wg, ptr(pos), pos.shape[0], ctx.img[0],
-                     ctx.img[1], ptr(ctx.plan), ptr(gf), stream_of(pos))
-            else:
-                call("atl_sample_grid_bwd", ptr(g), B, C, Hg, Wg, ptr(pos), ptr(b), pos.shape[0], ctx.img[0],
-                     ctx.img[1], ptr(gf), stream_of(pos))
-        return gf, None, None, None, None, None
+            if ctx.needs_input_grad[0]:
+                gf = torch.zeros(B, C, Hg, Wg, device=pos.device, dtype=F32)
+                if ctx.plan is not None:
+                    call("atl_sample_grid_bwd_planned", ptr(g), B, C, Hg, Wg, ptr(pos), pos.shape[0], ctx.img[0],
+                         ctx.img[1], ptr(ctx.plan), ptr(gf), stream_of(pos))
+                else:
+                    call("atl_sample_grid_bwd", ptr(g), B, C, Hg, Wg, ptr(pos), ptr(b), pos.shape[0], ctx.img[0],
+                         ctx.img[1], ptr(gf), stream_of(pos))
+            if ctx.needs_input_grad[1]:
+                gp = torch.empty_like(pos)
+                call("atl_sample_grid_bwd_pos", ptr(g), ptr(fld), B, C, Hg, Wg, ptr(pos), ptr(b), pos.shape[0],
+                     ctx.img[0], ctx.img[1], ptr(gp), stream_of(pos))
+        return gf, gp, None, None, None, None
 
 
 def sample_grid_hip(fld: torch.Tensor, pos: torch.Tensor, b: torch.Tensor, img_hw=(0, 0)) -> torch.Tensor:
     """HIP flow lookup: ``pos`` are grid coordinates, or image pixels mapped by x / max(W-1, 1) * (Wg-1)
-    when ``img_hw`` = (H, W) is given (DenseLinearFlow.field).  Differentiable w.r.t. the field only."""
-    if pos.requires_grad:
-        raise NotImplementedError("the HIP flow lookup differentiates w.r.t. the field only (positions are data)")
+    when ``img_hw`` = (H, W) is given (DenseLinearFlow.field).  Differentiable w.r.t. the field and the
+    positions."""
     get_ext()
     plan = fld.requires_grad and torch.is_grad_enabled()     # sort the positions for a gather backward
     return _SampleGrid.apply(fld, pos, b, img_hw[0], img_hw[1], plan)

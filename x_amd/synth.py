@@ -169,3 +169,36 @@ def small_window(seed=0, n=3000, H=40, W=48, vmax=6.0, B=1, scene="segments") ->
     p = np.concatenate([w.p for w in parts])
     b = np.concatenate([np.full(w.n, k, np.int64) for k, w in enumerate(parts)])
     return Window(xy=xy, t=t, p=p, b=b, height=H, width=W, batch_size=B, motion={"kind": "dense", "grid": grid})
+
+
+def trajectory_coeffs(rng, B, K, H, W, tile=4, sigma_px=40.0, dmax=20.0):
+    """(B, 2K, H, W) f32 smooth random trajectory coefficients [y_1..y_K, x_1..x_K] for PixelTrajectories:
+    N(0, 1) filtered at tile resolution (sigma = sigma_px / tile tiles, mode='reflect'), scaled so that the
+    largest per-tile coefficient vector has norm dmax px; each tile's value fills its tile x tile block."""
+    from scipy.ndimage import gaussian_filter
+    Hq, Wq = -(-H // tile), -(-W // tile)
+    g = rng.standard_normal((B, 2 * K, Hq, Wq))
+    for k in range(B):
+        for c in range(2 * K):
+            g[k, c] = gaussian_filter(g[k, c], sigma=sigma_px / tile, mode="reflect", truncate=4.0)
+    mag = np.sqrt(g[:, :K] ** 2 + g[:, K:] ** 2).max()
+    g *= dmax / mag
+    full = np.repeat(np.repeat(g, tile, axis=2), tile, axis=3)[:, :, :H, :W]
+    return np.ascontiguousarray(full.astype(F32))
+
+
+def trajectory_windows(seed=0, B=4, n=500_000, H=480, W=640, K=10) -> Window:
+    """B windows of n events each (640x480, 25 ms per window, 50 segments + 30% noise moving under a smooth
+    dense flow of at most 20 px/window), packed and sorted by (b, t), plus the coefficients of degree-K
+    pixel trajectories (``motion["coeffs"]``, (B, 2K, H, W), largest coefficient norm 20 px)."""
+    rng = np.random.default_rng(seed)
+    parts = []
+    for k in range(B):
+        grid = smooth_flow(rng, H, W, sigma=40.0, vmax=20.0)
+        parts.append(make_window(n, H, W, {"kind": "dense", "grid": grid}, "segments", 50, 0.3, duration=0.025,
+                                 rng=rng))
+    coeffs = trajectory_coeffs(rng, B, K, H, W)
+    return Window(xy=np.concatenate([w.xy for w in parts]), t=np.concatenate([w.t for w in parts]),
+                  p=np.concatenate([w.p for w in parts]),
+                  b=np.concatenate([np.full(w.n, k, np.int64) for k, w in enumerate(parts)]), height=H, width=W,
+                  batch_size=B, duration=0.025, motion={"kind": "trajectories", "coeffs": coeffs, "K": K})
