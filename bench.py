@@ -328,7 +328,7 @@ def iwe_main(a, dev):
         step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1 in rec[k]])) for k in kernels if rec[k]}
+    ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec[k]])) for k in kernels if rec[k]}
     _ext.time_kernels(())
     hw = ev.height * ev.width
     g = 2 * hw if a.workload == "iwe" else 0
@@ -356,6 +356,7 @@ TRAJ_BYTES = {     # algorithmic bytes per entry point: per event, plus the fiel
     "atl_sample_grid_bwd_planned": lambda n, c, f, hw: (16 + 4 * c) * n + 8 * c * f,
     "atl_sample_grid_bwd_pos": lambda n, c, f, hw: (24 + 4 * c) * n + 4 * c * f,
     "atl_splat_gauss_fwd": lambda n, c, f, hw: 20 * n + 4 * hw,
+    "atl_splat_gauss_fwd_ws": lambda n, c, f, hw: 20 * n + 4 * hw,
     "atl_splat_gauss_bwd": lambda n, c, f, hw: 32 * n + 4 * hw,
     "atl_gather_bilinear_fwd": lambda n, c, f, hw: 20 * n + 4 * hw,
     "atl_gather_bilinear_bwd_ws": lambda n, c, f, hw: 28 * n + 8 * hw,
@@ -389,15 +390,19 @@ def trajectories_main(a, dev):
         step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1 in rec[k]])) for k in kernels if rec[k]}
+    ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec[k]])) for k in kernels if rec[k]}
     calls = {k: len(rec[k]) / a.steps for k in kernels if rec[k]}
+    rec_all = {k: list(v) for k, v in rec.items()}
     _ext.time_kernels(())
     tot = {k: ms[k] * calls[k] for k in ms}
     dom = max(tot, key=lambda k: tot[k])
-    # events per launch of the dominant entry point: sources of one slice (all within tau + delta/2) or anchors
-    n_launch = ev.n
-    gbs = TRAJ_BYTES[dom](n_launch, 2 * K, (win.height // 4) * (win.width // 4) * ev.batch_size,
-                          win.height * win.width * ev.batch_size) / (ms[dom] * 1e-3) / 1e9
+    # achieved bandwidth of the dominant entry point: algorithmic bytes of every call (its own event count)
+    # over the summed call durations
+    nodes, pix = (win.height // 4) * (win.width // 4) * ev.batch_size, win.height * win.width * ev.batch_size
+    calls_dom = [(e0.elapsed_time(e1), n) for e0, e1, n in rec_all[dom]]
+    gbs = (sum(TRAJ_BYTES[dom](n, 2 * K, nodes, pix) for _, n in calls_dom) /
+           (sum(t for t, _ in calls_dom) * 1e-3) / 1e9)
+    n_launch = float(np.mean([n for _, n in calls_dom]))
     line = {
         "metric": f"events/s for sliced anchored score fwd+bwd @{ev.n} events ({ev.batch_size} windows) 640x480, "
                   f"degree-{K} pixel trajectories; % HBM roofline",
@@ -410,7 +415,7 @@ def trajectories_main(a, dev):
                    "events": ev.n, "windows": ev.batch_size, "sensor": [640, 480], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": gbs, "peak": 8000.0, "unit": "GB/s",
                      "frac": gbs / 8000.0, "traffic": recorded_traffic(dom), "kernel_ms": ms[dom],
-                     "events_per_launch": n_launch},
+                     "mean_events_per_launch": n_launch},
         "kernel_ms": ms, "kernel_calls_per_step": calls, "kernel_ms_per_step": tot,
     }
     if not a.no_cpu:
@@ -482,7 +487,7 @@ def main():
         step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1 in rec[k]])) for k in kernels}
+    ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec[k]])) for k in kernels}
     _ext.time_kernels(())
     # contributing pairs K = sum_i n_i of one step (counted outside the timed region)
     with torch.no_grad():

@@ -57,6 +57,12 @@ int atl_splat_bilinear_fwd_ws(const float* pos, const float* w, const int64_t* b
 int atl_gather_bilinear_bwd_ws(const float* gval, const float* img, const float* pos, const int64_t* b, int64_t N,
                                int64_t B, int64_t H, int64_t W, float* gimg, float* gpos, void* ws, int64_t ws_bytes,
                                hipStream_t stream);
+/* The Gaussian splat forward with the same tile engine (tiles of the rounded centres, an LDS window of
+ * T + 2R pixels per tile); R <= 8.  ws: atl_splat_gauss_ws_bytes(N, B, H, W, R) bytes (-1: unsupported). */
+int64_t atl_splat_gauss_ws_bytes(int64_t N, int64_t B, int64_t H, int64_t W, int64_t R);
+int atl_splat_gauss_fwd_ws(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B, int64_t H,
+                           int64_t W, double sigma, int64_t R, float* img, void* ws, int64_t ws_bytes,
+                           hipStream_t stream);
 /* voxel_grid (csrc/atl_ops.h:49-50, csrc/atl_cpu.cpp:256-286): vox (B,C,H,W) accumulated. */
 int atl_voxel_grid(const float* pos, const float* t, const float* p, const int64_t* b, int64_t N, int64_t B,
                    int64_t C, int64_t H, int64_t W, float* vox, hipStream_t stream);

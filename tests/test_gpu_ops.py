@@ -88,13 +88,35 @@ def test_splat_gather_tile_paths(B, H, W):
     w[::17] = 0.0
     b = rng.integers(0, B, n).astype(np.int64)
     img = F.get_ext().splat_bilinear_fwd(T(pos), T(w), T(b), B, H, W)
-    close_rel(N(img), O.splat_bilinear_fwd(pos, w, b, B, H, W), 1e-5)
+    # signed weights cancel on the crowded pixel: the summation-order bar is relative to the sum of |terms|
+    mag = float(O.splat_bilinear_fwd(pos, np.abs(w), b, B, H, W).max())
+    close_rel(N(img), O.splat_bilinear_fwd(pos, w, b, B, H, W), 1e-5, floor=1e-6 * mag)
     src = rng.standard_normal((B, H, W)).astype(F32)
     g = rng.standard_normal(n).astype(F32)
     gimg, gp = F.get_ext().gather_bilinear_bwd(T(g), T(src), T(pos), T(b))
     want_img, want_p = O.gather_bilinear_bwd(g, src, pos, b)
     assert np.array_equal(N(gp), want_p)
     close_rel(N(gimg), want_img, 1e-5)
+
+
+@pytest.mark.parametrize("B,H,W,sigma,R", [(1, 480, 640, 1.0, 3), (2, 60, 80, 2.5, 8), (20, 480, 640, 1.0, 3),
+                                           (2, 40, 48, 3.0, 9), (1, 3, 2, 1.0, 3)])
+def test_splat_gauss_tile_paths(B, H, W, sigma, R):
+    """The tile-binned Gaussian splat (centres rounded into 16 or 32-px tiles, an LDS window of T + 2R) and its
+    per-event fallback (R > 8) against the oracle: a crowded pixel, centres within R outside the image, zero
+    weights."""
+    print(f"gauss tile paths B={B} {H}x{W} sigma={sigma} R={R}", flush=True)
+    rng = np.random.default_rng(B + R)
+    n = 40000
+    pos = np.stack([rng.uniform(-R - 1.5, W + R + 0.5, n), rng.uniform(-R - 1.5, H + R + 0.5, n)], 1).astype(F32)
+    pos[: n // 4] = np.array([min(W - 1, 9) + 0.3, min(H - 1, 4) + 0.6], F32)          # one crowded pixel
+    w = rng.standard_normal(n).astype(F32)
+    w[::13] = 0.0
+    b = rng.integers(0, B, n).astype(np.int64)
+    img = F.get_ext().splat_gauss_fwd(T(pos), T(w), T(b), B, H, W, sigma, R)
+    # signed weights cancel on the crowded pixel: the summation-order bar is relative to the sum of |terms|
+    mag = float(O.splat_gauss_fwd(pos, np.abs(w), b, B, H, W, sigma, R).max())
+    close_rel(N(img), O.splat_gauss_fwd(pos, w, b, B, H, W, sigma, R), 1e-5, floor=1e-6 * mag)
 
 
 def test_voxel_matches_oracle():

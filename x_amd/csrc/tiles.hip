@@ -30,7 +30,8 @@ constexpr int kTileMaxKeys = 16384;              // LDS histogram capacity (tile
 constexpr int kAccBlock = 256;                   // accumulation: threads per tile
 constexpr int kMaxChannels = 32;                 // field channels of the tile adjoint (LDS: C x 17 x 17 floats)
 
-enum { kImage = 0, kGrid = 1 };
+enum { kImage = 0, kGrid = 1, kGauss = 2 };
+constexpr int kMaxGaussRadius = 8;               // truncated-Gaussian splats of larger radius stay per event
 
 struct TileGeo {
   int B, H, W;               // image (kImage) or grid (kGrid) extent
@@ -39,6 +40,8 @@ struct TileGeo {
   int N, nblk;
   int mode;
   int C;                     // kGrid: channels of the field
+  int R;                     // kGauss: splat radius (pixels around round(pos))
+  float inv2s2, norm;        // kGauss: 1 / (2 sigma^2), 1 / (2 pi sigma^2)
   int scale;                 // kGrid: positions are image pixels mapped by sxw, syh
   float sxw, syh;
 };
@@ -83,6 +86,17 @@ __device__ __forceinline__ GridCell grid_cell(float x, float y, int Hg, int Wg, 
   return c;
 }
 
+// kGauss: centre (round(x), round(y)) of a truncated Gaussian splat and the test of csrc/atl_cpu.cpp:79-104
+// (its window of radius R must meet the image).
+__device__ __forceinline__ bool gauss_centre(float x, float y, const TileGeo& g, int& cx, int& cy) {
+  const float rx = roundf(x), ry = roundf(y);
+  if (!(rx >= (float)(-g.R) && rx <= (float)(g.W - 1 + g.R) && ry >= (float)(-g.R) && ry <= (float)(g.H - 1 + g.R)))
+    return false;
+  cx = (int)rx;
+  cy = (int)ry;
+  return true;
+}
+
 // Tile key of event n (-1: contributes nothing) and its LDS origin.
 template <int MODE>
 __device__ __forceinline__ int tile_key(float x, float y, int64_t b, const TileGeo& g) {
@@ -93,6 +107,11 @@ __device__ __forceinline__ int tile_key(float x, float y, int64_t b, const TileG
     if (!image_base(x, y, g.H, g.W, x0, y0)) return -1;
     tx = (x0 + 1) / g.T;
     ty = (y0 + 1) / g.T;
+  } else if (MODE == kGauss) {
+    int cx, cy;
+    if (!gauss_centre(x, y, g, cx, cy)) return -1;
+    tx = (cx + g.R) / g.T;
+    ty = (cy + g.R) / g.T;
   } else {
     const GridCell c = grid_cell(x, y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
     tx = c.x0 / g.T;
@@ -150,12 +169,27 @@ __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __rest
 constexpr int kAccItems = 8;
 constexpr int kAccRange = kAccBlock * kAccItems;
 
-template <int MODE, int C, int T>
+template <int MODE, int C>
 __device__ __forceinline__ void accum_record(const float4& q, const float* __restrict__ gout, const TileGeo& g,
-                                             int ox, int oy, float* acc) {
+                                             int ox, int oy, int L, float* acc) {
   const int nc = C > 0 ? C : g.C;                  // C = 0: the field's channel count at run time
-  constexpr int L = T + 1;
-  if (MODE == kImage) {
+  if (MODE == kGauss) {
+    int cx, cy;
+    if (!gauss_centre(q.x, q.y, g, cx, cy)) return;   // never taken: the binning applied this test
+    const float wn = q.z * g.norm;
+    const int ylo = max(cy - g.R, 0), yhi = min(cy + g.R, g.H - 1);
+    const int xlo = max(cx - g.R, 0), xhi = min(cx + g.R, g.W - 1);
+    for (int yy = ylo; yy <= yhi; ++yy) {
+      const float dy = (float)yy - q.y;
+      const int ly = yy - oy;
+      for (int xx = xlo; xx <= xhi; ++xx) {
+        const float dx = (float)xx - q.x;
+        const int lx = xx - ox;
+        if ((unsigned)ly < (unsigned)L && (unsigned)lx < (unsigned)L)
+          atomicAdd(acc + ly * L + lx, wn * expf(-(dx * dx + dy * dy) * g.inv2s2));
+      }
+    }
+  } else if (MODE == kImage) {
     int x0, y0;
     if (!image_base(q.x, q.y, g.H, g.W, x0, y0)) return;   // never taken: the binning applied this test
     const float fx = (float)x0, fy = (float)y0;
@@ -203,7 +237,7 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict_
                                                           const float4* __restrict__ rec,
                                                           const float* __restrict__ gout, TileGeo g,
                                                           float* __restrict__ out) {
-  constexpr int L = T + 1;
+  const int L = MODE == kGauss ? T + 2 * g.R : T + 1;   // LDS edge: the pixels one tile's events reach
   extern __shared__ float acc[];                  // nc * L * L floats
   const int nc = C > 0 ? C : g.C;
   __shared__ int ts[kAccBlock + 1];                       // starts of the tiles first .. first + kAccBlock
@@ -249,8 +283,8 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict_
       __syncthreads();
       const int b = key / plane, r = key - b * plane;
       const int ty = r / g.TX, tx = r - ty * g.TX;
-      const int ox = MODE == kImage ? tx * T - 1 : tx * T;   // pixel of LDS column 0
-      const int oy = MODE == kImage ? ty * T - 1 : ty * T;
+      const int ox = MODE == kImage ? tx * T - 1 : MODE == kGauss ? tx * T - 2 * g.R : tx * T;   // LDS column 0
+      const int oy = MODE == kImage ? ty * T - 1 : MODE == kGauss ? ty * T - 2 * g.R : ty * T;
       float4 q[kAccItems];
 #pragma unroll
       for (int u = 0; u < kAccItems; ++u) {
@@ -259,7 +293,7 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict_
       }
 #pragma unroll
       for (int u = 0; u < kAccItems; ++u)
-        if (s0 + u * kAccBlock + (int)threadIdx.x < s1) accum_record<MODE, C, T>(q[u], gout, g, ox, oy, acc);
+        if (s0 + u * kAccBlock + (int)threadIdx.x < s1) accum_record<MODE, C>(q[u], gout, g, ox, oy, L, acc);
       __syncthreads();
       for (int a = threadIdx.x; a < L * L; a += kAccBlock) {
         const int py = oy + a / L, px = ox + a % L;
@@ -317,10 +351,13 @@ __global__ void __launch_bounds__(kBlock) k_gather_bwd_pos(const float* __restri
 int64_t align256(int64_t n) { return (n + 255) & ~(int64_t)255; }
 
 // Geometry: the smallest tile edge (16 or 32) whose tile count fits the LDS histogram; false if none does.
-bool tile_geo(int mode, int64_t B, int64_t H, int64_t W, int64_t N, int64_t img_h, int64_t img_w, TileGeo& g) {
+bool tile_geo(int mode, int64_t B, int64_t H, int64_t W, int64_t N, int64_t img_h, int64_t img_w, TileGeo& g,
+              int R = 0) {
   if (B < 1 || H < 1 || W < 1 || N < 0 || N >= ((int64_t)1 << 30) || (double)B * H * W >= 2.0e9) return false;
+  if (mode == kGauss && (R < 0 || R > kMaxGaussRadius)) return false;
+  const int64_t ext = mode == kGauss ? 2 * R : 1;   // base corners / centres span W + ext positions per row
   for (int T : {16, 32}) {
-    const int64_t tx = (W + 1 + T - 1) / T, ty = (H + 1 + T - 1) / T;
+    const int64_t tx = (W + ext + T - 1) / T, ty = (H + ext + T - 1) / T;
     if (B * tx * ty <= kTileMaxKeys) {
       g.B = (int)B; g.H = (int)H; g.W = (int)W; g.T = T;
       g.TX = (int)tx; g.TY = (int)ty; g.nkeys = (int)(B * tx * ty);
@@ -328,6 +365,8 @@ bool tile_geo(int mode, int64_t B, int64_t H, int64_t W, int64_t N, int64_t img_
       g.nblk = (int)((N + kTilePerBlock - 1) / kTilePerBlock);
       g.mode = mode;
       g.C = 1;
+      g.R = R;
+      g.inv2s2 = g.norm = 0.f;
       g.scale = img_h > 0 && img_w > 0;
       g.sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1);
       g.syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
@@ -380,11 +419,13 @@ void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const flo
   const char* w = (const char*)ws;
   const unsigned grid = (unsigned)((g.N + kAccRange - 1) / kAccRange);   // records <= N
   const int nc = C > 0 ? C : g.C;
+  const size_t edge = MODE == kGauss ? (size_t)(g.T + 2 * g.R) : (size_t)(g.T + 1);
+  const size_t lds = (size_t)nc * edge * edge * sizeof(float);
   if (g.T == 16)
-    hipLaunchKernelGGL((k_tile_accum<MODE, C, 16>), dim3(grid), dim3(kAccBlock), (size_t)nc * 17 * 17 * 4, stream,
+    hipLaunchKernelGGL((k_tile_accum<MODE, C, 16>), dim3(grid), dim3(kAccBlock), lds, stream,
                        (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, out);
   else
-    hipLaunchKernelGGL((k_tile_accum<MODE, C, 32>), dim3(grid), dim3(kAccBlock), (size_t)nc * 33 * 33 * 4, stream,
+    hipLaunchKernelGGL((k_tile_accum<MODE, C, 32>), dim3(grid), dim3(kAccBlock), lds, stream,
                        (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, out);
 }
 
@@ -426,6 +467,29 @@ int atl_gather_bilinear_bwd_ws(const float* gval, const float* img, const float*
   tile_bin<kImage>(g, L, ws, pos, b, gval, stream);
   tile_accum<kImage, 1>(g, L, ws, nullptr, gimg, stream);
   return check_launch("gather_bilinear_bwd_ws");
+}
+
+int64_t atl_splat_gauss_ws_bytes(int64_t N, int64_t B, int64_t H, int64_t W, int64_t R) {
+  TileGeo g;
+  if (!tile_geo(kGauss, B, H, W, N, 0, 0, g, (int)R)) return -1;
+  return tile_layout(g).bytes;
+}
+
+int atl_splat_gauss_fwd_ws(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B, int64_t H,
+                           int64_t W, double sigma, int64_t R, float* img, void* ws, int64_t ws_bytes,
+                           hipStream_t stream) {
+  if (N == 0 || B == 0) return 0;
+  TileGeo g;
+  if (!(sigma > 0) || !tile_geo(kGauss, B, H, W, N, 0, 0, g, (int)R)) { set_error("splat_gauss_fwd_ws: unsupported arguments (sigma=%g R=%lld)", sigma, (long long)R); return 1; }
+  const TileLayout L = tile_layout(g);
+  if (!ws || ws_bytes < L.bytes) { set_error("splat_gauss_fwd_ws: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
+  if (!pos || !w || !b || !img) { set_error("splat_gauss_fwd_ws: null argument"); return 1; }
+  const float s2 = (float)(sigma * sigma);        // the per-event kernel's constants, same fp32 expressions
+  g.inv2s2 = 1.f / (2.f * s2);
+  g.norm = 1.f / (2.f * (float)M_PI * s2);
+  tile_bin<kGauss>(g, L, ws, pos, b, w, stream);
+  tile_accum<kGauss, 1>(g, L, ws, nullptr, img, stream);
+  return check_launch("splat_gauss_fwd_ws");
 }
 
 // Flow-grid adjoint through a tile plan: atl_grid_plan bins the positions once (in the forward), and

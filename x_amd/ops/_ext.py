@@ -57,6 +57,8 @@ _SIGS = {
     "atl_anchored_epilogue_bwd": [_P, _P, _P, _I, _P, _P],
     "atl_grid_plan_bytes": [_I, _I, _I, _I],
     "atl_tile_ws_bytes": [_I, _I, _I, _I],
+    "atl_splat_gauss_ws_bytes": [_I, _I, _I, _I, _I],
+    "atl_splat_gauss_fwd_ws": [_P, _P, _P, _I, _I, _I, _I, _D, _I, _P, _P, _I, _P],
     "atl_splat_bilinear_fwd_ws": [_P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P],
     "atl_gather_bilinear_bwd_ws": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P],
     "atl_grid_plan": [_I, _I, _I, _P, _P, _I, _I, _I, _P, _I, _P],
@@ -67,7 +69,7 @@ _SIGS = {
     "atl_fast_pair_bwd": [_P, _P, _P, _P, _P],
 }
 _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.c_int64,
-            "atl_tile_ws_bytes": ctypes.c_int64, "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
+            "atl_tile_ws_bytes": ctypes.c_int64, "atl_splat_gauss_ws_bytes": ctypes.c_int64, "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):
     """Mirror of ``atl_fast_geometry`` (include/atl_hip.h): sizes, grid and workspace layout of the fused
@@ -115,12 +117,18 @@ def exported_symbols():
     return sorted(_SIGS) + ["atl_last_error", "atl_abi_version"]
 
 
-_TIMED = {}          # entry point -> list of (start, end) events, while kernel timing is on
+_TIMED = {}          # entry point -> list of (start, end, events) per call, while kernel timing is on
+# position of the event count N in the arguments of the entry points whose calls are sized by it
+_NARG = {"atl_sample_grid_fwd": 7, "atl_sample_grid_bwd_planned": 6, "atl_sample_grid_bwd_pos": 8,
+         "atl_splat_gauss_fwd": 3, "atl_splat_gauss_bwd": 4, "atl_splat_gauss_fwd_ws": 3,
+         "atl_gather_bilinear_fwd": 3, "atl_gather_bilinear_bwd_ws": 4, "atl_splat_bilinear_fwd_ws": 3,
+         "atl_splat_bilinear_bwd": 4}
 
 
 def time_kernels(names) -> dict:
     """Bracket every later call of the named entry points with events on the caller's current stream (the
-    stream the kernels run on); returns the live {name: [(start, end), ...]} record.  ``time_kernels(())``
+    stream the kernels run on); returns the live {name: [(start, end, events), ...]} record (events: the
+    call's event count where the entry point has one, else None).  ``time_kernels(())``
     turns timing off."""
     _TIMED.clear()
     for n in names:
@@ -137,7 +145,8 @@ def call(name: str, *args):
         e0.record()
         rc = getattr(lib, name)(*args)
         e1.record()
-        rec.append((e0, e1))
+        k = _NARG.get(name)
+        rec.append((e0, e1, int(args[k]) if k is not None else None))
     else:
         rc = getattr(lib, name)(*args)
     if rc != 0:
@@ -211,9 +220,16 @@ class HipOps:
         N = pos.shape[0]
         _need(pos, "pos", F32, dev, (N, 2)); _need(w, "w", F32, dev, (N,)); _need(b, "b", I64, dev, (N,))
         img = torch.zeros(int(B), int(H), int(W), device=dev, dtype=F32)
+        nbytes = (load_library().atl_splat_gauss_ws_bytes(N, int(B), int(H), int(W), int(radius))
+                  if N > 0 and int(B) > 0 else -1)
         with torch.cuda.device(dev):
-            call("atl_splat_gauss_fwd", ptr(pos), ptr(w), ptr(b), N, int(B), int(H), int(W), float(sigma),
-                 int(radius), ptr(img), stream_of(pos))
+            if nbytes >= 0:          # tile-binned LDS accumulation
+                ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+                call("atl_splat_gauss_fwd_ws", ptr(pos), ptr(w), ptr(b), N, int(B), int(H), int(W), float(sigma),
+                     int(radius), ptr(img), ptr(ws), nbytes, stream_of(pos))
+            else:                    # radius beyond the tile engine's, or too many tiles: atomics per pixel
+                call("atl_splat_gauss_fwd", ptr(pos), ptr(w), ptr(b), N, int(B), int(H), int(W), float(sigma),
+                     int(radius), ptr(img), stream_of(pos))
         return img
 
     def splat_gauss_bwd(self, gimg, pos, w, b, sigma, radius):
