@@ -46,6 +46,7 @@ constexpr int kP1Block = 512;                      // pass-1 workgroup
 constexpr int kSrcPerBlock = 4096;                 // pass-1 sources per block (8 per thread)
 constexpr int kAncPerBlock = 8192;                 // pass-1 anchors per block (16 per thread)
 constexpr int kUnroll = 4;                         // candidates per walk step (record arrays padded by this)
+constexpr int kSliceBatch = 4;                     // pass 1: slices of one source keyed and placed together
 
 constexpr int kXcd = 8;                            // XCDs: consecutive workgroups go round-robin over them
 
@@ -101,18 +102,11 @@ __device__ __forceinline__ void search_radius(const FParams* P, const FGeo& G, f
   R2 = R * R;
 }
 
-__device__ __forceinline__ int cell_of(float p, float lo, float hi, float cf, int n) {
-  const float c = fminf(fmaxf(p, lo), hi);          // NaN -> lo
-  const int i = (int)floorf((c - lo) / cf);
-  return min(max(i, 0), n - 1);
-}
-
 __device__ __forceinline__ float clampf(float p, float lo, float hi) { return fminf(fmaxf(p, lo), hi); }
 
-// Cell of a walk bound (a query position -/+ a search half-width), by a multiplication with 1/cf instead of
-// the binning's division.  The two can differ only where the quotient lies within a few ulps (< 1e-4 cells)
-// of an integer; R carries 0.01 px (> 6e-3 cells) of slack beyond the largest distance a contributing pair
-// can have in fp32, so every cell that holds a contributing item is still inside [c(lo - w), c(lo + w)].
+// Cell of a position: floor((clamp(p) - lo) / cf) by a multiplication with 1/cf.  The binning and the walk
+// bounds use this same monotone function, so an item at p with lo_q <= p <= hi_q lies in a cell between
+// cell(lo_q) and cell(hi_q); the 0.01 px slack in R covers the rounding of the walk bounds themselves.
 __device__ __forceinline__ int cell_walk(float p, float lo, float hi, float icf, int n) {
   const float c = fminf(fmaxf(p, lo), hi);          // NaN -> lo
   const int i = (int)floorf((c - lo) * icf);
@@ -168,7 +162,7 @@ __device__ __forceinline__ int entry_key(float2 xj, float2 vj, float tj, int bj,
   const float dt = slice_centre(s, G.delta) - tj;
   yx = xj.x + vj.x * dt;
   yy = xj.y + vj.y * dt;
-  const int cx = cell_of(yx, G.gx0, G.gx1, G.cf, G.GW), cy = cell_of(yy, G.gy0, G.gy1, G.cf, G.GH);
+  const int cx = cell_walk(yx, G.gx0, G.gx1, G.icf, G.GW), cy = cell_walk(yy, G.gy0, G.gy1, G.icf, G.GH);
   return ((bj * G.S + s) * G.GH + cy) * G.GW + cx;
 }
 
@@ -184,7 +178,7 @@ __device__ __forceinline__ bool anchor_rec(int64_t m, const float2* x, const flo
   const float ta = t[a];
   const float2 xa = anchor_xy ? anchor_xy[m] : x[a];
   const int s = (int)fminf(fmaxf(floorf(ta / G.delta), 0.f), (float)(G.S - 1));   // = anchor_slice(ta, G)
-  const int cx = cell_of(xa.x, G.gx0, G.gx1, G.cf, G.GW), cy = cell_of(xa.y, G.gy0, G.gy1, G.cf, G.GH);
+  const int cx = cell_walk(xa.x, G.gx0, G.gx1, G.icf, G.GW), cy = cell_walk(xa.y, G.gy0, G.gy1, G.icf, G.GH);
   key = G.ncell_pad + ((((int)ba * G.S + s) * G.GH + cy) * G.GW + cx);
   rec.f = make_float4(xa.x, xa.y, ta, ta - slice_centre(s, G.delta));
   rec.i = make_int4((int)a, (int)m, key, 0);
@@ -222,14 +216,6 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
   const int blk = blockIdx.x;
   for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) hist[i] = SCATTER ? cnt[i * nblk + blk] : 0;
   __syncthreads();
-  auto emit = [&](int key, const Rec& r) {
-    const int bucket = key >> G.bshift;
-    if (!SCATTER) {
-      atomicAdd(hist + bucket, 1);
-    } else {
-      trec[atomicAdd(hist + bucket, 1)] = r;
-    }
-  };
   if (blk < G.nblk_e) {
     constexpr int per = kSrcPerBlock / kP1Block;
     const int64_t j0 = (int64_t)blk * kSrcPerBlock;
@@ -254,29 +240,65 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
       int lo, hi;
       slice_range(tj[u], G, lo, hi);
       const int own = min(max((int)fminf(fmaxf(floorf(tj[u] / G.delta), 0.f), (float)(G.S - 1)), lo), hi);
-      for (int s = lo; s <= hi; ++s) {
-        Rec r;
-        float yx, yy;
-        const int key = entry_key(xj[u], vj[u], tj[u], (int)bj[u], s, G, yx, yy);
-        r.f = make_float4(yx, yy, vj[u].x, vj[u].y);
-        r.i = make_int4(__float_as_int(tj[u]), (int)j, key, 0);
-        emit(key, r);
-        if (s == own) {
-          r.f = make_float4(xj[u].x, xj[u].y, vj[u].x, vj[u].y);
-          r.i.z = 2 * G.ncell_pad + key;
-          emit(r.i.z, r);
+      // kSliceBatch slices at a time: keys, then all LDS slot atomics, then all stores (no atomic -> store
+      // round trip per record)
+      for (int s0 = lo; s0 <= hi; s0 += kSliceBatch) {
+        int key[kSliceBatch + 1], slot[kSliceBatch + 1];
+        float yx[kSliceBatch], yy[kSliceBatch];
+#pragma unroll
+        for (int q = 0; q < kSliceBatch; ++q) key[q] = entry_key(xj[u], vj[u], tj[u], (int)bj[u], min(s0 + q, hi), G,
+                                                                yx[q], yy[q]);
+        const int oq = own - s0;                   // the source record goes with its own slice
+        key[kSliceBatch] = -1;
+#pragma unroll
+        for (int q = 0; q < kSliceBatch; ++q)
+          if (q == oq) key[kSliceBatch] = 2 * G.ncell_pad + key[q];
+#pragma unroll
+        for (int q = 0; q <= kSliceBatch; ++q) {
+          const bool live = q < kSliceBatch ? s0 + q <= hi : key[kSliceBatch] >= 0;
+          if (live) slot[q] = atomicAdd(hist + (key[q] >> G.bshift), 1);
+        }
+        if (SCATTER) {
+#pragma unroll
+          for (int q = 0; q < kSliceBatch; ++q) {
+            if (s0 + q > hi) continue;
+            Rec r;
+            r.f = make_float4(yx[q], yy[q], vj[u].x, vj[u].y);
+            r.i = make_int4(__float_as_int(tj[u]), (int)j, key[q], 0);
+            trec[slot[q]] = r;
+          }
+          if (key[kSliceBatch] >= 0) {
+            Rec r;
+            r.f = make_float4(xj[u].x, xj[u].y, vj[u].x, vj[u].y);
+            r.i = make_int4(__float_as_int(tj[u]), (int)j, key[kSliceBatch], 0);
+            trec[slot[kSliceBatch]] = r;
+          }
         }
       }
     }
   } else {
     const int64_t m0 = (int64_t)(blk - G.nblk_e) * kAncPerBlock;
     const int64_t m1 = m0 + kAncPerBlock < M ? m0 + kAncPerBlock : M;
-    for (int64_t m = m0 + threadIdx.x; m < m1; m += blockDim.x) {
-      int key;
-      Rec r;
-      if (anchor_rec(m, x, t, b, anchors, anchor_xy, N, G, key, r)) {
-        emit(key, r);
-        if (!SCATTER) vm = max(vm, float_to_ordered(fabsf(r.f.w)));
+    constexpr int kAB = 4;                       // anchors per batch: loads, slot atomics and stores grouped
+    for (int64_t mb = m0 + threadIdx.x; mb < m1; mb += kAB * blockDim.x) {
+      int key[kAB], slot[kAB];
+      bool ok[kAB];
+      Rec r[kAB];
+#pragma unroll
+      for (int q = 0; q < kAB; ++q) {
+        const int64_t m = mb + q * blockDim.x;
+        ok[q] = m < m1 && anchor_rec(m, x, t, b, anchors, anchor_xy, N, G, key[q], r[q]);
+      }
+#pragma unroll
+      for (int q = 0; q < kAB; ++q)
+        if (ok[q]) {
+          slot[q] = atomicAdd(hist + (key[q] >> G.bshift), 1);
+          if (!SCATTER) vm = max(vm, float_to_ordered(fabsf(r[q].f.w)));
+        }
+      if (SCATTER) {
+#pragma unroll
+        for (int q = 0; q < kAB; ++q)
+          if (ok[q]) trec[slot[q]] = r[q];
       }
     }
   }
