@@ -79,7 +79,7 @@ struct FParams {
 // One 32-byte record per sorted item, written with a single scattered line (separate arrays would cost one
 // scattered cache line each, and scattered lines are what the sort pays for):
 //   entries  f = (y.x, y.y, v.x, v.y) at the slice centre, i = (t bits, source id, key, 0)
-//   anchors  f = (x, y, t, at),                            i = (event id, input position, key, gS bits)
+//   anchors  f = (x, y, t, at),                            i = (event id, input position, key, cy << 16 | cx)
 //   sources  f = (x, y, v.x, v.y),                         i = (t bits, source id, key, 0)
 // key is the cell key within the item's own key space (the tmp records carry the combined key).
 struct Rec {
@@ -181,7 +181,7 @@ __device__ __forceinline__ bool anchor_rec(int64_t m, const float2* x, const flo
   const int cx = cell_walk(xa.x, G.gx0, G.gx1, G.icf, G.GW), cy = cell_walk(xa.y, G.gy0, G.gy1, G.icf, G.GH);
   key = G.ncell_pad + ((((int)ba * G.S + s) * G.GH + cy) * G.GW + cx);
   rec.f = make_float4(xa.x, xa.y, ta, ta - slice_centre(s, G.delta));
-  rec.i = make_int4((int)a, (int)m, key, 0);
+  rec.i = make_int4((int)a, (int)m, key, (cy << 16) | cx);
   return true;
 }
 
@@ -678,8 +678,8 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
 // (mine_n).  es is each anchor lane's own entry position: the leave-one-out test skips that candidate.
 template <int WD, bool COUNT>
 __device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plane, float x0, float x1, float y0,
-                                         float R, float R2, const float4& A, int es, int src0, int na, int lane,
-                                         float& mine, int& mine_n) {
+                                         float R, float R2, float vmax, const float4& A, int es, int src0, int na,
+                                         int lane, float& mine, int& mine_n) {
   float ax[WD], ay[WD], ta[WD], at[WD], acc[WD];
   int id[WD], cnt[WD];
 #pragma unroll
@@ -692,6 +692,16 @@ __device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plan
     id[a] = rdlane(es, src);
     acc[a] = 0.f;
     cnt[a] = 0;
+  }
+  {                                                // these anchors' own radius: vmax * max |at| over the pass
+    float atg = 0.f;
+#pragma unroll
+    for (int a = 0; a < WD; ++a) atg = fmaxf(atg, fabsf(at[a]));
+    const float rg = G.cuth * 1.000001f + vmax * atg * 1.000001f + 0.01f;
+    if (rg < R) {                                  // false for NaN / inf: keep the whole-slice walk
+      R = rg;
+      R2 = rg * rg;
+    }
   }
   struct Cand {
     float4 e;
@@ -744,6 +754,7 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
   search_radius(p.P, G, R, R2);
   R = unif(R);
   R2 = unif(R2);
+  const float vmax = unif(ordered_to_float(p.P->vmax));
   const bool have = lane < n;
   const int q = wbase + min(lane, n - 1);
   const Rec AR = p.arec[q];
@@ -758,9 +769,9 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
   while (todo) {
     const int i = __ffsll((unsigned long long)todo) - 1;
     const int gkey = rdlane(key, i);
-    const int g = gkey / plane_cells;
-    const int rem = gkey - g * plane_cells;
-    const int cy = rem / G.GW, cx = rem - cy * G.GW;
+    const int cyx = rdlane(ai.w, i);               // the group's cell, packed by the plan (no divisions)
+    const int cy = cyx >> 16, cx = cyx & 0xffff;
+    const int plane = gkey - (cy * G.GW + cx);
     // the group: anchors of up to kGroupCells consecutive cells of one row (lanes i .. i + gsize - 1)
     const int span = min(kGroupCells, G.GW - cx);
     const uint64_t gmask = __ballot(have && key >= gkey && key - gkey < span) & todo;
@@ -769,17 +780,16 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
     const int last_cx = cx + (rdlane(key, i + gsize - 1) - gkey);
     const float x0 = G.gx0 + (float)cx * G.cf, x1 = G.gx0 + (float)(last_cx + 1) * G.cf;
     const float y0 = G.gy0 + (float)cy * G.cf;
-    const int plane = g * plane_cells;
     for (int a0 = 0; a0 < gsize; a0 += kGroup) {
       const int na = min(kGroup, gsize - a0);
       if (na == 1)
-        fwd_pass<1, COUNT>(p, G, plane, x0, x1, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<1, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
       else if (na == 2)
-        fwd_pass<2, COUNT>(p, G, plane, x0, x1, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<2, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
       else if (na <= 4)
-        fwd_pass<4, COUNT>(p, G, plane, x0, x1, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<4, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
       else
-        fwd_pass<kGroup, COUNT>(p, G, plane, x0, x1, y0, R, R2, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<kGroup, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
     }
   }
   if (have) {
@@ -870,6 +880,15 @@ __global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, flo
   const Rec SR = p.srec[wbase + lane];
   const int4 si = SR.i;
   const float tj = __int_as_float(si.x);
+  // this source's own search radius: its entries all move with its own velocity, |v_j| * max|at| <= vmax * max|at|
+  {
+    const float vj = sqrtf(SR.f.z * SR.f.z + SR.f.w * SR.f.w);
+    const float rj = G.cuth * 1.000001f + vj * ordered_to_float(p.P->atmax) * 1.000001f + 0.01f;
+    if (rj < R) {                                  // false for NaN / inf velocities: keep the whole-slice walk
+      R = rj;
+      R2 = rj * rj;
+    }
+  }
   const int sp = p.self[si.y];
   int2* mytab = tab + threadIdx.x;
   const float2 m = uni(p.P->dup) ? bwd_source<true>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, mytab)
@@ -971,7 +990,9 @@ int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W
     if (nbuckets <= kMaxBuckets) break;
   }
   const double nblk = std::ceil((double)N / kSrcPerBlock) + std::ceil((double)M / kAncPerBlock);
-  if (3 * ncell_pad + 1 >= 2.0e9 || ecap + M + N >= 2.0e9 || nbuckets > kMaxBuckets || nbuckets * nblk + 1 >= 2.0e9) {
+  // GW, GH < 32768: anchor records pack (cy, cx) into 16-bit halves
+  if (3 * ncell_pad + 1 >= 2.0e9 || ecap + M + N >= 2.0e9 || nbuckets > kMaxBuckets || nbuckets * nblk + 1 >= 2.0e9 ||
+      g.GW >= 32768 || g.GH >= 32768) {
     set_error("fast_geometry_init: problem too large for the 32-bit plan (cells %.0f, entries %.0f)", ncell, ecap);
     return 1;
   }
