@@ -603,6 +603,22 @@ __device__ __forceinline__ void walk_flat(const int* __restrict__ cstart, int ba
 // general loop.
 constexpr int kRowTable = 8;
 
+// Candidate position of chunk index idx: idx plus the offset of the last row starting at or before idx
+// (e_k: row starts in the chunk numbering, o_k: row offsets); -1 past the last candidate.  All operands are
+// passed by value, so the select chain stays in registers.
+__device__ __forceinline__ int row_map(int idx, int total, int e1, int e2, int e3, int e4, int e5, int e6, int e7,
+                                       int o0, int o1, int o2, int o3, int o4, int o5, int o6, int o7) {
+  int off = o0;
+  off = idx >= e1 ? o1 : off;
+  off = idx >= e2 ? o2 : off;
+  off = idx >= e3 ? o3 : off;
+  off = idx >= e4 ? o4 : off;
+  off = idx >= e5 ? o5 : off;
+  off = idx >= e6 ? o6 : off;
+  off = idx >= e7 ? o7 : off;
+  return idx < total ? idx + off : -1;
+}
+
 template <typename Load, typename Use>
 __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int base, int plane, float x0, float x1,
                                            float y0, float y1, float R, float R2, const FGeo& G, Load&& load,
@@ -630,19 +646,18 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
     const int excl = incl - len;
     const int total = rdlane(incl, kWave - 1);
     if (nrb <= kRowTable) {
-      // lanes >= nrb hold len 0 and excl = total, so their entries never match a valid index
-      int ex[kRowTable], of[kRowTable];
-#pragma unroll
-      for (int k = 0; k < kRowTable; ++k) {
-        ex[k] = rdlane(excl, k);
-        of[k] = rdlane(s0 - excl, k);
-      }
-      auto map = [&](int c0) {
-        const int idx = c0 + lane;
-        int off = of[0];
-#pragma unroll
-        for (int k = 1; k < kRowTable; ++k) off = idx >= ex[k] ? of[k] : off;   // last row starting <= idx
-        return idx < total ? idx + off : -1;
+      // lanes >= nrb hold len 0 and excl = total, so their entries never match a valid index.  Row starts
+      // are scalars; row offsets are copied once into vector registers, so that each row of the select chain
+      // is one compare and one VCC select.  They are separate variables, not an array: a select chain over
+      // an array is folded into an indexed load from a table in private memory.
+      static_assert(kRowTable == 8, "the row table below has eight rows");
+#define ATL_ROW(k) const int e##k = rdlane(excl, k); int o##k; \
+      asm("v_mov_b32 %0, %1" : "=v"(o##k) : "s"(rdlane(s0 - excl, k)));
+      ATL_ROW(0) ATL_ROW(1) ATL_ROW(2) ATL_ROW(3) ATL_ROW(4) ATL_ROW(5) ATL_ROW(6) ATL_ROW(7)
+#undef ATL_ROW
+      (void)e0;
+      auto map = [=](int c0) {
+        return row_map(c0 + lane, total, e1, e2, e3, e4, e5, e6, e7, o0, o1, o2, o3, o4, o5, o6, o7);
       };
       int pos = map(0);
       auto cur = load(pos);
