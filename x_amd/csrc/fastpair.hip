@@ -23,7 +23,8 @@
 // bucket one workgroup that sorts it by cell with an LDS histogram and writes the cell offsets and the final
 // records.  Entries and anchors
 // share one key space (anchor keys offset by the padded cell count), so both sorts run in the same
-// launches.  The same sort also orders the sources by the cell of their own-slice position, and the
+// launches.  The same sort also orders the sources by the cell of their own-slice position (in tiles of
+// 8 x 8 cells, so that a wave's sources form a compact patch), and the
 // backward gives each source one lane that walks the anchors of all its slices: the gradient of a source
 // is complete in registers and written once, without atomics.
 #include "common.h"
@@ -166,6 +167,21 @@ __device__ __forceinline__ int entry_key(float2 xj, float2 vj, float tj, int bj,
   return ((bj * G.S + s) * G.GH + cy) * G.GW + cx;
 }
 
+// Sources are ordered by their own-slice cell in tile order: bands of kSrcTile cell rows, within a band tiles
+// of kSrcTile columns, within a tile row by row.  This is a bijection of the cells of a plane onto
+// [0, GH * GW) (partial tiles at the right and bottom edges included), so the key space is the entries' and
+// the plane index is still key / (GH * GW); 64 consecutive sources then cover a compact patch rather than a
+// strip of a row, which keeps a wave's neighbourhoods (and its staged anchors) small.
+constexpr int kSrcTile = 8;
+__device__ __forceinline__ int source_key(int key, const FGeo& G) {
+  const int pc = G.GH * G.GW;
+  const int plane = key / pc, rem = key - plane * pc;
+  const int cy = rem / G.GW, cx = rem - cy * G.GW;
+  const int band = cy / kSrcTile, ly = cy - band * kSrcTile, tx = cx / kSrcTile, lx = cx - tx * kSrcTile;
+  const int hb = min(kSrcTile, G.GH - band * kSrcTile), wt = min(kSrcTile, G.GW - tx * kSrcTile);
+  return plane * pc + band * kSrcTile * G.GW + tx * kSrcTile * hb + ly * wt + lx;
+}
+
 // Anchor m: slice floor(t / delta) clamped (functional.py:171), fine cell of its clamped position; the key
 // is offset by ncell_pad into the anchors' half of the key space.
 __device__ __forceinline__ bool anchor_rec(int64_t m, const float2* x, const float* t, const int64_t* b,
@@ -252,7 +268,7 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
         key[kSliceBatch] = -1;
 #pragma unroll
         for (int q = 0; q < kSliceBatch; ++q)
-          if (q == oq) key[kSliceBatch] = 2 * G.ncell_pad + key[q];
+          if (q == oq) key[kSliceBatch] = 2 * G.ncell_pad + source_key(key[q], G);
 #pragma unroll
         for (int q = 0; q <= kSliceBatch; ++q) {
           const bool live = q < kSliceBatch ? s0 + q <= hi : key[kSliceBatch] >= 0;
@@ -449,7 +465,7 @@ struct FPlan {
   const float* etim;           // entries in cell order: t
   const int* eself;            // per event: position of its own-slice entry, -1 if none
   const Rec* arec;             // anchors in cell order
-  const Rec* srec;             // sources in own-slice cell order
+  const Rec* srec;             // sources in own-slice cell order, tile by tile (source_key)
   float4* brec;                // anchors in cell order for the backward: (x, y, t, gS / h^2)
   int* self;                   // per event: position of its own anchor record, -1 if it is no anchor
   const int* start;            // 3*ncell_pad + 1: entry cells, anchor cells (offset by E), source cells
@@ -801,8 +817,12 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
         fwd_pass<1, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
       else if (na == 2)
         fwd_pass<2, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
-      else if (na <= 4)
+      else if (na == 3)
+        fwd_pass<3, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+      else if (na == 4)
         fwd_pass<4, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+      else if (na <= 6)
+        fwd_pass<6, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
       else
         fwd_pass<kGroup, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
     }
@@ -874,7 +894,7 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
   return make_float2(mgx, mgy);
 }
 
-// Backward: every source (one lane each, own-slice cell order) sums, over the anchors of each slice of its
+// Backward: every source (one lane each, own-slice tile order) sums, over the anchors of each slice of its
 // range within R of its slice-centre position, gS_i * k * dt / h^2 * r (csrc/atl_cpu.cpp:240-248);
 // gv[j] += the total (each source once: no atomics).
 __global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, float2* __restrict__ gv) {
