@@ -169,7 +169,8 @@ typedef struct atl_fast_geometry {
 
 int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W, int64_t S, double h, double tau,
                            double cut, atl_fast_geometry* geo);
-/* Plan: entries and anchors binned and sorted by (batch, slice, cell) in ws. */
+/* Plan: entries and anchors binned and sorted by (batch, slice, cell) in ws.  anchors may be null when M == N:
+ * every event is then its own anchor, in event order (the reference's anchors = arange(N)). */
 int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, const float* v, const int64_t* b,
                   const int64_t* anchors, const float* anchor_xy, void* ws, int64_t ws_bytes, hipStream_t stream);
 /* out (M) written for every valid anchor (zero-fill it first); count (M) int32 receives n_i when non-null. */
@@ -180,7 +181,8 @@ int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, f
 /* ---------------------------------------------------------------- anchored-score pieces */
 
 /* window_counts (atl/ops/functional.py:210-217): out (M) written.  Requires keys b*4 + t ascending in event
- * order (the EventPacket invariant, atl/core/events.py:11-12); atl_check_sorted tests it (flag = 1 if not). */
+ * order (the EventPacket invariant, atl/core/events.py:11-12); atl_check_sorted tests it (flag = 1 if not).
+ * idx may be null (M <= N): the first M events, in order. */
 int atl_window_counts(const float* t, const int64_t* b, int64_t N, const int64_t* idx, int64_t M, double tau,
                       float* out, hipStream_t stream);
 int atl_check_sorted(const float* t, const int64_t* b, int64_t N, int* flag, hipStream_t stream);
@@ -199,6 +201,17 @@ int atl_anchored_epilogue_fwd(const float* S, const float* wc, const float* vis,
                               double eps, float* ls, float* q, float* D, hipStream_t stream);
 int atl_anchored_epilogue_bwd(const float* g, const float* q, const float* D, int64_t M, float* gS,
                               hipStream_t stream);
+/* The epilogue fused with the loss of atl/objectives/ats.py:102-105: out[0] = -mean_i ls_i (the loss),
+ * out[1] = mean_i ls_i (the score), q and D saved as above; the mean is summed in double in a fixed order
+ * (deterministic).  scratch: atl_anchored_score_mean_scratch_bytes() bytes, zero before the first call; every
+ * call leaves it zero again, and calls that share one scratch must not overlap.  The backward takes the loss
+ * gradient g (1 float on the device): gS = (((-g) / M) / q) / D, the chain of the negation, the mean and the
+ * epilogue. */
+int64_t atl_anchored_score_mean_scratch_bytes(void);
+int atl_anchored_score_mean_fwd(const float* S, const float* wc, const float* vis, int64_t M, double h, double eps,
+                                float* q, float* D, void* scratch, float* out, hipStream_t stream);
+int atl_anchored_score_mean_bwd(const float* g, const float* q, const float* D, int64_t M, float* gS,
+                                hipStream_t stream);
 
 #ifdef __cplusplus
 }

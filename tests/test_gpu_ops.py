@@ -316,6 +316,49 @@ def test_anchored_exact_end_to_end():
     close_rel(N(m.grid.grad), ggrid, 1e-4)
 
 
+def test_anchored_exact_fused_loss():
+    """The objective's loss (epilogue, mean and negation fused in one launch, double sum in a fixed order) and
+    its flow-grid gradient vs the oracle pipeline; score = -loss."""
+    from x_amd.core import EventPacket
+    from x_amd.motion import DenseLinearFlow
+    from x_amd.objectives import AnchoredExact
+    win = synth.small_window(seed=8, n=4000, B=2)
+    H, W = win.height, win.width
+    ev = EventPacket.from_window(win, DEV)
+    grid = win.motion["grid"]
+    m = DenseLinearFlow(2, H, W, grid=grid.shape[-2:], init=torch.as_tensor(grid)).to(DEV)
+    out = AnchoredExact(h=1.0, tau=0.2, n_anchors=None, seed=0, n_slices=16)(ev, m)
+    out["loss"].backward()
+    assert float(out["score"]) == -float(out["loss"]) and not out["score"].requires_grad
+    g = torch.Generator().manual_seed(0)
+    xs = win.xy + (torch.rand(win.xy.shape, generator=g).numpy() - F32(0.5))
+    xa = xs + F32(1.0) * torch.randn(xs.shape, generator=g).numpy()
+    v, idx, wts = O.dense_velocity(grid, xs, win.b, H, W)
+    p = O.build_pair_plan(xs, win.t, v, win.b, 2, H, W, np.arange(win.n), 1.0, 0.2, 3.0, 16, anchor_xy=xa)
+    Sv = O.ats_pair_fwd(p, 1.0, 0.2, 3.0)
+    wc = O.window_counts(win.t, win.b, np.arange(win.n), 0.2)
+    vis = O.visible_fraction_dense(grid, xa, win.t, win.b, win.t, win.b, 2, H, W, 0.2)
+    want, gS, _ = O.anchored_epilogue(Sv, wc, 1.0, H, W, vis=vis)
+    loss = -float(np.mean(want.astype(np.float64)))
+    assert abs(float(out["loss"]) - loss) <= 1e-5 * abs(loss)
+    gv = O.ats_pair_bwd(gS, p, 1.0, 0.2, 3.0, win.n)
+    close_rel(N(m.grid.grad), O.sample_grid_bwd(gv, idx, wts, grid.shape), 1e-4)
+
+
+def test_window_counts_and_pair_sums_without_index():
+    """anchors=None (every event, in order) gives the same window counts and pair sums as anchors=arange(N)
+    (the sums to the last bits only: the order of the records within a cell, and so the summation order, is set
+    by LDS atomics in the sort)."""
+    pos, _, bb, tt = rand_events(seed=5, n=5000, B=2, H=30, W=40)
+    t, b, x = T(tt), T(bb), T(pos)
+    v = torch.randn(x.shape, device=DEV)
+    ar = torch.arange(x.shape[0], device=DEV)
+    assert torch.equal(F.window_counts(t, b, None, 0.2), F.window_counts(t, b, ar, 0.2))
+    s0 = F.ats_pair_sums(x, t, v, b, 2, 30, 40, None, 1.0, 0.2)
+    s1 = F.ats_pair_sums(x, t, v, b, 2, 30, 40, ar, 1.0, 0.2)
+    close_rel(N(s0), N(s1), 1e-6)
+
+
 # ------------------------------------------------------------------------------------------- full size
 def test_full_size_splat_gather_properties():
     """1M events at 640x480 (dense flow, warp to t_ref = 0.5): mass conservation of the splat and the adjoint

@@ -187,7 +187,7 @@ __device__ __forceinline__ int source_key(int key, const FGeo& G) {
 __device__ __forceinline__ bool anchor_rec(int64_t m, const float2* x, const float* t, const int64_t* b,
                                            const int64_t* anchors, const float2* anchor_xy, int64_t N,
                                            const FGeo& G, int& key, Rec& rec) {
-  const int64_t a = anchors[m];
+  const int64_t a = anchors ? anchors[m] : m;     // no index array: every event is its own anchor
   if (a < 0 || a >= N) return false;
   const int64_t ba = b[a];
   if (ba < 0 || ba >= G.B) return false;
@@ -207,10 +207,6 @@ __global__ void __launch_bounds__(kBlock) k_fill_zero(int* __restrict__ p, int64
   if (i < n) p[i] = 0;
 }
 
-__global__ void __launch_bounds__(kBlock) k_fill_i32(int* __restrict__ p, int64_t n, int v) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
-}
 
 // Pass 1.  Blocks [0, nblk_e) cover kSrcPerBlock sources each (their entries and one source record keyed
 // by the cell of the own-slice entry), blocks [nblk_e, nblk_e + nblk_a) kAncPerBlock anchors each.
@@ -224,7 +220,8 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
                                                        int64_t N, const int64_t* __restrict__ anchors,
                                                        const float2* __restrict__ anchor_xy, int64_t M, FGeo G,
                                                        int* __restrict__ cnt, Rec* __restrict__ trec,
-                                                       FParams* __restrict__ P) {
+                                                       FParams* __restrict__ P, int* __restrict__ self,
+                                                       int* __restrict__ eself) {
   extern __shared__ int hist[];
   __shared__ int red[kP1Block / kWave];
   int vm = 0;                                    // this thread's max ||v|| (sources) or max |at| (anchors)
@@ -246,6 +243,10 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
         tj[u] = t[j];
         xj[u] = x[j];
         vj[u] = v[j];
+        if (!SCATTER) {                            // "no anchor record" / "no own-slice entry" until pass 2
+          self[j] = -1;
+          eself[j] = -1;
+        }
       }
     }
 #pragma unroll
@@ -1063,7 +1064,7 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
   if (!make_geo(geo, G)) { set_error("fast_plan: geometry not initialised by atl_fast_geometry_init"); return 1; }
   if (!ws || ws_bytes < geo->ws_bytes) { set_error("fast_plan: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)geo->ws_bytes); return 1; }
   const int64_t N = geo->N, M = geo->M;
-  if ((N > 0 && (!x || !t || !v || !b)) || (M > 0 && !anchors)) { set_error("fast_plan: null input"); return 1; }
+  if ((N > 0 && (!x || !t || !v || !b)) || (M > 0 && !anchors && M != N)) { set_error("fast_plan: null input"); return 1; }
   FParams* P = at_off<FParams>(ws, geo->off_params);
   int* cnt = at_off<int>(ws, geo->off_cnt);
   int* boff = at_off<int>(ws, geo->off_boff);
@@ -1075,17 +1076,14 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
   const size_t lds = (size_t)G.nbuckets * sizeof(int);
   if (nblk > 0) {
     hipLaunchKernelGGL(k_sort_pass1<false>, dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
-                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, (Rec*)nullptr, P);
+                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, (Rec*)nullptr, P,
+                       at_off<int>(ws, geo->off_self), at_off<int>(ws, geo->off_eself));
     scan32(cnt, nbh, part, boff, stream);
     hipLaunchKernelGGL(k_sort_pass1<true>, dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
-                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, boff, trec, (FParams*)nullptr);
+                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, boff, trec, (FParams*)nullptr,
+                       (int*)nullptr, (int*)nullptr);
   } else {
     hipLaunchKernelGGL(k_fill_zero, dim3(1), dim3(64), 0, stream, boff, (int64_t)1);
-  }
-  if (N > 0) {
-    hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(N)), dim3(kBlock), 0, stream, at_off<int>(ws, geo->off_self), N, -1);
-    hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(N)), dim3(kBlock), 0, stream, at_off<int>(ws, geo->off_eself), N,
-                       -1);
   }
   auto pass2 = G.bshift == 10 ? k_sort_pass2<10> : G.bshift == 11 ? k_sort_pass2<11>
              : G.bshift == 12 ? k_sort_pass2<12> : k_sort_pass2<13>;

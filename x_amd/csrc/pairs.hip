@@ -9,6 +9,7 @@
 #include "common.h"
 #include "../../include/atl_hip.h"
 
+#include <algorithm>
 #include <cmath>
 
 using namespace atlhip;
@@ -322,7 +323,7 @@ __global__ void __launch_bounds__(kBlock) k_window_counts(const float* __restric
                                                           float* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= M) return;
-  const int64_t a = idx[i];
+  const int64_t a = idx ? idx[i] : i;            // no index array: every event in order
   if (a < 0 || a >= N) { out[i] = 0.f; return; }
   const double ki = bt_key(t, b, a);
   const double lo_v = ki - tau, hi_v = ki + tau;
@@ -416,6 +417,71 @@ __global__ void __launch_bounds__(kBlock) k_epilogue_fwd(const float* __restrict
   ls[i] = logf(qq);
   q[i] = qq;
   D[i] = d;
+}
+
+// The same epilogue fused with the loss: out = (-mean_i ls_i, mean_i ls_i) (atl/objectives/ats.py:102-105), q and D
+// saved.  The mean is deterministic: each block adds its terms in double and stores the partial in part[block];
+// the last block to finish (ticket counter, which it resets to zero) adds the partials in block order.
+constexpr int kMeanBlocks = 1024;
+
+__device__ __forceinline__ double block_sum_d(double v, double* red) {
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_down(v, o);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double tot = 0.0;
+  if (threadIdx.x == 0)
+    for (int w = 0; w < kBlock / 64; ++w) tot += red[w];
+  __syncthreads();
+  return tot;                                    // valid in thread 0
+}
+
+__global__ void __launch_bounds__(kBlock) k_epilogue_mean(const float* __restrict__ S, const float* __restrict__ wc,
+                                                          const float* __restrict__ vis, int64_t M, float pi_f,
+                                                          float hh, float eps, float* __restrict__ q,
+                                                          float* __restrict__ D, double* __restrict__ part,
+                                                          unsigned* __restrict__ ticket, float* __restrict__ out) {
+  __shared__ double red[kBlock / 64];
+  __shared__ bool last;
+  double acc = 0.0;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < M; i += stride) {
+    float wn = fmaxf(wc[i], 1.f);
+    if (vis) wn = wn * vis[i];
+    const float d = ((wn * 2.f) * pi_f) * hh;
+    const float qq = eps + S[i] / d;
+    acc += (double)logf(qq);
+    q[i] = qq;
+    D[i] = d;
+  }
+  const double bs = block_sum_d(acc, red);
+  if (threadIdx.x == 0) {
+    part[blockIdx.x] = bs;
+    __threadfence();
+    last = atomicAdd(ticket, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  double t = 0.0;                                // partials in block order: thread k adds k, k + 256, ...
+  for (int k = threadIdx.x; k < (int)gridDim.x; k += kBlock) t += ((volatile double*)part)[k];
+  const double tot = block_sum_d(t, red);
+  if (threadIdx.x == 0) {
+    const float mean = (float)(tot / (double)M);
+    out[0] = -mean;
+    out[1] = mean;
+    *ticket = 0u;
+  }
+}
+
+// Backward of the fused loss: d loss / d ls_i = (-g) / M (the gradients of the negation and of the mean), then
+// gS = (that / q) / D.
+__global__ void __launch_bounds__(kBlock) k_epilogue_mean_bwd(const float* __restrict__ g, const float* __restrict__ q,
+                                                              const float* __restrict__ D, int64_t M,
+                                                              float* __restrict__ gS) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M) return;
+  const float gl = (-g[0]) / (float)M;
+  gS[i] = (gl / q[i]) / D[i];
 }
 
 __global__ void __launch_bounds__(kBlock) k_epilogue_bwd(const float* __restrict__ g, const float* __restrict__ q,
@@ -574,7 +640,7 @@ int atl_ats_pair_bwd(const float* gS, const float* src_y, const float* src_v, co
 
 int atl_window_counts(const float* t, const int64_t* b, int64_t N, const int64_t* idx, int64_t M, double tau,
                       float* out, hipStream_t stream) {
-  if (N < 0 || M < 0) { set_error("window_counts: bad sizes"); return 1; }
+  if (N < 0 || M < 0 || (!idx && M > N)) { set_error("window_counts: bad sizes"); return 1; }
   if (M == 0) return 0;
   hipLaunchKernelGGL(k_window_counts, dim3(grid_for(M)), dim3(kBlock), 0, stream, t, b, N, idx, M, tau, out);
   return check_launch("window_counts");
@@ -623,6 +689,29 @@ int atl_anchored_epilogue_bwd(const float* g, const float* q, const float* D, in
   if (M == 0) return 0;
   hipLaunchKernelGGL(k_epilogue_bwd, dim3(grid_for(M)), dim3(kBlock), 0, stream, g, q, D, M, gS);
   return check_launch("anchored_epilogue_bwd");
+}
+
+int64_t atl_anchored_score_mean_scratch_bytes(void) { return (int64_t)kMeanBlocks * 8 + 256; }
+
+int atl_anchored_score_mean_fwd(const float* S, const float* wc, const float* vis, int64_t M, double h, double eps,
+                                float* q, float* D, void* scratch, float* out, hipStream_t stream) {
+  if (M < 0 || !scratch || !out || (M > 0 && (!S || !wc || !q || !D))) {
+    set_error("anchored_score_mean_fwd: bad arguments");
+    return 1;
+  }
+  const unsigned grid = M > 0 ? std::min(grid_for(M), (unsigned)kMeanBlocks) : 1u;
+  hipLaunchKernelGGL(k_epilogue_mean, dim3(grid), dim3(kBlock), 0, stream, S, wc, vis, M, (float)M_PI,
+                     (float)(h * h), (float)eps, q, D, (double*)scratch, (unsigned*)((char*)scratch + kMeanBlocks * 8),
+                     out);
+  return check_launch("anchored_score_mean_fwd");
+}
+
+int atl_anchored_score_mean_bwd(const float* g, const float* q, const float* D, int64_t M, float* gS,
+                                hipStream_t stream) {
+  if (M < 0 || !g) { set_error("anchored_score_mean_bwd: bad arguments"); return 1; }
+  if (M == 0) return 0;
+  hipLaunchKernelGGL(k_epilogue_mean_bwd, dim3(grid_for(M)), dim3(kBlock), 0, stream, g, q, D, M, gS);
+  return check_launch("anchored_score_mean_bwd");
 }
 
 }  // extern "C"

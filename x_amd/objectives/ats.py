@@ -21,7 +21,7 @@ from typing import Optional
 import torch
 
 from ..core.events import EventPacket
-from ..ops import anchored_log_scores, ats_pair_sums, gather, splat, visible_fraction_linear, window_counts
+from ..ops import anchored_log_scores, anchored_score_mean, ats_pair_sums, gather, splat, visible_fraction_linear, window_counts
 from .base import Objective
 
 
@@ -51,9 +51,10 @@ def visible_fraction(motion, xa, ta, ba, ev: EventPacket, tau: float, n_check: i
     return (vis / tot.clamp(min=1)).clamp(min=1e-3)
 
 
-def _pick_anchors(ev: EventPacket, n_anchors: Optional[int], gen: Optional[torch.Generator]) -> torch.Tensor:
+def _pick_anchors(ev: EventPacket, n_anchors: Optional[int], gen: Optional[torch.Generator]):
+    """Anchor indices, or None for every event in order (no index array is then built or gathered through)."""
     if n_anchors is None or n_anchors >= ev.n:
-        return torch.arange(ev.n, device=ev.device)
+        return None
     idx = torch.randperm(ev.n, generator=gen, device="cpu")[:n_anchors].to(ev.device)
     return torch.sort(idx).values
 
@@ -77,50 +78,73 @@ class AnchoredExact(Objective):
         self.gen = torch.Generator().manual_seed(seed) if seed is not None else None
         self._dgen = None
 
-    def _noise(self, shape, like: torch.Tensor, kind: str) -> torch.Tensor:
+    def _noise(self, shape, like: torch.Tensor, kind: str, scale: float = 1.0) -> torch.Tensor:
+        """Dequantisation noise U(-1/2, 1/2) (kind "uniform") or smoothing noise N(0, scale^2) ("normal").  From
+        the CPU generator the reference's ops are kept (rand - 0.5, scale * randn); on the device each draw is
+        one in-place fill of the target distribution."""
         if self.rng == "device" and like.is_cuda:
             if self._dgen is None:
                 self._dgen = torch.Generator(device=like.device)
                 self._dgen.manual_seed(self.seed if self.seed is not None else torch.seed())
-            f = torch.rand if kind == "uniform" else torch.randn
-            return f(shape, generator=self._dgen, device=like.device, dtype=like.dtype)
-        f = torch.rand if kind == "uniform" else torch.randn
-        return f(shape, generator=self.gen).to(like)
+            out = torch.empty(shape, device=like.device, dtype=like.dtype)
+            if kind == "uniform":
+                return out.uniform_(-0.5, 0.5, generator=self._dgen)
+            return out.normal_(0.0, scale, generator=self._dgen)
+        if kind == "uniform":
+            return torch.rand(shape, generator=self.gen).to(like) - 0.5
+        return scale * torch.randn(shape, generator=self.gen).to(like)
 
     def log_scores(self, ev: EventPacket, motion, anchors: Optional[torch.Tensor] = None):
         """Per-anchor log predictive densities and the anchor indices (atl/objectives/ats.py:75-96)."""
+        parts, anchors = self._terms(ev, motion, anchors)
+        if anchors is None:
+            anchors = torch.arange(ev.n, device=ev.device)
+        if ev.xy.is_cuda:
+            S, wc, vis, eps = parts
+            return anchored_log_scores(S, wc, vis, self.h, eps), anchors
+        return parts, anchors
+
+    def _terms(self, ev: EventPacket, motion, anchors: Optional[torch.Tensor] = None):
+        """On device: (S, window counts, visible fraction or None, eps) for the epilogue; on the CPU the log
+        scores themselves."""
         if not getattr(motion, "linear_at_event", False):
             raise ValueError("AnchoredExact needs a motion that is linear at the event")
         if anchors is None:
             anchors = _pick_anchors(ev, self.n_anchors, self.gen)
             if self.anchor_margin > 0:
+                if anchors is None:
+                    anchors = torch.arange(ev.n, device=ev.device)
                 anchors = anchors[ev.inside(ev.xy[anchors], margin=-self.anchor_margin)]
+        pick = (lambda a: a) if anchors is None else (lambda a: a[anchors])   # None: every event, in order
         xs = ev.xy
         if self.dequantize:
-            xs = xs + (self._noise(xs.shape, xs, "uniform") - 0.5)
-        xa = xs[anchors]
+            xs = xs + self._noise(xs.shape, xs, "uniform")
+        xa = pick(xs)
         if self.smooth_anchors:
-            xa = xa + self.h * self._noise(xa.shape, xa, "normal")
+            xa = xa + self._noise(xa.shape, xa, "normal", self.h)
         v = motion.velocity(xs, ev.t, ev.b)
         S = ats_pair_sums(xs, ev.t, v, ev.b, ev.batch_size, ev.height, ev.width, anchors, self.h, self.tau,
                           self.cut, self.n_slices, anchor_xy=xa)
         eps = self.eps_frac / (ev.height * ev.width)
         if ev.xy.is_cuda:
             wc = window_counts(ev.t, ev.b, anchors, self.tau, assume_sorted=ev.meta.get("sorted"))
-            vis = (visible_fraction(motion, xa.detach(), ev.t[anchors], ev.b[anchors], ev, self.tau)
+            vis = (visible_fraction(motion, xa.detach(), pick(ev.t), pick(ev.b), ev, self.tau)
                    if self.visibility else None)
-            return anchored_log_scores(S, wc, vis, self.h, eps), anchors
+            return (S, wc, vis, eps), anchors
         Wn = window_counts(ev.t, ev.b, anchors, self.tau).clamp(min=1)
         if self.visibility:
-            Wn = Wn * visible_fraction(motion, xa.detach(), ev.t[anchors], ev.b[anchors], ev, self.tau)
+            Wn = Wn * visible_fraction(motion, xa.detach(), pick(ev.t), pick(ev.b), ev, self.tau)
         return torch.log(eps + S / (Wn * 2 * math.pi * self.h ** 2)), anchors
 
     def set_bandwidth(self, h: float):
         self.h = float(h)
 
     def __call__(self, ev, motion):
-        ls, _ = self.log_scores(ev, motion)
-        s = ls.mean()
+        parts, _ = self._terms(ev, motion)
+        if ev.xy.is_cuda:                          # epilogue, mean and negation in one launch
+            loss, score = anchored_score_mean(*parts[:3], self.h, parts[3])
+            return {"loss": loss, "score": score}
+        s = parts.mean()
         return {"loss": -s, "score": s.detach()}
 
 

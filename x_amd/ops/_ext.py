@@ -55,6 +55,9 @@ _SIGS = {
     "atl_visible_fraction": [_P, _P, _P, _P, _I, _P, _P, _I, _I, _D, _I, _I, _P, _P],
     "atl_anchored_epilogue_fwd": [_P, _P, _P, _I, _D, _D, _P, _P, _P, _P],
     "atl_anchored_epilogue_bwd": [_P, _P, _P, _I, _P, _P],
+    "atl_anchored_score_mean_scratch_bytes": [],
+    "atl_anchored_score_mean_fwd": [_P, _P, _P, _I, _D, _D, _P, _P, _P, _P, _P],
+    "atl_anchored_score_mean_bwd": [_P, _P, _P, _I, _P, _P],
     "atl_grid_plan_bytes": [_I, _I, _I, _I],
     "atl_tile_ws_bytes": [_I, _I, _I, _I],
     "atl_splat_gauss_ws_bytes": [_I, _I, _I, _I, _I],
@@ -69,7 +72,8 @@ _SIGS = {
     "atl_fast_pair_bwd": [_P, _P, _P, _P, _P],
 }
 _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.c_int64,
-            "atl_tile_ws_bytes": ctypes.c_int64, "atl_splat_gauss_ws_bytes": ctypes.c_int64, "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
+            "atl_tile_ws_bytes": ctypes.c_int64, "atl_splat_gauss_ws_bytes": ctypes.c_int64,
+            "atl_anchored_score_mean_scratch_bytes": ctypes.c_int64, "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):
     """Mirror of ``atl_fast_geometry`` (include/atl_hip.h): sizes, grid and workspace layout of the fused

@@ -372,9 +372,11 @@ class FastPairPlan:
     def __init__(self, x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, anchor_xy=None):
         dev = x.device
         self.x, self.t, self.v = _f32(x), _f32(t), _f32(v.detach())
-        self.b, self.anchors = b.contiguous().long(), anchors.contiguous().long()
+        self.b = b.contiguous().long()
+        self.anchors = None if anchors is None else anchors.contiguous().long()   # None: every event, in order
         self.anchor_xy = None if anchor_xy is None else _f32(anchor_xy.detach())
-        N, M = self.t.shape[0], self.anchors.shape[0]
+        N = self.t.shape[0]
+        M = N if self.anchors is None else self.anchors.shape[0]
         if self.x.shape != (N, 2) or self.v.shape != (N, 2) or self.b.shape != (N,):
             raise ValueError("x, v must be (N, 2) and t, b (N,)")
         if self.anchor_xy is not None and self.anchor_xy.shape != (M, 2):
@@ -430,9 +432,11 @@ class _ATSPairFast(torch.autograd.Function):
 def ats_pair_sums(x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, force_ref=False, anchor_xy=None):
     """S_i = sum_{j != i} 1[|t_i - t_j| <= tau] exp(-|x_i - x_j - v_j (t_i - t_j)|^2 / 2h^2) for anchors i
     (atl/ops/functional.py:199-207).  ``x`` are raw event positions, ``v`` per-event velocities in px per
-    window; the gradient flows to ``v`` only.  Device tensors run the fused HIP path (same contributing pairs
+    window; the gradient flows to ``v`` only.  ``anchors=None`` means every event, in order.  Device tensors run the fused HIP path (same contributing pairs
     as the reference's plan + kernel, no host synchronisation)."""
     if force_ref or not ext_supports(x):
+        if anchors is None:
+            anchors = torch.arange(x.shape[0], device=x.device)
         return ref.ats_pair_sums(x.float(), t.float(), v.float(), b, anchors, h, tau, cut, anchor_xy=anchor_xy)
     get_ext()
     return _ATSPairFast.apply(v.float(), x.detach(), t.detach(), b, anchors, anchor_xy, int(B), int(H), int(W),
@@ -460,7 +464,8 @@ def events_sorted(t: torch.Tensor, b: torch.Tensor) -> bool:
 
 def window_counts(t: torch.Tensor, b: torch.Tensor, idx: torch.Tensor, tau: float,
                   assume_sorted: Optional[bool] = None) -> torch.Tensor:
-    """#{j != i, same batch, |t_j - t_i| <= tau} for i in idx (atl/ops/functional.py:210-217).
+    """#{j != i, same batch, |t_j - t_i| <= tau} for i in idx (atl/ops/functional.py:210-217); ``idx=None``
+    means every event, in order.
 
     Device path: binary searches over the float64 keys b*4 + t in event order, which the EventPacket
     invariant (sorted by (b, t)) keeps ascending; ``assume_sorted=None`` verifies that first, an unsorted
@@ -468,24 +473,27 @@ def window_counts(t: torch.Tensor, b: torch.Tensor, idx: torch.Tensor, tau: floa
     if not t.is_cuda:
         key = b.double() * 4.0 + t.double()
         ks, _ = torch.sort(key)
-        ki = key[idx]
+        ki = key if idx is None else key[idx]
         lo = torch.searchsorted(ks, ki - tau, right=False)
         hi = torch.searchsorted(ks, ki + tau, right=True)
         return (hi - lo - 1).clamp(min=0).to(t.dtype)
     get_ext()
-    t, b, idx = _f32(t), b.contiguous().long(), idx.contiguous().long()
+    t, b = _f32(t), b.contiguous().long()
     if assume_sorted is None:
         assume_sorted = events_sorted(t, b)
+    if idx is None and not assume_sorted:
+        idx = torch.arange(t.shape[0], device=t.device)
+    idx = None if idx is None else idx.contiguous().long()
     if not assume_sorted:
         key = b.double() * 4.0 + t.double()
         order = torch.argsort(key, stable=True)
         inv = torch.empty_like(order)
         inv[order] = torch.arange(order.numel(), device=order.device)
         t, b, idx = t[order].contiguous(), b[order].contiguous(), inv[idx].contiguous()
-    out = torch.empty(idx.shape[0], dtype=F32, device=t.device)
+    M = t.shape[0] if idx is None else idx.shape[0]
+    out = torch.empty(M, dtype=F32, device=t.device)
     with torch.cuda.device(t.device):
-        call("atl_window_counts", ptr(t), ptr(b), t.shape[0], ptr(idx), idx.shape[0], float(tau), ptr(out),
-             stream_of(t))
+        call("atl_window_counts", ptr(t), ptr(b), t.shape[0], ptr(idx), M, float(tau), ptr(out), stream_of(t))
     return out
 
 
@@ -550,6 +558,56 @@ def anchored_log_scores(S, wc, vis, h, eps):
     """Device log-score epilogue (gradient to S only)."""
     get_ext()
     return _AnchoredEpilogue.apply(S, wc, vis, h, eps)
+
+
+_MEAN_SCRATCH = {}   # (device, stream) -> zeroed scratch of the fused loss (every call leaves it zero)
+
+
+def _mean_scratch(dev, stream):
+    key = (dev, getattr(stream, "value", stream))
+    buf = _MEAN_SCRATCH.get(key)
+    if buf is None:
+        nbytes = int(load_library().atl_anchored_score_mean_scratch_bytes())
+        buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        _MEAN_SCRATCH[key] = buf
+    return buf
+
+
+class _AnchoredScoreMean(torch.autograd.Function):
+    """loss = -mean_i log(eps + S_i / (Wn_i 2 pi h^2)) and the score = -loss in one launch
+    (atl/objectives/ats.py:92-105); gradient to S only."""
+
+    @staticmethod
+    def forward(ctx, S, wc, vis, h, eps):
+        S, wc = _f32(S), _f32(wc)
+        vis = None if vis is None else _f32(vis)
+        M = S.shape[0]
+        q, D = (torch.empty(M, dtype=F32, device=S.device) for _ in range(2))
+        out = torch.empty(2, dtype=F32, device=S.device)
+        st = stream_of(S)
+        with torch.cuda.device(S.device):
+            call("atl_anchored_score_mean_fwd", ptr(S), ptr(wc), ptr(vis), M, float(h), float(eps), ptr(q), ptr(D),
+                 ptr(_mean_scratch(S.device, st)), ptr(out), st)
+        ctx.save_for_backward(q, D)
+        loss, score = out[0], out[1]
+        ctx.mark_non_differentiable(score)
+        return loss, score
+
+    @staticmethod
+    def backward(ctx, g, _gscore):
+        q, D = ctx.saved_tensors
+        gS = torch.empty_like(q)
+        g = g.contiguous().float()
+        with torch.cuda.device(q.device):
+            call("atl_anchored_score_mean_bwd", ptr(g), ptr(q), ptr(D), q.shape[0], ptr(gS), stream_of(q))
+        return gS, None, None, None, None
+
+
+def anchored_score_mean(S, wc, vis, h, eps):
+    """Device loss of the anchored score: (loss, score) with loss = -mean log-score (differentiable w.r.t. S)
+    and score = -loss (detached)."""
+    get_ext()
+    return _AnchoredScoreMean.apply(S, wc, vis, h, eps)
 
 
 # ------------------------------------------------------------------------------------------- voxel grid
