@@ -203,8 +203,8 @@ int atl_anchored_epilogue_bwd(const float* g, const float* q, const float* D, in
                               hipStream_t stream);
 /* The epilogue fused with the loss of atl/objectives/ats.py:102-105: out[0] = -mean_i ls_i (the loss),
  * out[1] = mean_i ls_i (the score), q and D saved as above; the mean is summed in double in a fixed order
- * (deterministic).  scratch: atl_anchored_score_mean_scratch_bytes() bytes, zero before the first call; every
- * call leaves it zero again, and calls that share one scratch must not overlap.  The backward takes the loss
+ * (deterministic, two launches).  scratch: atl_anchored_score_mean_scratch_bytes() bytes of device memory for the
+ * per-block partial sums (no initial contents needed).  The backward takes the loss
  * gradient g (1 float on the device): gS = (((-g) / M) / q) / D, the chain of the negation, the mean and the
  * epilogue. */
 int64_t atl_anchored_score_mean_scratch_bytes(void);

@@ -421,7 +421,8 @@ __global__ void __launch_bounds__(kBlock) k_epilogue_fwd(const float* __restrict
 
 // The same epilogue fused with the loss: out = (-mean_i ls_i, mean_i ls_i) (atl/objectives/ats.py:102-105), q and D
 // saved.  The mean is deterministic: each block adds its terms in double and stores the partial in part[block];
-// the last block to finish (ticket counter, which it resets to zero) adds the partials in block order.
+// a second one-block launch adds the partials in block order (a launch boundary orders the two; a ticket in
+// one launch would need a device-scope fence per block, which writes back the whole L2 of its XCD).
 constexpr int kMeanBlocks = 1024;
 
 __device__ __forceinline__ double block_sum_d(double v, double* red) {
@@ -438,10 +439,8 @@ __device__ __forceinline__ double block_sum_d(double v, double* red) {
 __global__ void __launch_bounds__(kBlock) k_epilogue_mean(const float* __restrict__ S, const float* __restrict__ wc,
                                                           const float* __restrict__ vis, int64_t M, float pi_f,
                                                           float hh, float eps, float* __restrict__ q,
-                                                          float* __restrict__ D, double* __restrict__ part,
-                                                          unsigned* __restrict__ ticket, float* __restrict__ out) {
+                                                          float* __restrict__ D, double* __restrict__ part) {
   __shared__ double red[kBlock / 64];
-  __shared__ bool last;
   double acc = 0.0;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < M; i += stride) {
@@ -454,22 +453,19 @@ __global__ void __launch_bounds__(kBlock) k_epilogue_mean(const float* __restric
     D[i] = d;
   }
   const double bs = block_sum_d(acc, red);
-  if (threadIdx.x == 0) {
-    part[blockIdx.x] = bs;
-    __threadfence();
-    last = atomicAdd(ticket, 1u) == gridDim.x - 1;
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  double t = 0.0;                                // partials in block order: thread k adds k, k + 256, ...
-  for (int k = threadIdx.x; k < (int)gridDim.x; k += kBlock) t += ((volatile double*)part)[k];
+  if (threadIdx.x == 0) part[blockIdx.x] = bs;
+}
+
+__global__ void __launch_bounds__(kBlock) k_epilogue_mean_total(const double* __restrict__ part, int nparts,
+                                                                int64_t M, float* __restrict__ out) {
+  __shared__ double red[kBlock / 64];
+  double t = 0.0;                                // thread k adds partials k, k + 256, ... in order
+  for (int k = threadIdx.x; k < nparts; k += kBlock) t += part[k];
   const double tot = block_sum_d(t, red);
   if (threadIdx.x == 0) {
     const float mean = (float)(tot / (double)M);
     out[0] = -mean;
     out[1] = mean;
-    *ticket = 0u;
   }
 }
 
@@ -691,7 +687,7 @@ int atl_anchored_epilogue_bwd(const float* g, const float* q, const float* D, in
   return check_launch("anchored_epilogue_bwd");
 }
 
-int64_t atl_anchored_score_mean_scratch_bytes(void) { return (int64_t)kMeanBlocks * 8 + 256; }
+int64_t atl_anchored_score_mean_scratch_bytes(void) { return (int64_t)kMeanBlocks * 8; }
 
 int atl_anchored_score_mean_fwd(const float* S, const float* wc, const float* vis, int64_t M, double h, double eps,
                                 float* q, float* D, void* scratch, float* out, hipStream_t stream) {
@@ -701,7 +697,8 @@ int atl_anchored_score_mean_fwd(const float* S, const float* wc, const float* vi
   }
   const unsigned grid = M > 0 ? std::min(grid_for(M), (unsigned)kMeanBlocks) : 1u;
   hipLaunchKernelGGL(k_epilogue_mean, dim3(grid), dim3(kBlock), 0, stream, S, wc, vis, M, (float)M_PI,
-                     (float)(h * h), (float)eps, q, D, (double*)scratch, (unsigned*)((char*)scratch + kMeanBlocks * 8),
+                     (float)(h * h), (float)eps, q, D, (double*)scratch);
+  hipLaunchKernelGGL(k_epilogue_mean_total, dim3(1), dim3(kBlock), 0, stream, (const double*)scratch, (int)grid, M,
                      out);
   return check_launch("anchored_score_mean_fwd");
 }

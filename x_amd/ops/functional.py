@@ -560,17 +560,9 @@ def anchored_log_scores(S, wc, vis, h, eps):
     return _AnchoredEpilogue.apply(S, wc, vis, h, eps)
 
 
-_MEAN_SCRATCH = {}   # (device, stream) -> zeroed scratch of the fused loss (every call leaves it zero)
-
-
-def _mean_scratch(dev, stream):
-    key = (dev, getattr(stream, "value", stream))
-    buf = _MEAN_SCRATCH.get(key)
-    if buf is None:
-        nbytes = int(load_library().atl_anchored_score_mean_scratch_bytes())
-        buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
-        _MEAN_SCRATCH[key] = buf
-    return buf
+def _mean_scratch(dev):
+    """Per-block partial sums of the fused loss (8 KB, allocated per call from torch's caching allocator)."""
+    return torch.empty(int(load_library().atl_anchored_score_mean_scratch_bytes()), dtype=torch.uint8, device=dev)
 
 
 class _AnchoredScoreMean(torch.autograd.Function):
@@ -587,14 +579,17 @@ class _AnchoredScoreMean(torch.autograd.Function):
         st = stream_of(S)
         with torch.cuda.device(S.device):
             call("atl_anchored_score_mean_fwd", ptr(S), ptr(wc), ptr(vis), M, float(h), float(eps), ptr(q), ptr(D),
-                 ptr(_mean_scratch(S.device, st)), ptr(out), st)
+                 ptr(_mean_scratch(S.device)), ptr(out), st)
         ctx.save_for_backward(q, D)
+        ctx.set_materialize_grads(False)
         loss, score = out[0], out[1]
         ctx.mark_non_differentiable(score)
         return loss, score
 
     @staticmethod
     def backward(ctx, g, _gscore):
+        if g is None:
+            return None, None, None, None, None
         q, D = ctx.saved_tensors
         gS = torch.empty_like(q)
         g = g.contiguous().float()
