@@ -359,6 +359,22 @@ def test_window_counts_and_pair_sums_without_index():
     close_rel(N(s0), N(s1), 1e-6)
 
 
+@pytest.mark.parametrize("n,B,dup", [(1_000_000, 1, False), (300_000, 3, True), (700, 2, True)])
+def test_window_counts_every_event_bit_exact(n, B, dup):
+    """Window counts with every event as anchor (the block-cooperative bound search) vs the oracle, bit-exact:
+    1M events in one window, several batches, and runs of equal timestamps."""
+    print(f"window counts n={n} B={B} dup={dup}", flush=True)
+    rng = np.random.default_rng(n)
+    t = rng.random(n).astype(np.float32)
+    if dup:
+        t = np.round(t * 997).astype(np.float32) / np.float32(997)   # many equal keys
+    b = rng.integers(0, B, n).astype(np.int64)
+    order = np.lexsort((t, b))
+    t, b = t[order], b[order]
+    got = N(F.window_counts(T(t), T(b), None, 0.2, assume_sorted=True))
+    assert np.array_equal(got, O.window_counts(t, b, np.arange(n), 0.2))
+
+
 # ------------------------------------------------------------------------------------------- full size
 def test_full_size_splat_gather_properties():
     """1M events at 640x480 (dense flow, warp to t_ref = 0.5): mass conservation of the splat and the adjoint
