@@ -283,6 +283,20 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_fwd(const float* __restr
   const GridCorners g = grid_corners(p.x, p.y, Hg, Wg, sxw, syh, scale != 0);
   const int64_t plane = (int64_t)Hg * Wg;
   const float* f = field + b * C * plane;
+  if (Wg >= 2) {                                 // o01 = o00 + 1, o11 = o10 + 1: one 8-byte load per grid row
+    for (int c = 0; c < C; ++c) {
+      const float* fc = f + c * plane;
+      float2 r0, r1;
+      __builtin_memcpy(&r0, fc + g.o00, sizeof(float2));   // 4-byte aligned: unaligned 8-byte loads are legal
+      __builtin_memcpy(&r1, fc + g.o10, sizeof(float2));
+      float v = r0.x * g.w00;
+      v = v + r0.y * g.w01;
+      v = v + r1.x * g.w10;
+      v = v + r1.y * g.w11;
+      o[c] = v;
+    }
+    return;
+  }
   for (int c = 0; c < C; ++c) {
     const float* fc = f + c * plane;
     float v = fc[g.o00] * g.w00;

@@ -452,6 +452,8 @@ __global__ void __launch_bounds__(kBlock) k_check_sorted(const float* __restrict
 
 // ------------------------------------------------------------------------------------------ exposure
 // Per-batch event counts in n_check time bins, atl/objectives/ats.py:39-41 (LDS histogram per block).
+constexpr int kBinPer = 16;                        // events per thread (loads issued together)
+
 __global__ void __launch_bounds__(kBlock) k_bin_counts(const float* __restrict__ t, const int64_t* __restrict__ b,
                                                        int64_t N, int64_t B, int n_check, float* __restrict__ counts) {
   extern __shared__ int hist[];
@@ -459,13 +461,37 @@ __global__ void __launch_bounds__(kBlock) k_bin_counts(const float* __restrict__
   for (int k = threadIdx.x; k < nb; k += blockDim.x) hist[k] = 0;
   __syncthreads();
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < N; j += stride) {
-    const int64_t bj = b[j];
-    if (bj < 0 || bj >= B) continue;
-    const float q = t[j] * (float)n_check;
-    int s = (q > -1.f && q < 2147483520.f) ? (int)q : (q >= 2147483520.f ? n_check - 1 : 0);
-    s = min(max(s, 0), n_check - 1);
-    atomicAdd(hist + bj * n_check + s, 1);
+  const int lane = threadIdx.x & 63;
+  for (int64_t j0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j0 < N; j0 += stride * kBinPer) {
+    int64_t bq[kBinPer];
+    float tq[kBinPer];
+#pragma unroll
+    for (int u = 0; u < kBinPer; ++u) {            // all loads of the thread in flight together
+      const int64_t j = j0 + u * stride;
+      bq[u] = j < N ? b[j] : -1;
+      tq[u] = j < N ? t[j] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kBinPer; ++u) {
+      const int64_t bj = bq[u];
+      int key = -1;
+      if (bj >= 0 && bj < B) {
+        const float q = tq[u] * (float)n_check;
+        int s = (q > -1.f && q < 2147483520.f) ? (int)q : (q >= 2147483520.f ? n_check - 1 : 0);
+        s = min(max(s, 0), n_check - 1);
+        key = (int)bj * n_check + s;
+      }
+      // lanes with equal bins add once: time-ordered events put a whole wave in one or two bins, and 64 LDS
+      // atomics on one address would run one after the other
+      uint64_t todo = __ballot(1);
+      while (todo) {
+        const int leader = __ffsll((unsigned long long)todo) - 1;
+        const int kl = __shfl(key, leader);
+        const uint64_t same = __ballot(key == kl) & todo;
+        if (lane == leader && kl >= 0) atomicAdd(hist + kl, __popcll(same));
+        todo &= ~same;
+      }
+    }
   }
   __syncthreads();
   for (int k = threadIdx.x; k < nb; k += blockDim.x)
@@ -758,7 +784,7 @@ int atl_bin_counts(const float* t, const int64_t* b, int64_t N, int64_t B, int64
                    hipStream_t stream) {
   if (N < 0 || B < 0 || n_check < 1 || B * n_check > 8192) { set_error("bin_counts: bad sizes (B*n_check <= 8192)"); return 1; }
   if (N == 0 || B == 0) return 0;
-  unsigned grid = grid_for(N, kBlock * 16);
+  unsigned grid = grid_for(N, kBlock * kBinPer);
   hipLaunchKernelGGL(k_bin_counts, dim3(grid), dim3(kBlock), (size_t)(B * n_check) * sizeof(int), stream, t, b, N,
                      B, (int)n_check, counts);
   return check_launch("bin_counts");
