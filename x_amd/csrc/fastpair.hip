@@ -43,9 +43,9 @@ constexpr int kMinBucketShift = 10;
 constexpr int kMaxBucketShift = 13;
 constexpr int kMaxBuckets = 16384;
 constexpr int kSortBlock = 512;                    // pass-2 workgroup
-constexpr int kP1Block = 512;                      // pass-1 workgroup
-constexpr int kSrcPerBlock = 4096;                 // pass-1 sources per block (8 per thread)
-constexpr int kAncPerBlock = 8192;                 // pass-1 anchors per block (16 per thread)
+constexpr int kP1Block = 1024;                     // pass-1 workgroup
+constexpr int kSrcPerBlock = 4096;                 // pass-1 sources per block (4 per thread)
+constexpr int kAncPerBlock = 8192;                 // pass-1 anchors per block (8 per thread)
 constexpr int kUnroll = 4;                         // candidates per walk step (record arrays padded by this)
 constexpr int kSliceBatch = 4;                     // pass 1: slices of one source keyed and placed together
 
