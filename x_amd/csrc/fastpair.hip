@@ -497,7 +497,7 @@ __device__ __forceinline__ bool pair_test(int id_a, int id_s, float ta, float ts
 // per-slice positions differ, so a group shares less there than it costs to set up).
 
 constexpr int kGroup = 8;                          // queries evaluated per pass over a group's candidates
-constexpr int kGroupCells = 3;                     // a forward group spans up to this many cells of one row
+constexpr int kGroupCells = 4;                     // a forward group spans up to this many cells of one row
 
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ float unif(float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); }
@@ -709,9 +709,9 @@ __device__ __forceinline__ void group_walk(const int* __restrict__ cstart, int b
 // repeat the last anchor and are discarded): lane src0 + a receives anchor a's sum (and count) in mine
 // (mine_n).  es is each anchor lane's own entry position: the leave-one-out test skips that candidate.
 template <int WD, bool COUNT>
-__device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plane, float x0, float x1, float y0,
-                                         float R, float R2, float vmax, const float4& A, int es, int src0, int na,
-                                         int lane, float& mine, int& mine_n) {
+__device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plane, float R, float R2, float vmax,
+                                         const float4& A, int es, int src0, int na, int lane, float& mine,
+                                         int& mine_n) {
   float ax[WD], ay[WD], ta[WD], at[WD], acc[WD];
   int id[WD], cnt[WD];
 #pragma unroll
@@ -743,7 +743,19 @@ __device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plan
     const uint32_t k = (uint32_t)max(pos, 0);
     return Cand{ld(p.epos, k), ld(p.etim, k)};
   };
-  group_walk(p.start, 0, plane, x0, x1, y0, y0 + G.cf, R, R2, G, load, [&](const Cand& c, int pos) {
+  // The walk covers the R-neighbourhood of the box of these anchors' clamped positions (tighter than their
+  // cells' box: every contributing candidate lies within R of its anchor, and clamping never increases a
+  // distance).  Slots past na repeat the last anchor, so they do not widen it.
+  float bx0 = clampf(ax[0], G.gx0, G.gx1), bx1 = bx0, by0 = clampf(ay[0], G.gy0, G.gy1), by1 = by0;
+#pragma unroll
+  for (int a = 1; a < WD; ++a) {
+    const float cx = clampf(ax[a], G.gx0, G.gx1), cy = clampf(ay[a], G.gy0, G.gy1);
+    bx0 = fminf(bx0, cx);
+    bx1 = fmaxf(bx1, cx);
+    by0 = fminf(by0, cy);
+    by1 = fmaxf(by1, cy);
+  }
+  group_walk(p.start, 0, plane, bx0, bx1, by0, by1, R, R2, G, load, [&](const Cand& c, int pos) {
     const float4 e = c.e;
     const float ts = c.t;
 #pragma unroll
@@ -809,23 +821,20 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
     const uint64_t gmask = __ballot(have && key >= gkey && key - gkey < span) & todo;
     todo &= ~gmask;
     const int gsize = __popcll(gmask);
-    const int last_cx = cx + (rdlane(key, i + gsize - 1) - gkey);
-    const float x0 = G.gx0 + (float)cx * G.cf, x1 = G.gx0 + (float)(last_cx + 1) * G.cf;
-    const float y0 = G.gy0 + (float)cy * G.cf;
     for (int a0 = 0; a0 < gsize; a0 += kGroup) {
       const int na = min(kGroup, gsize - a0);
       if (na == 1)
-        fwd_pass<1, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<1, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
       else if (na == 2)
-        fwd_pass<2, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<2, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
       else if (na == 3)
-        fwd_pass<3, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<3, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
       else if (na == 4)
-        fwd_pass<4, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<4, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
       else if (na <= 6)
-        fwd_pass<6, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<6, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
       else
-        fwd_pass<kGroup, COUNT>(p, G, plane, x0, x1, y0, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<kGroup, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
     }
   }
   if (have) {
