@@ -208,8 +208,8 @@ __global__ void __launch_bounds__(kBlock) k_fill_zero(int* __restrict__ p, int64
 }
 
 
-// Pass 1.  Blocks [0, nblk_e) cover kSrcPerBlock sources each (their entries and one source record keyed
-// by the cell of the own-slice entry), blocks [nblk_e, nblk_e + nblk_a) kAncPerBlock anchors each.
+// Pass 1.  Blocks [0, nblk_a) cover kAncPerBlock anchors each, blocks [nblk_a, nblk_a + nblk_e) kSrcPerBlock
+// sources each (their entries and one source record keyed by the cell of the own-slice entry).
 // SCATTER = false: per-block bucket histogram into cnt[bucket * nblk + block], and the reductions behind the
 // search radius: vmax over the sources' velocities and max |at| over the anchors (block maxima, one atomic max
 // per block into P, zeroed beforehand; ordered-int encodings of non-negative floats).  SCATTER = true: the
@@ -229,9 +229,12 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
   const int blk = blockIdx.x;
   for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) hist[i] = SCATTER ? cnt[i * nblk + blk] : 0;
   __syncthreads();
-  if (blk < G.nblk_e) {
+  // anchor blocks first: they are about a quarter of a source block's work, and dispatched last they would
+  // queue on the few CUs left free by the source blocks
+  const bool src_blk = blk >= G.nblk_a;
+  if (src_blk) {
     constexpr int per = kSrcPerBlock / kP1Block;
-    const int64_t j0 = (int64_t)blk * kSrcPerBlock;
+    const int64_t j0 = (int64_t)(blk - G.nblk_a) * kSrcPerBlock;
     float2 xj[per], vj[per];
     float tj[per];
     int64_t bj[per];
@@ -294,7 +297,7 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
       }
     }
   } else {
-    const int64_t m0 = (int64_t)(blk - G.nblk_e) * kAncPerBlock;
+    const int64_t m0 = (int64_t)blk * kAncPerBlock;
     const int64_t m1 = m0 + kAncPerBlock < M ? m0 + kAncPerBlock : M;
     constexpr int kAB = 4;                       // anchors per batch: loads, slot atomics and stores grouped
     for (int64_t mb = m0 + threadIdx.x; mb < m1; mb += kAB * blockDim.x) {
@@ -326,7 +329,7 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
     for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) cnt[i * nblk + blk] = hist[i];
     if (threadIdx.x == 0) {
       for (int w = 1; w < kP1Block / kWave; ++w) vm = max(vm, red[w]);
-      if (vm > 0) atomicMax(blk < G.nblk_e ? &P->vmax : &P->atmax, vm);
+      if (vm > 0) atomicMax(src_blk ? &P->vmax : &P->atmax, vm);
     }
   }
 }
