@@ -74,7 +74,8 @@ struct FParams {
   int vmax;                    // max ||v|| over sources
   int atmax;                   // max |t_a - c_s| over anchors
   int dup;                     // non-zero if an event occurs more than once among the anchors
-  int pad[5];
+  int unique;                  // non-zero if the anchors are every event in order (no index array): no repeats
+  int pad[4];
 };
 
 // One 32-byte record per sorted item, written with a single scattered line (separate arrays would cost one
@@ -228,6 +229,7 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
   const int nblk = G.nblk_e + G.nblk_a;
   const int blk = blockIdx.x;
   for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) hist[i] = SCATTER ? cnt[i * nblk + blk] : 0;
+  if (!SCATTER && blk == 0 && threadIdx.x == 0 && !anchors) P->unique = 1;
   __syncthreads();
   // anchor blocks first: they are about a quarter of a source block's work, and dispatched last they would
   // queue on the few CUs left free by the source blocks
@@ -848,14 +850,15 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
 
 // Backward records of the anchors in cell order, brec[q] = (x, y, t, gS / h^2): one 16-byte load per candidate in
 // the backward's per-lane walks (the anchor's at = t - c_s is recomputed there with the same fp32 operation).
-// Also checks that no event occurs twice among the anchors (self[id] then names only one of the records).
+// Also checks that no event occurs twice among the anchors (self[id] then names only one of the records); an
+// index-free plan (every event once) skips that check.
 __global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int M, const float* __restrict__ gS) {
   const int q = blockIdx.x * blockDim.x + threadIdx.x;
   const int Mv = p.start[2 * G.ncell_pad] - p.start[G.ncell_pad];
   if (q >= Mv || q >= M) return;
   const Rec r = p.arec[q];
   p.brec[q] = make_float4(r.f.x, r.f.y, r.f.z, gS[r.i.y] * G.invh2);
-  if (p.self[r.i.x] != q) p.P->dup = 1;
+  if (!p.P->unique && p.self[r.i.x] != q) p.P->dup = 1;
 }
 
 // One source's walk over the anchors of every slice of its range (csrc/atl_cpu.cpp:240-248): returns
@@ -883,11 +886,13 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
     walk_flat(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, tab, [&](int k, int e) {
       float4 A[kUnroll];
       int id[kUnroll];
+      // one lane offset for the kUnroll loads, the step within the record run folded into the (scalar) base
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        A[u] = ld((const float4*)p.brec, (uint32_t)(k + u));
-        if (DUP) id[u] = ld(aid, 8u * (uint32_t)(k + u));
+        A[u] = ld((const float4*)p.brec + u, (uint32_t)k);
+        if (DUP) id[u] = ld(aid + 8 * u, 8u * (uint32_t)k);
       }
+      const int rem = e - k, self_u = sp - k;
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const float at = A[u].z - cs;
@@ -895,8 +900,8 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
         const float rx = A[u].x - (sv.x + sv.z * at);
         const float ry = A[u].y - (sv.y + sv.w * at);
         const float d2 = rx * rx + ry * ry;
-        const bool other = DUP ? id[u] != sid : k + u != sp;
-        const bool ok = other & !(fabsf(dt) > G.tau) & !(d2 > G.r2max) & (k + u < e);
+        const bool other = DUP ? id[u] != sid : u != self_u;
+        const bool ok = other & !(fabsf(dt) > G.tau) & !(d2 > G.r2max) & (u < rem);
         const float kern = __builtin_amdgcn_exp2f(d2 * G.kexp);
         const float f = A[u].w * kern * dt;           // A.w = gS / h^2
         mgx = ok ? fmaf(f, rx, mgx) : mgx;

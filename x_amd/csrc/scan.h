@@ -1,5 +1,6 @@
-// Device-wide exclusive scan of int32 counts (three launches: per-tile totals, one-block scan of the
-// totals, per-tile rescan), shared by the plan builders.  Tiles are kScanTile = 2048 counts.
+// Device-wide exclusive scan of int32 counts (two launches: per-tile totals, then a per-tile rescan that
+// first sums the totals of the tiles before its own), shared by the plan builders.  Tiles are
+// kScanTile = 2048 counts.
 #pragma once
 #include "common.h"
 
@@ -24,25 +25,15 @@ __global__ void __launch_bounds__(kBlock) k_scan32_reduce(const int* __restrict_
   if (threadIdx.x == 0) part[blockIdx.x] = total;
 }
 
-// Exclusive scan of the tile totals in place (one block); part[nparts] receives the grand total.
-__global__ void __launch_bounds__(kBlock) k_scan32_parts(int* __restrict__ part, int64_t nparts) {
-  __shared__ int lds[kBlock / kWave + 1];
-  int carry = 0;
-  for (int64_t base = 0; base < nparts; base += kBlock) {
-    const int64_t i = base + threadIdx.x;
-    const int v = i < nparts ? part[i] : 0;
-    int total;
-    const int excl = block_exclusive_scan<kBlock>(v, lds, total);
-    if (i < nparts) part[i] = carry + excl;
-    carry += total;
-  }
-  if (threadIdx.x == 0) part[nparts] = carry;
-}
-
-// out[i + 1] = sum(in[0..i]), out[0] = 0.
+// out[i + 1] = sum(in[0..i]), out[0] = 0.  part holds the tile totals; each block adds up those of the tiles
+// before its own (a few thousand at most: cheaper than a launch of its own).
 __global__ void __launch_bounds__(kBlock) k_scan32_write(const int* __restrict__ in, int64_t n,
                                                          const int* __restrict__ part, int* __restrict__ out) {
   __shared__ int lds[kBlock / kWave + 1];
+  int pre = 0;
+  for (int64_t i = threadIdx.x; i < (int64_t)blockIdx.x; i += kBlock) pre += part[i];
+  int offset;
+  block_exclusive_scan<kBlock>(pre, lds, offset);
   const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
   int vals[kScanItems];
   int s = 0;
@@ -53,7 +44,7 @@ __global__ void __launch_bounds__(kBlock) k_scan32_write(const int* __restrict__
   }
   int total;
   const int excl = block_exclusive_scan<kBlock>(s, lds, total);
-  int run = part[blockIdx.x] + excl;
+  int run = offset + excl;
 #pragma unroll
   for (int k = 0; k < kScanItems; ++k) {
     run += vals[k];
@@ -62,11 +53,10 @@ __global__ void __launch_bounds__(kBlock) k_scan32_write(const int* __restrict__
   if (blockIdx.x == 0 && threadIdx.x == 0) out[0] = 0;
 }
 
-// Launches the three passes; `part` holds scan_tiles(n) + 1 ints.  n >= 1.
+// Launches the two passes; `part` holds scan_tiles(n) ints (callers reserve one more).  n >= 1.
 inline void scan32(const int* in, int64_t n, int* part, int* out, hipStream_t stream) {
   const int64_t tiles = scan_tiles(n);
   hipLaunchKernelGGL(k_scan32_reduce, dim3((unsigned)tiles), dim3(kBlock), 0, stream, in, n, part);
-  hipLaunchKernelGGL(k_scan32_parts, dim3(1), dim3(kBlock), 0, stream, part, tiles);
   hipLaunchKernelGGL(k_scan32_write, dim3((unsigned)tiles), dim3(kBlock), 0, stream, in, n, (const int*)part, out);
 }
 
