@@ -97,6 +97,16 @@ int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t
                                 int64_t N, int64_t img_h, int64_t img_w, const void* ws, float* gfield,
                                 hipStream_t stream);
 
+/* ---------------------------------------------------------------- event noise */
+
+/* Dequantisation and smoothing noise of AnchoredExact (atl/objectives/ats.py:79-84, where torch.rand - 0.5 and
+ * h * torch.randn are drawn on a CPU generator and added): xs (N,2) = xy + U(-1/2, 1/2) per coordinate when
+ * dequantize != 0 (else a copy of xy); xa (N,2) = xs + h N(0, 1) per coordinate when xa is not null.  Philox4x32-10
+ * keyed by seed, counter (event index, offset): the same (seed, offset) gives the same draws, a new offset new
+ * ones.  Not the reference's random numbers (those come from torch's CPU generator). */
+int atl_event_noise(const float* xy, int64_t N, uint64_t seed, uint64_t offset, double h, int dequantize, float* xs,
+                    float* xa, hipStream_t stream);
+
 /* ---------------------------------------------------------------- pair plan (atl/ops/functional.py:132-178) */
 
 /* Reductions behind the plan geometry (functional.py:139,144-145): stats (5 ints, ordered-int encoding of

@@ -373,6 +373,54 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos(const float* __r
 
 bool dims_ok(int64_t H, int64_t W) { return H > 0 && W > 0 && H * W < (int64_t)1 << 31; }
 
+// ------------------------------------------------------------------------------------------- event noise
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as easy as 1, 2, 3", SC 2011): a
+// counter-based generator, so every event draws its own four words from (its index, the call's offset) under
+// the seed, in any order and without state.
+struct U4 {
+  uint32_t x, y, z, w;
+};
+
+__device__ __forceinline__ U4 philox4x32_10(U4 c, uint32_t k0, uint32_t k1) {
+  constexpr uint32_t kM0 = 0xD2511F53u, kM1 = 0xCD9E8D57u, kW0 = 0x9E3779B9u, kW1 = 0xBB67AE85u;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t hi0 = __umulhi(kM0, c.x), lo0 = kM0 * c.x;
+    const uint32_t hi1 = __umulhi(kM1, c.z), lo1 = kM1 * c.z;
+    c = U4{hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0};
+    k0 += kW0;
+    k1 += kW1;
+  }
+  return c;
+}
+
+// Dequantisation and anchor smoothing noise of the anchored score (atl/objectives/ats.py:79-84 draws them with
+// torch.rand / torch.randn): xs = xy + U(-1/2, 1/2)^2 if dequantize, else xy; xa = xs + h N(0, 1)^2 (Box-Muller
+// on the other two words) if xa is given.  One pass over the events instead of two fills and two adds.
+__global__ void __launch_bounds__(kBlock) k_event_noise(const float2* __restrict__ xy, int64_t N, uint32_t s0,
+                                                        uint32_t s1, uint32_t o0, uint32_t o1, float h,
+                                                        int dequantize, float2* __restrict__ xs,
+                                                        float2* __restrict__ xa) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const U4 r = philox4x32_10(U4{(uint32_t)n, (uint32_t)(n >> 32), o0, o1}, s0, s1);
+  constexpr float k24 = 1.f / 16777216.f;          // 24-bit mantissa fractions
+  float2 p = xy[n];
+  if (dequantize) {
+    p.x = p.x + ((float)(r.x >> 8) * k24 - 0.5f);
+    p.y = p.y + ((float)(r.y >> 8) * k24 - 0.5f);
+  }
+  xs[n] = p;
+  if (xa) {
+    const float u1 = (float)((r.z >> 8) + 1u) * k24;   // (0, 1]: log finite
+    const float u2 = (float)(r.w >> 8) * k24;          // [0, 1)
+    const float rad = sqrtf(-2.f * logf(u1));
+    float sn, cs;
+    sincospif(2.f * u2, &sn, &cs);
+    xa[n] = make_float2(p.x + h * (rad * cs), p.y + h * (rad * sn));
+  }
+}
+
 }  // namespace
 
 // ================================================================================================ C-ABI
@@ -478,6 +526,16 @@ int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int
   hipLaunchKernelGGL(k_sample_grid_bwd, dim3(grid_for(N)), dim3(kBlock), 0, stream, gout, B, (int)C, (int)Hg,
                      (int)Wg, (const float2*)pos, b, N, sxw, syh, scale, gfield);
   return check_launch("sample_grid_bwd");
+}
+
+int atl_event_noise(const float* xy, int64_t N, uint64_t seed, uint64_t offset, double h, int dequantize, float* xs,
+                    float* xa, hipStream_t stream) {
+  if (N < 0 || (N > 0 && (!xy || !xs)) || !(h >= 0) || !(h < 1e30)) { set_error("event_noise: bad arguments"); return 1; }
+  if (N == 0) return 0;
+  hipLaunchKernelGGL(k_event_noise, dim3(grid_for(N)), dim3(kBlock), 0, stream, (const float2*)xy, N,
+                     (uint32_t)seed, (uint32_t)(seed >> 32), (uint32_t)offset, (uint32_t)(offset >> 32), (float)h,
+                     dequantize, (float2*)xs, (float2*)xa);
+  return check_launch("event_noise");
 }
 
 }  // extern "C"

@@ -16,12 +16,14 @@ visible fraction and the log-score epilogue.
 from __future__ import annotations
 
 import math
+import os
 from typing import Optional
 
 import torch
 
 from ..core.events import EventPacket
-from ..ops import anchored_log_scores, anchored_score_mean, ats_pair_sums, gather, splat, visible_fraction_linear, window_counts
+from ..ops import (anchored_log_scores, anchored_score_mean, ats_pair_sums, event_noise, gather, splat,
+                   visible_fraction_linear, window_counts)
 from .base import Objective
 
 
@@ -64,7 +66,8 @@ class AnchoredExact(Objective):
 
     Same constructor as atl/objectives/ats.py:65-73, plus ``rng``: ``"cpu"`` draws the dequantisation and
     smoothing noise from a CPU ``torch.Generator`` exactly like the reference (then copies it to the device);
-    ``"device"`` draws it on the device (no host round trip; different random numbers for the same seed)."""
+    ``"device"`` draws it on the device (no host round trip; different random numbers for the same seed); with
+    every event as anchor both draws and both adds are one pass (``event_noise``, Philox4x32-10)."""
     name = "ats_exact"
     reference_frame = False
 
@@ -77,6 +80,7 @@ class AnchoredExact(Objective):
         self.seed, self.rng = seed, rng
         self.gen = torch.Generator().manual_seed(seed) if seed is not None else None
         self._dgen = None
+        self._dseed, self._draws = None, 0          # fused device noise: Philox key and call counter
 
     def _noise(self, shape, like: torch.Tensor, kind: str, scale: float = 1.0) -> torch.Tensor:
         """Dequantisation noise U(-1/2, 1/2) (kind "uniform") or smoothing noise N(0, scale^2) ("normal").  From
@@ -93,6 +97,11 @@ class AnchoredExact(Objective):
         if kind == "uniform":
             return torch.rand(shape, generator=self.gen).to(like) - 0.5
         return scale * torch.randn(shape, generator=self.gen).to(like)
+
+    def _device_seed(self) -> int:
+        if self._dseed is None:
+            self._dseed = self.seed if self.seed is not None else int.from_bytes(os.urandom(8), "little")
+        return self._dseed
 
     def log_scores(self, ev: EventPacket, motion, anchors: Optional[torch.Tensor] = None):
         """Per-anchor log predictive densities and the anchor indices (atl/objectives/ats.py:75-96)."""
@@ -117,11 +126,18 @@ class AnchoredExact(Objective):
                 anchors = anchors[ev.inside(ev.xy[anchors], margin=-self.anchor_margin)]
         pick = (lambda a: a) if anchors is None else (lambda a: a[anchors])   # None: every event, in order
         xs = ev.xy
-        if self.dequantize:
-            xs = xs + self._noise(xs.shape, xs, "uniform")
-        xa = pick(xs)
-        if self.smooth_anchors:
-            xa = xa + self._noise(xa.shape, xa, "normal", self.h)
+        if (self.rng == "device" and xs.is_cuda and anchors is None and not xs.requires_grad
+                and (self.dequantize or self.smooth_anchors)):
+            # both draws and both adds in one pass over the events
+            xs, xa = event_noise(xs, self._device_seed(), self._draws, self.h, self.dequantize, self.smooth_anchors)
+            self._draws += 1
+            xa = xs if xa is None else xa
+        else:
+            if self.dequantize:
+                xs = xs + self._noise(xs.shape, xs, "uniform")
+            xa = pick(xs)
+            if self.smooth_anchors:
+                xa = xa + self._noise(xa.shape, xa, "normal", self.h)
         v = motion.velocity(xs, ev.t, ev.b)
         S = ats_pair_sums(xs, ev.t, v, ev.b, ev.batch_size, ev.height, ev.width, anchors, self.h, self.tau,
                           self.cut, self.n_slices, anchor_xy=xa)

@@ -39,6 +39,7 @@ _SIGS = {
     "atl_sample_grid_fwd": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_sample_grid_bwd": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_sample_grid_bwd_pos": [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
+    "atl_event_noise": [_P, _I, ctypes.c_uint64, ctypes.c_uint64, _D, _C, _P, _P, _P],
     "atl_plan_stats": [_P, _I, _P, _I, _P, _P],
     "atl_plan_count": [_P, _P, _P, _P, _I, _I, _D, _D, _D, _D, _I, _I, _I, _P, _P],
     "atl_scan_counts": [_P, _I, _P, _P, _P],

@@ -512,6 +512,24 @@ def bin_centres(n_check: int, device) -> torch.Tensor:
     return c
 
 
+def event_noise(xy: torch.Tensor, seed: int, offset: int, h: float, dequantize: bool = True,
+                smooth: bool = True):
+    """Dequantised positions xs = xy + U(-1/2, 1/2) and smoothed anchor positions xa = xs + h N(0, 1), per
+    coordinate, drawn in one device pass (Philox4x32-10 keyed by ``seed``, counter (event, ``offset``); the
+    noise of atl/objectives/ats.py:79-84, not its random numbers).  Returns (xs, xa), xa None without
+    ``smooth``.  No gradient flows to ``xy``."""
+    get_ext()
+    xy = _f32(xy.detach())
+    if xy.dim() != 2 or xy.shape[1] != 2:
+        raise ValueError("xy must be (N, 2)")
+    xs = torch.empty_like(xy)
+    xa = torch.empty_like(xy) if smooth else None
+    with torch.cuda.device(xy.device):
+        call("atl_event_noise", ptr(xy), xy.shape[0], int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 64 - 1),
+             float(h), int(bool(dequantize)), ptr(xs), ptr(xa), stream_of(xy))
+    return xs, xa
+
+
 def visible_fraction_linear(xa, va, ta, ba, t_all, b_all, B, H, W, tau, n_check=16):
     """Exposure correction of atl/objectives/ats.py:31-50 for motion linear at the event: anchors (xa, ta, ba)
     with velocities ``va`` transported to the n_check bin centres.  No grad."""
