@@ -322,7 +322,7 @@ def iwe_main(a, dev):
         step()
     torch.cuda.synchronize()
     kernels = list(IWE_BYTES)
-    rec = _ext.time_kernels(kernels)
+    rec = _ext.time_kernels(kernels, every=5)      # every bracket delays the next launch: sample the steps
     t0 = time.perf_counter()
     for _ in range(a.steps):
         step()
@@ -384,14 +384,15 @@ def trajectories_main(a, dev):
         step()
     torch.cuda.synchronize()
     kernels = list(TRAJ_BYTES)
-    rec = _ext.time_kernels(kernels)
+    rec = _ext.time_kernels(kernels, every=25)     # hundreds of calls a step: time a sample of them
     t0 = time.perf_counter()
     for _ in range(a.steps):
         step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec[k]])) for k in kernels if rec[k]}
-    calls = {k: len(rec[k]) / a.steps for k in kernels if rec[k]}
+    ncall = _ext.timed_calls()
+    calls = {k: ncall.get(k, 0) / a.steps for k in kernels if rec[k]}
     rec_all = {k: list(v) for k, v in rec.items()}
     _ext.time_kernels(())
     tot = {k: ms[k] * calls[k] for k in ms}
@@ -481,7 +482,7 @@ def main():
         step()
     torch.cuda.synchronize()
     kernels = ["atl_fast_pair_fwd", "atl_fast_pair_bwd"]
-    rec = _ext.time_kernels(kernels)
+    rec = _ext.time_kernels(kernels, every=4)      # every bracket delays the next launch: sample the steps
     t0 = time.perf_counter()
     for _ in range(a.steps):
         step()

@@ -185,7 +185,7 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
                   const int64_t* anchors, const float* anchor_xy, void* ws, int64_t ws_bytes, hipStream_t stream);
 /* out (M) written for every valid anchor (zero-fill it first); count (M) int32 receives n_i when non-null. */
 int atl_fast_pair_fwd(const atl_fast_geometry* geo, const void* ws, float* out, int* count, hipStream_t stream);
-/* gv (N,2) accumulated (zero-fill it first). */
+/* gv (N,2) written: each source's gradient, zero for sources outside the plan (no fill needed). */
 int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, float* gv, hipStream_t stream);
 
 /* ---------------------------------------------------------------- anchored-score pieces */

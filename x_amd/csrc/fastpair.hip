@@ -27,6 +27,8 @@
 // 8 x 8 cells, so that a wave's sources form a compact patch), and the
 // backward gives each source one lane that walks the anchors of all its slices: the gradient of a source
 // is complete in registers and written once, without atomics.
+#include <algorithm>
+
 #include "common.h"
 #include "scan.h"
 #include "../../include/atl_hip.h"
@@ -851,9 +853,12 @@ __global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, flo
 // Backward records of the anchors in cell order, brec[q] = (x, y, t, gS / h^2): one 16-byte load per candidate in
 // the backward's per-lane walks (the anchor's at = t - c_s is recomputed there with the same fp32 operation).
 // Also checks that no event occurs twice among the anchors (self[id] then names only one of the records); an
-// index-free plan (every event once) skips that check.
-__global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int M, const float* __restrict__ gS) {
+// index-free plan (every event once) skips that check.  Threads q < N clear gv[q] for the backward, which then
+// writes each source's total (sources without a record keep the zero).
+__global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int M, const float* __restrict__ gS,
+                                                           int N, float2* __restrict__ gv) {
   const int q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (q < N) gv[q] = make_float2(0.f, 0.f);
   const int Mv = p.start[2 * G.ncell_pad] - p.start[G.ncell_pad];
   if (q >= Mv || q >= M) return;
   const Rec r = p.arec[q];
@@ -914,7 +919,7 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
 
 // Backward: every source (one lane each, own-slice tile order) sums, over the anchors of each slice of its
 // range within R of its slice-centre position, gS_i * k * dt / h^2 * r (csrc/atl_cpu.cpp:240-248);
-// gv[j] += the total (each source once: no atomics).
+// gv[j] = the total (each source has one record: no atomics).
 __global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, float2* __restrict__ gv) {
   __shared__ int2 tab[kRowTab * kBlock];           // per-lane row spans of the current slice (column threadIdx.x)
   const int lb = xcd_block((N + kBlock - 1) / kBlock);
@@ -946,10 +951,7 @@ __global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, flo
   int2* mytab = tab + threadIdx.x;
   const float2 m = uni(p.P->dup) ? bwd_source<true>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, mytab)
                                  : bwd_source<false>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, mytab);
-  float2 o = gv[si.y];
-  o.x += m.x;
-  o.y += m.y;
-  gv[si.y] = o;
+  gv[si.y] = m;
 }
 
 // ------------------------------------------------------------------------------------------ host side
@@ -1130,12 +1132,14 @@ int atl_fast_pair_fwd(const atl_fast_geometry* geo, const void* ws, float* out, 
 int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, float* gv, hipStream_t stream) {
   FGeo G;
   if (!make_geo(geo, G)) { set_error("fast_pair_bwd: geometry not initialised"); return 1; }
-  if (!ws || (geo->M > 0 && (!gS || !gv))) { set_error("fast_pair_bwd: null argument"); return 1; }
-  if (geo->M == 0 || geo->N == 0) return 0;
+  if (!ws || (geo->N > 0 && !gv) || (geo->M > 0 && !gS)) { set_error("fast_pair_bwd: null argument"); return 1; }
+  if (geo->N == 0) return 0;
   const FPlan p = make_plan(ws, geo);
-  hipLaunchKernelGGL(k_fast_gather_gs, dim3(grid_for(geo->M)), dim3(kBlock), 0, stream, p, G, (int)geo->M, gS);
-  hipLaunchKernelGGL(k_fast_bwd, dim3(xcd_grid((geo->N + kBlock - 1) / kBlock)), dim3(kBlock), 0, stream, p, G,
-                     (int)geo->N, (float2*)gv);
+  hipLaunchKernelGGL(k_fast_gather_gs, dim3(grid_for(std::max(geo->M, geo->N))), dim3(kBlock), 0, stream, p, G,
+                     (int)geo->M, gS, (int)geo->N, (float2*)gv);
+  if (geo->M > 0)
+    hipLaunchKernelGGL(k_fast_bwd, dim3(xcd_grid((geo->N + kBlock - 1) / kBlock)), dim3(kBlock), 0, stream, p, G,
+                       (int)geo->N, (float2*)gv);
   return check_launch("fast_pair_bwd");
 }
 

@@ -166,7 +166,7 @@ __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __rest
 // tile segment inside its range adds the contributions into LDS and flushes the non-zero pixels.
 // kImage, C = 1: value * bilinear corner weight into out (B, H, W), zero padding.
 // kGrid: gout[j * C + c] * corner weight into out (B, C, Hg, Wg).
-constexpr int kAccItems = 8;
+constexpr int kAccItems = 2;
 constexpr int kAccRange = kAccBlock * kAccItems;
 
 template <int MODE, int C>

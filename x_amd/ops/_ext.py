@@ -122,7 +122,8 @@ def exported_symbols():
     return sorted(_SIGS) + ["atl_last_error", "atl_abi_version"]
 
 
-_TIMED = {}          # entry point -> list of (start, end, events) per call, while kernel timing is on
+_TIMED = {}          # entry point -> list of (start, end, events) per timed call, while kernel timing is on
+_EVERY = {"n": 1, "calls": {}}   # time one call in n of each entry point
 # position of the event count N in the arguments of the entry points whose calls are sized by it
 _NARG = {"atl_sample_grid_fwd": 7, "atl_sample_grid_bwd_planned": 6, "atl_sample_grid_bwd_pos": 8,
          "atl_splat_gauss_fwd": 3, "atl_splat_gauss_bwd": 4, "atl_splat_gauss_fwd_ws": 3,
@@ -130,21 +131,33 @@ _NARG = {"atl_sample_grid_fwd": 7, "atl_sample_grid_bwd_planned": 6, "atl_sample
          "atl_splat_bilinear_bwd": 4}
 
 
-def time_kernels(names) -> dict:
-    """Bracket every later call of the named entry points with events on the caller's current stream (the
-    stream the kernels run on); returns the live {name: [(start, end, events), ...]} record (events: the
-    call's event count where the entry point has one, else None).  ``time_kernels(())``
-    turns timing off."""
+def time_kernels(names, every: int = 1) -> dict:
+    """Bracket later calls of the named entry points (the first call and then one in ``every``) with events on
+    the caller's current stream (the stream the kernels run on); returns the live {name: [(start, end, events),
+    ...]} record (events: the call's event count where the entry point has one, else None).  Each bracket
+    holds the next launch back by a few microseconds, hence the sampling.  ``time_kernels(())`` turns timing
+    off."""
     _TIMED.clear()
+    _EVERY["n"], _EVERY["calls"] = max(int(every), 1), {}
     for n in names:
         _TIMED[n] = []
     return _TIMED
+
+
+def timed_calls() -> dict:
+    """Calls of each timed entry point since time_kernels (sampled or not)."""
+    return dict(_EVERY["calls"])
 
 
 def call(name: str, *args):
     """Invoke a C-ABI entry point; raise HipLibraryError with the library's message on failure."""
     lib = load_library()
     rec = _TIMED.get(name)
+    if rec is not None:
+        i = _EVERY["calls"].get(name, 0)
+        _EVERY["calls"][name] = i + 1
+        if i % _EVERY["n"]:
+            rec = None
     if rec is not None:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()

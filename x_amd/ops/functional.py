@@ -402,7 +402,7 @@ class FastPairPlan:
         gS = _f32(gS)
         if gS.shape != (self.M,):
             raise ValueError(f"gS has shape {tuple(gS.shape)}, expected ({self.M},)")
-        gv = torch.zeros(self.N, 2, dtype=F32, device=self.device)
+        gv = torch.empty(self.N, 2, dtype=F32, device=self.device)
         with torch.cuda.device(self.device):
             call("atl_fast_pair_bwd", ctypes.byref(self.geo), ptr(self.ws), ptr(gS), ptr(gv), stream_of(gv))
         return gv
