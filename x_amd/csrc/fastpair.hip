@@ -44,6 +44,7 @@ namespace {
 constexpr int kMinBucketShift = 10;
 constexpr int kMaxBucketShift = 13;
 constexpr int kMaxBuckets = 16384;
+static_assert(kMaxBuckets <= kScanSmallMax, "bucket totals are scanned by one workgroup");
 constexpr int kSortBlock = 512;                    // pass-2 workgroup
 constexpr int kP1Block = 1024;                     // pass-1 workgroup
 constexpr int kSrcPerBlock = 4096;                 // pass-1 sources per block (4 per thread)
@@ -211,26 +212,37 @@ __global__ void __launch_bounds__(kBlock) k_fill_zero(int* __restrict__ p, int64
 }
 
 
+
 // Pass 1.  Blocks [0, nblk_a) cover kAncPerBlock anchors each, blocks [nblk_a, nblk_a + nblk_e) kSrcPerBlock
 // sources each (their entries and one source record keyed by the cell of the own-slice entry).
-// SCATTER = false: per-block bucket histogram into cnt[bucket * nblk + block], and the reductions behind the
+// SCATTER = false: per-block bucket histogram into cnt[block * nbuckets + bucket] (block-major: written and read
+// back coalesced), its non-zero counts added into the bucket totals tot[bucket], and the reductions behind the
 // search radius: vmax over the sources' velocities and max |at| over the anchors (block maxima, one atomic max
-// per block into P, zeroed beforehand; ordered-int encodings of non-negative floats).  SCATTER = true: the
-// block's scanned offsets cnt[bucket * nblk + block] are loaded into LDS once, and each record takes its slot.
+// per block into P, zeroed beforehand; ordered-int encodings of non-negative floats).  SCATTER = true: the block
+// reserves its run of every bucket it feeds with one atomic add on the bucket's position bpos[bucket] (the
+// exclusive scan of the totals; after this pass it holds the bucket's end), keeps the run starts in LDS, and
+// each record takes its slot.  The runs of one bucket follow in no fixed block order; pass 2 orders the bucket.
 template <bool SCATTER>
 __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restrict__ x, const float* __restrict__ t,
                                                        const float2* __restrict__ v, const int64_t* __restrict__ b,
                                                        int64_t N, const int64_t* __restrict__ anchors,
                                                        const float2* __restrict__ anchor_xy, int64_t M, FGeo G,
-                                                       int* __restrict__ cnt, Rec* __restrict__ trec,
-                                                       FParams* __restrict__ P, int* __restrict__ self,
-                                                       int* __restrict__ eself) {
+                                                       int* __restrict__ cnt, int* __restrict__ bsum,
+                                                       Rec* __restrict__ trec, FParams* __restrict__ P,
+                                                       int* __restrict__ self, int* __restrict__ eself) {
   extern __shared__ int hist[];
   __shared__ int red[kP1Block / kWave];
   int vm = 0;                                    // this thread's max ||v|| (sources) or max |at| (anchors)
-  const int nblk = G.nblk_e + G.nblk_a;
   const int blk = blockIdx.x;
-  for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) hist[i] = SCATTER ? cnt[i * nblk + blk] : 0;
+  int* __restrict__ mycnt = cnt + (int64_t)blk * G.nbuckets;
+  for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) {
+    int h = 0;
+    if (SCATTER) {
+      const int c = mycnt[i];
+      if (c > 0) h = atomicAdd(bsum + i, c);   // bsum = bpos: this block's run of bucket i
+    }
+    hist[i] = h;
+  }
   if (!SCATTER && blk == 0 && threadIdx.x == 0 && !anchors) P->unique = 1;
   __syncthreads();
   // anchor blocks first: they are about a quarter of a source block's work, and dispatched last they would
@@ -330,7 +342,11 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
     vm = wave_max_i(vm);
     if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = vm;
     __syncthreads();
-    for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) cnt[i * nblk + blk] = hist[i];
+    for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) {   // bsum = tot
+      const int c = hist[i];
+      mycnt[i] = c;
+      if (c > 0) atomicAdd(bsum + i, c);
+    }
     if (threadIdx.x == 0) {
       for (int w = 1; w < kP1Block / kWave; ++w) vm = max(vm, red[w]);
       if (vm > 0) atomicMax(src_blk ? &P->vmax : &P->atmax, vm);
@@ -361,19 +377,18 @@ __device__ __forceinline__ int anchor_slice(float t, const FGeo& G) {
 }
 
 template <int SHIFT>
-__global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict__ boff, const Rec* __restrict__ trec,
+__global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict__ bend, const Rec* __restrict__ trec,
                                                            FGeo G, SortOut o) {
   int* __restrict__ start = o.start;
   constexpr int kBucketKeys = 1 << SHIFT;
   __shared__ int cnt[kBucketKeys];
   __shared__ int cur[kBucketKeys];
   __shared__ int wsum[kSortBlock / kWave + 1];
-  const int nblk = G.nblk_e + G.nblk_a;
   const int bucket = blockIdx.x;
-  const int lo = boff[bucket * nblk];
-  const int hi = boff[(bucket + 1) * nblk];        // boff has nbuckets * nblk + 1 entries (total last)
+  const int lo = bucket > 0 ? bend[bucket - 1] : 0;  // bend: end of every bucket (bpos after pass 1)
+  const int hi = bend[bucket];
   const int bpk = G.ncell_pad >> SHIFT;            // buckets per key space
-  const int E = boff[bpk * nblk], EA = boff[2 * bpk * nblk];
+  const int E = bend[bpk - 1], EA = bend[2 * bpk - 1];
   const int4* tki = (const int4*)trec;             // int half of record p: tki[2 * p + 1]
   for (int i = threadIdx.x; i < kBucketKeys; i += kSortBlock) {
     cnt[i] = 0;
@@ -1058,10 +1073,11 @@ int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W
   const int64_t nbh = (int64_t)(nbuckets * nblk);
   const int64_t ntmp = g.ecap + M + N;
   int64_t off = 0;
+  // params and the bucket totals are adjacent: one fill clears both
   g.off_params = off;  off += align256(sizeof(FParams));
-  g.off_cnt = off;     off += align256(nbh * 4);
-  g.off_boff = off;    off += align256((nbh + 1) * 4);
-  g.off_part = off;    off += align256((scan_tiles(nbh > 0 ? nbh : 1) + 1) * 4);
+  g.off_part = off;    off += align256((int64_t)nbuckets * 4);        // bucket totals
+  g.off_boff = off;    off += align256((int64_t)nbuckets * 4);        // bucket positions, then bucket ends
+  g.off_cnt = off;     off += align256(nbh * 4);                      // per-block histograms, block-major
   g.off_start = off;   off += align256((3 * g.ncell_pad + 1) * 4);
   g.off_trec = off;    off += align256(ntmp * (int64_t)sizeof(Rec));
   // the walks read up to kUnroll - 1 records past a range end: entry and anchor arrays carry that padding
@@ -1086,27 +1102,25 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
   if ((N > 0 && (!x || !t || !v || !b)) || (M > 0 && !anchors && M != N)) { set_error("fast_plan: null input"); return 1; }
   FParams* P = at_off<FParams>(ws, geo->off_params);
   int* cnt = at_off<int>(ws, geo->off_cnt);
-  int* boff = at_off<int>(ws, geo->off_boff);
-  int* part = at_off<int>(ws, geo->off_part);
+  int* bpos = at_off<int>(ws, geo->off_boff);
+  int* tot = at_off<int>(ws, geo->off_part);
   Rec* trec = at_off<Rec>(ws, geo->off_trec);
   const int nblk = G.nblk_e + G.nblk_a;
-  const int64_t nbh = (int64_t)G.nbuckets * nblk;
-  hipLaunchKernelGGL(k_fill_zero, dim3(1), dim3(64), 0, stream, (int*)P, (int64_t)(sizeof(FParams) / 4));
+  const int64_t nclear = (geo->off_part - geo->off_params) / 4 + G.nbuckets;   // params and bucket totals
+  hipLaunchKernelGGL(k_fill_zero, dim3(grid_for(nclear)), dim3(kBlock), 0, stream, (int*)P, nclear);
   const size_t lds = (size_t)G.nbuckets * sizeof(int);
-  if (nblk > 0) {
+  if (nblk > 0)
     hipLaunchKernelGGL(k_sort_pass1<false>, dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
-                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, (Rec*)nullptr, P,
+                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, tot, (Rec*)nullptr, P,
                        at_off<int>(ws, geo->off_self), at_off<int>(ws, geo->off_eself));
-    scan32(cnt, nbh, part, boff, stream);
+  scan_small(tot, G.nbuckets, bpos, stream);
+  if (nblk > 0)
     hipLaunchKernelGGL(k_sort_pass1<true>, dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
-                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, boff, trec, (FParams*)nullptr,
-                       (int*)nullptr, (int*)nullptr);
-  } else {
-    hipLaunchKernelGGL(k_fill_zero, dim3(1), dim3(64), 0, stream, boff, (int64_t)1);
-  }
+                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, bpos, trec,
+                       (FParams*)nullptr, (int*)nullptr, (int*)nullptr);
   auto pass2 = G.bshift == 10 ? k_sort_pass2<10> : G.bshift == 11 ? k_sort_pass2<11>
              : G.bshift == 12 ? k_sort_pass2<12> : k_sort_pass2<13>;
-  hipLaunchKernelGGL(pass2, dim3(G.nbuckets), dim3(kSortBlock), 0, stream, (const int*)boff,
+  hipLaunchKernelGGL(pass2, dim3(G.nbuckets), dim3(kSortBlock), 0, stream, (const int*)bpos,
                      (const Rec*)trec, G,
                      SortOut{at_off<int>(ws, geo->off_start), at_off<float4>(ws, geo->off_epos),
                              at_off<float>(ws, geo->off_etim), at_off<int>(ws, geo->off_eself),

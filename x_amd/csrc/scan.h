@@ -1,6 +1,6 @@
-// Device-wide exclusive scan of int32 counts (two launches: per-tile totals, then a per-tile rescan that
-// first sums the totals of the tiles before its own), shared by the plan builders.  Tiles are
-// kScanTile = 2048 counts.
+// Device-wide exclusive scans of int32 counts shared by the plan builders: scan32 (two launches: per-tile
+// totals, then a per-tile rescan that first sums the totals of the tiles before its own; tiles of
+// kScanTile = 2048 counts) and scan_small (up to 16384 counts in one workgroup).
 #pragma once
 #include "common.h"
 
@@ -58,6 +58,37 @@ inline void scan32(const int* in, int64_t n, int* part, int* out, hipStream_t st
   const int64_t tiles = scan_tiles(n);
   hipLaunchKernelGGL(k_scan32_reduce, dim3((unsigned)tiles), dim3(kBlock), 0, stream, in, n, part);
   hipLaunchKernelGGL(k_scan32_write, dim3((unsigned)tiles), dim3(kBlock), 0, stream, in, n, (const int*)part, out);
+}
+
+// Exclusive scan of n <= kScanSmallMax counts (bucket or tile totals) into their start positions: one
+// workgroup, one launch.
+constexpr int kScanSmallBlock = 1024;
+constexpr int kScanSmallMax = 16384;
+
+__global__ void __launch_bounds__(kScanSmallBlock) k_scan_small(const int* __restrict__ tot, int n,
+                                                                int* __restrict__ pos) {
+  __shared__ int wsum[kScanSmallBlock / kWave + 1];
+  constexpr int kPer = kScanSmallMax / kScanSmallBlock;
+  int v[kPer];
+  int s = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = threadIdx.x * kPer + k;
+    v[k] = i < n ? tot[i] : 0;
+    s += v[k];
+  }
+  int total;
+  int run = block_exclusive_scan<kScanSmallBlock>(s, wsum, total);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = threadIdx.x * kPer + k;
+    if (i < n) pos[i] = run;
+    run += v[k];
+  }
+}
+
+inline void scan_small(const int* tot, int n, int* pos, hipStream_t stream) {
+  hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(kScanSmallBlock), 0, stream, tot, n, pos);
 }
 
 }  // namespace
