@@ -200,6 +200,10 @@ int atl_check_sorted(const float* t, const int64_t* b, int64_t N, int* flag, hip
  * accumulated. */
 int atl_bin_counts(const float* t, const int64_t* b, int64_t N, int64_t B, int64_t n_check, float* counts,
                    hipStream_t stream);
+/* The same counts for events sorted by (b, t) (the EventPacket order): counts (B, n_check) written (no fill
+ * needed), by binary searches for the bin edges of every batch instead of a pass with atomics. */
+int atl_bin_counts_sorted(const float* t, const int64_t* b, int64_t N, int64_t B, int64_t n_check, float* counts,
+                          hipStream_t stream);
 /* visible_fraction for linear motion (atl/objectives/ats.py:31-50): anchors xa (M,2) with velocities va (M,2)
  * transported to the bin centres (n_check floats), out (M) written. */
 int atl_visible_fraction(const float* xa, const float* va, const float* ta, const int64_t* ba, int64_t M,

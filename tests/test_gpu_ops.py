@@ -277,14 +277,35 @@ def test_window_counts_bit_exact():
     assert np.array_equal(N(got), O.window_counts(t[perm], b[perm], idx, 0.2))
 
 
-def test_visible_fraction_bit_exact():
+@pytest.mark.parametrize("sorted_path", [False, True])
+def test_visible_fraction_bit_exact(sorted_path):
     win, xs, v, anchors, xa = _pair_case(seed=6)
     grid = win.motion["grid"]
     va, _, _ = O.dense_velocity(grid, xa, win.b[anchors], 40, 48)
     got = F.visible_fraction_linear(T(xa), T(va), T(win.t[anchors]), T(win.b[anchors]), T(win.t), T(win.b), 2, 40,
-                                    48, 0.2)
+                                    48, 0.2, assume_sorted=sorted_path)
     want = O.visible_fraction_dense(grid, xa, win.t[anchors], win.b[anchors], win.t, win.b, 2, 40, 48, 0.2)
     assert np.array_equal(N(got), want)
+
+
+@pytest.mark.parametrize("n_check", [16, 10, 1])
+def test_bin_counts_sorted_matches_index_put(n_check):
+    """Counts per (batch, time bin) from the bin-edge searches over (b, t)-sorted events vs the reference's
+    index_put accumulate (atl/objectives/ats.py:39-41): times on bin edges, below 0, at and above 1, an empty
+    batch."""
+    rng = np.random.default_rng(3)
+    B = 4
+    t = np.concatenate([rng.random(30000), np.arange(n_check + 1) / n_check, [-0.5, -1e-7, 1.0, 1.5, 7.0]])
+    t = t.astype(F32)
+    b = rng.choice([0, 1, 3], size=t.size).astype(np.int64)           # batch 2 empty
+    order = np.lexsort((t, b))
+    t, b = t[order], b[order]
+    sl = np.clip(torch.as_tensor(t * F32(n_check)).long().numpy(), 0, n_check - 1)
+    want = np.zeros((B, n_check), np.float32)
+    np.add.at(want, (b, sl), 1.0)
+    got_sorted = N(F.bin_counts(T(t), T(b), B, n_check, assume_sorted=True))
+    got_atomic = N(F.bin_counts(T(t), T(b), B, n_check, assume_sorted=False))
+    assert np.array_equal(got_sorted, want) and np.array_equal(got_atomic, want)
 
 
 def test_anchored_exact_end_to_end():

@@ -34,7 +34,8 @@ def visible_fraction(motion, xa, ta, ba, ev: EventPacket, tau: float, n_check: i
     if xa.is_cuda and getattr(motion, "linear_at_event", False):
         with torch.no_grad():
             va = motion.velocity(xa, ta, ba)
-        return visible_fraction_linear(xa, va, ta, ba, ev.t, ev.b, ev.batch_size, ev.height, ev.width, tau, n_check)
+        return visible_fraction_linear(xa, va, ta, ba, ev.t, ev.b, ev.batch_size, ev.height, ev.width, tau, n_check,
+                                       assume_sorted=bool(ev.meta.get("sorted")))
     edges = torch.linspace(0, 1, n_check + 1, device=ev.device)
     centres = 0.5 * (edges[:-1] + edges[1:])
     sl = torch.clamp((ev.t * n_check).long(), 0, n_check - 1)

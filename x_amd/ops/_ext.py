@@ -53,6 +53,7 @@ _SIGS = {
     "atl_window_counts": [_P, _P, _I, _P, _I, _D, _P, _P],
     "atl_check_sorted": [_P, _P, _I, _P, _P],
     "atl_bin_counts": [_P, _P, _I, _I, _I, _P, _P],
+    "atl_bin_counts_sorted": [_P, _P, _I, _I, _I, _P, _P],
     "atl_visible_fraction": [_P, _P, _P, _P, _I, _P, _P, _I, _I, _D, _I, _I, _P, _P],
     "atl_anchored_epilogue_fwd": [_P, _P, _P, _I, _D, _D, _P, _P, _P, _P],
     "atl_anchored_epilogue_bwd": [_P, _P, _P, _I, _P, _P],

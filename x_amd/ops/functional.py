@@ -530,18 +530,34 @@ def event_noise(xy: torch.Tensor, seed: int, offset: int, h: float, dequantize: 
     return xs, xa
 
 
-def visible_fraction_linear(xa, va, ta, ba, t_all, b_all, B, H, W, tau, n_check=16):
+def bin_counts(t_all, b_all, B, n_check=16, assume_sorted: bool = False) -> torch.Tensor:
+    """Events per (batch, time bin) (atl/objectives/ats.py:37-41): a (B, n_check) float tensor.  With events
+    sorted by (b, t) the counts come from binary searches for the bin edges; otherwise from a pass with
+    atomics."""
+    t_all, b_all = _f32(t_all), b_all.contiguous().long()
+    dev = t_all.device
+    with torch.cuda.device(dev):
+        if assume_sorted:
+            counts = torch.empty(B, n_check, dtype=F32, device=dev)
+            call("atl_bin_counts_sorted", ptr(t_all), ptr(b_all), t_all.shape[0], B, n_check, ptr(counts),
+                 stream_of(t_all))
+        else:
+            counts = torch.zeros(B, n_check, dtype=F32, device=dev)
+            call("atl_bin_counts", ptr(t_all), ptr(b_all), t_all.shape[0], B, n_check, ptr(counts), stream_of(t_all))
+    return counts
+
+
+def visible_fraction_linear(xa, va, ta, ba, t_all, b_all, B, H, W, tau, n_check=16, assume_sorted: bool = False):
     """Exposure correction of atl/objectives/ats.py:31-50 for motion linear at the event: anchors (xa, ta, ba)
-    with velocities ``va`` transported to the n_check bin centres.  No grad."""
+    with velocities ``va`` transported to the n_check bin centres.  ``assume_sorted``: the events (t_all,
+    b_all) are sorted by (b, t).  No grad."""
     dev = xa.device
     xa, va, ta, ba = _f32(xa), _f32(va), _f32(ta), ba.contiguous().long()
-    t_all, b_all = _f32(t_all), b_all.contiguous().long()
-    counts = torch.zeros(B, n_check, dtype=F32, device=dev)
+    counts = bin_counts(t_all, b_all, B, n_check, assume_sorted)
     out = torch.empty(ta.shape[0], dtype=F32, device=dev)
     centres = bin_centres(n_check, dev)
     with torch.cuda.device(dev):
         st = stream_of(xa)
-        call("atl_bin_counts", ptr(t_all), ptr(b_all), t_all.shape[0], B, n_check, ptr(counts), st)
         call("atl_visible_fraction", ptr(xa), ptr(va), ptr(ta), ptr(ba), ta.shape[0], ptr(counts), ptr(centres), B,
              n_check, float(tau), int(H), int(W), ptr(out), st)
     return out
