@@ -5,9 +5,7 @@
 // Device-wide float atomics are resolved in the memory fabric on this multi-XCD part and run at ~25 G/s when
 // scattered, and events concentrated on edges put many of them on the same pixels.  Here every call:
 //   1. bins the events by the 16x16 (or 32x32) tile of their base corner: an LDS histogram per block of 4096
-//      events (kept block-major, its counts added into per-tile totals), a scan of the totals, and a scatter
-//      of 16-byte records (x, y, value, event index) into tile order, each block reserving its run of every
-//      tile with one atomic add;
+//      events, a device scan, and a scatter of 16-byte records (x, y, value, event index) into tile order;
 //   2. splits the tile-ordered records into equal ranges, one per workgroup, which adds the weighted
 //      contributions of each tile segment of its range into an LDS copy of the (T+1) x (T+1) pixels they can
 //      reach (corners reach one past the tile);
@@ -29,7 +27,6 @@ namespace {
 constexpr int kTilePerBlock = 4096;              // binning: events per block
 constexpr int kTileBinBlock = 512;               // binning: threads per block (8 events each)
 constexpr int kTileMaxKeys = 16384;              // LDS histogram capacity (tiles over all batches)
-static_assert(kTileMaxKeys <= kScanSmallMax, "tile totals are scanned by one workgroup");
 constexpr int kAccBlock = 256;                   // accumulation: threads per tile
 constexpr int kMaxChannels = 32;                 // field channels of the tile adjoint (LDS: C x 17 x 17 floats)
 
@@ -123,27 +120,16 @@ __device__ __forceinline__ int tile_key(float x, float y, int64_t b, const TileG
   return ((int)b * g.TY + ty) * g.TX + tx;
 }
 
-// Binning.  SCATTER = false: per-block tile histogram into cnt[block * nkeys + key] and its non-zero counts
-// added into tot[key].  SCATTER = true: the block reserves its run of every tile it feeds with one atomic add
-// on tot = the tile's position (the scanned totals; afterwards the tile's end), and every event writes
-// (x, y, value, index) to its slot.
+// Binning.  SCATTER = false: per-block tile histogram into cnt[key * nblk + block].  SCATTER = true: the
+// block's scanned offsets are loaded into LDS and every event writes (x, y, value, index) to its slot.
 template <int MODE, bool SCATTER>
 __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __restrict__ pos,
                                                             const int64_t* __restrict__ bidx,
                                                             const float* __restrict__ val, TileGeo g,
-                                                            int* __restrict__ cnt, int* __restrict__ tot,
-                                                            float4* __restrict__ rec) {
+                                                            int* __restrict__ cnt, float4* __restrict__ rec) {
   extern __shared__ int hist[];
   const int blk = blockIdx.x;
-  int* __restrict__ mycnt = cnt + (int64_t)blk * g.nkeys;
-  for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) {
-    int h = 0;
-    if (SCATTER) {
-      const int c = mycnt[i];
-      if (c > 0) h = atomicAdd(tot + i, c);
-    }
-    hist[i] = h;
-  }
+  for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) hist[i] = SCATTER ? cnt[i * g.nblk + blk] : 0;
   __syncthreads();
   constexpr int per = kTilePerBlock / kTileBinBlock;
   const int j0 = blk * kTilePerBlock;
@@ -171,11 +157,7 @@ __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __rest
   }
   if (!SCATTER) {
     __syncthreads();
-    for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) {
-      const int c = hist[i];
-      mycnt[i] = c;
-      if (c > 0) atomicAdd(tot + i, c);
-    }
+    for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) cnt[i * g.nblk + blk] = hist[i];
   }
 }
 
@@ -251,7 +233,7 @@ __device__ __forceinline__ void accum_record(const float4& q, const float* __res
 }
 
 template <int MODE, int C, int T>
-__global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict__ tend,
+__global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict__ boff,
                                                           const float4* __restrict__ rec,
                                                           const float* __restrict__ gout, TileGeo g,
                                                           float* __restrict__ out) {
@@ -260,11 +242,11 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict_
   const int nc = C > 0 ? C : g.C;
   __shared__ int ts[kAccBlock + 1];                       // starts of the tiles first .. first + kAccBlock
   __shared__ int found, found2;
-  const int total = tend[g.nkeys - 1];
+  const int total = boff[g.nkeys * g.nblk];
   const int r0 = blockIdx.x * kAccRange;
   if (r0 >= total) return;
   const int r1 = min(r0 + kAccRange, total);
-  auto tstart = [&](int k) { return k > 0 ? tend[min(k, g.nkeys) - 1] : 0; };   // tile k's first record; nkeys: total
+  auto tstart = [&](int k) { return boff[min(k, g.nkeys) * g.nblk]; };   // tile k's first record; nkeys: total
   // the last tile starting at or before r0, in two parallel rounds (coarse stride, then within the stride)
   const int step = (g.nkeys + kAccBlock - 1) / kAccBlock;
   if (threadIdx.x == 0) {
@@ -395,42 +377,39 @@ bool tile_geo(int mode, int64_t B, int64_t H, int64_t W, int64_t N, int64_t img_
 }
 
 struct TileLayout {
-  int64_t cnt, tot, pos, rec, bytes;
+  int64_t cnt, boff, part, rec, bytes;
 };
 
 TileLayout tile_layout(const TileGeo& g) {
   TileLayout L;
   const int64_t nbh = (int64_t)g.nkeys * g.nblk;
   int64_t off = 0;
-  L.tot = off;  off += align256((int64_t)g.nkeys * 4);      // tile totals
-  L.pos = off;  off += align256((int64_t)g.nkeys * 4);      // tile positions, then tile ends
-  L.cnt = off;  off += align256(nbh * 4);                   // per-block histograms, block-major
+  L.cnt = off;  off += align256(nbh * 4);
+  L.boff = off; off += align256((nbh + 1) * 4);
+  L.part = off; off += align256((scan_tiles(nbh > 0 ? nbh : 1) + 1) * 4);
   L.rec = off;  off += align256((int64_t)g.N * 16);
   L.bytes = off;
   return L;
 }
 
-__global__ void __launch_bounds__(kBlock) k_tile_zero(int* __restrict__ p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
+__global__ void k_tile_zero1(int* p) { p[0] = 0; }
 
 template <int MODE>
 void tile_bin(const TileGeo& g, const TileLayout& L, void* ws, const float* pos, const int64_t* b, const float* val,
               hipStream_t stream) {
   char* w = (char*)ws;
   int* cnt = (int*)(w + L.cnt);
-  int* tot = (int*)(w + L.tot);
-  int* tpos = (int*)(w + L.pos);
-  hipLaunchKernelGGL(k_tile_zero, dim3((g.nkeys + kBlock - 1) / kBlock), dim3(kBlock), 0, stream, tot, g.nkeys);
+  int* boff = (int*)(w + L.boff);
+  if (g.nblk == 0) {
+    hipLaunchKernelGGL(k_tile_zero1, dim3(1), dim3(1), 0, stream, boff);
+    return;
+  }
   const size_t lds = (size_t)g.nkeys * sizeof(int);
-  if (g.nblk > 0)
-    hipLaunchKernelGGL((k_tile_bin<MODE, false>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream,
-                       (const float2*)pos, b, val, g, cnt, tot, (float4*)nullptr);
-  scan_small(tot, g.nkeys, tpos, stream);
-  if (g.nblk > 0)
-    hipLaunchKernelGGL((k_tile_bin<MODE, true>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream,
-                       (const float2*)pos, b, val, g, cnt, tpos, (float4*)(w + L.rec));
+  hipLaunchKernelGGL((k_tile_bin<MODE, false>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
+                     b, val, g, cnt, (float4*)nullptr);
+  scan32(cnt, (int64_t)g.nkeys * g.nblk, (int*)(w + L.part), boff, stream);
+  hipLaunchKernelGGL((k_tile_bin<MODE, true>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
+                     b, val, g, boff, (float4*)(w + L.rec));
 }
 
 template <int MODE, int C>
@@ -444,10 +423,10 @@ void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const flo
   const size_t lds = (size_t)nc * edge * edge * sizeof(float);
   if (g.T == 16)
     hipLaunchKernelGGL((k_tile_accum<MODE, C, 16>), dim3(grid), dim3(kAccBlock), lds, stream,
-                       (const int*)(w + L.pos), (const float4*)(w + L.rec), gout, g, out);
+                       (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, out);
   else
     hipLaunchKernelGGL((k_tile_accum<MODE, C, 32>), dim3(grid), dim3(kAccBlock), lds, stream,
-                       (const int*)(w + L.pos), (const float4*)(w + L.rec), gout, g, out);
+                       (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, out);
 }
 
 }  // namespace
