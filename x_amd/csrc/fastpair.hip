@@ -517,6 +517,8 @@ __device__ __forceinline__ bool pair_test(int id_a, int id_s, float ta, float ts
 // lane, and that is what bounds it.  Backward: one lane per source walks its own neighbourhoods (sources'
 // per-slice positions differ, so a group shares less there than it costs to set up).
 
+constexpr int kBwdParts = 2;                       // backward lanes per source (each walks part of its slices)
+static_assert(kBwdParts == 1 || kBwdParts == 2 || kBwdParts == 4, "a source's parts are combined by a butterfly");
 constexpr int kGroup = 8;                          // queries evaluated per pass over a group's candidates
 constexpr int kGroupCells = 4;                     // a forward group spans up to this many cells of one row
 
@@ -893,13 +895,19 @@ __global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int 
 // compares event ids instead, as the reference does.
 template <bool DUP>
 __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, float R, float R2, float4 sr, int sid,
-                                             float tj, int key, int sp, int2* tab) {
+                                             float tj, int key, int sp, int part, int2* tab) {
   const int plane_cells = G.GH * G.GW;
   const int* astart = p.start + G.ncell_pad;
   const int E = uni(p.start[G.ncell_pad]);
   const int* aid = (const int*)p.arec + 4;         // event id of record k: aid[8 * k]
   int lo_l, hi_l;
   slice_range(tj, G, lo_l, hi_l);
+  if (kBwdParts > 1) {                             // part p of kBwdParts: its share of the slices, in order
+    const int L = max(hi_l - lo_l + 1, 0);
+    const int a = lo_l + (part * L) / kBwdParts, b = lo_l + ((part + 1) * L) / kBwdParts - 1;
+    lo_l = a;
+    hi_l = b;
+  }
   const int bj = key / (G.S * plane_cells);
   float mgx = 0.f, mgy = 0.f;
   for (int s = lo_l; s <= hi_l; ++s) {
@@ -943,20 +951,22 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
 // gv[j] = the total (each source has one record: no atomics).
 __global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, float2* __restrict__ gv) {
   __shared__ int2 tab[kRowTab * kBlock];           // per-lane row spans of the current slice (column threadIdx.x)
-  const int lb = xcd_block((N + kBlock - 1) / kBlock);
+  constexpr int kSrcPerWave = kWave / kBwdParts;
+  const int lb = xcd_block((N + kBlock / kBwdParts - 1) / (kBlock / kBwdParts));
   if (lb < 0) return;
   const int lane = threadIdx.x & (kWave - 1);
-  const int wbase = lb * kBlock + (threadIdx.x & ~(kWave - 1));
+  const int part = lane / kSrcPerWave, ls = lane - part * kSrcPerWave;
+  const int wbase = (lb * (kBlock / kWave) + (int)(threadIdx.x / kWave)) * kSrcPerWave;
   const int EA = uni(p.start[2 * G.ncell_pad]);
   const int Nv = uni(p.start[3 * G.ncell_pad]) - EA;
   if (wbase >= Nv) return;
-  const int n = min(kWave, Nv - wbase);
+  const int n = min(kSrcPerWave, Nv - wbase);
   float R, R2;
   search_radius(p.P, G, R, R2);
   R = unif(R);
   R2 = unif(R2);
-  if (lane >= n) return;
-  const Rec SR = p.srec[wbase + lane];
+  const bool have = ls < n;
+  const Rec SR = p.srec[wbase + min(ls, n - 1)];
   const int4 si = SR.i;
   const float tj = __int_as_float(si.x);
   // this source's own search radius: its entries all move with its own velocity, |v_j| * max|at| <= vmax * max|at|
@@ -970,9 +980,16 @@ __global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, flo
   }
   const int sp = p.self[si.y];
   int2* mytab = tab + threadIdx.x;
-  const float2 m = uni(p.P->dup) ? bwd_source<true>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, mytab)
-                                 : bwd_source<false>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, mytab);
-  gv[si.y] = m;
+  float2 m = make_float2(0.f, 0.f);
+  if (have)
+    m = uni(p.P->dup) ? bwd_source<true>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, part, mytab)
+                      : bwd_source<false>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, part, mytab);
+#pragma unroll
+  for (int o = kSrcPerWave; o < kWave; o <<= 1) {  // the parts of a source sit kSrcPerWave lanes apart
+    m.x += __shfl_xor(m.x, o);
+    m.y += __shfl_xor(m.y, o);
+  }
+  if (have && part == 0) gv[si.y] = m;
 }
 
 // ------------------------------------------------------------------------------------------ host side
@@ -1158,8 +1175,8 @@ int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, f
   hipLaunchKernelGGL(k_fast_gather_gs, dim3(grid_for(std::max(geo->M, geo->N))), dim3(kBlock), 0, stream, p, G,
                      (int)geo->M, gS, (int)geo->N, (float2*)gv);
   if (geo->M > 0)
-    hipLaunchKernelGGL(k_fast_bwd, dim3(xcd_grid((geo->N + kBlock - 1) / kBlock)), dim3(kBlock), 0, stream, p, G,
-                       (int)geo->N, (float2*)gv);
+    hipLaunchKernelGGL(k_fast_bwd, dim3(xcd_grid((geo->N + kBlock / kBwdParts - 1) / (kBlock / kBwdParts))),
+                       dim3(kBlock), 0, stream, p, G, (int)geo->N, (float2*)gv);
   return check_launch("fast_pair_bwd");
 }
 
