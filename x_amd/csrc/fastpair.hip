@@ -128,7 +128,7 @@ __device__ __forceinline__ T ld(const T* base, uint32_t i) {
 // Workgroup index such that runs of kXcdRun consecutive logical blocks (neighbouring cells) execute on one
 // XCD and share its L2, while the runs still alternate over the XCDs (the hardware places workgroup w on
 // XCD w % 8) so that every XCD sees every part of the problem.  -1 for the padding blocks of the last group.
-constexpr int kXcdRun = 16;
+constexpr int kXcdRun = 64;
 __device__ __forceinline__ int xcd_block(int nblocks) {
   const int w = blockIdx.x;
   const int grp = w / (kXcd * kXcdRun), rem = w - grp * (kXcd * kXcdRun);
@@ -517,6 +517,7 @@ __device__ __forceinline__ bool pair_test(int id_a, int id_s, float ta, float ts
 // lane, and that is what bounds it.  Backward: one lane per source walks its own neighbourhoods (sources'
 // per-slice positions differ, so a group shares less there than it costs to set up).
 
+constexpr int kPairBlock = 64;                     // workgroup of the pair walks
 constexpr int kBwdParts = 2;                       // backward lanes per source (each walks part of its slices)
 static_assert(kBwdParts == 1 || kBwdParts == 2 || kBwdParts == 4, "a source's parts are combined by a butterfly");
 constexpr int kGroup = 8;                          // queries evaluated per pass over a group's candidates
@@ -617,7 +618,7 @@ __device__ __forceinline__ void walk_flat(const int* __restrict__ cstart, int ba
     }
   }
 #pragma unroll
-  for (int i = 0; i < kRowTab; ++i) tab[i * kBlock] = make_int2(kk[i] - base, ee[i] - base);
+  for (int i = 0; i < kRowTab; ++i) tab[i * kPairBlock] = make_int2(kk[i] - base, ee[i] - base);
   int ri = 0;                                      // row of cur; nxt holds row ri + 1 (read one row ahead)
   int2 cur = make_int2(kk[0] - base, ee[0] - base);
   int2 nxt = make_int2(kk[1] - base, ee[1] - base);
@@ -626,7 +627,7 @@ __device__ __forceinline__ void walk_flat(const int* __restrict__ cstart, int ba
       do {
         cur = nxt;
         ++ri;
-        nxt = ri + 1 < nrows ? tab[(ri + 1) * kBlock] : make_int2(0, 0);
+        nxt = ri + 1 < nrows ? tab[(ri + 1) * kPairBlock] : make_int2(0, 0);
       } while (cur.x >= cur.y && ri < nrows - 1);
       if (cur.x >= cur.y) break;
     }
@@ -811,15 +812,15 @@ __device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plan
 // smaller units let the hardware's wave queue even out dense and sparse regions: 16 anchors per wave run the
 // C3 forward in 365 us against 410 us with 64 (32: 379 us; 8 or 12: as 16; 4: 390 us).
 constexpr int kAnchorsPerWave = 16;
-constexpr int kAnchorsPerBlock = kBlock / kWave * kAnchorsPerWave;
+constexpr int kAnchorsPerBlock = kPairBlock / kWave * kAnchorsPerWave;
 
 template <bool COUNT>
-__global__ void __launch_bounds__(kBlock) k_fast_fwd(FPlan p, FGeo G, int M, float* __restrict__ out,
+__global__ void __launch_bounds__(kPairBlock) k_fast_fwd(FPlan p, FGeo G, int M, float* __restrict__ out,
                                                      int* __restrict__ count) {
   const int lb = xcd_block((M + kAnchorsPerBlock - 1) / kAnchorsPerBlock);
   if (lb < 0) return;
   const int lane = threadIdx.x & (kWave - 1);
-  const int wbase = (lb * (kBlock / kWave) + (int)(threadIdx.x / kWave)) * kAnchorsPerWave;
+  const int wbase = (lb * (kPairBlock / kWave) + (int)(threadIdx.x / kWave)) * kAnchorsPerWave;
   const int E = uni(p.start[G.ncell_pad]);
   const int Mv = uni(p.start[2 * G.ncell_pad]) - E;
   if (wbase >= Mv) return;
@@ -949,14 +950,14 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
 // Backward: every source (one lane each, own-slice tile order) sums, over the anchors of each slice of its
 // range within R of its slice-centre position, gS_i * k * dt / h^2 * r (csrc/atl_cpu.cpp:240-248);
 // gv[j] = the total (each source has one record: no atomics).
-__global__ void __launch_bounds__(kBlock) k_fast_bwd(FPlan p, FGeo G, int N, float2* __restrict__ gv) {
-  __shared__ int2 tab[kRowTab * kBlock];           // per-lane row spans of the current slice (column threadIdx.x)
+__global__ void __launch_bounds__(kPairBlock) k_fast_bwd(FPlan p, FGeo G, int N, float2* __restrict__ gv) {
+  __shared__ int2 tab[kRowTab * kPairBlock];           // per-lane row spans of the current slice (column threadIdx.x)
   constexpr int kSrcPerWave = kWave / kBwdParts;
-  const int lb = xcd_block((N + kBlock / kBwdParts - 1) / (kBlock / kBwdParts));
+  const int lb = xcd_block((N + kPairBlock / kBwdParts - 1) / (kPairBlock / kBwdParts));
   if (lb < 0) return;
   const int lane = threadIdx.x & (kWave - 1);
   const int part = lane / kSrcPerWave, ls = lane - part * kSrcPerWave;
-  const int wbase = (lb * (kBlock / kWave) + (int)(threadIdx.x / kWave)) * kSrcPerWave;
+  const int wbase = (lb * (kPairBlock / kWave) + (int)(threadIdx.x / kWave)) * kSrcPerWave;
   const int EA = uni(p.start[2 * G.ncell_pad]);
   const int Nv = uni(p.start[3 * G.ncell_pad]) - EA;
   if (wbase >= Nv) return;
@@ -1160,9 +1161,9 @@ int atl_fast_pair_fwd(const atl_fast_geometry* geo, const void* ws, float* out, 
   const FPlan p = make_plan((void*)ws, geo);
   const unsigned grid = xcd_grid((geo->M + kAnchorsPerBlock - 1) / kAnchorsPerBlock);
   if (count)
-    hipLaunchKernelGGL(k_fast_fwd<true>, dim3(grid), dim3(kBlock), 0, stream, p, G, (int)geo->M, out, count);
+    hipLaunchKernelGGL(k_fast_fwd<true>, dim3(grid), dim3(kPairBlock), 0, stream, p, G, (int)geo->M, out, count);
   else
-    hipLaunchKernelGGL(k_fast_fwd<false>, dim3(grid), dim3(kBlock), 0, stream, p, G, (int)geo->M, out, count);
+    hipLaunchKernelGGL(k_fast_fwd<false>, dim3(grid), dim3(kPairBlock), 0, stream, p, G, (int)geo->M, out, count);
   return check_launch("fast_pair_fwd");
 }
 
@@ -1175,8 +1176,8 @@ int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, f
   hipLaunchKernelGGL(k_fast_gather_gs, dim3(grid_for(std::max(geo->M, geo->N))), dim3(kBlock), 0, stream, p, G,
                      (int)geo->M, gS, (int)geo->N, (float2*)gv);
   if (geo->M > 0)
-    hipLaunchKernelGGL(k_fast_bwd, dim3(xcd_grid((geo->N + kBlock / kBwdParts - 1) / (kBlock / kBwdParts))),
-                       dim3(kBlock), 0, stream, p, G, (int)geo->N, (float2*)gv);
+    hipLaunchKernelGGL(k_fast_bwd, dim3(xcd_grid((geo->N + kPairBlock / kBwdParts - 1) / (kPairBlock / kBwdParts))),
+                       dim3(kPairBlock), 0, stream, p, G, (int)geo->N, (float2*)gv);
   return check_launch("fast_pair_bwd");
 }
 
