@@ -558,6 +558,45 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return __builtin_amdgcn_readlane(v, 63);
 }
 
+// Sums over the 64 lanes of WD values at once, returned wave-uniform.  gfx950's lane swaps fold pairs of values
+// together: permlane32_swap(a, b) + its partner gives a's 32-lane partial sums in lanes 0-31 and b's in 32-63;
+// permlane16_swap then folds two such vectors into four 16-lane rows (a, c, b, d for the pairs (a, b), (c, d)),
+// and four DPP steps sum each row.  Eight values cost 20 VALU operations instead of 8 tree reductions of 6.
+__device__ __forceinline__ float fold32(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(a), __float_as_int(b), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+__device__ __forceinline__ float fold16(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(a), __float_as_int(b), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dppf<0xB1, 0xF>(v);                       // quad_perm [1, 0, 3, 2]
+  v += dppf<0x4E, 0xF>(v);                       // quad_perm [2, 3, 0, 1]
+  v += dppf<0x141, 0xF>(v);                      // row_half_mirror
+  v += dppf<0x140, 0xF>(v);                      // row_mirror: every lane holds its row's sum
+  return v;
+}
+template <int WD>
+__device__ __forceinline__ void multi_sum_f(const float (&v)[WD], float (&out)[WD]) {
+  if (WD == 1) {
+    out[0] = wave_sum_f(v[0]);
+    return;
+  }
+  constexpr int kQ = (WD + 3) / 4;               // vectors of four values after the two folds
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    auto at = [&](int k) { return 4 * q + k < WD ? v[4 * q + k] : 0.f; };
+    const float w0 = fold32(at(0), at(1));
+    const float w1 = 4 * q + 2 < WD ? fold32(at(2), at(3)) : 0.f;
+    const float x = row_sum16(fold16(w0, w1));   // rows: values 4q, 4q + 2, 4q + 1, 4q + 3
+    constexpr int kLane[4] = {0, 32, 16, 48};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (4 * q + k < WD) out[4 * q + k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), kLane[k]));
+  }
+}
+
 // Inclusive prefix sum over the 64 lanes.
 __device__ __forceinline__ int wave_incl_scan(int v) {
   v += dpp<0x111, 0xF>(v);                       // row_shr:1
@@ -791,11 +830,12 @@ __device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plan
       if (COUNT) cnt[a] += ok ? 1 : 0;
     }
   });
+  float sum[WD];
+  multi_sum_f<WD>(acc, sum);
 #pragma unroll
   for (int a = 0; a < WD; ++a) {
     if (a < na) {
-      const float sa = wave_sum_f(acc[a]);
-      if (lane == src0 + a) mine = sa;
+      if (lane == src0 + a) mine = sum[a];
       if (COUNT) {
         const int ca = wave_sum_i(cnt[a]);
         if (lane == src0 + a) mine_n = ca;
