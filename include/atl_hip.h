@@ -85,6 +85,21 @@ int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int
 int atl_sample_grid_bwd_pos(const float* gout, const float* field, int64_t B, int64_t C, int64_t Hg, int64_t Wg,
                             const float* pos, const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gpos,
                             hipStream_t stream);
+/* Many-channel fields (a trajectory coefficient grid: C = 2K channels sampled at every event), no counterpart
+ * in the reference's extension: they replace the same sample_grid (atl/motion/parametric.py:235-251) where the
+ * plane layout would cost C loads per corner.  atl_field_channels_last writes the channels-last copy
+ * field_cl (B, Hg, Wg, 4*ceil(C/4)) float, channels past C zero.  atl_sample_grid_fwd_cl and
+ * atl_sample_grid_bwd_pos_cl then return the same bits as atl_sample_grid_fwd and atl_sample_grid_bwd_pos on
+ * the plane field.  field_cl 16-byte aligned (out and gout too when C % 4 == 0); N * ceil(C/4) < 2^31 for the
+ * forward. */
+int atl_field_channels_last(const float* field, int64_t B, int64_t C, int64_t Hg, int64_t Wg, float* field_cl,
+                            hipStream_t stream);
+int atl_sample_grid_fwd_cl(const float* field_cl, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                           const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* out,
+                           hipStream_t stream);
+int atl_sample_grid_bwd_pos_cl(const float* gout, const float* field_cl, int64_t B, int64_t C, int64_t Hg,
+                               int64_t Wg, const float* pos, const int64_t* b, int64_t N, int64_t img_h,
+                               int64_t img_w, float* gpos, hipStream_t stream);
 /* The same adjoint through a tile plan: atl_grid_plan bins the positions by the 16x16 tile of their base
  * grid node into a workspace of atl_grid_plan_bytes(B, Hg, Wg, N) bytes (-1 if the sizes are unsupported);
  * atl_sample_grid_bwd_planned then accumulates gout tile by tile in LDS and adds each touched node once.

@@ -371,6 +371,123 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos(const float* __r
   gpos[n] = make_float2(sx, sy);
 }
 
+// ---------------------------------------------------------------------- many-channel fields (channels last)
+// A field of many channels (a coefficient grid) is sampled from a channels-last copy (B, Hg, Wg, Q) of float4,
+// Q = ceil(C / 4), channels past C zero: a node's channels are then one contiguous run, so a corner costs Q
+// 16-byte loads instead of C loads from C separate planes.  The forward gives each event Q lanes (one channel
+// quad each), so the (N, C) output rows are written with consecutive lanes on consecutive quads.  Both kernels
+// keep the plane kernels' fp32 operation order, so their results are the same bits.
+__global__ void __launch_bounds__(kBlock) k_field_channels_last(const float* __restrict__ field, int C, int Q,
+                                                                int64_t plane, int64_t total,
+                                                                float4* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int64_t node = i / Q;
+  const int q = (int)(i - node * Q);
+  const int64_t b = node / plane, o = node - b * plane;
+  const float* f = field + b * C * plane + o;
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = 4 * q + j;
+    v[j] = c < C ? f[c * plane] : 0.f;
+  }
+  out[i] = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+__device__ __forceinline__ float corner_sum(float f00, float f01, float f10, float f11, const GridCorners& g) {
+  float v = f00 * g.w00;
+  v = v + f01 * g.w01;
+  v = v + f10 * g.w10;
+  v = v + f11 * g.w11;
+  return v;
+}
+
+__global__ void __launch_bounds__(kBlock) k_sample_grid_fwd_cl(const float4* __restrict__ fcl, int64_t B, int C,
+                                                               int Q, int Hg, int Wg,
+                                                               const float2* __restrict__ pos,
+                                                               const int64_t* __restrict__ bidx, int N, float sxw,
+                                                               float syh, int scale, float* __restrict__ out) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;   // lane = (event, channel quad); N * Q < 2^31
+  const int n = g / Q;
+  if (n >= N) return;
+  const int q = g - n * Q;
+  const int64_t b = bidx[n];
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (batch_ok(b, B)) {
+    const float2 p = pos[n];
+    const GridCorners c = grid_corners(p.x, p.y, Hg, Wg, sxw, syh, scale != 0);
+    const float4* f = fcl + b * ((int64_t)Hg * Wg) * Q + q;
+    const float4 a = f[(int64_t)c.o00 * Q], e = f[(int64_t)c.o01 * Q], h = f[(int64_t)c.o10 * Q],
+                 k = f[(int64_t)c.o11 * Q];
+    v = make_float4(corner_sum(a.x, e.x, h.x, k.x, c), corner_sum(a.y, e.y, h.y, k.y, c),
+                    corner_sum(a.z, e.z, h.z, k.z, c), corner_sum(a.w, e.w, h.w, k.w, c));
+  }
+  float* o = out + (int64_t)n * C + 4 * q;
+  if ((C & 3) == 0) {
+    *(float4*)o = v;
+  } else {
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * q + j < C) o[j] = vv[j];
+  }
+}
+
+__global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos_cl(const float* __restrict__ gout,
+                                                                   const float4* __restrict__ fcl, int64_t B, int C,
+                                                                   int Q, int Hg, int Wg,
+                                                                   const float2* __restrict__ pos,
+                                                                   const int64_t* __restrict__ bidx, int64_t N,
+                                                                   float sxw, float syh, int scale,
+                                                                   float2* __restrict__ gpos) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  const float2 p = pos[n];
+  float sx = 0.f, sy = 0.f;
+  if (batch_ok(b, B)) {
+    float gx = p.x, gy = p.y, kx = 1.f, ky = 1.f;
+    if (scale) {
+      gx = p.x / sxw * (float)(Wg - 1);
+      gy = p.y / syh * (float)(Hg - 1);
+      kx = (float)(Wg - 1) / sxw;
+      ky = (float)(Hg - 1) / syh;
+    }
+    const bool inx = gx >= 0.f && gx <= (float)(Wg - 1), iny = gy >= 0.f && gy <= (float)(Hg - 1);
+    const GridCorners c = grid_corners(p.x, p.y, Hg, Wg, sxw, syh, scale != 0);
+    const float ax = c.ax, ay = c.ay;
+    const float4* f = fcl + b * ((int64_t)Hg * Wg) * Q;
+    const float* go_row = gout + n * C;
+    for (int q = 0; q < Q; ++q) {
+      const float4 a = f[(int64_t)c.o00 * Q + q], e = f[(int64_t)c.o01 * Q + q], h = f[(int64_t)c.o10 * Q + q],
+                   k = f[(int64_t)c.o11 * Q + q];
+      const float f00[4] = {a.x, a.y, a.z, a.w}, f01[4] = {e.x, e.y, e.z, e.w}, f10[4] = {h.x, h.y, h.z, h.w},
+                  f11[4] = {k.x, k.y, k.z, k.w};
+      float go[4];
+      if ((C & 3) == 0) {
+        const float4 g4 = *(const float4*)(go_row + 4 * q);
+        go[0] = g4.x;
+        go[1] = g4.y;
+        go[2] = g4.z;
+        go[3] = g4.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) go[j] = 4 * q + j < C ? go_row[4 * q + j] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {                // channel order as the plane kernel (padded channels skipped)
+        if (4 * q + j >= C) break;
+        sx += go[j] * ((1.f - ay) * (f01[j] - f00[j]) + ay * (f11[j] - f10[j]));
+        sy += go[j] * ((1.f - ax) * (f10[j] - f00[j]) + ax * (f11[j] - f01[j]));
+      }
+    }
+    sx = inx ? sx * kx : 0.f;
+    sy = iny ? sy * ky : 0.f;
+  }
+  gpos[n] = make_float2(sx, sy);
+}
+
 bool dims_ok(int64_t H, int64_t W) { return H > 0 && W > 0 && H * W < (int64_t)1 << 31; }
 
 // ------------------------------------------------------------------------------------------- event noise
@@ -514,6 +631,53 @@ int atl_sample_grid_bwd_pos(const float* gout, const float* field, int64_t B, in
   hipLaunchKernelGGL(k_sample_grid_bwd_pos, dim3(grid_for(N)), dim3(kBlock), 0, stream, gout, field, B, (int)C,
                      (int)Hg, (int)Wg, (const float2*)pos, b, N, sxw, syh, scale, (float2*)gpos);
   return check_launch("sample_grid_bwd_pos");
+}
+
+int atl_field_channels_last(const float* field, int64_t B, int64_t C, int64_t Hg, int64_t Wg, float* out,
+                            hipStream_t stream) {
+  if (B < 0 || C < 1 || !dims_ok(Hg, Wg) || C > (int64_t)1 << 20) { set_error("field_channels_last: bad sizes"); return 1; }
+  const int64_t Q = (C + 3) / 4, total = B * Hg * Wg * Q;
+  if (total == 0) return 0;
+  if (!field || !out) { set_error("field_channels_last: null pointer"); return 1; }
+  hipLaunchKernelGGL(k_field_channels_last, dim3(grid_for(total)), dim3(kBlock), 0, stream, field, (int)C, (int)Q,
+                     Hg * Wg, total, (float4*)out);
+  return check_launch("field_channels_last");
+}
+
+int atl_sample_grid_fwd_cl(const float* field_cl, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                           const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* out,
+                           hipStream_t stream) {
+  if (N < 0 || B < 0 || C < 1 || C > (int64_t)1 << 20 || !dims_ok(Hg, Wg)) { set_error("sample_grid_fwd_cl: bad sizes"); return 1; }
+  const int64_t Q = (C + 3) / 4;
+  if (N * Q >= ((int64_t)1 << 31) - kBlock) { set_error("sample_grid_fwd_cl: N * ceil(C/4) must stay below 2^31"); return 1; }
+  if (N == 0) return 0;
+  if ((reinterpret_cast<uintptr_t>(field_cl) & 15) || ((C & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15))) {
+    set_error("sample_grid_fwd_cl: field_cl (and out when C % 4 == 0) must be 16-byte aligned");
+    return 1;
+  }
+  const int scale = img_h > 0 && img_w > 0;
+  const float sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1), syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
+  hipLaunchKernelGGL(k_sample_grid_fwd_cl, dim3(grid_for(N * Q)), dim3(kBlock), 0, stream,
+                     (const float4*)field_cl, B, (int)C, (int)Q, (int)Hg, (int)Wg, (const float2*)pos, b, (int)N,
+                     sxw, syh, scale, out);
+  return check_launch("sample_grid_fwd_cl");
+}
+
+int atl_sample_grid_bwd_pos_cl(const float* gout, const float* field_cl, int64_t B, int64_t C, int64_t Hg,
+                               int64_t Wg, const float* pos, const int64_t* b, int64_t N, int64_t img_h,
+                               int64_t img_w, float* gpos, hipStream_t stream) {
+  if (N < 0 || B < 0 || C < 1 || C > (int64_t)1 << 20 || !dims_ok(Hg, Wg)) { set_error("sample_grid_bwd_pos_cl: bad sizes"); return 1; }
+  if (N == 0) return 0;
+  if ((reinterpret_cast<uintptr_t>(field_cl) & 15) || ((C & 3) == 0 && (reinterpret_cast<uintptr_t>(gout) & 15))) {
+    set_error("sample_grid_bwd_pos_cl: field_cl (and gout when C % 4 == 0) must be 16-byte aligned");
+    return 1;
+  }
+  const int scale = img_h > 0 && img_w > 0;
+  const float sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1), syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
+  hipLaunchKernelGGL(k_sample_grid_bwd_pos_cl, dim3(grid_for(N)), dim3(kBlock), 0, stream, gout,
+                     (const float4*)field_cl, B, (int)C, (int)((C + 3) / 4), (int)Hg, (int)Wg, (const float2*)pos, b,
+                     N, sxw, syh, scale, (float2*)gpos);
+  return check_launch("sample_grid_bwd_pos_cl");
 }
 
 int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,

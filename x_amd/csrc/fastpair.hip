@@ -396,9 +396,11 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
   }
   __syncthreads();
   // A bucket of at most kSortBlock * kSortItems records (the common case) is read once and kept in registers
-  // from the count to the scatter; larger buckets count from the keys and read the records again.
+  // from the count to the scatter, and the count's atomic returns each record's rank within its cell; larger
+  // buckets count from the keys, read the records again and rank them with a second atomic at the scatter.
   const bool one = hi - lo <= kSortBlock * kSortItems;
   Rec r1[kSortItems];
+  int rank[kSortItems];                            // one-read path: the record's rank within its cell
   if (one) {
 #pragma unroll
     for (int u = 0; u < kSortItems; ++u) {
@@ -407,7 +409,7 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
     }
 #pragma unroll
     for (int u = 0; u < kSortItems; ++u)
-      if (lo + u * kSortBlock + (int)threadIdx.x < hi) atomicAdd(cnt + (r1[u].i.z & (kBucketKeys - 1)), 1);
+      if (lo + u * kSortBlock + (int)threadIdx.x < hi) rank[u] = atomicAdd(cnt + (r1[u].i.z & (kBucketKeys - 1)), 1);
   } else {
     for (int base = lo; base < hi; base += kSortBlock * kSortItems) {
       int key[kSortItems];
@@ -447,9 +449,9 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
   Rec* out = space == 1 ? o.arec : o.srec;
   const int kbase = space * G.ncell_pad;
   const int plane_cells = G.GH * G.GW;
-  auto place = [&](Rec r) {
+  auto place = [&](Rec r, int rk) {               // rk: the record's rank within its cell
     const int kk = r.i.z & (kBucketKeys - 1);
-    const int pos = lo + cnt[kk] + atomicAdd(cur + kk, 1) - off;
+    const int pos = lo + cnt[kk] + rk - off;
     r.i.z -= kbase;
     if (space == 0) {
       o.epos[pos] = r.f;
@@ -464,7 +466,7 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
   if (one) {
 #pragma unroll
     for (int u = 0; u < kSortItems; ++u)
-      if (lo + u * kSortBlock + (int)threadIdx.x < hi) place(r1[u]);
+      if (lo + u * kSortBlock + (int)threadIdx.x < hi) place(r1[u], rank[u]);
     return;
   }
   for (int base = lo; base < hi; base += kSortBlock * kSortItems) {
@@ -478,7 +480,7 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
     }
 #pragma unroll
     for (int u = 0; u < kSortItems; ++u)
-      if (live[u]) place(r[u]);
+      if (live[u]) place(r[u], atomicAdd(cur + (r[u].i.z & (kBucketKeys - 1)), 1));
   }
 }
 

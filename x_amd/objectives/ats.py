@@ -43,8 +43,7 @@ def visible_fraction(motion, xa, ta, ba, ev: EventPacket, tau: float, n_check: i
     counts.index_put_((ev.b, sl), torch.ones_like(ev.t), accumulate=True)
     vis = torch.zeros_like(ta)
     tot = torch.zeros_like(ta)
-    for k in range(n_check):
-        c = float(centres[k])
+    for k, c in enumerate(centres.tolist()):     # one host transfer for the bin centres
         near = ((ta - c).abs() <= tau).to(ta.dtype)
         y = motion.transport(xa, ta, c, ba)
         inside = ((y[:, 0] >= 0) & (y[:, 0] <= ev.width - 1) & (y[:, 1] >= 0) & (y[:, 1] <= ev.height - 1)).to(ta.dtype)
@@ -241,6 +240,9 @@ class AnchoredSliced(Objective):
         if self.dequantize:
             xs = xs + (noise(xs.shape, xs, "uniform") - 0.5)
         xsm = xs + self.sigma * noise(xs.shape, xs, "normal") if self.smooth_anchors else xs
+        if self.nap is None:
+            return self._scores_all_slices(ev, motion, xs, xsm, slices, slice_of, delta, eps, anchor_mask,
+                                           source_mask)
         scores, picked = [], []
         for s in slices:
             c = (s + 0.5) * delta
@@ -280,6 +282,54 @@ class AnchoredSliced(Objective):
             z = ev.t.new_zeros(0)
             return z, z.long()
         return torch.cat(scores), torch.cat(picked)
+
+    def _scores_all_slices(self, ev, motion, xs, xsm, slices, slice_of, delta, eps, anchor_mask, source_mask):
+        """Every scored slice at once: the per-slice terms of the loop in ``log_scores`` (the reference's loop,
+        atl/objectives/ats.py:133-176), each computed once over all slices.  Slice j's splats are images
+        j*B .. j*B + B - 1 of one splat; the anchors' moves, look-ups, leave-one-out terms and exposure
+        correction are elementwise, so they run over every anchor together.  Scores come slice by slice in the
+        order of ``slices``, anchors in event order within a slice, as the loop appends them.  (Each slice's
+        targets are per-element times, so a motion's transport must accept a tensor ``t_dst``.)"""
+        dev, B, H, W = ev.device, ev.batch_size, ev.height, ev.width
+        nsl = len(slices)
+        # the slice centres in the events' dtype, as the loop's Python-float centre enters each op
+        cen = torch.tensor([(s + 0.5) * delta for s in slices], dtype=ev.t.dtype, device=dev)
+        src = (ev.t[None, :] - cen[:, None]).abs() <= self.tau + delta / 2          # (slices, N)
+        if source_mask is not None:
+            src = src & source_mask[None, :]
+        slot = torch.full((self.S,), -1, dtype=torch.long, device=dev)
+        slot[torch.tensor(slices, dtype=torch.long, device=dev)] = torch.arange(nsl, device=dev)
+        aslot = slot[slice_of]
+        anc = aslot >= 0
+        if anchor_mask is not None:
+            anc = anc & anchor_mask
+        ai = torch.nonzero(anc).squeeze(1)
+        if ai.numel() == 0:
+            z = ev.t.new_zeros(0)
+            return z, z.long()
+        ai = ai[torch.argsort(aslot[ai], stable=True)]                                 # slice-major
+        ja = aslot[ai]
+        js, si = torch.nonzero(src, as_tuple=True)                                     # slice-major pairs
+        y = motion.transport(xs[si], ev.t[si], cen[js], ev.b[si])
+        img = splat(y, torch.ones_like(ev.t[si]), js * B + ev.b[si], nsl * B, H, W, kernel="gauss",
+                    sigma=self.sigma)
+        ca, ta, ba = cen[ja], ev.t[ai], ev.b[ai]
+        if self.logdet:
+            a, ld = motion.transport_logdet(xsm[ai], ta, ca, ba)
+        else:
+            a, ld = motion.transport(xsm[ai], ta, ca, ba), 0.0
+        ia = ja * B + ba
+        val = gather(img, a, ia)
+        in_src = src[ja, ai].to(val.dtype)
+        if self.smooth_anchors:
+            own = in_src * cross_term(a, motion.transport(xs[ai], ta, ca, ba), self.sigma, H, W)
+        else:
+            own = in_src * self_term(a, self.sigma, H, W)
+        nsrc = torch.bincount(js * B + ev.b[si], minlength=nsl * B).to(val.dtype)[ia] - in_src
+        if self.visibility:
+            nsrc = nsrc * visible_fraction(motion, xsm[ai].detach(), ta, ba, ev, self.tau)
+        rho = (val - own).clamp(min=0) / nsrc.clamp(min=1)
+        return torch.log(eps + rho) + ld, ai
 
     def set_bandwidth(self, h: float):
         self.sigma = float(h)

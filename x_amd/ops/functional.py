@@ -136,7 +136,10 @@ class _SampleGrid(torch.autograd.Function):
 
     When the field needs a gradient, the forward also bins the positions by the tile of their base corner (a
     device plan), so that the backward accumulates tile by tile in LDS instead of scattered atomic adds.  The
-    positions' gradient (through the interpolation weights) is a per-event gather."""
+    positions' gradient (through the interpolation weights) is a per-event gather.  Fields of CL_MIN_CHANNELS
+    channels or more are sampled from a channels-last copy (same bits, a node's channels in one run)."""
+
+    CL_MIN_CHANNELS = 4
 
     @staticmethod
     def forward(ctx, fld, pos, b, img_h, img_w, plan):
@@ -145,10 +148,20 @@ class _SampleGrid(torch.autograd.Function):
         N = pos.shape[0]
         out = torch.empty(N, C, device=pos.device, dtype=F32)
         ctx.plan = None
+        Q = (C + 3) // 4
+        cl = C >= _SampleGrid.CL_MIN_CHANNELS and N * Q < 2 ** 31 - 1024
         with torch.cuda.device(pos.device):
             st = stream_of(pos)
-            call("atl_sample_grid_fwd", ptr(fld), B, C, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w),
-                 ptr(out), st)
+            if cl:
+                fcl = torch.empty(B, Hg, Wg, 4 * Q, device=pos.device, dtype=F32)
+                call("atl_field_channels_last", ptr(fld), B, C, Hg, Wg, ptr(fcl), st)
+                call("atl_sample_grid_fwd_cl", ptr(fcl), B, C, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w),
+                     ptr(out), st)
+                fld = fcl                          # the backward's position gradient reads the same copy
+            else:
+                call("atl_sample_grid_fwd", ptr(fld), B, C, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w),
+                     ptr(out), st)
+            ctx.cl = cl
             if plan and _tile_plan_ok(B, C, Hg, Wg):
                 nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N))
                 if nbytes >= 0:
@@ -176,8 +189,8 @@ class _SampleGrid(torch.autograd.Function):
                          ctx.img[1], ptr(gf), stream_of(pos))
             if ctx.needs_input_grad[1]:
                 gp = torch.empty_like(pos)
-                call("atl_sample_grid_bwd_pos", ptr(g), ptr(fld), B, C, Hg, Wg, ptr(pos), ptr(b), pos.shape[0],
-                     ctx.img[0], ctx.img[1], ptr(gp), stream_of(pos))
+                call("atl_sample_grid_bwd_pos_cl" if ctx.cl else "atl_sample_grid_bwd_pos", ptr(g), ptr(fld), B, C,
+                     Hg, Wg, ptr(pos), ptr(b), pos.shape[0], ctx.img[0], ctx.img[1], ptr(gp), stream_of(pos))
         return gf, gp, None, None, None, None
 
 
