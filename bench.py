@@ -356,6 +356,8 @@ TRAJ_BYTES = {     # algorithmic bytes per entry point: per event, plus the fiel
     "atl_sample_grid_bwd_planned": lambda n, c, f, hw: (16 + 4 * c) * n + 8 * c * f,
     "atl_sample_grid_bwd_pos": lambda n, c, f, hw: (24 + 4 * c) * n + 4 * c * f,
     "atl_sample_grid_fwd_cl": lambda n, c, f, hw: (16 + 4 * c) * n + 4 * c * f,
+    "atl_traj_displacement": lambda n, c, f, hw: 28 * n + 4 * c * f,
+    "atl_traj_gout": lambda n, c, f, hw: (12 + 4 * c) * n,
     "atl_sample_grid_bwd_pos_cl": lambda n, c, f, hw: (24 + 4 * c) * n + 4 * c * f,
     "atl_splat_gauss_fwd": lambda n, c, f, hw: 20 * n + 4 * hw,
     "atl_splat_gauss_fwd_ws": lambda n, c, f, hw: 20 * n + 4 * hw,

@@ -100,6 +100,17 @@ int atl_sample_grid_fwd_cl(const float* field_cl, int64_t B, int64_t C, int64_t 
 int atl_sample_grid_bwd_pos_cl(const float* gout, const float* field_cl, int64_t B, int64_t C, int64_t Hg,
                                int64_t Wg, const float* pos, const int64_t* b, int64_t N, int64_t img_h,
                                int64_t img_w, float* gpos, hipStream_t stream);
+/* PixelTrajectories.displacement (atl/motion/trajectories.py:26-37 basis, the coefficient look-up and the sum
+ * over k), fused, no counterpart in the reference's extension: out (N,2) written, d = (sum_k c_{K+k} g_k,
+ * sum_k c_k g_k) of the channels-last coefficient grid field_cl (B, Hg, Wg, 4*ceil(2K/4), channels
+ * [y_1..y_K, x_1..x_K]) sampled at grid coordinates gpos, with g_k(t) = t^k (basis 0) or
+ * binom(K,k) t^k (1-t)^(K-k) (basis 1); 1 <= K <= 16.  atl_traj_gout writes the (N, 2K) output gradient per
+ * channel, gout[n, k-1] = g_k gd.y and gout[n, K+k-1] = g_k gd.x, which atl_sample_grid_bwd_planned (field)
+ * and atl_sample_grid_bwd_pos_cl (positions) take. */
+int atl_traj_displacement(const float* field_cl, int64_t B, int64_t K, int64_t Hg, int64_t Wg, const float* gpos,
+                          const int64_t* b, const float* t, int64_t N, int64_t basis, float* out, hipStream_t stream);
+int atl_traj_gout(const float* gd, const float* t, int64_t N, int64_t K, int64_t basis, float* gout,
+                  hipStream_t stream);
 /* The same adjoint through a tile plan: atl_grid_plan bins the positions by the 16x16 tile of their base
  * grid node into a workspace of atl_grid_plan_bytes(B, Hg, Wg, N) bytes (-1 if the sizes are unsupported);
  * atl_sample_grid_bwd_planned then accumulates gout tile by tile in LDS and adds each touched node once.

@@ -1,10 +1,13 @@
 """Pixel trajectories and the sliced anchored score on the HIP path (the continuous-time workload).
 
-The trajectory model and the sliced score are host compositions (torch) of the HIP flow sampler (forward,
-field adjoint through the tile plan, position gradient), the Gaussian splat and the bilinear gather.  They run
-here on the device against the same composition on CPU tensors, where every op is plain PyTorch
-(x_amd/ops/reference.py); the kernels themselves are pinned to the oracle in test_gpu_ops.py.  Bars: values
+The trajectory model and the sliced score are host compositions (torch) of the fused displacement kernel, the
+HIP flow sampler (forward, field adjoint through the tile plan, position gradient), the Gaussian splat and the
+bilinear gather.  They run here on the device against the same composition on CPU tensors, where every op is
+plain PyTorch (x_amd/ops/reference.py); the fused displacement is also pinned to float64 here, the other
+kernels to the oracle in test_gpu_ops.py.  Bars: values
 within 1e-5 relative, gradients within 1e-4 relative to the largest magnitude."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -63,7 +66,53 @@ def test_sample_grid_position_and_field_gradients(C, scale):
     close_rel(res[DEV][2], res["cpu"][2], 1e-4)
 
 
-@pytest.mark.parametrize("K,kind", [(1, "polynomial"), (3, "bezier"), (4, "polynomial")])
+@pytest.mark.parametrize("K,kind", [(1, "polynomial"), (2, "bezier"), (7, "bezier"), (10, "bezier"),
+                                    (16, "polynomial")])
+def test_traj_displacement_matches_fp64_and_torch_gradients(K, kind):
+    """The fused displacement against the oracle's exact coefficient samples times the basis in float64; its
+    field gradient against the float64 adjoint, its position gradient against the CPU torch composition (sample
+    the 2K channels, multiply by the basis, sum over k) under autograd; absent batches give zero rows."""
+    print(f"traj_displacement K={K} {kind}", flush=True)
+    from x_amd.ops import functional as F
+    rng = np.random.default_rng(K * 7 + len(kind))
+    n, B, Hg, Wg = 5000, 2, 19, 27
+    fld = (rng.standard_normal((B, 2 * K, Hg, Wg)) * 2).astype(F32)
+    gpos = np.stack([rng.uniform(-2, Wg + 1, n), rng.uniform(-2, Hg + 1, n)], 1).astype(F32)
+    b = rng.integers(0, B, n).astype(np.int64)
+    b[::89] = B
+    t = rng.uniform(0, 1, n).astype(F32)
+    t[:4] = [0.0, 1.0, 0.5, 1e-3]
+    ok = b < B
+    tf = torch.tensor(fld, device=DEV, requires_grad=True)
+    tp = torch.tensor(gpos, device=DEV, requires_grad=True)
+    d = F.traj_displacement(tf, tp, torch.tensor(b, device=DEV), torch.tensor(t, device=DEV), K, kind)
+    coef, idx, wts = O.sample_grid(fld, gpos[ok], b[ok])
+    tt = t[ok].astype(np.float64)[:, None]
+    k = np.arange(1, K + 1)
+    if kind == "bezier":
+        g = np.array([math.comb(K, j) for j in k], np.float64) * tt ** k * (1 - tt) ** (K - k)
+    else:
+        g = tt ** k
+    c64 = coef.astype(np.float64)
+    want = np.stack([(c64[:, K:] * g).sum(1), (c64[:, :K] * g).sum(1)], 1)
+    got = N(d)
+    close_rel(got[ok], want, 1e-5)
+    assert not got[~ok].any()
+    gd = rng.standard_normal((n, 2)).astype(F32)
+    d.backward(torch.tensor(gd, device=DEV))
+    gout = np.concatenate([g * gd[ok, 1:2], g * gd[ok, 0:1]], 1)
+    close_rel(N(tf.grad), O.sample_grid_bwd(gout, idx, wts, fld.shape), 1e-4)
+    cf = torch.tensor(fld)
+    cp = torch.tensor(gpos[ok], requires_grad=True)
+    cc = sample_grid(cf, cp, torch.tensor(b[ok]))
+    gk = torch.tensor(g.astype(F32))
+    cd = torch.stack([(cc[:, K:] * gk).sum(1), (cc[:, :K] * gk).sum(1)], 1)
+    cd.backward(torch.tensor(gd[ok]))
+    close_rel(N(tp.grad)[ok], N(cp.grad), 1e-4)
+    assert not N(tp.grad)[~ok].any()
+
+
+@pytest.mark.parametrize("K,kind", [(1, "polynomial"), (3, "bezier"), (4, "polynomial"), (10, "bezier")])
 def test_pixel_trajectories_device_matches_cpu(K, kind):
     """Transport (fixed-point origin + displacement) values and coefficient gradients, device vs CPU."""
     print(f"trajectories K={K} {kind}", flush=True)

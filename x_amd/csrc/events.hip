@@ -488,6 +488,96 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos_cl(const float* 
   gpos[n] = make_float2(sx, sy);
 }
 
+// ------------------------------------------------------------------------------ trajectory displacement
+// d(p, t) = sum_k c_k(p) g_k(t) of a coefficient grid with channels [y_1..y_K, x_1..x_K] (the displacement of
+// atl/motion/trajectories.py: the coefficients are the bilinear border-clamped sample at p, g_k(t) = t^k for
+// the polynomial basis, binom(K, k) t^k (1 - t)^(K - k) for the Bernstein basis, k = 1..K).  One pass per
+// event instead of the (N, 2K) coefficient rows and the products and sums over them.  The powers are repeated
+// products (torch's pow rounds differently by a few ulps) and the k sum runs in order.
+constexpr int kTrajMaxK = 16;
+
+template <int K>
+__device__ __forceinline__ void traj_basis(float t, int bernstein, float (&g)[K]) {
+  const float u = 1.f - t;
+  float tk = 1.f, binom = 1.f;
+#pragma unroll
+  for (int k = 1; k <= K; ++k) {
+    tk = tk * t;
+    if (!bernstein) {
+      g[k - 1] = tk;
+      continue;
+    }
+    binom = binom * (float)(K - k + 1) / (float)k;   // binom(K, k): exact integers in fp32 for K <= 24
+    float uk = 1.f;
+#pragma unroll
+    for (int j = 0; j < K - k; ++j) uk = uk * u;
+    g[k - 1] = binom * tk * uk;
+  }
+}
+
+template <int K>
+__global__ void __launch_bounds__(kBlock) k_traj_displacement(const float4* __restrict__ fcl, int64_t B, int Hg,
+                                                              int Wg, const float2* __restrict__ gpos,
+                                                              const int64_t* __restrict__ bidx,
+                                                              const float* __restrict__ t, int bernstein, int64_t N,
+                                                              float2* __restrict__ out) {
+  constexpr int Q = (2 * K + 3) / 4;
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  float dx = 0.f, dy = 0.f;
+  if (batch_ok(b, B)) {
+    const float2 p = gpos[n];
+    const GridCorners c = grid_corners(p.x, p.y, Hg, Wg, 1.f, 1.f, false);
+    float g[K];
+    traj_basis<K>(t[n], bernstein, g);
+    const float4* f = fcl + b * ((int64_t)Hg * Wg) * Q;
+    float v[4 * Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const float4 a = f[(int64_t)c.o00 * Q + q], e = f[(int64_t)c.o01 * Q + q], h = f[(int64_t)c.o10 * Q + q],
+                   k = f[(int64_t)c.o11 * Q + q];
+      v[4 * q] = corner_sum(a.x, e.x, h.x, k.x, c);
+      v[4 * q + 1] = corner_sum(a.y, e.y, h.y, k.y, c);
+      v[4 * q + 2] = corner_sum(a.z, e.z, h.z, k.z, c);
+      v[4 * q + 3] = corner_sum(a.w, e.w, h.w, k.w, c);
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      dy = dy + v[k] * g[k];
+      dx = dx + v[K + k] * g[k];
+    }
+  }
+  out[n] = make_float2(dx, dy);
+}
+
+// Its output gradient per coefficient channel: gout[n, c] = g_k(t_n) * gd_n.y for c = k - 1 < K and
+// g_k(t_n) * gd_n.x for c = K + k - 1, the rows that the field adjoint and the position gradient of the sampler
+// take.  One lane per (event, channel quad), so the rows are written by consecutive lanes.
+template <int K>
+__global__ void __launch_bounds__(kBlock) k_traj_gout(const float2* __restrict__ gd, const float* __restrict__ t,
+                                                      int bernstein, int N, float* __restrict__ gout) {
+  constexpr int C = 2 * K, Q = (C + 3) / 4;
+  const int gl = blockIdx.x * blockDim.x + threadIdx.x;   // N * Q < 2^31
+  const int n = gl / Q;
+  if (n >= N) return;
+  const int q = gl - n * Q;
+  float g[K];
+  traj_basis<K>(t[n], bernstein, g);
+  const float2 d = gd[n];
+  float* o = gout + (int64_t)n * C;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int ch = 4 * q + j;
+    if (ch >= C) break;
+    const int k = ch < K ? ch : ch - K;
+    float gk = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < K; ++kk) gk = kk == k ? g[kk] : gk;   // register select, no indexed private array
+    o[ch] = gk * (ch < K ? d.y : d.x);
+  }
+}
+
 bool dims_ok(int64_t H, int64_t W) { return H > 0 && W > 0 && H * W < (int64_t)1 << 31; }
 
 // ------------------------------------------------------------------------------------------- event noise
@@ -678,6 +768,52 @@ int atl_sample_grid_bwd_pos_cl(const float* gout, const float* field_cl, int64_t
                      (const float4*)field_cl, B, (int)C, (int)((C + 3) / 4), (int)Hg, (int)Wg, (const float2*)pos, b,
                      N, sxw, syh, scale, (float2*)gpos);
   return check_launch("sample_grid_bwd_pos_cl");
+}
+
+int atl_traj_displacement(const float* field_cl, int64_t B, int64_t K, int64_t Hg, int64_t Wg, const float* gpos,
+                          const int64_t* b, const float* t, int64_t N, int64_t basis, float* out, hipStream_t stream) {
+  if (N < 0 || B < 0 || K < 1 || K > kTrajMaxK || !dims_ok(Hg, Wg) || (basis != 0 && basis != 1)) {
+    set_error("traj_displacement: bad sizes (1 <= K <= %d, basis 0 or 1)", kTrajMaxK);
+    return 1;
+  }
+  if (N == 0) return 0;
+  if (reinterpret_cast<uintptr_t>(field_cl) & 15) { set_error("traj_displacement: field_cl must be 16-byte aligned"); return 1; }
+  const dim3 grid(grid_for(N)), block(kBlock);
+  const float4* f = (const float4*)field_cl;
+  const float2* p = (const float2*)gpos;
+  float2* o = (float2*)out;
+  const int bern = (int)basis;
+  switch (K) {
+#define ATL_TRAJ_CASE(k) \
+    case k: hipLaunchKernelGGL(k_traj_displacement<k>, grid, block, 0, stream, f, B, (int)Hg, (int)Wg, p, b, t, bern, N, o); break;
+    ATL_TRAJ_CASE(1) ATL_TRAJ_CASE(2) ATL_TRAJ_CASE(3) ATL_TRAJ_CASE(4) ATL_TRAJ_CASE(5) ATL_TRAJ_CASE(6)
+    ATL_TRAJ_CASE(7) ATL_TRAJ_CASE(8) ATL_TRAJ_CASE(9) ATL_TRAJ_CASE(10) ATL_TRAJ_CASE(11) ATL_TRAJ_CASE(12)
+    ATL_TRAJ_CASE(13) ATL_TRAJ_CASE(14) ATL_TRAJ_CASE(15) ATL_TRAJ_CASE(16)
+#undef ATL_TRAJ_CASE
+  }
+  return check_launch("traj_displacement");
+}
+
+int atl_traj_gout(const float* gd, const float* t, int64_t N, int64_t K, int64_t basis, float* gout,
+                  hipStream_t stream) {
+  if (N < 0 || K < 1 || K > kTrajMaxK || (basis != 0 && basis != 1)) {
+    set_error("traj_gout: bad sizes (1 <= K <= %d, basis 0 or 1)", kTrajMaxK);
+    return 1;
+  }
+  const int64_t Q = (2 * K + 3) / 4;
+  if (N * Q >= ((int64_t)1 << 31) - kBlock) { set_error("traj_gout: N * ceil(K/2) must stay below 2^31"); return 1; }
+  if (N == 0) return 0;
+  const dim3 grid(grid_for(N * Q)), block(kBlock);
+  const float2* g = (const float2*)gd;
+  const int bern = (int)basis, n = (int)N;
+  switch (K) {
+#define ATL_TRAJ_CASE(k) case k: hipLaunchKernelGGL(k_traj_gout<k>, grid, block, 0, stream, g, t, bern, n, gout); break;
+    ATL_TRAJ_CASE(1) ATL_TRAJ_CASE(2) ATL_TRAJ_CASE(3) ATL_TRAJ_CASE(4) ATL_TRAJ_CASE(5) ATL_TRAJ_CASE(6)
+    ATL_TRAJ_CASE(7) ATL_TRAJ_CASE(8) ATL_TRAJ_CASE(9) ATL_TRAJ_CASE(10) ATL_TRAJ_CASE(11) ATL_TRAJ_CASE(12)
+    ATL_TRAJ_CASE(13) ATL_TRAJ_CASE(14) ATL_TRAJ_CASE(15) ATL_TRAJ_CASE(16)
+#undef ATL_TRAJ_CASE
+  }
+  return check_launch("traj_gout");
 }
 
 int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,

@@ -18,6 +18,7 @@ import math
 import torch
 
 from .base import Motion, as_time
+from ..ops.functional import TRAJ_MAX_K, traj_displacement
 from .parametric import sample_grid
 
 
@@ -61,7 +62,9 @@ class PixelTrajectories(Motion):
         return torch.stack([c[:, self.K:], c[:, :self.K]], -1)
 
     def displacement(self, p: torch.Tensor, b: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
-        """q(p, t) - p for trajectories starting at ``p``."""
+        """q(p, t) - p for trajectories starting at ``p`` (on the device: one fused kernel)."""
+        if p.is_cuda and self.K <= TRAJ_MAX_K and not t.requires_grad:
+            return traj_displacement(self.tile_c, (p - self.offset) / self.tile, b, t, self.K, self.basis_kind)
         return (self._coeff_at(p, b) * basis(t, self.K, self.basis_kind)[..., None]).sum(1)
 
     def origin(self, xy: torch.Tensor, t: torch.Tensor, b: torch.Tensor) -> torch.Tensor:

@@ -40,6 +40,8 @@ _SIGS = {
     "atl_sample_grid_bwd": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_sample_grid_bwd_pos": [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_field_channels_last": [_P, _I, _I, _I, _I, _P, _P],
+    "atl_traj_displacement": [_P, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P, _P],
+    "atl_traj_gout": [_P, _P, _I, _I, _I, _P, _P],
     "atl_sample_grid_fwd_cl": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_sample_grid_bwd_pos_cl": [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_event_noise": [_P, _I, ctypes.c_uint64, ctypes.c_uint64, _D, _C, _P, _P, _P],
@@ -130,7 +132,8 @@ _TIMED = {}          # entry point -> list of (start, end, events) per timed cal
 _EVERY = {"n": 1, "calls": {}}   # time one call in n of each entry point
 # position of the event count N in the arguments of the entry points whose calls are sized by it
 _NARG = {"atl_sample_grid_fwd": 7, "atl_sample_grid_bwd_planned": 6, "atl_sample_grid_bwd_pos": 8,
-         "atl_sample_grid_fwd_cl": 7, "atl_sample_grid_bwd_pos_cl": 8,
+         "atl_sample_grid_fwd_cl": 7, "atl_sample_grid_bwd_pos_cl": 8, "atl_traj_displacement": 8,
+         "atl_traj_gout": 2,
          "atl_splat_gauss_fwd": 3, "atl_splat_gauss_bwd": 4, "atl_splat_gauss_fwd_ws": 3,
          "atl_gather_bilinear_fwd": 3, "atl_gather_bilinear_bwd_ws": 4, "atl_splat_bilinear_fwd_ws": 3,
          "atl_splat_bilinear_bwd": 4}

@@ -194,6 +194,77 @@ class _SampleGrid(torch.autograd.Function):
         return gf, gp, None, None, None, None
 
 
+class _TrajDisplacement(torch.autograd.Function):
+    """PixelTrajectories.displacement in one kernel (atl/motion/trajectories.py: d = sum_k c_k(p) g_k(t), the
+    coefficients c_k the border-clamped bilinear sample of a (B, 2K, Hg, Wg) grid at grid coordinates p).
+    Differentiable w.r.t. the grid and the positions; the times carry no gradient.  The backward writes the
+    per-channel output gradient (g_k times the displacement's gradient) and hands it to the flow sampler's
+    field adjoint and position gradient."""
+
+    @staticmethod
+    def forward(ctx, fld, gpos, b, t, K, basis, plan):
+        fld, gpos, b, t = _f32(fld), _f32(gpos), b.contiguous().long(), _f32(t)
+        B, C, Hg, Wg = fld.shape
+        N = gpos.shape[0]
+        out = torch.empty(N, 2, device=gpos.device, dtype=F32)
+        fcl = torch.empty(B, Hg, Wg, 4 * ((C + 3) // 4), device=gpos.device, dtype=F32)
+        ctx.plan = None
+        with torch.cuda.device(gpos.device):
+            st = stream_of(gpos)
+            call("atl_field_channels_last", ptr(fld), B, C, Hg, Wg, ptr(fcl), st)
+            call("atl_traj_displacement", ptr(fcl), B, K, Hg, Wg, ptr(gpos), ptr(b), ptr(t), N, basis, ptr(out), st)
+            if plan and _tile_plan_ok(B, C, Hg, Wg):
+                nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N))
+                if nbytes >= 0:
+                    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=gpos.device)
+                    call("atl_grid_plan", B, Hg, Wg, ptr(gpos), ptr(b), N, 0, 0, ptr(ws), nbytes, st)
+                    ctx.plan = ws
+        ctx.save_for_backward(gpos, b, t, fcl)
+        ctx.shape, ctx.K, ctx.basis = (B, C, Hg, Wg), K, basis
+        return out
+
+    @staticmethod
+    def backward(ctx, gd):
+        gpos, b, t, fcl = ctx.saved_tensors
+        B, C, Hg, Wg = ctx.shape
+        N = gpos.shape[0]
+        gd = gd.contiguous().float()
+        gf = gp = None
+        with torch.cuda.device(gpos.device):
+            st = stream_of(gpos)
+            g = torch.empty(N, C, device=gpos.device, dtype=F32)
+            call("atl_traj_gout", ptr(gd), ptr(t), N, ctx.K, ctx.basis, ptr(g), st)
+            if ctx.needs_input_grad[0]:
+                gf = torch.zeros(B, C, Hg, Wg, device=gpos.device, dtype=F32)
+                if ctx.plan is not None:
+                    call("atl_sample_grid_bwd_planned", ptr(g), B, C, Hg, Wg, ptr(gpos), N, 0, 0, ptr(ctx.plan),
+                         ptr(gf), st)
+                else:
+                    call("atl_sample_grid_bwd", ptr(g), B, C, Hg, Wg, ptr(gpos), ptr(b), N, 0, 0, ptr(gf), st)
+            if ctx.needs_input_grad[1]:
+                gp = torch.empty_like(gpos)
+                call("atl_sample_grid_bwd_pos_cl", ptr(g), ptr(fcl), B, C, Hg, Wg, ptr(gpos), ptr(b), N, 0, 0,
+                     ptr(gp), st)
+        return gf, gp, None, None, None, None, None
+
+
+TRAJ_MAX_K = 16
+
+
+def traj_displacement(fld: torch.Tensor, gpos: torch.Tensor, b: torch.Tensor, t: torch.Tensor, K: int,
+                      basis: str) -> torch.Tensor:
+    """Displacement (N, 2) in (x, y) of trajectories with coefficient grid ``fld`` (B, 2K, Hg, Wg), channels
+    [y_1..y_K, x_1..x_K], at grid coordinates ``gpos``; ``basis`` "polynomial" or "bezier".  Device tensors,
+    K <= TRAJ_MAX_K."""
+    get_ext()
+    if basis not in ("polynomial", "bezier"):
+        raise ValueError(f"unknown basis {basis!r}")
+    if t.requires_grad:
+        raise ValueError("traj_displacement: event times carry no gradient")
+    plan = fld.requires_grad and torch.is_grad_enabled()
+    return _TrajDisplacement.apply(fld, gpos, b, t, int(K), int(basis == "bezier"), plan)
+
+
 def sample_grid_hip(fld: torch.Tensor, pos: torch.Tensor, b: torch.Tensor, img_hw=(0, 0)) -> torch.Tensor:
     """HIP flow lookup: ``pos`` are grid coordinates, or image pixels mapped by x / max(W-1, 1) * (Wg-1)
     when ``img_hw`` = (H, W) is given (DenseLinearFlow.field).  Differentiable w.r.t. the field and the
