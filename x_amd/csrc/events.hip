@@ -515,40 +515,60 @@ __device__ __forceinline__ void traj_basis(float t, int bernstein, float (&g)[K]
   }
 }
 
+// One lane per (event, channel quad), the Q = ceil(2K/4) lanes of an event side by side in one wave (64 / Q
+// events per wave, the remaining lanes idle): the lanes of an event read the same corner's channels in
+// consecutive 16-byte pieces, and the event's first lane adds the Q partial sums.
 template <int K>
 __global__ void __launch_bounds__(kBlock) k_traj_displacement(const float4* __restrict__ fcl, int64_t B, int Hg,
                                                               int Wg, const float2* __restrict__ gpos,
                                                               const int64_t* __restrict__ bidx,
                                                               const float* __restrict__ t, int bernstein, int64_t N,
                                                               float2* __restrict__ out) {
-  constexpr int Q = (2 * K + 3) / 4;
-  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= N) return;
-  const int64_t b = bidx[n];
+  constexpr int C = 2 * K, Q = (C + 3) / 4, EPW = kWave / Q;   // events per wave
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int e = lane / Q, q = lane - e * Q;
+  const int64_t n = wave * EPW + e;
+  const bool live = e < EPW && n < N;
   float dx = 0.f, dy = 0.f;
-  if (batch_ok(b, B)) {
+  int64_t b = -1;
+  if (live) b = bidx[n];
+  if (live && batch_ok(b, B)) {
     const float2 p = gpos[n];
     const GridCorners c = grid_corners(p.x, p.y, Hg, Wg, 1.f, 1.f, false);
     float g[K];
     traj_basis<K>(t[n], bernstein, g);
-    const float4* f = fcl + b * ((int64_t)Hg * Wg) * Q;
-    float v[4 * Q];
+    const float4* f = fcl + b * ((int64_t)Hg * Wg) * Q + q;
+    const float4 a = f[(int64_t)c.o00 * Q], h0 = f[(int64_t)c.o01 * Q], h1 = f[(int64_t)c.o10 * Q],
+                 k1 = f[(int64_t)c.o11 * Q];
+    const float v[4] = {corner_sum(a.x, h0.x, h1.x, k1.x, c), corner_sum(a.y, h0.y, h1.y, k1.y, c),
+                        corner_sum(a.z, h0.z, h1.z, k1.z, c), corner_sum(a.w, h0.w, h1.w, k1.w, c)};
 #pragma unroll
-    for (int q = 0; q < Q; ++q) {
-      const float4 a = f[(int64_t)c.o00 * Q + q], e = f[(int64_t)c.o01 * Q + q], h = f[(int64_t)c.o10 * Q + q],
-                   k = f[(int64_t)c.o11 * Q + q];
-      v[4 * q] = corner_sum(a.x, e.x, h.x, k.x, c);
-      v[4 * q + 1] = corner_sum(a.y, e.y, h.y, k.y, c);
-      v[4 * q + 2] = corner_sum(a.z, e.z, h.z, k.z, c);
-      v[4 * q + 3] = corner_sum(a.w, e.w, h.w, k.w, c);
-    }
+    for (int j = 0; j < 4; ++j) {
+      const int ch = 4 * q + j;
+      if (ch >= C) break;
+      const int k = ch < K ? ch : ch - K;
+      float gk = 0.f;
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      dy = dy + v[k] * g[k];
-      dx = dx + v[K + k] * g[k];
+      for (int kk = 0; kk < K; ++kk) gk = kk == k ? g[kk] : gk;   // register select, no indexed private array
+      if (ch < K)
+        dy = dy + v[j] * gk;
+      else
+        dx = dx + v[j] * gk;
     }
   }
-  out[n] = make_float2(dx, dy);
+  // the event's first lane adds its other lanes' sums (every lane takes part in the shuffles)
+  float sx = dx, sy = dy;
+#pragma unroll
+  for (int i = 1; i < Q; ++i) {
+    const int src = min(lane + i, kWave - 1);
+    const float ox = __shfl(dx, src), oy = __shfl(dy, src);
+    if (q + i < Q) {
+      sx = sx + ox;
+      sy = sy + oy;
+    }
+  }
+  if (live && q == 0) out[n] = make_float2(sx, sy);
 }
 
 // Its output gradient per coefficient channel: gout[n, c] = g_k(t_n) * gd_n.y for c = k - 1 < K and
@@ -778,7 +798,8 @@ int atl_traj_displacement(const float* field_cl, int64_t B, int64_t K, int64_t H
   }
   if (N == 0) return 0;
   if (reinterpret_cast<uintptr_t>(field_cl) & 15) { set_error("traj_displacement: field_cl must be 16-byte aligned"); return 1; }
-  const dim3 grid(grid_for(N)), block(kBlock);
+  const int64_t Q = (2 * K + 3) / 4, waves = (N + kWave / Q - 1) / (kWave / Q);
+  const dim3 grid(grid_for(waves * kWave)), block(kBlock);
   const float4* f = (const float4*)field_cl;
   const float2* p = (const float2*)gpos;
   float2* o = (float2*)out;
