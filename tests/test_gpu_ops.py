@@ -195,14 +195,17 @@ def test_sample_grid_channels_last_same_bits(C, img):
     assert np.array_equal(N(tp.grad), N(gp))
 
 
-@pytest.mark.parametrize("Hg,Wg", [(1, 1), (2, 3), (5, 1), (1, 7), (17, 13)])
-def test_sample_grid_planned_backward_small_grids(Hg, Wg):
-    """The tile-plan adjoint on degenerate and odd grids, positions inside and far outside (clamped)."""
-    rng = np.random.default_rng(Hg * 100 + Wg)
+@pytest.mark.parametrize("C", [2, 12])
+@pytest.mark.parametrize("Hg,Wg", [(1, 1), (2, 3), (5, 1), (1, 7), (17, 13), (40, 37)])
+def test_sample_grid_planned_backward_small_grids(Hg, Wg, C):
+    """The tile-plan adjoint on degenerate and odd grids, positions inside and far outside (clamped); 12
+    channels take the gather form on grids of at least 2 x 2 nodes and the scatter form otherwise."""
+    print(f"planned backward Hg={Hg} Wg={Wg} C={C}", flush=True)
+    rng = np.random.default_rng(Hg * 100 + Wg + C)
     n = 3000
     pos = np.stack([rng.uniform(-5, Wg + 4, n), rng.uniform(-5, Hg + 4, n)], 1).astype(F32)
     b = rng.integers(0, 2, n).astype(np.int64)
-    fld = rng.standard_normal((2, 2, Hg, Wg)).astype(F32)
+    fld = rng.standard_normal((2, C, Hg, Wg)).astype(F32)
     tf = T(fld).requires_grad_(True)
     out = F.sample_grid_hip(tf, T(pos), T(b))
     want, idx, wts = O.sample_grid(fld, pos, b)

@@ -44,6 +44,7 @@ struct TileGeo {
   float inv2s2, norm;        // kGauss: 1 / (2 sigma^2), 1 / (2 pi sigma^2)
   int scale;                 // kGrid: positions are image pixels mapped by sxw, syh
   float sxw, syh;
+  int vec4;                  // kGrid: C % 4 == 0 and gout 16-byte aligned (rows read as float4)
 };
 
 __device__ __forceinline__ bool batch_ok(int64_t b, int64_t B) { return b >= 0 && b < B; }
@@ -310,6 +311,154 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict_
   }
 }
 
+// Many-channel grid adjoint (kGrid, C > 4, grids of at least 2 x 2 nodes) in gather form: four LDS float
+// atomics per event and channel bound the scatter form there.  A workgroup takes the same records as
+// k_tile_accum (a kAccRange range of the tile-ordered array) kGatherBlock at a time: it bins them in LDS by
+// base node (one integer atomic each), stages their gradient rows in LDS, and then each of its threads owns one
+// of the tile's (T + 1)^2 nodes and adds, channel by channel in registers, the events of the four bins whose
+// corners include that node.  The terms are the same fp32 products go * w as the scatter form's; they are added
+// in another order.  The flush is the scatter form's: one global atomic per non-zero node and channel.
+constexpr int kGatherBlock = 320;                // >= 17 * 17 node owners
+constexpr int kGatherBins = 16 * 16;
+
+__global__ void __launch_bounds__(kGatherBlock) k_tile_gather_grid(const int* __restrict__ boff,
+                                                                   const float4* __restrict__ rec,
+                                                                   const float* __restrict__ gout, TileGeo g,
+                                                                   float* __restrict__ out) {
+  constexpr int T = 16, L = T + 1;
+  extern __shared__ float gs[];                   // kGatherBlock rows of nc floats
+  __shared__ float sax[kGatherBlock], say[kGatherBlock];
+  __shared__ int bin_of[kGatherBlock], rank_of[kGatherBlock];
+  __shared__ int bcnt[kGatherBins], boffs[kGatherBins + 1];
+  __shared__ int order[kGatherBlock];
+  __shared__ int wsum[kGatherBlock / kWave + 1];
+  __shared__ int ts[kGatherBlock + 1];
+  __shared__ int found, found2;
+  const int nc = g.C;
+  const int tid = threadIdx.x;
+  const int total = boff[g.nkeys * g.nblk];
+  const int r0 = blockIdx.x * kAccRange;
+  if (r0 >= total) return;
+  const int r1 = min(r0 + kAccRange, total);
+  auto tstart = [&](int k) { return boff[min(k, g.nkeys) * g.nblk]; };
+  const int step = (g.nkeys + kGatherBlock - 1) / kGatherBlock;
+  if (tid == 0) {
+    found = 0;
+    found2 = 0;
+  }
+  __syncthreads();
+  {
+    const int k = tid * step;
+    if (k < g.nkeys && tstart(k) <= r0) atomicMax(&found, k);
+  }
+  __syncthreads();
+  const int coarse = found;
+  {
+    const int k = coarse + tid;
+    if (tid < step && k < g.nkeys && tstart(k) <= r0) atomicMax(&found2, k);
+  }
+  __syncthreads();
+  const int64_t pl = (int64_t)g.H * g.W;
+  const int plane = g.TY * g.TX;
+  const int ly = tid / L, lx = tid - ly * L;      // this thread's node (tid < L * L)
+  for (int base = max(coarse, found2); base < g.nkeys; base += kGatherBlock) {
+    for (int i = tid; i <= kGatherBlock; i += kGatherBlock) ts[i] = tstart(base + i);
+    __syncthreads();
+    bool done = false;
+    for (int i = 0; i < kGatherBlock && base + i < g.nkeys; ++i) {
+      const int key = base + i;
+      const int s0 = max(r0, ts[i]), s1 = min(r1, ts[i + 1]);
+      if (s0 >= r1) {
+        done = true;
+        break;
+      }
+      if (s0 >= s1) continue;                     // empty tile
+      const int b = key / plane, r = key - b * plane;
+      const int ty = r / g.TX, tx = r - ty * g.TX;
+      const int ox = tx * T, oy = ty * T;
+      float acc[kMaxChannels];
+#pragma unroll
+      for (int c = 0; c < kMaxChannels; ++c) acc[c] = 0.f;
+      for (int c0 = s0; c0 < s1; c0 += kGatherBlock) {
+        for (int k = tid; k < kGatherBins; k += kGatherBlock) bcnt[k] = 0;
+        __syncthreads();
+        const int k = c0 + tid;
+        int bin = -1, rank = 0;
+        if (k < s1) {
+          const float4 q = rec[k];
+          const GridCell c = grid_cell(q.x, q.y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
+          const int bx = c.x0 - ox, by = c.y0 - oy;
+          if ((unsigned)bx < (unsigned)T && (unsigned)by < (unsigned)T) {   // always: the binning chose this tile
+            bin = by * T + bx;
+            sax[tid] = c.ax;
+            say[tid] = c.ay;
+            const int j = __float_as_int(q.w);
+            const float* row = gout + (int64_t)j * nc;
+            float* dst = gs + tid * nc;
+            if (g.vec4) {
+              for (int c4 = 0; c4 < nc; c4 += 4) {
+                const float4 v = *(const float4*)(row + c4);
+                dst[c4] = v.x;
+                dst[c4 + 1] = v.y;
+                dst[c4 + 2] = v.z;
+                dst[c4 + 3] = v.w;
+              }
+            } else {
+              for (int c = 0; c < nc; ++c) dst[c] = row[c];
+            }
+            rank = atomicAdd(bcnt + bin, 1);
+          }
+        }
+        bin_of[tid] = bin;
+        rank_of[tid] = rank;
+        __syncthreads();
+        {                                         // bin offsets: kGatherBins counts over the block's threads
+          const int v = tid < kGatherBins ? bcnt[tid] : 0;
+          int tot;
+          const int ex = block_exclusive_scan<kGatherBlock>(v, wsum, tot);
+          if (tid < kGatherBins) boffs[tid] = ex;
+          if (tid == 0) boffs[kGatherBins] = tot;
+        }
+        __syncthreads();
+        if (bin_of[tid] >= 0) order[boffs[bin_of[tid]] + rank_of[tid]] = tid;
+        __syncthreads();
+        if (tid < L * L) {
+          // corner 00 from bin (lx, ly), 01 from (lx - 1, ly), 10 from (lx, ly - 1), 11 from (lx - 1, ly - 1)
+#pragma unroll
+          for (int corner = 0; corner < 4; ++corner) {
+            const int cx = lx - (corner & 1), cy = ly - (corner >> 1);
+            if (cx < 0 || cy < 0 || cx >= T || cy >= T) continue;
+            const int bb = cy * T + cx;
+            for (int o = boffs[bb]; o < boffs[bb + 1]; ++o) {
+              const int e = order[o];
+              const float ax = sax[e], ay = say[e];
+              const float w = corner == 0 ? (1.f - ax) * (1.f - ay)
+                            : corner == 1 ? ax * (1.f - ay)
+                            : corner == 2 ? (1.f - ax) * ay
+                                          : ax * ay;
+              const float* row = gs + e * nc;
+#pragma unroll
+              for (int c = 0; c < kMaxChannels; ++c)
+                if (c < nc) acc[c] += row[c] * w;
+            }
+          }
+        }
+        __syncthreads();                          // the staging arrays are refilled by the next chunk
+      }
+      if (tid < L * L) {
+        const int py = oy + ly, px = ox + lx;
+        if (py < g.H && px < g.W) {
+#pragma unroll
+          for (int c = 0; c < kMaxChannels; ++c)
+            if (c < nc && acc[c] != 0.f) atomicAdd(out + ((int64_t)b * nc + c) * pl + (int64_t)py * g.W + px, acc[c]);
+        }
+      }
+    }
+    if (done) break;
+    __syncthreads();                              // ts is reloaded
+  }
+}
+
 // gpos of the bilinear gather backward (csrc/atl_cpu.cpp:151-172, the position half): per event, no atomics.
 __global__ void __launch_bounds__(kBlock) k_gather_bwd_pos(const float* __restrict__ gval,
                                                            const float* __restrict__ img,
@@ -355,6 +504,7 @@ bool tile_geo(int mode, int64_t B, int64_t H, int64_t W, int64_t N, int64_t img_
               int R = 0) {
   if (B < 1 || H < 1 || W < 1 || N < 0 || N >= ((int64_t)1 << 30) || (double)B * H * W >= 2.0e9) return false;
   if (mode == kGauss && (R < 0 || R > kMaxGaussRadius)) return false;
+  g.vec4 = 0;
   const int64_t ext = mode == kGauss ? 2 * R : 1;   // base corners / centres span W + ext positions per row
   for (int T : {16, 32}) {
     const int64_t tx = (W + ext + T - 1) / T, ty = (H + ext + T - 1) / T;
@@ -517,6 +667,7 @@ int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t
   TileGeo g;
   if (!tile_geo(kGrid, B, Hg, Wg, N, img_h, img_w, g) || C < 1 || C > kMaxChannels || (C > 4 && g.T != 16)) { set_error("sample_grid_bwd_planned: bad sizes (C <= 4, or C <= 32 on grids of at most 16384 16x16 tiles)"); return 1; }
   g.C = (int)C;
+  g.vec4 = (C & 3) == 0 && (reinterpret_cast<uintptr_t>(gout) & 15) == 0;
   if (!ws || !gfield || (N > 0 && !gout)) { set_error("sample_grid_bwd_planned: null argument"); return 1; }
   (void)pos;                                     // the plan's records carry the positions
   const TileLayout L = tile_layout(g);
@@ -525,7 +676,17 @@ int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t
     case 2: tile_accum<kGrid, 2>(g, L, ws, gout, gfield, stream); break;
     case 3: tile_accum<kGrid, 3>(g, L, ws, gout, gfield, stream); break;
     case 4: tile_accum<kGrid, 4>(g, L, ws, gout, gfield, stream); break;
-    default: tile_accum<kGrid, 0>(g, L, ws, gout, gfield, stream); break;
+    default:
+      if (g.T == 16 && Hg >= 2 && Wg >= 2) {     // gather form (C > 4 is only planned with 16 x 16 tiles)
+        if (g.nblk == 0) break;
+        const char* w = (const char*)ws;
+        hipLaunchKernelGGL(k_tile_gather_grid, dim3((unsigned)((g.N + kAccRange - 1) / kAccRange)),
+                           dim3(kGatherBlock), (size_t)kGatherBlock * C * sizeof(float), stream,
+                           (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, gfield);
+      } else {
+        tile_accum<kGrid, 0>(g, L, ws, gout, gfield, stream);
+      }
+      break;
   }
   return check_launch("sample_grid_bwd_planned");
 }
