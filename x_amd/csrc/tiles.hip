@@ -395,14 +395,8 @@ __global__ void __launch_bounds__(kGatherBlock) k_tile_gather_grid(const int* __
             const int j = __float_as_int(q.w);
             const float* row = gout + (int64_t)j * nc;
             float* dst = gs + tid * nc;
-            if (g.vec4) {
-              for (int c4 = 0; c4 < nc; c4 += 4) {
-                const float4 v = *(const float4*)(row + c4);
-                dst[c4] = v.x;
-                dst[c4 + 1] = v.y;
-                dst[c4 + 2] = v.z;
-                dst[c4 + 3] = v.w;
-              }
+            if (g.vec4) {                         // nc % 4 == 0: 16-byte rows in global memory and in LDS
+              for (int c4 = 0; c4 < nc; c4 += 4) *(float4*)(dst + c4) = *(const float4*)(row + c4);
             } else {
               for (int c = 0; c < nc; ++c) dst[c] = row[c];
             }
@@ -437,9 +431,21 @@ __global__ void __launch_bounds__(kGatherBlock) k_tile_gather_grid(const int* __
                             : corner == 2 ? (1.f - ax) * ay
                                           : ax * ay;
               const float* row = gs + e * nc;
+              if (g.vec4) {
 #pragma unroll
-              for (int c = 0; c < kMaxChannels; ++c)
-                if (c < nc) acc[c] += row[c] * w;
+                for (int c4 = 0; c4 < kMaxChannels; c4 += 4) {
+                  if (c4 >= nc) break;
+                  const float4 v = *(const float4*)(row + c4);
+                  acc[c4] += v.x * w;
+                  acc[c4 + 1] += v.y * w;
+                  acc[c4 + 2] += v.z * w;
+                  acc[c4 + 3] += v.w * w;
+                }
+              } else {
+#pragma unroll
+                for (int c = 0; c < kMaxChannels; ++c)
+                  if (c < nc) acc[c] += row[c] * w;
+              }
             }
           }
         }
