@@ -91,7 +91,7 @@ int atl_sample_grid_bwd_pos(const float* gout, const float* field, int64_t B, in
  * field_cl (B, Hg, Wg, 4*ceil(C/4)) float, channels past C zero.  atl_sample_grid_fwd_cl and
  * atl_sample_grid_bwd_pos_cl then return the same bits as atl_sample_grid_fwd and atl_sample_grid_bwd_pos on
  * the plane field.  field_cl 16-byte aligned (out and gout too when C % 4 == 0); N * ceil(C/4) < 2^31 for the
- * forward. */
+ * forward; C <= 256 for the position gradient. */
 int atl_field_channels_last(const float* field, int64_t B, int64_t C, int64_t Hg, int64_t Wg, float* field_cl,
                             hipStream_t stream);
 int atl_sample_grid_fwd_cl(const float* field_cl, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,

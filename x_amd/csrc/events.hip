@@ -434,6 +434,9 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_fwd_cl(const float4* __r
   }
 }
 
+// Position gradient: one lane per (event, channel quad) as in the forward, so the field and gout reads of an
+// event are consecutive 16-byte pieces; each lane forms its four channel terms and the event's first lane adds
+// all of them in channel order, as the plane kernel does (same bits).
 __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos_cl(const float* __restrict__ gout,
                                                                    const float4* __restrict__ fcl, int64_t B, int C,
                                                                    int Q, int Hg, int Wg,
@@ -441,29 +444,37 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos_cl(const float* 
                                                                    const int64_t* __restrict__ bidx, int64_t N,
                                                                    float sxw, float syh, int scale,
                                                                    float2* __restrict__ gpos) {
-  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= N) return;
-  const int64_t b = bidx[n];
-  const float2 p = pos[n];
-  float sx = 0.f, sy = 0.f;
-  if (batch_ok(b, B)) {
-    float gx = p.x, gy = p.y, kx = 1.f, ky = 1.f;
-    if (scale) {
-      gx = p.x / sxw * (float)(Wg - 1);
-      gy = p.y / syh * (float)(Hg - 1);
-      kx = (float)(Wg - 1) / sxw;
-      ky = (float)(Hg - 1) / syh;
-    }
-    const bool inx = gx >= 0.f && gx <= (float)(Wg - 1), iny = gy >= 0.f && gy <= (float)(Hg - 1);
-    const GridCorners c = grid_corners(p.x, p.y, Hg, Wg, sxw, syh, scale != 0);
-    const float ax = c.ax, ay = c.ay;
-    const float4* f = fcl + b * ((int64_t)Hg * Wg) * Q;
-    const float* go_row = gout + n * C;
-    for (int q = 0; q < Q; ++q) {
-      const float4 a = f[(int64_t)c.o00 * Q + q], e = f[(int64_t)c.o01 * Q + q], h = f[(int64_t)c.o10 * Q + q],
-                   k = f[(int64_t)c.o11 * Q + q];
-      const float f00[4] = {a.x, a.y, a.z, a.w}, f01[4] = {e.x, e.y, e.z, e.w}, f10[4] = {h.x, h.y, h.z, h.w},
-                  f11[4] = {k.x, k.y, k.z, k.w};
+  const int lane = threadIdx.x & (kWave - 1);
+  const int epw = kWave / Q;                     // events per wave
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int e = lane / Q, q = lane - e * Q;
+  const int64_t n = wave * epw + e;
+  const bool live = e < epw && n < N;
+  float tx[4] = {0.f, 0.f, 0.f, 0.f}, ty[4] = {0.f, 0.f, 0.f, 0.f};
+  bool ok = false, inx = false, iny = false;
+  float kx = 1.f, ky = 1.f;
+  if (live) {
+    const int64_t b = bidx[n];
+    ok = batch_ok(b, B);
+    if (ok) {
+      const float2 p = pos[n];
+      float gx = p.x, gy = p.y;
+      if (scale) {
+        gx = p.x / sxw * (float)(Wg - 1);
+        gy = p.y / syh * (float)(Hg - 1);
+        kx = (float)(Wg - 1) / sxw;
+        ky = (float)(Hg - 1) / syh;
+      }
+      inx = gx >= 0.f && gx <= (float)(Wg - 1);
+      iny = gy >= 0.f && gy <= (float)(Hg - 1);
+      const GridCorners c = grid_corners(p.x, p.y, Hg, Wg, sxw, syh, scale != 0);
+      const float ax = c.ax, ay = c.ay;
+      const float4* f = fcl + b * ((int64_t)Hg * Wg) * Q + q;
+      const float4 a = f[(int64_t)c.o00 * Q], h0 = f[(int64_t)c.o01 * Q], h1 = f[(int64_t)c.o10 * Q],
+                   k1 = f[(int64_t)c.o11 * Q];
+      const float f00[4] = {a.x, a.y, a.z, a.w}, f01[4] = {h0.x, h0.y, h0.z, h0.w},
+                  f10[4] = {h1.x, h1.y, h1.z, h1.w}, f11[4] = {k1.x, k1.y, k1.z, k1.w};
+      const float* go_row = gout + n * C;
       float go[4];
       if ((C & 3) == 0) {
         const float4 g4 = *(const float4*)(go_row + 4 * q);
@@ -476,16 +487,35 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos_cl(const float* 
         for (int j = 0; j < 4; ++j) go[j] = 4 * q + j < C ? go_row[4 * q + j] : 0.f;
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {                // channel order as the plane kernel (padded channels skipped)
-        if (4 * q + j >= C) break;
-        sx += go[j] * ((1.f - ay) * (f01[j] - f00[j]) + ay * (f11[j] - f10[j]));
-        sy += go[j] * ((1.f - ax) * (f10[j] - f00[j]) + ax * (f11[j] - f01[j]));
+      for (int j = 0; j < 4; ++j) {
+        tx[j] = go[j] * ((1.f - ay) * (f01[j] - f00[j]) + ay * (f11[j] - f10[j]));
+        ty[j] = go[j] * ((1.f - ax) * (f10[j] - f00[j]) + ax * (f11[j] - f01[j]));
       }
     }
-    sx = inx ? sx * kx : 0.f;
-    sy = iny ? sy * ky : 0.f;
   }
-  gpos[n] = make_float2(sx, sy);
+  // the event's first lane adds the terms of channels 0 .. C-1 in order (every lane takes part in the shuffles)
+  float sx = 0.f, sy = 0.f;
+  for (int i = 0; i < Q; ++i) {
+    const int src = min(lane + i, kWave - 1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float ox = __shfl(tx[j], src), oy = __shfl(ty[j], src);
+      if (4 * i + j < C) {
+        sx += ox;
+        sy += oy;
+      }
+    }
+  }
+  if (live && q == 0) {
+    if (ok) {
+      sx = inx ? sx * kx : 0.f;
+      sy = iny ? sy * ky : 0.f;
+    } else {
+      sx = 0.f;
+      sy = 0.f;
+    }
+    gpos[n] = make_float2(sx, sy);
+  }
 }
 
 // ------------------------------------------------------------------------------ trajectory displacement
@@ -784,9 +814,12 @@ int atl_sample_grid_bwd_pos_cl(const float* gout, const float* field_cl, int64_t
   }
   const int scale = img_h > 0 && img_w > 0;
   const float sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1), syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
-  hipLaunchKernelGGL(k_sample_grid_bwd_pos_cl, dim3(grid_for(N)), dim3(kBlock), 0, stream, gout,
-                     (const float4*)field_cl, B, (int)C, (int)((C + 3) / 4), (int)Hg, (int)Wg, (const float2*)pos, b,
-                     N, sxw, syh, scale, (float2*)gpos);
+  const int64_t Q = (C + 3) / 4;
+  if (Q > kWave) { set_error("sample_grid_bwd_pos_cl: at most %d channels", 4 * kWave); return 1; }
+  const int64_t waves = (N + kWave / Q - 1) / (kWave / Q);
+  hipLaunchKernelGGL(k_sample_grid_bwd_pos_cl, dim3(grid_for(waves * kWave)), dim3(kBlock), 0, stream, gout,
+                     (const float4*)field_cl, B, (int)C, (int)Q, (int)Hg, (int)Wg, (const float2*)pos, b, N, sxw, syh,
+                     scale, (float2*)gpos);
   return check_launch("sample_grid_bwd_pos_cl");
 }
 

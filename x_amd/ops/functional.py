@@ -149,7 +149,7 @@ class _SampleGrid(torch.autograd.Function):
         out = torch.empty(N, C, device=pos.device, dtype=F32)
         ctx.plan = None
         Q = (C + 3) // 4
-        cl = C >= _SampleGrid.CL_MIN_CHANNELS and N * Q < 2 ** 31 - 1024
+        cl = _SampleGrid.CL_MIN_CHANNELS <= C <= 256 and N * Q < 2 ** 31 - 1024
         with torch.cuda.device(pos.device):
             st = stream_of(pos)
             if cl:
