@@ -526,22 +526,32 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos_cl(const float* 
 // products (torch's pow rounds differently by a few ulps) and the k sum runs in order.
 constexpr int kTrajMaxK = 16;
 
+__host__ __device__ constexpr int binom_int(int n, int k) {   // exact for n <= 16
+  int r = 1;
+  for (int i = 1; i <= k; ++i) r = r * (n - k + i) / i;
+  return r;
+}
+
 template <int K>
 __device__ __forceinline__ void traj_basis(float t, int bernstein, float (&g)[K]) {
+  float tk = 1.f;
+  if (!bernstein) {
+#pragma unroll
+    for (int k = 1; k <= K; ++k) {
+      tk = tk * t;
+      g[k - 1] = tk;
+    }
+    return;
+  }
   const float u = 1.f - t;
-  float tk = 1.f, binom = 1.f;
+  float pw[K];                                   // pw[m] = u^m by repeated products
+  pw[0] = 1.f;
+#pragma unroll
+  for (int m = 1; m < K; ++m) pw[m] = pw[m - 1] * u;
 #pragma unroll
   for (int k = 1; k <= K; ++k) {
     tk = tk * t;
-    if (!bernstein) {
-      g[k - 1] = tk;
-      continue;
-    }
-    binom = binom * (float)(K - k + 1) / (float)k;   // binom(K, k): exact integers in fp32 for K <= 24
-    float uk = 1.f;
-#pragma unroll
-    for (int j = 0; j < K - k; ++j) uk = uk * u;
-    g[k - 1] = binom * tk * uk;
+    g[k - 1] = (float)binom_int(K, k) * tk * pw[K - k];
   }
 }
 
