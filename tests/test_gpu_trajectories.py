@@ -112,6 +112,25 @@ def test_traj_displacement_matches_fp64_and_torch_gradients(K, kind):
     assert not N(tp.grad)[~ok].any()
 
 
+def test_traj_displacement_empty_and_rejected_inputs():
+    """No events: an empty (0, 2) result and zero gradients; a basis the kernel does not know and times that
+    carry a gradient are refused on the host."""
+    print("traj_displacement empty", flush=True)
+    from x_amd.ops import functional as F
+    tf = torch.randn(2, 8, 9, 11, device=DEV, requires_grad=True)
+    tp = torch.zeros(0, 2, device=DEV, requires_grad=True)
+    tb = torch.zeros(0, dtype=torch.long, device=DEV)
+    tt = torch.zeros(0, device=DEV)
+    d = F.traj_displacement(tf, tp, tb, tt, 4, "bezier")
+    assert d.shape == (0, 2)
+    d.sum().backward()
+    assert not N(tf.grad).any() and tp.grad.shape == (0, 2)
+    with pytest.raises(ValueError):
+        F.traj_displacement(tf, tp, tb, tt, 4, "spline")
+    with pytest.raises(ValueError):
+        F.traj_displacement(tf, tp, tb, tt.clone().requires_grad_(True), 4, "bezier")
+
+
 @pytest.mark.parametrize("K,kind", [(1, "polynomial"), (3, "bezier"), (4, "polynomial"), (10, "bezier")])
 def test_pixel_trajectories_device_matches_cpu(K, kind):
     """Transport (fixed-point origin + displacement) values and coefficient gradients, device vs CPU."""
@@ -163,6 +182,6 @@ def test_anchored_sliced_device_matches_cpu(smooth):
         obj = AnchoredSliced(n_slices=6, sigma=1.0, tau=0.3, seed=0, smooth_anchors=smooth)
         out = obj(ev, PixelTrajectories(c, 3, "bezier"))
         out["loss"].backward()
-        res[dev] = (float(out["loss"]), N(c.grad))
+        res[dev] = (float(out["loss"].detach()), N(c.grad))
     assert abs(res[DEV][0] - res["cpu"][0]) <= 1e-5 * abs(res["cpu"][0])
     close_rel(res[DEV][1], res["cpu"][1], 1e-4)
