@@ -388,7 +388,7 @@ def trajectories_main(a, dev):
         step()
     torch.cuda.synchronize()
     kernels = list(TRAJ_BYTES)
-    rec = _ext.time_kernels(kernels, every=25)     # hundreds of calls a step: time a sample of them
+    rec = _ext.time_kernels(kernels, every=5)      # hundreds of calls a step: time one in five
     t0 = time.perf_counter()
     for _ in range(a.steps):
         step()
