@@ -312,13 +312,14 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict_
 }
 
 // Many-channel grid adjoint (kGrid, C > 4, grids of at least 2 x 2 nodes) in gather form: four LDS float
-// atomics per event and channel bound the scatter form there.  A workgroup takes the same records as
-// k_tile_accum (a kAccRange range of the tile-ordered array) kGatherBlock at a time: it bins them in LDS by
+// atomics per event and channel bound the scatter form there.  A workgroup takes a range of kGatherRange
+// records of the tile-ordered array, kGatherBlock at a time: it bins them in LDS by
 // base node (one integer atomic each), stages their gradient rows in LDS, and then each of its threads owns one
 // of the tile's (T + 1)^2 nodes and adds, channel by channel in registers, the events of the four bins whose
 // corners include that node.  The terms are the same fp32 products go * w as the scatter form's; they are added
 // in another order.  The flush is the scatter form's: one global atomic per non-zero node and channel.
 constexpr int kGatherBlock = 320;                // >= 17 * 17 node owners
+constexpr int kGatherRange = 2 * kGatherBlock;   // records per workgroup: two full chunks
 constexpr int kGatherBins = 16 * 16;
 
 __global__ void __launch_bounds__(kGatherBlock) k_tile_gather_grid(const int* __restrict__ boff,
@@ -337,9 +338,9 @@ __global__ void __launch_bounds__(kGatherBlock) k_tile_gather_grid(const int* __
   const int nc = g.C;
   const int tid = threadIdx.x;
   const int total = boff[g.nkeys * g.nblk];
-  const int r0 = blockIdx.x * kAccRange;
+  const int r0 = blockIdx.x * kGatherRange;
   if (r0 >= total) return;
-  const int r1 = min(r0 + kAccRange, total);
+  const int r1 = min(r0 + kGatherRange, total);
   auto tstart = [&](int k) { return boff[min(k, g.nkeys) * g.nblk]; };
   const int step = (g.nkeys + kGatherBlock - 1) / kGatherBlock;
   if (tid == 0) {
@@ -686,7 +687,7 @@ int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t
       if (g.T == 16 && Hg >= 2 && Wg >= 2) {     // gather form (C > 4 is only planned with 16 x 16 tiles)
         if (g.nblk == 0) break;
         const char* w = (const char*)ws;
-        hipLaunchKernelGGL(k_tile_gather_grid, dim3((unsigned)((g.N + kAccRange - 1) / kAccRange)),
+        hipLaunchKernelGGL(k_tile_gather_grid, dim3((unsigned)((g.N + kGatherRange - 1) / kGatherRange)),
                            dim3(kGatherBlock), (size_t)kGatherBlock * C * sizeof(float), stream,
                            (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, gfield);
       } else {
