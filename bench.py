@@ -17,9 +17,11 @@ Other workloads (parity-test configurations, not the headline metric), same outp
     python bench.py --workload iwe-plumbing    # the same on 100k events 240x180, constant flow (2, -1.25)
     python bench.py --workload anchored-blobs  # contention stress: the anchored score on 4M events, 90% in 5
                                                # Gaussian blobs (sigma 8 px), Sim2 flow (0, 0, 0.1, 0.1)
-    python bench.py --workload trajectories    # 4 windows x 500k events 640x480, degree-10 Bezier pixel
-                                               # trajectories, sliced anchored score (10 slices, sigma 1,
-                                               # tau 0.8), grad to the coefficient grid
+    python bench.py --workload trajectories    # 4 windows x 500k events 640x480 (25 ms each), per-pixel cubic
+                                               # B-spline trajectories with 10 control points: anchored
+                                               # pair-sum score (h 1, tau 20 ms = 0.8, 16 slices) + the IWE
+                                               # contrast (bilinear splat at t = 0.5), grad to the control
+                                               # points
 
 Two helpers for the rocprofv3 summaries under profiles/ (no GPU work beyond what they name):
 
@@ -51,8 +53,11 @@ import torch  # noqa: E402
 VALU_PEAK = 256 * 4 * 16 * 2.4e9      # fp32 lane-slots/s (non-packed): 256 CUs x 4 SIMD x 16 lanes x 2.4 GHz
 FP32_PEAK = 157.3e12                   # fp32 FLOP/s (packed FMA), MI355X
 SLOTS_FWD, SLOTS_BWD = 14, 16          # VALU lane-slots per contributing pair (forward, backward)
+SLOTS_BWD_TRAJ = 20                    # trajectory backward: the pair recomputed (13) + k gS (1) + k gS r (2) +
+                                       # position and velocity gradient sums (2 adds, 2 FMAs)
 FLOPS_FWD, FLOPS_BWD = 13, 19          # fp32 flops per contributing pair (FMA = 2, exp = 1)
-KERNEL_OF = {"atl_fast_pair_fwd": "k_fast_fwd<false>", "atl_fast_pair_bwd": "k_fast_bwd"}
+KERNEL_OF = {"atl_fast_pair_fwd": "k_fast_fwd<false>", "atl_fast_pair_bwd": "k_fast_bwd",
+             "atl_fast_pair_bwd_traj": "k_fast_bwd_traj<10>"}
 COUNTERS = ROOT / "profiles" / "anchored_score_1M_640x480_counters.md"
 
 
@@ -179,10 +184,50 @@ def workload(kind, n_events, device):
     return win, EventPacket.from_window(win, device), motion.to(device), desc
 
 
+def _host_cpu():
+    """Model name and physical cores of the host (/proc/cpuinfo), and the CPUs this process may use."""
+    model, cores = "unknown", set()
+    phys = core = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+            elif not k and phys is not None and core is not None:
+                cores.add((phys, core))
+                phys = core = None
+    except OSError:
+        pass
+    return {"cpu_model": model, "host_physical_cores": len(cores) or None,
+            "cpus_available": len(os.sched_getaffinity(0))}
+
+
+def _oracle():
+    """The oracle, with its OpenMP threads bound close (set before its runtime starts)."""
+    os.environ.setdefault("OMP_PROC_BIND", "close")
+    os.environ.setdefault("OMP_PLACES", "cores")
+    import oracle as O
+    return O
+
+
+def _baseline_line(O, n, n_all, dt, what):
+    return dict({"value": n / dt, "unit": "events/s", "cores": O.num_threads(), "kind": "port",
+                 "omp_proc_bind": os.environ.get("OMP_PROC_BIND"),
+                 "sample": (f"{what} on the whole window, {dt:.2f} s" if n == n_all else
+                            f"{what} on the first {n} events of the same window (time-sorted prefix, the largest of "
+                            f"a doubling series that fits the budget; it truncates the +-tau neighbourhoods near "
+                            f"its end), {dt:.2f} s")}, **_host_cpu())
+
+
 def _velocity_np(win, xy, b):
     """The window's motion field at xy (NumPy, fp32 op order of the motion models) and, for a dense grid,
     the flow-lookup indices and weights."""
-    import oracle as O
+    O = _oracle()
     if win.motion["kind"] == "dense":
         return O.dense_velocity(win.motion["grid"], xy, b, win.height, win.width)
     th = win.motion["theta"].astype(np.float32)
@@ -209,9 +254,10 @@ def _bounded_run(run, n_all, budget):
 
 
 def cpu_baseline(win, sigma, budget):
-    """Oracle (OpenMP restatement of the reference CPU loops + NumPy plan) on the same workload: the full
-    anchored score forward + backward, timed once after a warm-up on a subset."""
-    import oracle as O
+    """Oracle on the same workload: the full anchored score forward + backward, the plan built with torch CPU
+    ops as the reference builds it on CPU tensors (atl/ops/functional.py:132-178), the pair sums, splat and
+    gather in the OpenMP restatement of csrc/atl_cpu.cpp; timed once on a bounded prefix."""
+    O = _oracle()
     H, W = win.height, win.width
     rng = np.random.default_rng(0)
     xs = (win.xy + rng.uniform(-0.5, 0.5, win.xy.shape)).astype(np.float32)
@@ -222,8 +268,8 @@ def cpu_baseline(win, sigma, budget):
         sl = slice(0, n)
         v, idx, wts = _velocity_np(win, xs[sl], win.b[sl])
         anchors = np.arange(n)
-        p = O.build_pair_plan(xs[sl], win.t[sl], v, win.b[sl], 1, H, W, anchors, sigma, 0.2, 3.0, 16,
-                              anchor_xy=xa[sl])
+        p = O.build_pair_plan_torch(xs[sl], win.t[sl], v, win.b[sl], 1, H, W, anchors, sigma, 0.2, 3.0, 16,
+                                    anchor_xy=xa[sl])
         S = O.ats_pair_fwd(p, sigma, 0.2, 3.0)
         wc = O.window_counts(win.t[sl], win.b[sl], anchors, 0.2)
         vis = (O.visible_fraction_dense(win.motion["grid"], xa[sl], win.t[sl], win.b[sl], win.t[sl], win.b[sl], 1,
@@ -234,11 +280,7 @@ def cpu_baseline(win, sigma, budget):
             O.sample_grid_bwd(gv, idx, wts, win.motion["grid"].shape)
 
     n, dt, _ = _bounded_run(run, win.n, budget)
-    return {"value": n / dt, "unit": "events/s", "cores": O.num_threads(), "kind": "port",
-            "sample": (f"anchored score fwd+bwd on the whole window, {dt:.2f} s" if n == win.n else
-                       f"anchored score fwd+bwd on the first {n} events of the same window (time-sorted prefix, "
-                       f"the largest of a doubling series that fits the budget; it truncates the +-tau "
-                       f"neighbourhoods near its end), {dt:.2f} s")}
+    return _baseline_line(O, n, win.n, dt, "anchored score fwd+bwd")
 
 
 # ----------------------------------------------------------------------------------------- IWE workloads
@@ -275,7 +317,7 @@ def iwe_workload(kind, dev):
 def iwe_cpu_baseline(win, t_ref, budget):
     """Oracle on the host: NumPy warp (+ flow lookup), OpenMP splat / gather forward and backward, flow-grid
     adjoint; same loss as the GPU step."""
-    import oracle as O
+    O = _oracle()
     H, W = win.height, win.width
 
     def run(n):
@@ -298,10 +340,7 @@ def iwe_cpu_baseline(win, t_ref, budget):
             gv.sum(0)
 
     n, dt, _ = _bounded_run(run, win.n, budget)
-    return {"value": n / dt, "unit": "events/s", "cores": O.num_threads(), "kind": "port",
-            "sample": (f"IWE step on the whole window, {dt:.2f} s" if n == win.n else
-                       f"IWE step on the first {n} events of the same window (time-sorted prefix, the largest of "
-                       f"a doubling series that fits the budget), {dt:.2f} s")}
+    return _baseline_line(O, n, win.n, dt, "IWE step")
 
 
 def iwe_main(a, dev):
@@ -351,77 +390,75 @@ def iwe_main(a, dev):
 
 
 # ----------------------------------------------------------------------------------- trajectories workload
-TRAJ_BYTES = {     # algorithmic bytes per entry point: per event, plus the field / image once (C channels)
-    "atl_sample_grid_fwd": lambda n, c, f, hw: (16 + 4 * c) * n + 4 * c * f,
-    "atl_sample_grid_bwd_planned": lambda n, c, f, hw: (16 + 4 * c) * n + 8 * c * f,
-    "atl_sample_grid_bwd_pos": lambda n, c, f, hw: (24 + 4 * c) * n + 4 * c * f,
-    "atl_sample_grid_fwd_cl": lambda n, c, f, hw: (16 + 4 * c) * n + 4 * c * f,
-    "atl_traj_displacement": lambda n, c, f, hw: 28 * n + 4 * c * f,
-    "atl_traj_gout": lambda n, c, f, hw: (12 + 4 * c) * n,
-    "atl_sample_grid_bwd_pos_cl": lambda n, c, f, hw: (24 + 4 * c) * n + 4 * c * f,
-    "atl_splat_gauss_fwd": lambda n, c, f, hw: 20 * n + 4 * hw,
-    "atl_splat_gauss_fwd_ws": lambda n, c, f, hw: 20 * n + 4 * hw,
-    "atl_splat_gauss_bwd": lambda n, c, f, hw: 32 * n + 4 * hw,
-    "atl_gather_bilinear_fwd": lambda n, c, f, hw: 20 * n + 4 * hw,
-    "atl_gather_bilinear_bwd_ws": lambda n, c, f, hw: 28 * n + 8 * hw,
-}
+TRAJ_TAU = 0.8                         # 20 ms of a 25 ms window
 
 
 def trajectories_main(a, dev):
+    """The continuous-time workload: AnchoredTrajectories (pair sums over per-pixel cubic B-spline trajectories,
+    h = 1, tau = 0.8, 16 slices, every event an anchor) plus the IWE contrast at t = 0.5, backward to the
+    (4, 20, 480, 640) control points."""
     from x_amd import synth
     from x_amd.core import EventPacket
     from x_amd.motion import PixelTrajectories
-    from x_amd.objectives import AnchoredSliced
+    from x_amd.objectives import AnchoredTrajectories, iwe_variance
     from x_amd.ops import _ext
-    win = synth.trajectory_windows(seed=0)
+    from x_amd.ops import functional as F
+    win = synth.bspline_windows(seed=0)
     K = win.motion["K"]
     ev = EventPacket.from_window(win, dev)
     coeff = torch.tensor(win.motion["coeffs"], device=dev, requires_grad=True)
-    obj = AnchoredSliced(n_slices=10, sigma=1.0, tau=0.8, seed=0, rng="device")
+    obj = AnchoredTrajectories(h=1.0, tau=TRAJ_TAU, cut=3.0, n_slices=16, n_anchors=None, seed=0, rng="device")
 
     def step():
         coeff.grad = None
-        out = obj(ev, PixelTrajectories(coeff, K, "bezier"))
-        out["loss"].backward()
+        m = PixelTrajectories(coeff, K, "bspline", tile=1)
+        loss = obj(ev, m)["loss"] - iwe_variance(ev, m, 0.5)
+        loss.backward()
 
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
-    kernels = list(TRAJ_BYTES)
-    rec = _ext.time_kernels(kernels, every=5)      # hundreds of calls a step: time one in five
+    kernels = ["atl_fast_pair_fwd", "atl_fast_pair_bwd_traj"]
+    rec = _ext.time_kernels(kernels, every=4)
+    first_draw = obj._philox[1]
     t0 = time.perf_counter()
     for _ in range(a.steps):
         step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec[k]])) for k in kernels if rec[k]}
-    ncall = _ext.timed_calls()
-    calls = {k: ncall.get(k, 0) / a.steps for k in kernels if rec[k]}
-    rec_all = {k: list(v) for k, v in rec.items()}
+    ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec[k]])) for k in kernels}
     _ext.time_kernels(())
-    tot = {k: ms[k] * calls[k] for k in ms}
-    dom = max(tot, key=lambda k: tot[k])
-    # achieved bandwidth of the dominant entry point: algorithmic bytes of every call (its own event count)
-    # over the summed call durations
-    nodes, pix = (win.height // 4) * (win.width // 4) * ev.batch_size, win.height * win.width * ev.batch_size
-    calls_dom = [(e0.elapsed_time(e1), n) for e0, e1, n in rec_all[dom]]
-    gbs = (sum(TRAJ_BYTES[dom](n, 2 * K, nodes, pix) for _, n in calls_dom) /
-           (sum(t for t, _ in calls_dom) * 1e-3) / 1e9)
-    n_launch = float(np.mean([n for _, n in calls_dom]))
+    # contributing pairs of the timed steps' own noise draws (counted outside the timed region)
+    pairs = []
+    with torch.no_grad():
+        m = PixelTrajectories(coeff.detach(), K, "bspline", tile=1)
+        tab = m.slice_tables(16, dev)
+        for draw in range(first_draw, first_draw + a.steps):
+            xs, xa = F.event_noise(ev.xy, 0, draw, 1.0)
+            p = m.origin(xs, ev.t, ev.b)
+            plan = F.FastPairPlan(p, ev.t, None, ev.b, ev.batch_size, ev.height, ev.width, None, 1.0, TRAJ_TAU, 3.0,
+                                  16, xa, traj=(m.coeff_rows(p, ev.b), K, tab))
+            pairs.append(int(plan.counts().sum()))
+    Kp = float(np.mean(pairs))
+    dom = max(kernels, key=lambda k: ms[k])
+    slots = SLOTS_FWD if dom.endswith("fwd") else SLOTS_BWD_TRAJ
+    achieved = Kp * slots / (ms[dom] * 1e-3)
     line = {
-        "metric": f"events/s for sliced anchored score fwd+bwd @{ev.n} events ({ev.batch_size} windows) 640x480, "
-                  f"degree-{K} pixel trajectories; % HBM roofline",
+        "metric": f"events/s for anchored-score (pair-sum + splat) fwd+bwd @{ev.n} events ({ev.batch_size} windows) "
+                  f"640x480, cubic B-spline trajectories; % VALU roofline",
         "value": ev.n * a.steps / dt, "unit": "events/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": 1e3 * dt / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"AnchoredSliced(n_slices=10, sigma=1, tau=0.8) on {ev.batch_size} windows x "
-                               f"{ev.n // ev.batch_size} events, 640x480, PixelTrajectories(K={K}, bezier, tile 4, "
-                               f"6 fixed-point steps), grad to the (4, {2 * K}, 480, 640) coefficient grid",
+        "config": {"workload": f"AnchoredTrajectories(h=1, tau={TRAJ_TAU}, cut=3, S=16, all anchors) - IWE variance "
+                               f"at t=0.5 on {ev.batch_size} windows x {ev.n // ev.batch_size} events, 640x480, "
+                               f"PixelTrajectories(K={K}, bspline, tile 1, 6 fixed-point steps), grad to the "
+                               f"({ev.batch_size}, {2 * K}, 480, 640) control points",
                    "events": ev.n, "windows": ev.batch_size, "sensor": [640, 480], "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": gbs, "peak": 8000.0, "unit": "GB/s",
-                     "frac": gbs / 8000.0, "traffic": recorded_traffic(dom), "kernel_ms": ms[dom],
-                     "mean_events_per_launch": n_launch},
-        "kernel_ms": ms, "kernel_calls_per_step": calls, "kernel_ms_per_step": tot,
+        "roofline": {"bound": "valu", "kernel": dom, "achieved": achieved / 1e12, "peak": VALU_PEAK / 1e12,
+                     "unit": "Tslot/s", "frac": achieved / VALU_PEAK, "traffic": recorded_traffic(KERNEL_OF[dom]),
+                     "pairs": Kp, "slots_per_pair": slots, "kernel_ms": ms[dom]},
+        "kernel_ms": ms,
+        "pairs_per_anchor": Kp / ev.n,
     }
     if not a.no_cpu:
         line["cpu_baseline"] = trajectories_cpu_baseline(win, a.cpu_budget)
@@ -429,25 +466,44 @@ def trajectories_main(a, dev):
 
 
 def trajectories_cpu_baseline(win, budget):
-    """The same objective on the host's cores (PyTorch CPU ops: the package's CPU path) on a prefix of the
-    first window; forward + backward."""
-    from x_amd.core import EventPacket
-    from x_amd.motion import PixelTrajectories
-    from x_amd.objectives import AnchoredSliced
-    K = win.motion["K"]
-    coeff = torch.tensor(win.motion["coeffs"][:1], requires_grad=True)
+    """Oracle on a prefix of window 0: trajectory starts (fixed point on the fp32 sampler), coefficient rows,
+    the fp32 plan and OpenMP pair loops forward and backward, window counts, exposure, epilogue, the coefficient
+    adjoint; the IWE leg (transport to 0.5, OpenMP splat forward and backward, coefficient adjoint).  The
+    fixed-point inversion's own backward is not included (the oracle has no position gradient of the sampler),
+    so the baseline does less work than the GPU step."""
+    O = _oracle()
+    H, W, K = win.height, win.width, win.motion["K"]
+    coeffs = np.ascontiguousarray(win.motion["coeffs"][:1])
+    rng = np.random.default_rng(0)
+    tab = O.traj_slice_table(K, "bspline", 16)
+    g_ref, _ = O.traj_basis_table(np.array([0.5]), K, "bspline")
 
     def run(n):
-        sub = type(win)(xy=win.xy[:n], t=win.t[:n], p=win.p[:n], b=win.b[:n], height=win.height, width=win.width)
-        ev = EventPacket.from_window(sub, "cpu")
-        obj = AnchoredSliced(n_slices=10, sigma=1.0, tau=0.8, seed=0)
-        coeff.grad = None
-        obj(ev, PixelTrajectories(coeff, K, "bezier"))["loss"].backward()
+        xy, t, b = win.xy[:n], win.t[:n], win.b[:n]
+        xs = (xy + rng.uniform(-0.5, 0.5, xy.shape)).astype(np.float32)
+        xa = (xs + rng.standard_normal(xs.shape)).astype(np.float32)
+        p = O.traj_origin(coeffs, xs, t, b, K, "bspline")
+        rows, idx, wts = O.sample_grid(coeffs, p, b)
+        anchors = np.arange(n)
+        plan = O.build_pair_plan_traj(p, rows, tab, t, b, 1, H, W, anchors, xa, 1.0, TRAJ_TAU, 3.0, 16)
+        S = O.ats_pair_fwd(plan, 1.0, TRAJ_TAU, 3.0)
+        wc = O.window_counts(t, b, anchors, TRAJ_TAU)
+        vis = O.traj_visible_fraction(coeffs, xa, t, b, t, b, 1, H, W, TRAJ_TAU, K, "bspline")
+        _, gS, _ = O.anchored_epilogue(S, wc, 1.0, H, W, vis=vis)
+        _, gc = O.ats_pair_bwd_traj(gS, plan, tab, K, 1.0, TRAJ_TAU, 3.0, n)
+        O.sample_grid_bwd(gc.astype(np.float32), idx, wts, coeffs.shape)
+        q = O.traj_origin(coeffs, xy, t, b, K, "bspline")
+        d, _, qidx, qwts = O.traj_displacement(coeffs, q, np.full(n, 0.5, np.float32), b, K, "bspline")
+        y = q + d
+        w = ((y[:, 0] >= 0) & (y[:, 0] <= W - 1) & (y[:, 1] >= 0) & (y[:, 1] <= H - 1)).astype(np.float32)
+        img = O.splat_bilinear_fwd(y, w, b, 1, H, W)
+        gimg = (2.0 / (H * W - 1)) * (img - img.mean())
+        gpos, _ = O.splat_bilinear_bwd(gimg.astype(np.float32), y, w, b)
+        gout = np.concatenate([g_ref * gpos[:, 1:2], g_ref * gpos[:, 0:1]], 1).astype(np.float32)
+        O.sample_grid_bwd(gout, qidx, qwts, coeffs.shape)
 
     n, dt, _ = _bounded_run(run, int((win.b == 0).sum()), budget)
-    return {"value": n / dt, "unit": "events/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"the same objective with PyTorch CPU ops on the first {n} events of window 0 (time-sorted "
-                      f"prefix, the largest of a doubling series that fits the budget), {dt:.2f} s"}
+    return _baseline_line(O, n, int((win.b == 0).sum()), dt, "the trajectory step (window 0)")
 
 
 def main():
@@ -487,6 +543,7 @@ def main():
     torch.cuda.synchronize()
     kernels = ["atl_fast_pair_fwd", "atl_fast_pair_bwd"]
     rec = _ext.time_kernels(kernels, every=4)      # every bracket delays the next launch: sample the steps
+    first_draw = obj._philox[1]
     t0 = time.perf_counter()
     for _ in range(a.steps):
         step()
@@ -494,15 +551,16 @@ def main():
     dt = time.perf_counter() - t0
     ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec[k]])) for k in kernels}
     _ext.time_kernels(())
-    # contributing pairs K = sum_i n_i of one step (counted outside the timed region)
+    # contributing pairs K = sum_i n_i of the timed steps' own noise draws (counted outside the timed region)
+    pairs = []
     with torch.no_grad():
-        g = torch.Generator(device=dev).manual_seed(1)
-        xs = ev.xy + (torch.rand(ev.xy.shape, generator=g, device=dev) - 0.5)
-        xa = xs + a.sigma * torch.randn(xs.shape, generator=g, device=dev)
-        v = motion.velocity(xs, ev.t, ev.b)
-        plan = F.FastPairPlan(xs, ev.t, v, ev.b, 1, ev.height, ev.width, torch.arange(ev.n, device=dev), a.sigma,
-                              0.2, 3.0, 16, anchor_xy=xa)
-        K = int(plan.counts().sum())
+        for draw in range(first_draw, first_draw + a.steps):
+            xs, xa = F.event_noise(ev.xy, 0, draw, a.sigma)
+            v = motion.velocity(xs, ev.t, ev.b)
+            plan = F.FastPairPlan(xs, ev.t, v, ev.b, 1, ev.height, ev.width, None, a.sigma, 0.2, 3.0, 16,
+                                  anchor_xy=xa)
+            pairs.append(int(plan.counts().sum()))
+    K = float(np.mean(pairs))
     dom = max(kernels, key=lambda k: ms[k])
     fwd = dom.endswith("fwd")
     slots = SLOTS_FWD if fwd else SLOTS_BWD

@@ -102,13 +102,16 @@ int atl_sample_grid_bwd_pos_cl(const float* gout, const float* field_cl, int64_t
                                int64_t img_w, float* gpos, hipStream_t stream);
 /* PixelTrajectories.displacement (atl/motion/trajectories.py:26-37 basis, the coefficient look-up and the sum
  * over k), fused, no counterpart in the reference's extension: out (N,2) written, d = (sum_k c_{K+k} g_k,
- * sum_k c_k g_k) of the channels-last coefficient grid field_cl (B, Hg, Wg, 4*ceil(2K/4), channels
- * [y_1..y_K, x_1..x_K]) sampled at grid coordinates gpos, with g_k(t) = t^k (basis 0) or
- * binom(K,k) t^k (1-t)^(K-k) (basis 1); 1 <= K <= 16.  atl_traj_gout writes the (N, 2K) output gradient per
- * channel, gout[n, k-1] = g_k gd.y and gout[n, K+k-1] = g_k gd.x, which atl_sample_grid_bwd_planned (field)
- * and atl_sample_grid_bwd_pos_cl (positions) take. */
-int atl_traj_displacement(const float* field_cl, int64_t B, int64_t K, int64_t Hg, int64_t Wg, const float* gpos,
-                          const int64_t* b, const float* t, int64_t N, int64_t basis, float* out, hipStream_t stream);
+ * sum_k c_k g_k) of the channels-last coefficient grid field_cl (B, Hg, Wg, 4*ceil(C/4), channels
+ * [y_1..y_K, x_1..x_K], C = 2K: any other C is rejected) sampled at grid coordinates gpos, with
+ * g_k(t) = t^k (basis 0), binom(K,k) t^k (1-t)^(K-k) (basis 1) or N_k(t) (basis 2: the clamped uniform
+ * B-spline of degree min(3, K) with K + 1 functions N_0..N_K on [0, 1], N_0 pinned to the start); 1 <= K <= 16.
+ * atl_traj_gout writes the (N, 2K) output gradient per channel, gout[n, k-1] = g_k gd.y and
+ * gout[n, K+k-1] = g_k gd.x, which atl_sample_grid_bwd_planned (field) and atl_sample_grid_bwd_pos_cl
+ * (positions) take. */
+int atl_traj_displacement(const float* field_cl, int64_t B, int64_t C, int64_t K, int64_t Hg, int64_t Wg,
+                          const float* gpos, const int64_t* b, const float* t, int64_t N, int64_t basis, float* out,
+                          hipStream_t stream);
 int atl_traj_gout(const float* gd, const float* t, int64_t N, int64_t K, int64_t basis, float* gout,
                   hipStream_t stream);
 /* The same adjoint through a tile plan: atl_grid_plan bins the positions by the 16x16 tile of their base
@@ -213,6 +216,22 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
 int atl_fast_pair_fwd(const atl_fast_geometry* geo, const void* ws, float* out, int* count, hipStream_t stream);
 /* gv (N,2) written: each source's gradient, zero for sources outside the plan (no fill needed). */
 int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, float* gv, hipStream_t stream);
+
+/* The same fused pair sums for trajectory motion (the anchored score with PixelTrajectories, which the
+ * reference's exact kernel does not take: atl/objectives/ats.py:77-78 requires motion linear at the event).
+ * No counterpart in the reference's extension; it replaces atl_fast_plan / atl_fast_pair_bwd where each
+ * source's slice-centre position and velocity come from its trajectory instead of x + v (c_s - t):
+ * source j has the trajectory start p[j] (N,2) and coefficients coef[j] (N, 2K, channels [y_1..y_K,
+ * x_1..x_K]); tab (S, 2K) holds the basis at the slice centres, row s = [g_1..g_K(c_s), g_1'..g_K'(c_s)].
+ * Entry (j, s): y = p + sum_k coef_k g_k(c_s), v = sum_k coef_k g_k'(c_s) (fp32, sums in k order); the pairs,
+ * tests and sums are then those of atl_fast_pair_fwd, which evaluates the forward unchanged.
+ * atl_fast_pair_bwd_traj writes, for every source, gp (N,2) = dL/dp and gcoef (N, 2K) = dL/dcoef (zero for
+ * sources outside the plan).  1 <= K <= 12. */
+int atl_fast_plan_traj(const atl_fast_geometry* geo, const float* p, const float* coef, int64_t K, const float* tab,
+                       const float* t, const int64_t* b, const int64_t* anchors, const float* anchor_xy, void* ws,
+                       int64_t ws_bytes, hipStream_t stream);
+int atl_fast_pair_bwd_traj(const atl_fast_geometry* geo, void* ws, const float* gS, const float* coef, int64_t K,
+                           const float* tab, float* gp, float* gcoef, hipStream_t stream);
 
 /* ---------------------------------------------------------------- anchored-score pieces */
 

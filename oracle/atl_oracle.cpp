@@ -245,6 +245,43 @@ void oracle_ats_pair_bwd(const float* G, const float* SY, const float* SV, const
   }
 }
 
+// Backward of the trajectory pair sums (no reference implementation; the definition's gradient in the loop form
+// of csrc/atl_cpu.cpp:224-253): per visited pair (anchor i, entry k of source j in slice s), dL/dy = g k r / h^2
+// and dL/dv = g k r at / h^2 (at = t_i - c_s), chained through y = p + sum_c coef_c tab[s][c] and
+// v = sum_c coef_c tab[s][K + c] into GP (N,2) and GC (N, 2K, channels [y_1..y_K, x_1..x_K]); float64
+// accumulators, zero-filled by the caller.
+void oracle_ats_pair_bwd_traj(const float* G, const float* SY, const float* SV, const float* ST, const int64_t* SID,
+                              const int64_t* CS, const float* AX, const float* AT, const int64_t* AC,
+                              const int64_t* AID, const float* SC, int64_t M, int64_t S, int64_t GH, int64_t GW,
+                              double h, double tau, double cut, const float* TAB, int64_t K, double* GP,
+                              double* GC) {
+  const PairView p{SY, SV, ST, AX, AT, SC, SID, CS, AC, AID, S, GH, GW, (float)h, (float)tau, (float)cut};
+  const double invh2 = 1.0 / (h * h);
+#pragma omp parallel for schedule(dynamic, 64)
+  for (int64_t i = 0; i < M; ++i) {
+    const double gi = G[i];
+    if (gi == 0.0) continue;
+    const int64_t s = AC[3 * i] % S;
+    const double at = (double)(AT[i] - SC[s]);
+    const float* row = TAB + s * 2 * K;
+    pairs_of(i, p, [&](int64_t k, float rx, float ry, float, float kern) {
+      const double f = gi * kern * invh2;
+      const int64_t j = SID[k];
+#pragma omp atomic
+      GP[2 * j] += f * rx;
+#pragma omp atomic
+      GP[2 * j + 1] += f * ry;
+      for (int64_t c = 0; c < K; ++c) {
+        const double wy = row[c] + at * row[K + c];
+#pragma omp atomic
+        GC[j * 2 * K + c] += f * ry * wy;
+#pragma omp atomic
+        GC[j * 2 * K + K + c] += f * rx * wy;
+      }
+    });
+  }
+}
+
 // csrc/atl_cpu.cpp:256-286
 void oracle_voxel_grid(const float* P, const float* T, const float* Pol, const int64_t* Bi, int64_t N, int64_t C,
                        int64_t H, int64_t W, float* V) {

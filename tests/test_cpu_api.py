@@ -3,6 +3,7 @@ oracle; device tensors never take this path."""
 import math
 
 import numpy as np
+import pytest
 import torch
 
 import oracle as O
@@ -44,32 +45,60 @@ def test_reference_module_is_differentiable():
     assert p.grad is not None and torch.isfinite(p.grad).all()
 
 
-def test_sliced_score_all_slices_matches_slice_loop():
-    """The sliced score computed over every slice at once equals the reference's slice-by-slice loop (the loop
-    path is taken with an anchor cap no slice reaches): same anchors in the same order, same scores, same
-    coefficient gradient; with a random subset of slices and anchor and source masks."""
+def test_cpu_trajectory_pair_sums_match_oracle():
+    """The CPU (pure torch) trajectory pair sums against the oracle's float64 brute force: values and the
+    gradients to the starts and the coefficient rows."""
+    rng = np.random.default_rng(4)
+    pos, _, b, t = rand_events(n=500, seed=6)
+    K = 4
+    coef = (rng.standard_normal((500, 2 * K)) * 2).astype(F32)
+    p = (pos - rng.uniform(-1, 1, pos.shape)).astype(F32)
+    anchors = np.arange(0, 500, 2)
+    xa = (pos[anchors] + rng.standard_normal((250, 2)) * 0.5).astype(F32)
+    tab = O.traj_slice_table(K, "bspline", 16)
+    tp, tc = torch.from_numpy(p).requires_grad_(True), torch.from_numpy(coef).requires_grad_(True)
+    S = F.ats_pair_sums_traj(tp, tc, torch.from_numpy(t), torch.from_numpy(b), 2, 20, 24, torch.from_numpy(anchors),
+                             1.2, 0.3, 3.0, 16, anchor_xy=torch.from_numpy(xa), K=K, table=torch.from_numpy(tab))
+    S64, _, grad = O.traj_pair_sums_fp64(p, coef, t, b, anchors, xa, 1.2, 0.3, 3.0, 16, K, "bspline")
+    assert np.allclose(S.detach().numpy(), S64, rtol=1e-5, atol=1e-5)
+    gS = rng.standard_normal(250).astype(F32)
+    S.backward(torch.from_numpy(gS))
+    gp, gc = grad(gS)
+    assert np.allclose(tp.grad.numpy(), gp, rtol=1e-3, atol=1e-4 * np.abs(gp).max())
+    assert np.allclose(tc.grad.numpy(), gc, rtol=1e-3, atol=1e-4 * np.abs(gc).max())
+
+
+def test_cpu_anchored_trajectories_straight_equals_exact():
+    """On CPU tensors: straight B-spline trajectories (control points v xi_k) score as AnchoredExact with the
+    translation v (same noise)."""
     from x_amd import synth
     from x_amd.core import EventPacket
-    from x_amd.motion import PixelTrajectories
-    from x_amd.objectives import AnchoredSliced
-    win = synth.small_window(seed=5, n=1500, B=2)
-    rng = np.random.default_rng(5)
-    coeffs = synth.trajectory_coeffs(rng, 2, 3, win.height, win.width, sigma_px=8.0, dmax=3.0)
+    from x_amd.motion import PixelTrajectories, Translation
+    from x_amd.motion.trajectories import greville
+    from x_amd.objectives import AnchoredExact, AnchoredTrajectories
+    win = synth.small_window(seed=5, n=1200, B=1)
     ev = EventPacket.from_window(win, "cpu")
-    g = torch.Generator().manual_seed(1)
-    amask = torch.rand(ev.n, generator=g) < 0.7
-    smask = torch.rand(ev.n, generator=g) < 0.8
-    for smooth, sps, masks in ((True, None, False), (False, 3, True), (True, 4, True)):
-        res = []
-        for nap in (None, 10 ** 9):
-            c = torch.tensor(coeffs, requires_grad=True)
-            obj = AnchoredSliced(n_slices=6, slices_per_step=sps, sigma=1.0, tau=0.3, seed=0, smooth_anchors=smooth,
-                                 n_anchors_per_slice=nap)
-            ls, ai = obj.log_scores(ev, PixelTrajectories(c, 3, "bezier"), anchor_mask=amask if masks else None,
-                                    source_mask=smask if masks else None)
-            ls.sum().backward()
-            res.append((ls.detach().numpy(), ai.numpy(), c.grad.numpy()))
-        (l0, a0, g0), (l1, a1, g1) = res
-        assert np.array_equal(a0, a1) and len(a0) > 0
-        assert np.allclose(l0, l1, rtol=1e-6, atol=1e-6)
-        assert np.allclose(g0, g1, rtol=1e-5, atol=1e-5 * np.abs(g1).max())
+    K, v = 6, (-1.5, 2.0)
+    xi = torch.tensor(greville(K), dtype=torch.float32)
+    c = torch.cat([v[1] * xi, v[0] * xi]).view(1, 2 * K, 1, 1).expand(1, 2 * K, win.height, win.width).contiguous()
+    ls_t, _ = AnchoredTrajectories(h=1.0, tau=0.3, n_anchors=None, seed=0).log_scores(
+        ev, PixelTrajectories(c, K, "bspline", tile=1))
+    ls_e, _ = AnchoredExact(h=1.0, tau=0.3, n_anchors=None, seed=0).log_scores(
+        ev, Translation(1, win.height, win.width, init=torch.tensor([v])))
+    assert np.allclose(ls_t.detach().numpy(), ls_e.detach().numpy(), rtol=1e-5, atol=1e-5)
+
+
+def test_cpu_objectives_refuse_the_wrong_motion():
+    from x_amd import synth
+    from x_amd.core import EventPacket
+    from x_amd.motion import PixelTrajectories, Translation
+    from x_amd.objectives import AnchoredExact, AnchoredTrajectories
+    win = synth.small_window(seed=5, n=300, B=1)
+    ev = EventPacket.from_window(win, "cpu")
+    traj = PixelTrajectories(torch.zeros(1, 6, win.height, win.width), 3, "bspline")
+    with pytest.raises(ValueError):
+        AnchoredExact(n_anchors=None)(ev, traj)
+    with pytest.raises(ValueError):
+        AnchoredTrajectories(n_anchors=None)(ev, Translation(1, win.height, win.width))
+    with pytest.raises(ValueError):
+        AnchoredExact(rng="gpu")

@@ -403,6 +403,43 @@ def test_anchored_exact_fused_loss():
     close_rel(N(m.grid.grad), O.sample_grid_bwd(gv, idx, wts, grid.shape), 1e-4)
 
 
+def test_anchored_exact_device_rng_full_size():
+    """The benchmarked step end to end: AnchoredExact(rng="device") on the 1M-event 640x480 dense-flow window
+    (h = 1, tau = 0.2, cut = 3, 16 slices, every event an anchor), whose noise is the fused Philox draw.  The
+    oracle gets the same draw (event_noise with the objective's seed and first offset) and runs the whole
+    pipeline: log scores within 1e-5, the fused loss within 1e-5 and the flow-grid gradient within 1e-4."""
+    from x_amd.core import EventPacket
+    from x_amd.motion import DenseLinearFlow
+    from x_amd.objectives import AnchoredExact
+    print("anchored exact rng=device, 1M events", flush=True)
+    win = synth.dense_flow_window(seed=0)
+    H, W, n = win.height, win.width, win.n
+    ev = EventPacket.from_window(win, DEV)
+    grid = win.motion["grid"]
+    xs_d, xa_d = F.event_noise(ev.xy, 0, 0, 1.0)                 # the draw of the objective's first call
+    xs, xa = N(xs_d), N(xa_d)
+    v, idx, wts = O.dense_velocity(grid, xs, win.b, H, W)
+    p = O.build_pair_plan(xs, win.t, v, win.b, 1, H, W, np.arange(n), 1.0, 0.2, 3.0, 16, anchor_xy=xa)
+    Sv = O.ats_pair_fwd(p, 1.0, 0.2, 3.0)
+    wc = O.window_counts(win.t, win.b, np.arange(n), 0.2)
+    vis = O.visible_fraction_dense(grid, xa, win.t, win.b, win.t, win.b, 1, H, W, 0.2)
+    want, gS, _ = O.anchored_epilogue(Sv, wc, 1.0, H, W, vis=vis)
+    ggrid = O.sample_grid_bwd(O.ats_pair_bwd(gS, p, 1.0, 0.2, 3.0, n), idx, wts, grid.shape)
+    for form in ("log_scores", "loss"):
+        m = DenseLinearFlow(1, H, W, grid=grid.shape[-2:], init=torch.as_tensor(grid)).to(DEV)
+        obj = AnchoredExact(h=1.0, tau=0.2, cut=3.0, n_slices=16, n_anchors=None, seed=0, rng="device")
+        if form == "log_scores":
+            ls, _ = obj.log_scores(ev, m)
+            close_rel(N(ls), want, 1e-5)
+            (-ls.mean()).backward()
+        else:
+            out = obj(ev, m)
+            loss = -float(np.mean(want.astype(np.float64)))
+            assert abs(float(out["loss"]) - loss) <= 1e-5 * abs(loss)
+            out["loss"].backward()
+        close_rel(N(m.grid.grad), ggrid, 1e-4)
+
+
 def test_window_counts_and_pair_sums_without_index():
     """anchors=None (every event, in order) gives the same window counts and pair sums as anchors=arange(N)
     (the sums to the last bits only: the order of the records within a cell, and so the summation order, is set
@@ -452,3 +489,38 @@ def test_full_size_splat_gather_properties():
     assert abs(lhs - rhs) < 1e-4 * (abs(lhs) + float(inside.sum()))
     _, gw = F.get_ext().splat_bilinear_bwd(G.contiguous(), pos.contiguous(), inside.contiguous(), b)
     assert torch.equal(gw, val)
+
+
+@pytest.mark.parametrize("kernel,sigma,polarity,mask,dt", [("bilinear", 0.0, "pooled", True, False),
+                                                          ("bilinear", 1.0, "split", True, True),
+                                                          ("bilinear", 2.5, "pooled", False, True),
+                                                          ("gauss", 1.0, "split", False, False),
+                                                          ("gauss", 0.7, "pooled", True, True)])
+def test_make_iwe_matches_oracle(kernel, sigma, polarity, mask, dt):
+    """make_iwe on the device (weights, border mask, time weighting, polarity split, splat, blur) against the
+    oracle's IWE (atl/objectives/base.py:40-60): within 1e-5 of the largest pixel."""
+    from x_amd.core import EventPacket
+    from x_amd.objectives import IWEConfig, make_iwe
+    print(f"make_iwe {kernel} sigma={sigma} {polarity} mask={mask} dt={dt}", flush=True)
+    win = synth.small_window(seed=17, n=5000, B=2)
+    rng = np.random.default_rng(17)
+    xy_ref = (win.xy + rng.normal(0, 2, win.xy.shape)).astype(F32)          # some outside the sensor
+    ev = EventPacket.from_window(win, DEV)
+    cfg = IWEConfig(kernel=kernel, sigma=sigma, polarity=polarity, mask_border=mask, scale_by_dt=dt)
+    got = N(make_iwe(ev, T(xy_ref), 0.3, cfg))
+    want = O.make_iwe(xy_ref, win.t, win.p, win.b, 2, win.height, win.width, 0.3, kernel, sigma, polarity, mask, dt)
+    assert got.shape == want.shape
+    close_rel(got, want, 1e-5)
+
+
+def test_blur_matches_oracle_and_keeps_interior_mass():
+    """blur (two 1-D passes) against the oracle's scipy correlate1d blur, (B, H, W) and (B, C, H, W); an image
+    whose support stays 3 sigma from the border keeps its mass."""
+    rng = np.random.default_rng(18)
+    for shape, sigma in (((2, 40, 52), 1.0), ((2, 3, 30, 31), 1.7)):
+        img = rng.standard_normal(shape).astype(F32)
+        close_rel(N(F.blur(T(img), sigma)), O.blur(img, sigma), 1e-5)
+    img = np.zeros((1, 40, 40), F32)
+    img[0, 10:30, 12:28] = rng.random((20, 16))
+    out = N(F.blur(T(img), 2.0))
+    assert abs(float(out.sum()) - float(img.sum())) <= 1e-5 * float(img.sum())

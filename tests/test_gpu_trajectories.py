@@ -1,26 +1,34 @@
-"""Pixel trajectories and the sliced anchored score on the HIP path (the continuous-time workload).
+"""Pixel trajectories and the anchored score for trajectories on the HIP path (the continuous-time workload:
+per-pixel cubic B-spline trajectories with 10 control points, 4 windows x 500k events).
 
-The trajectory model and the sliced score are host compositions (torch) of the fused displacement kernel, the
-HIP flow sampler (forward, field adjoint through the tile plan, position gradient), the Gaussian splat and the
-bilinear gather.  They run here on the device against the same composition on CPU tensors, where every op is
-plain PyTorch (x_amd/ops/reference.py); the fused displacement is also pinned to float64 here, the other
-kernels to the oracle in test_gpu_ops.py.  Bars: values
-within 1e-5 relative, gradients within 1e-4 relative to the largest magnitude."""
-import math
-
+* the fused displacement (polynomial, Bernstein and B-spline bases) against float64 (basis from scipy's BSpline
+  in the oracle) and the flow sampler's adjoints;
+* the trajectory pair sums (atl_fast_plan_traj, atl_fast_pair_fwd, atl_fast_pair_bwd_traj) against the oracle:
+  per-anchor neighbour counts bit-exact with the oracle's fp32 plan and pair loops, sums within 1e-5, gradients
+  to the starts and coefficients within 1e-4 of the float64 brute force (small) or the oracle's pair loops
+  (full size);
+* AnchoredTrajectories end to end against the same chain on CPU tensors, and straight trajectories against
+  AnchoredExact.
+Bars: values within 1e-5 relative, gradients within 1e-4 relative to the largest magnitude."""
 import numpy as np
 import pytest
 import torch
 
 import oracle as O
+from tests.conftest import rand_events
 from x_amd import synth
 from x_amd.core import EventPacket
 from x_amd.motion import PixelTrajectories, sample_grid
-from x_amd.objectives import AnchoredSliced
+from x_amd.objectives import AnchoredExact, AnchoredTrajectories
+from x_amd.ops import functional as F
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 F32 = np.float32
+
+
+def T(a):
+    return torch.as_tensor(np.ascontiguousarray(a), device=DEV)
 
 
 def N(t):
@@ -67,7 +75,8 @@ def test_sample_grid_position_and_field_gradients(C, scale):
 
 
 @pytest.mark.parametrize("K,kind", [(1, "polynomial"), (2, "bezier"), (7, "bezier"), (10, "bezier"),
-                                    (16, "polynomial")])
+                                    (16, "polynomial"), (1, "bspline"), (3, "bspline"), (10, "bspline"),
+                                    (16, "bspline")])
 def test_traj_displacement_matches_fp64_and_torch_gradients(K, kind):
     """The fused displacement against the oracle's exact coefficient samples times the basis in float64; its
     field gradient against the float64 adjoint, its position gradient against the CPU torch composition (sample
@@ -87,12 +96,7 @@ def test_traj_displacement_matches_fp64_and_torch_gradients(K, kind):
     tp = torch.tensor(gpos, device=DEV, requires_grad=True)
     d = F.traj_displacement(tf, tp, torch.tensor(b, device=DEV), torch.tensor(t, device=DEV), K, kind)
     coef, idx, wts = O.sample_grid(fld, gpos[ok], b[ok])
-    tt = t[ok].astype(np.float64)[:, None]
-    k = np.arange(1, K + 1)
-    if kind == "bezier":
-        g = np.array([math.comb(K, j) for j in k], np.float64) * tt ** k * (1 - tt) ** (K - k)
-    else:
-        g = tt ** k
+    g, _ = O.traj_basis_table(t[ok].astype(np.float64), K, kind)     # float64, scipy's BSpline for the spline
     c64 = coef.astype(np.float64)
     want = np.stack([(c64[:, K:] * g).sum(1), (c64[:, :K] * g).sum(1)], 1)
     got = N(d)
@@ -129,12 +133,34 @@ def test_traj_displacement_empty_and_rejected_inputs():
         F.traj_displacement(tf, tp, tb, tt, 4, "spline")
     with pytest.raises(ValueError):
         F.traj_displacement(tf, tp, tb, tt.clone().requires_grad_(True), 4, "bezier")
+    # shapes the kernel would read past: all refused on the host before any launch
+    p5 = torch.zeros(5, 2, device=DEV)
+    b5 = torch.zeros(5, dtype=torch.long, device=DEV)
+    t5 = torch.zeros(5, device=DEV)
+    for args in ((tf, p5, b5, t5, 3), (tf, p5, b5, t5, 5),                     # C != 2K
+                 (tf, torch.zeros(5, 3, device=DEV), b5, t5, 4),                # positions not (N, 2)
+                 (tf, p5, b5[:4], t5, 4), (tf, p5, b5, t5[:3], 4),              # short b, short t
+                 (tf[0], p5, b5, t5, 4), (tf, p5, b5, t5, 17)):                 # not 4-D, K > 16
+        with pytest.raises(ValueError):
+            F.traj_displacement(*args, "bspline")
+    with pytest.raises(ValueError):
+        F.sample_grid_hip(tf, torch.zeros(5, 3, device=DEV), b5)
+    with pytest.raises(ValueError):
+        F.sample_grid_hip(tf, p5, b5[:2])
+    # the C entry point itself rejects a channel count that is not 2K
+    from x_amd.ops import _ext
+    fcl = torch.zeros(2, 9, 11, 8, device=DEV)
+    rc = _ext.load_library().atl_traj_displacement(_ext.ptr(fcl), 2, 6, 4, 9, 11, _ext.ptr(p5), _ext.ptr(b5),
+                                                     _ext.ptr(t5), 5, 2, _ext.ptr(p5), None)
+    assert rc == 1 and b"expected 2K" in _ext.load_library().atl_last_error()
 
 
-@pytest.mark.parametrize("K,kind", [(1, "polynomial"), (3, "bezier"), (4, "polynomial"), (10, "bezier")])
-def test_pixel_trajectories_device_matches_cpu(K, kind):
+@pytest.mark.parametrize("K,kind,tile", [(1, "polynomial", 4), (3, "bezier", 4), (4, "polynomial", 4),
+                                         (10, "bezier", 4), (3, "bspline", 1), (10, "bspline", 1),
+                                         (10, "bspline", 4)])
+def test_pixel_trajectories_device_matches_cpu(K, kind, tile):
     """Transport (fixed-point origin + displacement) values and coefficient gradients, device vs CPU."""
-    print(f"trajectories K={K} {kind}", flush=True)
+    print(f"trajectories K={K} {kind} tile={tile}", flush=True)
     win = synth.small_window(seed=K, n=3000, B=2)
     rng = np.random.default_rng(K)
     coeffs = synth.trajectory_coeffs(rng, 2, K, win.height, win.width, sigma_px=8.0, dmax=3.0)
@@ -143,7 +169,7 @@ def test_pixel_trajectories_device_matches_cpu(K, kind):
     for dev in ("cpu", DEV):
         ev = EventPacket.from_window(win, dev)
         c = torch.tensor(coeffs, device=dev, requires_grad=True)
-        m = PixelTrajectories(c, K, kind)
+        m = PixelTrajectories(c, K, kind, tile=tile)
         y = m.transport(ev.xy, ev.t, 0.7, ev.b)
         (y * torch.tensor(w, device=dev)).sum().backward()
         res[dev] = (N(y), N(c.grad))
@@ -166,22 +192,169 @@ def test_pixel_trajectories_linear_closed_form():
     assert np.allclose(N(m.velocity(ev.xy, ev.t, ev.b)), np.array([[-2.25, 1.5]], F32))
 
 
-@pytest.mark.parametrize("smooth", [True, False])
-def test_anchored_sliced_device_matches_cpu(smooth):
-    """The sliced anchored score (Gaussian splats, gathers, finite-difference log-det, leave-one-out terms,
-    exposure correction) on degree-3 Bezier trajectories: loss and coefficient gradient, device vs CPU, with the
-    same CPU-generated noise."""
-    print(f"anchored sliced smooth={smooth}", flush=True)
-    win = synth.small_window(seed=9, n=4000, B=2)
-    rng = np.random.default_rng(9)
-    coeffs = synth.trajectory_coeffs(rng, 2, 3, win.height, win.width, sigma_px=8.0, dmax=3.0)
+def test_pixel_trajectories_straight_bspline_closed_form():
+    """Cubic B-spline control points c_k = v xi_k at the Greville abscissae are the straight trajectory p + v t:
+    transport(x, t, t') = x + v (t' - t) (linear precision of the basis)."""
+    from x_amd.motion.trajectories import greville
+    win = synth.small_window(seed=4, n=2000, B=1)
+    ev = EventPacket.from_window(win, DEV)
+    K = 10
+    xi = torch.tensor(greville(K), dtype=torch.float32, device=DEV)
+    v = (1.75, -3.5)                                       # (x, y) px per window
+    c = torch.cat([v[1] * xi, v[0] * xi]).view(1, 2 * K, 1, 1).expand(1, 2 * K, win.height, win.width)
+    m = PixelTrajectories(c.contiguous(), K, "bspline", tile=1)
+    y = N(m.transport(ev.xy, ev.t, 0.6, ev.b))
+    want = win.xy + np.array(v, F32) * (F32(0.6) - win.t)[:, None]
+    assert np.allclose(y, want, atol=2e-5)
+
+
+def _traj_case(seed, n, B, H, W, K, kind, h, tau, S):
+    """Events of a small window, trajectory starts p near the events, smooth coefficient rows, smoothed anchors,
+    the slice table (oracle: scipy's BSpline)."""
+    win = synth.small_window(seed=seed, n=n // B, H=H, W=W, B=B)
+    rng = np.random.default_rng(seed + 50)
+    xs = (win.xy + rng.uniform(-0.5, 0.5, win.xy.shape)).astype(F32)
+    fld = synth.trajectory_coeffs(rng, B, K, H, W, sigma_px=6.0, dmax=4.0)
+    coef, _, _ = O.sample_grid(fld, xs, win.b)
+    p = (xs - rng.uniform(-1, 1, xs.shape)).astype(F32)
+    xa = (xs + h * rng.standard_normal(xs.shape)).astype(F32)
+    return win, p, coef.astype(F32), xa, O.traj_slice_table(K, kind, S)
+
+
+def check_traj_against_oracle(p, coef, tab, t, b, B, H, W, anchors, xa, h, tau, S, K, kind, fp64=True,
+                              index_free=False):
+    """Device trajectory pair sums vs the oracle: counts bit-exact with the fp32 plan and pair loops, sums within
+    1e-5 of them, gradients within 1e-4 of the float64 brute force (or, without fp64, of the pair loops)."""
+    print(f"traj pair case N={len(t)} M={len(anchors)} K={K} {kind} h={h} tau={tau} S={S}", flush=True)
+    plan_o = O.build_pair_plan_traj(p, coef, tab, t, b, B, H, W, anchors, xa, h, tau, 3.0, S)
+    want, wcnt = O.ats_pair_fwd(plan_o, h, tau, 3.0, with_counts=True)
+    plan = F.FastPairPlan(T(p), T(t), None, T(b), B, H, W, None if index_free else T(anchors), h, tau, 3.0, S, T(xa),
+                          traj=(T(coef), K, T(tab)))
+    assert np.array_equal(N(plan.counts()), wcnt)
+    assert np.allclose(N(plan.forward()), want, rtol=1e-5, atol=1e-6 * max(1.0, float(np.abs(want).max(initial=0))))
+    gS = np.random.default_rng(7).standard_normal(len(anchors)).astype(F32)
+    gp, gc = plan.backward_traj(T(gS))
+    if fp64:
+        S64, c64, grad = O.traj_pair_sums_fp64(p, coef, t, b, anchors, xa, h, tau, 3.0, S, K, kind)
+        close_rel(N(plan.forward()), S64, 1e-5)
+        wp, wc = grad(gS)
+    else:
+        wp, wc = O.ats_pair_bwd_traj(gS, plan_o, tab, K, h, tau, 3.0, len(t))
+    close_rel(N(gp), wp, 1e-4)
+    close_rel(N(gc), wc, 1e-4)
+    return wcnt
+
+
+@pytest.mark.parametrize("K,kind,tau,S,h", [(10, "bspline", 0.8, 16, 1.0), (3, "bspline", 0.2, 16, 1.0),
+                                            (1, "bspline", 0.3, 8, 1.5), (4, "bezier", 0.5, 16, 0.5),
+                                            (2, "polynomial", 1.0, 4, 1.0)])
+def test_traj_pair_sums_match_oracle(K, kind, tau, S, h):
+    win, p, coef, xa, tab = _traj_case(21 + K, 4000, 2, 40, 48, K, kind, h, tau, S)
+    cnt = check_traj_against_oracle(p, coef, tab, win.t, win.b, 2, 40, 48, np.arange(win.n), xa, h, tau, S, K, kind)
+    assert cnt.sum() > win.n
+
+
+def test_traj_pair_sums_anchor_subsets_duplicates_and_edges():
+    """Unsorted anchor subsets, an event listed twice among the anchors (leave-one-out by id), starts far
+    outside the sensor (clamped bins), and no events at all."""
+    K, kind = 10, "bspline"
+    win, p, coef, xa, tab = _traj_case(31, 3000, 2, 40, 48, K, kind, 1.0, 0.4, 16)
+    rng = np.random.default_rng(3)
+    sub = rng.permutation(win.n)[: win.n // 3]
+    check_traj_against_oracle(p, coef, tab, win.t, win.b, 2, 40, 48, sub, xa[sub], 1.0, 0.4, 16, K, kind)
+    dup = np.concatenate([np.arange(0, win.n, 2), np.arange(0, win.n, 6)])
+    check_traj_against_oracle(p, coef, tab, win.t, win.b, 2, 40, 48, dup, xa[dup], 1.0, 0.4, 16, K, kind)
+    p2 = p.copy()
+    p2[::9] += F32(200.0)
+    check_traj_against_oracle(p2, coef, tab, win.t, win.b, 2, 40, 48, np.arange(win.n), xa, 1.0, 0.4, 16, K, kind,
+                              index_free=True)
+    z2, z1 = torch.zeros(0, 2, device=DEV), torch.zeros(0, device=DEV)
+    zb = torch.zeros(0, dtype=torch.long, device=DEV)
+    plan = F.FastPairPlan(z2, z1, None, zb, 1, 40, 48, None, 1.0, 0.4, 3.0, 16, z2,
+                          traj=(torch.zeros(0, 2 * K, device=DEV), K, T(tab)))
+    gp, gc = plan.backward_traj(z1)
+    assert plan.forward().shape == (0,) and gp.shape == (0, 2) and gc.shape == (0, 2 * K)
+
+
+def test_traj_pair_sums_straight_trajectories_are_the_linear_sums():
+    """Straight trajectories (starts p = x - v t, control points v xi_k) give the reference's linear pair sums:
+    device values within 1e-5 and the velocity gradient recovered from the start and coefficient gradients,
+    -t gp + sum_k xi_k gcoef_k, within 1e-4 of the reference's dS/dv (float64 brute force)."""
+    from x_amd.motion.trajectories import greville
+    pos, _, b, t = rand_events(n=800, seed=9)
+    rng = np.random.default_rng(2)
+    v = (rng.standard_normal((800, 2)) * 5).astype(F32)
+    K = 10
+    xi = greville(K)
+    p = (pos - v * t[:, None]).astype(F32)
+    coef = np.concatenate([v[:, 1:2] * xi, v[:, 0:1] * xi], 1).astype(F32)
+    tab = O.traj_slice_table(K, "bspline", 16)
+    anchors = np.arange(0, 800, 2)
+    xa = (pos[anchors] + rng.standard_normal((400, 2)) * 0.5).astype(F32)
+    plan = F.FastPairPlan(T(p), T(t), None, T(b), 2, 20, 24, T(anchors), 1.5, 0.3, 3.0, 16, T(xa),
+                          traj=(T(coef), K, T(tab)))
+    Sl, _, grad = O.pair_sums_fp64(pos, t, v, b, anchors, 1.5, 0.3, 3.0, anchor_xy=xa)
+    close_rel(N(plan.forward()), Sl, 1e-5)
+    gS = rng.standard_normal(400).astype(F32)
+    gp, gc = (N(a).astype(np.float64) for a in plan.backward_traj(T(gS)))
+    gv = -t[:, None] * gp + np.stack([(gc[:, K:] * xi).sum(1), (gc[:, :K] * xi).sum(1)], 1)
+    close_rel(gv, grad(gS), 1e-4)
+
+
+def test_traj_pair_sums_full_size():
+    """The continuous-time workload at full size: 4 windows x 500k events at 640x480 on per-pixel cubic B-spline
+    trajectories (10 control points), starts and coefficients from the model on the device, tau = 0.8, h = 1, 16
+    slices, every event an anchor: counts bit-exact with the oracle's fp32 plan and pair loops, sums within
+    1e-5, start and coefficient gradients within 1e-4 of the oracle's pair loops."""
+    print("traj pair sums full size 4 x 500k", flush=True)
+    win = synth.bspline_windows(seed=0)
+    K = win.motion["K"]
+    ev = EventPacket.from_window(win, DEV)
+    m = PixelTrajectories(torch.as_tensor(win.motion["coeffs"], device=DEV), K, "bspline", tile=1)
+    xs_d, xa_d = F.event_noise(ev.xy, 0, 0, 1.0)
+    with torch.no_grad():
+        p_d = m.origin(xs_d, ev.t, ev.b)
+        coef_d = m.coeff_rows(p_d, ev.b)
+    tab = O.traj_slice_table(K, "bspline", 16)
+    assert np.array_equal(N(m.slice_tables(16, DEV)), tab)
+    cnt = check_traj_against_oracle(N(p_d), N(coef_d), tab, win.t, win.b, 4, 480, 640, np.arange(win.n), N(xa_d),
+                                    1.0, 0.8, 16, K, "bspline", fp64=False, index_free=True)
+    assert cnt.sum() > 20 * win.n
+
+
+def test_anchored_trajectories_device_matches_cpu():
+    """AnchoredTrajectories (B-spline, K = 10, per-pixel) end to end: log scores and coefficient gradient, device
+    vs the same chain on CPU tensors (CPU-generated noise on both)."""
+    print("anchored trajectories device vs cpu", flush=True)
+    win = synth.small_window(seed=12, n=2500, B=2)
+    rng = np.random.default_rng(12)
+    K = 10
+    coeffs = synth.trajectory_coeffs(rng, 2, K, win.height, win.width, sigma_px=8.0, dmax=3.0)
     res = {}
     for dev in ("cpu", DEV):
         ev = EventPacket.from_window(win, dev)
         c = torch.tensor(coeffs, device=dev, requires_grad=True)
-        obj = AnchoredSliced(n_slices=6, sigma=1.0, tau=0.3, seed=0, smooth_anchors=smooth)
-        out = obj(ev, PixelTrajectories(c, 3, "bezier"))
-        out["loss"].backward()
-        res[dev] = (float(out["loss"].detach()), N(c.grad))
-    assert abs(res[DEV][0] - res["cpu"][0]) <= 1e-5 * abs(res["cpu"][0])
+        obj = AnchoredTrajectories(h=1.0, tau=0.5, n_anchors=None, seed=0)
+        ls, _ = obj.log_scores(ev, PixelTrajectories(c, K, "bspline", tile=1))
+        (-ls.mean()).backward()
+        res[dev] = (N(ls), N(c.grad))
+    close_rel(res[DEV][0], res["cpu"][0], 1e-5)
     close_rel(res[DEV][1], res["cpu"][1], 1e-4)
+
+
+def test_anchored_trajectories_straight_equals_exact():
+    """Constant straight B-spline trajectories (control points v xi_k everywhere) and the translation v: the
+    trajectory score equals AnchoredExact's (same noise), log scores within 1e-5."""
+    from x_amd.motion import Translation
+    from x_amd.motion.trajectories import greville
+    win = synth.small_window(seed=13, n=3000, B=1)
+    ev = EventPacket.from_window(win, DEV)
+    K = 10
+    v = (2.5, -1.25)
+    xi = torch.tensor(greville(K), dtype=torch.float32, device=DEV)
+    c = torch.cat([v[1] * xi, v[0] * xi]).view(1, 2 * K, 1, 1).expand(1, 2 * K, win.height, win.width).contiguous()
+    ls_t, _ = AnchoredTrajectories(h=1.0, tau=0.3, n_anchors=None, seed=0).log_scores(
+        ev, PixelTrajectories(c, K, "bspline", tile=1))
+    mt = Translation(1, win.height, win.width, init=torch.tensor([v])).to(DEV)
+    ls_e, _ = AnchoredExact(h=1.0, tau=0.3, n_anchors=None, seed=0).log_scores(ev, mt)
+    close_rel(N(ls_t), N(ls_e), 1e-5)

@@ -325,3 +325,166 @@ def test_anchored_epilogue_closed_form():
     qd = 1e-2 / (48 * 64) + S / Dd
     assert np.allclose(ls, np.log(qd), rtol=1e-6, atol=1e-6)
     assert np.allclose(gS, -1.0 / 100 / qd / Dd, rtol=1e-5)
+
+
+def test_dense_grid_pos_aligns_the_corners():
+    """DenseLinearFlow's pixel -> grid map (atl/motion/parametric.py:214-215) with Hg != H, Wg != W: pixel 0 lands
+    on node 0 and pixel W-1 (H-1) on node Wg-1 (Hg-1), so a field linear in the node index is sampled as the same
+    linear function of the pixel, scaled by (Wg-1)/(W-1)."""
+    H, W, Hg, Wg = 48, 64, 7, 11
+    corners = np.array([[0, 0], [W - 1, 0], [0, H - 1], [W - 1, H - 1]], F32)
+    g = O.dense_grid_pos(corners, H, W, Hg, Wg)
+    assert np.array_equal(g, np.array([[0, 0], [Wg - 1, 0], [0, Hg - 1], [Wg - 1, Hg - 1]], F32))
+    yy, xx = np.meshgrid(np.arange(Hg), np.arange(Wg), indexing="ij")
+    grid = np.stack([0.5 * xx + 2.0, -0.25 * yy + 1.0])[None].astype(F32)
+    rng = np.random.default_rng(15)
+    xy = np.stack([rng.uniform(0, W - 1, 300), rng.uniform(0, H - 1, 300)], 1).astype(F32)
+    v, _, _ = O.dense_velocity(grid, xy, np.zeros(300, np.int64), H, W)
+    want = np.stack([0.5 * xy[:, 0] * (Wg - 1) / (W - 1) + 2.0, -0.25 * xy[:, 1] * (Hg - 1) / (H - 1) + 1.0], 1)
+    assert np.allclose(v, want, atol=1e-5)
+
+
+# ------------------------------------------------------------------------------------------- trajectories
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 10, 12])
+def test_traj_basis_bspline_identities(K):
+    """The B-spline table (scipy's BSpline): with N_0 = 1 - sum_k g_k, the K + 1 functions are a partition of
+    unity, non-negative, reproduce t at the Greville abscissae (linear precision), vanish at t = 0 for k >= 1;
+    K = 1 is t and K = 2 the quadratic Bernstein basis; derivatives match central differences."""
+    t = np.linspace(0, 1, 101)[:-1]
+    g, gd = O.traj_basis_table(t, K, "bspline")
+    P, L = min(3, K), K + 1 - min(3, K)
+    knots = np.concatenate([np.zeros(P), np.linspace(0, 1, L + 1), np.ones(P)])
+    xi = np.array([knots[k + 1:k + P + 1].mean() for k in range(1, K + 1)])
+    assert np.all(g >= -1e-15) and np.all(g.sum(1) <= 1 + 1e-12)
+    assert np.allclose(g @ xi, t, atol=1e-12)
+    g0, _ = O.traj_basis_table(np.zeros(1), K, "bspline")
+    assert np.allclose(g0, 0)
+    if K == 1:
+        assert np.allclose(g[:, 0], t)
+    if K == 2:
+        assert np.allclose(g, np.stack([2 * t * (1 - t), t * t], 1))
+    e = 1e-6
+    tt = np.linspace(0.01, 0.99, 37)
+    gp, _ = O.traj_basis_table(tt + e, K, "bspline")
+    gm, _ = O.traj_basis_table(tt - e, K, "bspline")
+    _, d = O.traj_basis_table(tt, K, "bspline")
+    assert np.allclose((gp - gm) / (2 * e), d, atol=1e-5 * max(1, np.abs(d).max()))
+
+
+def test_traj_basis_polynomial_and_bezier():
+    t = np.linspace(0, 1, 23)
+    g, gd = O.traj_basis_table(t, 4, "polynomial")
+    assert np.allclose(g, np.stack([t, t ** 2, t ** 3, t ** 4], 1)) and np.allclose(gd[:, 2], 3 * t ** 2)
+    g, gd = O.traj_basis_table(t, 3, "bezier")
+    assert np.allclose(g, np.stack([3 * t * (1 - t) ** 2, 3 * t ** 2 * (1 - t), t ** 3], 1))
+    assert np.allclose(gd[:, 2], 3 * t ** 2)
+
+
+def test_traj_pair_sums_straight_trajectories_are_the_reference_sums():
+    """Closed form: starts p = x - v t and control points v xi_k (straight B-spline trajectories) give the
+    reference's pair sums (fp64 brute force of atl/ops/reference.py:58-71), the same counts, and
+    -t gp + sum_k xi_k gcoef_k = dS/dv."""
+    rng = np.random.default_rng(16)
+    n, K = 400, 10
+    x = np.stack([rng.uniform(0, 30, n), rng.uniform(0, 20, n)], 1)
+    t = np.sort(rng.random(n))
+    b = np.sort(rng.integers(0, 2, n))
+    v = rng.standard_normal((n, 2)) * 4
+    P, L = 3, K - 2
+    knots = np.concatenate([np.zeros(P), np.linspace(0, 1, L + 1), np.ones(P)])
+    xi = np.array([knots[k + 1:k + P + 1].mean() for k in range(1, K + 1)])
+    coef = np.concatenate([v[:, 1:2] * xi, v[:, 0:1] * xi], 1)
+    anchors = np.arange(n)
+    xa = x + rng.standard_normal((n, 2)) * 0.5
+    S1, c1, g1 = O.traj_pair_sums_fp64(x - v * t[:, None], coef, t, b, anchors, xa, 1.0, 0.25, 3.0, 16, K, "bspline")
+    S0, c0, g0 = O.pair_sums_fp64(x, t, v, b, anchors, 1.0, 0.25, 3.0, anchor_xy=xa)
+    assert np.allclose(S1, S0, atol=1e-12) and np.array_equal(c1, c0) and c0.sum() > n
+    gS = rng.standard_normal(n)
+    gp, gc = g1(gS)
+    gv = -t[:, None] * gp + np.stack([(gc[:, K:] * xi).sum(1), (gc[:, :K] * xi).sum(1)], 1)
+    assert np.allclose(gv, g0(gS), atol=1e-10)
+
+
+def test_traj_pair_sums_gradients_match_finite_differences():
+    rng = np.random.default_rng(17)
+    n, K = 250, 5
+    x = np.stack([rng.uniform(0, 12, n), rng.uniform(0, 9, n)], 1)
+    t = np.sort(rng.random(n))
+    b = np.zeros(n, np.int64)
+    coef = rng.standard_normal((n, 2 * K)) * 2
+    xa = x + rng.standard_normal((n, 2)) * 0.5
+    gS = rng.standard_normal(n)
+    args = (t, b, np.arange(n), xa, 1.0, 0.3, 3.0, 16, K, "bspline")
+    _, _, grad = O.traj_pair_sums_fp64(x, coef, *args)
+    gp, gc = grad(gS)
+    e = 1e-6
+    j, k = np.unravel_index(np.abs(gc).argmax(), gc.shape)
+    c2 = coef.copy(); c2[j, k] += e
+    sp = O.traj_pair_sums_fp64(x, c2, *args)[0] @ gS
+    c2[j, k] -= 2 * e
+    sm = O.traj_pair_sums_fp64(x, c2, *args)[0] @ gS
+    assert abs((sp - sm) / (2 * e) - gc[j, k]) <= 1e-6 * max(1.0, abs(gc[j, k]))
+    i = int(np.abs(gp[:, 1]).argmax())
+    x2 = x.copy(); x2[i, 1] += e
+    sp = O.traj_pair_sums_fp64(x2, coef, *args)[0] @ gS
+    x2[i, 1] -= 2 * e
+    sm = O.traj_pair_sums_fp64(x2, coef, *args)[0] @ gS
+    assert abs((sp - sm) / (2 * e) - gp[i, 1]) <= 1e-6 * max(1.0, abs(gp[i, 1]))
+
+
+def test_traj_fp32_plan_and_pair_loops_match_fp64():
+    """The oracle's fp32 trajectory plan through its OpenMP pair loops against the float64 brute force: counts equal
+    except for pairs within 1e-5 of a cut-off, sums within 1e-5, the loops' gradients within 1e-4."""
+    rng = np.random.default_rng(18)
+    n, K, H, W = 3000, 10, 30, 40
+    x = np.stack([rng.uniform(0, W, n), rng.uniform(0, H, n)], 1).astype(F32)
+    t = np.sort(rng.random(n)).astype(F32)
+    b = np.zeros(n, np.int64)
+    coef = (rng.standard_normal((n, 2 * K)) * 2).astype(F32)
+    xa = (x + rng.standard_normal((n, 2)) * 0.5).astype(F32)
+    tab = O.traj_slice_table(K, "bspline", 16)
+    plan = O.build_pair_plan_traj(x, coef, tab, t, b, 1, H, W, np.arange(n), xa, 1.0, 0.3, 3.0, 16)
+    S32, c32 = O.ats_pair_fwd(plan, 1.0, 0.3, 3.0, with_counts=True)
+    S64, c64, grad = O.traj_pair_sums_fp64(x, coef, t, b, np.arange(n), xa, 1.0, 0.3, 3.0, 16, K, "bspline")
+    assert np.abs(c32 - c64).sum() <= 3 and c64.sum() > 10 * n
+    assert np.allclose(S32, S64, rtol=1e-5, atol=1e-5 * S64.max())
+    gS = rng.standard_normal(n).astype(F32)
+    gp, gc = O.ats_pair_bwd_traj(gS, plan, tab, K, 1.0, 0.3, 3.0, n)
+    wp, wc = grad(gS)
+    assert np.abs(gp - wp).max() <= 1e-4 * np.abs(wp).max() and np.abs(gc - wc).max() <= 1e-4 * np.abs(wc).max()
+
+
+def test_blur_impulse_response_and_mass():
+    """The oracle's blur: an impulse far from the border becomes the outer product of the normalised taps (mass
+    1); an image at the border loses exactly the mass that falls outside (zero padding)."""
+    img = np.zeros((1, 31, 33), F32)
+    img[0, 15, 16] = 1.0
+    out = O.blur(img, 1.3)
+    r = int(math.ceil(3 * 1.3))
+    x = np.arange(-r, r + 1)
+    k = np.exp(-x * x / (2 * 1.3 ** 2))
+    k /= k.sum()
+    assert np.allclose(out[0, 15 - r:16 + r, 16 - r:17 + r], np.outer(k, k), atol=1e-7)
+    assert abs(float(out.sum()) - 1.0) < 1e-6
+    edge = np.zeros((1, 20, 20), F32)
+    edge[0, 0, 10] = 1.0                         # on the top row: the taps at rows -3..-1 fall outside
+    k1 = np.exp(-np.arange(-3, 4) ** 2 / 2.0)
+    k1 /= k1.sum()
+    assert abs(float(O.blur(edge, 1.0).sum()) - k1[3:].sum()) < 1e-6
+
+
+def test_make_iwe_weights_and_polarity_split():
+    """The oracle's IWE: integer positions deposit their weights in one pixel; the border mask drops events
+    outside; scale_by_dt weights 1 - |t - t_ref|; split polarity puts positive events in entry 2b, negative
+    ones in 2b + 1."""
+    xy = np.array([[2, 3], [2, 3], [5, 1], [-1, 2], [4, 4]], F32)
+    t = np.array([0.5, 0.1, 0.9, 0.5, 1.7], F32)
+    p = np.array([1, -1, 1, 1, -1], F32)
+    b = np.array([0, 0, 1, 1, 1])
+    img = O.make_iwe(xy, t, p, b, 2, 6, 7, 0.5, sigma=0.0)
+    assert img[0, 3, 2] == 2 and img[1, 1, 5] == 1 and img[1, 4, 4] == 1 and img.sum() == 4
+    img = O.make_iwe(xy, t, p, b, 2, 6, 7, 0.5, sigma=0.0, scale_by_dt=True)
+    assert np.isclose(img[0, 3, 2], 1.0 + 0.6) and np.isclose(img[1, 1, 5], 0.6) and img[1, 4, 4] == 0
+    img = O.make_iwe(xy, t, p, b, 2, 6, 7, 0.5, sigma=0.0, polarity="split")
+    assert img.shape == (4, 6, 7) and img[0, 3, 2] == 1 and img[1, 3, 2] == 1 and img[2, 1, 5] == 1
+    assert img[3, 4, 4] == 1

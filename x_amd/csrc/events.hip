@@ -520,10 +520,14 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos_cl(const float* 
 
 // ------------------------------------------------------------------------------ trajectory displacement
 // d(p, t) = sum_k c_k(p) g_k(t) of a coefficient grid with channels [y_1..y_K, x_1..x_K] (the displacement of
-// atl/motion/trajectories.py: the coefficients are the bilinear border-clamped sample at p, g_k(t) = t^k for
-// the polynomial basis, binom(K, k) t^k (1 - t)^(K - k) for the Bernstein basis, k = 1..K).  One pass per
-// event instead of the (N, 2K) coefficient rows and the products and sums over them.  The powers are repeated
-// products (torch's pow rounds differently by a few ulps) and the k sum runs in order.
+// atl/motion/trajectories.py: the coefficients are the bilinear border-clamped sample at p, k = 1..K).  Bases:
+//   0  polynomial  g_k(t) = t^k
+//   1  Bernstein   g_k(t) = binom(K, k) t^k (1 - t)^(K - k)            (degree K, control point 0 pinned to p)
+//   2  B-spline    g_k(t) = N_k(t), the clamped uniform B-spline basis of degree P = min(3, K) with K + 1
+//                  functions N_0..N_K on [0, 1] (L = K + 1 - P equal spans); N_0 belongs to the pinned start
+//                  p, and N_k(0) = 0 for k >= 1, so g_k(t) - g_k(0) = N_k(t).
+// One pass per event instead of the (N, 2K) coefficient rows and the products and sums over them.  The powers
+// are repeated products (torch's pow rounds differently by a few ulps) and the k sum runs in order.
 constexpr int kTrajMaxK = 16;
 
 __host__ __device__ constexpr int binom_int(int n, int k) {   // exact for n <= 16
@@ -532,14 +536,55 @@ __host__ __device__ constexpr int binom_int(int n, int k) {   // exact for n <= 
   return r;
 }
 
+// The nonzero B-spline functions at t: N_{j..j+P}(t) in nb[0..P] for the span j = clamp(floor(t L), 0, L - 1)
+// (outside [0, 1] the end span's polynomial continues), by the triangular Cox-de Boor recursion (Piegl and
+// Tiller, The NURBS Book, algorithm A2.2) on the knots u_i = clamp(i - P, 0, L) / L.  Every denominator is at
+// least one span wide.
 template <int K>
-__device__ __forceinline__ void traj_basis(float t, int bernstein, float (&g)[K]) {
+__device__ __forceinline__ int bspline_nonzero(float t, float (&nb)[(K < 3 ? K : 3) + 1]) {
+  constexpr int P = K < 3 ? K : 3, L = K + 1 - P;
+  const float fl = (float)L;
+  const int j = min(max((int)floorf(t * fl), 0), L - 1);
+  auto knot = [&](int i) { return (float)min(max(i - P, 0), L) / fl; };
+  float left[P + 1], right[P + 1];
+  nb[0] = 1.f;
+#pragma unroll
+  for (int d = 1; d <= P; ++d) {
+    left[d] = t - knot(j + P + 1 - d);
+    right[d] = knot(j + P + d) - t;
+    float saved = 0.f;
+#pragma unroll
+    for (int r = 0; r < d; ++r) {
+      const float tmp = nb[r] / (right[r + 1] + left[d - r]);
+      nb[r] = saved + right[r + 1] * tmp;
+      saved = left[d - r] * tmp;
+    }
+    nb[d] = saved;
+  }
+  return j;
+}
+
+template <int K>
+__device__ __forceinline__ void traj_basis(float t, int basis, float (&g)[K]) {
   float tk = 1.f;
-  if (!bernstein) {
+  if (basis == 0) {
 #pragma unroll
     for (int k = 1; k <= K; ++k) {
       tk = tk * t;
       g[k - 1] = tk;
+    }
+    return;
+  }
+  if (basis == 2) {
+    constexpr int P = K < 3 ? K : 3;
+    float nb[P + 1];
+    const int j = bspline_nonzero<K>(t, nb);
+#pragma unroll
+    for (int k = 1; k <= K; ++k) {               // g_k = N_k = nb[k - j] if 0 <= k - j <= P (register selects)
+      float v = 0.f;
+#pragma unroll
+      for (int r = 0; r <= P; ++r) v = k - j == r ? nb[r] : v;
+      g[k - 1] = v;
     }
     return;
   }
@@ -562,7 +607,7 @@ template <int K>
 __global__ void __launch_bounds__(kBlock) k_traj_displacement(const float4* __restrict__ fcl, int64_t B, int Hg,
                                                               int Wg, const float2* __restrict__ gpos,
                                                               const int64_t* __restrict__ bidx,
-                                                              const float* __restrict__ t, int bernstein, int64_t N,
+                                                              const float* __restrict__ t, int basis, int64_t N,
                                                               float2* __restrict__ out) {
   constexpr int C = 2 * K, Q = (C + 3) / 4, EPW = kWave / Q;   // events per wave
   const int lane = threadIdx.x & (kWave - 1);
@@ -577,7 +622,7 @@ __global__ void __launch_bounds__(kBlock) k_traj_displacement(const float4* __re
     const float2 p = gpos[n];
     const GridCorners c = grid_corners(p.x, p.y, Hg, Wg, 1.f, 1.f, false);
     float g[K];
-    traj_basis<K>(t[n], bernstein, g);
+    traj_basis<K>(t[n], basis, g);
     const float4* f = fcl + b * ((int64_t)Hg * Wg) * Q + q;
     const float4 a = f[(int64_t)c.o00 * Q], h0 = f[(int64_t)c.o01 * Q], h1 = f[(int64_t)c.o10 * Q],
                  k1 = f[(int64_t)c.o11 * Q];
@@ -616,14 +661,14 @@ __global__ void __launch_bounds__(kBlock) k_traj_displacement(const float4* __re
 // take.  One lane per (event, channel quad), so the rows are written by consecutive lanes.
 template <int K>
 __global__ void __launch_bounds__(kBlock) k_traj_gout(const float2* __restrict__ gd, const float* __restrict__ t,
-                                                      int bernstein, int N, float* __restrict__ gout) {
+                                                      int basis, int N, float* __restrict__ gout) {
   constexpr int C = 2 * K, Q = (C + 3) / 4;
   const int gl = blockIdx.x * blockDim.x + threadIdx.x;   // N * Q < 2^31
   const int n = gl / Q;
   if (n >= N) return;
   const int q = gl - n * Q;
   float g[K];
-  traj_basis<K>(t[n], bernstein, g);
+  traj_basis<K>(t[n], basis, g);
   const float2 d = gd[n];
   float* o = gout + (int64_t)n * C;
 #pragma unroll
@@ -833,23 +878,26 @@ int atl_sample_grid_bwd_pos_cl(const float* gout, const float* field_cl, int64_t
   return check_launch("sample_grid_bwd_pos_cl");
 }
 
-int atl_traj_displacement(const float* field_cl, int64_t B, int64_t K, int64_t Hg, int64_t Wg, const float* gpos,
-                          const int64_t* b, const float* t, int64_t N, int64_t basis, float* out, hipStream_t stream) {
-  if (N < 0 || B < 0 || K < 1 || K > kTrajMaxK || !dims_ok(Hg, Wg) || (basis != 0 && basis != 1)) {
-    set_error("traj_displacement: bad sizes (1 <= K <= %d, basis 0 or 1)", kTrajMaxK);
+int atl_traj_displacement(const float* field_cl, int64_t B, int64_t C, int64_t K, int64_t Hg, int64_t Wg,
+                          const float* gpos, const int64_t* b, const float* t, int64_t N, int64_t basis, float* out,
+                          hipStream_t stream) {
+  if (N < 0 || B < 0 || K < 1 || K > kTrajMaxK || !dims_ok(Hg, Wg) || basis < 0 || basis > 2) {
+    set_error("traj_displacement: bad sizes (1 <= K <= %d, basis 0, 1 or 2)", kTrajMaxK);
     return 1;
   }
+  if (C != 2 * K) { set_error("traj_displacement: the coefficient grid has %lld channels, expected 2K = %lld", (long long)C, (long long)(2 * K)); return 1; }
   if (N == 0) return 0;
+  if (!field_cl || !gpos || !b || !t || !out) { set_error("traj_displacement: null argument"); return 1; }
   if (reinterpret_cast<uintptr_t>(field_cl) & 15) { set_error("traj_displacement: field_cl must be 16-byte aligned"); return 1; }
   const int64_t Q = (2 * K + 3) / 4, waves = (N + kWave / Q - 1) / (kWave / Q);
   const dim3 grid(grid_for(waves * kWave)), block(kBlock);
   const float4* f = (const float4*)field_cl;
   const float2* p = (const float2*)gpos;
   float2* o = (float2*)out;
-  const int bern = (int)basis;
+  const int bs = (int)basis;
   switch (K) {
 #define ATL_TRAJ_CASE(k) \
-    case k: hipLaunchKernelGGL(k_traj_displacement<k>, grid, block, 0, stream, f, B, (int)Hg, (int)Wg, p, b, t, bern, N, o); break;
+    case k: hipLaunchKernelGGL(k_traj_displacement<k>, grid, block, 0, stream, f, B, (int)Hg, (int)Wg, p, b, t, bs, N, o); break;
     ATL_TRAJ_CASE(1) ATL_TRAJ_CASE(2) ATL_TRAJ_CASE(3) ATL_TRAJ_CASE(4) ATL_TRAJ_CASE(5) ATL_TRAJ_CASE(6)
     ATL_TRAJ_CASE(7) ATL_TRAJ_CASE(8) ATL_TRAJ_CASE(9) ATL_TRAJ_CASE(10) ATL_TRAJ_CASE(11) ATL_TRAJ_CASE(12)
     ATL_TRAJ_CASE(13) ATL_TRAJ_CASE(14) ATL_TRAJ_CASE(15) ATL_TRAJ_CASE(16)
@@ -860,18 +908,19 @@ int atl_traj_displacement(const float* field_cl, int64_t B, int64_t K, int64_t H
 
 int atl_traj_gout(const float* gd, const float* t, int64_t N, int64_t K, int64_t basis, float* gout,
                   hipStream_t stream) {
-  if (N < 0 || K < 1 || K > kTrajMaxK || (basis != 0 && basis != 1)) {
-    set_error("traj_gout: bad sizes (1 <= K <= %d, basis 0 or 1)", kTrajMaxK);
+  if (N < 0 || K < 1 || K > kTrajMaxK || basis < 0 || basis > 2) {
+    set_error("traj_gout: bad sizes (1 <= K <= %d, basis 0, 1 or 2)", kTrajMaxK);
     return 1;
   }
   const int64_t Q = (2 * K + 3) / 4;
   if (N * Q >= ((int64_t)1 << 31) - kBlock) { set_error("traj_gout: N * ceil(K/2) must stay below 2^31"); return 1; }
   if (N == 0) return 0;
+  if (!gd || !t || !gout) { set_error("traj_gout: null argument"); return 1; }
   const dim3 grid(grid_for(N * Q)), block(kBlock);
   const float2* g = (const float2*)gd;
-  const int bern = (int)basis, n = (int)N;
+  const int bs = (int)basis, n = (int)N;
   switch (K) {
-#define ATL_TRAJ_CASE(k) case k: hipLaunchKernelGGL(k_traj_gout<k>, grid, block, 0, stream, g, t, bern, n, gout); break;
+#define ATL_TRAJ_CASE(k) case k: hipLaunchKernelGGL(k_traj_gout<k>, grid, block, 0, stream, g, t, bs, n, gout); break;
     ATL_TRAJ_CASE(1) ATL_TRAJ_CASE(2) ATL_TRAJ_CASE(3) ATL_TRAJ_CASE(4) ATL_TRAJ_CASE(5) ATL_TRAJ_CASE(6)
     ATL_TRAJ_CASE(7) ATL_TRAJ_CASE(8) ATL_TRAJ_CASE(9) ATL_TRAJ_CASE(10) ATL_TRAJ_CASE(11) ATL_TRAJ_CASE(12)
     ATL_TRAJ_CASE(13) ATL_TRAJ_CASE(14) ATL_TRAJ_CASE(15) ATL_TRAJ_CASE(16)

@@ -53,6 +53,7 @@ constexpr int kUnroll = 4;                         // candidates per walk step (
 constexpr int kSliceBatch = 4;                     // pass 1: slices of one source keyed and placed together
 
 constexpr int kXcd = 8;                            // XCDs: consecutive workgroups go round-robin over them
+constexpr int kTrajPairMaxK = 12;                  // trajectory model: coefficients per axis (K) the kernels take
 
 // Fixed geometry shared by every kernel (host-computed, passed by value).
 struct FGeo {
@@ -161,14 +162,42 @@ __device__ __forceinline__ bool row_span(int r, float qx, float qy, float R, flo
   return true;
 }
 
-// Entry (j, s): slice-centre position (functional.py:157-158) and cell key.
+// Cell key of an entry of slice s at slice-centre position (yx, yy).
+__device__ __forceinline__ int entry_key_at(float yx, float yy, int bj, int s, const FGeo& G) {
+  const int cx = cell_walk(yx, G.gx0, G.gx1, G.icf, G.GW), cy = cell_walk(yy, G.gy0, G.gy1, G.icf, G.GH);
+  return ((bj * G.S + s) * G.GH + cy) * G.GW + cx;
+}
+
+// Entry (j, s) of the linear model: slice-centre position (functional.py:157-158) and cell key.
 __device__ __forceinline__ int entry_key(float2 xj, float2 vj, float tj, int bj, int s, const FGeo& G, float& yx,
                                          float& yy) {
   const float dt = slice_centre(s, G.delta) - tj;
   yx = xj.x + vj.x * dt;
   yy = xj.y + vj.y * dt;
-  const int cx = cell_walk(yx, G.gx0, G.gx1, G.icf, G.GW), cy = cell_walk(yy, G.gy0, G.gy1, G.icf, G.GH);
-  return ((bj * G.S + s) * G.GH + cy) * G.GW + cx;
+  return entry_key_at(yx, yy, bj, s, G);
+}
+
+// Entry (j, s) of the trajectory model: source j carries its trajectory start p and its 2K coefficients
+// cf = [y_1..y_K, x_1..x_K]; tab row s = [g_1..g_K(c_s), g_1'..g_K'(c_s)].  The slice-centre position is
+// y = p + sum_k cf_k g_k(c_s) and the velocity v = sum_k cf_k g_k'(c_s), each sum in k order in fp32.
+template <int K>
+__device__ __forceinline__ void traj_entry(const float (&cf)[2 * K], float px, float py,
+                                           const float* __restrict__ tab, int s, float& yx, float& yy, float& vx,
+                                           float& vy) {
+  const float* row = tab + s * 2 * K;
+  float dx = 0.f, dy = 0.f, ux = 0.f, uy = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const float g = row[k], gd = row[K + k];
+    dy = dy + cf[k] * g;
+    dx = dx + cf[K + k] * g;
+    uy = uy + cf[k] * gd;
+    ux = ux + cf[K + k] * gd;
+  }
+  yx = px + dx;
+  yy = py + dy;
+  vx = ux;
+  vy = uy;
 }
 
 // Sources are ordered by their own-slice cell in tile order: bands of kSrcTile cell rows, within a band tiles
@@ -222,14 +251,18 @@ __global__ void __launch_bounds__(kBlock) k_fill_zero(int* __restrict__ p, int64
 // reserves its run of every bucket it feeds with one atomic add on the bucket's position bpos[bucket] (the
 // exclusive scan of the totals; after this pass it holds the bucket's end), keeps the run starts in LDS, and
 // each record takes its slot.  The runs of one bucket follow in no fixed block order; pass 2 orders the bucket.
-template <bool SCATTER>
+// The source model: K = 0 linear (x, v per source: y = x + v (c_s - t), the reference's), K > 0 trajectories
+// (x = the trajectory start p, `coef` the (N, 2K) coefficient rows, `tab` the (S, 2K) slice-centre basis table).
+template <bool SCATTER, int K>
 __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restrict__ x, const float* __restrict__ t,
                                                        const float2* __restrict__ v, const int64_t* __restrict__ b,
                                                        int64_t N, const int64_t* __restrict__ anchors,
                                                        const float2* __restrict__ anchor_xy, int64_t M, FGeo G,
                                                        int* __restrict__ cnt, int* __restrict__ bsum,
                                                        Rec* __restrict__ trec, FParams* __restrict__ P,
-                                                       int* __restrict__ self, int* __restrict__ eself) {
+                                                       int* __restrict__ self, int* __restrict__ eself,
+                                                       const float* __restrict__ coef,
+                                                       const float* __restrict__ tab) {
   extern __shared__ int hist[];
   __shared__ int red[kP1Block / kWave];
   int vm = 0;                                    // this thread's max ||v|| (sources) or max |at| (anchors)
@@ -248,7 +281,52 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
   // anchor blocks first: they are about a quarter of a source block's work, and dispatched last they would
   // queue on the few CUs left free by the source blocks
   const bool src_blk = blk >= G.nblk_a;
-  if (src_blk) {
+  if (src_blk && K > 0) {
+    // trajectory sources, one at a time: the 2K coefficients stay in registers across the source's slices
+    constexpr int KK = K > 0 ? K : 1;
+    const int64_t j0 = (int64_t)(blk - G.nblk_a) * kSrcPerBlock;
+    for (int u = 0; u < kSrcPerBlock / kP1Block; ++u) {
+      const int64_t j = j0 + u * kP1Block + threadIdx.x;
+      if (j >= N) break;
+      if (!SCATTER) {
+        self[j] = -1;
+        eself[j] = -1;
+      }
+      const int64_t bj = b[j];
+      if (bj < 0 || bj >= G.B) continue;
+      const float tj = t[j];
+      const float2 pj = x[j];
+      float cf[2 * KK];
+#pragma unroll
+      for (int c = 0; c < 2 * KK; ++c) cf[c] = coef[j * (2 * KK) + c];
+      int lo, hi;
+      slice_range(tj, G, lo, hi);
+      const int own = min(max((int)fminf(fmaxf(floorf(tj / G.delta), 0.f), (float)(G.S - 1)), lo), hi);
+      for (int s = lo; s <= hi; ++s) {
+        float yx, yy, vx, vy;
+        traj_entry<KK>(cf, pj.x, pj.y, tab, s, yx, yy, vx, vy);
+        if (!SCATTER) vm = max(vm, float_to_ordered(sqrtf(vx * vx + vy * vy)));
+        const int key = entry_key_at(yx, yy, (int)bj, s, G);
+        const int slot = atomicAdd(hist + (key >> G.bshift), 1);
+        int sslot = -1, skey = -1;
+        if (s == own) {                          // the source record goes with its own slice
+          skey = 2 * G.ncell_pad + source_key(key, G);
+          sslot = atomicAdd(hist + (skey >> G.bshift), 1);
+        }
+        if (SCATTER) {
+          Rec r;
+          r.f = make_float4(yx, yy, vx, vy);
+          r.i = make_int4(__float_as_int(tj), (int)j, key, 0);
+          trec[slot] = r;
+          if (sslot >= 0) {
+            r.f = make_float4(pj.x, pj.y, 0.f, 0.f);
+            r.i = make_int4(__float_as_int(tj), (int)j, skey, 0);
+            trec[sslot] = r;
+          }
+        }
+      }
+    }
+  } else if (src_blk) {
     constexpr int per = kSrcPerBlock / kP1Block;
     const int64_t j0 = (int64_t)(blk - G.nblk_a) * kSrcPerBlock;
     float2 xj[per], vj[per];
@@ -1035,6 +1113,129 @@ __global__ void __launch_bounds__(kPairBlock) k_fast_bwd(FPlan p, FGeo G, int N,
   if (have && part == 0) gv[si.y] = m;
 }
 
+// Backward of the trajectory model: every source (one lane per part of its slices, own-slice tile order) sums
+// over the anchors of each slice s of its range, within R of its slice-centre position y_s, the gradients of the
+// entry's position and velocity, Gy_s = sum_i gS_i k r / h^2 and Gv_s = sum_i gS_i k r at_i / h^2
+// (r = x_i - (y_s + v_s at_i), the pair terms of the forward), and chains them in registers through
+// y_s = p + sum_k cf_k g_k(c_s), v_s = sum_k cf_k g_k'(c_s): gp[j] = sum_s Gy_s and
+// gcoef[j, k] = sum_s (Gy_s g_k(c_s) + Gv_s g_k'(c_s)) per axis (channels [y_1..y_K, x_1..x_K]).  Each source's
+// gradients are complete in its lanes and written once, without atomics.
+template <int K, bool DUP>
+__device__ __forceinline__ void bwd_traj_source(const FPlan& p, const FGeo& G, float R, float R2, float px,
+                                                float py, const float (&cf)[2 * K], const float* __restrict__ tab,
+                                                int sid, float tj, int key, int sp, int part, int2* rowtab,
+                                                float (&gc)[2 * K], float& gpx, float& gpy) {
+  const int plane_cells = G.GH * G.GW;
+  const int* astart = p.start + G.ncell_pad;
+  const int E = uni(p.start[G.ncell_pad]);
+  const int* aid = (const int*)p.arec + 4;         // event id of record k: aid[8 * k]
+  int lo_l, hi_l;
+  slice_range(tj, G, lo_l, hi_l);
+  if (kBwdParts > 1) {
+    const int L = max(hi_l - lo_l + 1, 0);
+    const int a = lo_l + (part * L) / kBwdParts, b = lo_l + ((part + 1) * L) / kBwdParts - 1;
+    lo_l = a;
+    hi_l = b;
+  }
+  const int bj = key / (G.S * plane_cells);
+  for (int s = lo_l; s <= hi_l; ++s) {
+    float yx, yy, vx, vy;
+    traj_entry<K>(cf, px, py, tab, s, yx, yy, vx, vy);
+    const float cs = slice_centre(s, G.delta);
+    const float qx = clampf(yx, G.gx0, G.gx1), qy = clampf(yy, G.gy0, G.gy1);
+    float gyx = 0.f, gyy = 0.f, gvx = 0.f, gvy = 0.f;
+    walk_flat(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, rowtab, [&](int k, int e) {
+      float4 A[kUnroll];
+      int id[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        A[u] = ld((const float4*)p.brec + u, (uint32_t)k);
+        if (DUP) id[u] = ld(aid + 8 * u, 8u * (uint32_t)k);
+      }
+      const int rem = e - k, self_u = sp - k;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const float at = A[u].z - cs;
+        const float dt = A[u].z - tj;
+        const float rx = A[u].x - (yx + vx * at);
+        const float ry = A[u].y - (yy + vy * at);
+        const float d2 = rx * rx + ry * ry;
+        const bool other = DUP ? id[u] != sid : u != self_u;
+        const bool ok = other & !(fabsf(dt) > G.tau) & !(d2 > G.r2max) & (u < rem);
+        // selects, not products with zero: records past the range end may hold anything, NaN included
+        const float f = A[u].w * __builtin_amdgcn_exp2f(d2 * G.kexp);   // A.w = gS / h^2
+        const float fx = f * rx, fy = f * ry;
+        gyx = ok ? gyx + fx : gyx;
+        gyy = ok ? gyy + fy : gyy;
+        gvx = ok ? fmaf(fx, at, gvx) : gvx;
+        gvy = ok ? fmaf(fy, at, gvy) : gvy;
+      }
+    });
+    gpx += gyx;
+    gpy += gyy;
+    const float* row = tab + s * 2 * K;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float g = row[k], gd = row[K + k];
+      gc[k] = fmaf(gyy, g, fmaf(gvy, gd, gc[k]));
+      gc[K + k] = fmaf(gyx, g, fmaf(gvx, gd, gc[K + k]));
+    }
+  }
+}
+
+template <int K>
+__global__ void __launch_bounds__(kPairBlock) k_fast_bwd_traj(FPlan p, FGeo G, int N, const float* __restrict__ coef,
+                                                             const float* __restrict__ tab, float2* __restrict__ gp,
+                                                             float* __restrict__ gcoef) {
+  __shared__ int2 rowtab[kRowTab * kPairBlock];
+  constexpr int kSrcPerWave = kWave / kBwdParts;
+  const int lb = xcd_block((N + kPairBlock / kBwdParts - 1) / (kPairBlock / kBwdParts));
+  if (lb < 0) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int part = lane / kSrcPerWave, ls = lane - part * kSrcPerWave;
+  const int wbase = (lb * (kPairBlock / kWave) + (int)(threadIdx.x / kWave)) * kSrcPerWave;
+  const int EA = uni(p.start[2 * G.ncell_pad]);
+  const int Nv = uni(p.start[3 * G.ncell_pad]) - EA;
+  if (wbase >= Nv) return;
+  const int n = min(kSrcPerWave, Nv - wbase);
+  float R, R2;
+  search_radius(p.P, G, R, R2);
+  R = unif(R);
+  R2 = unif(R2);
+  const bool have = ls < n;
+  const Rec SR = p.srec[wbase + min(ls, n - 1)];
+  const int4 si = SR.i;
+  const float tj = __int_as_float(si.x);
+  float cf[2 * K], gc[2 * K];
+#pragma unroll
+  for (int c = 0; c < 2 * K; ++c) {
+    cf[c] = coef[(int64_t)si.y * (2 * K) + c];
+    gc[c] = 0.f;
+  }
+  const int sp = p.self[si.y];
+  float gpx = 0.f, gpy = 0.f;
+  if (have) {
+    if (uni(p.P->dup))
+      bwd_traj_source<K, true>(p, G, R, R2, SR.f.x, SR.f.y, cf, tab, si.y, tj, si.z, sp, part, rowtab + threadIdx.x,
+                               gc, gpx, gpy);
+    else
+      bwd_traj_source<K, false>(p, G, R, R2, SR.f.x, SR.f.y, cf, tab, si.y, tj, si.z, sp, part, rowtab + threadIdx.x,
+                                gc, gpx, gpy);
+  }
+#pragma unroll
+  for (int o = kSrcPerWave; o < kWave; o <<= 1) {  // the parts of a source sit kSrcPerWave lanes apart
+    gpx += __shfl_xor(gpx, o);
+    gpy += __shfl_xor(gpy, o);
+#pragma unroll
+    for (int c = 0; c < 2 * K; ++c) gc[c] += __shfl_xor(gc[c], o);
+  }
+  if (have && part == 0) {
+    gp[si.y] = make_float2(gpx, gpy);
+#pragma unroll
+    for (int c = 0; c < 2 * K; ++c) gcoef[(int64_t)si.y * (2 * K) + c] = gc[c];
+  }
+}
+
 // ------------------------------------------------------------------------------------------ host side
 int64_t align256(int64_t n) { return (n + 255) & ~(int64_t)255; }
 
@@ -1159,13 +1360,17 @@ int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W
   return 0;
 }
 
-int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, const float* v, const int64_t* b,
-                  const int64_t* anchors, const float* anchor_xy, void* ws, int64_t ws_bytes, hipStream_t stream) {
-  FGeo G;
-  if (!make_geo(geo, G)) { set_error("fast_plan: geometry not initialised by atl_fast_geometry_init"); return 1; }
-  if (!ws || ws_bytes < geo->ws_bytes) { set_error("fast_plan: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)geo->ws_bytes); return 1; }
+}  // extern "C"
+
+namespace {
+
+// The plan's launches for source model K (0: linear, x / v per source; K > 0: trajectories, x = starts p,
+// coef rows and the slice table tab).
+template <int K>
+int fast_plan_impl(const atl_fast_geometry* geo, const FGeo& G, const float* x, const float* t, const float* v,
+                   const int64_t* b, const int64_t* anchors, const float* anchor_xy, const float* coef,
+                   const float* tab, void* ws, hipStream_t stream) {
   const int64_t N = geo->N, M = geo->M;
-  if ((N > 0 && (!x || !t || !v || !b)) || (M > 0 && !anchors && M != N)) { set_error("fast_plan: null input"); return 1; }
   FParams* P = at_off<FParams>(ws, geo->off_params);
   int* cnt = at_off<int>(ws, geo->off_cnt);
   int* bpos = at_off<int>(ws, geo->off_boff);
@@ -1176,14 +1381,14 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
   hipLaunchKernelGGL(k_fill_zero, dim3(grid_for(nclear)), dim3(kBlock), 0, stream, (int*)P, nclear);
   const size_t lds = (size_t)G.nbuckets * sizeof(int);
   if (nblk > 0)
-    hipLaunchKernelGGL(k_sort_pass1<false>, dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
+    hipLaunchKernelGGL((k_sort_pass1<false, K>), dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
                        (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, tot, (Rec*)nullptr, P,
-                       at_off<int>(ws, geo->off_self), at_off<int>(ws, geo->off_eself));
+                       at_off<int>(ws, geo->off_self), at_off<int>(ws, geo->off_eself), coef, tab);
   scan_small(tot, G.nbuckets, bpos, stream);
   if (nblk > 0)
-    hipLaunchKernelGGL(k_sort_pass1<true>, dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
+    hipLaunchKernelGGL((k_sort_pass1<true, K>), dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
                        (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, bpos, trec,
-                       (FParams*)nullptr, (int*)nullptr, (int*)nullptr);
+                       (FParams*)nullptr, (int*)nullptr, (int*)nullptr, coef, tab);
   auto pass2 = G.bshift == 10 ? k_sort_pass2<10> : G.bshift == 11 ? k_sort_pass2<11>
              : G.bshift == 12 ? k_sort_pass2<12> : k_sort_pass2<13>;
   hipLaunchKernelGGL(pass2, dim3(G.nbuckets), dim3(kSortBlock), 0, stream, (const int*)bpos,
@@ -1192,7 +1397,43 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
                              at_off<float>(ws, geo->off_etim), at_off<int>(ws, geo->off_eself),
                              at_off<Rec>(ws, geo->off_arec), at_off<Rec>(ws, geo->off_srec),
                              at_off<int>(ws, geo->off_self)});
+  return 0;
+}
+
+bool plan_args_ok(const atl_fast_geometry* geo, FGeo& G, void* ws, int64_t ws_bytes, const char* what) {
+  if (!make_geo(geo, G)) { set_error("%s: geometry not initialised by atl_fast_geometry_init", what); return false; }
+  if (!ws || ws_bytes < geo->ws_bytes) { set_error("%s: workspace of %lld bytes, need %lld", what, (long long)ws_bytes, (long long)geo->ws_bytes); return false; }
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, const float* v, const int64_t* b,
+                  const int64_t* anchors, const float* anchor_xy, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  FGeo G;
+  if (!plan_args_ok(geo, G, ws, ws_bytes, "fast_plan")) return 1;
+  const int64_t N = geo->N, M = geo->M;
+  if ((N > 0 && (!x || !t || !v || !b)) || (M > 0 && !anchors && M != N)) { set_error("fast_plan: null input"); return 1; }
+  fast_plan_impl<0>(geo, G, x, t, v, b, anchors, anchor_xy, nullptr, nullptr, ws, stream);
   return check_launch("fast_plan");
+}
+
+int atl_fast_plan_traj(const atl_fast_geometry* geo, const float* p, const float* coef, int64_t K, const float* tab,
+                       const float* t, const int64_t* b, const int64_t* anchors, const float* anchor_xy, void* ws,
+                       int64_t ws_bytes, hipStream_t stream) {
+  FGeo G;
+  if (!plan_args_ok(geo, G, ws, ws_bytes, "fast_plan_traj")) return 1;
+  const int64_t N = geo->N, M = geo->M;
+  if (K < 1 || K > kTrajPairMaxK) { set_error("fast_plan_traj: K = %lld outside 1..%d", (long long)K, kTrajPairMaxK); return 1; }
+  if ((N > 0 && (!p || !coef || !tab || !t || !b)) || (M > 0 && !anchors && M != N)) { set_error("fast_plan_traj: null input"); return 1; }
+  switch (K) {
+#define ATL_K(k) case k: fast_plan_impl<k>(geo, G, p, t, nullptr, b, anchors, anchor_xy, coef, tab, ws, stream); break;
+    ATL_K(1) ATL_K(2) ATL_K(3) ATL_K(4) ATL_K(5) ATL_K(6) ATL_K(7) ATL_K(8) ATL_K(9) ATL_K(10) ATL_K(11) ATL_K(12)
+#undef ATL_K
+  }
+  return check_launch("fast_plan_traj");
 }
 
 int atl_fast_pair_fwd(const atl_fast_geometry* geo, const void* ws, float* out, int* count, hipStream_t stream) {
@@ -1221,6 +1462,29 @@ int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, f
     hipLaunchKernelGGL(k_fast_bwd, dim3(xcd_grid((geo->N + kPairBlock / kBwdParts - 1) / (kPairBlock / kBwdParts))),
                        dim3(kPairBlock), 0, stream, p, G, (int)geo->N, (float2*)gv);
   return check_launch("fast_pair_bwd");
+}
+
+int atl_fast_pair_bwd_traj(const atl_fast_geometry* geo, void* ws, const float* gS, const float* coef, int64_t K,
+                           const float* tab, float* gp, float* gcoef, hipStream_t stream) {
+  FGeo G;
+  if (!make_geo(geo, G)) { set_error("fast_pair_bwd_traj: geometry not initialised"); return 1; }
+  if (K < 1 || K > kTrajPairMaxK) { set_error("fast_pair_bwd_traj: K = %lld outside 1..%d", (long long)K, kTrajPairMaxK); return 1; }
+  if (!ws || (geo->N > 0 && (!gp || !gcoef || !coef || !tab)) || (geo->M > 0 && !gS)) { set_error("fast_pair_bwd_traj: null argument"); return 1; }
+  if (geo->N == 0) return 0;
+  const FPlan p = make_plan(ws, geo);
+  // gp cleared by the record pass, gcoef here: sources outside the plan keep zero gradients
+  hipLaunchKernelGGL(k_fill_zero, dim3(grid_for(geo->N * 2 * K)), dim3(kBlock), 0, stream, (int*)gcoef, geo->N * 2 * K);
+  hipLaunchKernelGGL(k_fast_gather_gs, dim3(grid_for(std::max(geo->M, geo->N))), dim3(kBlock), 0, stream, p, G,
+                     (int)geo->M, gS, (int)geo->N, (float2*)gp);
+  if (geo->M > 0) {
+    const dim3 grid(xcd_grid((geo->N + kPairBlock / kBwdParts - 1) / (kPairBlock / kBwdParts))), block(kPairBlock);
+    switch (K) {
+#define ATL_K(k) case k: hipLaunchKernelGGL(k_fast_bwd_traj<k>, grid, block, 0, stream, p, G, (int)geo->N, coef, tab, (float2*)gp, gcoef); break;
+      ATL_K(1) ATL_K(2) ATL_K(3) ATL_K(4) ATL_K(5) ATL_K(6) ATL_K(7) ATL_K(8) ATL_K(9) ATL_K(10) ATL_K(11) ATL_K(12)
+#undef ATL_K
+    }
+  }
+  return check_launch("fast_pair_bwd_traj");
 }
 
 }  // extern "C"

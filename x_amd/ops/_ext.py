@@ -40,7 +40,7 @@ _SIGS = {
     "atl_sample_grid_bwd": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_sample_grid_bwd_pos": [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_field_channels_last": [_P, _I, _I, _I, _I, _P, _P],
-    "atl_traj_displacement": [_P, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P, _P],
+    "atl_traj_displacement": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P, _P],
     "atl_traj_gout": [_P, _P, _I, _I, _I, _P, _P],
     "atl_sample_grid_fwd_cl": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_sample_grid_bwd_pos_cl": [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
@@ -77,10 +77,13 @@ _SIGS = {
     "atl_fast_plan": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P],
     "atl_fast_pair_fwd": [_P, _P, _P, _P, _P],
     "atl_fast_pair_bwd": [_P, _P, _P, _P, _P],
+    "atl_fast_plan_traj": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P],
+    "atl_fast_pair_bwd_traj": [_P, _P, _P, _P, _I, _P, _P, _P, _P],
 }
 _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.c_int64,
             "atl_tile_ws_bytes": ctypes.c_int64, "atl_splat_gauss_ws_bytes": ctypes.c_int64,
-            "atl_anchored_score_mean_scratch_bytes": ctypes.c_int64, "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
+            "atl_anchored_score_mean_scratch_bytes": ctypes.c_int64,
+"atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):
     """Mirror of ``atl_fast_geometry`` (include/atl_hip.h): sizes, grid and workspace layout of the fused
@@ -132,7 +135,7 @@ _TIMED = {}          # entry point -> list of (start, end, events) per timed cal
 _EVERY = {"n": 1, "calls": {}}   # time one call in n of each entry point
 # position of the event count N in the arguments of the entry points whose calls are sized by it
 _NARG = {"atl_sample_grid_fwd": 7, "atl_sample_grid_bwd_planned": 6, "atl_sample_grid_bwd_pos": 8,
-         "atl_sample_grid_fwd_cl": 7, "atl_sample_grid_bwd_pos_cl": 8, "atl_traj_displacement": 8,
+         "atl_sample_grid_fwd_cl": 7, "atl_sample_grid_bwd_pos_cl": 8, "atl_traj_displacement": 9,
          "atl_traj_gout": 2,
          "atl_splat_gauss_fwd": 3, "atl_splat_gauss_bwd": 4, "atl_splat_gauss_fwd_ws": 3,
          "atl_gather_bilinear_fwd": 3, "atl_gather_bilinear_bwd_ws": 4, "atl_splat_bilinear_fwd_ws": 3,

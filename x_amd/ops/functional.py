@@ -104,25 +104,27 @@ def gather(img: torch.Tensor, pos: torch.Tensor, b: torch.Tensor) -> torch.Tenso
 
 # ------------------------------------------------------------------------------------------- blur
 def gaussian_kernel1d(sigma: float, device, dtype=torch.float32):
-    """Normalised 1-D Gaussian kernel of radius ceil(3 sigma) (atl/ops/functional.py:91-96)."""
+    """Normalised Gaussian taps exp(-x^2 / 2 sigma^2) at x = -r..r, r = max(ceil(3 sigma), 1)
+    (atl/ops/functional.py:91-96)."""
     r = max(int(math.ceil(3 * sigma)), 1)
-    x = torch.arange(-r, r + 1, device=device, dtype=dtype)
-    k = torch.exp(-x * x / (2 * sigma * sigma))
-    return k / k.sum()
+    x = torch.linspace(-r, r, 2 * r + 1, device=device, dtype=dtype)
+    taps = torch.exp(-(x * x) / (2 * sigma * sigma))
+    return taps / taps.sum()
 
 
 def blur(img: torch.Tensor, sigma: float) -> torch.Tensor:
-    """Separable Gaussian blur of a (B, H, W) or (B, C, H, W) image, zero padding (functional.py:99-110)."""
+    """Separable Gaussian blur of a (B, H, W) or (B, C, H, W) image with zero padding (atl/ops/functional.py:
+    99-110): one 1-D pass along the rows, one along the columns, each a conv1d over every image line."""
     if sigma <= 0:
         return img
-    squeeze = img.dim() == 3
-    x = img[:, None] if squeeze else img
-    C = x.shape[1]
-    k = gaussian_kernel1d(sigma, img.device, img.dtype)
-    r = (k.numel() - 1) // 2
-    x = torch.nn.functional.conv2d(x, k.view(1, 1, 1, -1).expand(C, 1, 1, -1), padding=(0, r), groups=C)
-    x = torch.nn.functional.conv2d(x, k.view(1, 1, -1, 1).expand(C, 1, -1, 1), padding=(r, 0), groups=C)
-    return x[:, 0] if squeeze else x
+    taps = gaussian_kernel1d(sigma, img.device, img.dtype).view(1, 1, -1)
+    r = (taps.shape[-1] - 1) // 2
+    H, W = img.shape[-2:]
+    lead = img.shape[:-2]
+    along_w = torch.nn.functional.conv1d(img.reshape(-1, 1, W), taps, padding=r).view(*lead, H, W)
+    cols = along_w.transpose(-1, -2).reshape(-1, 1, H)
+    along_h = torch.nn.functional.conv1d(cols, taps, padding=r).view(*lead, W, H)
+    return along_h.transpose(-1, -2).contiguous()
 
 
 # ------------------------------------------------------------------------------------------- flow grid
@@ -212,7 +214,8 @@ class _TrajDisplacement(torch.autograd.Function):
         with torch.cuda.device(gpos.device):
             st = stream_of(gpos)
             call("atl_field_channels_last", ptr(fld), B, C, Hg, Wg, ptr(fcl), st)
-            call("atl_traj_displacement", ptr(fcl), B, K, Hg, Wg, ptr(gpos), ptr(b), ptr(t), N, basis, ptr(out), st)
+            call("atl_traj_displacement", ptr(fcl), B, C, K, Hg, Wg, ptr(gpos), ptr(b), ptr(t), N, basis, ptr(out),
+                 st)
             if plan and _tile_plan_ok(B, C, Hg, Wg):
                 nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N))
                 if nbytes >= 0:
@@ -249,20 +252,41 @@ class _TrajDisplacement(torch.autograd.Function):
 
 
 TRAJ_MAX_K = 16
+TRAJ_BASES = {"polynomial": 0, "bezier": 1, "bspline": 2}
+
+
+def _check_events(pos, b, *per_event, what):
+    """Shape checks of a device op's event arrays, before any launch: pos (N, 2), b and every per-event
+    array (N,)."""
+    if pos.dim() != 2 or pos.shape[1] != 2:
+        raise ValueError(f"{what}: positions must be (N, 2), got {tuple(pos.shape)}")
+    n = pos.shape[0]
+    if b.shape != (n,):
+        raise ValueError(f"{what}: batch index must be ({n},), got {tuple(b.shape)}")
+    for a in per_event:
+        if a.shape != (n,):
+            raise ValueError(f"{what}: per-event array must be ({n},), got {tuple(a.shape)}")
 
 
 def traj_displacement(fld: torch.Tensor, gpos: torch.Tensor, b: torch.Tensor, t: torch.Tensor, K: int,
                       basis: str) -> torch.Tensor:
     """Displacement (N, 2) in (x, y) of trajectories with coefficient grid ``fld`` (B, 2K, Hg, Wg), channels
-    [y_1..y_K, x_1..x_K], at grid coordinates ``gpos``; ``basis`` "polynomial" or "bezier".  Device tensors,
-    K <= TRAJ_MAX_K."""
+    [y_1..y_K, x_1..x_K], at grid coordinates ``gpos``; ``basis`` "polynomial", "bezier" or "bspline" (the
+    clamped uniform B-spline of degree min(3, K) with K + 1 functions, the first pinned to the start).  Device
+    tensors, K <= TRAJ_MAX_K."""
     get_ext()
-    if basis not in ("polynomial", "bezier"):
+    if basis not in TRAJ_BASES:
         raise ValueError(f"unknown basis {basis!r}")
     if t.requires_grad:
         raise ValueError("traj_displacement: event times carry no gradient")
+    if not 1 <= int(K) <= TRAJ_MAX_K:
+        raise ValueError(f"traj_displacement: K = {K} outside 1..{TRAJ_MAX_K}")
+    if fld.dim() != 4 or fld.shape[1] != 2 * int(K):
+        raise ValueError(f"traj_displacement: coefficient grid must be (B, 2K = {2 * int(K)}, Hg, Wg), got "
+                         f"{tuple(fld.shape)}")
+    _check_events(gpos, b, t, what="traj_displacement")
     plan = fld.requires_grad and torch.is_grad_enabled()
-    return _TrajDisplacement.apply(fld, gpos, b, t, int(K), int(basis == "bezier"), plan)
+    return _TrajDisplacement.apply(fld, gpos, b, t, int(K), TRAJ_BASES[basis], plan)
 
 
 def sample_grid_hip(fld: torch.Tensor, pos: torch.Tensor, b: torch.Tensor, img_hw=(0, 0)) -> torch.Tensor:
@@ -270,6 +294,9 @@ def sample_grid_hip(fld: torch.Tensor, pos: torch.Tensor, b: torch.Tensor, img_h
     when ``img_hw`` = (H, W) is given (DenseLinearFlow.field).  Differentiable w.r.t. the field and the
     positions."""
     get_ext()
+    if fld.dim() != 4:
+        raise ValueError(f"sample_grid: field must be (B, C, Hg, Wg), got {tuple(fld.shape)}")
+    _check_events(pos, b, what="sample_grid")
     plan = fld.requires_grad and torch.is_grad_enabled()     # sort the positions for a gather backward
     return _SampleGrid.apply(fld, pos, b, img_hw[0], img_hw[1], plan)
 
@@ -451,18 +478,37 @@ class _ATSPair(torch.autograd.Function):
 class FastPairPlan:
     """Device workspace of the fused pair-sum path (include/atl_hip.h, atl_fast_*): the reference's (source,
     slice) entries and the anchors binned on a fixed fine-cell grid, built without a host synchronisation.
-    Holds its inputs alive for as long as it is used."""
+    Holds its inputs alive for as long as it is used.
 
-    def __init__(self, x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, anchor_xy=None):
+    ``traj=(coef, K, table)`` selects the trajectory source model: ``x`` are then the trajectory starts p (N, 2),
+    ``coef`` the (N, 2K) coefficient rows and ``table`` the (S, 2K) basis at the slice centres; ``v`` is unused
+    (pass None) and ``anchor_xy`` is required (the anchors are not at the starts)."""
+
+    def __init__(self, x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, anchor_xy=None, traj=None):
         dev = x.device
-        self.x, self.t, self.v = _f32(x), _f32(t), _f32(v.detach())
+        self.x, self.t = _f32(x), _f32(t)
         self.b = b.contiguous().long()
         self.anchors = None if anchors is None else anchors.contiguous().long()   # None: every event, in order
         self.anchor_xy = None if anchor_xy is None else _f32(anchor_xy.detach())
         N = self.t.shape[0]
         M = N if self.anchors is None else self.anchors.shape[0]
-        if self.x.shape != (N, 2) or self.v.shape != (N, 2) or self.b.shape != (N,):
-            raise ValueError("x, v must be (N, 2) and t, b (N,)")
+        self.traj = traj is not None
+        if self.traj:
+            coef, K, table = traj
+            self.K = int(K)
+            self.coef, self.table = _f32(coef.detach()), _f32(table)
+            if self.coef.shape != (N, 2 * self.K) or self.table.shape != (int(n_slices), 2 * self.K):
+                raise ValueError(f"trajectory pair sums: coef must be ({N}, {2 * self.K}) and table "
+                                 f"({int(n_slices)}, {2 * self.K})")
+            if self.anchor_xy is None:
+                raise ValueError("trajectory pair sums need anchor_xy (the anchors are not at the trajectory starts)")
+            self.v = None
+        else:
+            self.v = _f32(v.detach())
+            if self.v.shape != (N, 2):
+                raise ValueError("x, v must be (N, 2) and t, b (N,)")
+        if self.x.shape != (N, 2) or self.b.shape != (N,):
+            raise ValueError("x must be (N, 2) and t, b (N,)")
         if self.anchor_xy is not None and self.anchor_xy.shape != (M, 2):
             raise ValueError("anchor_xy must be (M, 2)")
         self.N, self.M, self.device = N, M, dev
@@ -473,8 +519,13 @@ class FastPairPlan:
             raise HipLibraryError("atl_fast_geometry_init: " + lib.atl_last_error().decode(errors="replace"))
         self.ws = torch.empty(int(self.geo.ws_bytes), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
-            call("atl_fast_plan", ctypes.byref(self.geo), ptr(self.x), ptr(self.t), ptr(self.v), ptr(self.b),
-                 ptr(self.anchors), ptr(self.anchor_xy), ptr(self.ws), int(self.geo.ws_bytes), stream_of(self.x))
+            if self.traj:
+                call("atl_fast_plan_traj", ctypes.byref(self.geo), ptr(self.x), ptr(self.coef), self.K,
+                     ptr(self.table), ptr(self.t), ptr(self.b), ptr(self.anchors), ptr(self.anchor_xy), ptr(self.ws),
+                     int(self.geo.ws_bytes), stream_of(self.x))
+            else:
+                call("atl_fast_plan", ctypes.byref(self.geo), ptr(self.x), ptr(self.t), ptr(self.v), ptr(self.b),
+                     ptr(self.anchors), ptr(self.anchor_xy), ptr(self.ws), int(self.geo.ws_bytes), stream_of(self.x))
 
     def forward(self, count: Optional[torch.Tensor] = None) -> torch.Tensor:
         out = torch.zeros(self.M, dtype=F32, device=self.device)
@@ -482,14 +533,33 @@ class FastPairPlan:
             call("atl_fast_pair_fwd", ctypes.byref(self.geo), ptr(self.ws), ptr(out), ptr(count), stream_of(out))
         return out
 
-    def backward(self, gS: torch.Tensor) -> torch.Tensor:
+    def _check_gs(self, gS):
         gS = _f32(gS)
         if gS.shape != (self.M,):
             raise ValueError(f"gS has shape {tuple(gS.shape)}, expected ({self.M},)")
+        return gS
+
+    def backward(self, gS: torch.Tensor) -> torch.Tensor:
+        """Linear model: dL/dv (N, 2)."""
+        if self.traj:
+            raise ValueError("a trajectory plan has backward_traj")
+        gS = self._check_gs(gS)
         gv = torch.empty(self.N, 2, dtype=F32, device=self.device)
         with torch.cuda.device(self.device):
             call("atl_fast_pair_bwd", ctypes.byref(self.geo), ptr(self.ws), ptr(gS), ptr(gv), stream_of(gv))
         return gv
+
+    def backward_traj(self, gS: torch.Tensor):
+        """Trajectory model: (dL/dp (N, 2), dL/dcoef (N, 2K))."""
+        if not self.traj:
+            raise ValueError("a linear plan has backward")
+        gS = self._check_gs(gS)
+        gp = torch.empty(self.N, 2, dtype=F32, device=self.device)
+        gc = torch.empty(self.N, 2 * self.K, dtype=F32, device=self.device)
+        with torch.cuda.device(self.device):
+            call("atl_fast_pair_bwd_traj", ctypes.byref(self.geo), ptr(self.ws), ptr(gS), ptr(self.coef), self.K,
+                 ptr(self.table), ptr(gp), ptr(gc), stream_of(gp))
+        return gp, gc
 
     def counts(self) -> torch.Tensor:
         """n_i: number of contributing pairs of every anchor (bit-identical to the reference's visits)."""
@@ -525,6 +595,51 @@ def ats_pair_sums(x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, fo
     get_ext()
     return _ATSPairFast.apply(v.float(), x.detach(), t.detach(), b, anchors, anchor_xy, int(B), int(H), int(W),
                               float(h), float(tau), float(cut), int(n_slices))
+
+
+class _ATSPairTraj(torch.autograd.Function):
+    """Pair sums of the trajectory model: gradients to the trajectory starts p and the coefficient rows."""
+
+    @staticmethod
+    def forward(ctx, p, coef, t, b, anchors, anchor_xy, B, H, W, h, tau, cut, n_slices, K, table):
+        plan = FastPairPlan(p.detach(), t, None, b, B, H, W, anchors, h, tau, cut, n_slices, anchor_xy,
+                            traj=(coef, K, table))
+        ctx.plan = plan
+        return plan.forward()
+
+    @staticmethod
+    def backward(ctx, g):
+        gp, gc = ctx.plan.backward_traj(g)
+        return (gp, gc) + (None,) * 13
+
+
+TRAJ_PAIR_MAX_K = 12
+
+
+def ats_pair_sums_traj(p, coef, t, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, anchor_xy=None, K=None,
+                       table=None):
+    """Anchored pair sums for trajectory motion (no counterpart in the reference, whose exact pair sums need
+    motion linear at the event, atl/objectives/ats.py:77-78).  Source j moves on its trajectory
+    q_j(c) = p_j + sum_k coef_jk g_k(c); seen from an anchor i of slice s (c_s its centre, at_i = t_i - c_s) it
+    sits at q_j(c_s) + q_j'(c_s) at_i, the trajectory linearised at the slice centre (exact for straight
+    trajectories, where the sum is the reference's).  S_i sums exp(-|x_i - that|^2 / 2h^2) over j != i of the
+    same batch with |t_i - t_j| <= tau and distance <= cut h (the reference's tests, fp32 order).
+    ``coef`` (N, 2K) rows [y_1..y_K, x_1..x_K], ``table`` (S, 2K) = [g_k(c_s), g_k'(c_s)], ``anchor_xy``
+    (M, 2) the anchor positions (required).  Gradients flow to ``p`` and ``coef``.  CPU tensors: the O(MN)
+    torch reference."""
+    if anchor_xy is None:
+        raise ValueError("ats_pair_sums_traj needs anchor_xy")
+    K = int(K if K is not None else coef.shape[1] // 2)
+    if not ext_supports(p):
+        if anchors is None:
+            anchors = torch.arange(p.shape[0], device=p.device)
+        return ref.ats_pair_sums_traj(p.float(), coef.float(), t.float(), b, anchors, anchor_xy.float(), h, tau,
+                                      cut, int(n_slices), table.float())
+    if not 1 <= K <= TRAJ_PAIR_MAX_K:
+        raise ValueError(f"ats_pair_sums_traj: K = {K} outside 1..{TRAJ_PAIR_MAX_K}")
+    get_ext()
+    return _ATSPairTraj.apply(p.float(), coef.float(), t.detach(), b, anchors, anchor_xy, int(B), int(H), int(W),
+                              float(h), float(tau), float(cut), int(n_slices), K, table)
 
 
 def pair_counts(plan: PairPlan, h, tau, cut) -> torch.Tensor:

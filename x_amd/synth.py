@@ -58,7 +58,7 @@ def smooth_flow(rng, H, W, sigma=40.0, vmax=20.0, B=1):
 
 
 def _bilinear_np(field, x, y):
-    """Bilinear lookup of a (2, H, W) field at float positions (clamped to the grid), float64."""
+    """Bilinear lookup of a (C, H, W) field at float positions (clamped to the grid): (N, C) float64."""
     H, W = field.shape[-2:]
     x = np.clip(x, 0, W - 1)
     y = np.clip(y, 0, H - 1)
@@ -171,34 +171,58 @@ def small_window(seed=0, n=3000, H=40, W=48, vmax=6.0, B=1, scene="segments") ->
     return Window(xy=xy, t=t, p=p, b=b, height=H, width=W, batch_size=B, motion={"kind": "dense", "grid": grid})
 
 
-def trajectory_coeffs(rng, B, K, H, W, tile=4, sigma_px=40.0, dmax=20.0):
-    """(B, 2K, H, W) f32 smooth random trajectory coefficients [y_1..y_K, x_1..x_K] for PixelTrajectories:
-    N(0, 1) filtered at tile resolution (sigma = sigma_px / tile tiles, mode='reflect'), scaled so that the
-    largest per-tile coefficient vector has norm dmax px; each tile's value fills its tile x tile block."""
+def trajectory_coeffs(rng, B, K, H, W, sigma_px=40.0, dmax=5.0):
+    """(B, 2K, H, W) f32 per-pixel trajectory coefficients (control points) [y_1..y_K, x_1..x_K]: every channel
+    N(0, 1) Gaussian-filtered (sigma = sigma_px, mode='reflect'), scaled so that the largest coefficient
+    displacement norm is dmax px."""
     from scipy.ndimage import gaussian_filter
-    Hq, Wq = -(-H // tile), -(-W // tile)
-    g = rng.standard_normal((B, 2 * K, Hq, Wq))
+    g = rng.standard_normal((B, 2 * K, H, W))
     for k in range(B):
         for c in range(2 * K):
-            g[k, c] = gaussian_filter(g[k, c], sigma=sigma_px / tile, mode="reflect", truncate=4.0)
-    mag = np.sqrt(g[:, :K] ** 2 + g[:, K:] ** 2).max()
-    g *= dmax / mag
-    full = np.repeat(np.repeat(g, tile, axis=2), tile, axis=3)[:, :, :H, :W]
-    return np.ascontiguousarray(full.astype(F32))
+            g[k, c] = gaussian_filter(g[k, c], sigma=sigma_px, mode="reflect", truncate=4.0)
+    g *= dmax / np.sqrt(g[:, :K] ** 2 + g[:, K:] ** 2).max()
+    return np.ascontiguousarray(g.astype(F32))
 
 
-def trajectory_windows(seed=0, B=4, n=500_000, H=480, W=640, K=10) -> Window:
-    """B windows of n events each (640x480, 25 ms per window, 50 segments + 30% noise moving under a smooth
-    dense flow of at most 20 px/window), packed and sorted by (b, t), plus the coefficients of degree-K
-    pixel trajectories (``motion["coeffs"]``, (B, 2K, H, W), largest coefficient norm 20 px)."""
+def _trajectory_window(rng, n, H, W, coef, K, scene="segments", n_objects=50, noise=0.3, duration=0.025):
+    """One window of n events on per-pixel B-spline trajectories: scene points p at t = 0 (segments), each event
+    at q(p, t) = p + sum_k c_k(p) N_k(t) (coefficients bilinear at p, border clamp), rounded to the pixel grid,
+    redrawn while outside the sensor; uniform noise events on top."""
+    from .motion.trajectories import basis_table
+    n_sig = int(round(n * (1 - noise)))
+    xs, ts = [], []
+    need = n_sig
+    while need > 0:
+        m = int(need * 1.3) + 16
+        p = _scene_points(rng, m, W, H, scene, n_objects, 8.0)
+        t = rng.uniform(0, 1, m)
+        c = _bilinear_np(coef, p[:, 0], p[:, 1])                 # (m, 2K) control points at p
+        g, _ = basis_table(t, K, "bspline")
+        x = p + np.stack([(c[:, K:] * g).sum(1), (c[:, :K] * g).sum(1)], 1)
+        x = np.round(x)
+        ok = (x[:, 0] >= 0) & (x[:, 0] <= W - 1) & (x[:, 1] >= 0) & (x[:, 1] <= H - 1)
+        xs.append(x[ok][:need])
+        ts.append(t[ok][:need])
+        need -= xs[-1].shape[0]
+    n_noise = n - n_sig
+    xs.append(np.stack([rng.integers(0, W, n_noise), rng.integers(0, H, n_noise)], 1).astype(np.float64))
+    ts.append(rng.uniform(0, 1, n_noise))
+    x, t = np.concatenate(xs), np.concatenate(ts).astype(F32)
+    order = np.argsort(t, kind="stable")
+    pol = np.where(rng.uniform(0, 1, n) < 0.5, 1.0, -1.0).astype(F32)
+    return x[order].astype(F32), t[order], pol
+
+
+def bspline_windows(seed=0, B=4, n=500_000, H=480, W=640, K=10) -> Window:
+    """Continuous-time trajectory workload: B windows of n events (640x480, 25 ms each, 50 segments + 30%
+    noise) packed in one packet sorted by (b, t), moving on per-pixel cubic B-spline trajectories with K = 10
+    control points per axis (the start pinned), (B, 2K, H, W) smooth random control points (sigma 40 px) of
+    largest displacement 5 px = 200 px/s over 25 ms (``motion["coeffs"]``)."""
     rng = np.random.default_rng(seed)
-    parts = []
-    for k in range(B):
-        grid = smooth_flow(rng, H, W, sigma=40.0, vmax=20.0)
-        parts.append(make_window(n, H, W, {"kind": "dense", "grid": grid}, "segments", 50, 0.3, duration=0.025,
-                                 rng=rng))
-    coeffs = trajectory_coeffs(rng, B, K, H, W)
-    return Window(xy=np.concatenate([w.xy for w in parts]), t=np.concatenate([w.t for w in parts]),
-                  p=np.concatenate([w.p for w in parts]),
-                  b=np.concatenate([np.full(w.n, k, np.int64) for k, w in enumerate(parts)]), height=H, width=W,
-                  batch_size=B, duration=0.025, motion={"kind": "trajectories", "coeffs": coeffs, "K": K})
+    coef = trajectory_coeffs(rng, B, K, H, W)
+    parts = [_trajectory_window(rng, n, H, W, coef[k], K) for k in range(B)]
+    return Window(xy=np.ascontiguousarray(np.concatenate([w[0] for w in parts])),
+                  t=np.ascontiguousarray(np.concatenate([w[1] for w in parts])),
+                  p=np.concatenate([w[2] for w in parts]),
+                  b=np.concatenate([np.full(n, k, np.int64) for k in range(B)]), height=H, width=W, batch_size=B,
+                  duration=0.025, motion={"kind": "bspline", "coeffs": coef, "K": K})
