@@ -57,6 +57,14 @@ int atl_splat_bilinear_fwd_ws(const float* pos, const float* w, const int64_t* b
 int atl_gather_bilinear_bwd_ws(const float* gval, const float* img, const float* pos, const int64_t* b, int64_t N,
                                int64_t B, int64_t H, int64_t W, float* gimg, float* gpos, void* ws, int64_t ws_bytes,
                                hipStream_t stream);
+/* No counterpart in the reference: the tile-binned splat forward of atl_splat_bilinear_fwd_ws for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It allocates nothing: its workspace is a 64 MiB array held by the library on every GPU it runs on
+ * (until the process ends), which fits atl_tile_ws_bytes(N, B, H, W) <= 64 MiB (about 3.9M events at 640x480,
+ * B = 1); larger calls fail with status 1 and a message.  img (B,H,W) is accumulated, as by the _ws form.
+ * Calls that overlap on one GPU share the array and race. */
+int atl_splat_bilinear_fwd_noalloc(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B,
+                                   int64_t H, int64_t W, float* img, hipStream_t stream);
 /* The Gaussian splat forward with the same tile engine (tiles of the rounded centres, an LDS window of
  * T + 2R pixels per tile); R <= 8.  ws: atl_splat_gauss_ws_bytes(N, B, H, W, R) bytes (-1: unsupported). */
 int64_t atl_splat_gauss_ws_bytes(int64_t N, int64_t B, int64_t H, int64_t W, int64_t R);

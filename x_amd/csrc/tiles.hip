@@ -19,6 +19,7 @@
 #include "../../include/atl_hip.h"
 
 #include <cmath>
+#include <mutex>
 
 using namespace atlhip;
 
@@ -586,6 +587,39 @@ void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const flo
                        (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, out);
 }
 
+// Scratch of atl_splat_bilinear_fwd_noalloc: the tile engine's workspace (counts, offsets, records) for callers
+// that cannot allocate device memory.  Every GPU the library runs on holds its own copy until the process ends.
+// Host code never passes the array's name to a kernel (on the host it is a stand-in, not a device address): the
+// address of this device's copy is looked up once per device with hipGetSymbolAddress and kept in g_scratch_ptr.
+// Each call rewrites every byte of it that its kernels read (counts by the histogram pass, offsets by the scan,
+// records by the scatter), so nothing needs clearing; calls that overlap on one GPU share it and race.
+constexpr int64_t kNoAllocScratchBytes = 64ll << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+int noalloc_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("splat_bilinear_fwd_noalloc: no current device");
+    return 1;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("splat_bilinear_fwd_noalloc: hipGetSymbolAddress of the scratch array failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return 1;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 }  // namespace
 
 // ================================================================================================ C-ABI
@@ -608,6 +642,27 @@ int atl_splat_bilinear_fwd_ws(const float* pos, const float* w, const int64_t* b
   tile_bin<kImage>(g, L, ws, pos, b, w, stream);
   tile_accum<kImage, 1>(g, L, ws, nullptr, img, stream);
   return check_launch("splat_bilinear_fwd_ws");
+}
+
+int atl_splat_bilinear_fwd_noalloc(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B,
+                                   int64_t H, int64_t W, float* img, hipStream_t stream) {
+  if (N < 0 || B < 0 || H < 0 || W < 0) { set_error("splat_bilinear_fwd_noalloc: bad sizes"); return 1; }
+  if (N == 0 || B == 0) return 0;
+  TileGeo g;
+  if (!tile_geo(kImage, B, H, W, N, 0, 0, g)) { set_error("splat_bilinear_fwd_noalloc: unsupported sizes N=%lld B=%lld H=%lld W=%lld", (long long)N, (long long)B, (long long)H, (long long)W); return 1; }
+  const TileLayout L = tile_layout(g);
+  if (L.bytes > kNoAllocScratchBytes) {
+    set_error("splat_bilinear_fwd_noalloc: N=%lld B=%lld H=%lld W=%lld needs %lld bytes of scratch, more than the "
+              "library's %lld (use atl_splat_bilinear_fwd_ws with a workspace)", (long long)N, (long long)B,
+              (long long)H, (long long)W, (long long)L.bytes, (long long)kNoAllocScratchBytes);
+    return 1;
+  }
+  if (!pos || !w || !b || !img) { set_error("splat_bilinear_fwd_noalloc: null argument"); return 1; }
+  void* ws = nullptr;
+  if (noalloc_scratch(&ws) != 0) return 1;
+  tile_bin<kImage>(g, L, ws, pos, b, w, stream);
+  tile_accum<kImage, 1>(g, L, ws, nullptr, img, stream);
+  return check_launch("splat_bilinear_fwd_noalloc");
 }
 
 int atl_gather_bilinear_bwd_ws(const float* gval, const float* img, const float* pos, const int64_t* b, int64_t N,

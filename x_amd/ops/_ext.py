@@ -70,6 +70,7 @@ _SIGS = {
     "atl_splat_gauss_ws_bytes": [_I, _I, _I, _I, _I],
     "atl_splat_gauss_fwd_ws": [_P, _P, _P, _I, _I, _I, _I, _D, _I, _P, _P, _I, _P],
     "atl_splat_bilinear_fwd_ws": [_P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P],
+    "atl_splat_bilinear_fwd_noalloc": [_P, _P, _P, _I, _I, _I, _I, _P, _P],
     "atl_gather_bilinear_bwd_ws": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P],
     "atl_grid_plan": [_I, _I, _I, _P, _P, _I, _I, _I, _P, _I, _P],
     "atl_sample_grid_bwd_planned": [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _P],
