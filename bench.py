@@ -17,6 +17,10 @@ Other workloads (parity-test configurations, not the headline metric), same outp
     python bench.py --workload iwe-plumbing    # the same on 100k events 240x180, constant flow (2, -1.25)
     python bench.py --workload anchored-blobs  # contention stress: the anchored score on 4M events, 90% in 5
                                                # Gaussian blobs (sigma 8 px), Sim2 flow (0, 0, 0.1, 0.1)
+    python bench.py --workload mpcm-lut        # MotionPriorCMax's look-up table at its DSEC configuration: 15
+                                               # time bins x 19200 cells of 4 px (640x480), the 32 nearest of
+                                               # 19200 tile trajectories (K = 10 B-spline) per cell and bin,
+                                               # their mean displacement to t_ref, backward to the coefficients
     python bench.py --workload trajectories    # 4 windows x 500k events 640x480 (25 ms each), per-pixel cubic
                                                # B-spline trajectories with 10 control points: anchored
                                                # pair-sum score (h 1, tau 20 ms = 0.8, 16 slices) + the IWE
@@ -65,7 +69,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", default="anchored",
-                    choices=["anchored", "anchored-blobs", "iwe", "iwe-plumbing", "trajectories"])
+                    choices=["anchored", "anchored-blobs", "iwe", "iwe-plumbing", "trajectories", "mpcm-lut"])
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--sigma", type=float, default=1.0)
@@ -506,6 +510,73 @@ def trajectories_cpu_baseline(win, budget):
     return _baseline_line(O, n, int((win.b == 0).sum()), dt, "the trajectory step (window 0)")
 
 
+# ------------------------------------------------------------------------------ MotionPriorCMax look-up table
+def mpcm_lut_main(a, dev):
+    """MotionPriorCMaxLoss.lut_flow at the reference's DSEC configuration (atl/objectives/mpcm.py:4-7): 480x640,
+    4 px cells, tile-4 trajectories (K = 10 cubic B-splines from a smooth random coefficient grid), 15 bins,
+    32 neighbours; one step = the table and the backward of its sum of squares to the coefficient grid."""
+    from x_amd.motion import PixelTrajectories
+    from x_amd.objectives import MotionPriorCMaxLoss
+    from x_amd.ops import _ext
+    g = torch.Generator().manual_seed(0)
+    c = torch.nn.functional.avg_pool2d(torch.randn(1, 20, 480, 640, generator=g), 31, 1, 15, count_include_pad=False)
+    coef = (c / c.abs().amax() * 25.0).to(dev).requires_grad_(True)
+    loss = MotionPriorCMaxLoss()
+    t_ref = torch.tensor(0.37, device=dev)
+
+    def step():
+        coef.grad = None
+        table, _ = loss.lut_flow(PixelTrajectories(coef, 10, "bspline", tile=4), 480, 640, t_ref)
+        table.square().sum().backward()
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    rec = _ext.time_kernels(["atl_knn_indices"], every=1)
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    kms = float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec["atl_knn_indices"]]))
+    _ext.time_kernels(())
+    P, Q, n, k = 15, 120 * 160, 120 * 160, 32
+    # algorithmic bytes of the KNN entry point: the points (8 B each) and queries (8 B) read, the indices written
+    nbytes = P * n * 8 + Q * 8 + P * Q * k * 8
+    line = {
+        "metric": "look-up-table queries/s for MotionPriorCMax's KNN table fwd+bwd (15 bins x 19200 cells, k=32, "
+                  "19200 trajectories); % HBM roofline of the KNN pass",
+        "value": P * Q * a.steps / dt, "unit": "queries/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": 1e3 * dt / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "MotionPriorCMaxLoss.lut_flow, 640x480, lut 4, PixelTrajectories(K=10, bspline, tile 4), "
+                               "15 bins, 32 neighbours, backward to the (1, 20, 480, 640) coefficients",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "atl_knn_indices", "achieved": nbytes / (kms * 1e-3) / 1e9,
+                     "peak": 8000.0, "unit": "GB/s", "frac": nbytes / (kms * 1e-3) / 8e12, "traffic": None,
+                     "kernel_ms": kms, "algorithmic_bytes": nbytes},
+    }
+    if not a.no_cpu:
+        O = _oracle()
+        with torch.no_grad():
+            m = PixelTrajectories(coef.detach().cpu(), 10, "bspline", tile=4)
+            edges = torch.linspace(0, 1, 16)
+            pts = m.tile_trajectories((edges[:-1] + edges[1:]) * 0.5)[0].numpy()
+        q = loss.cell_centres(480, 640, "cpu").numpy()
+        nq, t0 = 256, time.perf_counter()
+        while True:
+            O.knn_indices(q[:nq], pts[:1], k)
+            el = time.perf_counter() - t0
+            if el > a.cpu_budget / 4 or nq >= Q:
+                break
+            nq, t0 = min(Q, nq * 2), time.perf_counter()
+        line["cpu_baseline"] = dict({"value": nq / el, "unit": "queries/s", "cores": 1, "kind": "port",
+                                     "sample": f"the oracle's brute-force KNN (NumPy, one thread) of {nq} cells on "
+                                               f"one bin's 19200 trajectories, {el:.2f} s (the table's gather and "
+                                               f"backward not included)"}, **_host_cpu())
+    print(json.dumps(line), flush=True)
+
+
 def main():
     a = parse()
     if a.summarize:
@@ -518,10 +589,10 @@ def main():
         print(f"bench.py measures one GPU only (asked for {a.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
         sys.exit(2)
-    if a.workload.startswith("iwe") or a.workload == "trajectories":
+    if a.workload.startswith("iwe") or a.workload in ("trajectories", "mpcm-lut"):
         dev = torch.device("cuda:0")
         torch.cuda.set_device(dev)
-        (iwe_main if a.workload.startswith("iwe") else trajectories_main)(a, dev)
+        {"trajectories": trajectories_main, "mpcm-lut": mpcm_lut_main}.get(a.workload, iwe_main)(a, dev)
         return
     from x_amd.objectives import AnchoredExact
     from x_amd.ops import _ext

@@ -280,6 +280,17 @@ int atl_anchored_score_mean_fwd(const float* S, const float* wc, const float* vi
 int atl_anchored_score_mean_bwd(const float* g, const float* q, const float* D, int64_t M, float* gS,
                                 hipStream_t stream);
 
+/* ---------------------------------------------------------------- MotionPriorCMax look-up table
+ * knn_indices (atl/objectives/mpcm.py:30-42): for every plane p < P and query q < Q, the k nearest of the plane's n
+ * points (points (P, n, 2), queries (Q, 2) shared by the planes); idx (P, Q, k) int64 written, in the order
+ * (squared distance (qx - px)^2 + (qy - py)^2 with each fp32 operation rounded, then lower index).  1 <= k <=
+ * min(n, 32).  Points with a non-finite distance are never selected (a slot without a point holds -1).  The
+ * reference's dense cdist + topk is replaced by a grid-binned ring search.  ws: atl_knn_ws_bytes(P, n) bytes (-1:
+ * too many cells for 32-bit indices). */
+int64_t atl_knn_ws_bytes(int64_t P, int64_t n);
+int atl_knn_indices(const float* queries, int64_t Q, const float* points, int64_t P, int64_t n, int64_t k,
+                    int64_t* idx, void* ws, int64_t ws_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

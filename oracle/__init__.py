@@ -15,6 +15,8 @@ Two halves:
 * The trajectory pair sums (no reference implementation: the reference's exact pair sums refuse trajectory
   motion): a basis table from library routines (scipy's BSpline), the plan's fp32 entries and an fp64 brute
   force with gradients.
+* MotionPriorCMax's look-up table (atl/objectives/mpcm.py:30-42,73-77): brute-force k nearest neighbours by a
+  stable sort of fp32 squared distances, and the table's mean.
   NumPy evaluates every fp32 operation separately with IEEE rounding and never fuses, which reproduces
   torch's CPU op-by-op rounding; Python scalars are rounded to fp32 first, as torch does when it combines
   them with fp32 tensors.
@@ -654,3 +656,32 @@ def make_iwe(xy_ref, t, p, b, B, H, W, t_ref, kernel="bilinear", sigma=1.0, pola
     if kernel == "gauss":
         return splat_gauss_fwd(xy_ref, w, b, nb, H, W, sigma, int(math.ceil(3 * sigma)))
     return blur(splat_bilinear_fwd(xy_ref, w, b, nb, H, W), sigma)
+
+
+# ----------------------------------------------------------------------------------- MotionPriorCMax KNN
+def knn_indices(queries, points, k):
+    """knn_indices (atl/objectives/mpcm.py:30-42): queries (Q, 2), points (P, n, 2) -> (P, Q, k) int64, the k
+    nearest points of each plane in the order (squared distance, index): d = (qx - px)^2 + (qy - py)^2 with every
+    fp32 operation rounded separately; ties by the lower index (a stable sort of d over the points' order)."""
+    q = _f32c(queries).reshape(-1, 2)
+    pts = _f32c(points)
+    P, n = pts.shape[0], pts.shape[1]
+    out = np.empty((P, q.shape[0], k), np.int64)
+    for s in range(P):
+        dx = q[:, None, 0] - pts[s][None, :, 0]
+        dy = q[:, None, 1] - pts[s][None, :, 1]
+        d = dx * dx + dy * dy                                  # float32 throughout
+        out[s] = np.argsort(d, axis=1, kind="stable")[:, :k]
+    return out
+
+
+def lut_mean(flow_to_ref, idx):
+    """The look-up table of MotionPriorCMaxLoss.lut_flow (atl/objectives/mpcm.py:73-77): the mean over the k
+    neighbours of their displacement to t_ref.  flow_to_ref (P, n, 2), idx (P, Q, k) -> (P, Q, 2) float32 (fp32
+    sum in neighbour order, then the division by k)."""
+    f = _f32c(flow_to_ref)
+    g = np.stack([f[s][idx[s]] for s in range(f.shape[0])])        # (P, Q, k, 2)
+    acc = np.zeros(g.shape[:2] + (2,), np.float32)
+    for j in range(g.shape[2]):
+        acc = acc + g[:, :, j]
+    return acc / np.float32(g.shape[2])

@@ -102,3 +102,29 @@ def test_cpu_objectives_refuse_the_wrong_motion():
         AnchoredTrajectories(n_anchors=None)(ev, Translation(1, win.height, win.width))
     with pytest.raises(ValueError):
         AnchoredExact(rng="gpu")
+
+
+def test_cpu_knn_indices_match_oracle_and_reject_bad_k():
+    rng = np.random.default_rng(3)
+    q = torch.as_tensor((rng.random((200, 2)) * 40).astype(np.float32))
+    pts = torch.as_tensor((rng.random((2, 3, 90, 2)) * 44 - 2).astype(np.float32))
+    got = F.knn_indices(q, pts, 10, chunk=64)
+    want = O.knn_indices(q.numpy(), pts.reshape(6, 90, 2).numpy(), 10).reshape(2, 3, 200, 10)
+    assert np.array_equal(got.numpy(), want)
+    for bad in (0, 33, 91):
+        with pytest.raises(ValueError):
+            F.knn_indices(q, pts, bad)
+
+
+def test_cpu_mpcm_loss_runs_and_backprops():
+    # the reference's test_objectives.py:86-90 on a synthetic window: K = 1 trajectories from a zero grid
+    from x_amd import synth
+    from x_amd.core import EventPacket
+    from x_amd.motion import PixelTrajectories
+    from x_amd.objectives import MotionPriorCMaxLoss
+    win = synth.small_window(seed=2, n=3000, B=1)
+    ev = EventPacket.from_window(win, "cpu")
+    g = torch.zeros(1, 2, ev.height, ev.width, requires_grad=True)
+    out = MotionPriorCMaxLoss(num_knn=8, t_ref=0.3)(ev, PixelTrajectories(g, K=1))
+    out["loss"].backward()
+    assert torch.isfinite(out["loss"]) and g.grad is not None and float(g.grad.abs().sum()) > 0

@@ -488,3 +488,71 @@ def test_make_iwe_weights_and_polarity_split():
     img = O.make_iwe(xy, t, p, b, 2, 6, 7, 0.5, sigma=0.0, polarity="split")
     assert img.shape == (4, 6, 7) and img[0, 3, 2] == 1 and img[1, 3, 2] == 1 and img[2, 1, 5] == 1
     assert img[3, 4, 4] == 1
+
+
+# --------------------------------------------------------------------------- MotionPriorCMax KNN (oracle)
+def _separated(d64, k, rel=1e-5):
+    """Rows whose k-th and (k+1)-th float64 distances are apart (the neighbour set is then unambiguous)."""
+    s = np.sort(d64, axis=1)
+    return (s[:, k] - s[:, k - 1]) > rel * np.maximum(s[:, k], 1e-12)
+
+
+def test_knn_oracle_matches_kd_tree_in_float64():
+    from scipy.spatial import cKDTree
+    rng = np.random.default_rng(5)
+    q = (rng.random((300, 2)) * [64, 48]).astype(F32)
+    pts = (rng.random((2, 400, 2)) * [70, 50] - 3).astype(F32)
+    k = 12
+    got = O.knn_indices(q, pts, k)
+    for s in range(2):
+        dist, ref = cKDTree(pts[s].astype(np.float64)).query(q.astype(np.float64), k=k + 1)
+        d64 = ((q[:, None, :].astype(np.float64) - pts[s][None].astype(np.float64)) ** 2).sum(-1)
+        ok = _separated(d64, k)
+        assert ok.mean() > 0.95
+        for i in np.nonzero(ok)[0]:
+            assert set(got[s, i]) == set(ref[i, :k])
+            # ascending distance (ties in fp32 only where float64 cannot tell them apart)
+            dd = d64[i, got[s, i]]
+            assert np.all(np.diff(dd) >= -1e-9 * dd.max())
+
+
+def test_knn_oracle_ties_by_index_on_a_regular_grid():
+    # points on a 4 px lattice, queries half a pixel off the lattice: many exactly equal distances
+    gy, gx = np.meshgrid(np.arange(6) * 4.0 + 2, np.arange(7) * 4.0 + 2, indexing="ij")
+    pts = np.stack([gx.ravel(), gy.ravel()], 1).astype(F32)[None]
+    q = np.array([[1.5, 1.5], [9.5, 5.5], [13.5, 13.5], [26.0, 22.0]], F32)
+    k = 9
+    got = O.knn_indices(q, pts, k)
+    for i, (qx, qy) in enumerate(q):
+        cand = []
+        for j, (px, py) in enumerate(pts[0]):
+            dx, dy = F32(qx) - F32(px), F32(qy) - F32(py)
+            cand.append((float(F32(F32(dx * dx) + F32(dy * dy))), j))
+        want = [j for _, j in sorted(cand)[:k]]                 # (distance, index) lexicographic
+        assert list(got[0, i]) == want
+
+
+def test_knn_oracle_agrees_with_the_reference_cpu_path():
+    # the reference's CPU path: torch.cdist + topk(largest=False) (atl/objectives/mpcm.py:37-41); same sets
+    # wherever the k-th and (k+1)-th distances are apart
+    rng = np.random.default_rng(9)
+    q = (rng.random((500, 2)) * 80).astype(F32)
+    pts = (rng.random((1, 3, 300, 2)) * 80).astype(F32)
+    k = 8
+    d = torch.cdist(torch.as_tensor(q)[None].expand(3, -1, -1), torch.as_tensor(pts[0]))
+    ref = torch.topk(d, k, dim=-1, largest=False).indices.numpy()
+    got = O.knn_indices(q, pts[0], k)
+    for s in range(3):
+        d64 = ((q[:, None, :].astype(np.float64) - pts[0, s][None].astype(np.float64)) ** 2).sum(-1)
+        ok = _separated(d64, k, rel=1e-4)
+        for i in np.nonzero(ok)[0]:
+            assert set(got[s, i]) == set(ref[s, i])
+
+
+def test_lut_mean_matches_float64_mean():
+    rng = np.random.default_rng(2)
+    f = rng.standard_normal((2, 50, 2)).astype(F32)
+    idx = rng.integers(0, 50, (2, 30, 7))
+    want = f.astype(np.float64)[np.arange(2)[:, None, None], idx].mean(2)
+    got = O.lut_mean(f, idx)
+    assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()

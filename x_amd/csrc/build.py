@@ -12,7 +12,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 ROOT = HERE.parents[1]
-SOURCES = ["abi.hip", "events.hip", "tiles.hip", "pairs.hip", "fastpair.hip"]
+SOURCES = ["abi.hip", "events.hip", "tiles.hip", "pairs.hip", "fastpair.hip", "knn.hip"]
 OUT = HERE / "libatl_hip.so"
 ARCH = os.environ.get("ATL_HIP_ARCH", "gfx950")
 

@@ -80,6 +80,18 @@ def make_iwe(ev: EventPacket, xy_ref: torch.Tensor, t_ref, cfg: IWEConfig,
     return blur(img, cfg.sigma) if cfg.sigma > 0 else img
 
 
+def sobel(img: torch.Tensor):
+    """Horizontal and vertical Sobel derivatives of a (B, H, W) image, zero padding (atl/objectives/base.py:63-68):
+    the x kernel is the outer product of the smoothing [1, 2, 1] (rows) and the difference [-1, 0, 1] (columns),
+    the y kernel its transpose."""
+    smooth = img.new_tensor([1.0, 2.0, 1.0])
+    diff = img.new_tensor([-1.0, 0.0, 1.0])
+    kx = torch.outer(smooth, diff)
+    k = torch.stack([kx, kx.t()])[:, None]                    # (2, 1, 3, 3): x then y
+    g = torch.nn.functional.conv2d(img[:, None], k, padding=1)
+    return g[:, 0], g[:, 1]
+
+
 def iwe_variance(ev: EventPacket, motion, t_ref: float, cfg: Optional[IWEConfig] = None) -> torch.Tensor:
     """Contrast of the IWE at ``t_ref``: its per-image variance over the pixels, averaged over the images (the
     variance metric of the reference's contrast maximisation, atl/objectives/cmax.py:23-25)."""

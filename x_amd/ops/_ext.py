@@ -80,10 +80,12 @@ _SIGS = {
     "atl_fast_pair_bwd": [_P, _P, _P, _P, _P],
     "atl_fast_plan_traj": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P],
     "atl_fast_pair_bwd_traj": [_P, _P, _P, _P, _I, _P, _P, _P, _P],
+    "atl_knn_ws_bytes": [_I, _I],
+    "atl_knn_indices": [_P, _I, _P, _I, _I, _I, _P, _P, _I, _P],
 }
 _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.c_int64,
             "atl_tile_ws_bytes": ctypes.c_int64, "atl_splat_gauss_ws_bytes": ctypes.c_int64,
-            "atl_anchored_score_mean_scratch_bytes": ctypes.c_int64,
+            "atl_anchored_score_mean_scratch_bytes": ctypes.c_int64, "atl_knn_ws_bytes": ctypes.c_int64,
 "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):

@@ -857,3 +857,50 @@ def voxel_grid(pos, t, p, b, B, C, H, W, normalize: str | None = "mean_std") -> 
             mx = vox.abs().amax(dim=(1, 2, 3), keepdim=True).clamp(min=1e-9)
             vox = vox / mx
     return vox
+
+
+# ------------------------------------------------------------------------------ k nearest neighbours
+KNN_MAX_K = 32
+
+
+def _knn_torch(queries: torch.Tensor, pts: torch.Tensor, k: int, chunk: int) -> torch.Tensor:
+    """CPU form of knn_indices: (P, n, 2) points -> (P, Q, k), same order as the HIP kernel (fp32 squared distance
+    with every operation rounded, ties by the lower index through a stable sort)."""
+    P = pts.shape[0]
+    out = torch.empty(P, queries.shape[0], k, dtype=torch.int64)
+    for s in range(0, queries.shape[0], chunk):
+        q = queries[s:s + chunk]
+        dx = q[None, :, None, 0] - pts[:, None, :, 0]
+        dy = q[None, :, None, 1] - pts[:, None, :, 1]
+        d = dx * dx + dy * dy
+        out[:, s:s + chunk] = torch.sort(d, dim=-1, stable=True).indices[..., :k]
+    return out
+
+
+def knn_indices(queries: torch.Tensor, points: torch.Tensor, k: int, chunk: int = 4096) -> torch.Tensor:
+    """queries (Q, 2), points (B, T, n, 2) -> (B, T, Q, k) int64 indices of the k nearest points per (b, t) plane
+    (atl/objectives/mpcm.py:30-42).  Order: squared distance (qx - px)^2 + (qy - py)^2 in fp32, ties by the lower
+    index.  On the device one HIP pass (grid-binned ring search); no gradient (the indices select, they do not
+    weigh)."""
+    if points.dim() != 4 or points.shape[-1] != 2 or queries.dim() != 2 or queries.shape[-1] != 2:
+        raise ValueError(f"queries must be (Q, 2) and points (B, T, n, 2), got {tuple(queries.shape)} and "
+                         f"{tuple(points.shape)}")
+    B, T, n, _ = points.shape
+    k = int(k)
+    if not 1 <= k <= min(n, KNN_MAX_K):
+        raise ValueError(f"k must be in [1, min(n, {KNN_MAX_K})], got k={k} with n={n}")
+    q = queries.detach().to(torch.float32).contiguous()
+    pts = points.detach().to(torch.float32).reshape(B * T, n, 2).contiguous()
+    if not pts.is_cuda:
+        return _knn_torch(q.cpu(), pts, k, chunk).view(B, T, -1, k)
+    if q.device != pts.device:
+        raise ValueError("queries and points must be on the same device")
+    Q = q.shape[0]
+    out = torch.empty(B, T, Q, k, dtype=torch.int64, device=pts.device)
+    nbytes = load_library().atl_knn_ws_bytes(B * T, n)
+    if nbytes < 0:
+        raise ValueError(f"knn_indices: {B * T} planes of {n} points are too many for 32-bit cell indices")
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=pts.device)
+    with torch.cuda.device(pts.device):
+        call("atl_knn_indices", ptr(q), Q, ptr(pts), B * T, n, k, ptr(out), ptr(ws), nbytes, stream_of(pts))
+    return out
