@@ -79,7 +79,8 @@ struct FParams {
   int atmax;                   // max |t_a - c_s| over anchors
   int dup;                     // non-zero if an event occurs more than once among the anchors
   int unique;                  // non-zero if the anchors are every event in order (no index array): no repeats
-  int pad[4];
+  int nonfinite;               // non-zero if a backward record (anchor position, time or gS) is not finite
+  int pad[3];
 };
 
 // One 32-byte record per sorted item, written with a single scattered line (separate arrays would cost one
@@ -994,6 +995,9 @@ __global__ void __launch_bounds__(kPairBlock) k_fast_fwd(FPlan p, FGeo G, int M,
   }
 }
 
+// Finite and small enough that products of two such values stay finite.
+__device__ __forceinline__ bool bounded(float v) { return fabsf(v) < 1e30f; }
+
 // Backward records of the anchors in cell order, brec[q] = (x, y, t, gS / h^2): one 16-byte load per candidate in
 // the backward's per-lane walks (the anchor's at = t - c_s is recomputed there with the same fp32 operation).
 // Also checks that no event occurs twice among the anchors (self[id] then names only one of the records); an
@@ -1004,17 +1008,24 @@ __global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int 
   const int q = blockIdx.x * blockDim.x + threadIdx.x;
   if (q < N) gv[q] = make_float2(0.f, 0.f);
   const int Mv = p.start[2 * G.ncell_pad] - p.start[G.ncell_pad];
+  // the walks' padding past the last record (Mv <= M: inside the M + kUnroll records): zeros
+  if (q < kUnroll) p.brec[Mv + q] = make_float4(0.f, 0.f, 0.f, 0.f);
   if (q >= Mv || q >= M) return;
   const Rec r = p.arec[q];
-  p.brec[q] = make_float4(r.f.x, r.f.y, r.f.z, gS[r.i.y] * G.invh2);
+  const float4 br = make_float4(r.f.x, r.f.y, r.f.z, gS[r.i.y] * G.invh2);
+  p.brec[q] = br;
   if (!p.P->unique && p.self[r.i.x] != q) p.P->dup = 1;
+  if (!(bounded(br.x) && bounded(br.y) && bounded(br.z) && bounded(br.w))) p.P->nonfinite = 1;
 }
 
 // One source's walk over the anchors of every slice of its range (csrc/atl_cpu.cpp:240-248): returns
-// sum_i gS_i * k * dt / h^2 * r.  The leave-one-out test compares the candidate's record position with the
-// position of the source's own anchor record (sp); with DUP (an event repeated among the anchors) it
-// compares event ids instead, as the reference does.
-template <bool DUP>
+// sum_i gS_i * k * dt / h^2 * r.  Leave-one-out (LOO): the pair of an event with its own anchor record has
+// dt = t_j - t_j = 0, so with finite records and source data its term is exactly zero and the test is skipped
+// (kLooNone); otherwise (kLooPos) the candidate's record position is compared with the position of the source's
+// own anchor record (sp), and with an event repeated among the anchors (kLooId) the event ids are compared, as
+// the reference does.
+enum { kLooNone = 0, kLooPos = 1, kLooId = 2 };
+template <int LOO>
 __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, float R, float R2, float4 sr, int sid,
                                              float tj, int key, int sp, int part, int2* tab) {
   const int plane_cells = G.GH * G.GW;
@@ -1045,7 +1056,7 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         A[u] = ld((const float4*)p.brec + u, (uint32_t)k);
-        if (DUP) id[u] = ld(aid + 8 * u, 8u * (uint32_t)k);
+        if (LOO == kLooId) id[u] = ld(aid + 8 * u, 8u * (uint32_t)k);
       }
       const int rem = e - k, self_u = sp - k;
 #pragma unroll
@@ -1055,12 +1066,19 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
         const float rx = A[u].x - (sv.x + sv.z * at);
         const float ry = A[u].y - (sv.y + sv.w * at);
         const float d2 = rx * rx + ry * ry;
-        const bool other = DUP ? id[u] != sid : u != self_u;
+        const bool other = LOO == kLooId ? id[u] != sid : LOO == kLooPos ? u != self_u : true;
         const bool ok = other & !(fabsf(dt) > G.tau) & !(d2 > G.r2max) & (u < rem);
         const float kern = __builtin_amdgcn_exp2f(d2 * G.kexp);
         const float f = A[u].w * kern * dt;           // A.w = gS / h^2
-        mgx = ok ? fmaf(f, rx, mgx) : mgx;
-        mgy = ok ? fmaf(f, ry, mgy) : mgy;
+        if (LOO == kLooNone) {                         // every record and the source are finite and below
+          float fo = ok ? f : 0.f;                     // 1e30 (checked), so a zero factor adds exactly nothing
+          asm volatile("" : "+v"(fo));                 // keep one select (not folded into two after the FMAs)
+          mgx = fmaf(fo, rx, mgx);
+          mgy = fmaf(fo, ry, mgy);
+        } else {                                       // selects: a record may hold anything, NaN included
+          mgx = ok ? fmaf(f, rx, mgx) : mgx;
+          mgy = ok ? fmaf(f, ry, mgy) : mgy;
+        }
       }
     });
   }
@@ -1102,9 +1120,18 @@ __global__ void __launch_bounds__(kPairBlock) k_fast_bwd(FPlan p, FGeo G, int N,
   const int sp = p.self[si.y];
   int2* mytab = tab + threadIdx.x;
   float2 m = make_float2(0.f, 0.f);
-  if (have)
-    m = uni(p.P->dup) ? bwd_source<true>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, part, mytab)
-                      : bwd_source<false>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, part, mytab);
+  // the leave-one-out test can be skipped when every term of a source with its own anchor is exactly zero
+  const bool src_finite = bounded(SR.f.x) && bounded(SR.f.y) && bounded(SR.f.z) && bounded(SR.f.w) && bounded(tj);
+  const int loo = uni(p.P->dup) ? kLooId : (uni(p.P->nonfinite) || __ballot(have && !src_finite)) ? kLooPos
+                                                                                                    : kLooNone;
+  if (have) {
+    if (loo == kLooId)
+      m = bwd_source<kLooId>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, part, mytab);
+    else if (loo == kLooPos)
+      m = bwd_source<kLooPos>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, part, mytab);
+    else
+      m = bwd_source<kLooNone>(p, G, R, R2, SR.f, si.y, tj, si.z, sp, part, mytab);
+  }
 #pragma unroll
   for (int o = kSrcPerWave; o < kWave; o <<= 1) {  // the parts of a source sit kSrcPerWave lanes apart
     m.x += __shfl_xor(m.x, o);
