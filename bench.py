@@ -17,6 +17,7 @@ Other workloads (parity-test configurations, not the headline metric), same outp
     python bench.py --workload iwe-plumbing    # the same on 100k events 240x180, constant flow (2, -1.25)
     python bench.py --workload anchored-blobs  # contention stress: the anchored score on 4M events, 90% in 5
                                                # Gaussian blobs (sigma 8 px), Sim2 flow (0, 0, 0.1, 0.1)
+    python bench.py --workload voxel           # voxel_grid (the training input): 1M events 640x480, 15 time bins
     python bench.py --workload mpcm-lut        # MotionPriorCMax's look-up table at its DSEC configuration: 15
                                                # time bins x 19200 cells of 4 px (640x480), the 32 nearest of
                                                # 19200 tile trajectories (K = 10 B-spline) per cell and bin,
@@ -69,7 +70,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", default="anchored",
-                    choices=["anchored", "anchored-blobs", "iwe", "iwe-plumbing", "trajectories", "mpcm-lut"])
+                    choices=["anchored", "anchored-blobs", "iwe", "iwe-plumbing", "trajectories", "mpcm-lut", "voxel"])
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--sigma", type=float, default=1.0)
@@ -510,6 +511,71 @@ def trajectories_cpu_baseline(win, budget):
     return _baseline_line(O, n, int((win.b == 0).sum()), dt, "the trajectory step (window 0)")
 
 
+# ----------------------------------------------------------------------------------------------- voxel grid
+def voxel_main(a, dev):
+    """voxel_grid (atl/ops/functional.py:221-238, the trainer's input, atl/train/trainer.py:136) on 1M line-segment
+    events at 640x480 with 15 time bins (configs/dsec_*.yaml num_bins), polarity +-1, no normalisation: the tile
+    engine (atl_voxel_grid_ws), with the per-event atomic kernel (atl_voxel_grid) timed beside it."""
+    from x_amd import synth
+    from x_amd.ops import _ext
+    from x_amd.ops import functional as F
+    win = synth.dense_flow_window(seed=0)
+    rng = np.random.default_rng(0)
+    pol = np.where(rng.random(win.n) > 0.5, 1.0, -1.0).astype(np.float32)
+    pos, t, p, b = (torch.as_tensor(v, device=dev) for v in (win.xy, win.t, pol, win.b))
+    C, H, W = 15, win.height, win.width
+
+    def step():
+        F.voxel_grid(pos, t, p, b, 1, C, H, W, normalize=None)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    rec = _ext.time_kernels(["atl_voxel_grid_ws"], every=1)
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    kms = float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec["atl_voxel_grid_ws"]]))
+    # the per-event kernel (one global atomic per corner) on the same input, for comparison
+    vox = torch.zeros(1, C, H, W, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(a.steps):
+        _ext.call("atl_voxel_grid", _ext.ptr(pos), _ext.ptr(t), _ext.ptr(p), _ext.ptr(b), win.n, 1, C, H, W,
+                  _ext.ptr(vox), s)
+    e1.record()
+    torch.cuda.synchronize()
+    atomic_ms = e0.elapsed_time(e1) / a.steps
+    _ext.time_kernels(())
+    nbytes = win.n * 24 + C * H * W * 4          # pos, t, p, b per event; the grid written once
+    line = {
+        "metric": "events/s for voxel_grid @1M events 640x480, 15 bins; % HBM roofline",
+        "value": win.n * a.steps / dt, "unit": "events/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": 1e3 * dt / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "voxel_grid, 1000000 line-segment events, 640x480, 15 time bins, polarity +-1, "
+                               "no normalisation", "events": win.n, "sensor": [W, H], "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "atl_voxel_grid_ws", "achieved": nbytes / (kms * 1e-3) / 1e9,
+                     "peak": 8000.0, "unit": "GB/s", "frac": nbytes / (kms * 1e-3) / 8e12, "traffic": None,
+                     "kernel_ms": kms, "algorithmic_bytes": nbytes},
+        "kernel_ms": {"atl_voxel_grid_ws": kms, "atl_voxel_grid (per-event atomics)": atomic_ms},
+    }
+    if not a.no_cpu:
+        O = _oracle()
+        n, t0 = 125_000, time.perf_counter()
+        while True:
+            O.voxel_grid(win.xy[:n], win.t[:n], pol[:n], win.b[:n], 1, C, H, W)
+            el = time.perf_counter() - t0
+            if el > a.cpu_budget / 4 or n >= win.n:
+                break
+            n, t0 = min(win.n, 2 * n), time.perf_counter()
+        line["cpu_baseline"] = _baseline_line(O, n, win.n, el, "voxel_grid")
+    print(json.dumps(line), flush=True)
+
+
 # ------------------------------------------------------------------------------ MotionPriorCMax look-up table
 def mpcm_lut_main(a, dev):
     """MotionPriorCMaxLoss.lut_flow at the reference's DSEC configuration (atl/objectives/mpcm.py:4-7): 480x640,
@@ -589,10 +655,10 @@ def main():
         print(f"bench.py measures one GPU only (asked for {a.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
         sys.exit(2)
-    if a.workload.startswith("iwe") or a.workload in ("trajectories", "mpcm-lut"):
+    if a.workload.startswith("iwe") or a.workload in ("trajectories", "mpcm-lut", "voxel"):
         dev = torch.device("cuda:0")
         torch.cuda.set_device(dev)
-        {"trajectories": trajectories_main, "mpcm-lut": mpcm_lut_main}.get(a.workload, iwe_main)(a, dev)
+        {"trajectories": trajectories_main, "mpcm-lut": mpcm_lut_main, "voxel": voxel_main}.get(a.workload, iwe_main)(a, dev)
         return
     from x_amd.objectives import AnchoredExact
     from x_amd.ops import _ext

@@ -74,6 +74,12 @@ int atl_splat_gauss_fwd_ws(const float* pos, const float* w, const int64_t* b, i
 /* voxel_grid (csrc/atl_ops.h:49-50, csrc/atl_cpu.cpp:256-286): vox (B,C,H,W) accumulated. */
 int atl_voxel_grid(const float* pos, const float* t, const float* p, const int64_t* b, int64_t N, int64_t B,
                    int64_t C, int64_t H, int64_t W, float* vox, hipStream_t stream);
+/* The same voxel grid on the tile-binned LDS engine (the C time bins are the channels of each tile's window;
+ * identical corner indices and weights, float sums in another order).  ws: atl_voxel_ws_bytes(N, B, C, H, W)
+ * bytes (-1: sizes unsupported, use atl_voxel_grid). */
+int64_t atl_voxel_ws_bytes(int64_t N, int64_t B, int64_t C, int64_t H, int64_t W);
+int atl_voxel_grid_ws(const float* pos, const float* t, const float* p, const int64_t* b, int64_t N, int64_t B,
+                      int64_t C, int64_t H, int64_t W, float* vox, void* ws, int64_t ws_bytes, hipStream_t stream);
 
 /* ---------------------------------------------------------------- flow-grid sampling */
 

@@ -126,6 +126,44 @@ def test_voxel_matches_oracle():
     close_rel(N(got), O.voxel_grid(pos, t, p, b, 2, 5, 20, 24), 1e-5)
 
 
+def _voxel_cases_close(got, want, mag):
+    # same voxels touched (bit-exact corner indices); values within 1e-5 of the sum of |terms|
+    assert np.array_equal(got != 0, want != 0) or np.abs(got - want).max() <= 1e-6 * mag
+    assert np.abs(got - want).max() <= 1e-5 * mag
+
+
+def test_voxel_tile_engine_at_full_sensor_and_edges():
+    from x_amd.ops import _ext
+    lib = _ext.load_library()
+    win = synth.dense_flow_window(seed=3)                      # 1M line-segment events, time-sorted
+    rng = np.random.default_rng(11)
+    pos, t, b = win.xy, win.t, win.b
+    p = np.where(rng.random(len(t)) > 0.5, 1.0, -1.0).astype(F32)
+    print("voxel grid: 1M events 640x480, 15 bins, tile engine", flush=True)
+    assert lib.atl_voxel_ws_bytes(len(t), 1, 15, 480, 640) > 0
+    got = N(F.voxel_grid(T(pos), T(t), T(p), T(b), 1, 15, 480, 640, normalize=None))
+    _voxel_cases_close(got, O.voxel_grid(pos, t, p, b, 1, 15, 480, 640),
+                       float(O.voxel_grid(pos, t, np.abs(p), b, 1, 15, 480, 640).max()))
+    # positions at and past the borders, times outside [0, 1], zero polarity, three batches
+    n = 60_000
+    pos = np.stack([rng.random(n) * 68 - 2, rng.random(n) * 52 - 2], 1).astype(F32)
+    pos[:500] = np.floor(pos[:500])
+    t = np.sort(rng.random(n) * 1.2 - 0.1).astype(F32)
+    b = np.sort(rng.integers(0, 3, n)).astype(np.int64)
+    p = rng.choice(np.array([-1.0, 0.0, 1.0], F32), n)
+    for C in (1, 2, 5, 15):
+        print(f"voxel grid edges C={C}", flush=True)
+        got = N(F.voxel_grid(T(pos), T(t), T(p), T(b), 3, C, 48, 64, normalize=None))
+        _voxel_cases_close(got, O.voxel_grid(pos, t, p, b, 3, C, 48, 64),
+                           float(O.voxel_grid(pos, t, np.abs(p), b, 3, C, 48, 64).max()) + 1e-30)
+    # more bins than an LDS window holds (64 x 17 x 17 floats): the per-event kernel takes over, same results
+    print("voxel grid: 64 bins (per-event fallback)", flush=True)
+    assert lib.atl_voxel_ws_bytes(n, 3, 64, 48, 64) < 0
+    got = N(F.voxel_grid(T(pos), T(t), T(p), T(b), 3, 64, 48, 64, normalize=None))
+    _voxel_cases_close(got, O.voxel_grid(pos, t, p, b, 3, 64, 48, 64),
+                       float(O.voxel_grid(pos, t, np.abs(p), b, 3, 64, 48, 64).max()))
+
+
 def test_plumbing_translation_splat_gather_fwd_bwd():
     """100k events at 240x180, translation (2.0, -1.25) px/window: warp to t_ref = 0, splat, gather back."""
     win = synth.plumbing_translation(seed=0)

@@ -31,7 +31,7 @@ constexpr int kTileMaxKeys = 16384;              // LDS histogram capacity (tile
 constexpr int kAccBlock = 256;                   // accumulation: threads per tile
 constexpr int kMaxChannels = 32;                 // field channels of the tile adjoint (LDS: C x 17 x 17 floats)
 
-enum { kImage = 0, kGrid = 1, kGauss = 2 };
+enum { kImage = 0, kGrid = 1, kGauss = 2, kVoxel = 3 };
 constexpr int kMaxGaussRadius = 8;               // truncated-Gaussian splats of larger radius stay per event
 
 struct TileGeo {
@@ -104,7 +104,7 @@ template <int MODE>
 __device__ __forceinline__ int tile_key(float x, float y, int64_t b, const TileGeo& g) {
   if (!batch_ok(b, g.B)) return -1;
   int tx, ty;
-  if (MODE == kImage) {
+  if (MODE == kImage || MODE == kVoxel) {
     int x0, y0;
     if (!image_base(x, y, g.H, g.W, x0, y0)) return -1;
     tx = (x0 + 1) / g.T;
@@ -123,12 +123,14 @@ __device__ __forceinline__ int tile_key(float x, float y, int64_t b, const TileG
 }
 
 // Binning.  SCATTER = false: per-block tile histogram into cnt[key * nblk + block].  SCATTER = true: the
-// block's scanned offsets are loaded into LDS and every event writes (x, y, value, index) to its slot.
+// block's scanned offsets are loaded into LDS and every event writes (x, y, value, index) to its slot; kVoxel
+// writes (x, y, polarity, t * (C - 1)) (aux = t) and skips events whose time bins both miss [0, C).
 template <int MODE, bool SCATTER>
 __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __restrict__ pos,
                                                             const int64_t* __restrict__ bidx,
                                                             const float* __restrict__ val, TileGeo g,
-                                                            int* __restrict__ cnt, float4* __restrict__ rec) {
+                                                            int* __restrict__ cnt, float4* __restrict__ rec,
+                                                            const float* __restrict__ aux = nullptr) {
   extern __shared__ int hist[];
   const int blk = blockIdx.x;
   for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) hist[i] = SCATTER ? cnt[i * g.nblk + blk] : 0;
@@ -152,10 +154,17 @@ __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __rest
   for (int u = 0; u < per; ++u) {
     const int j = j0 + u * kTileBinBlock + threadIdx.x;
     if (j >= g.N || vj[u] == 0.f) continue;      // a zero weight adds nothing (csrc/atl_cpu.cpp:44)
+    float tn = 0.f;
+    if (MODE == kVoxel) {                         // csrc/atl_cpu.cpp:265: tn = t * (C - 1)
+      tn = aux[j] * (float)(g.C - 1);
+      const float ft = floorf(tn);
+      if (!(ft >= -1.f && ft <= (float)(g.C - 1))) continue;
+    }
     const int key = tile_key<MODE>(p[u].x, p[u].y, bj[u], g);
     if (key < 0) continue;
     const int slot = atomicAdd(hist + key, 1);
-    if (SCATTER) rec[slot] = make_float4(p[u].x, p[u].y, vj[u], __int_as_float(j));
+    if (SCATTER)
+      rec[slot] = make_float4(p[u].x, p[u].y, vj[u], MODE == kVoxel ? tn : __int_as_float(j));
   }
   if (!SCATTER) {
     __syncthreads();
@@ -189,6 +198,33 @@ __device__ __forceinline__ void accum_record(const float4& q, const float* __res
         const int lx = xx - ox;
         if ((unsigned)ly < (unsigned)L && (unsigned)lx < (unsigned)L)
           atomicAdd(acc + ly * L + lx, wn * expf(-(dx * dx + dy * dy) * g.inv2s2));
+      }
+    }
+  } else if (MODE == kVoxel) {
+    // csrc/atl_cpu.cpp:264-283: corners (t0 + dt, y0 + dy, x0 + dx), each in range, value pol * wt * wy * wx
+    int x0, y0;
+    if (!image_base(q.x, q.y, g.H, g.W, x0, y0)) return;   // never taken: the binning applied this test
+    const float tn = q.w;
+    const int t0 = (int)floorf(tn);
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const int tt = t0 + dt;
+      if (tt < 0 || tt >= nc) continue;
+      const float wt = 1.f - fabsf((float)tt - tn);
+#pragma unroll
+      for (int dy = 0; dy < 2; ++dy) {
+        const int yy = y0 + dy;
+        if (yy < 0 || yy >= g.H) continue;
+        const float wy = 1.f - fabsf((float)yy - q.y);
+#pragma unroll
+        for (int dx = 0; dx < 2; ++dx) {
+          const int xx = x0 + dx;
+          if (xx < 0 || xx >= g.W) continue;
+          const float wx = 1.f - fabsf((float)xx - q.x);
+          const int ly = yy - oy, lx = xx - ox;
+          if ((unsigned)ly < (unsigned)L && (unsigned)lx < (unsigned)L)
+            atomicAdd(acc + (tt * L + ly) * L + lx, q.z * wt * wy * wx);
+        }
       }
     }
   } else if (MODE == kImage) {
@@ -285,8 +321,9 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict_
       __syncthreads();
       const int b = key / plane, r = key - b * plane;
       const int ty = r / g.TX, tx = r - ty * g.TX;
-      const int ox = MODE == kImage ? tx * T - 1 : MODE == kGauss ? tx * T - 2 * g.R : tx * T;   // LDS column 0
-      const int oy = MODE == kImage ? ty * T - 1 : MODE == kGauss ? ty * T - 2 * g.R : ty * T;
+      const bool img_org = MODE == kImage || MODE == kVoxel;
+      const int ox = img_org ? tx * T - 1 : MODE == kGauss ? tx * T - 2 * g.R : tx * T;   // LDS column 0
+      const int oy = img_org ? ty * T - 1 : MODE == kGauss ? ty * T - 2 * g.R : ty * T;
       float4 q[kAccItems];
 #pragma unroll
       for (int u = 0; u < kAccItems; ++u) {
@@ -554,7 +591,7 @@ __global__ void k_tile_zero1(int* p) { p[0] = 0; }
 
 template <int MODE>
 void tile_bin(const TileGeo& g, const TileLayout& L, void* ws, const float* pos, const int64_t* b, const float* val,
-              hipStream_t stream) {
+              hipStream_t stream, const float* aux = nullptr) {
   char* w = (char*)ws;
   int* cnt = (int*)(w + L.cnt);
   int* boff = (int*)(w + L.boff);
@@ -564,10 +601,10 @@ void tile_bin(const TileGeo& g, const TileLayout& L, void* ws, const float* pos,
   }
   const size_t lds = (size_t)g.nkeys * sizeof(int);
   hipLaunchKernelGGL((k_tile_bin<MODE, false>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
-                     b, val, g, cnt, (float4*)nullptr);
+                     b, val, g, cnt, (float4*)nullptr, aux);
   scan32(cnt, (int64_t)g.nkeys * g.nblk, (int*)(w + L.part), boff, stream);
   hipLaunchKernelGGL((k_tile_bin<MODE, true>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
-                     b, val, g, boff, (float4*)(w + L.rec));
+                     b, val, g, boff, (float4*)(w + L.rec), aux);
 }
 
 template <int MODE, int C>
@@ -663,6 +700,35 @@ int atl_splat_bilinear_fwd_noalloc(const float* pos, const float* w, const int64
   tile_bin<kImage>(g, L, ws, pos, b, w, stream);
   tile_accum<kImage, 1>(g, L, ws, nullptr, img, stream);
   return check_launch("splat_bilinear_fwd_noalloc");
+}
+
+// voxel_grid on the tile engine: the C time bins are the channels of a (T+1)^2 LDS window per tile segment.
+constexpr int kMaxVoxelLds = 65536;              // bytes of LDS for one window
+
+static bool voxel_geo(int64_t N, int64_t B, int64_t C, int64_t H, int64_t W, TileGeo& g) {
+  if (C < 1 || C > 1024 || !tile_geo(kVoxel, B, H, W, N, 0, 0, g)) return false;
+  g.C = (int)C;
+  return C * (g.T + 1) * (g.T + 1) * 4 <= kMaxVoxelLds && B * C * H * W < ((int64_t)1 << 31);
+}
+
+int64_t atl_voxel_ws_bytes(int64_t N, int64_t B, int64_t C, int64_t H, int64_t W) {
+  TileGeo g;
+  if (!voxel_geo(N, B, C, H, W, g)) return -1;
+  return tile_layout(g).bytes;
+}
+
+int atl_voxel_grid_ws(const float* pos, const float* t, const float* p, const int64_t* b, int64_t N, int64_t B,
+                      int64_t C, int64_t H, int64_t W, float* vox, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  if (N < 0 || B < 0 || C < 1 || H < 1 || W < 1) { set_error("voxel_grid_ws: bad sizes"); return 1; }
+  if (N == 0 || B == 0) return 0;
+  TileGeo g;
+  if (!voxel_geo(N, B, C, H, W, g)) { set_error("voxel_grid_ws: unsupported sizes N=%lld B=%lld C=%lld H=%lld W=%lld (use atl_voxel_grid)", (long long)N, (long long)B, (long long)C, (long long)H, (long long)W); return 1; }
+  const TileLayout L = tile_layout(g);
+  if (!ws || ws_bytes < L.bytes) { set_error("voxel_grid_ws: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
+  if (!pos || !t || !p || !b || !vox) { set_error("voxel_grid_ws: null argument"); return 1; }
+  tile_bin<kVoxel>(g, L, ws, pos, b, p, stream, t);
+  tile_accum<kVoxel, 0>(g, L, ws, nullptr, vox, stream);
+  return check_launch("voxel_grid_ws");
 }
 
 int atl_gather_bilinear_bwd_ws(const float* gval, const float* img, const float* pos, const int64_t* b, int64_t N,

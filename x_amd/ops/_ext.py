@@ -81,11 +81,14 @@ _SIGS = {
     "atl_fast_plan_traj": [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P],
     "atl_fast_pair_bwd_traj": [_P, _P, _P, _P, _I, _P, _P, _P, _P],
     "atl_knn_ws_bytes": [_I, _I],
+    "atl_voxel_ws_bytes": [_I, _I, _I, _I, _I],
+    "atl_voxel_grid_ws": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P],
     "atl_knn_indices": [_P, _I, _P, _I, _I, _I, _P, _P, _I, _P],
 }
 _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.c_int64,
             "atl_tile_ws_bytes": ctypes.c_int64, "atl_splat_gauss_ws_bytes": ctypes.c_int64,
             "atl_anchored_score_mean_scratch_bytes": ctypes.c_int64, "atl_knn_ws_bytes": ctypes.c_int64,
+            "atl_voxel_ws_bytes": ctypes.c_int64,
 "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):
@@ -142,7 +145,7 @@ _NARG = {"atl_sample_grid_fwd": 7, "atl_sample_grid_bwd_planned": 6, "atl_sample
          "atl_traj_gout": 2,
          "atl_splat_gauss_fwd": 3, "atl_splat_gauss_bwd": 4, "atl_splat_gauss_fwd_ws": 3,
          "atl_gather_bilinear_fwd": 3, "atl_gather_bilinear_bwd_ws": 4, "atl_splat_bilinear_fwd_ws": 3,
-         "atl_splat_bilinear_bwd": 4}
+         "atl_splat_bilinear_bwd": 4, "atl_voxel_grid_ws": 4, "atl_voxel_grid": 4}
 
 
 def time_kernels(names, every: int = 1) -> dict:
@@ -310,9 +313,15 @@ class HipOps:
         _need(pos, "pos", F32, dev, (N, 2)); _need(t, "t", F32, dev, (N,)); _need(p, "p", F32, dev, (N,))
         _need(b, "b", I64, dev, (N,))
         vox = torch.zeros(int(B), int(C), int(H), int(W), device=dev, dtype=F32)
+        nbytes = load_library().atl_voxel_ws_bytes(N, int(B), int(C), int(H), int(W)) if N > 0 and int(B) > 0 else -1
         with torch.cuda.device(dev):
-            call("atl_voxel_grid", ptr(pos), ptr(t), ptr(p), ptr(b), N, int(B), int(C), int(H), int(W), ptr(vox),
-                 stream_of(pos))
+            if nbytes >= 0:          # tile-binned LDS accumulation, the time bins as channels
+                ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+                call("atl_voxel_grid_ws", ptr(pos), ptr(t), ptr(p), ptr(b), N, int(B), int(C), int(H), int(W),
+                     ptr(vox), ptr(ws), nbytes, stream_of(pos))
+            else:                    # too many tiles or bins for the LDS window: one atomic per corner
+                call("atl_voxel_grid", ptr(pos), ptr(t), ptr(p), ptr(b), N, int(B), int(C), int(H), int(W),
+                     ptr(vox), stream_of(pos))
         return vox
 
     # -------------------------------------------------------------------------------- pair sums
