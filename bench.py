@@ -258,10 +258,11 @@ def _bounded_run(run, n_all, budget):
         prev, n = n, min(n_all, 2 * n)
 
 
-def cpu_baseline(win, sigma, budget):
+def cpu_baseline(win, sigma, budget, splat_leg=False):
     """Oracle on the same workload: the full anchored score forward + backward, the plan built with torch CPU
     ops as the reference builds it on CPU tensors (atl/ops/functional.py:132-178), the pair sums, splat and
-    gather in the OpenMP restatement of csrc/atl_cpu.cpp; timed once on a bounded prefix."""
+    gather in the OpenMP restatement of csrc/atl_cpu.cpp (with splat_leg, the IWE at t = 0.5 forward and
+    backward); timed once on a bounded prefix."""
     O = _oracle()
     H, W = win.height, win.width
     rng = np.random.default_rng(0)
@@ -283,6 +284,13 @@ def cpu_baseline(win, sigma, budget):
         gv = O.ats_pair_bwd(gS, p, sigma, 0.2, 3.0, n)
         if dense:
             O.sample_grid_bwd(gv, idx, wts, win.motion["grid"].shape)
+        if splat_leg:                              # IWE at t = 0.5: transport, inside mask, splat, variance grad
+            vr, _, _ = _velocity_np(win, win.xy[sl], win.b[sl])
+            y = (win.xy[sl] + vr * (np.float32(0.5) - win.t[sl])[:, None]).astype(np.float32)
+            w = ((y[:, 0] >= 0) & (y[:, 0] <= W - 1) & (y[:, 1] >= 0) & (y[:, 1] <= H - 1)).astype(np.float32)
+            img = O.splat_bilinear_fwd(y, w, win.b[sl], 1, H, W)
+            gimg = ((2.0 / (H * W - 1)) * (img - img.mean())).astype(np.float32)
+            O.splat_bilinear_bwd(gimg, y, w, win.b[sl])
 
     n, dt, _ = _bounded_run(run, win.n, budget)
     return _baseline_line(O, n, win.n, dt, "anchored score fwd+bwd")
@@ -668,17 +676,23 @@ def main():
     n_events = a.events if a.events else (4_000_000 if a.workload == "anchored-blobs" else 1_000_000)
     win, ev, motion, desc = workload(a.workload, n_events, dev)
     obj = AnchoredExact(h=a.sigma, tau=0.2, cut=3.0, n_slices=16, n_anchors=None, seed=0, rng="device")
+    blobs = a.workload == "anchored-blobs"
+    if blobs:
+        from x_amd.objectives import iwe_variance
 
     def step():
         for prm in motion.parameters():
             prm.grad = None
-        out = obj(ev, motion)
-        out["loss"].backward()
+        loss = obj(ev, motion)["loss"]
+        if blobs:                                  # the splat leg of the contention config: IWE contrast at 0.5
+            loss = loss - iwe_variance(ev, motion, 0.5)
+        loss.backward()
 
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
-    kernels = ["atl_fast_pair_fwd", "atl_fast_pair_bwd"]
+    kernels = ["atl_fast_pair_fwd", "atl_fast_pair_bwd"] + (
+        ["atl_splat_bilinear_fwd_ws", "atl_splat_bilinear_bwd"] if blobs else [])
     rec = _ext.time_kernels(kernels, every=4)      # every bracket delays the next launch: sample the steps
     first_draw = obj._philox[1]
     t0 = time.perf_counter()
@@ -688,6 +702,7 @@ def main():
     dt = time.perf_counter() - t0
     ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec[k]])) for k in kernels}
     _ext.time_kernels(())
+    kernels = ["atl_fast_pair_fwd", "atl_fast_pair_bwd"]   # the roofline's candidates: the pair kernels
     # contributing pairs K = sum_i n_i of the timed steps' own noise draws (counted outside the timed region)
     pairs = []
     with torch.no_grad():
@@ -707,11 +722,13 @@ def main():
     line = {
         "metric": ("events/s for anchored-score fwd+bwd @1M events 640x480; % HBM/VALU roofline"
                    if a.workload == "anchored" else
-                   f"events/s for anchored-score fwd+bwd @{ev.n} events 640x480 blobs; % VALU roofline"),
+                   f"events/s for anchored-score (pair-sum + splat) fwd+bwd @{ev.n} events 640x480 blobs; "
+                   f"% VALU roofline"),
         "value": value, "unit": "events/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": 1e3 * dt / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"{desc}, h={a.sigma}, tau=0.2, cut=3, S=16, all anchors",
+        "config": {"workload": f"{desc}, h={a.sigma}, tau=0.2, cut=3, S=16, all anchors"
+                               + (", minus the IWE variance at t=0.5 (bilinear splat fwd+bwd)" if blobs else ""),
                    "events": ev.n, "sensor": [640, 480], "sigma": a.sigma, "tau": 0.2, "slices": 16,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "valu", "kernel": dom, "achieved": achieved / 1e12, "peak": VALU_PEAK / 1e12,
@@ -726,7 +743,7 @@ def main():
         "pairs_per_anchor": K / ev.n,
     }
     if not a.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(win, a.sigma, a.cpu_budget)
+        line["cpu_baseline"] = cpu_baseline(win, a.sigma, a.cpu_budget, splat_leg=blobs)
     print(json.dumps(line), flush=True)
 
 

@@ -164,6 +164,30 @@ def test_voxel_tile_engine_at_full_sensor_and_edges():
                        float(O.voxel_grid(pos, t, np.abs(p), b, 3, 64, 48, 64).max()))
 
 
+def test_splat_contention_4m_blob_events():
+    """The contention shape: 4M events, 90% in 5 Gaussian blobs (sigma 8 px), transported to t = 0.5 by the Sim2
+    flow, bilinear splat forward (tile engine) and backward against the oracle."""
+    win = synth.blob_window(seed=0)
+    th = win.motion["theta"].astype(F32)
+    c = np.array([(win.width - 1) / 2.0, (win.height - 1) / 2.0], F32)
+    d = (win.xy - c).astype(F32)
+    v = np.stack([th[0] + (th[2] * d[:, 0] - th[3] * d[:, 1]), th[1] + (th[3] * d[:, 0] + th[2] * d[:, 1])], 1)
+    y = (win.xy + v.astype(F32) * (F32(0.5) - win.t)[:, None]).astype(F32)
+    w = np.ones(win.n, F32)
+    H, W = win.height, win.width
+    print("splat contention: 4M blob events, forward", flush=True)
+    img = N(F.get_ext().splat_bilinear_fwd(T(y), T(w), T(win.b), 1, H, W))
+    want = O.splat_bilinear_fwd(y, w, win.b, 1, H, W)
+    assert np.array_equal(img != 0, want != 0)
+    close_rel(img, want, 1e-5)
+    assert float(want.max()) > 1000.0                          # the crowded pixels the config is about
+    print("splat contention: backward", flush=True)
+    gimg = (np.random.default_rng(4).standard_normal((1, H, W))).astype(F32)
+    gpos, gw = F.get_ext().splat_bilinear_bwd(T(gimg), T(y), T(w), T(win.b))
+    wp, ww = O.splat_bilinear_bwd(gimg, y, w, win.b)
+    assert np.array_equal(N(gw), ww) and np.array_equal(N(gpos), wp)
+
+
 def test_plumbing_translation_splat_gather_fwd_bwd():
     """100k events at 240x180, translation (2.0, -1.25) px/window: warp to t_ref = 0, splat, gather back."""
     win = synth.plumbing_translation(seed=0)
