@@ -15,6 +15,9 @@ Other workloads (parity-test configurations, not the headline metric), same outp
                                                # (inside mask), gather of the IWE at the warped events,
                                                # loss = sum, backward to the flow grid
     python bench.py --workload iwe-plumbing    # the same on 100k events 240x180, constant flow (2, -1.25)
+    python bench.py --workload anchored-reflayout  # the headline workload through the reference's own call
+                                               # pattern (device plan in the reference layout + the pybind-surface
+                                               # ats_pair_fwd / ats_pair_bwd), as an unchanged functional.py gets it
     python bench.py --workload anchored-blobs  # contention stress: the anchored score on 4M events, 90% in 5
                                                # Gaussian blobs (sigma 8 px), Sim2 flow (0, 0, 0.1, 0.1)
     python bench.py --workload voxel           # voxel_grid (the training input): 1M events 640x480, 15 time bins
@@ -70,7 +73,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", default="anchored",
-                    choices=["anchored", "anchored-blobs", "iwe", "iwe-plumbing", "trajectories", "mpcm-lut", "voxel"])
+                    choices=["anchored", "anchored-reflayout", "anchored-blobs", "iwe", "iwe-plumbing", "trajectories", "mpcm-lut", "voxel"])
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--sigma", type=float, default=1.0)
@@ -677,6 +680,10 @@ def main():
     win, ev, motion, desc = workload(a.workload, n_events, dev)
     obj = AnchoredExact(h=a.sigma, tau=0.2, cut=3.0, n_slices=16, n_anchors=None, seed=0, rng="device")
     blobs = a.workload == "anchored-blobs"
+    reflayout = a.workload == "anchored-reflayout"
+    if reflayout:                                  # route the objective's pair sums through the reference layout
+        import x_amd.objectives.ats as ats_mod
+        ats_mod.ats_pair_sums = F.ats_pair_sums_reference_layout
     if blobs:
         from x_amd.objectives import iwe_variance
 
@@ -691,7 +698,7 @@ def main():
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
-    kernels = ["atl_fast_pair_fwd", "atl_fast_pair_bwd"] + (
+    kernels = (["atl_ats_pair_fwd", "atl_ats_pair_bwd"] if reflayout else ["atl_fast_pair_fwd", "atl_fast_pair_bwd"]) + (
         ["atl_splat_bilinear_fwd_ws", "atl_splat_bilinear_bwd"] if blobs else [])
     rec = _ext.time_kernels(kernels, every=4)      # every bracket delays the next launch: sample the steps
     first_draw = obj._philox[1]
@@ -702,7 +709,7 @@ def main():
     dt = time.perf_counter() - t0
     ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec[k]])) for k in kernels}
     _ext.time_kernels(())
-    kernels = ["atl_fast_pair_fwd", "atl_fast_pair_bwd"]   # the roofline's candidates: the pair kernels
+    kernels = kernels[:2]                          # the roofline's candidates: the pair kernels
     # contributing pairs K = sum_i n_i of the timed steps' own noise draws (counted outside the timed region)
     pairs = []
     with torch.no_grad():
@@ -722,12 +729,15 @@ def main():
     line = {
         "metric": ("events/s for anchored-score fwd+bwd @1M events 640x480; % HBM/VALU roofline"
                    if a.workload == "anchored" else
+                   "events/s for anchored-score fwd+bwd @1M events 640x480 through the reference-layout pair "
+                   "entry points; % VALU roofline" if reflayout else
                    f"events/s for anchored-score (pair-sum + splat) fwd+bwd @{ev.n} events 640x480 blobs; "
                    f"% VALU roofline"),
         "value": value, "unit": "events/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": 1e3 * dt / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"{desc}, h={a.sigma}, tau=0.2, cut=3, S=16, all anchors"
+                               + (", pair sums through the reference layout (ats_pair_fwd/bwd)" if reflayout else "")
                                + (", minus the IWE variance at t=0.5 (bilinear splat fwd+bwd)" if blobs else ""),
                    "events": ev.n, "sensor": [640, 480], "sigma": a.sigma, "tau": 0.2, "slices": 16,
                    "parallelism": "single GPU"},

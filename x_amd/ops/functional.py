@@ -597,6 +597,19 @@ def ats_pair_sums(x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, fo
                               float(h), float(tau), float(cut), int(n_slices))
 
 
+def ats_pair_sums_reference_layout(x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, anchor_xy=None):
+    """The call pattern of the reference's unchanged ats_pair_sums (atl/ops/functional.py:199-207) on this
+    library: the reference's plan layout built on the device (build_pair_plan, bit-exact with the reference's),
+    then the pybind-surface entry points ats_pair_fwd / ats_pair_bwd (one thread per anchor over 3 x 3 cells,
+    two global atomics per pair in the backward).  Same values as ats_pair_sums; kept to measure what a caller
+    gets without switching to the fused path."""
+    if anchors is None:
+        anchors = torch.arange(x.shape[0], device=x.device)
+    plan = build_pair_plan(x.detach(), t, v.detach(), b, B, H, W, anchors, h, tau, cut, n_slices,
+                           anchor_xy=None if anchor_xy is None else anchor_xy.detach())
+    return _ATSPair.apply(v.float(), plan, h, tau, cut)
+
+
 class _ATSPairTraj(torch.autograd.Function):
     """Pair sums of the trajectory model: gradients to the trajectory starts p and the coefficient rows."""
 
