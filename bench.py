@@ -309,6 +309,7 @@ IWE_BYTES = {
     "atl_gather_bilinear_bwd": lambda n, hw, g: 28 * n + 8 * hw,
     "atl_sample_grid_fwd": lambda n, hw, g: 24 * n + 4 * g,
     "atl_sample_grid_bwd_planned": lambda n, hw, g: 16 * n + 8 * g,
+    "atl_sample_grid_bwd_binned": lambda n, hw, g: 24 * n + 8 * g,
 }
 
 

@@ -60,7 +60,7 @@ int atl_gather_bilinear_bwd_ws(const float* gval, const float* img, const float*
 /* No counterpart in the reference: the tile-binned splat forward of atl_splat_bilinear_fwd_ws for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  It allocates nothing: its workspace is a 64 MiB array held by the library on every GPU it runs on
- * (until the process ends), which fits atl_tile_ws_bytes(N, B, H, W) <= 64 MiB (about 3.9M events at 640x480,
+ * (until the process ends), which fits atl_tile_ws_bytes(N, B, H, W) <= 64 MiB (about 3.6M events at 640x480,
  * B = 1); larger calls fail with status 1 and a message.  img (B,H,W) is accumulated, as by the _ws form.
  * Calls that overlap on one GPU share the array and race. */
 int atl_splat_bilinear_fwd_noalloc(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B,
@@ -130,14 +130,22 @@ int atl_traj_gout(const float* gd, const float* t, int64_t N, int64_t K, int64_t
                   hipStream_t stream);
 /* The same adjoint through a tile plan: atl_grid_plan bins the positions by the 16x16 tile of their base
  * grid node into a workspace of atl_grid_plan_bytes(B, Hg, Wg, N) bytes (-1 if the sizes are unsupported);
- * atl_sample_grid_bwd_planned then accumulates gout tile by tile in LDS and adds each touched node once.
+ * atl_sample_grid_bwd_planned then accumulates gout tile by tile in LDS and flushes each tile's touched nodes.
  * gfield accumulated; C <= 32 (C > 4 only where 16x16 tiles fit the binning).  The positions and img_h, img_w
- * must be the ones the plan was built from (the plan keeps its own copy of the positions; `pos` is not read). */
+ * must be the ones the plan was built from (the plan keeps its own copy of the positions; `pos` is not read).
+ * Each call also writes its list of record chunks into the plan's workspace: one call per plan at a time. */
 int64_t atl_grid_plan_bytes(int64_t B, int64_t Hg, int64_t Wg, int64_t N);
 int atl_grid_plan(int64_t B, int64_t Hg, int64_t Wg, const float* pos, const int64_t* b, int64_t N, int64_t img_h,
                   int64_t img_w, void* ws, int64_t ws_bytes, hipStream_t stream);
+/* The same adjoint for fields of C <= 2 channels with the binning done here, in the backward: the records carry
+ * the gradient rows (x, y, gout[j, 0], gout[j, 1]), so the accumulation reads no row by event index (a random
+ * 8-byte read that every XCD's L2 fetched separately).  ws: atl_grid_plan_bytes(B, Hg, Wg, N) bytes, no plan
+ * needed; gfield accumulated. */
+int atl_sample_grid_bwd_binned(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                               const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gfield, void* ws,
+                               int64_t ws_bytes, hipStream_t stream);
 int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
-                                int64_t N, int64_t img_h, int64_t img_w, const void* ws, float* gfield,
+                                int64_t N, int64_t img_h, int64_t img_w, void* ws, float* gfield,
                                 hipStream_t stream);
 
 /* ---------------------------------------------------------------- event noise */

@@ -257,11 +257,12 @@ def test_sample_grid_channels_last_same_bits(C, img):
     assert np.array_equal(N(tp.grad), N(gp))
 
 
-@pytest.mark.parametrize("C", [2, 12])
+@pytest.mark.parametrize("C", [1, 2, 12])
 @pytest.mark.parametrize("Hg,Wg", [(1, 1), (2, 3), (5, 1), (1, 7), (17, 13), (40, 37)])
 def test_sample_grid_planned_backward_small_grids(Hg, Wg, C):
-    """The tile-plan adjoint on degenerate and odd grids, positions inside and far outside (clamped); 12
-    channels take the gather form on grids of at least 2 x 2 nodes and the scatter form otherwise."""
+    """The tile adjoint on degenerate and odd grids, positions inside and far outside (clamped), some gradient
+    rows zero: 1 or 2 channels bin their rows in the backward; 12 channels take the forward plan, in gather form
+    on grids of at least 2 x 2 nodes and in scatter form otherwise."""
     print(f"planned backward Hg={Hg} Wg={Wg} C={C}", flush=True)
     rng = np.random.default_rng(Hg * 100 + Wg + C)
     n = 3000
@@ -273,6 +274,7 @@ def test_sample_grid_planned_backward_small_grids(Hg, Wg, C):
     want, idx, wts = O.sample_grid(fld, pos, b)
     assert np.array_equal(N(out), want)
     g = rng.standard_normal(want.shape).astype(F32)
+    g[::7] = 0.0                                   # rows of zeros add nothing (and are skipped by the binning)
     out.backward(T(g))
     close_rel(N(tf.grad), O.sample_grid_bwd(g, idx, wts, fld.shape), 1e-5)
 

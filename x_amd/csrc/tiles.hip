@@ -6,9 +6,9 @@
 // scattered, and events concentrated on edges put many of them on the same pixels.  Here every call:
 //   1. bins the events by the 16x16 (or 32x32) tile of their base corner: an LDS histogram per block of 4096
 //      events, a device scan, and a scatter of 16-byte records (x, y, value, event index) into tile order;
-//   2. splits the tile-ordered records into equal ranges, one per workgroup, which adds the weighted
-//      contributions of each tile segment of its range into an LDS copy of the (T+1) x (T+1) pixels they can
-//      reach (corners reach one past the tile);
+//   2. cuts every tile's records into chunks of at most 512 (a one-workgroup scan over the tiles lists them), one
+//      per workgroup, which adds the weighted contributions into an LDS copy of the (T+1) x (T+1) pixels the
+//      tile's events reach (corners reach one past the tile);
 //   3. flushes every non-zero LDS pixel with one global atomic add (neighbouring tiles share their border row
 //      and column, and a crowded tile spans several ranges, so the flush stays atomic; it costs at most
 //      (T+1)^2 atomics per tile segment).
@@ -31,7 +31,7 @@ constexpr int kTileMaxKeys = 16384;              // LDS histogram capacity (tile
 constexpr int kAccBlock = 256;                   // accumulation: threads per tile
 constexpr int kMaxChannels = 32;                 // field channels of the tile adjoint (LDS: C x 17 x 17 floats)
 
-enum { kImage = 0, kGrid = 1, kGauss = 2, kVoxel = 3 };
+enum { kImage = 0, kGrid = 1, kGauss = 2, kVoxel = 3, kGridVal = 4 };   // kGridVal: kGrid, values in the records
 constexpr int kMaxGaussRadius = 8;               // truncated-Gaussian splats of larger radius stay per event
 
 struct TileGeo {
@@ -114,7 +114,7 @@ __device__ __forceinline__ int tile_key(float x, float y, int64_t b, const TileG
     if (!gauss_centre(x, y, g, cx, cy)) return -1;
     tx = (cx + g.R) / g.T;
     ty = (cy + g.R) / g.T;
-  } else {
+  } else {                                         // kGrid, kGridVal
     const GridCell c = grid_cell(x, y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
     tx = c.x0 / g.T;
     ty = c.y0 / g.T;
@@ -139,21 +139,27 @@ __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __rest
   const int j0 = blk * kTilePerBlock;
   float2 p[per];
   int64_t bj[per];
-  float vj[per];
+  float vj[per], v2[per];
 #pragma unroll
   for (int u = 0; u < per; ++u) {
     const int j = j0 + u * kTileBinBlock + threadIdx.x;
     bj[u] = j < g.N ? bidx[j] : -1;
     vj[u] = 1.f;
+    v2[u] = 0.f;
     if (j < g.N) {
       p[u] = pos[j];
-      if (val) vj[u] = val[j];
+      if (MODE == kGridVal) {                     // the gradient row (C = 1 or 2): its values ride in the record
+        vj[u] = val[(int64_t)j * g.C];
+        if (g.C == 2) v2[u] = val[(int64_t)j * 2 + 1];
+      } else if (val) {
+        vj[u] = val[j];
+      }
     }
   }
 #pragma unroll
   for (int u = 0; u < per; ++u) {
     const int j = j0 + u * kTileBinBlock + threadIdx.x;
-    if (j >= g.N || vj[u] == 0.f) continue;      // a zero weight adds nothing (csrc/atl_cpu.cpp:44)
+    if (j >= g.N || (vj[u] == 0.f && v2[u] == 0.f)) continue;   // a zero weight adds nothing (csrc/atl_cpu.cpp:44)
     float tn = 0.f;
     if (MODE == kVoxel) {                         // csrc/atl_cpu.cpp:265: tn = t * (C - 1)
       tn = aux[j] * (float)(g.C - 1);
@@ -164,7 +170,8 @@ __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __rest
     if (key < 0) continue;
     const int slot = atomicAdd(hist + key, 1);
     if (SCATTER)
-      rec[slot] = make_float4(p[u].x, p[u].y, vj[u], MODE == kVoxel ? tn : __int_as_float(j));
+      rec[slot] = make_float4(p[u].x, p[u].y, vj[u],
+                              MODE == kVoxel ? tn : MODE == kGridVal ? v2[u] : __int_as_float(j));
   }
   if (!SCATTER) {
     __syncthreads();
@@ -172,13 +179,8 @@ __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __rest
   }
 }
 
-// Accumulation: workgroup w takes the records [w * kAccRange, (w + 1) * kAccRange) of the tile-ordered array
-// (so a crowded tile is shared by several workgroups and every workgroup has the same work), and for each
-// tile segment inside its range adds the contributions into LDS and flushes the non-zero pixels.
-// kImage, C = 1: value * bilinear corner weight into out (B, H, W), zero padding.
-// kGrid: gout[j * C + c] * corner weight into out (B, C, Hg, Wg).
 constexpr int kAccItems = 2;
-constexpr int kAccRange = kAccBlock * kAccItems;
+constexpr int kAccChunk = kAccBlock * kAccItems;   // records per accumulation workgroup, at most
 
 template <int MODE, int C>
 __device__ __forceinline__ void accum_record(const float4& q, const float* __restrict__ gout, const TileGeo& g,
@@ -247,6 +249,24 @@ __device__ __forceinline__ void accum_record(const float4& q, const float* __res
         if ((unsigned)ly < (unsigned)L && (unsigned)lx < (unsigned)L) atomicAdd(acc + ly * L + lx, q.z * (wx * wy));
       }
     }
+  } else if (MODE == kGridVal) {                  // record (x, y, g0, g1): no gather of the gradient rows
+    const GridCell c = grid_cell(q.x, q.y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
+    const float w00 = (1.f - c.ax) * (1.f - c.ay), w01 = c.ax * (1.f - c.ay);
+    const float w10 = (1.f - c.ax) * c.ay, w11 = c.ax * c.ay;
+    const int ly0 = c.y0 - oy, ly1 = c.y1 - oy, lx0 = c.x0 - ox, lx1 = c.x1 - ox;
+    if ((unsigned)ly0 >= (unsigned)L || (unsigned)ly1 >= (unsigned)L || (unsigned)lx0 >= (unsigned)L ||
+        (unsigned)lx1 >= (unsigned)L)
+      return;                                                // never taken: the binning chose this tile
+    const int i00 = ly0 * L + lx0, i01 = ly0 * L + lx1, i10 = ly1 * L + lx0, i11 = ly1 * L + lx1;
+#pragma unroll
+    for (int ch = 0; ch < (C > 0 ? C : 1); ++ch) {
+      const float go = ch == 0 ? q.z : q.w;
+      float* a = acc + ch * L * L;
+      atomicAdd(a + i00, go * w00);
+      atomicAdd(a + i01, go * w01);
+      atomicAdd(a + i10, go * w10);
+      atomicAdd(a + i11, go * w11);
+    }
   } else {
     const GridCell c = grid_cell(q.x, q.y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
     const int j = __float_as_int(q.w);
@@ -270,82 +290,75 @@ __device__ __forceinline__ void accum_record(const float4& q, const float* __res
   }
 }
 
+// Chunks of the tile-ordered records: every non-empty tile is cut into chunks of at most kAccChunk records, and
+// chunk w gets info[w] = (tile, first record, end record).  One workgroup: a scan of the chunk counts over the
+// tiles (at most kTileMaxKeys), then each tile writes its chunks; nchunk[0] = the number of chunks.
+constexpr int kChunkScanBlock = 1024;
+static_assert(kTileMaxKeys <= kChunkScanBlock * 16, "one scan thread handles at most 16 tiles");
+
+__global__ void __launch_bounds__(kChunkScanBlock) k_tile_chunks(const int* __restrict__ boff, TileGeo g,
+                                                                 int4* __restrict__ info, int* __restrict__ nchunk) {
+  __shared__ int wsum[kChunkScanBlock / kWave + 1];
+  constexpr int kPer = kTileMaxKeys / kChunkScanBlock;
+  int st[kPer + 1];                               // starts of this thread's tiles and of the next tile
+  const int t0 = threadIdx.x * kPer;
+#pragma unroll
+  for (int k = 0; k <= kPer; ++k) st[k] = boff[min(t0 + k, g.nkeys) * g.nblk];
+  int cnt = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k)
+    if (t0 + k < g.nkeys) cnt += (st[k + 1] - st[k] + kAccChunk - 1) / kAccChunk;
+  int total;
+  int base = block_exclusive_scan<kChunkScanBlock>(cnt, wsum, total);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    if (t0 + k >= g.nkeys) break;
+    for (int r = st[k]; r < st[k + 1]; r += kAccChunk) info[base++] = make_int4(t0 + k, r, min(r + kAccChunk, st[k + 1]), 0);
+  }
+  if (threadIdx.x == 0) *nchunk = total;
+}
+
+// Accumulation: workgroup w takes chunk w (at most kAccChunk records of one tile, so a crowded tile is shared by
+// several workgroups), adds the weighted contributions of its records into an LDS copy of the pixels that tile's
+// events reach, and flushes the non-zero pixels with one global atomic each.
 template <int MODE, int C, int T>
-__global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int* __restrict__ boff,
+__global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int4* __restrict__ info,
+                                                          const int* __restrict__ nchunk,
                                                           const float4* __restrict__ rec,
                                                           const float* __restrict__ gout, TileGeo g,
                                                           float* __restrict__ out) {
   const int L = MODE == kGauss ? T + 2 * g.R : T + 1;   // LDS edge: the pixels one tile's events reach
   extern __shared__ float acc[];                  // nc * L * L floats
   const int nc = C > 0 ? C : g.C;
-  __shared__ int ts[kAccBlock + 1];                       // starts of the tiles first .. first + kAccBlock
-  __shared__ int found, found2;
-  const int total = boff[g.nkeys * g.nblk];
-  const int r0 = blockIdx.x * kAccRange;
-  if (r0 >= total) return;
-  const int r1 = min(r0 + kAccRange, total);
-  auto tstart = [&](int k) { return boff[min(k, g.nkeys) * g.nblk]; };   // tile k's first record; nkeys: total
-  // the last tile starting at or before r0, in two parallel rounds (coarse stride, then within the stride)
-  const int step = (g.nkeys + kAccBlock - 1) / kAccBlock;
-  if (threadIdx.x == 0) {
-    found = 0;
-    found2 = 0;
+  if ((int)blockIdx.x >= *nchunk) return;
+  const int4 ci = info[blockIdx.x];
+  const int key = ci.x, s0 = ci.y, s1 = ci.z;
+  float4 q[kAccItems];
+#pragma unroll
+  for (int u = 0; u < kAccItems; ++u) {           // the records load while the window is cleared
+    const int k = s0 + u * kAccBlock + threadIdx.x;
+    if (k < s1) q[u] = rec[k];
   }
-  __syncthreads();
-  {
-    const int k = threadIdx.x * step;
-    if (k < g.nkeys && tstart(k) <= r0) atomicMax(&found, k);
-  }
-  __syncthreads();
-  const int coarse = found;
-  {
-    const int k = coarse + (int)threadIdx.x;
-    if (threadIdx.x < step && k < g.nkeys && tstart(k) <= r0) atomicMax(&found2, k);
-  }
+  for (int a = threadIdx.x; a < nc * L * L; a += kAccBlock) acc[a] = 0.f;
   __syncthreads();
   const int64_t pl = (int64_t)g.H * g.W;
   const int plane = g.TY * g.TX;
-  for (int base = max(coarse, found2); base < g.nkeys; base += kAccBlock) {
-    for (int i = threadIdx.x; i <= kAccBlock; i += kAccBlock) ts[i] = tstart(base + i);
-    __syncthreads();
-    bool done = false;
-    for (int i = 0; i < kAccBlock && base + i < g.nkeys; ++i) {
-      const int key = base + i;
-      const int s0 = max(r0, ts[i]), s1 = min(r1, ts[i + 1]);
-      if (s0 >= r1) {
-        done = true;
-        break;
-      }
-      if (s0 >= s1) continue;                             // empty tile
-      for (int a = threadIdx.x; a < nc * L * L; a += kAccBlock) acc[a] = 0.f;
-      __syncthreads();
-      const int b = key / plane, r = key - b * plane;
-      const int ty = r / g.TX, tx = r - ty * g.TX;
-      const bool img_org = MODE == kImage || MODE == kVoxel;
-      const int ox = img_org ? tx * T - 1 : MODE == kGauss ? tx * T - 2 * g.R : tx * T;   // LDS column 0
-      const int oy = img_org ? ty * T - 1 : MODE == kGauss ? ty * T - 2 * g.R : ty * T;
-      float4 q[kAccItems];
+  const int b = key / plane, r = key - b * plane;
+  const int ty = r / g.TX, tx = r - ty * g.TX;
+  const bool img_org = MODE == kImage || MODE == kVoxel;
+  const int ox = img_org ? tx * T - 1 : MODE == kGauss ? tx * T - 2 * g.R : tx * T;   // LDS column 0
+  const int oy = img_org ? ty * T - 1 : MODE == kGauss ? ty * T - 2 * g.R : ty * T;
 #pragma unroll
-      for (int u = 0; u < kAccItems; ++u) {
-        const int k = s0 + u * kAccBlock + threadIdx.x;
-        if (k < s1) q[u] = rec[k];
-      }
-#pragma unroll
-      for (int u = 0; u < kAccItems; ++u)
-        if (s0 + u * kAccBlock + (int)threadIdx.x < s1) accum_record<MODE, C>(q[u], gout, g, ox, oy, L, acc);
-      __syncthreads();
-      for (int a = threadIdx.x; a < L * L; a += kAccBlock) {
-        const int py = oy + a / L, px = ox + a % L;
-        if (py < 0 || py >= g.H || px < 0 || px >= g.W) continue;
-        for (int ch = 0; ch < nc; ++ch) {
-          const float v = acc[ch * L * L + a];
-          if (v != 0.f) atomicAdd(out + ((int64_t)b * nc + ch) * pl + (int64_t)py * g.W + px, v);
-        }
-      }
-      __syncthreads();
+  for (int u = 0; u < kAccItems; ++u)
+    if (s0 + u * kAccBlock + (int)threadIdx.x < s1) accum_record<MODE, C>(q[u], gout, g, ox, oy, L, acc);
+  __syncthreads();
+  for (int a = threadIdx.x; a < L * L; a += kAccBlock) {
+    const int py = oy + a / L, px = ox + a % L;
+    if (py < 0 || py >= g.H || px < 0 || px >= g.W) continue;
+    for (int ch = 0; ch < nc; ++ch) {
+      const float v = acc[ch * L * L + a];
+      if (v != 0.f) atomicAdd(out + ((int64_t)b * nc + ch) * pl + (int64_t)py * g.W + px, v);
     }
-    if (done) break;
-    __syncthreads();                                      // ts is reloaded
   }
 }
 
@@ -572,17 +585,22 @@ bool tile_geo(int mode, int64_t B, int64_t H, int64_t W, int64_t N, int64_t img_
 }
 
 struct TileLayout {
-  int64_t cnt, boff, part, rec, bytes;
+  int64_t cnt, boff, part, rec, info, nchunk, bytes;
 };
+
+// Chunks of one call, at most: one per non-empty tile plus one per kAccChunk records.
+inline int64_t max_chunks(const TileGeo& g) { return (int64_t)g.nkeys + ((int64_t)g.N + kAccChunk - 1) / kAccChunk; }
 
 TileLayout tile_layout(const TileGeo& g) {
   TileLayout L;
   const int64_t nbh = (int64_t)g.nkeys * g.nblk;
   int64_t off = 0;
-  L.cnt = off;  off += align256(nbh * 4);
-  L.boff = off; off += align256((nbh + 1) * 4);
-  L.part = off; off += align256((scan_tiles(nbh > 0 ? nbh : 1) + 1) * 4);
-  L.rec = off;  off += align256((int64_t)g.N * 16);
+  L.cnt = off;    off += align256(nbh * 4);
+  L.boff = off;   off += align256((nbh + 1) * 4);
+  L.part = off;   off += align256((scan_tiles(nbh > 0 ? nbh : 1) + 1) * 4);
+  L.rec = off;    off += align256((int64_t)g.N * 16);
+  L.info = off;   off += align256(max_chunks(g) * 16);
+  L.nchunk = off; off += 256;
   L.bytes = off;
   return L;
 }
@@ -611,17 +629,21 @@ template <int MODE, int C>
 void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const float* gout, float* out,
                 hipStream_t stream) {
   if (g.nblk == 0) return;
-  const char* w = (const char*)ws;
-  const unsigned grid = (unsigned)((g.N + kAccRange - 1) / kAccRange);   // records <= N
+  char* w = (char*)ws;                             // the chunk list is written here (a part of the plan)
+  int4* info = (int4*)(w + L.info);
+  int* nchunk = (int*)(w + L.nchunk);
+  hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.boff), g, info,
+                     nchunk);
+  const unsigned grid = (unsigned)max_chunks(g);  // workgroups past the chunk count return at once
   const int nc = C > 0 ? C : g.C;
   const size_t edge = MODE == kGauss ? (size_t)(g.T + 2 * g.R) : (size_t)(g.T + 1);
   const size_t lds = (size_t)nc * edge * edge * sizeof(float);
   if (g.T == 16)
-    hipLaunchKernelGGL((k_tile_accum<MODE, C, 16>), dim3(grid), dim3(kAccBlock), lds, stream,
-                       (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, out);
+    hipLaunchKernelGGL((k_tile_accum<MODE, C, 16>), dim3(grid), dim3(kAccBlock), lds, stream, (const int4*)info,
+                       (const int*)nchunk, (const float4*)(w + L.rec), gout, g, out);
   else
-    hipLaunchKernelGGL((k_tile_accum<MODE, C, 32>), dim3(grid), dim3(kAccBlock), lds, stream,
-                       (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, out);
+    hipLaunchKernelGGL((k_tile_accum<MODE, C, 32>), dim3(grid), dim3(kAccBlock), lds, stream, (const int4*)info,
+                       (const int*)nchunk, (const float4*)(w + L.rec), gout, g, out);
 }
 
 // Scratch of atl_splat_bilinear_fwd_noalloc: the tile engine's workspace (counts, offsets, records) for callers
@@ -789,8 +811,26 @@ int atl_grid_plan(int64_t B, int64_t Hg, int64_t Wg, const float* pos, const int
   return check_launch("grid_plan");
 }
 
+int atl_sample_grid_bwd_binned(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                               const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gfield, void* ws,
+                               int64_t ws_bytes, hipStream_t stream) {
+  TileGeo g;
+  if (!tile_geo(kGridVal, B, Hg, Wg, N, img_h, img_w, g) || C < 1 || C > 2) { set_error("sample_grid_bwd_binned: bad sizes (C <= 2, at most 16384 tiles)"); return 1; }
+  g.C = (int)C;
+  const TileLayout L = tile_layout(g);
+  if (!ws || ws_bytes < L.bytes) { set_error("sample_grid_bwd_binned: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
+  if (N == 0) return 0;
+  if (!gout || !pos || !b || !gfield) { set_error("sample_grid_bwd_binned: null argument"); return 1; }
+  tile_bin<kGridVal>(g, L, ws, pos, b, gout, stream);
+  if (C == 1)
+    tile_accum<kGridVal, 1>(g, L, ws, nullptr, gfield, stream);
+  else
+    tile_accum<kGridVal, 2>(g, L, ws, nullptr, gfield, stream);
+  return check_launch("sample_grid_bwd_binned");
+}
+
 int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
-                                int64_t N, int64_t img_h, int64_t img_w, const void* ws, float* gfield,
+                                int64_t N, int64_t img_h, int64_t img_w, void* ws, float* gfield,
                                 hipStream_t stream) {
   TileGeo g;
   if (!tile_geo(kGrid, B, Hg, Wg, N, img_h, img_w, g) || C < 1 || C > kMaxChannels || (C > 4 && g.T != 16)) { set_error("sample_grid_bwd_planned: bad sizes (C <= 4, or C <= 32 on grids of at most 16384 16x16 tiles)"); return 1; }

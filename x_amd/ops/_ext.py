@@ -74,6 +74,7 @@ _SIGS = {
     "atl_gather_bilinear_bwd_ws": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P],
     "atl_grid_plan": [_I, _I, _I, _P, _P, _I, _I, _I, _P, _I, _P],
     "atl_sample_grid_bwd_planned": [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _P],
+    "atl_sample_grid_bwd_binned": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _P],
     "atl_fast_geometry_init": [_I, _I, _I, _I, _I, _I, _D, _D, _D, _P],
     "atl_fast_plan": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P],
     "atl_fast_pair_fwd": [_P, _P, _P, _P, _P],
@@ -140,7 +141,7 @@ def exported_symbols():
 _TIMED = {}          # entry point -> list of (start, end, events) per timed call, while kernel timing is on
 _EVERY = {"n": 1, "calls": {}}   # time one call in n of each entry point
 # position of the event count N in the arguments of the entry points whose calls are sized by it
-_NARG = {"atl_sample_grid_fwd": 7, "atl_sample_grid_bwd_planned": 6, "atl_sample_grid_bwd_pos": 8,
+_NARG = {"atl_sample_grid_fwd": 7, "atl_sample_grid_bwd_planned": 6, "atl_sample_grid_bwd_binned": 7, "atl_sample_grid_bwd_pos": 8,
          "atl_sample_grid_fwd_cl": 7, "atl_sample_grid_bwd_pos_cl": 8, "atl_traj_displacement": 9,
          "atl_traj_gout": 2,
          "atl_splat_gauss_fwd": 3, "atl_splat_gauss_bwd": 4, "atl_splat_gauss_fwd_ws": 3,

@@ -136,10 +136,12 @@ def _tile_plan_ok(B, C, Hg, Wg):
 class _SampleGrid(torch.autograd.Function):
     """Bilinear border-clamped lookup of a (B, C, Hg, Wg) field (atl/motion/parametric.py:235-251).
 
-    When the field needs a gradient, the forward also bins the positions by the tile of their base corner (a
-    device plan), so that the backward accumulates tile by tile in LDS instead of scattered atomic adds.  The
-    positions' gradient (through the interpolation weights) is a per-event gather.  Fields of CL_MIN_CHANNELS
-    channels or more are sampled from a channels-last copy (same bits, a node's channels in one run)."""
+    The field's gradient accumulates tile by tile in LDS instead of scattered atomic adds.  Fields of one or two
+    channels (flows) bin the positions together with their gradient rows in the backward, so the accumulation
+    reads no row by event index; wider fields bin the positions in the forward (a device plan) and gather their
+    rows in the backward.  The positions' gradient (through the interpolation weights) is a per-event gather.
+    Fields of CL_MIN_CHANNELS channels or more are sampled from a channels-last copy (same bits, a node's channels
+    in one run)."""
 
     CL_MIN_CHANNELS = 4
 
@@ -164,7 +166,8 @@ class _SampleGrid(torch.autograd.Function):
                 call("atl_sample_grid_fwd", ptr(fld), B, C, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w),
                      ptr(out), st)
             ctx.cl = cl
-            if plan and _tile_plan_ok(B, C, Hg, Wg):
+            ctx.binned = bool(plan) and C <= 2 and int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N)) >= 0
+            if plan and not ctx.binned and _tile_plan_ok(B, C, Hg, Wg):
                 nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N))
                 if nbytes >= 0:
                     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=pos.device)
@@ -183,7 +186,13 @@ class _SampleGrid(torch.autograd.Function):
         with torch.cuda.device(pos.device):
             if ctx.needs_input_grad[0]:
                 gf = torch.zeros(B, C, Hg, Wg, device=pos.device, dtype=F32)
-                if ctx.plan is not None:
+                if ctx.binned:
+                    N = pos.shape[0]
+                    nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N))
+                    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=pos.device)
+                    call("atl_sample_grid_bwd_binned", ptr(g), B, C, Hg, Wg, ptr(pos), ptr(b), N, ctx.img[0],
+                         ctx.img[1], ptr(gf), ptr(ws), nbytes, stream_of(pos))
+                elif ctx.plan is not None:
                     call("atl_sample_grid_bwd_planned", ptr(g), B, C, Hg, Wg, ptr(pos), pos.shape[0], ctx.img[0],
                          ctx.img[1], ptr(ctx.plan), ptr(gf), stream_of(pos))
                 else:
