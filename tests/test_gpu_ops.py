@@ -164,6 +164,38 @@ def test_voxel_tile_engine_at_full_sensor_and_edges():
                        float(O.voxel_grid(pos, t, np.abs(p), b, 3, 64, 48, 64).max()))
 
 
+@pytest.mark.parametrize("form", ["gather", "scatter"])
+def test_tile_accumulation_forms_match_oracle(form, monkeypatch):
+    """Both accumulation forms of the tile engine (per-corner sums after an LDS sort by base corner, the default
+    for the bilinear modes; LDS float atomics, ATL_TILE_SCATTER=1) against the oracle: the splat forward with a
+    tile of more than 16384 events (2048-record chunks), the gather's image gradient, and the flow-grid adjoint
+    with 1, 2 and 4 channels."""
+    monkeypatch.setenv("ATL_TILE_SCATTER", "1" if form == "scatter" else "0")
+    print(f"tile accumulation form={form}", flush=True)
+    rng = np.random.default_rng(11)
+    H, W, n = 96, 128, 120000
+    pos = np.stack([rng.uniform(-1.5, W + 0.5, n), rng.uniform(-1.5, H + 0.5, n)], 1).astype(F32)
+    pos[: n // 3] = (np.array([40.0, 30.0]) + rng.uniform(0, 12, (n // 3, 2))).astype(F32)   # one crowded tile
+    w = rng.standard_normal(n).astype(F32)
+    b = rng.integers(0, 2, n).astype(np.int64)
+    img = F.get_ext().splat_bilinear_fwd(T(pos), T(w), T(b), 2, H, W)
+    mag = float(O.splat_bilinear_fwd(pos, np.abs(w), b, 2, H, W).max())
+    close_rel(N(img), O.splat_bilinear_fwd(pos, w, b, 2, H, W), 1e-5, floor=1e-6 * mag)
+    src = rng.standard_normal((2, H, W)).astype(F32)
+    g = rng.standard_normal(n).astype(F32)
+    gimg, _ = F.get_ext().gather_bilinear_bwd(T(g), T(src), T(pos), T(b))
+    close_rel(N(gimg), O.gather_bilinear_bwd(g, src, pos, b)[0], 1e-5)
+    for C in (1, 2, 4):
+        fld = rng.standard_normal((2, C, 24, 32)).astype(F32)
+        tf = T(fld).requires_grad_(True)
+        out = F.sample_grid_hip(tf, T(pos), T(b), img_hw=(H, W))
+        want, idx, wts = O.sample_grid(fld, O.dense_grid_pos(pos, H, W, 24, 32), b)
+        assert np.array_equal(N(out), want)
+        go = rng.standard_normal(want.shape).astype(F32)
+        out.backward(T(go))
+        close_rel(N(tf.grad), O.sample_grid_bwd(go, idx, wts, fld.shape), 1e-5)
+
+
 def test_splat_contention_4m_blob_events():
     """The contention shape: 4M events, 90% in 5 Gaussian blobs (sigma 8 px), transported to t = 0.5 by the Sim2
     flow, bilinear splat forward (tile engine) and backward against the oracle."""
@@ -257,12 +289,13 @@ def test_sample_grid_channels_last_same_bits(C, img):
     assert np.array_equal(N(tp.grad), N(gp))
 
 
-@pytest.mark.parametrize("C", [1, 2, 12])
+@pytest.mark.parametrize("C", [1, 2, 3, 12])
 @pytest.mark.parametrize("Hg,Wg", [(1, 1), (2, 3), (5, 1), (1, 7), (17, 13), (40, 37)])
 def test_sample_grid_planned_backward_small_grids(Hg, Wg, C):
     """The tile adjoint on degenerate and odd grids, positions inside and far outside (clamped), some gradient
-    rows zero: 1 or 2 channels bin their rows in the backward; 12 channels take the forward plan, in gather form
-    on grids of at least 2 x 2 nodes and in scatter form otherwise."""
+    rows zero: 1 or 2 channels bin their rows in the backward; 3 and 12 channels take the forward plan (3: the
+    per-corner sums of the bilinear accumulation; 12: the many-channel gather form on grids of at least 2 x 2
+    nodes, the scatter form otherwise)."""
     print(f"planned backward Hg={Hg} Wg={Wg} C={C}", flush=True)
     rng = np.random.default_rng(Hg * 100 + Wg + C)
     n = 3000

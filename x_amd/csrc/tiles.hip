@@ -6,9 +6,11 @@
 // scattered, and events concentrated on edges put many of them on the same pixels.  Here every call:
 //   1. bins the events by the 16x16 (or 32x32) tile of their base corner: an LDS histogram per block of 4096
 //      events, a device scan, and a scatter of 16-byte records (x, y, value, event index) into tile order;
-//   2. cuts every tile's records into chunks of at most 512 (a one-workgroup scan over the tiles lists them), one
-//      per workgroup, which adds the weighted contributions into an LDS copy of the (T+1) x (T+1) pixels the
-//      tile's events reach (corners reach one past the tile);
+//   2. cuts every tile's records into chunks (a one-workgroup scan over the tiles lists them), one per
+//      workgroup, which adds the weighted contributions into an LDS copy of the (T+1) x (T+1) pixels the tile's
+//      events reach (corners reach one past the tile): with LDS float atomics (scatter form, chunks of 512), or,
+//      for the bilinear modes, by sorting the records by base corner in LDS and summing per corner (gather
+//      form, chunks of 512, or of 2048 on crowded tiles);
 //   3. flushes every non-zero LDS pixel with one global atomic add (neighbouring tiles share their border row
 //      and column, and a crowded tile spans several ranges, so the flush stays atomic; it costs at most
 //      (T+1)^2 atomics per tile segment).
@@ -19,6 +21,7 @@
 #include "../../include/atl_hip.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <mutex>
 
 using namespace atlhip;
@@ -291,31 +294,50 @@ __device__ __forceinline__ void accum_record(const float4& q, const float* __res
 }
 
 // Chunks of the tile-ordered records: every non-empty tile is cut into chunks of at most kAccChunk records, and
-// chunk w gets info[w] = (tile, first record, end record).  One workgroup: a scan of the chunk counts over the
-// tiles (at most kTileMaxKeys), then each tile writes its chunks; nchunk[0] = the number of chunks.
+// chunk w gets info[w] = (tile, first record, end record).  One workgroup; thread i takes the tiles i, i + 1024,
+// ... (a run of crowded neighbouring tiles is spread over many threads, each writing its own tile's chunks), so
+// the scan of the chunk counts runs in rounds of 1024 tiles; nchunk[0] = the number of chunks.
 constexpr int kChunkScanBlock = 1024;
 static_assert(kTileMaxKeys <= kChunkScanBlock * 16, "one scan thread handles at most 16 tiles");
 
-__global__ void __launch_bounds__(kChunkScanBlock) k_tile_chunks(const int* __restrict__ boff, TileGeo g,
-                                                                 int4* __restrict__ info, int* __restrict__ nchunk) {
+__global__ void __launch_bounds__(kChunkScanBlock) k_tile_chunks(const int* __restrict__ boff, TileGeo g, int chunk,
+                                                                 int crowd, int4* __restrict__ info,
+                                                                 int* __restrict__ nchunk) {
   __shared__ int wsum[kChunkScanBlock / kWave + 1];
   constexpr int kPer = kTileMaxKeys / kChunkScanBlock;
-  int st[kPer + 1];                               // starts of this thread's tiles and of the next tile
-  const int t0 = threadIdx.x * kPer;
-#pragma unroll
-  for (int k = 0; k <= kPer; ++k) st[k] = boff[min(t0 + k, g.nkeys) * g.nblk];
-  int cnt = 0;
-#pragma unroll
-  for (int k = 0; k < kPer; ++k)
-    if (t0 + k < g.nkeys) cnt += (st[k + 1] - st[k] + kAccChunk - 1) / kAccChunk;
-  int total;
-  int base = block_exclusive_scan<kChunkScanBlock>(cnt, wsum, total);
+  const int rounds = (g.nkeys + kChunkScanBlock - 1) / kChunkScanBlock;
+  int r0[kPer], r1[kPer];                         // record range of this thread's tile of every round
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
-    if (t0 + k >= g.nkeys) break;
-    for (int r = st[k]; r < st[k + 1]; r += kAccChunk) info[base++] = make_int4(t0 + k, r, min(r + kAccChunk, st[k + 1]), 0);
+    const int t = k * kChunkScanBlock + threadIdx.x;
+    r0[k] = k < rounds ? boff[min(t, g.nkeys) * g.nblk] : 0;
+    r1[k] = k < rounds ? boff[min(t + 1, g.nkeys) * g.nblk] : 0;
   }
-  if (threadIdx.x == 0) *nchunk = total;
+  int base = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    if (k >= rounds) break;
+    const int t = k * kChunkScanBlock + threadIdx.x;
+    // chunk: records per chunk; crowded tiles (more than 32 * chunk records, where the flushes of many chunks
+    // would pile up on the same pixels) take chunks of `crowd` records
+    const int len = r1[k] - r0[k];
+    const int cs = len > 32 * chunk ? crowd : chunk;
+    const int n = t < g.nkeys ? (len + cs - 1) / cs : 0;
+    int total;
+    const int c = base + block_exclusive_scan<kChunkScanBlock>(n, wsum, total);
+    const bool crowded = n > kWave / 8;           // a crowded tile's chunks are written by its whole wave
+    if (!crowded)
+      for (int q = 0; q < n; ++q) info[c + q] = make_int4(t, r0[k] + q * cs, min(r0[k] + (q + 1) * cs, r1[k]), 0);
+    for (uint64_t m = __ballot(crowded); m; m &= m - 1) {
+      const int src = __ffsll((unsigned long long)m) - 1;
+      const int tt = __shfl(t, src), cc = __shfl(c, src), a0 = __shfl(r0[k], src), a1 = __shfl(r1[k], src);
+      const int nn = __shfl(n, src), ss = __shfl(cs, src);
+      for (int q = threadIdx.x & (kWave - 1); q < nn; q += kWave)
+        info[cc + q] = make_int4(tt, a0 + q * ss, min(a0 + (q + 1) * ss, a1), 0);
+    }
+    base += total;
+  }
+  if (threadIdx.x == 0) *nchunk = base;
 }
 
 // Accumulation: workgroup w takes chunk w (at most kAccChunk records of one tile, so a crowded tile is shared by
@@ -359,6 +381,154 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int4* __restrict
       const float v = acc[ch * L * L + a];
       if (v != 0.f) atomicAdd(out + ((int64_t)b * nc + ch) * pl + (int64_t)py * g.W + px, v);
     }
+  }
+}
+
+// Gather form of the accumulation for the bilinear modes on 16 x 16 tiles (kImage, kGridVal, and kGrid with at
+// most four channels).  An LDS float atomic retires about one lane every three cycles on this part, so the four
+// (or 4 C) of them per record bound the scatter form above.  Here a workgroup takes a chunk of one tile (512
+// records, or 2048 on a tile of more than 16384) in rounds of 512: it ranks a round's records by base corner with
+// one LDS integer atomic each and stores (ax, ay, values) in base-corner order; thread c then adds, per channel,
+// the four corner products value * (wx * wy) of the records of base corner c (the scatter form's fp32 products)
+// to its register sums.  After the last round every window pixel adds the sums of the base corners that reach it
+// and is flushed with one global atomic.  Only the order of the float additions differs from the scatter form.
+constexpr int kBinT = 16;
+constexpr int kBins = kBinT * kBinT;              // base corners of a tile: thread c sums corner c
+constexpr int kBinChunk = 4 * kAccChunk;          // records per workgroup on a crowded tile (four rounds), so
+                                                  // it is flushed once per 2048 records rather than per 512
+static_assert(kBins == kAccBlock, "one accumulation thread per base corner");
+
+// Base corner (window column bx, row by, both in [0, 16)), fractions and values of record q; false if q adds
+// nothing (never for binned records: the binning applied the same tests).
+template <int MODE, int C>
+__device__ __forceinline__ bool bin_record(const float4& q, const float* __restrict__ gout, const TileGeo& g, int ox,
+                                           int oy, int& bx, int& by, float& ax, float& ay, float (&val)[C]) {
+  if (MODE == kImage) {
+    int x0, y0;
+    if (!image_base(q.x, q.y, g.H, g.W, x0, y0)) return false;
+    ax = q.x - (float)x0;                         // the scatter form's wx1, wy1 (csrc/atl_cpu.cpp:46-53)
+    ay = q.y - (float)y0;
+    bx = x0 - ox;
+    by = y0 - oy;
+    val[0] = q.z;
+  } else {
+    const GridCell c = grid_cell(q.x, q.y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
+    ax = c.ax;
+    ay = c.ay;
+    bx = c.x0 - ox;
+    by = c.y0 - oy;
+    if (MODE == kGridVal) {
+      val[0] = q.z;
+      if (C > 1) val[C > 1 ? 1 : 0] = q.w;
+    } else {
+      const int j = __float_as_int(q.w);
+#pragma unroll
+      for (int ch = 0; ch < C; ++ch) val[ch] = gout[(int64_t)j * C + ch];
+    }
+  }
+  return (unsigned)bx < (unsigned)kBinT && (unsigned)by < (unsigned)kBinT;
+}
+
+template <int MODE, int C>
+__global__ void __launch_bounds__(kAccBlock) k_tile_accum_bins(const int4* __restrict__ info,
+                                                               const int* __restrict__ nchunk,
+                                                               const float4* __restrict__ rec,
+                                                               const float* __restrict__ gout, TileGeo g,
+                                                               float* __restrict__ out) {
+  constexpr int T = kBinT, L = T + 1;
+  __shared__ int bcnt[kBins];
+  __shared__ int bstart[kBins];
+  __shared__ int wsum[kAccBlock / kWave + 1];
+  __shared__ float sax[kAccChunk], say[kAccChunk], sval[C][kAccChunk];
+  __shared__ float bsum[4 * C][kBins];            // corner k = 2 * iy + ix of base corner c, per channel
+  if ((int)blockIdx.x >= *nchunk) return;
+  const int4 ci = info[blockIdx.x];
+  const int key = ci.x, s0 = ci.y, s1 = ci.z;
+  const int tid = threadIdx.x;
+  const int64_t pl = (int64_t)g.H * g.W;
+  const int plane = g.TY * g.TX;
+  const int b = key / plane, r = key - b * plane;
+  const int ty = r / g.TX, tx = r - ty * g.TX;
+  const int ox = MODE == kImage ? tx * T - 1 : tx * T;   // window column 0
+  const int oy = MODE == kImage ? ty * T - 1 : ty * T;
+  float s[4][C];                                  // this thread's base corner: corner sums over the rounds
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch) s[k][ch] = 0.f;
+  for (int base = s0; base < s1; base += kAccChunk) {   // rounds of kAccChunk records
+    float4 q[kAccItems];
+#pragma unroll
+    for (int u = 0; u < kAccItems; ++u) {
+      const int k = base + u * kAccBlock + tid;
+      if (k < s1) q[u] = rec[k];
+    }
+    bcnt[tid] = 0;
+    int bin[kAccItems], rank[kAccItems];
+    float ax[kAccItems], ay[kAccItems], val[kAccItems][C];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kAccItems; ++u) {
+      bin[u] = -1;
+      int bx, by;
+      if (base + u * kAccBlock + tid < s1 && bin_record<MODE, C>(q[u], gout, g, ox, oy, bx, by, ax[u], ay[u], val[u])) {
+        bin[u] = by * T + bx;
+        rank[u] = atomicAdd(bcnt + bin[u], 1);
+      }
+    }
+    __syncthreads();
+    const int mine = bcnt[tid];
+    int total;
+    const int first = block_exclusive_scan<kAccBlock>(mine, wsum, total);
+    bstart[tid] = first;
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kAccItems; ++u) {
+      if (bin[u] < 0) continue;
+      const int p = bstart[bin[u]] + rank[u];
+      sax[p] = ax[u];
+      say[p] = ay[u];
+#pragma unroll
+      for (int ch = 0; ch < C; ++ch) sval[ch][p] = val[u][ch];
+    }
+    __syncthreads();
+    for (int p = first; p < first + mine; ++p) {
+      const float fx = sax[p], fy = say[p];
+      const float wx0 = 1.f - fx, wy0 = 1.f - fy;
+      const float w[4] = {wx0 * wy0, fx * wy0, wx0 * fy, fx * fy};
+#pragma unroll
+      for (int ch = 0; ch < C; ++ch) {
+        const float v = sval[ch][p];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s[k][ch] += v * w[k];
+      }
+    }
+    __syncthreads();                              // the next round reuses the counts and the sorted records
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch) bsum[k * C + ch][tid] = s[k][ch];
+  __syncthreads();
+  // the second corner of an axis is the next pixel, or the same one on a grid of a single column (row)
+  const int sx = MODE == kImage || g.W > 1 ? 1 : 0, sy = MODE == kImage || g.H > 1 ? 1 : 0;
+  for (int a = tid; a < L * L; a += kAccBlock) {
+    const int ly = a / L, lx = a - ly * L;
+    const int py = oy + ly, px = ox + lx;
+    if (py < 0 || py >= g.H || px < 0 || px >= g.W) continue;
+    float v[C];
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch) v[ch] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int cx = lx - (k & 1) * sx, cy = ly - (k >> 1) * sy;
+      if ((unsigned)cx >= (unsigned)T || (unsigned)cy >= (unsigned)T) continue;
+#pragma unroll
+      for (int ch = 0; ch < C; ++ch) v[ch] += bsum[k * C + ch][cy * T + cx];
+    }
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch)
+      if (v[ch] != 0.f) atomicAdd(out + ((int64_t)b * C + ch) * pl + (int64_t)py * g.W + px, v[ch]);
   }
 }
 
@@ -625,6 +795,13 @@ void tile_bin(const TileGeo& g, const TileLayout& L, void* ws, const float* pos,
                      b, val, g, boff, (float4*)(w + L.rec), aux);
 }
 
+// ATL_TILE_SCATTER=1 in the environment selects the scatter form of the accumulation for every mode (read at
+// every call, so that a test can compare both forms in one process).
+bool tile_scatter_form() {
+  const char* e = std::getenv("ATL_TILE_SCATTER");
+  return e && e[0] == '1';
+}
+
 template <int MODE, int C>
 void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const float* gout, float* out,
                 hipStream_t stream) {
@@ -632,13 +809,18 @@ void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const flo
   char* w = (char*)ws;                             // the chunk list is written here (a part of the plan)
   int4* info = (int4*)(w + L.info);
   int* nchunk = (int*)(w + L.nchunk);
-  hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.boff), g, info,
-                     nchunk);
+  constexpr bool kGatherForm = MODE == kImage || MODE == kGridVal || (MODE == kGrid && C >= 1 && C <= 4);
+  const bool gather = kGatherForm && g.T == kBinT && !tile_scatter_form();
+  hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.boff), g,
+                     kAccChunk, gather ? kBinChunk : kAccChunk, info, nchunk);
   const unsigned grid = (unsigned)max_chunks(g);  // workgroups past the chunk count return at once
   const int nc = C > 0 ? C : g.C;
   const size_t edge = MODE == kGauss ? (size_t)(g.T + 2 * g.R) : (size_t)(g.T + 1);
   const size_t lds = (size_t)nc * edge * edge * sizeof(float);
-  if (g.T == 16)
+  if (gather)
+    hipLaunchKernelGGL((k_tile_accum_bins<MODE, kGatherForm ? (C > 0 ? C : 1) : 1>), dim3(grid), dim3(kAccBlock), 0,
+                       stream, (const int4*)info, (const int*)nchunk, (const float4*)(w + L.rec), gout, g, out);
+  else if (g.T == 16)
     hipLaunchKernelGGL((k_tile_accum<MODE, C, 16>), dim3(grid), dim3(kAccBlock), lds, stream, (const int4*)info,
                        (const int*)nchunk, (const float4*)(w + L.rec), gout, g, out);
   else
