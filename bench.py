@@ -73,7 +73,8 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", default="anchored",
-                    choices=["anchored", "anchored-reflayout", "anchored-blobs", "iwe", "iwe-plumbing", "trajectories", "mpcm-lut", "voxel"])
+                    choices=["anchored", "anchored-reflayout", "anchored-blobs", "iwe", "iwe-composed", "iwe-plumbing",
+                             "trajectories", "mpcm-lut", "voxel"])
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--sigma", type=float, default=1.0)
@@ -157,12 +158,20 @@ def summarize(dirs, out, title, command, copy_mb, cal_dirs=()):
     print(text)
 
 
-def recorded_traffic(kernel):
-    """Calibrated HBM bytes per launch of `kernel` from the committed counter summary, or None."""
-    if not COUNTERS.exists():
+def recorded_traffic(kernel, counters=None):
+    """Calibrated HBM bytes per launch of `kernel` (or the sum over a list of kernels) from a committed counter
+    summary (default: the anchored score's), or None."""
+    path = counters or COUNTERS
+    if not path.exists():
         return None
-    m = re.search(r"<!-- traffic: (\{.*\}) -->", COUNTERS.read_text())
-    return json.loads(m.group(1)).get(kernel) if m else None
+    m = re.search(r"<!-- traffic: (\{.*\}) -->", path.read_text())
+    if not m:
+        return None
+    table = json.loads(m.group(1))
+    if isinstance(kernel, str):
+        return table.get(kernel)
+    parts = [table.get(k) for k in kernel]
+    return None if any(v is None for v in parts) else float(sum(parts))
 
 
 def calibrate_copy(mb):
@@ -302,6 +311,14 @@ def cpu_baseline(win, sigma, budget, splat_leg=False):
 # ----------------------------------------------------------------------------------------- IWE workloads
 # Algorithmic HBM bytes of each entry point: per event (positions 8, batch 8, weights or values 4, outputs)
 # plus the image or flow grid once.
+IWE_COUNTERS = ROOT / "profiles" / "iwe_1M_640x480_counters.md"
+# the kernels of the fused entry points whose HBM counters the IWE counter summary holds
+IWE_KERNELS = {
+    "atl_warp_splat_gather_fwd": ["k_wsg_warp", "k_tile_bin<0, true, false>", "k_tile_accum_bins<0, 1>",
+                                  "k_wsg_gather"],
+    "atl_warp_splat_gather_bwd": ["k_wsg_pack", "k_tile_accum_bins<5, 1>", "k_wsg_grad", "k_tile_bin<4, true, true>",
+                                  "k_tile_accum_bins<4, 2>"],
+}
 IWE_BYTES = {
     "atl_splat_bilinear_fwd": lambda n, hw, g: 20 * n + 4 * hw,
     "atl_splat_bilinear_bwd": lambda n, hw, g: 32 * n + 4 * hw,
@@ -310,6 +327,10 @@ IWE_BYTES = {
     "atl_sample_grid_fwd": lambda n, hw, g: 24 * n + 4 * g,
     "atl_sample_grid_bwd_planned": lambda n, hw, g: 16 * n + 8 * g,
     "atl_sample_grid_bwd_binned": lambda n, hw, g: 24 * n + 8 * g,
+    # fused warp -> splat -> gather: events (xy, t, b) and values (or their gradients), the flow grid (or its
+    # gradient) and the image once per direction
+    "atl_warp_splat_gather_fwd": lambda n, hw, g: 24 * n + 4 * hw + 4 * g,
+    "atl_warp_splat_gather_bwd": lambda n, hw, g: 24 * n + 4 * hw + 4 * g,
 }
 
 
@@ -317,12 +338,14 @@ def iwe_workload(kind, dev):
     from x_amd import synth
     from x_amd.core import EventPacket
     from x_amd.motion import DenseLinearFlow, Translation
-    if kind == "iwe":
+    if kind in ("iwe", "iwe-composed"):
         win = synth.dense_flow_window(seed=0)
         grid = win.motion["grid"]
         motion = DenseLinearFlow(1, win.height, win.width, grid=grid.shape[-2:], init=torch.as_tensor(grid))
         desc = (f"IWE splat+gather fwd+bwd, {win.n} events, 640x480, dense flow 2x480x640 (max 20 px/window), "
-                f"warp to t=0.5, bilinear, inside mask, loss = sum of gathered IWE, grad to the flow grid")
+                f"warp to t=0.5, bilinear, inside mask, loss = sum of gathered IWE, grad to the flow grid"
+                + (" (transport, make_iwe and gather as separate ops)" if kind == "iwe-composed" else
+                   " (fused warp -> splat -> gather)"))
     else:
         win = synth.plumbing_translation(seed=0)
         motion = Translation(1, win.height, win.width, init=torch.as_tensor(win.motion["theta"])[None])
@@ -361,18 +384,22 @@ def iwe_cpu_baseline(win, t_ref, budget):
 
 
 def iwe_main(a, dev):
-    from x_amd.objectives.base import IWEConfig, make_iwe
+    from x_amd.objectives.base import IWEConfig, iwe_at_events, make_iwe
     from x_amd.ops import _ext, gather
     win, ev, motion, desc = iwe_workload(a.workload, dev)
-    t_ref = 0.5 if a.workload == "iwe" else 0.0
+    t_ref = 0.0 if a.workload == "iwe-plumbing" else 0.5
     cfg = IWEConfig(kernel="bilinear", sigma=0.0, mask_border=True)
 
     def step():
         for p in motion.parameters():
             p.grad = None
-        y = motion.transport(ev.xy, ev.t, t_ref, ev.b)
-        img = make_iwe(ev, y, t_ref, cfg)
-        gather(img, y, ev.b).sum().backward()
+        if a.workload == "iwe-composed":
+            y = motion.transport(ev.xy, ev.t, t_ref, ev.b)
+            img = make_iwe(ev, y, t_ref, cfg)
+            gather(img, y, ev.b).sum().backward()
+        else:
+            _, vals = iwe_at_events(ev, motion, t_ref, cfg)
+            vals.sum().backward()
 
     for _ in range(a.warmup):
         step()
@@ -387,7 +414,7 @@ def iwe_main(a, dev):
     ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec[k]])) for k in kernels if rec[k]}
     _ext.time_kernels(())
     hw = ev.height * ev.width
-    g = 2 * hw if a.workload == "iwe" else 0
+    g = 0 if a.workload == "iwe-plumbing" else 2 * hw
     gbs = {k: IWE_BYTES[k](ev.n, hw, g) / (ms[k] * 1e-3) / 1e9 for k in ms}
     dom = max(ms, key=lambda k: ms[k])
     line = {
@@ -397,7 +424,10 @@ def iwe_main(a, dev):
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": desc, "events": ev.n, "sensor": [ev.width, ev.height], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": gbs[dom], "peak": 8000.0, "unit": "GB/s",
-                     "frac": gbs[dom] / 8000.0, "traffic": recorded_traffic(dom), "kernel_ms": ms[dom]},
+                     "frac": gbs[dom] / 8000.0,
+                     "traffic": (recorded_traffic(IWE_KERNELS[dom], IWE_COUNTERS)
+                                 if a.workload == "iwe" and dom in IWE_KERNELS else None),
+                     "kernel_ms": ms[dom]},
         "kernel_ms": ms,
         "kernel_gbs": gbs,
     }

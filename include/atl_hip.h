@@ -81,6 +81,23 @@ int64_t atl_voxel_ws_bytes(int64_t N, int64_t B, int64_t C, int64_t H, int64_t W
 int atl_voxel_grid_ws(const float* pos, const float* t, const float* p, const int64_t* b, int64_t N, int64_t B,
                       int64_t C, int64_t H, int64_t W, float* vox, void* ws, int64_t ws_bytes, hipStream_t stream);
 
+/* Warp -> splat -> gather in one launch sequence: the composition of DenseLinearFlow.transport
+ * (atl/motion/parametric.py:53-56, 212-216, 235-251), make_iwe with a bilinear splat and pooled polarity
+ * (atl/objectives/base.py:40-60, csrc/atl_cpu.cpp:38-56) and gather (csrc/atl_cpu.cpp:134-149), which the
+ * reference runs as separate ops.  Forward: y = x + v(x) (t_ref - t) with v the border-clamped sample of the flow
+ * grid (B,2,Hg,Wg) at pixel x, w = [y inside the sensor] if mask_border else 1, img (B,H,W) = splat(y, w)
+ * (accumulated: zero it first), vals (N) = gather(img, y) (written; may be null).  Backward: ggrid (B,2,Hg,Wg)
+ * accumulated with the flow-grid gradient of <gvals, vals> + <gimg, img> (either may be null), from the
+ * forward's ws.  ws: atl_warp_splat_gather_ws_bytes bytes (-1: sizes unsupported). */
+int64_t atl_warp_splat_gather_ws_bytes(int64_t N, int64_t B, int64_t H, int64_t W, int64_t Hg, int64_t Wg);
+int atl_warp_splat_gather_fwd(const float* grid, int64_t B, int64_t Hg, int64_t Wg, const float* xy, const float* t,
+                              const int64_t* b, int64_t N, int64_t H, int64_t W, double t_ref, int64_t mask_border,
+                              float* img, float* vals, void* ws, int64_t ws_bytes, hipStream_t stream);
+int atl_warp_splat_gather_bwd(const float* img, const float* gvals, const float* gimg, const float* xy,
+                              const float* t, const int64_t* b, int64_t N, int64_t B, int64_t H, int64_t W,
+                              int64_t Hg, int64_t Wg, double t_ref, float* ggrid, void* ws, int64_t ws_bytes,
+                              hipStream_t stream);
+
 /* ---------------------------------------------------------------- flow-grid sampling */
 
 /* DenseLinearFlow.field + sample_grid (atl/motion/parametric.py:212-216, 235-251): out (N,C) written, bilinear

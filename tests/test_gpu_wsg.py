@@ -1,0 +1,131 @@
+"""The fused warp -> splat -> gather launches (atl_warp_splat_gather_fwd/bwd) against the oracle's composition of
+the same steps (dense-flow lookup, linear warp, inside mask, bilinear splat, gather, and their adjoints) and
+against the package's composed device path, on identical seeded inputs.
+
+Bars: image and gathered values within 1e-5 of the largest magnitude (float sums in another order), flow-grid
+gradient within 1e-4 of its largest magnitude."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from x_amd import synth
+from x_amd.core import EventPacket
+from x_amd.motion import DenseLinearFlow
+from x_amd.objectives import IWEConfig, iwe_at_events, make_iwe
+from x_amd.ops import functional as F
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+F32 = np.float32
+
+
+def T(a):
+    return torch.as_tensor(np.ascontiguousarray(a), device=DEV)
+
+
+def N(t):
+    return t.detach().cpu().numpy()
+
+
+def close_rel(got, want, rel):
+    scale = max(float(np.abs(want).max()), 1e-30)
+    err = float(np.abs(got.astype(np.float64) - want.astype(np.float64)).max())
+    assert err <= rel * scale, f"max err {err:.3e} vs scale {scale:.3e} (rel {err / scale:.2e})"
+
+
+def oracle_wsg(grid, xy, t, b, t_ref, B, H, W, mask, gvals, gimg):
+    """The composed reference steps on the host: returns img, vals, the flow-grid gradient of
+    <gvals, vals> + <gimg, img>."""
+    v, idx, wts = O.dense_velocity(grid, xy, b, H, W)
+    step = (F32(t_ref) - t).astype(F32)
+    y = (xy + v * step[:, None]).astype(F32)
+    if mask:
+        w = ((y[:, 0] >= 0) & (y[:, 0] <= W - 1) & (y[:, 1] >= 0) & (y[:, 1] <= H - 1)).astype(F32)
+    else:
+        w = np.ones(len(t), F32)
+    img = O.splat_bilinear_fwd(y, w, b, B, H, W)
+    vals = O.gather_bilinear_fwd(img, y, b)
+    gi, gp1 = O.gather_bilinear_bwd(gvals, img, y, b)
+    G = (gi + gimg).astype(F32)
+    gp2, _ = O.splat_bilinear_bwd(G, y, w, b)
+    gv = ((gp1 + gp2) * step[:, None]).astype(F32)
+    return img, vals, O.sample_grid_bwd(gv, idx, wts, grid.shape)
+
+
+@pytest.mark.parametrize("mask", [True, False])
+@pytest.mark.parametrize("B,H,W,vmax", [(1, 40, 48, 6.0), (2, 37, 53, 12.0), (3, 20, 24, 30.0)])
+def test_warp_splat_gather_matches_oracle(B, H, W, vmax, mask):
+    """Small windows: several batch entries, flows that carry events out of the sensor (masked, or splatted onto
+    the border with base corner -1), a value gradient and an image gradient together."""
+    print(f"warp_splat_gather oracle B={B} {H}x{W} vmax={vmax} mask={mask}", flush=True)
+    win = synth.small_window(seed=B + H, n=4000, H=H, W=W, vmax=vmax, B=B)
+    rng = np.random.default_rng(B)
+    grid = win.motion["grid"].astype(F32)
+    gvals = rng.standard_normal(win.n).astype(F32)
+    gimg = rng.standard_normal((B, H, W)).astype(F32)
+    t_ref = 0.37
+    want_img, want_vals, want_g = oracle_wsg(grid, win.xy, win.t, win.b, t_ref, B, H, W, mask, gvals, gimg)
+    tg = T(grid).requires_grad_(True)
+    img, vals = F.warp_splat_gather(tg, T(win.xy), T(win.t), T(win.b), t_ref, H, W, mask)
+    close_rel(N(img), want_img, 1e-5)
+    close_rel(N(vals), want_vals, 1e-5)
+    ((vals * T(gvals)).sum() + (img * T(gimg)).sum()).backward()
+    close_rel(N(tg.grad), want_g, 1e-4)
+
+
+def test_warp_splat_gather_values_only_and_image_only():
+    """Gradients through one output at a time (the other's gradient absent)."""
+    win = synth.small_window(seed=5, n=5000, H=30, W=44, vmax=8.0, B=2)
+    grid = win.motion["grid"].astype(F32)
+    rng = np.random.default_rng(9)
+    gvals = rng.standard_normal(win.n).astype(F32)
+    gimg = rng.standard_normal((2, 30, 44)).astype(F32)
+    for use_vals in (True, False):
+        print(f"warp_splat_gather one output: vals={use_vals}", flush=True)
+        gv = gvals if use_vals else np.zeros_like(gvals)
+        gi = np.zeros_like(gimg) if use_vals else gimg
+        _, _, want_g = oracle_wsg(grid, win.xy, win.t, win.b, 0.5, 2, 30, 44, True, gv, gi)
+        tg = T(grid).requires_grad_(True)
+        img, vals = F.warp_splat_gather(tg, T(win.xy), T(win.t), T(win.b), 0.5, 30, 44)
+        ((vals * T(gvals)).sum() if use_vals else (img * T(gimg)).sum()).backward()
+        close_rel(N(tg.grad), want_g, 1e-4)
+
+
+def test_warp_splat_gather_full_size_matches_oracle_and_composed():
+    """The IWE workload itself: 1M events, 640x480, dense flow of up to 20 px per window, t_ref = 0.5, inside
+    mask, loss = sum of the gathered values; against the oracle and against transport -> make_iwe -> gather on
+    the device."""
+    win = synth.dense_flow_window(seed=0)
+    ev = EventPacket.from_window(win, DEV)
+    grid = win.motion["grid"].astype(F32)
+    H, W = win.height, win.width
+    print("warp_splat_gather full size: oracle", flush=True)
+    want_img, want_vals, want_g = oracle_wsg(grid, win.xy, win.t, win.b, 0.5, 1, H, W, True,
+                                             np.ones(win.n, F32), np.zeros((1, H, W), F32))
+    print("warp_splat_gather full size: fused", flush=True)
+    motion = DenseLinearFlow(1, H, W, grid=grid.shape[-2:], init=torch.as_tensor(grid)).to(DEV)
+    cfg = IWEConfig(kernel="bilinear", sigma=0.0, mask_border=True)
+    img, vals = iwe_at_events(ev, motion, 0.5, cfg)
+    vals.sum().backward()
+    g_fused = N(motion.grid.grad)
+    close_rel(N(img), want_img, 1e-5)
+    close_rel(N(vals), want_vals, 1e-5)
+    close_rel(g_fused, want_g, 1e-4)
+    print("warp_splat_gather full size: composed device path", flush=True)
+    motion.grid.grad = None
+    y = motion.transport(ev.xy, ev.t, 0.5, ev.b)
+    img2 = make_iwe(ev, y, 0.5, cfg)
+    F.gather(img2, y, ev.b).sum().backward()
+    close_rel(N(img), N(img2), 1e-5)
+    close_rel(g_fused, N(motion.grid.grad), 1e-4)
+
+
+def test_warp_splat_gather_rejects_bad_shapes():
+    xy = torch.zeros(10, 2, device=DEV)
+    t = torch.zeros(10, device=DEV)
+    b = torch.zeros(10, dtype=torch.long, device=DEV)
+    with pytest.raises(ValueError):
+        F.warp_splat_gather(torch.zeros(1, 3, 8, 8, device=DEV), xy, t, b, 0.5, 8, 8)
+    with pytest.raises(ValueError):
+        F.warp_splat_gather(torch.zeros(1, 2, 8, 8, device=DEV), xy, t[:5], b, 0.5, 8, 8)

@@ -18,6 +18,7 @@
 // set of touched pixels is identical; only the order of the float additions differs.
 #include "common.h"
 #include "scan.h"
+#include "bilinear.h"
 #include "../../include/atl_hip.h"
 
 #include <cmath>
@@ -34,7 +35,9 @@ constexpr int kTileMaxKeys = 16384;              // LDS histogram capacity (tile
 constexpr int kAccBlock = 256;                   // accumulation: threads per tile
 constexpr int kMaxChannels = 32;                 // field channels of the tile adjoint (LDS: C x 17 x 17 floats)
 
-enum { kImage = 0, kGrid = 1, kGauss = 2, kVoxel = 3, kGridVal = 4 };   // kGridVal: kGrid, values in the records
+enum { kImage = 0, kGrid = 1, kGauss = 2, kVoxel = 3, kGridVal = 4, kImageG = 5 };
+// kGridVal: kGrid with the values in the records; kImageG: kImage records (x, y, w, index) accumulating the
+// per-event value gout[index] instead of w (the gather's image gradient on the splat's records)
 constexpr int kMaxGaussRadius = 8;               // truncated-Gaussian splats of larger radius stay per event
 
 struct TileGeo {
@@ -49,6 +52,8 @@ struct TileGeo {
   int scale;                 // kGrid: positions are image pixels mapped by sxw, syh
   float sxw, syh;
   int vec4;                  // kGrid: C % 4 == 0 and gout 16-byte aligned (rows read as float4)
+  int ilv;                   // flush: element 2 p + 1 of out for output element p when ilv = 2 (the odd
+                             // slots of an interleaved (value, gradient) image), element p otherwise
 };
 
 __device__ __forceinline__ bool batch_ok(int64_t b, int64_t B) { return b >= 0 && b < B; }
@@ -125,10 +130,12 @@ __device__ __forceinline__ int tile_key(float x, float y, int64_t b, const TileG
   return ((int)b * g.TY + ty) * g.TX + tx;
 }
 
-// Binning.  SCATTER = false: per-block tile histogram into cnt[key * nblk + block].  SCATTER = true: the
-// block's scanned offsets are loaded into LDS and every event writes (x, y, value, index) to its slot; kVoxel
-// writes (x, y, polarity, t * (C - 1)) (aux = t) and skips events whose time bins both miss [0, C).
-template <int MODE, bool SCATTER>
+// Binning.  SCATTER = false: per-block tile histogram into cnt[block * nkeys + key] (rows written coalesced; the
+// scan reads them transposed, key-major).  SCATTER = true: the block's scanned offsets (boff[key * nblk + block])
+// are loaded into LDS and every event writes (x, y, value, index) to its slot; kVoxel
+// writes (x, y, polarity, t * (C - 1)) (aux = t) and skips events whose time bins both miss [0, C).  Events of
+// value zero are skipped unless SKIP_ZERO is false (records whose index also serves a second accumulation).
+template <int MODE, bool SCATTER, bool SKIP_ZERO = true>
 __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __restrict__ pos,
                                                             const int64_t* __restrict__ bidx,
                                                             const float* __restrict__ val, TileGeo g,
@@ -162,7 +169,8 @@ __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __rest
 #pragma unroll
   for (int u = 0; u < per; ++u) {
     const int j = j0 + u * kTileBinBlock + threadIdx.x;
-    if (j >= g.N || (vj[u] == 0.f && v2[u] == 0.f)) continue;   // a zero weight adds nothing (csrc/atl_cpu.cpp:44)
+    if (j >= g.N || (SKIP_ZERO && vj[u] == 0.f && v2[u] == 0.f)) continue;   // a zero weight adds nothing
+                                                                              // (csrc/atl_cpu.cpp:44)
     float tn = 0.f;
     if (MODE == kVoxel) {                         // csrc/atl_cpu.cpp:265: tn = t * (C - 1)
       tn = aux[j] * (float)(g.C - 1);
@@ -178,7 +186,7 @@ __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __rest
   }
   if (!SCATTER) {
     __syncthreads();
-    for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) cnt[i * g.nblk + blk] = hist[i];
+    for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) cnt[(int64_t)blk * g.nkeys + i] = hist[i];
   }
 }
 
@@ -232,9 +240,10 @@ __device__ __forceinline__ void accum_record(const float4& q, const float* __res
         }
       }
     }
-  } else if (MODE == kImage) {
+  } else if (MODE == kImage || MODE == kImageG) {
     int x0, y0;
     if (!image_base(q.x, q.y, g.H, g.W, x0, y0)) return;   // never taken: the binning applied this test
+    const float val = MODE == kImageG ? gout[__float_as_int(q.w)] : q.z;
     const float fx = (float)x0, fy = (float)y0;
     const float ax = q.x - fx, ay = q.y - fy;
     const float wx0 = 1.f - ax, wy0 = 1.f - ay;
@@ -249,7 +258,7 @@ __device__ __forceinline__ void accum_record(const float4& q, const float* __res
         if (xx < 0 || xx >= g.W) continue;
         const float wx = ix ? ax : wx0;
         const int ly = yy - oy, lx = xx - ox;
-        if ((unsigned)ly < (unsigned)L && (unsigned)lx < (unsigned)L) atomicAdd(acc + ly * L + lx, q.z * (wx * wy));
+        if ((unsigned)ly < (unsigned)L && (unsigned)lx < (unsigned)L) atomicAdd(acc + ly * L + lx, val * (wx * wy));
       }
     }
   } else if (MODE == kGridVal) {                  // record (x, y, g0, g1): no gather of the gradient rows
@@ -367,7 +376,7 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int4* __restrict
   const int plane = g.TY * g.TX;
   const int b = key / plane, r = key - b * plane;
   const int ty = r / g.TX, tx = r - ty * g.TX;
-  const bool img_org = MODE == kImage || MODE == kVoxel;
+  const bool img_org = MODE == kImage || MODE == kImageG || MODE == kVoxel;
   const int ox = img_org ? tx * T - 1 : MODE == kGauss ? tx * T - 2 * g.R : tx * T;   // LDS column 0
   const int oy = img_org ? ty * T - 1 : MODE == kGauss ? ty * T - 2 * g.R : ty * T;
 #pragma unroll
@@ -379,7 +388,10 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int4* __restrict
     if (py < 0 || py >= g.H || px < 0 || px >= g.W) continue;
     for (int ch = 0; ch < nc; ++ch) {
       const float v = acc[ch * L * L + a];
-      if (v != 0.f) atomicAdd(out + ((int64_t)b * nc + ch) * pl + (int64_t)py * g.W + px, v);
+      if (v != 0.f) {
+        const int64_t o = ((int64_t)b * nc + ch) * pl + (int64_t)py * g.W + px;
+        atomicAdd(out + (g.ilv == 2 ? 2 * o + 1 : o), v);
+      }
     }
   }
 }
@@ -403,14 +415,14 @@ static_assert(kBins == kAccBlock, "one accumulation thread per base corner");
 template <int MODE, int C>
 __device__ __forceinline__ bool bin_record(const float4& q, const float* __restrict__ gout, const TileGeo& g, int ox,
                                            int oy, int& bx, int& by, float& ax, float& ay, float (&val)[C]) {
-  if (MODE == kImage) {
+  if (MODE == kImage || MODE == kImageG) {
     int x0, y0;
     if (!image_base(q.x, q.y, g.H, g.W, x0, y0)) return false;
     ax = q.x - (float)x0;                         // the scatter form's wx1, wy1 (csrc/atl_cpu.cpp:46-53)
     ay = q.y - (float)y0;
     bx = x0 - ox;
     by = y0 - oy;
-    val[0] = q.z;
+    val[0] = MODE == kImageG ? gout[__float_as_int(q.w)] : q.z;
   } else {
     const GridCell c = grid_cell(q.x, q.y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
     ax = c.ax;
@@ -449,8 +461,9 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum_bins(const int4* __res
   const int plane = g.TY * g.TX;
   const int b = key / plane, r = key - b * plane;
   const int ty = r / g.TX, tx = r - ty * g.TX;
-  const int ox = MODE == kImage ? tx * T - 1 : tx * T;   // window column 0
-  const int oy = MODE == kImage ? ty * T - 1 : ty * T;
+  constexpr bool kImg = MODE == kImage || MODE == kImageG;
+  const int ox = kImg ? tx * T - 1 : tx * T;     // window column 0
+  const int oy = kImg ? ty * T - 1 : ty * T;
   float s[4][C];                                  // this thread's base corner: corner sums over the rounds
 #pragma unroll
   for (int k = 0; k < 4; ++k)
@@ -511,7 +524,7 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum_bins(const int4* __res
     for (int ch = 0; ch < C; ++ch) bsum[k * C + ch][tid] = s[k][ch];
   __syncthreads();
   // the second corner of an axis is the next pixel, or the same one on a grid of a single column (row)
-  const int sx = MODE == kImage || g.W > 1 ? 1 : 0, sy = MODE == kImage || g.H > 1 ? 1 : 0;
+  const int sx = kImg || g.W > 1 ? 1 : 0, sy = kImg || g.H > 1 ? 1 : 0;
   for (int a = tid; a < L * L; a += kAccBlock) {
     const int ly = a / L, lx = a - ly * L;
     const int py = oy + ly, px = ox + lx;
@@ -528,7 +541,10 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum_bins(const int4* __res
     }
 #pragma unroll
     for (int ch = 0; ch < C; ++ch)
-      if (v[ch] != 0.f) atomicAdd(out + ((int64_t)b * C + ch) * pl + (int64_t)py * g.W + px, v[ch]);
+      if (v[ch] != 0.f) {
+        const int64_t o = ((int64_t)b * C + ch) * pl + (int64_t)py * g.W + px;
+        atomicAdd(out + (g.ilv == 2 ? 2 * o + 1 : o), v[ch]);
+      }
   }
 }
 
@@ -733,6 +749,7 @@ bool tile_geo(int mode, int64_t B, int64_t H, int64_t W, int64_t N, int64_t img_
   if (B < 1 || H < 1 || W < 1 || N < 0 || N >= ((int64_t)1 << 30) || (double)B * H * W >= 2.0e9) return false;
   if (mode == kGauss && (R < 0 || R > kMaxGaussRadius)) return false;
   g.vec4 = 0;
+  g.ilv = 1;
   const int64_t ext = mode == kGauss ? 2 * R : 1;   // base corners / centres span W + ext positions per row
   for (int T : {16, 32}) {
     const int64_t tx = (W + ext + T - 1) / T, ty = (H + ext + T - 1) / T;
@@ -790,7 +807,7 @@ void tile_bin(const TileGeo& g, const TileLayout& L, void* ws, const float* pos,
   const size_t lds = (size_t)g.nkeys * sizeof(int);
   hipLaunchKernelGGL((k_tile_bin<MODE, false>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
                      b, val, g, cnt, (float4*)nullptr, aux);
-  scan32(cnt, (int64_t)g.nkeys * g.nblk, (int*)(w + L.part), boff, stream);
+  scan32t(cnt, g.nkeys, g.nblk, (int*)(w + L.part), boff, stream);
   hipLaunchKernelGGL((k_tile_bin<MODE, true>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
                      b, val, g, boff, (float4*)(w + L.rec), aux);
 }
@@ -802,17 +819,20 @@ bool tile_scatter_form() {
   return e && e[0] == '1';
 }
 
+// listed: the chunk list in ws is already that of this form (an earlier accumulation on the same records).
 template <int MODE, int C>
 void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const float* gout, float* out,
-                hipStream_t stream) {
+                hipStream_t stream, bool listed = false) {
   if (g.nblk == 0) return;
   char* w = (char*)ws;                             // the chunk list is written here (a part of the plan)
   int4* info = (int4*)(w + L.info);
   int* nchunk = (int*)(w + L.nchunk);
-  constexpr bool kGatherForm = MODE == kImage || MODE == kGridVal || (MODE == kGrid && C >= 1 && C <= 4);
+  constexpr bool kGatherForm =
+      MODE == kImage || MODE == kImageG || MODE == kGridVal || (MODE == kGrid && C >= 1 && C <= 4);
   const bool gather = kGatherForm && g.T == kBinT && !tile_scatter_form();
-  hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.boff), g,
-                     kAccChunk, gather ? kBinChunk : kAccChunk, info, nchunk);
+  if (!listed)
+    hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.boff), g,
+                       kAccChunk, gather ? kBinChunk : kAccChunk, info, nchunk);
   const unsigned grid = (unsigned)max_chunks(g);  // workgroups past the chunk count return at once
   const int nc = C > 0 ? C : g.C;
   const size_t edge = MODE == kGauss ? (size_t)(g.T + 2 * g.R) : (size_t)(g.T + 1);
@@ -859,6 +879,254 @@ int noalloc_scratch(void** out) {
   }
   *out = g_scratch_ptr[dev];
   return 0;
+}
+
+// ------------------------------------------------------------------------------------ warp -> splat -> gather
+// The image of warped events sampled back at the events, forward and backward to a dense flow grid, in one
+// sequence of launches (the composition atl/motion/parametric.py:53-56 -> atl/objectives/base.py:40-60 ->
+// atl/ops/functional.py:67-87 with the flow of parametric.py:212-216):
+//   v_j = sample(grid, x_j), y_j = x_j + v_j (t_ref - t_j), w_j = [y_j inside the sensor] (or 1),
+//   img = splat(y, w), vals_j = gather(img, y_j).
+// The forward bins the warped events by image tile (the histogram is taken by the warp kernel itself) and keeps
+// y, w and the records for the backward, which splats the value gradient on those records, forms each event's
+// position gradient and flow gradient in one per-event kernel (with the flow grid's tile histogram), and
+// accumulates the flow-grid adjoint on the tile engine.  Every per-event expression is the composed path's, in
+// its fp32 order.
+struct WsgLayout {
+  TileGeo gi, gg;              // image tiles (kImage / kImageG), flow-grid tiles (kGridVal, 2 channels)
+  TileLayout Li, Lg;
+  int64_t ai, ag;              // byte offsets of the two tile-engine regions
+  int64_t y, w, gv, G, bytes;  // warped positions (N float2), weights (N), flow gradients (N float2), and the
+                               // (image, image gradient) pairs (B H W float2)
+};
+
+bool wsg_layout(int64_t N, int64_t B, int64_t H, int64_t W, int64_t Hg, int64_t Wg, WsgLayout& L) {
+  if (N < 1 || B < 1 || H < 1 || W < 1 || Hg < 1 || Wg < 1) return false;
+  if (!tile_geo(kImage, B, H, W, N, 0, 0, L.gi) || !tile_geo(kGridVal, B, Hg, Wg, N, H, W, L.gg)) return false;
+  if (B * H * W >= ((int64_t)1 << 31) || B * 2 * Hg * Wg >= ((int64_t)1 << 31)) return false;
+  L.gg.C = 2;
+  L.Li = tile_layout(L.gi);
+  L.Lg = tile_layout(L.gg);
+  int64_t off = 0;
+  L.ai = off; off += align256(L.Li.bytes);
+  L.ag = off; off += align256(L.Lg.bytes);
+  L.y = off;  off += align256(N * 8);
+  L.w = off;  off += align256(N * 4);
+  L.gv = off; off += align256(N * 8);
+  L.G = off;  off += align256(B * H * W * 8);
+  L.bytes = off;
+  return true;
+}
+
+// Warp, weight and the image-tile histogram, with the block partition of k_tile_bin (4096 events per block) so
+// that its scatter pass finds the same per-block counts.  Every event with an in-image base corner is counted,
+// masked ones (w = 0) included: the value gradient of the gather reaches them.
+__global__ void __launch_bounds__(kTileBinBlock) k_wsg_warp(const float* __restrict__ grid, int Hg, int Wg,
+                                                            float sxw, float syh, const float2* __restrict__ xy,
+                                                            const float* __restrict__ t,
+                                                            const int64_t* __restrict__ bidx, float t_ref, int mask,
+                                                            TileGeo g, float2* __restrict__ y, float* __restrict__ w,
+                                                            int* __restrict__ cnt) {
+  extern __shared__ int hist[];
+  const int blk = blockIdx.x;
+  for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) hist[i] = 0;
+  constexpr int per = kTilePerBlock / kTileBinBlock;
+  const int j0 = blk * kTilePerBlock;
+  const int64_t plane = (int64_t)Hg * Wg;
+  const float wmax = (float)(g.W - 1), hmax = (float)(g.H - 1);
+  float2 p[per];
+  float tj[per];
+  int64_t bj[per];
+#pragma unroll
+  for (int u = 0; u < per; ++u) {                 // every event's inputs first, then every flow row
+    const int j = j0 + u * kTileBinBlock + threadIdx.x;
+    bj[u] = j < g.N ? bidx[j] : -1;
+    p[u] = j < g.N ? xy[j] : make_float2(0.f, 0.f);
+    tj[u] = j < g.N ? t[j] : 0.f;
+  }
+  float4 ra[per], rb[per];                        // (row 0, row 1) corner pairs of the two flow channels
+  GridCorners c[per];
+#pragma unroll
+  for (int u = 0; u < per; ++u) {
+    c[u] = grid_corners(p[u].x, p[u].y, Hg, Wg, sxw, syh, true);
+    ra[u] = rb[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!batch_ok(bj[u], g.B)) continue;          // sample_grid of an event outside the batch: zero
+    const float* f = grid + bj[u] * 2 * plane;
+    if (Wg >= 2) {                                // o01 = o00 + 1, o11 = o10 + 1: one 8-byte load per row
+      float2 r0, r1, q0, q1;
+      __builtin_memcpy(&r0, f + c[u].o00, sizeof(float2));
+      __builtin_memcpy(&r1, f + c[u].o10, sizeof(float2));
+      __builtin_memcpy(&q0, f + plane + c[u].o00, sizeof(float2));
+      __builtin_memcpy(&q1, f + plane + c[u].o10, sizeof(float2));
+      ra[u] = make_float4(r0.x, r0.y, r1.x, r1.y);
+      rb[u] = make_float4(q0.x, q0.y, q1.x, q1.y);
+    } else {
+      ra[u] = make_float4(f[c[u].o00], f[c[u].o01], f[c[u].o10], f[c[u].o11]);
+      rb[u] = make_float4(f[plane + c[u].o00], f[plane + c[u].o01], f[plane + c[u].o10], f[plane + c[u].o11]);
+    }
+  }
+  __syncthreads();                                // the histogram is cleared
+#pragma unroll
+  for (int u = 0; u < per; ++u) {
+    const int j = j0 + u * kTileBinBlock + threadIdx.x;
+    if (j >= g.N) continue;
+    float vx = ra[u].x * c[u].w00;                // atl/motion/parametric.py:235-251, the device sampler's order
+    vx = vx + ra[u].y * c[u].w01;
+    vx = vx + ra[u].z * c[u].w10;
+    vx = vx + ra[u].w * c[u].w11;
+    float vy = rb[u].x * c[u].w00;
+    vy = vy + rb[u].y * c[u].w01;
+    vy = vy + rb[u].z * c[u].w10;
+    vy = vy + rb[u].w * c[u].w11;
+    if (!batch_ok(bj[u], g.B)) vx = vy = 0.f;
+    const float step = t_ref - tj[u];             // parametric.py:53-56: x + v * (t_ref - t)
+    const float yx = p[u].x + vx * step, yy = p[u].y + vy * step;
+    const float wj = !mask || (yx >= 0.f && yx <= wmax && yy >= 0.f && yy <= hmax) ? 1.f : 0.f;
+    y[j] = make_float2(yx, yy);
+    w[j] = wj;
+    const int key = tile_key<kImage>(yx, yy, bj[u], g);
+    if (key >= 0) atomicAdd(hist + key, 1);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) cnt[(int64_t)blk * g.nkeys + i] = hist[i];
+}
+
+// vals_j = gather(img, y_j): csrc/atl_cpu.cpp:134-149.
+__global__ void __launch_bounds__(kBlock) k_wsg_gather(const float* __restrict__ img, const float2* __restrict__ y,
+                                                       const int64_t* __restrict__ bidx, int64_t N, int64_t B, int H,
+                                                       int W, float* __restrict__ vals) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  float s = 0.f;
+  const float2 p = y[n];
+  const float fx = floorf(p.x), fy = floorf(p.y);
+  if (batch_ok(b, B) && fx >= -1.f && fx <= (float)(W - 1) && fy >= -1.f && fy <= (float)(H - 1)) {
+    const float* base = img + b * (int64_t)H * W;  // for_corners' corners and order, one 8-byte load per row
+    const int x0 = (int)fx, y0 = (int)fy;
+    const float ax = p.x - fx, ay = p.y - fy;
+    const float wx0 = 1.f - ax, wy0 = 1.f - ay;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int yy = y0 + j;
+      if (yy < 0 || yy >= H) continue;
+      const float wy = j ? ay : wy0;
+      const float* row = base + (int64_t)yy * W;
+      if (x0 >= 0 && x0 + 1 < W) {
+        float2 r;
+        __builtin_memcpy(&r, row + x0, sizeof(float2));
+        s += (wx0 * wy) * r.x;
+        s += (ax * wy) * r.y;
+      } else {
+        if (x0 >= 0) s += (wx0 * wy) * row[x0];
+        if (x0 + 1 < W) s += (ax * wy) * row[x0 + 1];
+      }
+    }
+  }
+  vals[n] = s;
+}
+
+// The backward's image pair: ig[p] = (img[p], gimg[p] or 0); the value gradient's splat is then added into the
+// second slots, and the per-event gradient reads both images of a corner row with one 16-byte load.
+__global__ void __launch_bounds__(kBlock) k_wsg_pack(const float* __restrict__ img, const float* __restrict__ gimg,
+                                                     int64_t n, float2* __restrict__ ig) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) ig[i] = make_float2(img[i], gimg ? gimg[i] : 0.f);
+}
+
+// Per-event gradient: the position gradient of the gather (gvals_j * grad img(y_j), csrc/atl_cpu.cpp:151-172) plus
+// that of the splat (w_j * grad G(y_j), csrc/atl_cpu.cpp:58-76, G the image gradient), times (t_ref - t_j) for the
+// flow sampled at x_j; and the flow-grid tile histogram of those rows (zero rows skipped, as k_tile_bin<kGridVal>
+// skips them), with k_tile_bin's block partition.
+__global__ void __launch_bounds__(kTileBinBlock) k_wsg_grad(const float2* __restrict__ ig,
+                                                            const float* __restrict__ gvals,
+                                                            const float2* __restrict__ y, const float* __restrict__ w,
+                                                            const float2* __restrict__ xy,
+                                                            const float* __restrict__ t,
+                                                            const int64_t* __restrict__ bidx, float t_ref,
+                                                            int H, int W, TileGeo gg, float2* __restrict__ gv,
+                                                            int* __restrict__ cnt) {
+  extern __shared__ int hist[];
+  const int blk = blockIdx.x;
+  for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) hist[i] = 0;
+  constexpr int per = kTilePerBlock / kTileBinBlock;
+  const int j0 = blk * kTilePerBlock;
+  const int64_t pl = (int64_t)H * W;
+  float2 p[per];
+  int64_t bj[per];
+#pragma unroll
+  for (int u = 0; u < per; ++u) {                 // positions first, then every corner row of every event
+    const int j = j0 + u * kTileBinBlock + threadIdx.x;
+    bj[u] = j < gg.N ? bidx[j] : -1;
+    p[u] = j < gg.N ? y[j] : make_float2(0.f, 0.f);
+  }
+  float4 row[per][2];                             // per corner row: (img, G) at x0 and at x0 + 1
+#pragma unroll
+  for (int u = 0; u < per; ++u) {
+    const float fx = floorf(p[u].x), fy = floorf(p[u].y);
+    const bool ok = batch_ok(bj[u], gg.B) && fx >= -1.f && fx <= (float)(W - 1) && fy >= -1.f &&
+                    fy <= (float)(H - 1);
+    const int x0 = ok ? (int)fx : 0, y0 = ok ? (int)fy : 0;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      row[u][r] = make_float4(0.f, 0.f, 0.f, 0.f);
+      const int yy = y0 + r;
+      if (!ok || yy < 0 || yy >= H) continue;
+      const float2* q = ig + bj[u] * pl + (int64_t)yy * W;
+      if (x0 >= 0 && x0 + 1 < W) {
+        __builtin_memcpy(&row[u][r], q + x0, sizeof(float4));   // both corners: one 16-byte load
+      } else {
+        if (x0 >= 0) { const float2 c = q[x0]; row[u][r].x = c.x; row[u][r].y = c.y; }
+        if (x0 + 1 < W) { const float2 c = q[x0 + 1]; row[u][r].z = c.x; row[u][r].w = c.y; }
+      }
+    }
+  }
+  __syncthreads();                                // the histogram is cleared
+#pragma unroll
+  for (int u = 0; u < per; ++u) {
+    const int j = j0 + u * kTileBinBlock + threadIdx.x;
+    if (j >= gg.N) continue;
+    float s1x = 0.f, s1y = 0.f, s2x = 0.f, s2y = 0.f;
+    const float fx = floorf(p[u].x), fy = floorf(p[u].y);
+    if (batch_ok(bj[u], gg.B) && fx >= -1.f && fx <= (float)(W - 1) && fy >= -1.f && fy <= (float)(H - 1)) {
+      const int x0 = (int)fx, y0 = (int)fy;       // for_corners' corners, weights and order
+      const float ax = p[u].x - fx, ay = p[u].y - fy;
+      const float wx0 = 1.f - ax, wy0 = 1.f - ay;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int yy = y0 + r;
+        if (yy < 0 || yy >= H) continue;
+        const float wy = r ? ay : wy0;
+        const float dwy = r ? 1.f : -1.f;
+        if (x0 >= 0) {                             // corner (x0, yy): wx = 1 - ax, dwx = -1
+          const float dcx = -1.f * wy, dcy = wx0 * dwy, v = row[u][r].x, q = row[u][r].y;
+          s1x += dcx * v;
+          s1y += dcy * v;
+          s2x += q * dcx;
+          s2y += q * dcy;
+        }
+        if (x0 + 1 < W) {                          // corner (x0 + 1, yy): wx = ax, dwx = 1
+          const float dcx = 1.f * wy, dcy = ax * dwy, v = row[u][r].z, q = row[u][r].w;
+          s1x += dcx * v;
+          s1y += dcy * v;
+          s2x += q * dcx;
+          s2y += q * dcy;
+        }
+      }
+    }
+    const float g = gvals ? gvals[j] : 0.f;
+    const float wj = w[j];
+    const float gx = g * s1x + wj * s2x, gy = g * s1y + wj * s2y;
+    const float step = t_ref - t[j];
+    const float vx = gx * step, vy = gy * step;
+    gv[j] = make_float2(vx, vy);
+    if (vx == 0.f && vy == 0.f) continue;
+    const float2 x = xy[j];
+    const int key = tile_key<kGridVal>(x.x, x.y, bj[u], gg);
+    if (key >= 0) atomicAdd(hist + key, 1);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) cnt[(int64_t)blk * gg.nkeys + i] = hist[i];
 }
 
 }  // namespace
@@ -1039,6 +1307,73 @@ int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t
       break;
   }
   return check_launch("sample_grid_bwd_planned");
+}
+
+// Warp -> splat -> gather (the fused pipeline above).  Workspace bytes, or -1 for unsupported sizes.
+int64_t atl_warp_splat_gather_ws_bytes(int64_t N, int64_t B, int64_t H, int64_t W, int64_t Hg, int64_t Wg) {
+  WsgLayout L;
+  return wsg_layout(N, B, H, W, Hg, Wg, L) ? L.bytes : -1;
+}
+
+int atl_warp_splat_gather_fwd(const float* grid, int64_t B, int64_t Hg, int64_t Wg, const float* xy, const float* t,
+                              const int64_t* b, int64_t N, int64_t H, int64_t W, double t_ref, int64_t mask_border,
+                              float* img, float* vals, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  if (N == 0) return 0;
+  WsgLayout L;
+  if (!wsg_layout(N, B, H, W, Hg, Wg, L)) { set_error("warp_splat_gather_fwd: unsupported sizes N=%lld B=%lld H=%lld W=%lld Hg=%lld Wg=%lld", (long long)N, (long long)B, (long long)H, (long long)W, (long long)Hg, (long long)Wg); return 1; }
+  if (!ws || ws_bytes < L.bytes) { set_error("warp_splat_gather_fwd: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
+  if (!grid || !xy || !t || !b || !img) { set_error("warp_splat_gather_fwd: null argument"); return 1; }
+  char* w = (char*)ws;
+  char* wi = w + L.ai;
+  const TileGeo& g = L.gi;
+  float2* y = (float2*)(w + L.y);
+  float* wt = (float*)(w + L.w);
+  const float sxw = (float)(W - 1 > 1 ? W - 1 : 1), syh = (float)(H - 1 > 1 ? H - 1 : 1);
+  const size_t lds = (size_t)g.nkeys * sizeof(int);
+  hipLaunchKernelGGL(k_wsg_warp, dim3(g.nblk), dim3(kTileBinBlock), lds, stream, grid, (int)Hg, (int)Wg, sxw, syh,
+                     (const float2*)xy, t, b, (float)t_ref, (int)(mask_border != 0), g, y, wt, (int*)(wi + L.Li.cnt));
+  scan32t((int*)(wi + L.Li.cnt), g.nkeys, g.nblk, (int*)(wi + L.Li.part), (int*)(wi + L.Li.boff), stream);
+  hipLaunchKernelGGL((k_tile_bin<kImage, true, false>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream,
+                     (const float2*)y, b, (const float*)wt, g, (int*)(wi + L.Li.boff), (float4*)(wi + L.Li.rec),
+                     (const float*)nullptr);
+  tile_accum<kImage, 1>(g, L.Li, wi, nullptr, img, stream);
+  if (vals)
+    hipLaunchKernelGGL(k_wsg_gather, dim3(grid_for(N)), dim3(kBlock), 0, stream, (const float*)img,
+                       (const float2*)y, b, N, B, (int)H, (int)W, vals);
+  return check_launch("warp_splat_gather_fwd");
+}
+
+int atl_warp_splat_gather_bwd(const float* img, const float* gvals, const float* gimg, const float* xy,
+                              const float* t, const int64_t* b, int64_t N, int64_t B, int64_t H, int64_t W,
+                              int64_t Hg, int64_t Wg, double t_ref, float* ggrid, void* ws, int64_t ws_bytes,
+                              hipStream_t stream) {
+  if (N == 0) return 0;
+  WsgLayout L;
+  if (!wsg_layout(N, B, H, W, Hg, Wg, L)) { set_error("warp_splat_gather_bwd: unsupported sizes"); return 1; }
+  if (!ws || ws_bytes < L.bytes) { set_error("warp_splat_gather_bwd: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
+  if (!img || !xy || !t || !b || !ggrid) { set_error("warp_splat_gather_bwd: null argument"); return 1; }
+  char* w = (char*)ws;
+  char* wi = w + L.ai;
+  char* wg = w + L.ag;
+  float2* ig = (float2*)(w + L.G);
+  const int64_t npix = B * H * W;
+  // (img, G) with G = gimg + splat(y, gvals), the image gradient, accumulated on the forward's records
+  hipLaunchKernelGGL(k_wsg_pack, dim3(grid_for(npix)), dim3(kBlock), 0, stream, img, gimg, npix, ig);
+  if (gvals) {
+    TileGeo gi = L.gi;
+    gi.ilv = 2;
+    tile_accum<kImageG, 1>(gi, L.Li, wi, gvals, (float*)ig, stream, true);
+  }
+  const TileGeo& gg = L.gg;
+  hipLaunchKernelGGL(k_wsg_grad, dim3(gg.nblk), dim3(kTileBinBlock), (size_t)gg.nkeys * sizeof(int), stream,
+                     (const float2*)ig, gvals, (const float2*)(w + L.y), (const float*)(w + L.w), (const float2*)xy,
+                     t, b, (float)t_ref, (int)H, (int)W, gg, (float2*)(w + L.gv), (int*)(wg + L.Lg.cnt));
+  scan32t((int*)(wg + L.Lg.cnt), gg.nkeys, gg.nblk, (int*)(wg + L.Lg.part), (int*)(wg + L.Lg.boff), stream);
+  hipLaunchKernelGGL((k_tile_bin<kGridVal, true>), dim3(gg.nblk), dim3(kTileBinBlock),
+                     (size_t)gg.nkeys * sizeof(int), stream, (const float2*)xy, b, (const float*)(w + L.gv), gg,
+                     (int*)(wg + L.Lg.boff), (float4*)(wg + L.Lg.rec), (const float*)nullptr);
+  tile_accum<kGridVal, 2>(gg, L.Lg, wg, nullptr, ggrid, stream);
+  return check_launch("warp_splat_gather_bwd");
 }
 
 }  // extern "C"

@@ -11,7 +11,7 @@ from typing import Optional
 import torch
 
 from ..core.events import EventPacket
-from ..ops import blur, splat
+from ..ops import blur, gather, splat, warp_splat_gather
 
 
 class Objective:
@@ -90,6 +90,23 @@ def sobel(img: torch.Tensor):
     k = torch.stack([kx, kx.t()])[:, None]                    # (2, 1, 3, 3): x then y
     g = torch.nn.functional.conv2d(img[:, None], k, padding=1)
     return g[:, 0], g[:, 1]
+
+
+def iwe_at_events(ev: EventPacket, motion, t_ref: float, cfg: Optional[IWEConfig] = None):
+    """The IWE at ``t_ref`` and its bilinear values at the transported events: ``(img, vals)``, both
+    differentiable with respect to the motion (the reference composes transport, make_iwe and gather:
+    atl/motion/parametric.py:53-56, atl/objectives/base.py:40-60, atl/ops/functional.py:67-87).  A dense flow on
+    the device with a plain bilinear IWE (sigma 0, pooled polarity, no time weight) runs the fused
+    warp -> splat -> gather launches; anything else composes the three ops."""
+    cfg = cfg or IWEConfig(kernel="bilinear", sigma=0.0)
+    from ..motion import DenseLinearFlow
+    fused = (ev.device.type == "cuda" and isinstance(motion, DenseLinearFlow) and cfg.kernel == "bilinear"
+             and cfg.sigma == 0 and cfg.polarity == "pooled" and not cfg.scale_by_dt)
+    if fused:
+        return warp_splat_gather(motion.grid, ev.xy, ev.t, ev.b, t_ref, ev.height, ev.width, cfg.mask_border)
+    xy_ref = motion.transport(ev.xy, ev.t, t_ref, ev.b)
+    img = make_iwe(ev, xy_ref, t_ref, cfg)
+    return img, gather(img, xy_ref, ev.b)
 
 
 def iwe_variance(ev: EventPacket, motion, t_ref: float, cfg: Optional[IWEConfig] = None) -> torch.Tensor:

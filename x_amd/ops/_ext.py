@@ -85,11 +85,14 @@ _SIGS = {
     "atl_voxel_ws_bytes": [_I, _I, _I, _I, _I],
     "atl_voxel_grid_ws": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P],
     "atl_knn_indices": [_P, _I, _P, _I, _I, _I, _P, _P, _I, _P],
+    "atl_warp_splat_gather_ws_bytes": [_I, _I, _I, _I, _I, _I],
+    "atl_warp_splat_gather_fwd": [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _D, _I, _P, _P, _P, _I, _P],
+    "atl_warp_splat_gather_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _D, _P, _P, _I, _P],
 }
 _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.c_int64,
             "atl_tile_ws_bytes": ctypes.c_int64, "atl_splat_gauss_ws_bytes": ctypes.c_int64,
             "atl_anchored_score_mean_scratch_bytes": ctypes.c_int64, "atl_knn_ws_bytes": ctypes.c_int64,
-            "atl_voxel_ws_bytes": ctypes.c_int64,
+            "atl_voxel_ws_bytes": ctypes.c_int64, "atl_warp_splat_gather_ws_bytes": ctypes.c_int64,
 "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):
@@ -146,7 +149,8 @@ _NARG = {"atl_sample_grid_fwd": 7, "atl_sample_grid_bwd_planned": 6, "atl_sample
          "atl_traj_gout": 2,
          "atl_splat_gauss_fwd": 3, "atl_splat_gauss_bwd": 4, "atl_splat_gauss_fwd_ws": 3,
          "atl_gather_bilinear_fwd": 3, "atl_gather_bilinear_bwd_ws": 4, "atl_splat_bilinear_fwd_ws": 3,
-         "atl_splat_bilinear_bwd": 4, "atl_voxel_grid_ws": 4, "atl_voxel_grid": 4}
+         "atl_splat_bilinear_bwd": 4, "atl_voxel_grid_ws": 4, "atl_voxel_grid": 4,
+         "atl_warp_splat_gather_fwd": 7, "atl_warp_splat_gather_bwd": 6}
 
 
 def time_kernels(names, every: int = 1) -> dict:

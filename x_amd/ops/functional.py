@@ -205,6 +205,61 @@ class _SampleGrid(torch.autograd.Function):
         return gf, gp, None, None, None, None
 
 
+class _WarpSplatGather(torch.autograd.Function):
+    """DenseLinearFlow warp -> bilinear splat -> gather in one launch sequence (the composition of
+    atl/motion/parametric.py:53-56, atl/objectives/base.py:40-60 and atl/ops/functional.py:67-87): returns the
+    image of warped events and its values at the warped events; the backward gives the flow grid's gradient.
+    The forward's workspace (warped positions, weights, the binned records) is kept for the backward."""
+
+    @staticmethod
+    def forward(ctx, grid, xy, t, b, t_ref, H, W, mask_border):
+        grid, xy, t, b = _f32(grid), _f32(xy), _f32(t), b.contiguous().long()
+        B, _, Hg, Wg = grid.shape
+        N = xy.shape[0]
+        lib = load_library()
+        nbytes = int(lib.atl_warp_splat_gather_ws_bytes(N, B, H, W, Hg, Wg))
+        if nbytes < 0:
+            raise ValueError(f"warp_splat_gather: unsupported sizes N={N} B={B} {H}x{W}, grid {Hg}x{Wg}")
+        img = torch.zeros(B, H, W, device=xy.device, dtype=F32)
+        vals = torch.empty(N, device=xy.device, dtype=F32)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=xy.device)
+        with torch.cuda.device(xy.device):
+            call("atl_warp_splat_gather_fwd", ptr(grid), B, Hg, Wg, ptr(xy), ptr(t), ptr(b), N, H, W, float(t_ref),
+                 int(bool(mask_border)), ptr(img), ptr(vals), ptr(ws), nbytes, stream_of(xy))
+        ctx.save_for_backward(img, xy, t, b, ws)
+        ctx.shape, ctx.t_ref = (B, H, W, Hg, Wg), float(t_ref)
+        ctx.set_materialize_grads(False)
+        return img, vals
+
+    @staticmethod
+    def backward(ctx, gimg, gvals):
+        img, xy, t, b, ws = ctx.saved_tensors
+        B, H, W, Hg, Wg = ctx.shape
+        if not ctx.needs_input_grad[0] or (gimg is None and gvals is None):
+            return (None,) * 8
+        ggrid = torch.zeros(B, 2, Hg, Wg, device=xy.device, dtype=F32)
+        gimg = None if gimg is None else gimg.contiguous().float()
+        gvals = None if gvals is None else gvals.contiguous().float()
+        with torch.cuda.device(xy.device):
+            call("atl_warp_splat_gather_bwd", ptr(img), ptr(gvals), ptr(gimg), ptr(xy), ptr(t), ptr(b), xy.shape[0],
+                 B, H, W, Hg, Wg, ctx.t_ref, ptr(ggrid), ptr(ws), ws.numel(), stream_of(xy))
+        return ggrid, None, None, None, None, None, None, None
+
+
+def warp_splat_gather(grid: torch.Tensor, xy: torch.Tensor, t: torch.Tensor, b: torch.Tensor, t_ref: float, H: int,
+                      W: int, mask_border: bool = True):
+    """Image of events warped by the dense flow ``grid`` (B, 2, Hg, Wg) to ``t_ref`` and its bilinear values at the
+    warped events: ``(img (B, H, W), vals (N))``, with ``vals.sum()`` (or any loss of img and vals)
+    differentiable with respect to the grid.  The same numbers as ``DenseLinearFlow.transport`` -> ``splat`` ->
+    ``gather`` with the weight ``inside(y)`` (or 1), on the device in one sequence of launches."""
+    if not xy.is_cuda:
+        raise ValueError("warp_splat_gather runs on the GPU (use transport, splat and gather on the CPU)")
+    _check_events(xy, b, t, what="warp_splat_gather")
+    if grid.dim() != 4 or grid.shape[1] != 2:
+        raise ValueError(f"warp_splat_gather: the flow grid must be (B, 2, Hg, Wg), got {tuple(grid.shape)}")
+    return _WarpSplatGather.apply(grid, xy, t, b, float(t_ref), int(H), int(W), bool(mask_border))
+
+
 class _TrajDisplacement(torch.autograd.Function):
     """PixelTrajectories.displacement in one kernel (atl/motion/trajectories.py: d = sum_k c_k(p) g_k(t), the
     coefficients c_k the border-clamped bilinear sample of a (B, 2K, Hg, Wg) grid at grid coordinates p).
