@@ -64,7 +64,7 @@ SLOTS_FWD, SLOTS_BWD = 14, 16          # VALU lane-slots per contributing pair (
 SLOTS_BWD_TRAJ = 20                    # trajectory backward: the pair recomputed (13) + k gS (1) + k gS r (2) +
                                        # position and velocity gradient sums (2 adds, 2 FMAs)
 FLOPS_FWD, FLOPS_BWD = 13, 19          # fp32 flops per contributing pair (FMA = 2, exp = 1)
-KERNEL_OF = {"atl_fast_pair_fwd": "k_fast_fwd<false>", "atl_fast_pair_bwd": "k_fast_bwd",
+KERNEL_OF = {"atl_fast_pair_fwd": "k_fast_fwd<false>", "atl_fast_pair_bwd": "k_fast_bwd", "atl_fast_pair_bwd_src": "k_fast_bwd",
              "atl_fast_pair_bwd_traj": "k_fast_bwd_traj<10>"}
 COUNTERS = ROOT / "profiles" / "anchored_score_1M_640x480_counters.md"
 
@@ -729,7 +729,10 @@ def main():
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
-    kernels = (["atl_ats_pair_fwd", "atl_ats_pair_bwd"] if reflayout else ["atl_fast_pair_fwd", "atl_fast_pair_bwd"]) + (
+    # the pair kernels first (the roofline's candidates); the objective's dense flow takes the flow path, whose
+    # backward is the pair backward (atl_fast_pair_bwd_src) and then the flow-grid adjoint
+    kernels = (["atl_ats_pair_fwd", "atl_ats_pair_bwd"] if reflayout else
+               ["atl_fast_pair_fwd", "atl_fast_pair_bwd_src", "atl_fast_flow_adjoint"]) + (
         ["atl_splat_bilinear_fwd_ws", "atl_splat_bilinear_bwd"] if blobs else [])
     rec = _ext.time_kernels(kernels, every=4)      # every bracket delays the next launch: sample the steps
     first_draw = obj._philox[1]

@@ -255,6 +255,18 @@ int atl_fast_plan(const atl_fast_geometry* geo, const float* x, const float* t, 
 int atl_fast_pair_fwd(const atl_fast_geometry* geo, const void* ws, float* out, int* count, hipStream_t stream);
 /* gv (N,2) written: each source's gradient, zero for sources outside the plan (no fill needed). */
 int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, float* gv, hipStream_t stream);
+/* The same backward when the velocities were DenseLinearFlow.field(x) (atl/motion/parametric.py:212-216,
+ * 235-251): the gradient goes to the flow grid (B,2,Hg,Wg), accumulated into ggrid (zero it first), as
+ * atl_fast_pair_bwd followed by sample_grid's adjoint at x would give it (float sums in another order), with no
+ * per-event gradient array.  img_h, img_w: the pixel -> grid scaling of atl_sample_grid_fwd (0, 0: x are grid
+ * coordinates).  The plan's temporary sort records (dead after the plan) hold the per-source gradients. */
+int atl_fast_pair_bwd_flow(const atl_fast_geometry* geo, void* ws, const float* gS, int64_t Hg, int64_t Wg,
+                           int64_t img_h, int64_t img_w, float* ggrid, hipStream_t stream);
+/* atl_fast_pair_bwd_flow in its two steps: the pair backward (the source gradients, kept in ws), then the
+ * adjoint into ggrid.  Run them in this order on one stream, with nothing in between that rebuilds the plan. */
+int atl_fast_pair_bwd_src(const atl_fast_geometry* geo, void* ws, const float* gS, hipStream_t stream);
+int atl_fast_flow_adjoint(const atl_fast_geometry* geo, void* ws, int64_t Hg, int64_t Wg, int64_t img_h,
+                          int64_t img_w, float* ggrid, hipStream_t stream);
 
 /* The same fused pair sums for trajectory motion (the anchored score with PixelTrajectories, which the
  * reference's exact kernel does not take: atl/objectives/ats.py:77-78 requires motion linear at the event).

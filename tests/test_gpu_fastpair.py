@@ -247,3 +247,58 @@ def test_fast_blob_contention_matches_reference_layout():
     assert np.allclose(N(plan.forward()), want, rtol=1e-5, atol=1e-6 * float(np.abs(want).max()))
     gS = torch.randn(len(anchors), device=DEV, generator=torch.Generator(device=DEV).manual_seed(5))
     close_rel(N(plan.backward(gS)), N(e.ats_pair_bwd(gS, *args, win.n)), 1e-4)
+
+
+@pytest.mark.parametrize("B,H,W,Hg,Wg,h", [(2, 40, 48, 40, 48, 1.0), (2, 37, 53, 9, 14, 0.5), (1, 30, 36, 30, 1, 2.0),
+                                            (3, 24, 20, 2, 2, 1.0)])
+def test_pair_sums_flow_matches_oracle(B, H, W, Hg, Wg, h):
+    """ats_pair_sums_flow (the flow sampled inside, its gradient accumulated over the plan's source records) against
+    the oracle: sums within 1e-5, and the flow-grid gradient (pair backward, then sample_grid's adjoint) within
+    1e-4, on full-resolution, coarse and degenerate grids, with sources far outside the sensor (clamped into the
+    border nodes and the plan's box, so that their records fall outside the tile's window)."""
+    print(f"pair sums flow B={B} {H}x{W} grid {Hg}x{Wg} h={h}", flush=True)
+    rng = np.random.default_rng(B * 100 + Hg)
+    n = 2500 * B
+    win = synth.small_window(seed=Hg + Wg, n=n // B, H=H, W=W, B=B)
+    grid = (rng.standard_normal((B, 2, Hg, Wg)) * 4.0).astype(F32)
+    xs = (win.xy + rng.uniform(-0.5, 0.5, win.xy.shape)).astype(F32)
+    xs[::97] = np.array([-40.0, 7.5], F32)                       # far outside: clamped in the grid and the box
+    xs[1::101] = np.array([W + 30.0, H + 25.0], F32)
+    xa = (xs + h * rng.standard_normal(xs.shape)).astype(F32)
+    v, idx, wts = O.dense_velocity(grid, xs, win.b, H, W)
+    anchors = np.arange(win.n)
+    p = O.build_pair_plan(xs, win.t, v, win.b, B, H, W, anchors, h, 0.2, 3.0, 16, anchor_xy=xa)
+    want = O.ats_pair_fwd(p, h, 0.2, 3.0)
+    gS = rng.standard_normal(win.n).astype(F32)
+    want_g = O.sample_grid_bwd(O.ats_pair_bwd(gS, p, h, 0.2, 3.0, win.n), idx, wts, grid.shape)
+    tg = T(grid).requires_grad_(True)
+    S = F.ats_pair_sums_flow(tg, T(xs), T(win.t), T(win.b), B, H, W, None, h, 0.2, 3.0, 16, anchor_xy=T(xa))
+    assert np.allclose(N(S), want, rtol=1e-5, atol=1e-6 * max(1.0, float(np.abs(want).max())))
+    (S * T(gS)).sum().backward()
+    close_rel(N(tg.grad), want_g, 1e-4)
+
+
+def test_pair_sums_flow_full_size_matches_composed():
+    """1M events, 640x480, dense flow: the flow path's sums and grid gradient against sampling the flow and calling
+    ats_pair_sums (whose own backward goes through sample_grid's binned adjoint)."""
+    print("pair sums flow vs composed, 1M events", flush=True)
+    win = synth.dense_flow_window(seed=0)
+    H, W = win.height, win.width
+    rng = np.random.default_rng(5)
+    xs = T((win.xy + rng.uniform(-0.5, 0.5, win.xy.shape)).astype(F32))
+    xa = T((N(xs) + rng.standard_normal(win.xy.shape)).astype(F32))
+    t, b = T(win.t), T(win.b)
+    gS = torch.randn(win.n, device=DEV)
+    res = []
+    for fused in (True, False):
+        tg = T(win.motion["grid"]).requires_grad_(True)
+        if fused:
+            S = F.ats_pair_sums_flow(tg, xs, t, b, 1, H, W, None, 1.0, 0.2, 3.0, 16, anchor_xy=xa)
+        else:
+            v = F.sample_grid_hip(tg, xs, b, img_hw=(H, W))
+            S = F.ats_pair_sums(xs, t, v, b, 1, H, W, None, 1.0, 0.2, 3.0, 16, anchor_xy=xa)
+        (S * gS).sum().backward()
+        res.append((N(S), N(tg.grad)))
+    # the same pairs; the within-cell record order follows the plan's LDS atomics, so sums differ in the last bits
+    assert np.allclose(res[0][0], res[1][0], rtol=1e-5, atol=1e-6 * float(np.abs(res[1][0]).max()))
+    close_rel(res[0][1], res[1][1], 1e-4)

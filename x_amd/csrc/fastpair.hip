@@ -31,6 +31,7 @@
 
 #include "common.h"
 #include "scan.h"
+#include "bilinear.h"
 #include "../../include/atl_hip.h"
 
 #include <cmath>
@@ -998,6 +999,14 @@ __global__ void __launch_bounds__(kPairBlock) k_fast_fwd(FPlan p, FGeo G, int M,
 // Finite and small enough that products of two such values stay finite.
 __device__ __forceinline__ bool bounded(float v) { return fabsf(v) < 1e30f; }
 
+// Record range of slice s of (batch b, tile (tb, tx)) in the source records.
+__device__ __forceinline__ int2 src_tile_range(const FPlan& p, const FGeo& G, int b, int s, int tb, int tx, int EA) {
+  const int hb = min(kSrcTile, G.GH - tb * kSrcTile), wt = min(kSrcTile, G.GW - tx * kSrcTile);
+  const int k0 = (b * G.S + s) * (G.GH * G.GW) + tb * kSrcTile * G.GW + tx * kSrcTile * hb;
+  const int* sstart = p.start + 2 * G.ncell_pad;
+  return make_int2(sstart[k0] - EA, sstart[k0 + hb * wt] - EA);
+}
+
 // Backward records of the anchors in cell order, brec[q] = (x, y, t, gS / h^2): one 16-byte load per candidate in
 // the backward's per-lane walks (the anchor's at = t - c_s is recomputed there with the same fp32 operation).
 // Also checks that no event occurs twice among the anchors (self[id] then names only one of the records); an
@@ -1006,7 +1015,7 @@ __device__ __forceinline__ bool bounded(float v) { return fabsf(v) < 1e30f; }
 __global__ void __launch_bounds__(kBlock) k_fast_gather_gs(FPlan p, FGeo G, int M, const float* __restrict__ gS,
                                                            int N, float2* __restrict__ gv) {
   const int q = blockIdx.x * blockDim.x + threadIdx.x;
-  if (q < N) gv[q] = make_float2(0.f, 0.f);
+  if (gv && q < N) gv[q] = make_float2(0.f, 0.f);
   const int Mv = p.start[2 * G.ncell_pad] - p.start[G.ncell_pad];
   // the walks' padding past the last record (Mv <= M: inside the M + kUnroll records): zeros
   if (q < kUnroll) p.brec[Mv + q] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1088,7 +1097,8 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
 // Backward: every source (one lane each, own-slice tile order) sums, over the anchors of each slice of its
 // range within R of its slice-centre position, gS_i * k * dt / h^2 * r (csrc/atl_cpu.cpp:240-248);
 // gv[j] = the total (each source has one record: no atomics).
-__global__ void __launch_bounds__(kPairBlock) k_fast_bwd(FPlan p, FGeo G, int N, float2* __restrict__ gv) {
+__global__ void __launch_bounds__(kPairBlock) k_fast_bwd(FPlan p, FGeo G, int N, float2* __restrict__ gv,
+                                                      float2* __restrict__ gvr) {
   __shared__ int2 tab[kRowTab * kPairBlock];           // per-lane row spans of the current slice (column threadIdx.x)
   constexpr int kSrcPerWave = kWave / kBwdParts;
   const int lb = xcd_block((N + kPairBlock / kBwdParts - 1) / (kPairBlock / kBwdParts));
@@ -1137,7 +1147,221 @@ __global__ void __launch_bounds__(kPairBlock) k_fast_bwd(FPlan p, FGeo G, int N,
     m.x += __shfl_xor(m.x, o);
     m.y += __shfl_xor(m.y, o);
   }
-  if (have && part == 0) gv[si.y] = m;
+  if (have && part == 0) {                         // by event (gv), or by source record (gvr, coalesced)
+    if (gv) gv[si.y] = m;
+    if (gvr) gvr[wbase + ls] = m;
+  }
+}
+
+// Flow-grid adjoint of the velocities v_j = sample(grid, x_j) (atl/motion/parametric.py:235-251 under autograd)
+// over the source records.  The sources are sorted by own-slice cell in 8 x 8-cell tiles, and a source lies within
+// |v| delta / 2 of its own-slice position, so the records of one tile (of all S slices) sit in a compact patch of
+// the grid and need no binning.  k_src_adj_list cuts every (batch, tile)'s records into chunks of at most 1024;
+// k_src_flow_adjoint gives each chunk one workgroup, which accumulates it in the tile engine's gather form: the
+// records are ranked by base node with one LDS integer atomic each, thread c adds value * (wx * wy) of its node's
+// records for the four corners and two channels (the scatter's fp32 products), and every window node adds the
+// sums of the base nodes that reach it and is flushed with one global atomic.  The 16 x 16 window of base nodes
+// starts at the chunk's smallest base node; a record outside it (a position clamped from far outside the box)
+// adds its four corners with global atomics.
+struct FlowGeo {
+  int Hg, Wg;
+  float sxw, syh;              // pixel -> grid scaling of DenseLinearFlow.field (scale on), parametric.py:214-215
+  int scale;
+};
+
+constexpr int kAdjBlock = 256;
+constexpr int kAdjT = 16;                        // window of base nodes
+constexpr int kAdjItems = 4;
+constexpr int kAdjChunk = kAdjBlock * kAdjItems; // records per chunk (one workgroup)
+constexpr int kAdjListBlock = 1024;
+constexpr int kAdjMaxSlices = 64;
+
+// Source records of every (batch, tile) over its S slices: one thread per (tile, slice), the slices of a tile in
+// SP consecutive lanes (SP: S rounded up to a power of two, at most 64), summed across them.
+__global__ void __launch_bounds__(kBlock) k_src_tile_counts(FPlan p, FGeo G, int ntiles, int SP,
+                                                            int* __restrict__ tilecnt) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int q = i / SP, s = i - q * SP;
+  int n = 0;
+  if (q < ntiles && s < G.S) {
+    const int TXb = (G.GW + kSrcTile - 1) / kSrcTile, TYb = (G.GH + kSrcTile - 1) / kSrcTile;
+    const int b = q / (TXb * TYb), tr = q - b * TXb * TYb;
+    const int tb = tr / TXb, tx = tr - tb * TXb;
+    const int2 r = src_tile_range(p, G, b, s, tb, tx, p.start[2 * G.ncell_pad]);
+    n = r.y - r.x;
+  }
+  for (int d = SP >> 1; d >= 1; d >>= 1) n += __shfl_xor(n, d, kWave);
+  if (s == 0 && q < ntiles) tilecnt[q] = n;
+}
+
+// Chunk list: info[w] = (batch-tile index, first record of the tile's concatenated slice ranges) from the tiles'
+// record counts; one workgroup, thread i takes the tiles i, i + 1024, ... in rounds.
+__global__ void __launch_bounds__(kAdjListBlock) k_src_adj_list(const int* __restrict__ tilecnt, int ntiles,
+                                                                int2* __restrict__ info, int* __restrict__ nchunk) {
+  __shared__ int wsum[kAdjListBlock / kWave + 1];
+  int base = 0;
+  for (int t0 = 0; t0 < ntiles; t0 += kAdjListBlock) {
+    const int t = t0 + threadIdx.x;
+    const int n = t < ntiles ? tilecnt[t] : 0;
+    const int nc = (n + kAdjChunk - 1) / kAdjChunk;
+    int total;
+    const int c = base + block_exclusive_scan<kAdjListBlock>(nc, wsum, total);
+    for (int k = 0; k < nc; ++k) info[c + k] = make_int2(t, k * kAdjChunk);
+    base += total;
+  }
+  if (threadIdx.x == 0) *nchunk = base;
+}
+
+__global__ void __launch_bounds__(kAdjBlock) k_src_flow_adjoint(FPlan p, FGeo G, FlowGeo F,
+                                                             const int2* __restrict__ info,
+                                                             const int* __restrict__ nchunk,
+                                                             const float2* __restrict__ gvr,
+                                                             float* __restrict__ ggrid) {
+  constexpr int T = kAdjT, L = T + 1;
+  __shared__ int seg[kAdjMaxSlices + 1];          // prefix of the S slice ranges' lengths
+  __shared__ int sbase[kAdjMaxSlices];
+  __shared__ int bcnt[T * T], bstart[T * T];
+  __shared__ int wsum[kAdjBlock / kWave + 1];
+  __shared__ float sax[kAdjChunk], say[kAdjChunk], sv0[kAdjChunk], sv1[kAdjChunk];
+  __shared__ float bsum[8][T * T];                // corner k = 2 * iy + ix, channel c: row 2 k + c
+  __shared__ int org[2];
+  if ((int)blockIdx.x >= *nchunk) return;
+  const int2 ci = info[blockIdx.x];
+  const int tid = threadIdx.x;
+  const int TXb = (G.GW + kSrcTile - 1) / kSrcTile, TYb = (G.GH + kSrcTile - 1) / kSrcTile;
+  const int b = ci.x / (TXb * TYb), tr = ci.x - b * TXb * TYb;
+  const int tb = tr / TXb, tx = tr - tb * TXb;
+  if (tid < kWave) {                               // slices s < S <= 64 of batch b: one wave
+    int lo = 0, len = 0;
+    if (tid < G.S) {
+      const int2 r = src_tile_range(p, G, b, tid, tb, tx, p.start[2 * G.ncell_pad]);
+      lo = r.x;
+      len = r.y - r.x;
+    }
+    int incl = len;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int y = __shfl_up(incl, d, kWave);
+      if (tid >= d) incl += y;
+    }
+    seg[tid + 1] = incl;
+    sbase[tid] = lo;
+    if (tid == 0) {
+      seg[0] = 0;
+      org[0] = 0x7fffffff;
+      org[1] = 0x7fffffff;
+    }
+  }
+  bcnt[tid] = 0;
+  __syncthreads();
+  const int r0 = ci.y, r1 = min(seg[G.S], ci.y + kAdjChunk);
+  GridCorners c[kAdjItems];
+  float2 g[kAdjItems];
+  bool live[kAdjItems];
+  int mx = 0x7fffffff, my = 0x7fffffff;
+#pragma unroll
+  for (int u = 0; u < kAdjItems; ++u) {           // the chunk's records and gradients, then their corners
+    const int r = r0 + u * kAdjBlock + tid;
+    live[u] = r < r1;
+    int q = 0;
+    if (live[u]) {
+      int s = 0;
+      while (seg[s + 1] <= r) ++s;
+      q = sbase[s] + (r - seg[s]);
+    }
+    const float4 f = live[u] ? p.srec[q].f : make_float4(0.f, 0.f, 0.f, 0.f);
+    g[u] = live[u] ? gvr[q] : make_float2(0.f, 0.f);
+    c[u] = grid_corners(f.x, f.y, F.Hg, F.Wg, F.sxw, F.syh, F.scale != 0);
+    live[u] = live[u] && !(g[u].x == 0.f && g[u].y == 0.f);   // a zero row adds nothing
+    if (live[u]) {
+      const int y0 = c[u].o00 / F.Wg;
+      mx = min(mx, c[u].o00 - y0 * F.Wg);
+      my = min(my, y0);
+    }
+  }
+  mx = wave_min_i(mx);
+  my = wave_min_i(my);
+  if ((tid & (kWave - 1)) == 0) {
+    atomicMin(org, mx);
+    atomicMin(org + 1, my);
+  }
+  __syncthreads();
+  const int ox = org[0], oy = org[1];
+  if (ox == 0x7fffffff) return;                   // every row of the chunk is zero
+  const int64_t plane = (int64_t)F.Hg * F.Wg;
+  float* gb = ggrid + (int64_t)b * 2 * plane;
+  int bin[kAdjItems], rank[kAdjItems];
+#pragma unroll
+  for (int u = 0; u < kAdjItems; ++u) {
+    bin[u] = -1;
+    if (!live[u]) continue;
+    const int y0 = c[u].o00 / F.Wg, x0 = c[u].o00 - y0 * F.Wg;
+    const int bx = x0 - ox, by = y0 - oy;
+    if ((unsigned)bx < (unsigned)T && (unsigned)by < (unsigned)T) {
+      bin[u] = by * T + bx;
+      rank[u] = atomicAdd(bcnt + bin[u], 1);
+    } else {                                      // outside the window: the four corners directly
+      atomicAdd(gb + c[u].o00, g[u].x * c[u].w00);
+      atomicAdd(gb + c[u].o01, g[u].x * c[u].w01);
+      atomicAdd(gb + c[u].o10, g[u].x * c[u].w10);
+      atomicAdd(gb + c[u].o11, g[u].x * c[u].w11);
+      atomicAdd(gb + plane + c[u].o00, g[u].y * c[u].w00);
+      atomicAdd(gb + plane + c[u].o01, g[u].y * c[u].w01);
+      atomicAdd(gb + plane + c[u].o10, g[u].y * c[u].w10);
+      atomicAdd(gb + plane + c[u].o11, g[u].y * c[u].w11);
+    }
+  }
+  __syncthreads();
+  const int mine = bcnt[tid];
+  int total;
+  const int first = block_exclusive_scan<kAdjBlock>(mine, wsum, total);
+  bstart[tid] = first;
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kAdjItems; ++u) {
+    if (bin[u] < 0) continue;
+    const int q = bstart[bin[u]] + rank[u];
+    sax[q] = c[u].ax;
+    say[q] = c[u].ay;
+    sv0[q] = g[u].x;
+    sv1[q] = g[u].y;
+  }
+  __syncthreads();
+  float sum[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) sum[k] = 0.f;
+  for (int q = first; q < first + mine; ++q) {
+    const float fx = sax[q], fy = say[q];
+    const float wx0 = 1.f - fx, wy0 = 1.f - fy;
+    const float w[4] = {wx0 * wy0, fx * wy0, wx0 * fy, fx * fy};
+    const float v0 = sv0[q], v1 = sv1[q];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      sum[2 * k] += v0 * w[k];
+      sum[2 * k + 1] += v1 * w[k];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) bsum[k][tid] = sum[k];
+  __syncthreads();
+  // the second corner of an axis is the next node, or the same one on a grid of a single column (row)
+  const int sx = F.Wg > 1 ? 1 : 0, sy = F.Hg > 1 ? 1 : 0;
+  for (int a = tid; a < L * L; a += kAdjBlock) {
+    const int ly = a / L, lx = a - ly * L;
+    const int py = oy + ly, px = ox + lx;
+    if (py >= F.Hg || px >= F.Wg) continue;
+    float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int cx = lx - (k & 1) * sx, cy = ly - (k >> 1) * sy;
+      if ((unsigned)cx >= (unsigned)T || (unsigned)cy >= (unsigned)T) continue;
+      v0 += bsum[2 * k][cy * T + cx];
+      v1 += bsum[2 * k + 1][cy * T + cx];
+    }
+    const int64_t o = (int64_t)py * F.Wg + px;
+    if (v0 != 0.f) atomicAdd(gb + o, v0);
+    if (v1 != 0.f) atomicAdd(gb + plane + o, v1);
+  }
 }
 
 // Backward of the trajectory model: every source (one lane per part of its slices, own-slice tile order) sums
@@ -1487,8 +1711,62 @@ int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, f
                      (int)geo->M, gS, (int)geo->N, (float2*)gv);
   if (geo->M > 0)
     hipLaunchKernelGGL(k_fast_bwd, dim3(xcd_grid((geo->N + kPairBlock / kBwdParts - 1) / (kPairBlock / kBwdParts))),
-                       dim3(kPairBlock), 0, stream, p, G, (int)geo->N, (float2*)gv);
+                       dim3(kPairBlock), 0, stream, p, G, (int)geo->N, (float2*)gv, (float2*)nullptr);
   return check_launch("fast_pair_bwd");
+}
+
+// The flow path's backward in two steps: the pair backward writes each source's velocity gradient by source
+// record into the plan's temporary sort records (dead after the plan), and the adjoint accumulates them into the
+// flow grid.  atl_fast_pair_bwd_flow runs both.
+int atl_fast_pair_bwd_src(const atl_fast_geometry* geo, void* ws, const float* gS, hipStream_t stream) {
+  FGeo G;
+  if (!make_geo(geo, G)) { set_error("fast_pair_bwd_src: geometry not initialised"); return 1; }
+  if (!ws || (geo->M > 0 && !gS)) { set_error("fast_pair_bwd_src: null argument"); return 1; }
+  if (geo->N == 0 || geo->M == 0) return 0;
+  const FPlan p = make_plan(ws, geo);
+  float2* gvr = at_off<float2>(ws, geo->off_trec);
+  hipLaunchKernelGGL(k_fast_gather_gs, dim3(grid_for(std::max(geo->M, geo->N))), dim3(kBlock), 0, stream, p, G,
+                     (int)geo->M, gS, (int)geo->N, (float2*)nullptr);
+  hipLaunchKernelGGL(k_fast_bwd, dim3(xcd_grid((geo->N + kPairBlock / kBwdParts - 1) / (kPairBlock / kBwdParts))),
+                     dim3(kPairBlock), 0, stream, p, G, (int)geo->N, (float2*)nullptr, gvr);
+  return check_launch("fast_pair_bwd_src");
+}
+
+int atl_fast_flow_adjoint(const atl_fast_geometry* geo, void* ws, int64_t Hg, int64_t Wg, int64_t img_h,
+                          int64_t img_w, float* ggrid, hipStream_t stream) {
+  FGeo G;
+  if (!make_geo(geo, G)) { set_error("fast_flow_adjoint: geometry not initialised"); return 1; }
+  if (Hg < 1 || Wg < 1 || (double)geo->B * 2 * Hg * Wg >= 2.0e9 || G.S > kAdjMaxSlices) { set_error("fast_flow_adjoint: bad sizes (Hg=%lld Wg=%lld, S=%d <= %d)", (long long)Hg, (long long)Wg, G.S, kAdjMaxSlices); return 1; }
+  if (!ws || !ggrid) { set_error("fast_flow_adjoint: null argument"); return 1; }
+  if (geo->N == 0 || geo->M == 0) return 0;
+  const FPlan p = make_plan(ws, geo);
+  const float2* gvr = at_off<float2>(ws, geo->off_trec);
+  FlowGeo F;
+  F.Hg = (int)Hg;
+  F.Wg = (int)Wg;
+  F.scale = img_h > 0 && img_w > 0;
+  F.sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1);
+  F.syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
+  const int64_t tiles = geo->B * ((G.GW + kSrcTile - 1) / kSrcTile) * ((G.GH + kSrcTile - 1) / kSrcTile);
+  const int64_t maxc = tiles + (geo->N + kAdjChunk - 1) / kAdjChunk;   // chunks, at most
+  int2* info = (int2*)(at_off<char>(ws, geo->off_trec) + align256(geo->N * 8));   // after the gradients
+  int* nchunk = (int*)(info + maxc);
+  int* tilecnt = nchunk + 64;
+  int SP = 1;
+  while (SP < G.S) SP <<= 1;
+  hipLaunchKernelGGL(k_src_tile_counts, dim3(grid_for(tiles * SP)), dim3(kBlock), 0, stream, p, G, (int)tiles, SP,
+                     tilecnt);
+  hipLaunchKernelGGL(k_src_adj_list, dim3(1), dim3(kAdjListBlock), 0, stream, (const int*)tilecnt, (int)tiles, info,
+                     nchunk);
+  hipLaunchKernelGGL(k_src_flow_adjoint, dim3((unsigned)maxc), dim3(kAdjBlock), 0, stream, p, G, F,
+                     (const int2*)info, (const int*)nchunk, gvr, ggrid);
+  return check_launch("fast_flow_adjoint");
+}
+
+int atl_fast_pair_bwd_flow(const atl_fast_geometry* geo, void* ws, const float* gS, int64_t Hg, int64_t Wg,
+                           int64_t img_h, int64_t img_w, float* ggrid, hipStream_t stream) {
+  if (atl_fast_pair_bwd_src(geo, ws, gS, stream) != 0) return 1;
+  return atl_fast_flow_adjoint(geo, ws, Hg, Wg, img_h, img_w, ggrid, stream);
 }
 
 int atl_fast_pair_bwd_traj(const atl_fast_geometry* geo, void* ws, const float* gS, const float* coef, int64_t K,

@@ -26,8 +26,8 @@ from typing import Optional
 import torch
 
 from ..core.events import EventPacket
-from ..ops import (anchored_log_scores, anchored_score_mean, ats_pair_sums, ats_pair_sums_traj, event_noise,
-                   visible_fraction_linear, window_counts)
+from ..ops import (anchored_log_scores, anchored_score_mean, ats_pair_sums, ats_pair_sums_flow, ats_pair_sums_traj,
+                   event_noise, visible_fraction_linear, window_counts)
 from .base import Objective
 
 
@@ -195,6 +195,10 @@ class AnchoredExact(_Anchored):
                              "for trajectories)")
 
     def _pair_sums(self, ev, motion, xs, xa, anchors):
+        from ..motion import DenseLinearFlow
+        if ev.xy.is_cuda and type(motion) is DenseLinearFlow:   # the flow's gradient straight from the pair sums
+            return ats_pair_sums_flow(motion.grid, xs, ev.t, ev.b, ev.batch_size, ev.height, ev.width, anchors,
+                                      self.h, self.tau, self.cut, self.n_slices, anchor_xy=xa)
         v = motion.velocity(xs, ev.t, ev.b)
         return ats_pair_sums(xs, ev.t, v, ev.b, ev.batch_size, ev.height, ev.width, anchors, self.h, self.tau,
                              self.cut, self.n_slices, anchor_xy=xa)

@@ -85,6 +85,9 @@ _SIGS = {
     "atl_voxel_ws_bytes": [_I, _I, _I, _I, _I],
     "atl_voxel_grid_ws": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P],
     "atl_knn_indices": [_P, _I, _P, _I, _I, _I, _P, _P, _I, _P],
+    "atl_fast_pair_bwd_flow": [_P, _P, _P, _I, _I, _I, _I, _P, _P],
+    "atl_fast_pair_bwd_src": [_P, _P, _P, _P],
+    "atl_fast_flow_adjoint": [_P, _P, _I, _I, _I, _I, _P, _P],
     "atl_warp_splat_gather_ws_bytes": [_I, _I, _I, _I, _I, _I],
     "atl_warp_splat_gather_fwd": [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _D, _I, _P, _P, _P, _I, _P],
     "atl_warp_splat_gather_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _D, _P, _P, _I, _P],

@@ -613,6 +613,21 @@ class FastPairPlan:
             call("atl_fast_pair_bwd", ctypes.byref(self.geo), ptr(self.ws), ptr(gS), ptr(gv), stream_of(gv))
         return gv
 
+    def backward_flow(self, gS: torch.Tensor, B: int, Hg: int, Wg: int, img_h: int, img_w: int) -> torch.Tensor:
+        """Linear model whose velocities are the dense flow sampled at x (DenseLinearFlow.field): dL/dgrid
+        (B, 2, Hg, Wg), the pair backward's source gradients accumulated into the grid tile by tile over the
+        source records (no per-event gradient array, no binning)."""
+        if self.traj:
+            raise ValueError("a trajectory plan has backward_traj")
+        gS = self._check_gs(gS)
+        gg = torch.zeros(int(B), 2, int(Hg), int(Wg), dtype=F32, device=self.device)
+        with torch.cuda.device(self.device):
+            st = stream_of(gg)
+            call("atl_fast_pair_bwd_src", ctypes.byref(self.geo), ptr(self.ws), ptr(gS), st)
+            call("atl_fast_flow_adjoint", ctypes.byref(self.geo), ptr(self.ws), int(Hg), int(Wg), int(img_h),
+                 int(img_w), ptr(gg), st)
+        return gg
+
     def backward_traj(self, gS: torch.Tensor):
         """Trajectory model: (dL/dp (N, 2), dL/dcoef (N, 2K))."""
         if not self.traj:
@@ -645,6 +660,40 @@ class _ATSPairFast(torch.autograd.Function):
     def backward(ctx, g):
         gv = ctx.plan.backward(g)
         return gv, None, None, None, None, None, None, None, None, None, None, None, None
+
+
+class _ATSPairFlow(torch.autograd.Function):
+    """ats_pair_sums with v = DenseLinearFlow.field(x) (atl/motion/parametric.py:212-216, 235-251) folded in:
+    the flow is sampled at x, the pairs summed as by _ATSPairFast, and the backward hands the pair gradients of
+    the velocities straight to the flow grid (one pass over the plan's source records) instead of returning them
+    per event for sample_grid's adjoint."""
+
+    @staticmethod
+    def forward(ctx, grid, x, t, b, anchors, anchor_xy, B, H, W, h, tau, cut, n_slices):
+        with torch.no_grad():
+            v = sample_grid_hip(grid.detach(), x, b, img_hw=(H, W))
+        plan = FastPairPlan(x, t, v, b, B, H, W, anchors, h, tau, cut, n_slices, anchor_xy)
+        ctx.plan, ctx.shape, ctx.img = plan, tuple(grid.shape), (int(H), int(W))
+        return plan.forward()
+
+    @staticmethod
+    def backward(ctx, g):
+        Bg, _, Hg, Wg = ctx.shape
+        gg = ctx.plan.backward_flow(g, Bg, Hg, Wg, ctx.img[0], ctx.img[1])
+        return gg, None, None, None, None, None, None, None, None, None, None, None, None
+
+
+def ats_pair_sums_flow(grid, x, t, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, anchor_xy=None):
+    """ats_pair_sums(x, t, DenseLinearFlow.field(x), ...) on the device with the gradient going to the dense flow
+    grid (B, 2, Hg, Wg) directly: the same sums and the same grid gradient as sampling the flow and calling
+    ats_pair_sums (float sums of the adjoint in another order)."""
+    if not x.is_cuda:
+        raise ValueError("ats_pair_sums_flow runs on the GPU (sample the flow and call ats_pair_sums on the CPU)")
+    if grid.dim() != 4 or grid.shape[1] != 2 or grid.shape[0] != int(B):
+        raise ValueError(f"ats_pair_sums_flow: the flow grid must be ({int(B)}, 2, Hg, Wg), got {tuple(grid.shape)}")
+    get_ext()
+    return _ATSPairFlow.apply(grid, x.detach(), t.detach(), b, anchors, anchor_xy, int(B), int(H), int(W),
+                              float(h), float(tau), float(cut), int(n_slices))
 
 
 def ats_pair_sums(x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, force_ref=False, anchor_xy=None):
