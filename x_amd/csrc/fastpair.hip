@@ -1051,45 +1051,50 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
   }
   const int bj = key / (G.S * plane_cells);
   float mgx = 0.f, mgy = 0.f;
+  float4 sv;                                       // the current slice's entry (y, v) and centre
+  float cs;
+  auto visit = [&](int k, int e) {
+    float4 A[kUnroll];
+    int id[kUnroll];
+    // one lane offset for the kUnroll loads, the step within the record run folded into the (scalar) base
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      A[u] = ld((const float4*)p.brec + u, (uint32_t)k);
+      if (LOO == kLooId) id[u] = ld(aid + 8 * u, 8u * (uint32_t)k);
+    }
+    const int rem = e - k, self_u = sp - k;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const float at = A[u].z - cs;
+      const float dt = A[u].z - tj;
+      const float rx = A[u].x - (sv.x + sv.z * at);
+      const float ry = A[u].y - (sv.y + sv.w * at);
+      const float d2 = rx * rx + ry * ry;
+      const bool other = LOO == kLooId ? id[u] != sid : LOO == kLooPos ? u != self_u : true;
+      const bool ok = other & !(fabsf(dt) > G.tau) & !(d2 > G.r2max) & (u < rem);
+      const float kern = __builtin_amdgcn_exp2f(d2 * G.kexp);
+      const float f = A[u].w * kern * dt;           // A.w = gS / h^2
+      if (LOO == kLooNone) {                         // every record and the source are finite and below
+        float fo = ok ? f : 0.f;                     // 1e30 (checked), so a zero factor adds exactly nothing
+        asm volatile("" : "+v"(fo));                 // keep one select (not folded into two after the FMAs)
+        mgx = fmaf(fo, rx, mgx);
+        mgy = fmaf(fo, ry, mgy);
+      } else {                                       // selects: a record may hold anything, NaN included
+        mgx = ok ? fmaf(f, rx, mgx) : mgx;
+        mgy = ok ? fmaf(f, ry, mgy) : mgy;
+      }
+    }
+  };
+  auto entry = [&](int s, float4& e4, float& c) {
+    entry_key(make_float2(sr.x, sr.y), make_float2(sr.z, sr.w), tj, bj, s, G, e4.x, e4.y);
+    e4.z = sr.z;
+    e4.w = sr.w;
+    c = slice_centre(s, G.delta);
+  };
   for (int s = lo_l; s <= hi_l; ++s) {
-    float4 sv;
-    entry_key(make_float2(sr.x, sr.y), make_float2(sr.z, sr.w), tj, bj, s, G, sv.x, sv.y);
-    sv.z = sr.z;
-    sv.w = sr.w;
-    const float cs = slice_centre(s, G.delta);
+    entry(s, sv, cs);
     const float qx = clampf(sv.x, G.gx0, G.gx1), qy = clampf(sv.y, G.gy0, G.gy1);
-    walk_flat(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, tab, [&](int k, int e) {
-      float4 A[kUnroll];
-      int id[kUnroll];
-      // one lane offset for the kUnroll loads, the step within the record run folded into the (scalar) base
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        A[u] = ld((const float4*)p.brec + u, (uint32_t)k);
-        if (LOO == kLooId) id[u] = ld(aid + 8 * u, 8u * (uint32_t)k);
-      }
-      const int rem = e - k, self_u = sp - k;
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const float at = A[u].z - cs;
-        const float dt = A[u].z - tj;
-        const float rx = A[u].x - (sv.x + sv.z * at);
-        const float ry = A[u].y - (sv.y + sv.w * at);
-        const float d2 = rx * rx + ry * ry;
-        const bool other = LOO == kLooId ? id[u] != sid : LOO == kLooPos ? u != self_u : true;
-        const bool ok = other & !(fabsf(dt) > G.tau) & !(d2 > G.r2max) & (u < rem);
-        const float kern = __builtin_amdgcn_exp2f(d2 * G.kexp);
-        const float f = A[u].w * kern * dt;           // A.w = gS / h^2
-        if (LOO == kLooNone) {                         // every record and the source are finite and below
-          float fo = ok ? f : 0.f;                     // 1e30 (checked), so a zero factor adds exactly nothing
-          asm volatile("" : "+v"(fo));                 // keep one select (not folded into two after the FMAs)
-          mgx = fmaf(fo, rx, mgx);
-          mgy = fmaf(fo, ry, mgy);
-        } else {                                       // selects: a record may hold anything, NaN included
-          mgx = ok ? fmaf(f, rx, mgx) : mgx;
-          mgy = ok ? fmaf(f, ry, mgy) : mgy;
-        }
-      }
-    });
+    walk_flat(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, tab, visit);
   }
   return make_float2(mgx, mgy);
 }
