@@ -167,9 +167,9 @@ def test_voxel_tile_engine_at_full_sensor_and_edges():
 @pytest.mark.parametrize("form", ["gather", "scatter"])
 def test_tile_accumulation_forms_match_oracle(form, monkeypatch):
     """Both accumulation forms of the tile engine (per-corner sums after an LDS sort by base corner, the default
-    for the bilinear modes; LDS float atomics, ATL_TILE_SCATTER=1) against the oracle: the splat forward with a
-    tile of more than 16384 events (2048-record chunks), the gather's image gradient, and the flow-grid adjoint
-    with 1, 2 and 4 channels."""
+    for the bilinear modes; LDS float atomics, ATL_TILE_SCATTER=1, and always for the voxel grid) against the
+    oracle: the splat forward with a tile of more than 16384 events (2048-record chunks), the gather's image
+    gradient, the voxel grid (5 bins, a crowded tile) and the flow-grid adjoint with 1, 2 and 4 channels."""
     monkeypatch.setenv("ATL_TILE_SCATTER", "1" if form == "scatter" else "0")
     print(f"tile accumulation form={form}", flush=True)
     rng = np.random.default_rng(11)
@@ -185,6 +185,13 @@ def test_tile_accumulation_forms_match_oracle(form, monkeypatch):
     g = rng.standard_normal(n).astype(F32)
     gimg, _ = F.get_ext().gather_bilinear_bwd(T(g), T(src), T(pos), T(b))
     close_rel(N(gimg), O.gather_bilinear_bwd(g, src, pos, b)[0], 1e-5)
+    print(f"tile accumulation form={form}: voxel grid", flush=True)
+    tv = np.sort(rng.random(n) * 1.2 - 0.1).astype(F32)
+    pv = np.where(rng.random(n) > 0.5, 1.0, -1.0).astype(F32)
+    bs = np.sort(b)
+    got = N(F.voxel_grid(T(pos), T(tv), T(pv), T(bs), 2, 5, H, W, normalize=None))
+    _voxel_cases_close(got, O.voxel_grid(pos, tv, pv, bs, 2, 5, H, W),
+                       float(O.voxel_grid(pos, tv, np.abs(pv), bs, 2, 5, H, W).max()))
     for C in (1, 2, 4):
         fld = rng.standard_normal((2, C, 24, 32)).astype(F32)
         tf = T(fld).requires_grad_(True)
