@@ -458,6 +458,9 @@ def trajectories_main(a, dev):
 
     def step():
         coeff.grad = None
+        # a training step changes the coefficients, so their channels-last copy (kept per field version) is made
+        # again in every timed step rather than reused from the previous one
+        F._CL_CACHE.clear()
         m = PixelTrajectories(coeff, K, "bspline", tile=1)
         loss = obj(ev, m)["loss"] - iwe_variance(ev, m, 0.5)
         loss.backward()

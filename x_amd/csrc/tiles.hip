@@ -548,158 +548,142 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum_bins(const int4* __res
   }
 }
 
-// Many-channel grid adjoint (kGrid, C > 4, grids of at least 2 x 2 nodes) in gather form: four LDS float
-// atomics per event and channel bound the scatter form there.  A workgroup takes a range of kGatherRange
-// records of the tile-ordered array, kGatherBlock at a time: it bins them in LDS by
-// base node (one integer atomic each), stages their gradient rows in LDS, and then each of its threads owns one
-// of the tile's (T + 1)^2 nodes and adds, channel by channel in registers, the events of the four bins whose
-// corners include that node.  The terms are the same fp32 products go * w as the scatter form's; they are added
-// in another order.  The flush is the scatter form's: one global atomic per non-zero node and channel.
-constexpr int kGatherBlock = 320;                // >= 17 * 17 node owners
-constexpr int kGatherRange = 2 * kGatherBlock;   // records per workgroup: two full chunks
-constexpr int kGatherBins = 16 * 16;
-
-__global__ void __launch_bounds__(kGatherBlock) k_tile_gather_grid(const int* __restrict__ boff,
-                                                                   const float4* __restrict__ rec,
-                                                                   const float* __restrict__ gout, TileGeo g,
-                                                                   float* __restrict__ out) {
-  constexpr int T = 16, L = T + 1;
-  extern __shared__ float gs[];                   // kGatherBlock rows of nc floats
-  __shared__ float sax[kGatherBlock], say[kGatherBlock];
-  __shared__ int bin_of[kGatherBlock], rank_of[kGatherBlock];
-  __shared__ int bcnt[kGatherBins], boffs[kGatherBins + 1];
-  __shared__ int order[kGatherBlock];
-  __shared__ int wsum[kGatherBlock / kWave + 1];
-  __shared__ int ts[kGatherBlock + 1];
-  __shared__ int found, found2;
-  const int nc = g.C;
+// Many-channel grid adjoint (kGrid, C > 4 channels, 16 x 16 tiles) in the gather form of k_tile_accum_bins: each
+// round of up to 512 records is ranked by base node with one LDS integer atomic each and its fractions are stored
+// in base-node order; then, four channels at a time, every thread loads those channels of its own records (16
+// bytes of the gradient row each, all in flight together) into LDS in the same order, thread c adds the four
+// corner products value * (wx * wy) of its node's records into registers, the sums go through an LDS table, and
+// every window node adds the sums of the base nodes that reach it into its own LDS window entry.  The window is flushed once per chunk with one global atomic per
+// non-zero node and channel.  The products are the scatter form's; only the order of the additions differs.
+__global__ void __launch_bounds__(kAccBlock) k_tile_accum_rows(const int4* __restrict__ info,
+                                                               const int* __restrict__ nchunk,
+                                                               const float4* __restrict__ rec,
+                                                               const float* __restrict__ gout, TileGeo g,
+                                                               float* __restrict__ out) {
+  constexpr int T = kBinT, L = T + 1;
+  extern __shared__ float acc[];                  // nc * L * L window
+  __shared__ int bcnt[kBins], bstart[kBins];
+  __shared__ int wsum[kAccBlock / kWave + 1];
+  __shared__ float sax[kAccChunk], say[kAccChunk];
+  __shared__ float4 srow[kAccChunk];              // the group's four channels of every record, in base-node order
+  __shared__ float bsum[16][kBins];               // corner k, channel c of the group: row 4 k + c
+  if ((int)blockIdx.x >= *nchunk) return;
+  const int4 ci = info[blockIdx.x];
+  const int key = ci.x, s0 = ci.y, s1 = ci.z;
   const int tid = threadIdx.x;
-  const int total = boff[g.nkeys * g.nblk];
-  const int r0 = blockIdx.x * kGatherRange;
-  if (r0 >= total) return;
-  const int r1 = min(r0 + kGatherRange, total);
-  auto tstart = [&](int k) { return boff[min(k, g.nkeys) * g.nblk]; };
-  const int step = (g.nkeys + kGatherBlock - 1) / kGatherBlock;
-  if (tid == 0) {
-    found = 0;
-    found2 = 0;
-  }
-  __syncthreads();
-  {
-    const int k = tid * step;
-    if (k < g.nkeys && tstart(k) <= r0) atomicMax(&found, k);
-  }
-  __syncthreads();
-  const int coarse = found;
-  {
-    const int k = coarse + tid;
-    if (tid < step && k < g.nkeys && tstart(k) <= r0) atomicMax(&found2, k);
-  }
-  __syncthreads();
+  const int nc = g.C;
   const int64_t pl = (int64_t)g.H * g.W;
   const int plane = g.TY * g.TX;
-  const int ly = tid / L, lx = tid - ly * L;      // this thread's node (tid < L * L)
-  for (int base = max(coarse, found2); base < g.nkeys; base += kGatherBlock) {
-    for (int i = tid; i <= kGatherBlock; i += kGatherBlock) ts[i] = tstart(base + i);
+  const int b = key / plane, r = key - b * plane;
+  const int ty = r / g.TX, tx = r - ty * g.TX;
+  const int ox = tx * T, oy = ty * T;
+  for (int a = tid; a < nc * L * L; a += kAccBlock) acc[a] = 0.f;
+  const int sx = g.W > 1 ? 1 : 0, sy = g.H > 1 ? 1 : 0;   // second corner: the next node, or the same one
+  for (int base = s0; base < s1; base += kAccChunk) {
+    float4 q[kAccItems];
+#pragma unroll
+    for (int u = 0; u < kAccItems; ++u) {
+      const int k = base + u * kAccBlock + tid;
+      if (k < s1) q[u] = rec[k];
+    }
+    bcnt[tid] = 0;
     __syncthreads();
-    bool done = false;
-    for (int i = 0; i < kGatherBlock && base + i < g.nkeys; ++i) {
-      const int key = base + i;
-      const int s0 = max(r0, ts[i]), s1 = min(r1, ts[i + 1]);
-      if (s0 >= r1) {
-        done = true;
-        break;
-      }
-      if (s0 >= s1) continue;                     // empty tile
-      const int b = key / plane, r = key - b * plane;
-      const int ty = r / g.TX, tx = r - ty * g.TX;
-      const int ox = tx * T, oy = ty * T;
-      float acc[kMaxChannels];
+    int bin[kAccItems], rank[kAccItems];
+    float ax[kAccItems], ay[kAccItems];
 #pragma unroll
-      for (int c = 0; c < kMaxChannels; ++c) acc[c] = 0.f;
-      for (int c0 = s0; c0 < s1; c0 += kGatherBlock) {
-        for (int k = tid; k < kGatherBins; k += kGatherBlock) bcnt[k] = 0;
-        __syncthreads();
-        const int k = c0 + tid;
-        int bin = -1, rank = 0;
-        if (k < s1) {
-          const float4 q = rec[k];
-          const GridCell c = grid_cell(q.x, q.y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
-          const int bx = c.x0 - ox, by = c.y0 - oy;
-          if ((unsigned)bx < (unsigned)T && (unsigned)by < (unsigned)T) {   // always: the binning chose this tile
-            bin = by * T + bx;
-            sax[tid] = c.ax;
-            say[tid] = c.ay;
-            const int j = __float_as_int(q.w);
-            const float* row = gout + (int64_t)j * nc;
-            float* dst = gs + tid * nc;
-            if (g.vec4) {                         // nc % 4 == 0: 16-byte rows in global memory and in LDS
-              for (int c4 = 0; c4 < nc; c4 += 4) *(float4*)(dst + c4) = *(const float4*)(row + c4);
-            } else {
-              for (int c = 0; c < nc; ++c) dst[c] = row[c];
-            }
-            rank = atomicAdd(bcnt + bin, 1);
-          }
-        }
-        bin_of[tid] = bin;
-        rank_of[tid] = rank;
-        __syncthreads();
-        {                                         // bin offsets: kGatherBins counts over the block's threads
-          const int v = tid < kGatherBins ? bcnt[tid] : 0;
-          int tot;
-          const int ex = block_exclusive_scan<kGatherBlock>(v, wsum, tot);
-          if (tid < kGatherBins) boffs[tid] = ex;
-          if (tid == 0) boffs[kGatherBins] = tot;
-        }
-        __syncthreads();
-        if (bin_of[tid] >= 0) order[boffs[bin_of[tid]] + rank_of[tid]] = tid;
-        __syncthreads();
-        if (tid < L * L) {
-          // corner 00 from bin (lx, ly), 01 from (lx - 1, ly), 10 from (lx, ly - 1), 11 from (lx - 1, ly - 1)
-#pragma unroll
-          for (int corner = 0; corner < 4; ++corner) {
-            const int cx = lx - (corner & 1), cy = ly - (corner >> 1);
-            if (cx < 0 || cy < 0 || cx >= T || cy >= T) continue;
-            const int bb = cy * T + cx;
-            for (int o = boffs[bb]; o < boffs[bb + 1]; ++o) {
-              const int e = order[o];
-              const float ax = sax[e], ay = say[e];
-              const float w = corner == 0 ? (1.f - ax) * (1.f - ay)
-                            : corner == 1 ? ax * (1.f - ay)
-                            : corner == 2 ? (1.f - ax) * ay
-                                          : ax * ay;
-              const float* row = gs + e * nc;
-              if (g.vec4) {
-#pragma unroll
-                for (int c4 = 0; c4 < kMaxChannels; c4 += 4) {
-                  if (c4 >= nc) break;
-                  const float4 v = *(const float4*)(row + c4);
-                  acc[c4] += v.x * w;
-                  acc[c4 + 1] += v.y * w;
-                  acc[c4 + 2] += v.z * w;
-                  acc[c4 + 3] += v.w * w;
-                }
-              } else {
-#pragma unroll
-                for (int c = 0; c < kMaxChannels; ++c)
-                  if (c < nc) acc[c] += row[c] * w;
-              }
-            }
-          }
-        }
-        __syncthreads();                          // the staging arrays are refilled by the next chunk
-      }
-      if (tid < L * L) {
-        const int py = oy + ly, px = ox + lx;
-        if (py < g.H && px < g.W) {
-#pragma unroll
-          for (int c = 0; c < kMaxChannels; ++c)
-            if (c < nc && acc[c] != 0.f) atomicAdd(out + ((int64_t)b * nc + c) * pl + (int64_t)py * g.W + px, acc[c]);
-        }
+    for (int u = 0; u < kAccItems; ++u) {
+      bin[u] = -1;
+      if (base + u * kAccBlock + tid >= s1) continue;
+      const GridCell c = grid_cell(q[u].x, q[u].y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
+      const int bx = c.x0 - ox, by = c.y0 - oy;
+      if ((unsigned)bx < (unsigned)T && (unsigned)by < (unsigned)T) {   // always: the binning chose this tile
+        ax[u] = c.ax;
+        ay[u] = c.ay;
+        bin[u] = by * T + bx;
+        rank[u] = atomicAdd(bcnt + bin[u], 1);
       }
     }
-    if (done) break;
-    __syncthreads();                              // ts is reloaded
+    __syncthreads();
+    const int mine = bcnt[tid];
+    int total;
+    const int first = block_exclusive_scan<kAccBlock>(mine, wsum, total);
+    bstart[tid] = first;
+    __syncthreads();
+    int pos[kAccItems];
+#pragma unroll
+    for (int u = 0; u < kAccItems; ++u) {
+      pos[u] = -1;
+      if (bin[u] < 0) continue;
+      pos[u] = bstart[bin[u]] + rank[u];
+      sax[pos[u]] = ax[u];
+      say[pos[u]] = ay[u];
+    }
+    for (int cg = 0; cg < nc; cg += 4) {
+      // every thread loads the group's channels of its own records (the loads in flight together) into srow
+      float4 v4[kAccItems];
+#pragma unroll
+      for (int u = 0; u < kAccItems; ++u) {
+        v4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (pos[u] < 0) continue;
+        const float* row = gout + (int64_t)__float_as_int(q[u].w) * nc + cg;
+        if (g.vec4) {                               // nc % 4 == 0, 16-byte aligned rows
+          v4[u] = *(const float4*)row;
+        } else {
+          v4[u].x = row[0];
+          if (cg + 1 < nc) v4[u].y = row[1];
+          if (cg + 2 < nc) v4[u].z = row[2];
+          if (cg + 3 < nc) v4[u].w = row[3];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kAccItems; ++u)
+        if (pos[u] >= 0) srow[pos[u]] = v4[u];
+      __syncthreads();
+      float s[4][4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s[k][c] = 0.f;
+      for (int p = first; p < first + mine; ++p) {
+        const float4 r4 = srow[p];
+        const float v[4] = {r4.x, r4.y, r4.z, r4.w};
+        const float fx = sax[p], fy = say[p];
+        const float wx0 = 1.f - fx, wy0 = 1.f - fy;
+        const float w[4] = {wx0 * wy0, fx * wy0, wx0 * fy, fx * fy};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) s[k][c] += v[c] * w[k];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) bsum[4 * k + c][tid] = s[k][c];
+      __syncthreads();
+      for (int a = tid; a < L * L; a += kAccBlock) {   // window node a adds the base nodes that reach it
+        const int ly = a / L, lx = a - ly * L;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int cx = lx - (k & 1) * sx, cy = ly - (k >> 1) * sy;
+          if ((unsigned)cx >= (unsigned)T || (unsigned)cy >= (unsigned)T) continue;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v[c] += bsum[4 * k + c][cy * T + cx];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (cg + c < nc) acc[(cg + c) * L * L + a] += v[c];
+      }
+      __syncthreads();                              // bsum and srow are rewritten by the next channel group
+    }
+  }
+  for (int a = tid; a < L * L; a += kAccBlock) {
+    const int py = oy + a / L, px = ox + a % L;
+    if (py >= g.H || px >= g.W) continue;
+    for (int ch = 0; ch < nc; ++ch) {
+      const float v = acc[ch * L * L + a];
+      if (v != 0.f) atomicAdd(out + ((int64_t)b * nc + ch) * pl + (int64_t)py * g.W + px, v);
+    }
   }
 }
 
@@ -1295,12 +1279,16 @@ int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t
     case 3: tile_accum<kGrid, 3>(g, L, ws, gout, gfield, stream); break;
     case 4: tile_accum<kGrid, 4>(g, L, ws, gout, gfield, stream); break;
     default:
-      if (g.T == 16 && Hg >= 2 && Wg >= 2) {     // gather form (C > 4 is only planned with 16 x 16 tiles)
+      if (g.T == kBinT && !tile_scatter_form()) {   // gather form (C > 4 is only planned with 16 x 16 tiles)
         if (g.nblk == 0) break;
-        const char* w = (const char*)ws;
-        hipLaunchKernelGGL(k_tile_gather_grid, dim3((unsigned)((g.N + kGatherRange - 1) / kGatherRange)),
-                           dim3(kGatherBlock), (size_t)kGatherBlock * C * sizeof(float), stream,
-                           (const int*)(w + L.boff), (const float4*)(w + L.rec), gout, g, gfield);
+        char* w = (char*)ws;
+        int4* info = (int4*)(w + L.info);
+        int* nchunk = (int*)(w + L.nchunk);
+        hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.boff), g,
+                           kAccChunk, kBinChunk, info, nchunk);
+        hipLaunchKernelGGL(k_tile_accum_rows, dim3((unsigned)max_chunks(g)), dim3(kAccBlock),
+                           (size_t)C * (kBinT + 1) * (kBinT + 1) * sizeof(float), stream, (const int4*)info,
+                           (const int*)nchunk, (const float4*)(w + L.rec), gout, g, gfield);
       } else {
         tile_accum<kGrid, 0>(g, L, ws, gout, gfield, stream);
       }

@@ -133,6 +133,27 @@ def _tile_plan_ok(B, C, Hg, Wg):
     return C <= 4 or (C <= 32 and B * ((Wg + 16) // 16) * ((Hg + 16) // 16) <= 16384)
 
 
+_CL_CACHE: list = []          # [(field, its version, its channels-last copy)]: the last few fields converted
+
+
+def _channels_last(fld: torch.Tensor) -> torch.Tensor:
+    """(B, Hg, Wg, 4 ceil(C / 4)) channels-last copy of a (B, C, Hg, Wg) field.  A field that is sampled several
+    times per step (the trajectory model's coefficient grid: every fixed-point step, the final look-up and their
+    backward) is converted once while it is unchanged: the copy is kept with the field object and its in-place
+    version counter, and any update of the field makes a new one."""
+    ver = fld._version
+    for src, v, fcl in _CL_CACHE:
+        if src is fld and v == ver:
+            return fcl
+    B, C, Hg, Wg = fld.shape
+    fcl = torch.empty(B, Hg, Wg, 4 * ((C + 3) // 4), device=fld.device, dtype=F32)
+    with torch.cuda.device(fld.device):
+        call("atl_field_channels_last", ptr(fld), B, C, Hg, Wg, ptr(fcl), stream_of(fld))
+    _CL_CACHE.insert(0, (fld, ver, fcl))
+    del _CL_CACHE[4:]
+    return fcl
+
+
 class _SampleGrid(torch.autograd.Function):
     """Bilinear border-clamped lookup of a (B, C, Hg, Wg) field (atl/motion/parametric.py:235-251).
 
@@ -147,7 +168,8 @@ class _SampleGrid(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, fld, pos, b, img_h, img_w, plan):
-        fld, pos, b = _f32(fld), _f32(pos), b.contiguous().long()
+        fld_in = fld if fld.dtype == F32 and fld.is_contiguous() else _f32(fld)
+        fld, pos, b = fld_in, _f32(pos), b.contiguous().long()
         B, C, Hg, Wg = fld.shape
         N = pos.shape[0]
         out = torch.empty(N, C, device=pos.device, dtype=F32)
@@ -157,8 +179,7 @@ class _SampleGrid(torch.autograd.Function):
         with torch.cuda.device(pos.device):
             st = stream_of(pos)
             if cl:
-                fcl = torch.empty(B, Hg, Wg, 4 * Q, device=pos.device, dtype=F32)
-                call("atl_field_channels_last", ptr(fld), B, C, Hg, Wg, ptr(fcl), st)
+                fcl = _channels_last(fld_in)
                 call("atl_sample_grid_fwd_cl", ptr(fcl), B, C, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w),
                      ptr(out), st)
                 fld = fcl                          # the backward's position gradient reads the same copy
@@ -273,11 +294,10 @@ class _TrajDisplacement(torch.autograd.Function):
         B, C, Hg, Wg = fld.shape
         N = gpos.shape[0]
         out = torch.empty(N, 2, device=gpos.device, dtype=F32)
-        fcl = torch.empty(B, Hg, Wg, 4 * ((C + 3) // 4), device=gpos.device, dtype=F32)
         ctx.plan = None
         with torch.cuda.device(gpos.device):
             st = stream_of(gpos)
-            call("atl_field_channels_last", ptr(fld), B, C, Hg, Wg, ptr(fcl), st)
+            fcl = _channels_last(fld)
             call("atl_traj_displacement", ptr(fcl), B, C, K, Hg, Wg, ptr(gpos), ptr(b), ptr(t), N, basis, ptr(out),
                  st)
             if plan and _tile_plan_ok(B, C, Hg, Wg):
