@@ -255,7 +255,10 @@ __global__ void __launch_bounds__(kBlock) k_fill_zero(int* __restrict__ p, int64
 // each record takes its slot.  The runs of one bucket follow in no fixed block order; pass 2 orders the bucket.
 // The source model: K = 0 linear (x, v per source: y = x + v (c_s - t), the reference's), K > 0 trajectories
 // (x = the trajectory start p, `coef` the (N, 2K) coefficient rows, `tab` the (S, 2K) slice-centre basis table).
-template <bool SCATTER, int K>
+// ENT = false (linear model, SCATTER only): the entries are counted (the totals fix every bucket's place) but not
+// written: the block reserves runs of the anchor and source buckets only, and k_entry_pass writes the entries
+// later from the sorted source records.
+template <bool SCATTER, int K, bool ENT = true>
 __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restrict__ x, const float* __restrict__ t,
                                                        const float2* __restrict__ v, const int64_t* __restrict__ b,
                                                        int64_t N, const int64_t* __restrict__ anchors,
@@ -270,9 +273,10 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
   int vm = 0;                                    // this thread's max ||v|| (sources) or max |at| (anchors)
   const int blk = blockIdx.x;
   int* __restrict__ mycnt = cnt + (int64_t)blk * G.nbuckets;
+  const int bpk = G.ncell_pad >> G.bshift;       // buckets per key space (the entries' buckets come first)
   for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) {
     int h = 0;
-    if (SCATTER) {
+    if (SCATTER && (ENT || i >= bpk)) {
       const int c = mycnt[i];
       if (c > 0) h = atomicAdd(bsum + i, c);   // bsum = bpos: this block's run of bucket i
     }
@@ -327,6 +331,40 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
           }
         }
       }
+    }
+  } else if (src_blk && SCATTER && !ENT) {
+    // the source record only: keyed by the cell of the own-slice entry, in the entries' fp32 operations.  All
+    // loads first (indices clamped to the last source), so that they are in flight together.
+    constexpr int per = kSrcPerBlock / kP1Block;
+    const int64_t j0 = (int64_t)(blk - G.nblk_a) * kSrcPerBlock + threadIdx.x;
+    int64_t bs[per];
+    float ts[per];
+    float2 xs[per], vs[per];
+#pragma unroll
+    for (int u = 0; u < per; ++u) {
+      const int64_t j = min(j0 + u * kP1Block, N - 1);
+      bs[u] = b[j];
+      ts[u] = t[j];
+      xs[u] = x[j];
+      vs[u] = v[j];
+    }
+#pragma unroll
+    for (int u = 0; u < per; ++u) {
+      const int64_t j = j0 + u * kP1Block;
+      const int64_t bj = bs[u];
+      if (j >= N || bj < 0 || bj >= G.B) continue;
+      const float tj = ts[u];
+      const float2 xj = xs[u], vj = vs[u];
+      int lo, hi;
+      slice_range(tj, G, lo, hi);
+      if (lo > hi) continue;                     // no entries, no record (as in the batched loop below)
+      const int own = min(max((int)fminf(fmaxf(floorf(tj / G.delta), 0.f), (float)(G.S - 1)), lo), hi);
+      float yx, yy;
+      const int skey = 2 * G.ncell_pad + source_key(entry_key(xj, vj, tj, (int)bj, own, G, yx, yy), G);
+      Rec r;
+      r.f = make_float4(xj.x, xj.y, vj.x, vj.y);
+      r.i = make_int4(__float_as_int(tj), (int)j, skey, 0);
+      trec[atomicAdd(hist + (skey >> G.bshift), 1)] = r;
     }
   } else if (src_blk) {
     constexpr int per = kSrcPerBlock / kP1Block;
@@ -456,19 +494,23 @@ __device__ __forceinline__ int anchor_slice(float t, const FGeo& G) {
   return (int)fminf(fmaxf(floorf(t / G.delta), 0.f), (float)(G.S - 1));
 }
 
+// Buckets [first, first + gridDim.x).  bend: the end of every bucket (bpos after pass 1), tot: the bucket totals;
+// a bucket starts at its end minus its total, so that the anchor and source buckets can be sorted before the
+// entry buckets are filled.
 template <int SHIFT>
-__global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict__ bend, const Rec* __restrict__ trec,
-                                                           FGeo G, SortOut o) {
+__global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict__ bend, const int* __restrict__ tot,
+                                                           int first, const Rec* __restrict__ trec, FGeo G,
+                                                           SortOut o) {
   int* __restrict__ start = o.start;
   constexpr int kBucketKeys = 1 << SHIFT;
   __shared__ int cnt[kBucketKeys];
   __shared__ int cur[kBucketKeys];
   __shared__ int wsum[kSortBlock / kWave + 1];
-  const int bucket = blockIdx.x;
-  const int lo = bucket > 0 ? bend[bucket - 1] : 0;  // bend: end of every bucket (bpos after pass 1)
+  const int bucket = first + (int)blockIdx.x;
   const int hi = bend[bucket];
+  const int lo = hi - tot[bucket];
   const int bpk = G.ncell_pad >> SHIFT;            // buckets per key space
-  const int E = bend[bpk - 1], EA = bend[2 * bpk - 1];
+  const int E = bend[bpk] - tot[bpk], EA = bend[2 * bpk] - tot[2 * bpk];
   const int4* tki = (const int4*)trec;             // int half of record p: tki[2 * p + 1]
   for (int i = threadIdx.x; i < kBucketKeys; i += kSortBlock) {
     cnt[i] = 0;
@@ -561,6 +603,193 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
 #pragma unroll
     for (int u = 0; u < kSortItems; ++u)
       if (live[u]) place(r[u], atomicAdd(cur + (r[u].i.z & (kBucketKeys - 1)), 1));
+  }
+}
+
+// Entries of the linear model from the sorted source records.  A source lies near its own-slice position in
+// every slice, so the source records (in own-slice tile order) are a spatially coherent order of the entries'
+// sources: pass E1 (SCATTER = false) counts, per block of kEntSrcPerBlock source records, the entries that each
+// entry bucket receives (cnt, block-major); pass E2 (SCATTER = true) reserves the block's run of every entry
+// bucket it feeds and writes one 8-byte item per entry, (source record, cell key), instead of a 32-byte record:
+// the slice-centre position is computed again from the source record by k_entry_write, in the same fp32
+// operations, after k_entry_rank has put the items in cell order.
+constexpr int kEntBlock = 512;                     // entry passes: workgroup
+constexpr int kEntSrcPerBlock = 2048;              // entry passes: source records per block (4 per thread)
+template <bool SCATTER>
+__global__ void __launch_bounds__(kEntBlock) k_entry_pass(const Rec* __restrict__ srec, const int* __restrict__ start,
+                                                       FGeo G, int* __restrict__ cnt, int* __restrict__ bpos,
+                                                       int2* __restrict__ item) {
+  extern __shared__ int hist[];
+  const int nb0 = G.ncell_pad >> G.bshift;       // the entries' buckets
+  const int EA = start[2 * G.ncell_pad];
+  const int Nv = start[3 * G.ncell_pad] - EA;
+  const int q0 = blockIdx.x * kEntSrcPerBlock;
+  if (q0 >= Nv) return;                          // the same blocks return in both passes
+  int* __restrict__ mycnt = cnt + (int64_t)blockIdx.x * nb0;
+  for (int i = threadIdx.x; i < nb0; i += blockDim.x) {
+    int h = 0;
+    if (SCATTER) {
+      const int c = mycnt[i];
+      if (c > 0) h = atomicAdd(bpos + i, c);
+    }
+    hist[i] = h;
+  }
+  __syncthreads();
+  const int scells = G.S * G.GH * G.GW;
+  constexpr int per = kEntSrcPerBlock / kEntBlock;
+  Rec r[per];
+#pragma unroll
+  for (int u = 0; u < per; ++u) r[u] = srec[min(q0 + u * kEntBlock + (int)threadIdx.x, Nv - 1)];   // all in flight
+#pragma unroll
+  for (int u = 0; u < per; ++u) {
+    const int q = q0 + u * kEntBlock + threadIdx.x;
+    if (q >= Nv) continue;
+    const float tj = __int_as_float(r[u].i.x);
+    const float2 xj = make_float2(r[u].f.x, r[u].f.y), vj = make_float2(r[u].f.z, r[u].f.w);
+    const int bj = r[u].i.z / scells;
+    int lo, hi;
+    slice_range(tj, G, lo, hi);
+    for (int s0 = lo; s0 <= hi; s0 += kSliceBatch) {
+      int key[kSliceBatch], slot[kSliceBatch];
+#pragma unroll
+      for (int k = 0; k < kSliceBatch; ++k) {
+        float yx, yy;
+        key[k] = entry_key(xj, vj, tj, bj, min(s0 + k, hi), G, yx, yy);
+      }
+#pragma unroll
+      for (int k = 0; k < kSliceBatch; ++k)
+        if (s0 + k <= hi) slot[k] = atomicAdd(hist + (key[k] >> G.bshift), 1);
+      if (SCATTER) {
+#pragma unroll
+        for (int k = 0; k < kSliceBatch; ++k)
+          if (s0 + k <= hi) item[slot[k]] = make_int2(q, key[k]);
+      }
+    }
+  }
+  if (!SCATTER) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < nb0; i += blockDim.x) mycnt[i] = hist[i];
+  }
+}
+
+// Pass E3: workgroup `bucket` (an entry bucket) orders its items by cell, as k_sort_pass2 orders records, into
+// `sorted` (items at their final positions) and writes the CSR of its keys.  bend: the bucket ends after pass E2,
+// tot: the bucket totals.  Up to kSortBlock * kEntItems items are read once and ranked as they arrive; larger
+// buckets count first and read their items again to place them.  Pass E4 (k_entry_write) then turns every
+// sorted item into its entry.
+constexpr int kEntItems = 16;
+template <int SHIFT>
+__global__ void __launch_bounds__(kSortBlock) k_entry_rank(const int* __restrict__ bend, const int* __restrict__ tot,
+                                                           const int2* __restrict__ item, int2* __restrict__ sorted,
+                                                           int* __restrict__ start, FGeo G) {
+  constexpr int kBucketKeys = 1 << SHIFT;
+  __shared__ int cnt[kBucketKeys];
+  __shared__ int cur[kBucketKeys];
+  __shared__ int wsum[kSortBlock / kWave + 1];
+  const int bucket = blockIdx.x;
+  const int hi = bend[bucket];
+  const int lo = hi - tot[bucket];
+  for (int i = threadIdx.x; i < kBucketKeys; i += kSortBlock) {
+    cnt[i] = 0;
+    cur[i] = 0;
+  }
+  __syncthreads();
+  const bool one = hi - lo <= kSortBlock * kEntItems;
+  int2 it[kEntItems];                              // (source record, key); key -1: no item
+  int rank[kEntItems];
+#pragma unroll
+  for (int u = 0; u < kEntItems; ++u) {
+    it[u] = make_int2(0, -1);
+    rank[u] = 0;
+  }
+  if (one && hi > lo) {
+    // unconditional loads (positions clamped into the bucket), so that all of them are in flight at once
+#pragma unroll
+    for (int u = 0; u < kEntItems; ++u) it[u] = item[min(lo + u * kSortBlock + (int)threadIdx.x, hi - 1)];
+#pragma unroll
+    for (int u = 0; u < kEntItems; ++u) {
+      if (lo + u * kSortBlock + (int)threadIdx.x >= hi) it[u].y = -1;
+      if (it[u].y >= 0) rank[u] = atomicAdd(cnt + (it[u].y & (kBucketKeys - 1)), 1);
+    }
+  } else if (!one) {
+    for (int base = lo; base < hi; base += kSortBlock * kSortItems) {
+      int key[kSortItems];
+#pragma unroll
+      for (int u = 0; u < kSortItems; ++u) key[u] = item[min(base + u * kSortBlock + (int)threadIdx.x, hi - 1)].y;
+#pragma unroll
+      for (int u = 0; u < kSortItems; ++u)
+        if (base + u * kSortBlock + (int)threadIdx.x < hi) atomicAdd(cnt + (key[u] & (kBucketKeys - 1)), 1);
+    }
+  }
+  __syncthreads();
+  constexpr int per = kBucketKeys / kSortBlock;
+  int vals[per];
+  int sum = 0;
+#pragma unroll
+  for (int k = 0; k < per; ++k) {
+    vals[k] = cnt[threadIdx.x * per + k];
+    sum += vals[k];
+  }
+  int total;
+  int run = block_exclusive_scan<kSortBlock>(sum, wsum, total);
+  const int base_key = bucket << SHIFT;
+#pragma unroll
+  for (int k = 0; k < per; ++k) {
+    const int i = threadIdx.x * per + k;
+    cnt[i] = run;
+    start[base_key + i] = lo + run;
+    run += vals[k];
+  }
+  __syncthreads();
+  if (one) {                                       // an empty bucket has no live item (key -1 throughout)
+#pragma unroll
+    for (int u = 0; u < kEntItems; ++u)
+      if (it[u].y >= 0) sorted[lo + cnt[it[u].y & (kBucketKeys - 1)] + rank[u]] = it[u];
+    return;
+  }
+  for (int base = lo; base < hi; base += kSortBlock * kSortItems) {
+    int2 jt[kSortItems];
+#pragma unroll
+    for (int u = 0; u < kSortItems; ++u) jt[u] = item[min(base + u * kSortBlock + (int)threadIdx.x, hi - 1)];
+#pragma unroll
+    for (int u = 0; u < kSortItems; ++u)
+      if (base + u * kSortBlock + (int)threadIdx.x < hi) {
+        const int kk = jt[u].y & (kBucketKeys - 1);
+        sorted[lo + cnt[kk] + atomicAdd(cur + kk, 1)] = jt[u];
+      }
+  }
+}
+
+// Pass E4: entry p from sorted item p = (source record q, key): slice s of the key's plane, position
+// y = x + v (c_s - t) in entry_key's fp32 operations; eself names the entry of the event's anchor slice.
+// Entries [0, E), E = start[ncell_pad] (the anchors' first position); kEntWrite per thread, the writes in entry
+// order.
+constexpr int kEntWrite = 8;
+__global__ void __launch_bounds__(kBlock) k_entry_write(const int2* __restrict__ sorted, const Rec* __restrict__ srec,
+                                                        FGeo G, SortOut o, int nblocks) {
+  const int lb = xcd_block(nblocks);
+  if (lb < 0) return;
+  const int E = o.start[G.ncell_pad];
+  const int p0 = lb * (kBlock * kEntWrite) + threadIdx.x;
+  if (p0 >= E) return;
+  const int Nv = o.start[3 * G.ncell_pad] - o.start[2 * G.ncell_pad];
+  const int plane_cells = G.GH * G.GW;
+  int2 it[kEntWrite];
+  Rec r[kEntWrite];
+#pragma unroll
+  for (int u = 0; u < kEntWrite; ++u) it[u] = sorted[min(p0 + u * kBlock, E - 1)];
+#pragma unroll
+  for (int u = 0; u < kEntWrite; ++u) r[u] = srec[min(max(it[u].x, 0), Nv - 1)];   // q < Nv by construction
+#pragma unroll
+  for (int u = 0; u < kEntWrite; ++u) {
+    const int pos = p0 + u * kBlock;
+    if (pos >= E) break;
+    const float tj = __int_as_float(r[u].i.x);
+    const int sl = (it[u].y / plane_cells) % G.S;
+    const float dt = slice_centre(sl, G.delta) - tj;
+    o.epos[pos] = make_float4(r[u].f.x + r[u].f.z * dt, r[u].f.y + r[u].f.w * dt, r[u].f.z, r[u].f.w);
+    o.etim[pos] = tj;
+    if (sl == anchor_slice(tj, G)) o.eself[r[u].i.y] = pos;
   }
 }
 
@@ -1641,18 +1870,46 @@ int fast_plan_impl(const atl_fast_geometry* geo, const FGeo& G, const float* x, 
                        (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, tot, (Rec*)nullptr, P,
                        at_off<int>(ws, geo->off_self), at_off<int>(ws, geo->off_eself), coef, tab);
   scan_small(tot, G.nbuckets, bpos, stream);
+  // the linear model defers its entries: pass 1 places the anchor and source records, pass 2 sorts them, and
+  // k_entry_pass / k_entry_rank / k_entry_write build the entries from the sorted source records (8-byte items)
+  constexpr bool kSplit = K == 0;
   if (nblk > 0)
-    hipLaunchKernelGGL((k_sort_pass1<true, K>), dim3(nblk), dim3(kP1Block), lds, stream, (const float2*)x, t,
-                       (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt, bpos, trec,
-                       (FParams*)nullptr, (int*)nullptr, (int*)nullptr, coef, tab);
+    hipLaunchKernelGGL((k_sort_pass1<true, K, !kSplit>), dim3(nblk), dim3(kP1Block), lds, stream,
+                       (const float2*)x, t, (const float2*)v, b, N, anchors, (const float2*)anchor_xy, M, G, cnt,
+                       bpos, trec, (FParams*)nullptr, (int*)nullptr, (int*)nullptr, coef, tab);
+  const SortOut out{at_off<int>(ws, geo->off_start), at_off<float4>(ws, geo->off_epos),
+                    at_off<float>(ws, geo->off_etim), at_off<int>(ws, geo->off_eself),
+                    at_off<Rec>(ws, geo->off_arec), at_off<Rec>(ws, geo->off_srec), at_off<int>(ws, geo->off_self)};
   auto pass2 = G.bshift == 10 ? k_sort_pass2<10> : G.bshift == 11 ? k_sort_pass2<11>
              : G.bshift == 12 ? k_sort_pass2<12> : k_sort_pass2<13>;
-  hipLaunchKernelGGL(pass2, dim3(G.nbuckets), dim3(kSortBlock), 0, stream, (const int*)bpos,
-                     (const Rec*)trec, G,
-                     SortOut{at_off<int>(ws, geo->off_start), at_off<float4>(ws, geo->off_epos),
-                             at_off<float>(ws, geo->off_etim), at_off<int>(ws, geo->off_eself),
-                             at_off<Rec>(ws, geo->off_arec), at_off<Rec>(ws, geo->off_srec),
-                             at_off<int>(ws, geo->off_self)});
+  const int bpk = G.ncell_pad >> G.bshift;
+  const int first = kSplit ? bpk : 0;
+  hipLaunchKernelGGL(pass2, dim3(G.nbuckets - first), dim3(kSortBlock), 0, stream, (const int*)bpos,
+                     (const int*)tot, first, (const Rec*)trec, G, out);
+  if (kSplit) {
+    int2* item = (int2*)trec;                    // [0, E) of the items; pass 2 has read the records
+    const Rec* srec = at_off<Rec>(ws, geo->off_srec);
+    const int* start = at_off<int>(ws, geo->off_start);
+    const size_t elds = (size_t)bpk * sizeof(int);
+    // per-block counts: (N / kEntSrcPerBlock) * bpk <= nblk * nbuckets ints (kEntSrcPerBlock = kSrcPerBlock / 2)
+    static_assert(2 * kEntSrcPerBlock >= kSrcPerBlock, "the entry passes' counts fit the plan's count array");
+    const unsigned eblk = (unsigned)((N + kEntSrcPerBlock - 1) / kEntSrcPerBlock);
+    if (eblk > 0) {
+      hipLaunchKernelGGL(k_entry_pass<false>, dim3(eblk), dim3(kEntBlock), elds, stream, srec, start, G, cnt,
+                         bpos, item);
+      hipLaunchKernelGGL(k_entry_pass<true>, dim3(eblk), dim3(kEntBlock), elds, stream, srec, start, G, cnt,
+                         bpos, item);
+    }
+    auto erank = G.bshift == 10 ? k_entry_rank<10> : G.bshift == 11 ? k_entry_rank<11>
+               : G.bshift == 12 ? k_entry_rank<12> : k_entry_rank<13>;
+    int2* sorted = item + geo->ecap;             // [ecap, ecap + E) of the items' space: 16 ecap <= 32 ntmp bytes
+    hipLaunchKernelGGL(erank, dim3(bpk), dim3(kSortBlock), 0, stream, (const int*)bpos, (const int*)tot,
+                       (const int2*)item, sorted, out.start, G);
+    const int64_t wblk = (geo->ecap + kBlock * kEntWrite - 1) / (kBlock * kEntWrite);
+    if (wblk > 0)                                // runs of consecutive entries on one XCD (see xcd_block)
+      hipLaunchKernelGGL(k_entry_write, dim3(xcd_grid(wblk)), dim3(kBlock), 0, stream, (const int2*)sorted, srec,
+                         G, out, (int)wblk);
+  }
   return 0;
 }
 
