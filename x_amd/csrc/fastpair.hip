@@ -494,32 +494,40 @@ __device__ __forceinline__ int anchor_slice(float t, const FGeo& G) {
   return (int)fminf(fmaxf(floorf(t / G.delta), 0.f), (float)(G.S - 1));
 }
 
-// Buckets [first, first + gridDim.x).  bend: the end of every bucket (bpos after pass 1), tot: the bucket totals;
-// a bucket starts at its end minus its total, so that the anchor and source buckets can be sorted before the
+// Key spaces [space0, space0 + gridDim.x / gps), gps = ceil(bpk / GROUP) workgroups per space: workgroup g of a
+// space sorts its buckets [g * GROUP, (g + 1) * GROUP) together (one CSR over their keys): the anchor and source
+// buckets hold a few hundred records each, and a workgroup per bucket would spend most of its time on the
+// per-bucket scan and barriers.  bend: the end of every bucket (bpos after pass 1), tot: the bucket totals; a
+// bucket starts at its end minus its total, so that the anchor and source buckets can be sorted before the
 // entry buckets are filled.
-template <int SHIFT>
+template <int SHIFT, int GROUP>
 __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict__ bend, const int* __restrict__ tot,
-                                                           int first, const Rec* __restrict__ trec, FGeo G,
+                                                           int space0, const Rec* __restrict__ trec, FGeo G,
                                                            SortOut o) {
   int* __restrict__ start = o.start;
-  constexpr int kBucketKeys = 1 << SHIFT;
-  __shared__ int cnt[kBucketKeys];
-  __shared__ int cur[kBucketKeys];
+  constexpr int kKeys = GROUP << SHIFT;            // keys of one workgroup
+  __shared__ int cnt[kKeys];
+  __shared__ int cur[kKeys];
   __shared__ int wsum[kSortBlock / kWave + 1];
-  const int bucket = first + (int)blockIdx.x;
-  const int hi = bend[bucket];
-  const int lo = hi - tot[bucket];
   const int bpk = G.ncell_pad >> SHIFT;            // buckets per key space
+  const int gps = (bpk + GROUP - 1) / GROUP;
+  const int space = space0 + (int)blockIdx.x / gps;   // 0 entries, 1 anchors, 2 sources
+  const int b0 = space * bpk + ((int)blockIdx.x % gps) * GROUP;
+  const int b1 = min(b0 + GROUP, (space + 1) * bpk);
+  const int hi = bend[b1 - 1];
+  const int lo = bend[b0] - tot[b0];
+  const int base_key = b0 << SHIFT;
+  const int nkeys = (b1 - b0) << SHIFT;
   const int E = bend[bpk] - tot[bpk], EA = bend[2 * bpk] - tot[2 * bpk];
   const int4* tki = (const int4*)trec;             // int half of record p: tki[2 * p + 1]
-  for (int i = threadIdx.x; i < kBucketKeys; i += kSortBlock) {
+  for (int i = threadIdx.x; i < kKeys; i += kSortBlock) {
     cnt[i] = 0;
     cur[i] = 0;
   }
   __syncthreads();
-  // A bucket of at most kSortBlock * kSortItems records (the common case) is read once and kept in registers
+  // A group of at most kSortBlock * kSortItems records (the common case) is read once and kept in registers
   // from the count to the scatter, and the count's atomic returns each record's rank within its cell; larger
-  // buckets count from the keys, read the records again and rank them with a second atomic at the scatter.
+  // groups count from the keys, read the records again and rank them with a second atomic at the scatter.
   const bool one = hi - lo <= kSortBlock * kSortItems;
   Rec r1[kSortItems];
   int rank[kSortItems];                            // one-read path: the record's rank within its cell
@@ -531,7 +539,7 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
     }
 #pragma unroll
     for (int u = 0; u < kSortItems; ++u)
-      if (lo + u * kSortBlock + (int)threadIdx.x < hi) rank[u] = atomicAdd(cnt + (r1[u].i.z & (kBucketKeys - 1)), 1);
+      if (lo + u * kSortBlock + (int)threadIdx.x < hi) rank[u] = atomicAdd(cnt + (r1[u].i.z - base_key), 1);
   } else {
     for (int base = lo; base < hi; base += kSortBlock * kSortItems) {
       int key[kSortItems];
@@ -542,11 +550,11 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
       }
 #pragma unroll
       for (int u = 0; u < kSortItems; ++u)
-        if (key[u] >= 0) atomicAdd(cnt + (key[u] & (kBucketKeys - 1)), 1);
+        if (key[u] >= 0) atomicAdd(cnt + (key[u] - base_key), 1);
     }
   }
   __syncthreads();
-  constexpr int per = kBucketKeys / kSortBlock;
+  constexpr int per = kKeys / kSortBlock;
   int vals[per];
   int s = 0;
 #pragma unroll
@@ -556,23 +564,21 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
   }
   int total;
   int run = block_exclusive_scan<kSortBlock>(s, wsum, total);
-  const int base_key = bucket << SHIFT;
 #pragma unroll
   for (int k = 0; k < per; ++k) {
     const int i = threadIdx.x * per + k;
     cnt[i] = run;
-    start[base_key + i] = lo + run;
+    if (i < nkeys) start[base_key + i] = lo + run;
     run += vals[k];
   }
-  if (bucket == G.nbuckets - 1 && threadIdx.x == 0) start[3 * G.ncell_pad] = hi;
+  if (b1 == G.nbuckets && threadIdx.x == 0) start[3 * G.ncell_pad] = hi;
   __syncthreads();
-  const int space = bucket / bpk;                  // 0 entries, 1 anchors, 2 sources
   const int off = space == 0 ? 0 : (space == 1 ? E : EA);
   Rec* out = space == 1 ? o.arec : o.srec;
   const int kbase = space * G.ncell_pad;
   const int plane_cells = G.GH * G.GW;
   auto place = [&](Rec r, int rk) {               // rk: the record's rank within its cell
-    const int kk = r.i.z & (kBucketKeys - 1);
+    const int kk = r.i.z - base_key;
     const int pos = lo + cnt[kk] + rk - off;
     r.i.z -= kbase;
     if (space == 0) {
@@ -602,7 +608,7 @@ __global__ void __launch_bounds__(kSortBlock) k_sort_pass2(const int* __restrict
     }
 #pragma unroll
     for (int u = 0; u < kSortItems; ++u)
-      if (live[u]) place(r[u], atomicAdd(cur + (r[u].i.z & (kBucketKeys - 1)), 1));
+      if (live[u]) place(r[u], atomicAdd(cur + (r[u].i.z - base_key), 1));
   }
 }
 
@@ -1880,12 +1886,22 @@ int fast_plan_impl(const atl_fast_geometry* geo, const FGeo& G, const float* x, 
   const SortOut out{at_off<int>(ws, geo->off_start), at_off<float4>(ws, geo->off_epos),
                     at_off<float>(ws, geo->off_etim), at_off<int>(ws, geo->off_eself),
                     at_off<Rec>(ws, geo->off_arec), at_off<Rec>(ws, geo->off_srec), at_off<int>(ws, geo->off_self)};
-  auto pass2 = G.bshift == 10 ? k_sort_pass2<10> : G.bshift == 11 ? k_sort_pass2<11>
-             : G.bshift == 12 ? k_sort_pass2<12> : k_sort_pass2<13>;
+  // the anchor and source spaces in groups of kSortGroupKeys keys; the entries' space (trajectory model) one
+  // bucket per workgroup
+  constexpr int kSortGroupKeys = 4096;
+  auto pass2g = G.bshift == 10 ? k_sort_pass2<10, kSortGroupKeys / 1024> : G.bshift == 11 ? k_sort_pass2<11, kSortGroupKeys / 2048>
+              : G.bshift == 12 ? k_sort_pass2<12, 1> : k_sort_pass2<13, 1>;
   const int bpk = G.ncell_pad >> G.bshift;
-  const int first = kSplit ? bpk : 0;
-  hipLaunchKernelGGL(pass2, dim3(G.nbuckets - first), dim3(kSortBlock), 0, stream, (const int*)bpos,
-                     (const int*)tot, first, (const Rec*)trec, G, out);
+  const int grp = std::max(1, kSortGroupKeys >> G.bshift);
+  const int gps = (bpk + grp - 1) / grp;
+  hipLaunchKernelGGL(pass2g, dim3(2 * gps), dim3(kSortBlock), 0, stream, (const int*)bpos, (const int*)tot, 1,
+                     (const Rec*)trec, G, out);
+  if (!kSplit) {
+    auto pass2 = G.bshift == 10 ? k_sort_pass2<10, 1> : G.bshift == 11 ? k_sort_pass2<11, 1>
+               : G.bshift == 12 ? k_sort_pass2<12, 1> : k_sort_pass2<13, 1>;
+    hipLaunchKernelGGL(pass2, dim3(bpk), dim3(kSortBlock), 0, stream, (const int*)bpos, (const int*)tot, 0,
+                       (const Rec*)trec, G, out);
+  }
   if (kSplit) {
     int2* item = (int2*)trec;                    // [0, E) of the items; pass 2 has read the records
     const Rec* srec = at_off<Rec>(ws, geo->off_srec);
