@@ -256,7 +256,7 @@ int atl_fast_pair_fwd(const atl_fast_geometry* geo, const void* ws, float* out, 
 /* gv (N,2) written: each source's gradient, zero for sources outside the plan (no fill needed). */
 int atl_fast_pair_bwd(const atl_fast_geometry* geo, void* ws, const float* gS, float* gv, hipStream_t stream);
 /* The same backward when the velocities were DenseLinearFlow.field(x) (atl/motion/parametric.py:212-216,
- * 235-251): the gradient goes to the flow grid (B,2,Hg,Wg), accumulated into ggrid (zero it first), as
+ * 235-251): the gradient goes to the flow grid (B,2,Hg,Wg), written to ggrid (no fill needed), as
  * atl_fast_pair_bwd followed by sample_grid's adjoint at x would give it (float sums in another order), with no
  * per-event gradient array.  img_h, img_w: the pixel -> grid scaling of atl_sample_grid_fwd (0, 0: x are grid
  * coordinates).  The plan's temporary sort records (dead after the plan) hold the per-source gradients. */

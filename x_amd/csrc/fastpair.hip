@@ -1417,10 +1417,13 @@ constexpr int kAdjListBlock = 1024;
 constexpr int kAdjMaxSlices = 64;
 
 // Source records of every (batch, tile) over its S slices: one thread per (tile, slice), the slices of a tile in
-// SP consecutive lanes (SP: S rounded up to a power of two, at most 64), summed across them.
+// SP consecutive lanes (SP: S rounded up to a power of two, at most 64), summed across them.  The same threads
+// clear the flow-grid gradient (ng floats), which k_src_flow_adjoint then accumulates.
 __global__ void __launch_bounds__(kBlock) k_src_tile_counts(FPlan p, FGeo G, int ntiles, int SP,
-                                                            int* __restrict__ tilecnt) {
+                                                            int* __restrict__ tilecnt, float* __restrict__ ggrid,
+                                                            int64_t ng) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t g = i; g < ng; g += (int64_t)gridDim.x * blockDim.x) ggrid[g] = 0.f;
   const int q = i / SP, s = i - q * SP;
   int n = 0;
   if (q < ntiles && s < G.S) {
@@ -2016,7 +2019,11 @@ int atl_fast_flow_adjoint(const atl_fast_geometry* geo, void* ws, int64_t Hg, in
   if (!make_geo(geo, G)) { set_error("fast_flow_adjoint: geometry not initialised"); return 1; }
   if (Hg < 1 || Wg < 1 || (double)geo->B * 2 * Hg * Wg >= 2.0e9 || G.S > kAdjMaxSlices) { set_error("fast_flow_adjoint: bad sizes (Hg=%lld Wg=%lld, S=%d <= %d)", (long long)Hg, (long long)Wg, G.S, kAdjMaxSlices); return 1; }
   if (!ws || !ggrid) { set_error("fast_flow_adjoint: null argument"); return 1; }
-  if (geo->N == 0 || geo->M == 0) return 0;
+  if (geo->N == 0 || geo->M == 0) {              // no pairs: a zero gradient (0.0f is all-zero bits)
+    const int64_t ng = geo->B * 2 * Hg * Wg;
+    hipLaunchKernelGGL(k_fill_zero, dim3(grid_for(ng)), dim3(kBlock), 0, stream, (int*)ggrid, ng);
+    return check_launch("fast_flow_adjoint");
+  }
   const FPlan p = make_plan(ws, geo);
   const float2* gvr = at_off<float2>(ws, geo->off_trec);
   FlowGeo F;
@@ -2032,8 +2039,9 @@ int atl_fast_flow_adjoint(const atl_fast_geometry* geo, void* ws, int64_t Hg, in
   int* tilecnt = nchunk + 64;
   int SP = 1;
   while (SP < G.S) SP <<= 1;
-  hipLaunchKernelGGL(k_src_tile_counts, dim3(grid_for(tiles * SP)), dim3(kBlock), 0, stream, p, G, (int)tiles, SP,
-                     tilecnt);
+  const int64_t ng = geo->B * 2 * Hg * Wg;      // the gradient is written, not added to: cleared here first
+  hipLaunchKernelGGL(k_src_tile_counts, dim3(grid_for(std::max<int64_t>(tiles * SP, ng / 4))), dim3(kBlock), 0, stream,
+                     p, G, (int)tiles, SP, tilecnt, ggrid, ng);
   hipLaunchKernelGGL(k_src_adj_list, dim3(1), dim3(kAdjListBlock), 0, stream, (const int*)tilecnt, (int)tiles, info,
                      nchunk);
   hipLaunchKernelGGL(k_src_flow_adjoint, dim3((unsigned)maxc), dim3(kAdjBlock), 0, stream, p, G, F,

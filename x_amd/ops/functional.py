@@ -640,7 +640,7 @@ class FastPairPlan:
         if self.traj:
             raise ValueError("a trajectory plan has backward_traj")
         gS = self._check_gs(gS)
-        gg = torch.zeros(int(B), 2, int(Hg), int(Wg), dtype=F32, device=self.device)
+        gg = torch.empty(int(B), 2, int(Hg), int(Wg), dtype=F32, device=self.device)   # written by the adjoint
         with torch.cuda.device(self.device):
             st = stream_of(gg)
             call("atl_fast_pair_bwd_src", ctypes.byref(self.geo), ptr(self.ws), ptr(gS), st)
