@@ -724,6 +724,9 @@ def main():
     def step():
         for prm in motion.parameters():
             prm.grad = None
+        # a training step changes the flow grid, so its interleaved copy (kept per field version) is made again in
+        # every timed step rather than reused from the previous one
+        F._CL_CACHE.clear()
         loss = obj(ev, motion)["loss"]
         if blobs:                                  # the splat leg of the contention config: IWE contrast at 0.5
             loss = loss - iwe_variance(ev, motion, 0.5)

@@ -116,6 +116,13 @@ int atl_sample_grid_bwd(const float* gout, int64_t B, int64_t C, int64_t Hg, int
 int atl_sample_grid_bwd_pos(const float* gout, const float* field, int64_t B, int64_t C, int64_t Hg, int64_t Wg,
                             const float* pos, const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gpos,
                             hipStream_t stream);
+/* Two-channel fields (flows): atl_flow_interleave copies a (B,2,Hg,Wg) field into out (B,Hg,Wg,2), node by node;
+ * atl_sample_flow_il then samples it as atl_sample_grid_fwd samples the planar field with C = 2 (the same bits)
+ * from two 16-byte reads per event instead of four 8-byte reads; needs Wg >= 2.  No counterpart in the
+ * reference (a layout of its sample_grid, atl/motion/parametric.py:235-251). */
+int atl_flow_interleave(const float* field, int64_t B, int64_t Hg, int64_t Wg, float* out, hipStream_t stream);
+int atl_sample_flow_il(const float* field_il, int64_t B, int64_t Hg, int64_t Wg, const float* pos, const int64_t* b,
+                       int64_t N, int64_t img_h, int64_t img_w, float* out, hipStream_t stream);
 /* Many-channel fields (a trajectory coefficient grid: C = 2K channels sampled at every event), no counterpart
  * in the reference's extension: they replace the same sample_grid (atl/motion/parametric.py:235-251) where the
  * plane layout would cost C loads per corner.  atl_field_channels_last writes the channels-last copy

@@ -262,6 +262,36 @@ def test_sample_grid_matches_oracle():
     close_rel(N(tg.grad), O.sample_grid_bwd(g, idx, wts, grid.shape), 1e-5)
 
 
+@pytest.mark.parametrize("Hg,Wg,img", [(23, 31, True), (40, 48, True), (9, 2, False), (1, 5, True)])
+def test_sample_flow_interleaved_same_bits(Hg, Wg, img):
+    """Two-channel fields are sampled from the node-interleaved copy: bit-equal to the oracle (positions inside and
+    outside the grid, absent batches zero), and an in-place update of the field makes a new copy."""
+    print(f"sample_grid flow interleaved {Hg}x{Wg} img={img}", flush=True)
+    rng = np.random.default_rng(Hg * 7 + Wg)
+    n, B = 5000, 2
+    H, W = (47, 61) if img else (0, 0)
+    span_x, span_y = (W, H) if img else (Wg, Hg)
+    pos = np.stack([rng.uniform(-3, span_x + 2, n), rng.uniform(-3, span_y + 2, n)], 1).astype(F32)
+    b = rng.integers(0, B, n).astype(np.int64)
+    b[::89] = B
+    fld = rng.standard_normal((B, 2, Hg, Wg)).astype(F32)
+    tf = T(fld)
+    ok = b < B
+
+    def check(f):
+        out = N(F.sample_grid_hip(tf, T(pos), T(b), img_hw=(H, W)))
+        want = (O.dense_velocity(f, pos[ok], b[ok], H, W) if img else O.sample_grid(f, pos[ok], b[ok]))[0]
+        assert np.array_equal(out[ok], want) and not out[~ok].any()
+
+    check(fld)
+    check(fld)                                     # the cached copy
+    if Wg >= 2:                                    # a view of the same field (detach) finds the same copy
+        assert F._interleaved(tf.detach()) is F._interleaved(tf)
+    with torch.no_grad():
+        tf.mul_(-0.5)                              # a new version of the field: a new copy
+    check(fld * np.float32(-0.5))
+
+
 @pytest.mark.parametrize("C,img", [(4, False), (5, False), (20, False), (7, True), (20, True)])
 def test_sample_grid_channels_last_same_bits(C, img):
     """Many-channel fields go through the channels-last copy: the forward equals the oracle bit for bit, the

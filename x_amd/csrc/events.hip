@@ -331,6 +331,47 @@ __global__ void __launch_bounds__(kBlock) k_field_channels_last(const float* __r
   out[i] = make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// Two-channel fields (flows) interleaved by node, (B, Hg, Wg, 2): a grid row's two corner nodes with both
+// channels are 16 contiguous bytes, so a lookup reads two pieces instead of four; the sums are
+// k_sample_grid_fwd's, bit for bit.
+__global__ void __launch_bounds__(kBlock) k_flow_interleave(const float* __restrict__ field, int64_t plane,
+                                                            int64_t total, float2* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // node (b, o)
+  if (i >= total) return;
+  const int64_t b = i / plane, o = i - b * plane;
+  const float* f = field + b * 2 * plane + o;
+  out[i] = make_float2(f[0], f[plane]);
+}
+
+// Wg >= 2 (a row's corners are adjacent nodes).
+__global__ void __launch_bounds__(kBlock) k_sample_flow_il(const float* __restrict__ fil, int64_t B, int Hg, int Wg,
+                                                           const float2* __restrict__ pos,
+                                                           const int64_t* __restrict__ bidx, int64_t N, float sxw,
+                                                           float syh, int scale, float2* __restrict__ out) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t b = bidx[n];
+  if (!batch_ok(b, B)) {
+    out[n] = make_float2(0.f, 0.f);
+    return;
+  }
+  const float2 p = pos[n];
+  const GridCorners g = grid_corners(p.x, p.y, Hg, Wg, sxw, syh, scale != 0);
+  const float* f = fil + b * 2 * ((int64_t)Hg * Wg);
+  float4 r0, r1;                                 // (c0, c1) of corner x0, then of x0 + 1: 8-byte aligned
+  __builtin_memcpy(&r0, f + 2 * (int64_t)g.o00, sizeof(float4));
+  __builtin_memcpy(&r1, f + 2 * (int64_t)g.o10, sizeof(float4));
+  float v0 = r0.x * g.w00;
+  v0 = v0 + r0.z * g.w01;
+  v0 = v0 + r1.x * g.w10;
+  v0 = v0 + r1.z * g.w11;
+  float v1 = r0.y * g.w00;
+  v1 = v1 + r0.w * g.w01;
+  v1 = v1 + r1.y * g.w10;
+  v1 = v1 + r1.w * g.w11;
+  out[n] = make_float2(v0, v1);
+}
+
 __device__ __forceinline__ float corner_sum(float f00, float f01, float f10, float f11, const GridCorners& g) {
   float v = f00 * g.w00;
   v = v + f01 * g.w01;
@@ -773,6 +814,28 @@ int atl_field_channels_last(const float* field, int64_t B, int64_t C, int64_t Hg
   hipLaunchKernelGGL(k_field_channels_last, dim3(grid_for(total)), dim3(kBlock), 0, stream, field, (int)C, (int)Q,
                      Hg * Wg, total, (float4*)out);
   return check_launch("field_channels_last");
+}
+
+int atl_flow_interleave(const float* field, int64_t B, int64_t Hg, int64_t Wg, float* out, hipStream_t stream) {
+  if (B < 0 || !dims_ok(Hg, Wg)) { set_error("flow_interleave: bad sizes"); return 1; }
+  const int64_t total = B * Hg * Wg;
+  if (total == 0) return 0;
+  if (!field || !out) { set_error("flow_interleave: null pointer"); return 1; }
+  hipLaunchKernelGGL(k_flow_interleave, dim3(grid_for(total)), dim3(kBlock), 0, stream, field, Hg * Wg, total,
+                     (float2*)out);
+  return check_launch("flow_interleave");
+}
+
+int atl_sample_flow_il(const float* field_il, int64_t B, int64_t Hg, int64_t Wg, const float* pos, const int64_t* b,
+                       int64_t N, int64_t img_h, int64_t img_w, float* out, hipStream_t stream) {
+  if (N < 0 || B < 0 || !dims_ok(Hg, Wg) || Wg < 2) { set_error("sample_flow_il: bad sizes (Wg >= 2)"); return 1; }
+  if (N == 0) return 0;
+  if (!field_il || !pos || !b || !out) { set_error("sample_flow_il: null pointer"); return 1; }
+  const int scale = img_h > 0 && img_w > 0;
+  const float sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1), syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
+  hipLaunchKernelGGL(k_sample_flow_il, dim3(grid_for(N)), dim3(kBlock), 0, stream, field_il, B, (int)Hg, (int)Wg,
+                     (const float2*)pos, b, N, sxw, syh, scale, (float2*)out);
+  return check_launch("sample_flow_il");
 }
 
 int atl_sample_grid_fwd_cl(const float* field_cl, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,

@@ -60,6 +60,8 @@ _SIGS = {
     "atl_bin_counts": [_P, _P, _I, _I, _I, _P, _P],
     "atl_bin_counts_sorted": [_P, _P, _I, _I, _I, _P, _P],
     "atl_visible_fraction": [_P, _P, _P, _P, _I, _P, _P, _I, _I, _D, _I, _I, _P, _P],
+    "atl_flow_interleave": [_P, _I, _I, _I, _P, _P],
+    "atl_sample_flow_il": [_P, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_anchored_epilogue_fwd": [_P, _P, _P, _I, _D, _D, _P, _P, _P, _P],
     "atl_anchored_epilogue_bwd": [_P, _P, _P, _I, _P, _P],
     "atl_anchored_score_mean_scratch_bytes": [],
@@ -148,7 +150,7 @@ _TIMED = {}          # entry point -> list of (start, end, events) per timed cal
 _EVERY = {"n": 1, "calls": {}}   # time one call in n of each entry point
 # position of the event count N in the arguments of the entry points whose calls are sized by it
 _NARG = {"atl_sample_grid_fwd": 7, "atl_sample_grid_bwd_planned": 6, "atl_sample_grid_bwd_binned": 7, "atl_sample_grid_bwd_pos": 8,
-         "atl_sample_grid_fwd_cl": 7, "atl_sample_grid_bwd_pos_cl": 8, "atl_traj_displacement": 9,
+         "atl_sample_grid_fwd_cl": 7, "atl_sample_flow_il": 6, "atl_sample_grid_bwd_pos_cl": 8, "atl_traj_displacement": 9,
          "atl_traj_gout": 2,
          "atl_splat_gauss_fwd": 3, "atl_splat_gauss_bwd": 4, "atl_splat_gauss_fwd_ws": 3,
          "atl_gather_bilinear_fwd": 3, "atl_gather_bilinear_bwd_ws": 4, "atl_splat_bilinear_fwd_ws": 3,

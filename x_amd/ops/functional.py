@@ -133,25 +133,45 @@ def _tile_plan_ok(B, C, Hg, Wg):
     return C <= 4 or (C <= 32 and B * ((Wg + 16) // 16) * ((Hg + 16) // 16) <= 16384)
 
 
-_CL_CACHE: list = []          # [(field, its version, its channels-last copy)]: the last few fields converted
+_CL_CACHE: list = []          # [(field, its version, layout, the copy)]: the last few fields converted
+
+
+def _cached_copy(fld: torch.Tensor, layout: str, make) -> torch.Tensor:
+    """A layout copy of a field that is sampled several times per step (the trajectory model's coefficient grid:
+    every fixed-point step, the final look-up and their backward; a flow: at the sources and at the anchors),
+    made once while the field is unchanged: the copy is kept with the field (which it holds alive) and its in-place
+    version counter, which views of it (detach()) share, and any update of the field makes a new one."""
+    ver = fld._version
+    for src, v, lay, cp in _CL_CACHE:
+        if (lay == layout and v == ver and src.data_ptr() == fld.data_ptr() and src.shape == fld.shape
+                and src.stride() == fld.stride() and src.dtype == fld.dtype and src._version == ver):
+            return cp
+    cp = make()
+    _CL_CACHE.insert(0, (fld, ver, layout, cp))
+    del _CL_CACHE[4:]
+    return cp
 
 
 def _channels_last(fld: torch.Tensor) -> torch.Tensor:
-    """(B, Hg, Wg, 4 ceil(C / 4)) channels-last copy of a (B, C, Hg, Wg) field.  A field that is sampled several
-    times per step (the trajectory model's coefficient grid: every fixed-point step, the final look-up and their
-    backward) is converted once while it is unchanged: the copy is kept with the field object and its in-place
-    version counter, and any update of the field makes a new one."""
-    ver = fld._version
-    for src, v, fcl in _CL_CACHE:
-        if src is fld and v == ver:
-            return fcl
-    B, C, Hg, Wg = fld.shape
-    fcl = torch.empty(B, Hg, Wg, 4 * ((C + 3) // 4), device=fld.device, dtype=F32)
-    with torch.cuda.device(fld.device):
-        call("atl_field_channels_last", ptr(fld), B, C, Hg, Wg, ptr(fcl), stream_of(fld))
-    _CL_CACHE.insert(0, (fld, ver, fcl))
-    del _CL_CACHE[4:]
-    return fcl
+    """(B, Hg, Wg, 4 ceil(C / 4)) channels-last copy of a (B, C, Hg, Wg) field (cached, _cached_copy)."""
+    def make():
+        B, C, Hg, Wg = fld.shape
+        fcl = torch.empty(B, Hg, Wg, 4 * ((C + 3) // 4), device=fld.device, dtype=F32)
+        with torch.cuda.device(fld.device):
+            call("atl_field_channels_last", ptr(fld), B, C, Hg, Wg, ptr(fcl), stream_of(fld))
+        return fcl
+    return _cached_copy(fld, "cl", make)
+
+
+def _interleaved(fld: torch.Tensor) -> torch.Tensor:
+    """(B, Hg, Wg, 2) node-interleaved copy of a (B, 2, Hg, Wg) flow (cached, _cached_copy)."""
+    def make():
+        B, _, Hg, Wg = fld.shape
+        fil = torch.empty(B, Hg, Wg, 2, device=fld.device, dtype=F32)
+        with torch.cuda.device(fld.device):
+            call("atl_flow_interleave", ptr(fld), B, Hg, Wg, ptr(fil), stream_of(fld))
+        return fil
+    return _cached_copy(fld, "il", make)
 
 
 class _SampleGrid(torch.autograd.Function):
@@ -162,7 +182,8 @@ class _SampleGrid(torch.autograd.Function):
     reads no row by event index; wider fields bin the positions in the forward (a device plan) and gather their
     rows in the backward.  The positions' gradient (through the interpolation weights) is a per-event gather.
     Fields of CL_MIN_CHANNELS channels or more are sampled from a channels-last copy (same bits, a node's channels
-    in one run)."""
+    in one run), two-channel fields (flows) from a node-interleaved copy (same bits, a grid row's two corners in
+    one 16-byte read)."""
 
     CL_MIN_CHANNELS = 4
 
@@ -183,6 +204,9 @@ class _SampleGrid(torch.autograd.Function):
                 call("atl_sample_grid_fwd_cl", ptr(fcl), B, C, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w),
                      ptr(out), st)
                 fld = fcl                          # the backward's position gradient reads the same copy
+            elif C == 2 and Wg >= 2:               # a flow: two 16-byte reads per lookup (the backward: planar)
+                call("atl_sample_flow_il", ptr(_interleaved(fld_in)), B, Hg, Wg, ptr(pos), ptr(b), N, int(img_h),
+                     int(img_w), ptr(out), st)
             else:
                 call("atl_sample_grid_fwd", ptr(fld), B, C, Hg, Wg, ptr(pos), ptr(b), N, int(img_h), int(img_w),
                      ptr(out), st)
