@@ -150,6 +150,17 @@ int atl_sample_grid_bwd_pos_cl(const float* gout, const float* field_cl, int64_t
 int atl_traj_displacement(const float* field_cl, int64_t B, int64_t C, int64_t K, int64_t Hg, int64_t Wg,
                           const float* gpos, const int64_t* b, const float* t, int64_t N, int64_t basis, float* out,
                           hipStream_t stream);
+/* The exposure correction of atl/objectives/ats.py:31-50 (visible_fraction) for PixelTrajectories in one pass:
+ * each anchor's trajectory start (n_fp Picard steps from xa, as PixelTrajectories.origin), its coefficients looked
+ * up once there, the trajectory evaluated at the n_check bin centres, and the weighted share of centres inside the
+ * sensor (counts (B, n_check), centres (n_check)), out (M) written; bit-identical to the composed
+ * atl_traj_displacement calls and atl_visible_fraction's sums.  Grid coordinates of a pixel position p:
+ * (p - offset) / tile (tile 1: p).  No counterpart in the reference (its visible_fraction transports the anchors
+ * once per centre). */
+int atl_traj_visible(const float* field_cl, int64_t B, int64_t C, int64_t K, int64_t Hg, int64_t Wg, const float* xa,
+                     const float* ta, const int64_t* ba, int64_t M, int64_t n_fp, double offset, int64_t tile,
+                     int64_t basis, const float* counts, const float* centres, int64_t n_check, double tau,
+                     int64_t H, int64_t W, float* out, hipStream_t stream);
 int atl_traj_gout(const float* gd, const float* t, int64_t N, int64_t K, int64_t basis, float* gout,
                   hipStream_t stream);
 /* The same adjoint through a tile plan: atl_grid_plan bins the positions by the 16x16 tile of their base

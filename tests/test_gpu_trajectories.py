@@ -177,6 +177,37 @@ def test_pixel_trajectories_device_matches_cpu(K, kind, tile):
     close_rel(res[DEV][1], res["cpu"][1], 1e-4)
 
 
+@pytest.mark.parametrize("K,kind,tile", [(10, "bspline", 1), (3, "bezier", 4), (1, "polynomial", 1),
+                                         (10, "bspline", 4)])
+def test_traj_visible_fraction_same_bits(K, kind, tile):
+    """The one-pass exposure correction for trajectories against the composed device ops (origin, then the
+    displacement at every bin centre, then the weighted share), bit for bit."""
+    print(f"trajectory visible fraction K={K} {kind} tile={tile}", flush=True)
+    win = synth.small_window(seed=K + tile, n=4000, B=2)
+    rng = np.random.default_rng(K * 3 + tile)
+    coeffs = synth.trajectory_coeffs(rng, 2, K, win.height, win.width, sigma_px=8.0, dmax=6.0)
+    ev = EventPacket.from_window(win, DEV)
+    m = PixelTrajectories(T(coeffs), K, kind, tile=tile)
+    xa = ev.xy + T(rng.standard_normal((win.n, 2)).astype(F32))
+    tau, n_check = 0.3, 16
+    got = F.traj_visible_fraction(m.tile_c, K, kind, m.n_fp, m.offset, m.tile, xa, ev.t, ev.b, ev.t, ev.b, 2,
+                                  win.height, win.width, tau, n_check)
+    with torch.no_grad():
+        counts = F.bin_counts(ev.t, ev.b, 2, n_check)
+        edges = torch.linspace(0, 1, n_check + 1, device=DEV)
+        start = m.origin(xa, ev.t, ev.b)
+        vis, tot = torch.zeros_like(ev.t), torch.zeros_like(ev.t)
+        for k, c in enumerate((0.5 * (edges[:-1] + edges[1:])).tolist()):
+            y = start + m.displacement(start, ev.b, torch.full_like(ev.t, c))
+            seen = (y[:, 0] >= 0) & (y[:, 0] <= win.width - 1) & (y[:, 1] >= 0) & (y[:, 1] <= win.height - 1)
+            w = counts[ev.b, k] * ((ev.t - c).abs() <= tau).float()
+            vis += w * seen.float()
+            tot += w
+        want = (vis / tot.clamp(min=1)).clamp(min=1e-3)
+    assert torch.equal(got, want)
+    assert 0.01 < float((want < 0.999).float().mean()) < 0.99      # trajectories leave the sensor and stay
+
+
 def test_pixel_trajectories_linear_closed_form():
     """Degree-1 polynomial trajectories with a constant coefficient field are the linear warp:
     transport(x, t, t') = x + c (t' - t), velocity = c."""

@@ -636,6 +636,104 @@ __global__ void __launch_bounds__(kBlock) k_traj_displacement(const float4* __re
 // Its output gradient per coefficient channel: gout[n, c] = g_k(t_n) * gd_n.y for c = k - 1 < K and
 // g_k(t_n) * gd_n.x for c = K + k - 1, the rows that the field adjoint and the position gradient of the sampler
 // take.  One lane per (event, channel quad), so the rows are written by consecutive lanes.
+// The exposure correction of atl/objectives/ats.py:31-50 for PixelTrajectories in one pass: anchor i's trajectory
+// start p (n_fp Picard steps p <- xa - d(p, t_a) from p = xa, as PixelTrajectories.origin), its coefficients
+// looked up once at p, the trajectory evaluated at the n_check bin centres, y = p + d(p, c_k), and k_visible's
+// weighted share of the centres where y is inside the sensor.  Lanes as in k_traj_displacement (Q per anchor, one
+// channel quad each) and the same sums in the same order, so every p and y equals the composed ops' bits.  Grid
+// coordinates of a pixel position: (p - off) / tile (tile 1: p itself).
+template <int K>
+__global__ void __launch_bounds__(kBlock) k_traj_visible(const float4* __restrict__ fcl, int64_t B, int Hg, int Wg,
+                                                         const float2* __restrict__ xa,
+                                                         const float* __restrict__ ta,
+                                                         const int64_t* __restrict__ bidx, int basis, int64_t M,
+                                                         int n_fp, float off, float tile,
+                                                         const float* __restrict__ counts,
+                                                         const float* __restrict__ centres, int n_check, float tau,
+                                                         float wmax, float hmax, float* __restrict__ out) {
+  constexpr int C = 2 * K, Q = (C + 3) / 4, EPW = kWave / Q;   // anchors per wave
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int e = lane / Q, q = lane - e * Q;
+  const int64_t n = wave * EPW + e;
+  const bool live = e < EPW && n < M;
+  const int lead = min(e * Q, kWave - 1);        // the anchor's first lane
+  int64_t b = -1;
+  float2 x0 = make_float2(0.f, 0.f);
+  float t = 0.f;
+  if (live) {
+    b = bidx[n];
+    x0 = xa[n];
+    t = ta[n];
+  }
+  const bool ok = live && batch_ok(b, B);
+  const float4* f = fcl + (ok ? b : 0) * ((int64_t)Hg * Wg) * Q + q;
+  // this lane's quad of the coefficients at grid coordinates of pixel position p: v[4]
+  auto lookup = [&](float2 p, float (&v)[4]) {
+    const float gx = tile == 1.f ? p.x : (p.x - off) / tile, gy = tile == 1.f ? p.y : (p.y - off) / tile;
+    const GridCorners c = grid_corners(gx, gy, Hg, Wg, 1.f, 1.f, false);
+    const float4 a = f[(int64_t)c.o00 * Q], h0 = f[(int64_t)c.o01 * Q], h1 = f[(int64_t)c.o10 * Q],
+                 k1 = f[(int64_t)c.o11 * Q];
+    v[0] = corner_sum(a.x, h0.x, h1.x, k1.x, c);
+    v[1] = corner_sum(a.y, h0.y, h1.y, k1.y, c);
+    v[2] = corner_sum(a.z, h0.z, h1.z, k1.z, c);
+    v[3] = corner_sum(a.w, h0.w, h1.w, k1.w, c);
+  };
+  // d = sum_k c_k g_k(tt) from this lane's quad v, combined over the anchor's lanes in lane order (the event's
+  // first lane adds the others' sums, k_traj_displacement's order), returned to every lane of the anchor
+  auto disp = [&](const float (&v)[4], float tt) {
+    float g[K];
+    traj_basis<K>(tt, basis, g);
+    float dx = 0.f, dy = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ch = 4 * q + j;
+      if (ch >= C) break;
+      const int k = ch < K ? ch : ch - K;
+      float gk = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < K; ++kk) gk = kk == k ? g[kk] : gk;
+      if (ch < K)
+        dy = dy + v[j] * gk;
+      else
+        dx = dx + v[j] * gk;
+    }
+    float sx = dx, sy = dy;
+#pragma unroll
+    for (int i = 1; i < Q; ++i) {
+      const int src = min(lane + i, kWave - 1);
+      const float ox = __shfl(dx, src), oy = __shfl(dy, src);
+      if (q + i < Q) {
+        sx = sx + ox;
+        sy = sy + oy;
+      }
+    }
+    return make_float2(__shfl(sx, lead), __shfl(sy, lead));
+  };
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  float2 p = x0;
+  for (int it = 0; it < n_fp; ++it) {            // p <- xa - d(p, t_a)
+    if (ok) lookup(p, v);
+    const float2 d = disp(v, t);                  // every lane takes part in the shuffles
+    if (ok) p = make_float2(x0.x - d.x, x0.y - d.y);
+  }
+  if (ok) lookup(p, v);
+  float vis = 0.f, tot = 0.f;
+  const float* cnt = counts + (ok ? b : 0) * n_check;
+  for (int k = 0; k < n_check; ++k) {
+    const float c = centres[k];
+    const float2 d = disp(v, c);                  // every lane takes part in the shuffles
+    if (!ok) continue;
+    const float yx = p.x + d.x, yy = p.y + d.y;
+    const float near = fabsf(t - c) <= tau ? 1.f : 0.f;
+    const float inside = (yx >= 0.f && yx <= wmax && yy >= 0.f && yy <= hmax) ? 1.f : 0.f;
+    const float w = cnt[k] * near;
+    vis = vis + w * inside;
+    tot = tot + w;
+  }
+  if (live && q == 0) out[n] = fmaxf(vis / fmaxf(tot, 1.f), 1e-3f);
+}
+
 template <int K>
 __global__ void __launch_bounds__(kBlock) k_traj_gout(const float2* __restrict__ gd, const float* __restrict__ t,
                                                       int basis, int N, float* __restrict__ gout) {
@@ -903,6 +1001,37 @@ int atl_traj_displacement(const float* field_cl, int64_t B, int64_t C, int64_t K
 #undef ATL_TRAJ_CASE
   }
   return check_launch("traj_displacement");
+}
+
+int atl_traj_visible(const float* field_cl, int64_t B, int64_t C, int64_t K, int64_t Hg, int64_t Wg, const float* xa,
+                     const float* ta, const int64_t* ba, int64_t M, int64_t n_fp, double offset, int64_t tile,
+                     int64_t basis, const float* counts, const float* centres, int64_t n_check, double tau,
+                     int64_t H, int64_t W, float* out, hipStream_t stream) {
+  if (M < 0 || B < 0 || K < 1 || K > kTrajMaxK || !dims_ok(Hg, Wg) || basis < 0 || basis > 2 || n_fp < 0 ||
+      n_check < 1 || tile < 1 || H < 1 || W < 1) {
+    set_error("traj_visible: bad sizes (1 <= K <= %d, basis 0, 1 or 2)", kTrajMaxK);
+    return 1;
+  }
+  if (C != 2 * K) { set_error("traj_visible: the coefficient grid has %lld channels, expected 2K = %lld", (long long)C, (long long)(2 * K)); return 1; }
+  if (M == 0) return 0;
+  if (!field_cl || !xa || !ta || !ba || !counts || !centres || !out) { set_error("traj_visible: null argument"); return 1; }
+  if (reinterpret_cast<uintptr_t>(field_cl) & 15) { set_error("traj_visible: field_cl must be 16-byte aligned"); return 1; }
+  const int64_t Q = (2 * K + 3) / 4, waves = (M + kWave / Q - 1) / (kWave / Q);
+  const dim3 grid(grid_for(waves * kWave)), block(kBlock);
+  const float4* f = (const float4*)field_cl;
+  const float2* p = (const float2*)xa;
+  const int bs = (int)basis;
+  switch (K) {
+#define ATL_TRAJ_CASE(k) \
+    case k: hipLaunchKernelGGL(k_traj_visible<k>, grid, block, 0, stream, f, B, (int)Hg, (int)Wg, p, ta, ba, bs, M, \
+                               (int)n_fp, (float)offset, (float)tile, counts, centres, (int)n_check, (float)tau, \
+                               (float)(W - 1), (float)(H - 1), out); break;
+    ATL_TRAJ_CASE(1) ATL_TRAJ_CASE(2) ATL_TRAJ_CASE(3) ATL_TRAJ_CASE(4) ATL_TRAJ_CASE(5) ATL_TRAJ_CASE(6)
+    ATL_TRAJ_CASE(7) ATL_TRAJ_CASE(8) ATL_TRAJ_CASE(9) ATL_TRAJ_CASE(10) ATL_TRAJ_CASE(11) ATL_TRAJ_CASE(12)
+    ATL_TRAJ_CASE(13) ATL_TRAJ_CASE(14) ATL_TRAJ_CASE(15) ATL_TRAJ_CASE(16)
+#undef ATL_TRAJ_CASE
+  }
+  return check_launch("traj_visible");
 }
 
 int atl_traj_gout(const float* gd, const float* t, int64_t N, int64_t K, int64_t basis, float* gout,

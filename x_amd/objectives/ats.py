@@ -27,7 +27,7 @@ import torch
 
 from ..core.events import EventPacket
 from ..ops import (anchored_log_scores, anchored_score_mean, ats_pair_sums, ats_pair_sums_flow, ats_pair_sums_traj,
-                   event_noise, visible_fraction_linear, window_counts)
+                   event_noise, traj_visible_fraction, visible_fraction_linear, window_counts)
 from .base import Objective
 
 
@@ -53,6 +53,13 @@ def visible_fraction(motion, xa, ta, ba, ev: EventPacket, tau: float, n_check: i
         va = motion.velocity(xa, ta, ba)
         return visible_fraction_linear(xa, va, ta, ba, ev.t, ev.b, ev.batch_size, ev.height, ev.width, tau, n_check,
                                        assume_sorted=bool(ev.meta.get("sorted")))
+    from ..motion import PixelTrajectories
+    from ..ops.functional import TRAJ_MAX_K
+    if (xa.is_cuda and type(motion) is PixelTrajectories and motion.K <= TRAJ_MAX_K and motion.assign == "invert"
+            and motion.tile_c.is_cuda):             # start, one coefficient look-up, every centre: one pass
+        return traj_visible_fraction(motion.tile_c, motion.K, motion.basis_kind, motion.n_fp, motion.offset,
+                                     motion.tile, xa, ta, ba, ev.t, ev.b, ev.batch_size, ev.height, ev.width, tau,
+                                     n_check, assume_sorted=bool(ev.meta.get("sorted")))
     edges = torch.linspace(0, 1, n_check + 1, device=ev.device)
     centres = (0.5 * (edges[:-1] + edges[1:])).tolist()           # one host transfer
     counts = _bin_counts_cpu(ev, n_check) if not xa.is_cuda else None

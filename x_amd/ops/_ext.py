@@ -41,6 +41,7 @@ _SIGS = {
     "atl_sample_grid_bwd_pos": [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_field_channels_last": [_P, _I, _I, _I, _I, _P, _P],
     "atl_traj_displacement": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P, _P],
+    "atl_traj_visible": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _D, _I, _I, _P, _P, _I, _D, _I, _I, _P, _P],
     "atl_traj_gout": [_P, _P, _I, _I, _I, _P, _P],
     "atl_sample_grid_fwd_cl": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_sample_grid_bwd_pos_cl": [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],

@@ -932,6 +932,29 @@ def visible_fraction_linear(xa, va, ta, ba, t_all, b_all, B, H, W, tau, n_check=
     return out
 
 
+def traj_visible_fraction(fld, K: int, basis: str, n_fp: int, offset: float, tile: int, xa, ta, ba, t_all, b_all, B,
+                          H, W, tau, n_check=16, assume_sorted: bool = False):
+    """Exposure correction for PixelTrajectories (atl/objectives/ats.py:31-50) in one pass: each anchor's
+    trajectory start (n_fp Picard steps), its coefficients from ``fld`` (B, 2K, Hg, Wg; the model's tile-centre
+    grid) looked up once, the trajectory at the n_check bin centres; bit-identical to origin, then displacement per
+    centre.  No grad."""
+    dev = xa.device
+    fld = _f32(fld.detach())
+    B_, C, Hg, Wg = fld.shape
+    if C != 2 * int(K) or K > TRAJ_MAX_K or basis not in TRAJ_BASES:
+        raise ValueError(f"traj_visible_fraction: coefficient grid of {C} channels, K = {K}, basis {basis!r}")
+    xa, ta, ba = _f32(xa.detach()), _f32(ta), ba.contiguous().long()
+    counts = bin_counts(t_all, b_all, B, n_check, assume_sorted)
+    edges = torch.linspace(0, 1, n_check + 1, device=dev)
+    centres = (0.5 * (edges[:-1] + edges[1:])).contiguous()
+    out = torch.empty(ta.shape[0], dtype=F32, device=dev)
+    with torch.cuda.device(dev):
+        call("atl_traj_visible", ptr(_channels_last(fld)), B_, C, int(K), Hg, Wg, ptr(xa), ptr(ta), ptr(ba),
+             ta.shape[0], int(n_fp), float(offset), int(tile), TRAJ_BASES[basis], ptr(counts), ptr(centres), n_check,
+             float(tau), int(H), int(W), ptr(out), stream_of(xa))
+    return out
+
+
 class _AnchoredEpilogue(torch.autograd.Function):
     """log(eps + S / (Wn 2 pi h^2)) with Wn = max(count, 1) * vis (atl/objectives/ats.py:92-96)."""
 
