@@ -161,6 +161,16 @@ int atl_traj_visible(const float* field_cl, int64_t B, int64_t C, int64_t K, int
                      const float* ta, const int64_t* ba, int64_t M, int64_t n_fp, double offset, int64_t tile,
                      int64_t basis, const float* counts, const float* centres, int64_t n_check, double tau,
                      int64_t H, int64_t W, float* out, hipStream_t stream);
+/* The backward of atl_traj_displacement for the B-spline basis (basis 2) without the (N, 2K) gradient rows of
+ * atl_traj_gout: each kernel forms an event's row from the displacement's gradient gd (N,2) and its time t.
+ * atl_traj_field_bwd_planned accumulates the coefficient grid's gradient (B, 2K, Hg, Wg; accumulated: zero it
+ * first) on the positions' tile plan (atl_grid_plan with img 0, 0), K >= 3; atl_traj_pos_bwd_cl writes the positions'
+ * gradient gpos (N,2) as atl_sample_grid_bwd_pos_cl does (the same bits).  No counterpart in the reference (the
+ * adjoint of its per-channel lookup under autograd). */
+int atl_traj_field_bwd_planned(const float* gd, const float* t, int64_t K, int64_t B, int64_t Hg, int64_t Wg,
+                               int64_t N, void* ws, float* gfield, hipStream_t stream);
+int atl_traj_pos_bwd_cl(const float* gd, const float* t, int64_t K, const float* field_cl, int64_t B, int64_t Hg,
+                        int64_t Wg, const float* gpos_in, const int64_t* b, int64_t N, float* gpos, hipStream_t stream);
 int atl_traj_gout(const float* gd, const float* t, int64_t N, int64_t K, int64_t basis, float* gout,
                   hipStream_t stream);
 /* The same adjoint through a tile plan: atl_grid_plan bins the positions by the 16x16 tile of their base

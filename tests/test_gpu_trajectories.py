@@ -116,6 +116,40 @@ def test_traj_displacement_matches_fp64_and_torch_gradients(K, kind):
     assert not N(tp.grad)[~ok].any()
 
 
+@pytest.mark.parametrize("K", [3, 10, 16])
+def test_traj_bspline_backward_forms_rows_in_kernel(K):
+    """The B-spline backward that forms each event's gradient row from gd and t inside the kernels equals the one
+    that writes the rows first (atl_traj_gout): position gradient bit for bit, field gradient to the order of
+    the flush atomics."""
+    print(f"traj bspline backward K={K}", flush=True)
+    from x_amd.ops import functional as F
+    rng = np.random.default_rng(K)
+    n, B, Hg, Wg = 6000, 2, 21, 34
+    C = 2 * K
+    fld = T((rng.standard_normal((B, C, Hg, Wg)) * 2).astype(F32))
+    gpos = T(np.stack([rng.uniform(-2, Wg + 1, n), rng.uniform(-2, Hg + 1, n)], 1).astype(F32))
+    b = T(rng.integers(0, B, n).astype(np.int64))
+    t = T(rng.uniform(-0.1, 1.1, n).astype(F32))                 # the end spans continue outside [0, 1]
+    gd = T(rng.standard_normal((n, 2)).astype(F32))
+    fcl = F._channels_last(fld)
+    nbytes = int(F.load_library().atl_grid_plan_bytes(B, Hg, Wg, n))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=DEV)
+    st = F.stream_of(gpos)
+    F.call("atl_grid_plan", B, Hg, Wg, F.ptr(gpos), F.ptr(b), n, 0, 0, F.ptr(ws), nbytes, st)
+    rows = torch.empty(n, C, device=DEV)
+    F.call("atl_traj_gout", F.ptr(gd), F.ptr(t), n, K, 2, F.ptr(rows), st)
+    gf_old, gf_new = torch.zeros_like(fld), torch.zeros_like(fld)
+    F.call("atl_sample_grid_bwd_planned", F.ptr(rows), B, C, Hg, Wg, F.ptr(gpos), n, 0, 0, F.ptr(ws), F.ptr(gf_old), st)
+    F.call("atl_traj_field_bwd_planned", F.ptr(gd), F.ptr(t), K, B, Hg, Wg, n, F.ptr(ws), F.ptr(gf_new), st)
+    gp_old, gp_new = torch.empty_like(gpos), torch.empty_like(gpos)
+    F.call("atl_sample_grid_bwd_pos_cl", F.ptr(rows), F.ptr(fcl), B, C, Hg, Wg, F.ptr(gpos), F.ptr(b), n, 0, 0,
+           F.ptr(gp_old), st)
+    F.call("atl_traj_pos_bwd_cl", F.ptr(gd), F.ptr(t), K, F.ptr(fcl), B, Hg, Wg, F.ptr(gpos), F.ptr(b), n,
+           F.ptr(gp_new), st)
+    assert torch.equal(gp_new, gp_old)
+    close_rel(N(gf_new), N(gf_old), 1e-6)
+
+
 def test_traj_displacement_empty_and_rejected_inputs():
     """No events: an empty (0, 2) result and zero gradients; a basis the kernel does not know and times that
     carry a gradient are refused on the host."""

@@ -8,6 +8,7 @@
 #include "common.h"
 #include "scan.h"
 #include "bilinear.h"
+#include "traj.h"
 #include "../../include/atl_hip.h"
 
 #include <cmath>
@@ -414,13 +415,17 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_fwd_cl(const float4* __r
 // Position gradient: one lane per (event, channel quad) as in the forward, so the field and gout reads of an
 // event are consecutive 16-byte pieces; each lane forms its four channel terms and the event's first lane adds
 // all of them in channel order, as the plane kernel does (same bits).
+// With gd set (the trajectory model, B-spline basis, C = 2K): the gradient rows are formed from the displacement's
+// gradient gd and the event time tt (k_traj_gout's values) instead of read.
 __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos_cl(const float* __restrict__ gout,
                                                                    const float4* __restrict__ fcl, int64_t B, int C,
                                                                    int Q, int Hg, int Wg,
                                                                    const float2* __restrict__ pos,
                                                                    const int64_t* __restrict__ bidx, int64_t N,
                                                                    float sxw, float syh, int scale,
-                                                                   float2* __restrict__ gpos) {
+                                                                   float2* __restrict__ gpos,
+                                                                   const float2* __restrict__ gd,
+                                                                   const float* __restrict__ tt) {
   const int lane = threadIdx.x & (kWave - 1);
   const int epw = kWave / Q;                     // events per wave
   const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
@@ -451,15 +456,23 @@ __global__ void __launch_bounds__(kBlock) k_sample_grid_bwd_pos_cl(const float* 
                    k1 = f[(int64_t)c.o11 * Q];
       const float f00[4] = {a.x, a.y, a.z, a.w}, f01[4] = {h0.x, h0.y, h0.z, h0.w},
                   f10[4] = {h1.x, h1.y, h1.z, h1.w}, f11[4] = {k1.x, k1.y, k1.z, k1.w};
-      const float* go_row = gout + n * C;
       float go[4];
-      if ((C & 3) == 0) {
+      if (gd) {
+        float nb[4];
+        const int K = C / 2;
+        const int j = bspline_nonzero_rt(tt[n], K, nb);
+        const float2 d = gd[n];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) go[jj] = 4 * q + jj < C ? bspline_row(4 * q + jj, K, j, nb, d) : 0.f;
+      } else if ((C & 3) == 0) {
+        const float* go_row = gout + n * C;
         const float4 g4 = *(const float4*)(go_row + 4 * q);
         go[0] = g4.x;
         go[1] = g4.y;
         go[2] = g4.z;
         go[3] = g4.w;
       } else {
+        const float* go_row = gout + n * C;
 #pragma unroll
         for (int j = 0; j < 4; ++j) go[j] = 4 * q + j < C ? go_row[4 * q + j] : 0.f;
       }
@@ -971,8 +984,22 @@ int atl_sample_grid_bwd_pos_cl(const float* gout, const float* field_cl, int64_t
   const int64_t waves = (N + kWave / Q - 1) / (kWave / Q);
   hipLaunchKernelGGL(k_sample_grid_bwd_pos_cl, dim3(grid_for(waves * kWave)), dim3(kBlock), 0, stream, gout,
                      (const float4*)field_cl, B, (int)C, (int)Q, (int)Hg, (int)Wg, (const float2*)pos, b, N, sxw, syh,
-                     scale, (float2*)gpos);
+                     scale, (float2*)gpos, (const float2*)nullptr, (const float*)nullptr);
   return check_launch("sample_grid_bwd_pos_cl");
+}
+
+int atl_traj_pos_bwd_cl(const float* gd, const float* t, int64_t K, const float* field_cl, int64_t B, int64_t Hg,
+                        int64_t Wg, const float* gpos_in, const int64_t* b, int64_t N, float* gpos, hipStream_t stream) {
+  if (N < 0 || B < 0 || K < 1 || K > kTrajMaxK || !dims_ok(Hg, Wg)) { set_error("traj_pos_bwd_cl: bad sizes (1 <= K <= %d)", kTrajMaxK); return 1; }
+  if (N == 0) return 0;
+  if (!gd || !t || !field_cl || !gpos_in || !b || !gpos) { set_error("traj_pos_bwd_cl: null argument"); return 1; }
+  if (reinterpret_cast<uintptr_t>(field_cl) & 15) { set_error("traj_pos_bwd_cl: field_cl must be 16-byte aligned"); return 1; }
+  const int64_t C = 2 * K, Q = (C + 3) / 4;
+  const int64_t waves = (N + kWave / Q - 1) / (kWave / Q);
+  hipLaunchKernelGGL(k_sample_grid_bwd_pos_cl, dim3(grid_for(waves * kWave)), dim3(kBlock), 0, stream,
+                     (const float*)nullptr, (const float4*)field_cl, B, (int)C, (int)Q, (int)Hg, (int)Wg,
+                     (const float2*)gpos_in, b, N, 1.f, 1.f, 0, (float2*)gpos, (const float2*)gd, t);
+  return check_launch("traj_pos_bwd_cl");
 }
 
 int atl_traj_displacement(const float* field_cl, int64_t B, int64_t C, int64_t K, int64_t Hg, int64_t Wg,

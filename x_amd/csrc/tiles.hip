@@ -19,6 +19,7 @@
 #include "common.h"
 #include "scan.h"
 #include "bilinear.h"
+#include "traj.h"
 #include "../../include/atl_hip.h"
 
 #include <cmath>
@@ -555,11 +556,15 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum_bins(const int4* __res
 // corner products value * (wx * wy) of its node's records into registers, the sums go through an LDS table, and
 // every window node adds the sums of the base nodes that reach it into its own LDS window entry.  The window is flushed once per chunk with one global atomic per
 // non-zero node and channel.  The products are the scatter form's; only the order of the additions differs.
+// With gd set (the trajectory model, B-spline basis): the gradient rows are not read but formed per record from
+// the displacement's gradient gd and the event time tt, K = C / 2 (k_traj_gout's values: bspline_row).
 __global__ void __launch_bounds__(kAccBlock) k_tile_accum_rows(const int4* __restrict__ info,
                                                                const int* __restrict__ nchunk,
                                                                const float4* __restrict__ rec,
                                                                const float* __restrict__ gout, TileGeo g,
-                                                               float* __restrict__ out) {
+                                                               float* __restrict__ out,
+                                                               const float2* __restrict__ gd,
+                                                               const float* __restrict__ tt) {
   constexpr int T = kBinT, L = T + 1;
   extern __shared__ float acc[];                  // nc * L * L window
   __shared__ int bcnt[kBins], bstart[kBins];
@@ -618,6 +623,22 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum_rows(const int4* __res
       sax[pos[u]] = ax[u];
       say[pos[u]] = ay[u];
     }
+    const int K = nc / 2;
+    float2 dd[kAccItems];                          // gd set: each record's displacement gradient, span, basis
+    int jb[kAccItems];
+    float nb[kAccItems][4];
+    if (gd) {
+#pragma unroll
+      for (int u = 0; u < kAccItems; ++u) {
+        dd[u] = make_float2(0.f, 0.f);
+        jb[u] = 0;
+        nb[u][0] = nb[u][1] = nb[u][2] = nb[u][3] = 0.f;
+        if (pos[u] < 0) continue;
+        const int e = __float_as_int(q[u].w);
+        dd[u] = gd[e];
+        jb[u] = bspline_nonzero_rt(tt[e], K, nb[u]);
+      }
+    }
     for (int cg = 0; cg < nc; cg += 4) {
       // every thread loads the group's channels of its own records (the loads in flight together) into srow
       float4 v4[kAccItems];
@@ -625,6 +646,13 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum_rows(const int4* __res
       for (int u = 0; u < kAccItems; ++u) {
         v4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (pos[u] < 0) continue;
+        if (gd) {
+          v4[u].x = bspline_row(cg, K, jb[u], nb[u], dd[u]);
+          if (cg + 1 < nc) v4[u].y = bspline_row(cg + 1, K, jb[u], nb[u], dd[u]);
+          if (cg + 2 < nc) v4[u].z = bspline_row(cg + 2, K, jb[u], nb[u], dd[u]);
+          if (cg + 3 < nc) v4[u].w = bspline_row(cg + 3, K, jb[u], nb[u], dd[u]);
+          continue;
+        }
         const float* row = gout + (int64_t)__float_as_int(q[u].w) * nc + cg;
         if (g.vec4) {                               // nc % 4 == 0, 16-byte aligned rows
           v4[u] = *(const float4*)row;
@@ -1288,13 +1316,38 @@ int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t
                            kAccChunk, kBinChunk, info, nchunk);
         hipLaunchKernelGGL(k_tile_accum_rows, dim3((unsigned)max_chunks(g)), dim3(kAccBlock),
                            (size_t)C * (kBinT + 1) * (kBinT + 1) * sizeof(float), stream, (const int4*)info,
-                           (const int*)nchunk, (const float4*)(w + L.rec), gout, g, gfield);
+                           (const int*)nchunk, (const float4*)(w + L.rec), gout, g, gfield, (const float2*)nullptr,
+                           (const float*)nullptr);
       } else {
         tile_accum<kGrid, 0>(g, L, ws, gout, gfield, stream);
       }
       break;
   }
   return check_launch("sample_grid_bwd_planned");
+}
+
+int atl_traj_field_bwd_planned(const float* gd, const float* t, int64_t K, int64_t B, int64_t Hg, int64_t Wg,
+                               int64_t N, void* ws, float* gfield, hipStream_t stream) {
+  TileGeo g;
+  if (K < 3 || 2 * K > kMaxChannels || !tile_geo(kGrid, B, Hg, Wg, N, 0, 0, g) || g.T != kBinT) {
+    set_error("traj_field_bwd_planned: bad sizes (3 <= K <= %d on grids of at most 16384 16x16 tiles)", kMaxChannels / 2);
+    return 1;
+  }
+  g.C = (int)(2 * K);
+  g.vec4 = false;
+  if (!ws || !gfield || (N > 0 && (!gd || !t))) { set_error("traj_field_bwd_planned: null argument"); return 1; }
+  if (N == 0 || g.nblk == 0) return 0;
+  const TileLayout L = tile_layout(g);
+  char* w = (char*)ws;
+  int4* info = (int4*)(w + L.info);
+  int* nchunk = (int*)(w + L.nchunk);
+  hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.boff), g, kAccChunk,
+                     kBinChunk, info, nchunk);
+  hipLaunchKernelGGL(k_tile_accum_rows, dim3((unsigned)max_chunks(g)), dim3(kAccBlock),
+                     (size_t)g.C * (kBinT + 1) * (kBinT + 1) * sizeof(float), stream, (const int4*)info,
+                     (const int*)nchunk, (const float4*)(w + L.rec), (const float*)nullptr, g, gfield,
+                     (const float2*)gd, t);
+  return check_launch("traj_field_bwd_planned");
 }
 
 // Warp -> splat -> gather (the fused pipeline above).  Workspace bytes, or -1 for unsupported sizes.

@@ -343,6 +343,17 @@ class _TrajDisplacement(torch.autograd.Function):
         gf = gp = None
         with torch.cuda.device(gpos.device):
             st = stream_of(gpos)
+            if ctx.basis == TRAJ_BASES["bspline"] and ctx.K >= 3 and ctx.plan is not None:
+                # the gradient rows are formed from gd and t inside both kernels (no (N, 2K) rows in memory)
+                if ctx.needs_input_grad[0]:
+                    gf = torch.zeros(B, C, Hg, Wg, device=gpos.device, dtype=F32)
+                    call("atl_traj_field_bwd_planned", ptr(gd), ptr(t), ctx.K, B, Hg, Wg, N, ptr(ctx.plan), ptr(gf),
+                         st)
+                if ctx.needs_input_grad[1]:
+                    gp = torch.empty_like(gpos)
+                    call("atl_traj_pos_bwd_cl", ptr(gd), ptr(t), ctx.K, ptr(fcl), B, Hg, Wg, ptr(gpos), ptr(b), N,
+                         ptr(gp), st)
+                return gf, gp, None, None, None, None, None
             g = torch.empty(N, C, device=gpos.device, dtype=F32)
             call("atl_traj_gout", ptr(gd), ptr(t), N, ctx.K, ctx.basis, ptr(g), st)
             if ctx.needs_input_grad[0]:
