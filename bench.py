@@ -715,9 +715,12 @@ def main():
     obj = AnchoredExact(h=a.sigma, tau=0.2, cut=3.0, n_slices=16, n_anchors=None, seed=0, rng="device")
     blobs = a.workload == "anchored-blobs"
     reflayout = a.workload == "anchored-reflayout"
-    if reflayout:                                  # route the objective's pair sums through the reference layout
-        import x_amd.objectives.ats as ats_mod
-        ats_mod.ats_pair_sums = F.ats_pair_sums_reference_layout
+    if reflayout:                                  # the reference's call: v from the flow, then plan + pair sums
+        def ref_pair_sums(ev_, motion_, xs, xa, anchors):
+            v = motion_.velocity(xs, ev_.t, ev_.b)
+            return F.ats_pair_sums_reference_layout(xs, ev_.t, v, ev_.b, ev_.batch_size, ev_.height, ev_.width,
+                                                    anchors, obj.h, obj.tau, obj.cut, obj.n_slices, anchor_xy=xa)
+        obj._pair_sums = ref_pair_sums
     if blobs:
         from x_amd.objectives import iwe_variance
 
@@ -737,7 +740,7 @@ def main():
     torch.cuda.synchronize()
     # the pair kernels first (the roofline's candidates); the objective's dense flow takes the flow path, whose
     # backward is the pair backward (atl_fast_pair_bwd_src) and then the flow-grid adjoint
-    kernels = (["atl_ats_pair_fwd", "atl_ats_pair_bwd"] if reflayout else
+    kernels = (["atl_ats_pair_fwd_ws", "atl_ats_pair_bwd_ws"] if reflayout else
                ["atl_fast_pair_fwd", "atl_fast_pair_bwd_src", "atl_fast_flow_adjoint"]) + (
         ["atl_splat_bilinear_fwd_ws", "atl_splat_bilinear_bwd"] if blobs else [])
     rec = _ext.time_kernels(kernels, every=4)      # every bracket delays the next launch: sample the steps

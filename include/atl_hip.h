@@ -235,18 +235,40 @@ int atl_plan_anchors(const float* x, const float* t, const int64_t* b, const int
 
 /* ats_pair_fwd (csrc/atl_ops.h:31-42, csrc/atl_cpu.cpp:203-222): out (M) written.  E = number of plan
  * entries, ncell = B*S*GH*GW (cell_start has ncell+1 entries).  count (M) int32 receives n_i, the number of
- * visited pairs of each anchor, when non-null (not output by the reference). */
+ * visited pairs of each anchor, when non-null (not output by the reference).  Sixteen lanes per anchor read
+ * the anchor's three CSR row ranges coalesced, in the plan's anchor order.  E, M, N < 2^29, ncell < 2^31. */
 int atl_ats_pair_fwd(const float* src_y, const float* src_v, const float* src_t, const int64_t* src_id,
                      const int64_t* cell_start, int64_t E, int64_t ncell, const float* anc_x, const float* anc_t,
                      const int64_t* anc_cell, const int64_t* anc_id, int64_t M, const float* slice_c, int64_t S,
                      int64_t GH, int64_t GW, double h, double tau, double cut, float* out, int* count,
                      hipStream_t stream);
-/* ats_pair_bwd (csrc/atl_ops.h:43-47, csrc/atl_cpu.cpp:224-253): gv (N,2) accumulated. */
+/* ats_pair_bwd (csrc/atl_ops.h:43-47, csrc/atl_cpu.cpp:224-253): gv (N,2) accumulated, with the reference's
+ * two global atomics per pair (csrc/atl_cuda.cu:169-180); for a caller that cannot pass a workspace.
+ * E, M, N < 2^29. */
 int atl_ats_pair_bwd(const float* gS, const float* src_y, const float* src_v, const float* src_t,
                      const int64_t* src_id, const int64_t* cell_start, int64_t E, int64_t ncell, const float* anc_x,
                      const float* anc_t, const int64_t* anc_cell, const int64_t* anc_id, int64_t M,
                      const float* slice_c, int64_t S, int64_t GH, int64_t GW, double h, double tau, double cut,
                      int64_t N, float* gv, hipStream_t stream);
+/* Workspace entries of the same two ops (csrc/atl_ops.h:31-47), for a binding that allocates a workspace
+ * with its outputs: ws is atl_ats_pair_ws_bytes(E, ncell, M, GW) bytes of device memory, 256-byte aligned,
+ * contents on entry ignored, and serves either call.  Both bin the anchors by cell first.
+ * atl_ats_pair_fwd_ws: the same out and count as atl_ats_pair_fwd, the anchors walked in cell order (the
+ * anchors of a wave share their records).  atl_ats_pair_bwd_ws, source-centric: each chunk of 64 plan entries
+ * of a run of four cells of a row gathers over the binned anchors (gS != 0) around it and adds every entry's
+ * sum to gv once (two atomics per entry instead of two per pair); the same visited pairs and terms as
+ * atl_ats_pair_bwd, gv (N,2) accumulated. */
+int64_t atl_ats_pair_ws_bytes(int64_t E, int64_t ncell, int64_t M, int64_t GW);
+int atl_ats_pair_fwd_ws(const float* src_y, const float* src_v, const float* src_t, const int64_t* src_id,
+                        const int64_t* cell_start, int64_t E, int64_t ncell, const float* anc_x, const float* anc_t,
+                        const int64_t* anc_cell, const int64_t* anc_id, int64_t M, const float* slice_c, int64_t S,
+                        int64_t GH, int64_t GW, double h, double tau, double cut, float* out, int* count, void* ws,
+                        int64_t ws_bytes, hipStream_t stream);
+int atl_ats_pair_bwd_ws(const float* gS, const float* src_y, const float* src_v, const float* src_t,
+                        const int64_t* src_id, const int64_t* cell_start, int64_t E, int64_t ncell,
+                        const float* anc_x, const float* anc_t, const int64_t* anc_cell, const int64_t* anc_id,
+                        int64_t M, const float* slice_c, int64_t S, int64_t GH, int64_t GW, double h, double tau,
+                        double cut, int64_t N, float* gv, void* ws, int64_t ws_bytes, hipStream_t stream);
 
 /* ---------------------------------------------------------------- fused pair sums (no host synchronisation)
  *

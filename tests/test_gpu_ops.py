@@ -416,6 +416,44 @@ def test_pair_sums_match_oracle(tau, S, h):
     close_rel(N(tv.grad), O.ats_pair_bwd(gS, p, h, tau, 3.0, win.n), 1e-4)
 
 
+@pytest.mark.parametrize("scene,n,tau,S,h,zero_frac", [("segments", 6000, 0.2, 16, 1.0, 0.0),
+                                                       ("segments", 6000, 1.0, 8, 1.5, 0.7),
+                                                       ("segments", 6000, 0.05, 4, 0.5, 0.3),
+                                                       ("blobs", 40000, 0.2, 16, 1.0, 0.5)])
+def test_pair_entries_match_oracle(scene, n, tau, S, h, zero_frac):
+    """Both forward entry points over the reference-layout plan (binned anchors over a workspace; the plan's
+    anchor order) and both backward ones (source-centric over a workspace; per-pair atomics) against the oracle:
+    counts bit-exact, S within 1e-5, gv within 1e-4, with a share of the anchors' gS exactly zero (skipped by
+    both backwards).
+    The anchors sit h * N(0, 1) off the events, so records two cells from an anchor pass the distance test and
+    only the neighbourhood test keeps them out; the blob case fills cells with hundreds of records and
+    anchors (several 64-wide chunks on both sides)."""
+    win = synth.small_window(seed=4, n=n, H=40, W=48, B=1, scene=scene)
+    v, _, _ = O.dense_velocity(win.motion["grid"], win.xy, win.b, 40, 48)
+    rng = np.random.default_rng(104)
+    xs = (win.xy + rng.uniform(-0.5, 0.5, win.xy.shape)).astype(F32)
+    anchors = np.arange(win.n)
+    xa = (xs + h * rng.standard_normal(xs.shape)).astype(F32)
+    p = O.build_pair_plan(xs, win.t, v, win.b, 1, 40, 48, anchors, h, tau, 3.0, S, anchor_xy=xa)
+    q = F.build_pair_plan(T(xs), T(win.t), T(v), T(win.b), 1, 40, 48, T(anchors), h, tau, 3.0, S, anchor_xy=T(xa))
+    gS = rng.standard_normal(len(anchors)).astype(F32)
+    gS[rng.random(len(anchors)) < zero_frac] = 0
+    want = O.ats_pair_bwd(gS, p, h, tau, 3.0, win.n)
+    e = F.get_ext()
+    args = (q.src_y, q.src_v, q.src_t, q.src_id, q.cell_start, q.anc_x, q.anc_t, q.anc_cell, q.anc_id, q.slice_c,
+            q.S, q.GH, q.GW, h, tau, 3.0, win.n)
+    if scene == "blobs":
+        assert np.diff(N(q.cell_start)).max() > 200
+    want_s, want_n = O.ats_pair_fwd(p, h, tau, 3.0, with_counts=True)
+    for plan_order in (False, True):
+        cnt = torch.full((len(anchors),), -7, dtype=torch.int32, device=DEV)
+        got = N(e.ats_pair_fwd(*args[:-1], count=cnt, plan_order=plan_order))
+        assert np.array_equal(N(cnt), want_n)
+        close_rel(got, want_s, 1e-5)
+    for atomics in (False, True):
+        close_rel(N(e.ats_pair_bwd(T(gS), *args, per_pair_atomics=atomics)), want, 1e-4)
+
+
 def test_ats_pair_sums_api_matches_bruteforce():
     """Reference test_ats_pair_matches_bruteforce (tests/test_ops.py:62-77) on the device: plan + kernel vs the
     O(MN) brute force, values and gradients."""

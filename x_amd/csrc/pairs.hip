@@ -239,6 +239,8 @@ __global__ void k_fill_i32(int* __restrict__ p, int64_t n, int v) {
 }
 
 // ------------------------------------------------------------------------------------------ pair walk
+constexpr int64_t kMaxRecords = (int64_t)1 << 29;   // records, anchors, events: int indices, 32-bit offsets
+
 struct PairRef {
   const float2 *SY, *SV, *AX;
   const float *ST, *AT, *SC;
@@ -249,65 +251,386 @@ struct PairRef {
 
 __device__ __forceinline__ float gauss(float d2, float kexp) { return __builtin_amdgcn_exp2f(d2 * kexp); }
 
-// Visits the contributing pairs of anchor i over its 3x3 cell neighbourhood; the three cells of a row are
-// consecutive keys, so each row is one contiguous CSR range (csrc/atl_cpu.cpp:176-200).
-template <typename Visit>
-__device__ __forceinline__ void walk_ref(int64_t i, const PairRef& a, Visit&& visit) {
-  const int64_t g = a.AC[3 * i], cx = a.AC[3 * i + 1], cy = a.AC[3 * i + 2], id = a.AID[i];
-  if (g < 0 || g >= a.G || cx < 0 || cx >= a.GW || cy < 0 || cy >= a.GH) return;
-  const float2 xi = a.AX[i];
-  const float ti = a.AT[i];
-  const float cs = a.SC[g % a.S];
-  const float at = ti - cs;
-  const int64_t ylo = cy > 0 ? cy - 1 : 0, yhi = cy + 1 < a.GH ? cy + 1 : a.GH - 1;
-  const int64_t xlo = cx > 0 ? cx - 1 : 0, xhi = cx + 1 < a.GW ? cx + 1 : a.GW - 1;
-  for (int64_t yy = ylo; yy <= yhi; ++yy) {
-    const int64_t row = (g * a.GH + yy) * a.GW;
-    int64_t k = a.CS[row + xlo];
-    int64_t k1 = a.CS[row + xhi + 1];
-    k = k < 0 ? 0 : k;
-    k1 = k1 > a.E ? a.E : k1;
-    for (; k < k1; ++k) {
-      if (a.SID[k] == id) continue;
-      const float dt = ti - a.ST[k];
-      if (fabsf(dt) > a.tau) continue;
-      const float2 sy = a.SY[k], sv = a.SV[k];
-      const float rx = xi.x - (sy.x + sv.x * at);
-      const float ry = xi.y - (sy.y + sv.y * at);
-      const float d2 = rx * rx + ry * ry;
-      if (d2 > a.r2max) continue;
-      visit(k, rx, ry, dt, gauss(d2, a.kexp));
+// The pair tests of csrc/atl_cpu.cpp:186-195 in their fp32 order: not the anchor's own event, |dt| <= tau,
+// |r|^2 <= (cut h)^2, with rx, ry = x_i - (y_k + v_k at).  A NaN passes a test exactly where it does there.
+__device__ __forceinline__ bool pair_hit(int sid, int id, float dt, float d2, const PairRef& a) {
+  return sid != id && !(fabsf(dt) > a.tau) && !(d2 > a.r2max);
+}
+
+// Three CSR row ranges over one plane g: rows ylo..yhi (at most three), columns xlo..xhi of each row as one
+// contiguous range (the cells of a row are consecutive keys), clamped to [0, cap).  k0[r] is the first record
+// of row r; c1, c2, c3 the running lengths, so position p < c3 of the concatenated list is record
+// list_pos(p).  Rows past yhi are empty.  Record and anchor counts are below 2^29 (host-checked), so int.
+struct Rows3 {
+  int k0[3];
+  int c1, c2, c3;
+};
+
+__device__ __forceinline__ Rows3 row_ranges(const int64_t* __restrict__ start, int64_t cap, int64_t g, int64_t ylo,
+                                            int64_t yhi, int64_t xlo, int64_t xhi, int64_t GH, int64_t GW) {
+  Rows3 r;
+  int run = 0;
+  int c[3];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    int64_t lo = 0, hi = 0;
+    if (ylo + q <= yhi) {
+      const int64_t row = (g * GH + ylo + q) * GW;
+      lo = start[row + xlo];
+      hi = start[row + xhi + 1];
+      lo = lo < 0 ? 0 : lo;
+      hi = hi > cap ? cap : hi;
+      hi = hi < lo ? lo : hi;
     }
+    r.k0[q] = (int)lo;
+    run += (int)(hi - lo);
+    c[q] = run;
+  }
+  r.c1 = c[0];
+  r.c2 = c[1];
+  r.c3 = c[2];
+  return r;
+}
+
+__device__ __forceinline__ int list_pos(int p, const Rows3& r) {
+  const int base = p >= r.c2 ? r.k0[2] - r.c2 : (p >= r.c1 ? r.k0[1] - r.c1 : r.k0[0]);
+  return base + p;
+}
+
+// Load with a 32-bit byte offset from a uniform base (the saddr + voffset addressing form; i * sizeof(T) is
+// below 2^32 for records < 2^29).
+template <typename T>
+__device__ __forceinline__ T ldr(const T* base, uint32_t i) {
+  return *(const T*)((const char*)base + i * (uint32_t)sizeof(T));
+}
+
+// An anchor as the walk sees it.  id is the low word of the anchor's event id (ids are below 2^31, and -1, an
+// anchor without an event, matches no source); g < 0 for an anchor outside the grid, which visits nothing.
+struct AnchorView {
+  float x, y, t, at;          // position, time, t - slice centre
+  int id, g, cx, cy;
+};
+
+__device__ __forceinline__ AnchorView no_anchor() {
+  AnchorView v;
+  v.x = v.y = v.t = v.at = 0.f;
+  v.id = -1;
+  v.g = -1;
+  v.cx = v.cy = 0;
+  return v;
+}
+
+__device__ __forceinline__ AnchorView anchor_from_plan(int64_t i, bool on, const PairRef& a) {
+  AnchorView v = no_anchor();
+  if (on) {
+    const int64_t g = a.AC[3 * i], cx = a.AC[3 * i + 1], cy = a.AC[3 * i + 2];
+    if (g >= 0 && g < a.G && cx >= 0 && cx < a.GW && cy >= 0 && cy < a.GH) {
+      const float2 xi = a.AX[i];
+      v.x = xi.x;
+      v.y = xi.y;
+      v.t = a.AT[i];
+      v.at = v.t - a.SC[g % a.S];
+      v.id = (int)a.AID[i];
+      v.g = (int)g;
+      v.cx = (int)cx;
+      v.cy = (int)cy;
+    }
+  }
+  return v;
+}
+
+// Sixteen lanes per anchor, four anchors per wave: the 3x3 cells around the anchor's cell (csrc/atl_cpu.cpp:
+// 176-200) are three row ranges, walked as one list in steps of 16 consecutive records, so each group reads
+// its records coalesced and the four anchors' dependent loads (cell, row starts, records) overlap.
+// Visit(j, rx, ry, dt, kernel) runs on the lanes whose candidate contributes.  The trip count is the wave's
+// longest list; E >= 1 (the host handles an empty plan), so a dead lane's clamped record index is valid.
+constexpr int kWalkBlock = 256;
+constexpr int kGroup = 16;
+
+template <typename Visit>
+__device__ __forceinline__ void walk_group(const AnchorView& v, const PairRef& a, Visit&& visit) {
+  const int sub = threadIdx.x & (kGroup - 1);
+  Rows3 r;
+  r.k0[0] = r.k0[1] = r.k0[2] = 0;
+  r.c1 = r.c2 = r.c3 = 0;
+  if (v.g >= 0)
+    r = row_ranges(a.CS, a.E, v.g, v.cy > 0 ? v.cy - 1 : 0, v.cy + 1 < a.GH ? v.cy + 1 : a.GH - 1,
+                   v.cx > 0 ? v.cx - 1 : 0, v.cx + 1 < a.GW ? v.cx + 1 : a.GW - 1, a.GH, a.GW);
+  const int last = (int)a.E - 1;
+  const int trips = wave_max_i((r.c3 + kGroup - 1) / kGroup);
+  for (int it = 0; it < trips; ++it) {
+    const int p = it * kGroup + sub;
+    const bool live = p < r.c3;
+    int k = list_pos(live ? p : 0, r);
+    k = k < last ? k : last;
+    const int sid = ldr((const int*)a.SID, 2u * (uint32_t)k);
+    const float st = ldr(a.ST, k);
+    const float2 sy = ldr(a.SY, k), sv = ldr(a.SV, k);
+    const float dt = v.t - st;
+    const float rx = v.x - (sy.x + sv.x * v.at);
+    const float ry = v.y - (sy.y + sv.y * v.at);
+    const float d2 = rx * rx + ry * ry;
+    if (live && pair_hit(sid, v.id, dt, d2, a)) visit(sid, rx, ry, dt, gauss(d2, a.kexp));
   }
 }
 
-__global__ void __launch_bounds__(kBlock) k_pair_fwd_ref(PairRef a, int64_t M, float* __restrict__ out,
-                                                         int* __restrict__ count) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= M) return;
-  double acc = 0.0;
-  int n = 0;
-  walk_ref(i, a, [&](int64_t, float, float, float, float k) {
-    acc += (double)k;
-    ++n;
-  });
-  out[i] = (float)acc;
-  if (count) count[i] = n;
+__device__ __forceinline__ void group_sum(float& acc, int& n) {
+#pragma unroll
+  for (int d = kGroup / 2; d >= 1; d >>= 1) {
+    acc += __shfl_xor(acc, d, kWave);
+    n += __shfl_xor(n, d, kWave);
+  }
 }
 
-__global__ void __launch_bounds__(kBlock) k_pair_bwd_ref(PairRef a, int64_t M, const float* __restrict__ gS,
-                                                         float invh2, float* __restrict__ gv) {
+// Forward in the plan's anchor order (the workspace-free entry).
+__global__ void __launch_bounds__(kWalkBlock) k_pair_fwd_group(PairRef a, int64_t M, float* __restrict__ out,
+                                                               int* __restrict__ count) {
+  const int64_t i = ((int64_t)blockIdx.x * kWalkBlock + threadIdx.x) / kGroup;
+  const bool on = i < M;
+  const AnchorView v = anchor_from_plan(i, on, a);
+  float acc = 0.f;
+  int n = 0;
+  walk_group(v, a, [&](int, float, float, float, float k) {
+    acc += k;
+    ++n;
+  });
+  group_sum(acc, n);
+  if (on && (threadIdx.x & (kGroup - 1)) == 0) {
+    out[i] = acc;
+    if (count) count[i] = n;
+  }
+}
+
+// Backward with the reference's per-pair scatter (csrc/atl_cuda.cu:169-180): two global atomics per pair.
+// Used only where no workspace is given.  Anchors with gS == 0 are skipped, as there.
+__global__ void __launch_bounds__(kWalkBlock) k_pair_bwd_group(PairRef a, int64_t M, const float* __restrict__ gS,
+                                                               float invh2, float* __restrict__ gv) {
+  const int64_t i = ((int64_t)blockIdx.x * kWalkBlock + threadIdx.x) / kGroup;
+  const float gi = i < M ? gS[i] : 0.f;
+  const AnchorView v = anchor_from_plan(i, i < M && gi != 0.f, a);
+  walk_group(v, a, [&](int j, float rx, float ry, float dt, float kern) {
+    const float f = gi * kern * dt * invh2;
+    if (j < 0 || j >= a.N) return;
+    atomicAdd(gv + 2 * (int64_t)j, f * rx);
+    atomicAdd(gv + 2 * (int64_t)j + 1, f * ry);
+  });
+}
+
+// ---- anchors binned by cell (the workspace entries).  Each anchor inside the grid (and, for the backward,
+// with gS != 0, as the reference's backward skips the others) gets a record in its cell's run of the list.
+// Within a cell the order follows the atomics; the forward's sums do not depend on it.
+struct __align__(16) AnchorRec {
+  float x, y, t, g;     // position, time, gS (0 in the forward)
+  int id, col, row, idx;  // event id (low word), cell column, plane row g * GH + cy, anchor index
+};
+
+__device__ __forceinline__ int64_t anchor_key(int64_t i, const PairRef& a) {
+  const int64_t g = a.AC[3 * i], cx = a.AC[3 * i + 1], cy = a.AC[3 * i + 2];
+  if (g < 0 || g >= a.G || cx < 0 || cx >= a.GW || cy < 0 || cy >= a.GH) return -1;
+  return (g * a.GH + cy) * a.GW + cx;
+}
+
+__global__ void __launch_bounds__(kBlock) k_anchor_count(PairRef a, int64_t M, const float* __restrict__ gS,
+                                                         int* __restrict__ cnt) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M || (gS && gS[i] == 0.f)) return;
+  const int64_t key = anchor_key(i, a);
+  if (key >= 0) atomicAdd(cnt + key, 1);
+}
+
+// Writes each anchor's record into its cell's run, filled from the run's end (the counts run down to zero).
+__global__ void __launch_bounds__(kBlock) k_anchor_place(PairRef a, int64_t M, const float* __restrict__ gS,
+                                                         const int64_t* __restrict__ astart, int* __restrict__ cnt,
+                                                         AnchorRec* __restrict__ arec) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= M) return;
-  const float gi = gS[i];
-  if (gi == 0.f) return;
-  walk_ref(i, a, [&](int64_t k, float rx, float ry, float dt, float kern) {
-    const float f = gi * kern * dt * invh2;
-    const int64_t j = a.SID[k];
-    if (j < 0 || j >= a.N) return;
-    atomicAdd(gv + 2 * j, f * rx);
-    atomicAdd(gv + 2 * j + 1, f * ry);
+  const float gi = gS ? gS[i] : 0.f;
+  if (gS && gi == 0.f) return;
+  const int64_t key = anchor_key(i, a);
+  if (key < 0) return;
+  const int slot = atomicSub(cnt + key, 1) - 1;
+  const float2 xi = a.AX[i];
+  AnchorRec rec;
+  rec.x = xi.x;
+  rec.y = xi.y;
+  rec.t = a.AT[i];
+  rec.g = gi;
+  rec.id = (int)a.AID[i];
+  rec.col = (int)a.AC[3 * i + 1];
+  rec.row = (int)(key / a.GW);
+  rec.idx = (int)i;
+  arec[astart[key] + slot] = rec;
+}
+
+// Forward over the binned anchors: four consecutive anchors of a wave mostly share a cell and so read the same
+// records (one set of cache lines per instruction), and neighbouring waves share L2 lines.  nb = the number of
+// binned anchors (read on the device); out and count of the anchors outside the grid are zero-filled first.
+__global__ void __launch_bounds__(kWalkBlock) k_pair_fwd_binned(PairRef a, const AnchorRec* __restrict__ arec,
+                                                                const int64_t* __restrict__ nb_ptr,
+                                                                float* __restrict__ out, int* __restrict__ count) {
+  const int64_t pos = ((int64_t)blockIdx.x * kWalkBlock + threadIdx.x) / kGroup;
+  const bool on = pos < *nb_ptr;
+  AnchorView v = no_anchor();
+  int idx = 0;
+  if (on) {
+    const AnchorRec q = arec[pos];
+    v.x = q.x;
+    v.y = q.y;
+    v.t = q.t;
+    v.id = q.id;
+    v.g = q.row / (int)a.GH;
+    v.cy = q.row - v.g * (int)a.GH;
+    v.cx = q.col;
+    v.at = q.t - a.SC[v.g % (int)a.S];
+    idx = q.idx;
+  }
+  float acc = 0.f;
+  int n = 0;
+  walk_group(v, a, [&](int, float, float, float, float k) {
+    acc += k;
+    ++n;
   });
+  group_sum(acc, n);
+  if (on && (threadIdx.x & (kGroup - 1)) == 0) {
+    out[idx] = acc;
+    if (count) count[idx] = n;
+  }
+}
+
+// ---- source-centric backward.  Work unit: a run of kSegCells source cells of a row; work item: one chunk of
+// 64 consecutive records of a unit (so a dense unit spreads over many waves).  One wave per item gathers over
+// the binned anchors of the 3 x (kSegCells + 2) cells around the unit and adds each record's sum to gv once
+// (two atomics per record instead of two per pair).  A pair (anchor in cell c, record in cell c') is visited
+// iff |c - c'| <= 1 in both coordinates of the same plane (the column test is explicit: the unit's anchors
+// span kSegCells + 2 columns), the reference's neighbourhood seen from the record's side, and the tests are
+// the same, so the visited pairs are the reference's.
+constexpr int kSegCells = 4;       // source cells of a row per unit (~4 x 16 records at the 1M-event density)
+constexpr int kGatherWaves = 4;    // waves per workgroup, each on its own item
+constexpr int kXcds = 8, kXcdRun = 64;
+constexpr int kNoCol = -(1 << 29); // column of a padding slot: never within one of a record's column
+
+struct UnitGeo {
+  int64_t rowid, g, cy, cx0, cx1;
+};
+
+__device__ __forceinline__ UnitGeo unit_geo(int64_t u, int64_t nseg, const PairRef& a) {
+  UnitGeo q;
+  const int64_t seg = u % nseg;
+  q.rowid = u / nseg;
+  q.cy = q.rowid % a.GH;
+  q.g = q.rowid / a.GH;
+  q.cx0 = seg * kSegCells;
+  q.cx1 = q.cx0 + kSegCells < a.GW ? q.cx0 + kSegCells : a.GW;
+  return q;
+}
+
+__device__ __forceinline__ Rows3 unit_anchors(const UnitGeo& q, const int64_t* __restrict__ astart, int64_t Mlist,
+                                              const PairRef& a) {
+  return row_ranges(astart, Mlist, q.g, q.cy > 0 ? q.cy - 1 : 0, q.cy + 1 < a.GH ? q.cy + 1 : a.GH - 1,
+                    q.cx0 > 0 ? q.cx0 - 1 : 0, q.cx1 < a.GW ? q.cx1 : a.GW - 1, a.GH, a.GW);
+}
+
+// Items per unit: its 64-record chunks, or none without records or without anchors around it.
+__global__ void __launch_bounds__(kBlock) k_unit_chunks(PairRef a, const int64_t* __restrict__ astart, int64_t Mlist,
+                                                        int64_t nseg, int64_t units, int* __restrict__ ucnt) {
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= units) return;
+  const UnitGeo q = unit_geo(u, nseg, a);
+  int64_t e0 = a.CS[q.rowid * a.GW + q.cx0], e1 = a.CS[q.rowid * a.GW + q.cx1];
+  e0 = e0 < 0 ? 0 : e0;
+  e1 = e1 > a.E ? a.E : e1;
+  int n = e1 > e0 ? (int)((e1 - e0 + kWave - 1) / kWave) : 0;
+  if (n > 0 && unit_anchors(q, astart, Mlist, a).c3 == 0) n = 0;
+  ucnt[u] = n;
+}
+
+__global__ void __launch_bounds__(kBlock) k_unit_items(const int* __restrict__ ucnt,
+                                                       const int64_t* __restrict__ ustart, int64_t units,
+                                                       int2* __restrict__ items) {
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= units) return;
+  const int n = ucnt[u];
+  const int64_t base = ustart[u];
+  for (int c = 0; c < n; ++c) items[base + c] = make_int2((int)u, c);
+}
+
+// Workgroup -> logical block such that runs of kXcdRun consecutive blocks (neighbouring cells) share one XCD's
+// L2; the hardware places workgroup w on XCD w % 8.  -1 for the padding workgroups of the last group.
+__device__ __forceinline__ int64_t xcd_unit(int64_t nblocks) {
+  const int64_t w = blockIdx.x;
+  const int64_t grp = w / (kXcds * kXcdRun), rem = w - grp * (kXcds * kXcdRun);
+  const int64_t u = grp * (kXcds * kXcdRun) + (rem % kXcds) * kXcdRun + rem / kXcds;
+  return u < nblocks ? u : -1;
+}
+
+// Orders this wave's LDS writes before its later LDS reads (a wave's LDS operations execute in order; this is
+// the compiler barrier plus the wait for the writes).
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// max_items bounds the item count (the grid); the count itself is read on the device (nitems_ptr).
+__global__ void __launch_bounds__(kGatherWaves * kWave)
+k_pair_bwd_gather(PairRef a, const int64_t* __restrict__ astart, const AnchorRec* __restrict__ arec, int64_t Mlist,
+                  const int2* __restrict__ items, const int64_t* __restrict__ nitems_ptr, int64_t max_items,
+                  float invh2, int64_t nseg, float* __restrict__ gv) {
+  __shared__ float4 sa[kGatherWaves][kWave];   // anchor x, y, t, gS
+  __shared__ int4 sb[kGatherWaves][kWave];     // at = t - slice centre (bits), anchor id, anchor cell column
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const int64_t lb = xcd_unit((max_items + kGatherWaves - 1) / kGatherWaves);
+  if (lb < 0) return;
+  const int64_t it = lb * kGatherWaves + w;
+  if (it >= *nitems_ptr) return;               // per wave: the waves of a workgroup never synchronise
+  const int2 item = items[it];
+  const UnitGeo q = unit_geo(item.x, nseg, a);
+  int64_t b0 = a.CS[q.rowid * a.GW + q.cx0], e1 = a.CS[q.rowid * a.GW + q.cx1];
+  b0 = b0 < 0 ? 0 : b0;                               // the clamps of k_unit_chunks
+  e1 = e1 > a.E ? a.E : e1;
+  const int64_t e0 = b0 + (int64_t)item.y * kWave;    // item.y < the unit's chunk count, so e0 < e1
+  const Rows3 r = unit_anchors(q, astart, Mlist, a);
+  const float cs = a.SC[q.g % a.S];
+  const bool live = e0 + lane < e1;
+  const int k = (int)(live ? e0 + lane : e1 - 1);
+  const int sid = ldr((const int*)a.SID, 2u * (uint32_t)k);
+  const float st = ldr(a.ST, k);
+  const float2 sy = ldr(a.SY, k), sv = ldr(a.SV, k);
+  int ce = (int)q.cx0;                                 // the record's cell column
+  for (int64_t c = q.cx0 + 1; c < q.cx1; ++c) ce = k >= a.CS[q.rowid * a.GW + c] ? (int)c : ce;
+  float gx = 0.f, gy = 0.f;
+  bool any = false;
+  for (int pb = 0; pb < r.c3; pb += kWave) {
+    const int p = pb + lane;
+    if (p < r.c3) {
+      const AnchorRec an = arec[list_pos(p, r)];
+      sa[w][lane] = make_float4(an.x, an.y, an.t, an.g);
+      sb[w][lane] = make_int4(__float_as_int(an.t - cs), an.id, an.col, 0);
+    } else {
+      sa[w][lane] = make_float4(0.f, 0.f, 0.f, 0.f);
+      sb[w][lane] = make_int4(0, -1, kNoCol, 0);
+    }
+    wave_lds_sync();
+    const int nj = r.c3 - pb < kWave ? r.c3 - pb : kWave;
+    for (int q0 = 0; q0 < nj; q0 += 4) {
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const float4 A = sa[w][q0 + qq];
+        const int4 Bq = sb[w][q0 + qq];
+        const float at = __int_as_float(Bq.x);
+        const float dt = A.z - st;
+        const float rx = A.x - (sy.x + sv.x * at);
+        const float ry = A.y - (sy.y + sv.y * at);
+        const float d2 = rx * rx + ry * ry;
+        const bool hit = (unsigned)(Bq.z - ce + 1) <= 2u && pair_hit(sid, Bq.y, dt, d2, a);
+        const float f = A.w * gauss(d2, a.kexp) * dt * invh2;
+        gx += hit ? f * rx : 0.f;
+        gy += hit ? f * ry : 0.f;
+        any = any || hit;
+      }
+    }
+    wave_lds_sync();
+  }
+  if (live && any && sid >= 0 && sid < a.N) {
+    atomicAdd(gv + 2 * (int64_t)sid, gx);
+    atomicAdd(gv + 2 * (int64_t)sid + 1, gy);
+  }
 }
 
 // ------------------------------------------------------------------------------------------ window counts
@@ -693,6 +1016,72 @@ PairRef make_ref(const float* src_y, const float* src_v, const float* src_t, con
   return a;
 }
 
+bool pair_args_ok(int64_t E, int64_t ncell, int64_t M, int64_t S, int64_t GH, int64_t GW, double h, int64_t N) {
+  return M >= 0 && E >= 0 && N >= 0 && S >= 1 && GH >= 1 && GW >= 1 && ncell >= 0 && ncell % (GH * GW) == 0 &&
+         h > 0 && E < kMaxRecords && M < kMaxRecords && N < kMaxRecords && ncell < ((int64_t)1 << 31);
+}
+
+int64_t align256(int64_t n) { return (n + 255) & ~(int64_t)255; }
+
+// Workspace of the binned entries: anchor counts per cell (int), their CSR starts (int64, ncell + 1), the
+// scan's tile totals, the anchor records binned by cell (32 bytes, M); the backward adds, per unit of
+// kSegCells cells, its item count (int) and CSR starts (int64, units + 1) with their scan totals, and the
+// items (int2, at most units + E / 64).
+struct PairWs {
+  int* cnt;
+  int64_t* start;
+  int64_t* work;
+  AnchorRec* arec;
+  int* ucnt;
+  int64_t* ustart;
+  int64_t* uwork;
+  int2* items;
+  int64_t units, nseg, max_items, bytes;
+};
+
+PairWs pair_ws_layout(void* base, int64_t E, int64_t ncell, int64_t M, int64_t GW) {
+  PairWs w;
+  w.nseg = (GW + kSegCells - 1) / kSegCells;
+  w.units = ncell / GW * w.nseg;
+  w.max_items = w.units + E / kWave + 1;
+  char* p = (char*)base;
+  int64_t off = 0;
+  auto take = [&](int64_t nbytes) {
+    char* q = p + off;
+    off += align256(nbytes > 0 ? nbytes : 1);
+    return q;
+  };
+  w.cnt = (int*)take(4 * ncell);
+  w.start = (int64_t*)take(8 * (ncell + 1));
+  w.work = (int64_t*)take(8 * atl_scan_work_size(ncell));
+  w.arec = (AnchorRec*)take((int64_t)sizeof(AnchorRec) * M);
+  w.ucnt = (int*)take(4 * w.units);
+  w.ustart = (int64_t*)take(8 * (w.units + 1));
+  w.uwork = (int64_t*)take(8 * atl_scan_work_size(w.units));
+  w.items = (int2*)take(8 * w.max_items);
+  w.bytes = off;
+  return w;
+}
+
+bool pair_ws_ok(const PairWs& w, void* ws, int64_t ws_bytes, const char* what) {
+  if (!ws || ws_bytes < w.bytes || ((uintptr_t)ws & 255)) {
+    set_error("%s: workspace of %lld bytes (256-aligned) needed, got %lld", what, (long long)w.bytes,
+              (long long)ws_bytes);
+    return false;
+  }
+  return true;
+}
+
+// Bins the anchors (all inside the grid, or those with gS != 0) into w.arec by cell.
+int bin_anchors(const PairRef& a, int64_t M, int64_t ncell, const float* gS, const PairWs& w, hipStream_t stream) {
+  hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(ncell)), dim3(kBlock), 0, stream, w.cnt, ncell, 0);
+  hipLaunchKernelGGL(k_anchor_count, dim3(grid_for(M)), dim3(kBlock), 0, stream, a, M, gS, w.cnt);
+  if (atl_scan_counts(w.cnt, ncell, w.start, w.work, stream)) return 1;
+  hipLaunchKernelGGL(k_anchor_place, dim3(grid_for(M)), dim3(kBlock), 0, stream, a, M, gS,
+                     (const int64_t*)w.start, w.cnt, w.arec);
+  return 0;
+}
+
 }  // namespace
 
 // ================================================================================================ C-ABI
@@ -704,7 +1093,7 @@ int atl_plan_stats(const float* v, int64_t N, const float* xa, int64_t M, int* s
   const int64_t n = N > M ? N : M;
   if (n > 0) {
     unsigned grid = grid_for(n);
-    if (grid > 2048) grid = 2048;
+    if (grid > 256) grid = 256;                   // few blocks: their same-address atomics serialise
     hipLaunchKernelGGL(k_stats, dim3(grid), dim3(kBlock), 0, stream, (const float2*)v, N, (const float2*)xa, M,
                        stats);
   }
@@ -774,15 +1163,51 @@ int atl_ats_pair_fwd(const float* src_y, const float* src_v, const float* src_t,
                      const int64_t* anc_cell, const int64_t* anc_id, int64_t M, const float* slice_c, int64_t S,
                      int64_t GH, int64_t GW, double h, double tau, double cut, float* out, int* count,
                      hipStream_t stream) {
-  if (M < 0 || E < 0 || S < 1 || GH < 1 || GW < 1 || ncell < 0 || ncell % (GH * GW) != 0 || !(h > 0)) {
-    set_error("ats_pair_fwd: bad arguments (S=%lld GH=%lld GW=%lld ncell=%lld h=%g)", (long long)S, (long long)GH, (long long)GW, (long long)ncell, h);
+  if (!pair_args_ok(E, ncell, M, S, GH, GW, h, 0)) {
+    set_error("ats_pair_fwd: bad arguments (S=%lld GH=%lld GW=%lld ncell=%lld E=%lld M=%lld h=%g)", (long long)S,
+              (long long)GH, (long long)GW, (long long)ncell, (long long)E, (long long)M, h);
     return 1;
   }
   if (M == 0) return 0;
   const PairRef a = make_ref(src_y, src_v, src_t, src_id, cell_start, E, ncell, anc_x, anc_t, anc_cell, anc_id,
                              slice_c, S, GH, GW, h, tau, cut, 0);
-  hipLaunchKernelGGL(k_pair_fwd_ref, dim3(grid_for(M)), dim3(kBlock), 0, stream, a, M, out, count);
+  if (E == 0) {                                   // no records: every sum and count is zero
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(M)), dim3(kBlock), 0, stream, (int*)out, M, 0);
+    if (count) hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(M)), dim3(kBlock), 0, stream, count, M, 0);
+    return check_launch("ats_pair_fwd");
+  }
+  hipLaunchKernelGGL(k_pair_fwd_group, dim3(grid_for(M, kWalkBlock / kGroup)), dim3(kWalkBlock), 0, stream, a, M,
+                     out, count);
   return check_launch("ats_pair_fwd");
+}
+
+int64_t atl_ats_pair_ws_bytes(int64_t E, int64_t ncell, int64_t M, int64_t GW) {
+  if (E < 0 || ncell < 0 || M < 0 || GW < 1) return -1;
+  return pair_ws_layout(nullptr, E, ncell, M, GW).bytes;
+}
+
+int atl_ats_pair_fwd_ws(const float* src_y, const float* src_v, const float* src_t, const int64_t* src_id,
+                        const int64_t* cell_start, int64_t E, int64_t ncell, const float* anc_x, const float* anc_t,
+                        const int64_t* anc_cell, const int64_t* anc_id, int64_t M, const float* slice_c, int64_t S,
+                        int64_t GH, int64_t GW, double h, double tau, double cut, float* out, int* count, void* ws,
+                        int64_t ws_bytes, hipStream_t stream) {
+  if (!pair_args_ok(E, ncell, M, S, GH, GW, h, 0)) {
+    set_error("ats_pair_fwd_ws: bad arguments (S=%lld GH=%lld GW=%lld ncell=%lld E=%lld M=%lld h=%g)",
+              (long long)S, (long long)GH, (long long)GW, (long long)ncell, (long long)E, (long long)M, h);
+    return 1;
+  }
+  const PairWs w = pair_ws_layout(ws, E, ncell, M, GW);
+  if (!pair_ws_ok(w, ws, ws_bytes, "ats_pair_fwd_ws")) return 1;
+  if (M == 0) return 0;
+  hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(M)), dim3(kBlock), 0, stream, (int*)out, M, 0);
+  if (count) hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(M)), dim3(kBlock), 0, stream, count, M, 0);
+  if (E == 0 || ncell == 0) return check_launch("ats_pair_fwd_ws");
+  const PairRef a = make_ref(src_y, src_v, src_t, src_id, cell_start, E, ncell, anc_x, anc_t, anc_cell, anc_id,
+                             slice_c, S, GH, GW, h, tau, cut, 0);
+  if (bin_anchors(a, M, ncell, nullptr, w, stream)) return 1;
+  hipLaunchKernelGGL(k_pair_fwd_binned, dim3(grid_for(M, kWalkBlock / kGroup)), dim3(kWalkBlock), 0, stream, a,
+                     (const AnchorRec*)w.arec, (const int64_t*)(w.start + ncell), out, count);
+  return check_launch("ats_pair_fwd_ws");
 }
 
 int atl_ats_pair_bwd(const float* gS, const float* src_y, const float* src_v, const float* src_t,
@@ -790,16 +1215,50 @@ int atl_ats_pair_bwd(const float* gS, const float* src_y, const float* src_v, co
                      const float* anc_t, const int64_t* anc_cell, const int64_t* anc_id, int64_t M,
                      const float* slice_c, int64_t S, int64_t GH, int64_t GW, double h, double tau, double cut,
                      int64_t N, float* gv, hipStream_t stream) {
-  if (M < 0 || E < 0 || N < 0 || S < 1 || GH < 1 || GW < 1 || ncell < 0 || ncell % (GH * GW) != 0 || !(h > 0)) {
+  if (!pair_args_ok(E, ncell, M, S, GH, GW, h, N)) {
     set_error("ats_pair_bwd: bad arguments");
     return 1;
   }
-  if (M == 0 || N == 0) return 0;
+  if (M == 0 || N == 0 || E == 0) return 0;
   const PairRef a = make_ref(src_y, src_v, src_t, src_id, cell_start, E, ncell, anc_x, anc_t, anc_cell, anc_id,
                              slice_c, S, GH, GW, h, tau, cut, N);
   const float invh2 = 1.f / (float)(h * h);
-  hipLaunchKernelGGL(k_pair_bwd_ref, dim3(grid_for(M)), dim3(kBlock), 0, stream, a, M, gS, invh2, gv);
+  hipLaunchKernelGGL(k_pair_bwd_group, dim3(grid_for(M, kWalkBlock / kGroup)), dim3(kWalkBlock), 0, stream, a, M,
+                     gS, invh2, gv);
   return check_launch("ats_pair_bwd");
+}
+
+int atl_ats_pair_bwd_ws(const float* gS, const float* src_y, const float* src_v, const float* src_t,
+                        const int64_t* src_id, const int64_t* cell_start, int64_t E, int64_t ncell,
+                        const float* anc_x, const float* anc_t, const int64_t* anc_cell, const int64_t* anc_id,
+                        int64_t M, const float* slice_c, int64_t S, int64_t GH, int64_t GW, double h, double tau,
+                        double cut, int64_t N, float* gv, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  if (!pair_args_ok(E, ncell, M, S, GH, GW, h, N)) {
+    set_error("ats_pair_bwd_ws: bad arguments");
+    return 1;
+  }
+  const PairWs w = pair_ws_layout(ws, E, ncell, M, GW);
+  if (!pair_ws_ok(w, ws, ws_bytes, "ats_pair_bwd_ws")) return 1;
+  if (M == 0 || N == 0 || E == 0 || ncell == 0) return 0;
+  const int64_t grp = kXcds * kXcdRun;
+  const int64_t blocks = ((w.max_items + kGatherWaves - 1) / kGatherWaves + grp - 1) / grp * grp;
+  if (w.units >= kMaxRecords || blocks > 0x7fffffff) {
+    set_error("ats_pair_bwd_ws: grid of %lld cells too large", (long long)ncell);
+    return 1;
+  }
+  const PairRef a = make_ref(src_y, src_v, src_t, src_id, cell_start, E, ncell, anc_x, anc_t, anc_cell, anc_id,
+                             slice_c, S, GH, GW, h, tau, cut, N);
+  const float invh2 = 1.f / (float)(h * h);
+  if (bin_anchors(a, M, ncell, gS, w, stream)) return 1;
+  hipLaunchKernelGGL(k_unit_chunks, dim3(grid_for(w.units)), dim3(kBlock), 0, stream, a, (const int64_t*)w.start, M,
+                     w.nseg, w.units, w.ucnt);
+  if (atl_scan_counts(w.ucnt, w.units, w.ustart, w.uwork, stream)) return 1;
+  hipLaunchKernelGGL(k_unit_items, dim3(grid_for(w.units)), dim3(kBlock), 0, stream, (const int*)w.ucnt,
+                     (const int64_t*)w.ustart, w.units, w.items);
+  hipLaunchKernelGGL(k_pair_bwd_gather, dim3((unsigned)blocks), dim3(kGatherWaves * kWave), 0, stream, a,
+                     (const int64_t*)w.start, (const AnchorRec*)w.arec, M, (const int2*)w.items,
+                     (const int64_t*)(w.ustart + w.units), w.max_items, invh2, w.nseg, gv);
+  return check_launch("ats_pair_bwd_ws");
 }
 
 int atl_window_counts(const float* t, const int64_t* b, int64_t N, const int64_t* idx, int64_t M, double tau,

@@ -58,6 +58,11 @@ _SIGS = {
     "atl_ats_pair_fwd": [_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _D, _D, _D, _P, _P, _P],
     "atl_ats_pair_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _D, _D, _D, _I, _P,
                          _P],
+    "atl_ats_pair_ws_bytes": [_I, _I, _I, _I],
+    "atl_ats_pair_fwd_ws": [_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _D, _D, _D, _P, _P, _P,
+                            _I, _P],
+    "atl_ats_pair_bwd_ws": [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _D, _D, _D, _I,
+                            _P, _P, _I, _P],
     "atl_window_counts": [_P, _P, _I, _P, _I, _D, _P, _P],
     "atl_check_sorted": [_P, _P, _I, _P, _P],
     "atl_bin_counts": [_P, _P, _I, _I, _I, _P, _P],
@@ -101,6 +106,7 @@ _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.
             "atl_tile_ws_bytes": ctypes.c_int64, "atl_splat_gauss_ws_bytes": ctypes.c_int64,
             "atl_anchored_score_mean_scratch_bytes": ctypes.c_int64, "atl_knn_ws_bytes": ctypes.c_int64,
             "atl_voxel_ws_bytes": ctypes.c_int64, "atl_warp_splat_gather_ws_bytes": ctypes.c_int64,
+            "atl_ats_pair_ws_bytes": ctypes.c_int64,
 "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):
@@ -348,23 +354,43 @@ class HipOps:
         _need(aid, "anc_id", I64, dev, (M,)); _need(sc, "slice_c", F32, dev)
         return E, M, cs.shape[0] - 1
 
-    def ats_pair_fwd(self, sy, sv, st, sid, cs, ax, at, ac, aid, sc, S, GH, GW, h, tau, cut, count=None):
+    def _pair_ws(self, E, ncell, M, GW, dev):
+        nbytes = load_library().atl_ats_pair_ws_bytes(E, ncell, M, int(GW))
+        if nbytes < 0:
+            raise HipLibraryError(f"ats_pair: no workspace size for E={E} ncell={ncell} M={M} GW={GW}")
+        return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev), nbytes
+
+    def ats_pair_fwd(self, sy, sv, st, sid, cs, ax, at, ac, aid, sc, S, GH, GW, h, tau, cut, count=None,
+                     plan_order=False):
+        """S (M,).  By default over a workspace allocated here with the output (atl_ats_pair_fwd_ws, anchors
+        walked in cell order); ``plan_order`` selects the workspace-free entry."""
         E, M, ncell = self._pair_args(sy, sv, st, sid, cs, ax, at, ac, aid, sc)
         out = torch.empty(M, device=ax.device, dtype=F32)
+        args = (ptr(sy), ptr(sv), ptr(st), ptr(sid), ptr(cs), E, ncell, ptr(ax), ptr(at), ptr(ac), ptr(aid), M,
+                ptr(sc), int(S), int(GH), int(GW), float(h), float(tau), float(cut), ptr(out), ptr(count))
         with torch.cuda.device(ax.device):
-            call("atl_ats_pair_fwd", ptr(sy), ptr(sv), ptr(st), ptr(sid), ptr(cs), E, ncell, ptr(ax), ptr(at),
-                 ptr(ac), ptr(aid), M, ptr(sc), int(S), int(GH), int(GW), float(h), float(tau), float(cut), ptr(out),
-                 ptr(count), stream_of(ax))
+            if plan_order:
+                call("atl_ats_pair_fwd", *args, stream_of(ax))
+            else:
+                ws, nbytes = self._pair_ws(E, ncell, M, GW, ax.device)
+                call("atl_ats_pair_fwd_ws", *args, ptr(ws), nbytes, stream_of(ax))
         return out
 
-    def ats_pair_bwd(self, g, sy, sv, st, sid, cs, ax, at, ac, aid, sc, S, GH, GW, h, tau, cut, N):
+    def ats_pair_bwd(self, g, sy, sv, st, sid, cs, ax, at, ac, aid, sc, S, GH, GW, h, tau, cut, N,
+                     per_pair_atomics=False):
+        """gv (N, 2).  By default the source-centric backward over a workspace allocated here with the output
+        (atl_ats_pair_bwd_ws); ``per_pair_atomics`` selects the workspace-free entry (two atomics per pair)."""
         E, M, ncell = self._pair_args(sy, sv, st, sid, cs, ax, at, ac, aid, sc)
         _need(g, "gS", F32, ax.device, (M,))
         gv = torch.zeros(int(N), 2, device=ax.device, dtype=F32)
+        args = (ptr(g), ptr(sy), ptr(sv), ptr(st), ptr(sid), ptr(cs), E, ncell, ptr(ax), ptr(at), ptr(ac), ptr(aid),
+                M, ptr(sc), int(S), int(GH), int(GW), float(h), float(tau), float(cut), int(N), ptr(gv))
         with torch.cuda.device(ax.device):
-            call("atl_ats_pair_bwd", ptr(g), ptr(sy), ptr(sv), ptr(st), ptr(sid), ptr(cs), E, ncell, ptr(ax),
-                 ptr(at), ptr(ac), ptr(aid), M, ptr(sc), int(S), int(GH), int(GW), float(h), float(tau), float(cut),
-                 int(N), ptr(gv), stream_of(ax))
+            if per_pair_atomics:
+                call("atl_ats_pair_bwd", *args, stream_of(ax))
+            else:
+                ws, nbytes = self._pair_ws(E, ncell, M, GW, ax.device)
+                call("atl_ats_pair_bwd_ws", *args, ptr(ws), nbytes, stream_of(ax))
         return gv
 
 
