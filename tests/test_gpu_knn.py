@@ -101,7 +101,7 @@ def test_mpcm_loss_device_matches_cpu():
         g = coef.clone().to(dev).requires_grad_(True)
         out = MotionPriorCMaxLoss(num_knn=16, t_ref=0.35)(ev, PixelTrajectories(g, 3, "bspline", tile=4))
         out["loss"].backward()
-        res[dev] = (float(out["loss"]), g.grad.detach().cpu().numpy())
+        res[dev] = (float(out["loss"].detach()), g.grad.detach().cpu().numpy())
     (l0, g0), (l1, g1) = res["cpu"], res[DEV]
     assert abs(l1 - l0) <= 1e-5 * abs(l0)
     assert np.abs(g1 - g0).max() <= 1e-4 * np.abs(g0).max()
