@@ -25,7 +25,7 @@ import math
 import numpy as np
 import torch
 
-from ..ops.functional import TRAJ_BASES, TRAJ_MAX_K, traj_displacement
+from ..ops.functional import TRAJ_BASES, TRAJ_MAX_K, _tile_plan_ok, traj_displacement, traj_origin
 from .base import Motion, as_time
 from .parametric import sample_grid
 
@@ -181,7 +181,12 @@ class PixelTrajectories(Motion):
         return d.flip(-1)
 
     def origin(self, xy: torch.Tensor, t: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-        """Start p of the trajectory through (xy, t): n_fixed_point Picard steps on p = xy - d(p, t)."""
+        """Start p of the trajectory through (xy, t): n_fixed_point Picard steps on p = xy - d(p, t).  On the
+        device, B-spline trajectories take the steps as one autograd node (traj_origin: one coefficient-grid
+        accumulation for all steps in the backward)."""
+        if (xy.is_cuda and self.basis_kind == "bspline" and 3 <= self.K <= TRAJ_MAX_K and not t.requires_grad
+                and self.n_fp >= 1 and _tile_plan_ok(*self.tile_c.shape)):
+            return traj_origin(self.tile_c, xy, b, t, self.K, "bspline", self.n_fp, self.offset, self.tile)
         p = xy
         for _ in range(self.n_fp):
             p = xy - self.displacement(p, b, t)

@@ -408,6 +408,94 @@ def traj_displacement(fld: torch.Tensor, gpos: torch.Tensor, b: torch.Tensor, t:
     return _TrajDisplacement.apply(fld, gpos, b, t, int(K), TRAJ_BASES[basis], plan)
 
 
+class _TrajOrigin(torch.autograd.Function):
+    """PixelTrajectories.origin's n Picard steps p_{k+1} = xy - d(p_k, t), p_0 = xy, as one autograd node
+    (atl/motion/trajectories.py:68-73 differentiated step by step, as autograd does there).  The forward keeps the
+    n positions the displacement is taken at; the backward runs the steps' position gradients in reverse order
+    and then adds every step's coefficient-grid gradient in one accumulation over the n x N records (one tile
+    plan instead of n), each record's row formed from its displacement gradient and time.  B-spline basis with
+    K >= 3 on a grid the tile adjoint takes (the caller checks); grid coordinates g = (p - offset) / tile."""
+
+    @staticmethod
+    def forward(ctx, fld, xy, b, t, K, basis, n, offset, tile):
+        fld, xy, b, t = _f32(fld), _f32(xy), b.contiguous().long(), _f32(t)
+        B, C, Hg, Wg = fld.shape
+        N = xy.shape[0]
+        P = torch.empty(n, N, 2, device=xy.device, dtype=F32)      # grid coordinates of p_0 .. p_{n-1}
+        d = torch.empty(N, 2, device=xy.device, dtype=F32)
+        p = xy
+        with torch.cuda.device(xy.device):
+            st = stream_of(xy)
+            fcl = _channels_last(fld)
+            for k in range(n):
+                P[k] = p if tile == 1 else (p - offset) / tile
+                call("atl_traj_displacement", ptr(fcl), B, C, K, Hg, Wg, ptr(P[k]), ptr(b), ptr(t), N, basis, ptr(d),
+                     st)
+                p = xy - d
+        ctx.save_for_backward(P, b, t, fcl)
+        ctx.shape, ctx.K, ctx.tile = (B, C, Hg, Wg), K, tile
+        return p
+
+    @staticmethod
+    def backward(ctx, gp):
+        P, b, t, fcl = ctx.saved_tensors
+        B, C, Hg, Wg = ctx.shape
+        n, N = P.shape[0], P.shape[1]
+        g = gp.contiguous().float()
+        gD = torch.empty(n, N, 2, device=g.device, dtype=F32)      # gradient of each step's displacement
+        gxy = torch.zeros_like(g) if ctx.needs_input_grad[1] else None
+        gf = None
+        with torch.cuda.device(g.device):
+            st = stream_of(g)
+            for k in range(n - 1, -1, -1):
+                torch.neg(g, out=gD[k])                              # p_{k+1} = xy - d_k
+                if gxy is not None:
+                    gxy += g
+                if k == 0 and gxy is None:
+                    break
+                gk = torch.empty(N, 2, device=g.device, dtype=F32)
+                call("atl_traj_pos_bwd_cl", ptr(gD[k]), ptr(t), ctx.K, ptr(fcl), B, Hg, Wg, ptr(P[k]), ptr(b), N,
+                     ptr(gk), st)
+                g = gk if ctx.tile == 1 else gk / ctx.tile
+                if k == 0:
+                    gxy += g                                         # p_0 = xy
+            if ctx.needs_input_grad[0]:
+                nN = n * N
+                pos, bb, tt = P.view(nN, 2), b.repeat(n), t.repeat(n)
+                nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, nN))
+                if nbytes < 0:
+                    raise HipLibraryError(f"traj origin: no tile plan for {nN} records")
+                ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=g.device)
+                call("atl_grid_plan", B, Hg, Wg, ptr(pos), ptr(bb), nN, 0, 0, ptr(ws), nbytes, st)
+                gf = torch.zeros(B, C, Hg, Wg, device=g.device, dtype=F32)
+                call("atl_traj_field_bwd_planned", ptr(gD.view(nN, 2)), ptr(tt), ctx.K, B, Hg, Wg, nN, ptr(ws),
+                     ptr(gf), st)
+        return gf, gxy, None, None, None, None, None, None, None
+
+
+def traj_origin(fld: torch.Tensor, xy: torch.Tensor, b: torch.Tensor, t: torch.Tensor, K: int, basis: str,
+                n_steps: int, offset: float = 0.0, tile: int = 1) -> torch.Tensor:
+    """Trajectory starts p with p = xy - d(p, t) after ``n_steps`` Picard steps from p = xy, on the device, with
+    the fixed-point steps as one autograd node (the same values and gradients as composing traj_displacement
+    n_steps times; the coefficient-grid gradient of all steps is added in one accumulation).  B-spline basis,
+    3 <= K <= TRAJ_MAX_K, ``fld`` (B, 2K, Hg, Wg) taken by the tile adjoint; grid coordinates (p - offset) / tile."""
+    get_ext()
+    if basis != "bspline" or not 3 <= int(K) <= TRAJ_MAX_K:
+        raise ValueError("traj_origin: B-spline basis with 3 <= K <= TRAJ_MAX_K")
+    if t.requires_grad:
+        raise ValueError("traj_origin: event times carry no gradient")
+    if fld.dim() != 4 or fld.shape[1] != 2 * int(K):
+        raise ValueError(f"traj_origin: coefficient grid must be (B, 2K = {2 * int(K)}, Hg, Wg), got "
+                         f"{tuple(fld.shape)}")
+    B, C, Hg, Wg = fld.shape
+    if not _tile_plan_ok(B, C, Hg, Wg):
+        raise ValueError("traj_origin: grid too large for the tile adjoint")
+    _check_events(xy, b, t, what="traj_origin")
+    if int(n_steps) < 1:
+        raise ValueError("traj_origin: at least one step")
+    return _TrajOrigin.apply(fld, xy, b, t, int(K), TRAJ_BASES[basis], int(n_steps), float(offset), int(tile))
+
+
 def sample_grid_hip(fld: torch.Tensor, pos: torch.Tensor, b: torch.Tensor, img_hw=(0, 0)) -> torch.Tensor:
     """HIP flow lookup: ``pos`` are grid coordinates, or image pixels mapped by x / max(W-1, 1) * (Wg-1)
     when ``img_hw`` = (H, W) is given (DenseLinearFlow.field).  Differentiable w.r.t. the field and the
