@@ -747,6 +747,155 @@ __global__ void __launch_bounds__(kBlock) k_traj_visible(const float4* __restric
   if (live && q == 0) out[n] = fmaxf(vis / fmaxf(tot, 1.f), 1e-3f);
 }
 
+// PixelTrajectories.origin's n_fp Picard steps p <- xy - d(p, t) from p = xy in one pass (atl/motion/
+// trajectories.py:68-73): lanes as in k_traj_displacement (Q per event, one channel quad each) and its sums in
+// its order, so every step equals the composed ops' bits.  P (n_fp x N, may be null) receives the grid
+// coordinates (p - off) / tile of each step's p, where the displacement is taken (the backward's positions).
+template <int K>
+__global__ void __launch_bounds__(kBlock) k_traj_origin(const float4* __restrict__ fcl, int64_t B, int Hg, int Wg,
+                                                        const float2* __restrict__ xy, const float* __restrict__ tt,
+                                                        const int64_t* __restrict__ bidx, int basis, int64_t N,
+                                                        int n_fp, float off, float tile, float2* __restrict__ P,
+                                                        float2* __restrict__ out) {
+  constexpr int C = 2 * K, Q = (C + 3) / 4, EPW = kWave / Q;   // events per wave
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int e = lane / Q, q = lane - e * Q;
+  const int64_t n = wave * EPW + e;
+  const bool live = e < EPW && n < N;
+  int64_t b = -1;
+  float2 x0 = make_float2(0.f, 0.f);
+  float t = 0.f;
+  if (live) {
+    b = bidx[n];
+    x0 = xy[n];
+    t = tt[n];
+  }
+  const bool ok = live && batch_ok(b, B);
+  const float4* f = fcl + (ok ? b : 0) * ((int64_t)Hg * Wg) * Q + q;
+  float g[K];
+  traj_basis<K>(t, basis, g);
+  float2 p = x0;
+  for (int it = 0; it < n_fp; ++it) {
+    const float gx = tile == 1.f ? p.x : (p.x - off) / tile, gy = tile == 1.f ? p.y : (p.y - off) / tile;
+    if (P && live && q == 0) P[(int64_t)it * N + n] = make_float2(gx, gy);
+    float dx = 0.f, dy = 0.f;
+    if (ok) {
+      const GridCorners c = grid_corners(gx, gy, Hg, Wg, 1.f, 1.f, false);
+      const float4 a = f[(int64_t)c.o00 * Q], h0 = f[(int64_t)c.o01 * Q], h1 = f[(int64_t)c.o10 * Q],
+                   k1 = f[(int64_t)c.o11 * Q];
+      const float v[4] = {corner_sum(a.x, h0.x, h1.x, k1.x, c), corner_sum(a.y, h0.y, h1.y, k1.y, c),
+                          corner_sum(a.z, h0.z, h1.z, k1.z, c), corner_sum(a.w, h0.w, h1.w, k1.w, c)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int ch = 4 * q + j;
+        if (ch >= C) break;
+        const int k = ch < K ? ch : ch - K;
+        float gk = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < K; ++kk) gk = kk == k ? g[kk] : gk;
+        if (ch < K)
+          dy = dy + v[j] * gk;
+        else
+          dx = dx + v[j] * gk;
+      }
+    }
+    float sx = dx, sy = dy;                       // the event's first lane adds the others' sums, in lane order
+#pragma unroll
+    for (int i = 1; i < Q; ++i) {
+      const int src = min(lane + i, kWave - 1);
+      const float ox = __shfl(dx, src), oy = __shfl(dy, src);
+      if (q + i < Q) {
+        sx = sx + ox;
+        sy = sy + oy;
+      }
+    }
+    const int lead = min(e * Q, kWave - 1);
+    sx = __shfl(sx, lead);
+    sy = __shfl(sy, lead);
+    p = make_float2(x0.x - sx, x0.y - sy);        // invalid batch: d = 0, p stays xy
+  }
+  if (live && q == 0) out[n] = p;
+}
+
+// The steps' backward of k_traj_origin (B-spline basis) in one pass: for k = n_fp - 1 .. 0, the gradient g of
+// p_{k+1} = xy - d(p_k, t) gives the step's displacement gradient gD_k = -g (written to gD, n_fp x N, for the
+// coefficient-grid accumulation), gxy += g, and, through d's position derivative at the step's grid coordinates
+// P[k] (k_sample_grid_bwd_pos_cl's terms and order, rows formed from gD_k and t), the gradient of p_k divided by
+// tile; p_0 = xy adds the last one to gxy.  gxy (N,2) may be null: then the k = 0 position derivative is skipped.
+template <int K>
+__global__ void __launch_bounds__(kBlock) k_traj_origin_bwd(const float4* __restrict__ fcl, int64_t B, int Hg,
+                                                            int Wg, const float2* __restrict__ P,
+                                                            const float* __restrict__ tt,
+                                                            const int64_t* __restrict__ bidx, int64_t N, int n_fp,
+                                                            float tile, const float2* __restrict__ gp,
+                                                            float2* __restrict__ gD, float2* __restrict__ gxy) {
+  constexpr int C = 2 * K, Q = (C + 3) / 4, EPW = kWave / Q;   // events per wave
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int e = lane / Q, q = lane - e * Q;
+  const int64_t n = wave * EPW + e;
+  const bool live = e < EPW && n < N;
+  const int lead = min(e * Q, kWave - 1);
+  int64_t b = -1;
+  float2 g = make_float2(0.f, 0.f);
+  float t = 0.f;
+  if (live) {
+    b = bidx[n];
+    g = gp[n];
+    t = tt[n];
+  }
+  const bool ok = live && batch_ok(b, B);
+  const float4* f = fcl + (ok ? b : 0) * ((int64_t)Hg * Wg) * Q + q;
+  float nb[4];
+  const int js = bspline_nonzero_rt(t, K, nb);
+  float2 acc = make_float2(0.f, 0.f);
+  for (int k = n_fp - 1; k >= 0; --k) {
+    const float2 d = make_float2(-g.x, -g.y);
+    if (live && q == 0) gD[(int64_t)k * N + n] = d;
+    acc = make_float2(acc.x + g.x, acc.y + g.y);
+    if (k == 0 && !gxy) break;                     // uniform: gxy is a kernel argument
+    float tx[4] = {0.f, 0.f, 0.f, 0.f}, ty[4] = {0.f, 0.f, 0.f, 0.f};
+    bool inx = false, iny = false;
+    if (ok) {
+      const float2 pk = P[(int64_t)k * N + n];
+      inx = pk.x >= 0.f && pk.x <= (float)(Wg - 1);
+      iny = pk.y >= 0.f && pk.y <= (float)(Hg - 1);
+      const GridCorners c = grid_corners(pk.x, pk.y, Hg, Wg, 1.f, 1.f, false);
+      const float ax = c.ax, ay = c.ay;
+      const float4 a = f[(int64_t)c.o00 * Q], h0 = f[(int64_t)c.o01 * Q], h1 = f[(int64_t)c.o10 * Q],
+                   k1 = f[(int64_t)c.o11 * Q];
+      const float f00[4] = {a.x, a.y, a.z, a.w}, f01[4] = {h0.x, h0.y, h0.z, h0.w},
+                  f10[4] = {h1.x, h1.y, h1.z, h1.w}, f11[4] = {k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float go = 4 * q + jj < C ? bspline_row(4 * q + jj, K, js, nb, d) : 0.f;
+        tx[jj] = go * ((1.f - ay) * (f01[jj] - f00[jj]) + ay * (f11[jj] - f10[jj]));
+        ty[jj] = go * ((1.f - ax) * (f10[jj] - f00[jj]) + ax * (f11[jj] - f01[jj]));
+      }
+    }
+    float sx = 0.f, sy = 0.f;                      // the event's first lane adds channels 0 .. C-1 in order
+    for (int i = 0; i < Q; ++i) {
+      const int src = min(lane + i, kWave - 1);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float ox = __shfl(tx[jj], src), oy = __shfl(ty[jj], src);
+        if (4 * i + jj < C) {
+          sx += ox;
+          sy += oy;
+        }
+      }
+    }
+    sx = ok && inx ? sx : 0.f;
+    sy = ok && iny ? sy : 0.f;
+    sx = __shfl(sx, lead);
+    sy = __shfl(sy, lead);
+    g = tile == 1.f ? make_float2(sx, sy) : make_float2(sx / tile, sy / tile);
+    if (k == 0) acc = make_float2(acc.x + g.x, acc.y + g.y);   // p_0 = xy
+  }
+  if (gxy && live && q == 0) gxy[n] = acc;
+}
+
 template <int K>
 __global__ void __launch_bounds__(kBlock) k_traj_gout(const float2* __restrict__ gd, const float* __restrict__ t,
                                                       int basis, int N, float* __restrict__ gout) {
@@ -1028,6 +1177,60 @@ int atl_traj_displacement(const float* field_cl, int64_t B, int64_t C, int64_t K
 #undef ATL_TRAJ_CASE
   }
   return check_launch("traj_displacement");
+}
+
+int atl_traj_origin(const float* field_cl, int64_t B, int64_t C, int64_t K, int64_t Hg, int64_t Wg, const float* xy,
+                    const float* t, const int64_t* b, int64_t N, int64_t n_fp, double offset, int64_t tile,
+                    int64_t basis, float* P, float* out, hipStream_t stream) {
+  if (N < 0 || B < 0 || K < 1 || K > kTrajMaxK || !dims_ok(Hg, Wg) || basis < 0 || basis > 2 || n_fp < 0 ||
+      tile < 1) {
+    set_error("traj_origin: bad sizes (1 <= K <= %d, basis 0, 1 or 2)", kTrajMaxK);
+    return 1;
+  }
+  if (C != 2 * K) { set_error("traj_origin: the coefficient grid has %lld channels, expected 2K = %lld", (long long)C, (long long)(2 * K)); return 1; }
+  if (N == 0) return 0;
+  if (!field_cl || !xy || !t || !b || !out) { set_error("traj_origin: null argument"); return 1; }
+  if (reinterpret_cast<uintptr_t>(field_cl) & 15) { set_error("traj_origin: field_cl must be 16-byte aligned"); return 1; }
+  const int64_t Q = (2 * K + 3) / 4, waves = (N + kWave / Q - 1) / (kWave / Q);
+  const dim3 grid(grid_for(waves * kWave)), block(kBlock);
+  const float4* f = (const float4*)field_cl;
+  const int bs = (int)basis;
+  switch (K) {
+#define ATL_TRAJ_CASE(k) \
+    case k: hipLaunchKernelGGL(k_traj_origin<k>, grid, block, 0, stream, f, B, (int)Hg, (int)Wg, (const float2*)xy, t, \
+                               b, bs, N, (int)n_fp, (float)offset, (float)tile, (float2*)P, (float2*)out); break;
+    ATL_TRAJ_CASE(1) ATL_TRAJ_CASE(2) ATL_TRAJ_CASE(3) ATL_TRAJ_CASE(4) ATL_TRAJ_CASE(5) ATL_TRAJ_CASE(6)
+    ATL_TRAJ_CASE(7) ATL_TRAJ_CASE(8) ATL_TRAJ_CASE(9) ATL_TRAJ_CASE(10) ATL_TRAJ_CASE(11) ATL_TRAJ_CASE(12)
+    ATL_TRAJ_CASE(13) ATL_TRAJ_CASE(14) ATL_TRAJ_CASE(15) ATL_TRAJ_CASE(16)
+#undef ATL_TRAJ_CASE
+  }
+  return check_launch("traj_origin");
+}
+
+int atl_traj_origin_bwd(const float* field_cl, int64_t B, int64_t C, int64_t K, int64_t Hg, int64_t Wg,
+                        const float* P, const float* t, const int64_t* b, int64_t N, int64_t n_fp, int64_t tile,
+                        const float* gp, float* gD, float* gxy, hipStream_t stream) {
+  if (N < 0 || B < 0 || K < 3 || K > kTrajMaxK || !dims_ok(Hg, Wg) || n_fp < 1 || tile < 1) {
+    set_error("traj_origin_bwd: bad sizes (3 <= K <= %d, n_fp >= 1)", kTrajMaxK);
+    return 1;
+  }
+  if (C != 2 * K) { set_error("traj_origin_bwd: the coefficient grid has %lld channels, expected 2K = %lld", (long long)C, (long long)(2 * K)); return 1; }
+  if (N == 0) return 0;
+  if (!field_cl || !P || !t || !b || !gp || !gD) { set_error("traj_origin_bwd: null argument"); return 1; }
+  if (reinterpret_cast<uintptr_t>(field_cl) & 15) { set_error("traj_origin_bwd: field_cl must be 16-byte aligned"); return 1; }
+  const int64_t Q = (2 * K + 3) / 4, waves = (N + kWave / Q - 1) / (kWave / Q);
+  const dim3 grid(grid_for(waves * kWave)), block(kBlock);
+  const float4* f = (const float4*)field_cl;
+  switch (K) {
+#define ATL_TRAJ_CASE(k) \
+    case k: hipLaunchKernelGGL(k_traj_origin_bwd<k>, grid, block, 0, stream, f, B, (int)Hg, (int)Wg, (const float2*)P, \
+                               t, b, N, (int)n_fp, (float)tile, (const float2*)gp, (float2*)gD, (float2*)gxy); break;
+    ATL_TRAJ_CASE(3) ATL_TRAJ_CASE(4) ATL_TRAJ_CASE(5) ATL_TRAJ_CASE(6) ATL_TRAJ_CASE(7) ATL_TRAJ_CASE(8)
+    ATL_TRAJ_CASE(9) ATL_TRAJ_CASE(10) ATL_TRAJ_CASE(11) ATL_TRAJ_CASE(12) ATL_TRAJ_CASE(13) ATL_TRAJ_CASE(14)
+    ATL_TRAJ_CASE(15) ATL_TRAJ_CASE(16)
+#undef ATL_TRAJ_CASE
+  }
+  return check_launch("traj_origin_bwd");
 }
 
 int atl_traj_visible(const float* field_cl, int64_t B, int64_t C, int64_t K, int64_t Hg, int64_t Wg, const float* xa,

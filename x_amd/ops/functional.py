@@ -410,9 +410,10 @@ def traj_displacement(fld: torch.Tensor, gpos: torch.Tensor, b: torch.Tensor, t:
 
 class _TrajOrigin(torch.autograd.Function):
     """PixelTrajectories.origin's n Picard steps p_{k+1} = xy - d(p_k, t), p_0 = xy, as one autograd node
-    (atl/motion/trajectories.py:68-73 differentiated step by step, as autograd does there).  The forward keeps the
-    n positions the displacement is taken at; the backward runs the steps' position gradients in reverse order
-    and then adds every step's coefficient-grid gradient in one accumulation over the n x N records (one tile
+    (atl/motion/trajectories.py:68-73 differentiated step by step, as autograd does there).  The forward runs the
+    steps in one kernel (atl_traj_origin, the composed ops' bits) and keeps the n positions the displacement is
+    taken at; the backward runs the steps' position gradients in reverse order
+    in one kernel (atl_traj_origin_bwd) and then adds every step's coefficient-grid gradient in one accumulation over the n x N records (one tile
     plan instead of n), each record's row formed from its displacement gradient and time.  B-spline basis with
     K >= 3 on a grid the tile adjoint takes (the caller checks); grid coordinates g = (p - offset) / tile."""
 
@@ -422,16 +423,11 @@ class _TrajOrigin(torch.autograd.Function):
         B, C, Hg, Wg = fld.shape
         N = xy.shape[0]
         P = torch.empty(n, N, 2, device=xy.device, dtype=F32)      # grid coordinates of p_0 .. p_{n-1}
-        d = torch.empty(N, 2, device=xy.device, dtype=F32)
-        p = xy
+        p = torch.empty(N, 2, device=xy.device, dtype=F32)
         with torch.cuda.device(xy.device):
-            st = stream_of(xy)
             fcl = _channels_last(fld)
-            for k in range(n):
-                P[k] = p if tile == 1 else (p - offset) / tile
-                call("atl_traj_displacement", ptr(fcl), B, C, K, Hg, Wg, ptr(P[k]), ptr(b), ptr(t), N, basis, ptr(d),
-                     st)
-                p = xy - d
+            call("atl_traj_origin", ptr(fcl), B, C, K, Hg, Wg, ptr(xy), ptr(t), ptr(b), N, n, float(offset), int(tile),
+                 basis, ptr(P), ptr(p), stream_of(xy))
         ctx.save_for_backward(P, b, t, fcl)
         ctx.shape, ctx.K, ctx.tile = (B, C, Hg, Wg), K, tile
         return p
@@ -443,22 +439,13 @@ class _TrajOrigin(torch.autograd.Function):
         n, N = P.shape[0], P.shape[1]
         g = gp.contiguous().float()
         gD = torch.empty(n, N, 2, device=g.device, dtype=F32)      # gradient of each step's displacement
-        gxy = torch.zeros_like(g) if ctx.needs_input_grad[1] else None
+        gxy = torch.empty_like(g) if ctx.needs_input_grad[1] else None
         gf = None
         with torch.cuda.device(g.device):
             st = stream_of(g)
-            for k in range(n - 1, -1, -1):
-                torch.neg(g, out=gD[k])                              # p_{k+1} = xy - d_k
-                if gxy is not None:
-                    gxy += g
-                if k == 0 and gxy is None:
-                    break
-                gk = torch.empty(N, 2, device=g.device, dtype=F32)
-                call("atl_traj_pos_bwd_cl", ptr(gD[k]), ptr(t), ctx.K, ptr(fcl), B, Hg, Wg, ptr(P[k]), ptr(b), N,
-                     ptr(gk), st)
-                g = gk if ctx.tile == 1 else gk / ctx.tile
-                if k == 0:
-                    gxy += g                                         # p_0 = xy
+            # the steps in reverse order: gD_k = -g, g <- d's position derivative at P[k] applied to gD_k / tile
+            call("atl_traj_origin_bwd", ptr(fcl), B, C, ctx.K, Hg, Wg, ptr(P), ptr(t), ptr(b), N, n, ctx.tile,
+                 ptr(g), ptr(gD), ptr(gxy), st)
             if ctx.needs_input_grad[0]:
                 nN = n * N
                 pos, bb, tt = P.view(nN, 2), b.repeat(n), t.repeat(n)
