@@ -243,19 +243,21 @@ def test_pixel_trajectories_device_matches_cpu(K, kind, tile):
     close_rel(res[DEV][1], res["cpu"][1], 1e-4)
 
 
-@pytest.mark.parametrize("K,kind,tile", [(10, "bspline", 1), (3, "bezier", 4), (1, "polynomial", 1),
-                                         (10, "bspline", 4)])
-def test_traj_visible_fraction_same_bits(K, kind, tile):
+@pytest.mark.parametrize("K,kind,tile,n_check", [(10, "bspline", 1, 16), (3, "bezier", 4, 16),
+                                                 (1, "polynomial", 1, 16), (10, "bspline", 4, 16),
+                                                 (10, "bspline", 1, 70)])
+def test_traj_visible_fraction_same_bits(K, kind, tile, n_check):
     """The one-pass exposure correction for trajectories against the composed device ops (origin, then the
-    displacement at every bin centre, then the weighted share), bit for bit."""
-    print(f"trajectory visible fraction K={K} {kind} tile={tile}", flush=True)
+    displacement at every bin centre, then the weighted share), bit for bit; the bin-centre basis from the
+    kernel's LDS table (n_check <= 64) and computed per centre (more bins)."""
+    print(f"trajectory visible fraction K={K} {kind} tile={tile} n_check={n_check}", flush=True)
     win = synth.small_window(seed=K + tile, n=4000, B=2)
     rng = np.random.default_rng(K * 3 + tile)
     coeffs = synth.trajectory_coeffs(rng, 2, K, win.height, win.width, sigma_px=8.0, dmax=6.0)
     ev = EventPacket.from_window(win, DEV)
     m = PixelTrajectories(T(coeffs), K, kind, tile=tile)
     xa = ev.xy + T(rng.standard_normal((win.n, 2)).astype(F32))
-    tau, n_check = 0.3, 16
+    tau = 0.3
     got = F.traj_visible_fraction(m.tile_c, K, kind, m.n_fp, m.offset, m.tile, xa, ev.t, ev.b, ev.t, ev.b, 2,
                                   win.height, win.width, tau, n_check)
     with torch.no_grad():

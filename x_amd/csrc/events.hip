@@ -646,15 +646,15 @@ __global__ void __launch_bounds__(kBlock) k_traj_displacement(const float4* __re
   if (live && q == 0) out[n] = make_float2(sx, sy);
 }
 
-// Its output gradient per coefficient channel: gout[n, c] = g_k(t_n) * gd_n.y for c = k - 1 < K and
-// g_k(t_n) * gd_n.x for c = K + k - 1, the rows that the field adjoint and the position gradient of the sampler
-// take.  One lane per (event, channel quad), so the rows are written by consecutive lanes.
 // The exposure correction of atl/objectives/ats.py:31-50 for PixelTrajectories in one pass: anchor i's trajectory
 // start p (n_fp Picard steps p <- xa - d(p, t_a) from p = xa, as PixelTrajectories.origin), its coefficients
 // looked up once at p, the trajectory evaluated at the n_check bin centres, y = p + d(p, c_k), and k_visible's
 // weighted share of the centres where y is inside the sensor.  Lanes as in k_traj_displacement (Q per anchor, one
 // channel quad each) and the same sums in the same order, so every p and y equals the composed ops' bits.  Grid
-// coordinates of a pixel position: (p - off) / tile (tile 1: p itself).
+// coordinates of a pixel position: (p - off) / tile (tile 1: p itself).  The basis at the anchor's time is
+// evaluated once, and at the bin centres once per workgroup into LDS (the same function: the same values).
+constexpr int kVisMaxCheck = 64;
+
 template <int K>
 __global__ void __launch_bounds__(kBlock) k_traj_visible(const float4* __restrict__ fcl, int64_t B, int Hg, int Wg,
                                                          const float2* __restrict__ xa,
@@ -681,6 +681,19 @@ __global__ void __launch_bounds__(kBlock) k_traj_visible(const float4* __restric
   }
   const bool ok = live && batch_ok(b, B);
   const float4* f = fcl + (ok ? b : 0) * ((int64_t)Hg * Wg) * Q + q;
+  __shared__ float gcs[kVisMaxCheck * K];        // basis at the bin centres, centre-major
+  const bool table = n_check <= kVisMaxCheck;
+  if (table) {
+    for (int i = threadIdx.x; i < n_check; i += blockDim.x) {
+      float gc[K];
+      traj_basis<K>(centres[i], basis, gc);
+#pragma unroll
+      for (int k = 0; k < K; ++k) gcs[i * K + k] = gc[k];
+    }
+  }
+  __syncthreads();
+  float gt[K];                                   // basis at the anchor's own time
+  traj_basis<K>(t, basis, gt);
   // this lane's quad of the coefficients at grid coordinates of pixel position p: v[4]
   auto lookup = [&](float2 p, float (&v)[4]) {
     const float gx = tile == 1.f ? p.x : (p.x - off) / tile, gy = tile == 1.f ? p.y : (p.y - off) / tile;
@@ -694,18 +707,15 @@ __global__ void __launch_bounds__(kBlock) k_traj_visible(const float4* __restric
   };
   // d = sum_k c_k g_k(tt) from this lane's quad v, combined over the anchor's lanes in lane order (the event's
   // first lane adds the others' sums, k_traj_displacement's order), returned to every lane of the anchor
-  auto disp = [&](const float (&v)[4], float tt) {
-    float g[K];
-    traj_basis<K>(tt, basis, g);
+  // gsel(k) = g_k at the time in question (k = 0 .. K-1)
+  auto disp = [&](const float (&v)[4], auto&& gsel) {
     float dx = 0.f, dy = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int ch = 4 * q + j;
       if (ch >= C) break;
       const int k = ch < K ? ch : ch - K;
-      float gk = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < K; ++kk) gk = kk == k ? g[kk] : gk;
+      const float gk = gsel(k);
       if (ch < K)
         dy = dy + v[j] * gk;
       else
@@ -723,11 +733,17 @@ __global__ void __launch_bounds__(kBlock) k_traj_visible(const float4* __restric
     }
     return make_float2(__shfl(sx, lead), __shfl(sy, lead));
   };
+  auto own = [&](int k) {                        // register select, no indexed private array
+    float gk = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < K; ++kk) gk = kk == k ? gt[kk] : gk;
+    return gk;
+  };
   float v[4] = {0.f, 0.f, 0.f, 0.f};
   float2 p = x0;
   for (int it = 0; it < n_fp; ++it) {            // p <- xa - d(p, t_a)
     if (ok) lookup(p, v);
-    const float2 d = disp(v, t);                  // every lane takes part in the shuffles
+    const float2 d = disp(v, own);                // every lane takes part in the shuffles
     if (ok) p = make_float2(x0.x - d.x, x0.y - d.y);
   }
   if (ok) lookup(p, v);
@@ -735,7 +751,19 @@ __global__ void __launch_bounds__(kBlock) k_traj_visible(const float4* __restric
   const float* cnt = counts + (ok ? b : 0) * n_check;
   for (int k = 0; k < n_check; ++k) {
     const float c = centres[k];
-    const float2 d = disp(v, c);                  // every lane takes part in the shuffles
+    float2 d;                                     // every lane takes part in the shuffles
+    if (table) {
+      d = disp(v, [&](int kk) { return gcs[k * K + kk]; });
+    } else {
+      float gc[K];
+      traj_basis<K>(c, basis, gc);
+      d = disp(v, [&](int kk) {
+        float gk = 0.f;
+#pragma unroll
+        for (int k2 = 0; k2 < K; ++k2) gk = k2 == kk ? gc[k2] : gk;
+        return gk;
+      });
+    }
     if (!ok) continue;
     const float yx = p.x + d.x, yy = p.y + d.y;
     const float near = fabsf(t - c) <= tau ? 1.f : 0.f;
@@ -896,6 +924,9 @@ __global__ void __launch_bounds__(kBlock) k_traj_origin_bwd(const float4* __rest
   if (gxy && live && q == 0) gxy[n] = acc;
 }
 
+// The displacement's output gradient per coefficient channel: gout[n, c] = g_k(t_n) * gd_n.y for c = k - 1 < K and
+// g_k(t_n) * gd_n.x for c = K + k - 1, the rows that the field adjoint and the position gradient of the sampler
+// take.  One lane per (event, channel quad), so the rows are written by consecutive lanes.
 template <int K>
 __global__ void __launch_bounds__(kBlock) k_traj_gout(const float2* __restrict__ gd, const float* __restrict__ t,
                                                       int basis, int N, float* __restrict__ gout) {
