@@ -1341,7 +1341,11 @@ int atl_traj_field_bwd_planned(const float* gd, const float* t, int64_t K, int64
   char* w = (char*)ws;
   int4* info = (int4*)(w + L.info);
   int* nchunk = (int*)(w + L.nchunk);
-  hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.boff), g, kAccChunk,
+  // with more than kBinChunk / 2 records per tile on average (the many-step origin adjoints), chunks of kBinChunk
+  // records (four accumulation rounds per workgroup): a window is cleared and flushed once per 2048 records, not
+  // per 512; sparser planes keep the 512-record chunks, which spread a dense tile over more workgroups
+  const int chunk = N > (int64_t)g.nkeys * (kBinChunk / 2) ? kBinChunk : kAccChunk;
+  hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.boff), g, chunk,
                      kBinChunk, info, nchunk);
   hipLaunchKernelGGL(k_tile_accum_rows, dim3((unsigned)max_chunks(g)), dim3(kAccBlock),
                      (size_t)g.C * (kBinT + 1) * (kBinT + 1) * sizeof(float), stream, (const int4*)info,
