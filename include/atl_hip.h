@@ -153,10 +153,11 @@ int atl_traj_displacement(const float* field_cl, int64_t B, int64_t C, int64_t K
 /* PixelTrajectories.origin (atl/motion/trajectories.py:68-73) in one pass: n_fp Picard steps p <- xy - d(p, t) from
  * p = xy, out (N,2) written, bit-identical to n_fp composed atl_traj_displacement calls with the subtraction between
  * them.  P (n_fp, N, 2), may be null, receives the grid coordinates (p - offset) / tile (tile 1: p) of every step's
- * p, where its displacement is taken: the positions of the steps' backward. */
+ * p, where its displacement is taken: the positions of the steps' backward; with final_row != 0, P has n_fp + 1
+ * rows and the last receives those of the returned p (where PixelTrajectories.transport's last look-up is). */
 int atl_traj_origin(const float* field_cl, int64_t B, int64_t C, int64_t K, int64_t Hg, int64_t Wg, const float* xy,
                     const float* t, const int64_t* b, int64_t N, int64_t n_fp, double offset, int64_t tile,
-                    int64_t basis, float* P, float* out, hipStream_t stream);
+                    int64_t basis, float* P, int64_t final_row, float* out, hipStream_t stream);
 /* The backward of atl_traj_origin's steps for the B-spline basis (K >= 3), in one pass: from gp (N,2), the gradient
  * of the returned p, for k = n_fp - 1 .. 0 the step's displacement gradient gD_k = -g (gD (n_fp, N, 2) written,
  * for atl_grid_plan + atl_traj_field_bwd_planned over all n_fp N records) and g <- the displacement's position

@@ -189,12 +189,14 @@ def test_traj_displacement_empty_and_rejected_inputs():
     assert rc == 1 and b"expected 2K" in _ext.load_library().atl_last_error()
 
 
-@pytest.mark.parametrize("K,tile,steps", [(3, 1, 6), (10, 1, 6), (10, 4, 6), (4, 4, 1)])
-def test_traj_origin_node_matches_composed_steps(K, tile, steps):
-    """The fixed-point origin as one autograd node (one field accumulation over every step's records) against
-    the same steps composed from traj_displacement: the same starts bit for bit, and the same coefficient-grid
-    and position gradients to the order of the accumulation's additions."""
-    print(f"traj origin node K={K} tile={tile} steps={steps}", flush=True)
+@pytest.mark.parametrize("K,tile,steps,dst", [(3, 1, 6, False), (10, 1, 6, False), (10, 4, 6, False),
+                                              (4, 4, 1, False), (10, 1, 6, True), (3, 4, 2, True)])
+def test_traj_origin_node_matches_composed_steps(K, tile, steps, dst):
+    """The fixed-point origin as one autograd node (one field accumulation over every step's records), and with
+    dst the transport's last look-up in the same node, against the same steps composed from traj_displacement:
+    the same positions bit for bit, and the same coefficient-grid and position gradients to the order of the
+    accumulation's additions."""
+    print(f"traj origin node K={K} tile={tile} steps={steps} dst={dst}", flush=True)
     from x_amd.ops import functional as F
     rng = np.random.default_rng(10 * K + tile)
     win = synth.small_window(seed=K + tile, n=4000, B=2)
@@ -202,18 +204,21 @@ def test_traj_origin_node_matches_composed_steps(K, tile, steps):
     w = T(rng.standard_normal((win.n, 2)).astype(F32))
     ev = EventPacket.from_window(win, DEV)
     off = float(tile // 2)
+    td = T(rng.uniform(0, 1, win.n).astype(F32)) if dst else None
     res = []
     for fused in (True, False):
         c = torch.tensor(coeffs, device=DEV, requires_grad=True)
         fld = c if tile == 1 else c[:, :, tile // 2::tile, tile // 2::tile]
         xy = ev.xy.clone().requires_grad_(True)
         if fused:
-            p = F.traj_origin(fld, xy, ev.b, ev.t, K, "bspline", steps, off, tile)
+            p = F.traj_origin(fld, xy, ev.b, ev.t, K, "bspline", steps, off, tile, t_dst=td)
         else:
             p = xy
             for _ in range(steps):
                 g = p if tile == 1 else (p - off) / tile
                 p = xy - F.traj_displacement(fld, g, ev.b, ev.t, K, "bspline")
+            if dst:
+                p = p + F.traj_displacement(fld, p if tile == 1 else (p - off) / tile, ev.b, td, K, "bspline")
         (p * w).sum().backward()
         res.append((p.detach(), c.grad, xy.grad))
     assert torch.equal(res[0][0], res[1][0])

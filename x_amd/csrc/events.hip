@@ -778,13 +778,14 @@ __global__ void __launch_bounds__(kBlock) k_traj_visible(const float4* __restric
 // PixelTrajectories.origin's n_fp Picard steps p <- xy - d(p, t) from p = xy in one pass (atl/motion/
 // trajectories.py:68-73): lanes as in k_traj_displacement (Q per event, one channel quad each) and its sums in
 // its order, so every step equals the composed ops' bits.  P (n_fp x N, may be null) receives the grid
-// coordinates (p - off) / tile of each step's p, where the displacement is taken (the backward's positions).
+// coordinates (p - off) / tile of each step's p, where the displacement is taken (the backward's positions),
+// and row n_fp those of the returned p when P holds n_fp + 1 rows (final = 1).
 template <int K>
 __global__ void __launch_bounds__(kBlock) k_traj_origin(const float4* __restrict__ fcl, int64_t B, int Hg, int Wg,
                                                         const float2* __restrict__ xy, const float* __restrict__ tt,
                                                         const int64_t* __restrict__ bidx, int basis, int64_t N,
                                                         int n_fp, float off, float tile, float2* __restrict__ P,
-                                                        float2* __restrict__ out) {
+                                                        int final, float2* __restrict__ out) {
   constexpr int C = 2 * K, Q = (C + 3) / 4, EPW = kWave / Q;   // events per wave
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
@@ -843,7 +844,11 @@ __global__ void __launch_bounds__(kBlock) k_traj_origin(const float4* __restrict
     sy = __shfl(sy, lead);
     p = make_float2(x0.x - sx, x0.y - sy);        // invalid batch: d = 0, p stays xy
   }
-  if (live && q == 0) out[n] = p;
+  if (live && q == 0) {
+    out[n] = p;
+    if (P && final)
+      P[(int64_t)n_fp * N + n] = make_float2(tile == 1.f ? p.x : (p.x - off) / tile, tile == 1.f ? p.y : (p.y - off) / tile);
+  }
 }
 
 // The steps' backward of k_traj_origin (B-spline basis) in one pass: for k = n_fp - 1 .. 0, the gradient g of
@@ -1212,7 +1217,7 @@ int atl_traj_displacement(const float* field_cl, int64_t B, int64_t C, int64_t K
 
 int atl_traj_origin(const float* field_cl, int64_t B, int64_t C, int64_t K, int64_t Hg, int64_t Wg, const float* xy,
                     const float* t, const int64_t* b, int64_t N, int64_t n_fp, double offset, int64_t tile,
-                    int64_t basis, float* P, float* out, hipStream_t stream) {
+                    int64_t basis, float* P, int64_t final_row, float* out, hipStream_t stream) {
   if (N < 0 || B < 0 || K < 1 || K > kTrajMaxK || !dims_ok(Hg, Wg) || basis < 0 || basis > 2 || n_fp < 0 ||
       tile < 1) {
     set_error("traj_origin: bad sizes (1 <= K <= %d, basis 0, 1 or 2)", kTrajMaxK);
@@ -1229,7 +1234,8 @@ int atl_traj_origin(const float* field_cl, int64_t B, int64_t C, int64_t K, int6
   switch (K) {
 #define ATL_TRAJ_CASE(k) \
     case k: hipLaunchKernelGGL(k_traj_origin<k>, grid, block, 0, stream, f, B, (int)Hg, (int)Wg, (const float2*)xy, t, \
-                               b, bs, N, (int)n_fp, (float)offset, (float)tile, (float2*)P, (float2*)out); break;
+                               b, bs, N, (int)n_fp, (float)offset, (float)tile, (float2*)P, final_row ? 1 : 0, \
+                               (float2*)out); break;
     ATL_TRAJ_CASE(1) ATL_TRAJ_CASE(2) ATL_TRAJ_CASE(3) ATL_TRAJ_CASE(4) ATL_TRAJ_CASE(5) ATL_TRAJ_CASE(6)
     ATL_TRAJ_CASE(7) ATL_TRAJ_CASE(8) ATL_TRAJ_CASE(9) ATL_TRAJ_CASE(10) ATL_TRAJ_CASE(11) ATL_TRAJ_CASE(12)
     ATL_TRAJ_CASE(13) ATL_TRAJ_CASE(14) ATL_TRAJ_CASE(15) ATL_TRAJ_CASE(16)

@@ -184,17 +184,24 @@ class PixelTrajectories(Motion):
         """Start p of the trajectory through (xy, t): n_fixed_point Picard steps on p = xy - d(p, t).  On the
         device, B-spline trajectories take the steps as one autograd node (traj_origin: one coefficient-grid
         accumulation for all steps in the backward)."""
-        if (xy.is_cuda and self.basis_kind == "bspline" and 3 <= self.K <= TRAJ_MAX_K and not t.requires_grad
-                and self.n_fp >= 1 and _tile_plan_ok(*self.tile_c.shape)):
+        if self._one_node(xy, t):
             return traj_origin(self.tile_c, xy, b, t, self.K, "bspline", self.n_fp, self.offset, self.tile)
         p = xy
         for _ in range(self.n_fp):
             p = xy - self.displacement(p, b, t)
         return p
 
+    def _one_node(self, xy, t) -> bool:
+        """Device B-spline trajectories: origin (and transport) run as one autograd node (traj_origin)."""
+        return (xy.is_cuda and self.basis_kind == "bspline" and 3 <= self.K <= TRAJ_MAX_K and not t.requires_grad
+                and self.n_fp >= 1 and _tile_plan_ok(*self.tile_c.shape))
+
     def transport(self, xy, t, t_dst, b):
+        td = as_time(t_dst, t)
+        if self._one_node(xy, t) and not td.requires_grad:
+            return traj_origin(self.tile_c, xy, b, t, self.K, "bspline", self.n_fp, self.offset, self.tile, t_dst=td)
         p = self.origin(xy, t, b)
-        return p + self.displacement(p, b, as_time(t_dst, t))
+        return p + self.displacement(p, b, td)
 
     def velocity(self, xy, t, b):
         """dq/dt at the event; defined here for K = 1 only (straight trajectories: the motion is linear at the

@@ -42,7 +42,7 @@ _SIGS = {
     "atl_field_channels_last": [_P, _I, _I, _I, _I, _P, _P],
     "atl_traj_displacement": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P, _P],
     "atl_traj_visible": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _D, _I, _I, _P, _P, _I, _D, _I, _I, _P, _P],
-    "atl_traj_origin": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _D, _I, _I, _P, _P, _P],
+    "atl_traj_origin": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _D, _I, _I, _P, _I, _P, _P],
     "atl_traj_origin_bwd": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P],
     "atl_traj_field_bwd_planned": [_P, _P, _I, _I, _I, _I, _I, _P, _P, _P],
     "atl_traj_pos_bwd_cl": [_P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _P],

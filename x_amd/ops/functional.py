@@ -410,66 +410,87 @@ def traj_displacement(fld: torch.Tensor, gpos: torch.Tensor, b: torch.Tensor, t:
 
 class _TrajOrigin(torch.autograd.Function):
     """PixelTrajectories.origin's n Picard steps p_{k+1} = xy - d(p_k, t), p_0 = xy, as one autograd node
-    (atl/motion/trajectories.py:68-73 differentiated step by step, as autograd does there).  The forward runs the
-    steps in one kernel (atl_traj_origin, the composed ops' bits) and keeps the n positions the displacement is
-    taken at; the backward runs the steps' position gradients in reverse order
-    in one kernel (atl_traj_origin_bwd) and then adds every step's coefficient-grid gradient in one accumulation over the n x N records (one tile
-    plan instead of n), each record's row formed from its displacement gradient and time.  B-spline basis with
-    K >= 3 on a grid the tile adjoint takes (the caller checks); grid coordinates g = (p - offset) / tile."""
+    (atl/motion/trajectories.py:68-73 differentiated step by step, as autograd does there), and with ``t_dst``
+    PixelTrajectories.transport's last look-up y = p + d(p, t_dst) (trajectories.py:75-77) in the same node.  The
+    forward runs the steps in one kernel (atl_traj_origin, the composed ops' bits) and keeps the positions the
+    displacements are taken at; the backward runs the steps' position gradients in reverse order in one kernel
+    (atl_traj_origin_bwd) and then adds the coefficient-grid gradient of every look-up in one accumulation over
+    their records (one tile plan instead of one per look-up), each record's row formed from its displacement
+    gradient and time.  B-spline basis with K >= 3 on a grid the tile adjoint takes (the caller checks); grid
+    coordinates g = (p - offset) / tile."""
 
     @staticmethod
-    def forward(ctx, fld, xy, b, t, K, basis, n, offset, tile):
+    def forward(ctx, fld, xy, b, t, K, basis, n, offset, tile, t_dst):
         fld, xy, b, t = _f32(fld), _f32(xy), b.contiguous().long(), _f32(t)
         B, C, Hg, Wg = fld.shape
         N = xy.shape[0]
-        P = torch.empty(n, N, 2, device=xy.device, dtype=F32)      # grid coordinates of p_0 .. p_{n-1}
+        fin = t_dst is not None
+        P = torch.empty(n + int(fin), N, 2, device=xy.device, dtype=F32)   # grid coordinates of every look-up
         p = torch.empty(N, 2, device=xy.device, dtype=F32)
         with torch.cuda.device(xy.device):
+            st = stream_of(xy)
             fcl = _channels_last(fld)
             call("atl_traj_origin", ptr(fcl), B, C, K, Hg, Wg, ptr(xy), ptr(t), ptr(b), N, n, float(offset), int(tile),
-                 basis, ptr(P), ptr(p), stream_of(xy))
-        ctx.save_for_backward(P, b, t, fcl)
-        ctx.shape, ctx.K, ctx.tile = (B, C, Hg, Wg), K, tile
+                 basis, ptr(P), int(fin), ptr(p), st)
+            if fin:
+                t_dst = _f32(t_dst)
+                d = torch.empty(N, 2, device=xy.device, dtype=F32)
+                call("atl_traj_displacement", ptr(fcl), B, C, K, Hg, Wg, ptr(P[n]), ptr(b), ptr(t_dst), N, basis,
+                     ptr(d), st)
+                p = p + d
+        ctx.save_for_backward(P, b, t, fcl, t_dst if fin else None)
+        ctx.shape, ctx.K, ctx.tile, ctx.n, ctx.fin = (B, C, Hg, Wg), K, tile, n, fin
         return p
 
     @staticmethod
-    def backward(ctx, gp):
-        P, b, t, fcl = ctx.saved_tensors
+    def backward(ctx, gy):
+        P, b, t, fcl, t_dst = ctx.saved_tensors
         B, C, Hg, Wg = ctx.shape
-        n, N = P.shape[0], P.shape[1]
-        g = gp.contiguous().float()
-        gD = torch.empty(n, N, 2, device=g.device, dtype=F32)      # gradient of each step's displacement
-        gxy = torch.empty_like(g) if ctx.needs_input_grad[1] else None
+        n, fin = ctx.n, ctx.fin
+        N = P.shape[1]
+        gy = gy.contiguous().float()
+        gD = torch.empty(n + int(fin), N, 2, device=gy.device, dtype=F32)   # gradient of every look-up
+        gxy = torch.empty_like(gy) if ctx.needs_input_grad[1] else None
         gf = None
-        with torch.cuda.device(g.device):
-            st = stream_of(g)
+        with torch.cuda.device(gy.device):
+            st = stream_of(gy)
+            g = gy
+            if fin:                                                  # y = p + d(p, t_dst)
+                gD[n] = gy
+                gk = torch.empty_like(gy)
+                call("atl_traj_pos_bwd_cl", ptr(gy), ptr(t_dst), ctx.K, ptr(fcl), B, Hg, Wg, ptr(P[n]), ptr(b), N,
+                     ptr(gk), st)
+                g = gy + (gk if ctx.tile == 1 else gk / ctx.tile)
             # the steps in reverse order: gD_k = -g, g <- d's position derivative at P[k] applied to gD_k / tile
             call("atl_traj_origin_bwd", ptr(fcl), B, C, ctx.K, Hg, Wg, ptr(P), ptr(t), ptr(b), N, n, ctx.tile,
                  ptr(g), ptr(gD), ptr(gxy), st)
             if ctx.needs_input_grad[0]:
-                nN = n * N
-                pos, bb, tt = P.view(nN, 2), b.repeat(n), t.repeat(n)
-                nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, nN))
+                m = (n + int(fin)) * N
+                tt = t.repeat(n) if not fin else torch.cat([t.repeat(n), t_dst])
+                pos, bb = P.view(m, 2), b.repeat(n + int(fin))
+                nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, m))
                 if nbytes < 0:
-                    raise HipLibraryError(f"traj origin: no tile plan for {nN} records")
-                ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=g.device)
-                call("atl_grid_plan", B, Hg, Wg, ptr(pos), ptr(bb), nN, 0, 0, ptr(ws), nbytes, st)
-                gf = torch.zeros(B, C, Hg, Wg, device=g.device, dtype=F32)
-                call("atl_traj_field_bwd_planned", ptr(gD.view(nN, 2)), ptr(tt), ctx.K, B, Hg, Wg, nN, ptr(ws),
+                    raise HipLibraryError(f"traj origin: no tile plan for {m} records")
+                ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=gy.device)
+                call("atl_grid_plan", B, Hg, Wg, ptr(pos), ptr(bb), m, 0, 0, ptr(ws), nbytes, st)
+                gf = torch.zeros(B, C, Hg, Wg, device=gy.device, dtype=F32)
+                call("atl_traj_field_bwd_planned", ptr(gD.view(m, 2)), ptr(tt), ctx.K, B, Hg, Wg, m, ptr(ws),
                      ptr(gf), st)
-        return gf, gxy, None, None, None, None, None, None, None
+        return gf, gxy, None, None, None, None, None, None, None, None
 
 
 def traj_origin(fld: torch.Tensor, xy: torch.Tensor, b: torch.Tensor, t: torch.Tensor, K: int, basis: str,
-                n_steps: int, offset: float = 0.0, tile: int = 1) -> torch.Tensor:
+                n_steps: int, offset: float = 0.0, tile: int = 1, t_dst: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Trajectory starts p with p = xy - d(p, t) after ``n_steps`` Picard steps from p = xy, on the device, with
     the fixed-point steps as one autograd node (the same values and gradients as composing traj_displacement
-    n_steps times; the coefficient-grid gradient of all steps is added in one accumulation).  B-spline basis,
-    3 <= K <= TRAJ_MAX_K, ``fld`` (B, 2K, Hg, Wg) taken by the tile adjoint; grid coordinates (p - offset) / tile."""
+    n_steps times; the coefficient-grid gradient of all steps is added in one accumulation).  With ``t_dst`` (N,)
+    the node returns the transported positions p + d(p, t_dst) instead (PixelTrajectories.transport).  B-spline
+    basis, 3 <= K <= TRAJ_MAX_K, ``fld`` (B, 2K, Hg, Wg) taken by the tile adjoint; grid coordinates
+    (p - offset) / tile."""
     get_ext()
     if basis != "bspline" or not 3 <= int(K) <= TRAJ_MAX_K:
         raise ValueError("traj_origin: B-spline basis with 3 <= K <= TRAJ_MAX_K")
-    if t.requires_grad:
+    if t.requires_grad or (t_dst is not None and t_dst.requires_grad):
         raise ValueError("traj_origin: event times carry no gradient")
     if fld.dim() != 4 or fld.shape[1] != 2 * int(K):
         raise ValueError(f"traj_origin: coefficient grid must be (B, 2K = {2 * int(K)}, Hg, Wg), got "
@@ -477,10 +498,10 @@ def traj_origin(fld: torch.Tensor, xy: torch.Tensor, b: torch.Tensor, t: torch.T
     B, C, Hg, Wg = fld.shape
     if not _tile_plan_ok(B, C, Hg, Wg):
         raise ValueError("traj_origin: grid too large for the tile adjoint")
-    _check_events(xy, b, t, what="traj_origin")
+    _check_events(xy, b, t, *(() if t_dst is None else (t_dst,)), what="traj_origin")
     if int(n_steps) < 1:
         raise ValueError("traj_origin: at least one step")
-    return _TrajOrigin.apply(fld, xy, b, t, int(K), TRAJ_BASES[basis], int(n_steps), float(offset), int(tile))
+    return _TrajOrigin.apply(fld, xy, b, t, int(K), TRAJ_BASES[basis], int(n_steps), float(offset), int(tile), t_dst)
 
 
 def sample_grid_hip(fld: torch.Tensor, pos: torch.Tensor, b: torch.Tensor, img_hw=(0, 0)) -> torch.Tensor:
