@@ -559,7 +559,7 @@ def test_anchored_exact_fused_loss():
     m = DenseLinearFlow(2, H, W, grid=grid.shape[-2:], init=torch.as_tensor(grid)).to(DEV)
     out = AnchoredExact(h=1.0, tau=0.2, n_anchors=None, seed=0, n_slices=16)(ev, m)
     out["loss"].backward()
-    assert float(out["score"]) == -float(out["loss"]) and not out["score"].requires_grad
+    assert float(out["score"]) == -float(out["loss"].detach()) and not out["score"].requires_grad
     g = torch.Generator().manual_seed(0)
     xs = win.xy + (torch.rand(win.xy.shape, generator=g).numpy() - F32(0.5))
     xa = xs + F32(1.0) * torch.randn(xs.shape, generator=g).numpy()
