@@ -121,6 +121,35 @@ def test_warp_splat_gather_full_size_matches_oracle_and_composed():
     close_rel(g_fused, N(motion.grid.grad), 1e-4)
 
 
+@pytest.mark.parametrize("B", [1, 3])
+def test_translation_iwe_takes_the_fused_launches(B):
+    """A translation's IWE at the events runs the fused launches on a one-node grid (whose bilinear sample is theta
+    exactly, so the warped positions are the composed transport's): image, values and theta's gradient within
+    1e-5 of transport -> make_iwe -> gather (sums in another order); on the plumbing workload (100k events
+    240x180) and on a batch of three windows."""
+    from x_amd.motion import Translation
+    win = synth.plumbing_translation(seed=B) if B == 1 else synth.small_window(seed=B, n=3000, B=B)
+    ev = EventPacket.from_window(win, DEV)
+    theta = (np.asarray(win.motion["theta"], F32)[None] if B == 1 else
+             np.random.default_rng(B).uniform(-3, 3, (B, 2)).astype(F32))
+    cfg = IWEConfig(kernel="bilinear", sigma=0.0, mask_border=True)
+    w = T(np.random.default_rng(B + 7).standard_normal(win.n).astype(F32))
+    res = []
+    for fused in (True, False):
+        m = Translation(B, win.height, win.width, init=torch.as_tensor(theta)).to(DEV)
+        if fused:
+            img, vals = iwe_at_events(ev, m, 0.0 if B == 1 else 0.5, cfg)
+        else:
+            y = m.transport(ev.xy, ev.t, 0.0 if B == 1 else 0.5, ev.b)
+            img = make_iwe(ev, y, 0.0 if B == 1 else 0.5, cfg)
+            vals = F.gather(img, y, ev.b)
+        (vals * w).sum().backward()
+        res.append((img.detach(), vals.detach(), m.theta.grad.clone()))
+    close_rel(N(res[0][0]), N(res[1][0]), 1e-5)
+    close_rel(N(res[0][1]), N(res[1][1]), 1e-5)
+    close_rel(N(res[0][2]), N(res[1][2]), 1e-5)
+
+
 def test_warp_splat_gather_rejects_bad_shapes():
     xy = torch.zeros(10, 2, device=DEV)
     t = torch.zeros(10, device=DEV)

@@ -99,11 +99,16 @@ def iwe_at_events(ev: EventPacket, motion, t_ref: float, cfg: Optional[IWEConfig
     the device with a plain bilinear IWE (sigma 0, pooled polarity, no time weight) runs the fused
     warp -> splat -> gather launches; anything else composes the three ops."""
     cfg = cfg or IWEConfig(kernel="bilinear", sigma=0.0)
-    from ..motion import DenseLinearFlow
-    fused = (ev.device.type == "cuda" and isinstance(motion, DenseLinearFlow) and cfg.kernel == "bilinear"
-             and cfg.sigma == 0 and cfg.polarity == "pooled" and not cfg.scale_by_dt)
-    if fused:
+    from ..motion import DenseLinearFlow, Translation
+    plain = (ev.device.type == "cuda" and cfg.kernel == "bilinear" and cfg.sigma == 0 and cfg.polarity == "pooled"
+             and not cfg.scale_by_dt)
+    if plain and isinstance(motion, DenseLinearFlow):
         return warp_splat_gather(motion.grid, ev.xy, ev.t, ev.b, t_ref, ev.height, ev.width, cfg.mask_border)
+    if plain and type(motion) is Translation:
+        # a translation is the constant field of a one-node grid (B, 2, 1, 1): its bilinear sample is theta_b
+        # exactly (weight 1 on the node), so the fused launches give the composed warp's bits
+        grid = motion.theta.view(motion.theta.shape[0], 2, 1, 1)
+        return warp_splat_gather(grid, ev.xy, ev.t, ev.b, t_ref, ev.height, ev.width, cfg.mask_border)
     xy_ref = motion.transport(ev.xy, ev.t, t_ref, ev.b)
     img = make_iwe(ev, xy_ref, t_ref, cfg)
     return img, gather(img, xy_ref, ev.b)
