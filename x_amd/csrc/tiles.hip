@@ -22,6 +22,7 @@
 #include "traj.h"
 #include "../../include/atl_hip.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <mutex>
@@ -1038,6 +1039,47 @@ __global__ void __launch_bounds__(kBlock) k_wsg_gather(const float* __restrict__
   vals[n] = s;
 }
 
+// Flow-grid adjoint of a one-node grid (Hg = Wg = 1, a translation): every event's sample is the node with weight
+// 1, so the node's gradient is the sum of its batch's per-event rows gv (N, 2); B <= kOneNodeMaxB windows.  Per
+// block: a wave whose lanes share one window adds its rows across the wave first; partial sums per window in LDS,
+// then one global atomic per window and channel (ggrid accumulated, as the tile adjoint accumulates).
+constexpr int kOneNodeMaxB = 64;
+constexpr int kOneNodeBlocks = 256;
+
+__global__ void __launch_bounds__(kBlock) k_one_node_adjoint(const float2* __restrict__ gv,
+                                                             const int64_t* __restrict__ bidx, int64_t N, int B,
+                                                             float* __restrict__ ggrid) {
+  __shared__ float part[2 * kOneNodeMaxB];
+  for (int i = threadIdx.x; i < 2 * B; i += blockDim.x) part[i] = 0.f;
+  __syncthreads();
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < N; base += stride) {   // uniform trip count
+    const int64_t n = base + threadIdx.x;
+    int64_t bb = -1;
+    float2 g = make_float2(0.f, 0.f);
+    if (n < N) {
+      bb = bidx[n];
+      g = gv[n];
+    }
+    const bool ok = bb >= 0 && bb < B;
+    const int bw = __shfl((int)bb, 0);
+    if (__all(!(n < N) || (int)bb == bw) && bw >= 0 && bw < B) {        // one window across the wave
+      const float sx = wave_sum(ok ? g.x : 0.f), sy = wave_sum(ok ? g.y : 0.f);
+      if (lane == 0) {
+        atomicAdd(part + 2 * bw, sx);
+        atomicAdd(part + 2 * bw + 1, sy);
+      }
+    } else if (ok) {
+      atomicAdd(part + 2 * bb, g.x);
+      atomicAdd(part + 2 * bb + 1, g.y);
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 2 * B; i += blockDim.x)
+    if (part[i] != 0.f) atomicAdd(ggrid + i, part[i]);   // ggrid (B, 2, 1, 1): element 2 b + c
+}
+
 // The backward's image pair: ig[p] = (img[p], gimg[p] or 0); the value gradient's splat is then added into the
 // second slots, and the per-event gradient reads both images of a corner row with one 16-byte load.
 __global__ void __launch_bounds__(kBlock) k_wsg_pack(const float* __restrict__ img, const float* __restrict__ gimg,
@@ -1413,6 +1455,12 @@ int atl_warp_splat_gather_bwd(const float* img, const float* gvals, const float*
   hipLaunchKernelGGL(k_wsg_grad, dim3(gg.nblk), dim3(kTileBinBlock), (size_t)gg.nkeys * sizeof(int), stream,
                      (const float2*)ig, gvals, (const float2*)(w + L.y), (const float*)(w + L.w), (const float2*)xy,
                      t, b, (float)t_ref, (int)H, (int)W, gg, (float2*)(w + L.gv), (int*)(wg + L.Lg.cnt));
+  if (Hg == 1 && Wg == 1 && B <= kOneNodeMaxB) {   // a translation: the adjoint is a sum per window
+    const unsigned nb = std::min<unsigned>(grid_for(N), kOneNodeBlocks);
+    hipLaunchKernelGGL(k_one_node_adjoint, dim3(nb), dim3(kBlock), 0, stream, (const float2*)(w + L.gv), b, N,
+                       (int)B, ggrid);
+    return check_launch("warp_splat_gather_bwd");
+  }
   scan32t((int*)(wg + L.Lg.cnt), gg.nkeys, gg.nblk, (int*)(wg + L.Lg.part), (int*)(wg + L.Lg.boff), stream);
   hipLaunchKernelGGL((k_tile_bin<kGridVal, true>), dim3(gg.nblk), dim3(kTileBinBlock),
                      (size_t)gg.nkeys * sizeof(int), stream, (const float2*)xy, b, (const float*)(w + L.gv), gg,
