@@ -80,6 +80,8 @@ def parse():
     ap.add_argument("--sigma", type=float, default=1.0)
     ap.add_argument("--events", type=int, default=0, help="events of the anchored workloads (default 1M; 4M blobs)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="iwe, iwe-plumbing: time eager steps instead of replays of the captured step")
     ap.add_argument("--cpu-budget", type=float, default=25.0, help="seconds of CPU baseline work, at most")
     ap.add_argument("--calibrate-copy", type=float, default=0.0, metavar="MB")
     ap.add_argument("--summarize", nargs="+", metavar="DIR")
@@ -390,9 +392,7 @@ def iwe_main(a, dev):
     t_ref = 0.0 if a.workload == "iwe-plumbing" else 0.5
     cfg = IWEConfig(kernel="bilinear", sigma=0.0, mask_border=True)
 
-    def step():
-        for p in motion.parameters():
-            p.grad = None
+    def body():
         if a.workload == "iwe-composed":
             y = motion.transport(ev.xy, ev.t, t_ref, ev.b)
             img = make_iwe(ev, y, t_ref, cfg)
@@ -401,18 +401,46 @@ def iwe_main(a, dev):
             _, vals = iwe_at_events(ev, motion, t_ref, cfg)
             vals.sum().backward()
 
+    def step():
+        for p in motion.parameters():
+            p.grad = None
+        body()
+
+    # The fused workloads are launch-bound at these sizes: their timed steps replay the whole forward + backward
+    # step captured once as a HIP graph (every kernel runs again in every replay; only the host launch work is
+    # gone).  The kernel times behind the roofline come from eager steps either way.
+    use_graph = a.workload in ("iwe", "iwe-plumbing") and not a.no_graph
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
     kernels = list(IWE_BYTES)
     rec = _ext.time_kernels(kernels, every=5)      # every bracket delays the next launch: sample the steps
     t0 = time.perf_counter()
-    for _ in range(a.steps):
+    for _ in range(10 if use_graph else a.steps):
         step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms = {k: float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in rec[k]])) for k in kernels if rec[k]}
     _ext.time_kernels(())
+    if use_graph:
+        side = torch.cuda.Stream()                 # torch's capture recipe: warm the step up on a side stream
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        for p in motion.parameters():
+            p.grad = None                          # the captured backward writes the gradients it allocates
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            body()
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
     hw = ev.height * ev.width
     g = 0 if a.workload == "iwe-plumbing" else 2 * hw
     gbs = {k: IWE_BYTES[k](ev.n, hw, g) / (ms[k] * 1e-3) / 1e9 for k in ms}
@@ -422,7 +450,8 @@ def iwe_main(a, dev):
         "value": ev.n * a.steps / dt, "unit": "events/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": 1e3 * dt / a.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": desc, "events": ev.n, "sensor": [ev.width, ev.height], "parallelism": "single GPU"},
+        "config": {"workload": desc, "events": ev.n, "sensor": [ev.width, ev.height], "parallelism": "single GPU",
+                   "timed": "HIP graph replays of the whole step" if use_graph else "eager steps"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": gbs[dom], "peak": 8000.0, "unit": "GB/s",
                      "frac": gbs[dom] / 8000.0,
                      "traffic": (recorded_traffic(IWE_KERNELS[dom], IWE_COUNTERS)

@@ -150,6 +150,57 @@ def test_translation_iwe_takes_the_fused_launches(B):
     close_rel(N(res[0][2]), N(res[1][2]), 1e-5)
 
 
+@pytest.mark.parametrize("kind", ["translation", "dense"])
+def test_iwe_step_graph_replays_match_eager(kind):
+    """The IWE step (fused launches, then the sum's backward to the motion) captured as one HIP graph, as the
+    bench times it: every replay, with eager work and a synchronisation between replays, gives the eager step's
+    values and gradient (to the order of the atomic additions)."""
+    from x_amd.motion import Translation
+    print(f"graph replays: {kind}", flush=True)
+    if kind == "translation":
+        win = synth.plumbing_translation(seed=3)
+        m = Translation(1, win.height, win.width, init=torch.as_tensor(np.asarray(win.motion["theta"], F32))[None])
+    else:
+        win = synth.small_window(seed=3, n=20000, H=40, W=48)
+        m = DenseLinearFlow(1, 40, 48, grid=(40, 48), init=torch.as_tensor(win.motion["grid"].astype(F32)))
+    m = m.to(DEV)
+    ev = EventPacket.from_window(win, DEV)
+    cfg = IWEConfig(kernel="bilinear", sigma=0.0, mask_border=True)
+    prm = list(m.parameters())
+
+    def body():
+        _, vals = iwe_at_events(ev, m, 0.5, cfg)
+        vals.sum().backward()
+        return vals
+
+    for q in prm:
+        q.grad = None
+    v_ref = body().detach().clone()
+    g_ref = [N(q.grad) for q in prm]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            for q in prm:
+                q.grad = None
+            body()
+    torch.cuda.current_stream().wait_stream(side)
+    for q in prm:
+        q.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        v_out = body()
+    for r in range(4):
+        for q in prm:
+            q.grad.fill_(123.0)                    # eager work between replays; the replay overwrites it
+        _ = torch.randn(1000, device=DEV).sum().item()
+        graph.replay()
+        torch.cuda.synchronize()
+        close_rel(N(v_out), N(v_ref), 1e-5)
+        for q, gr in zip(prm, g_ref):
+            close_rel(N(q.grad), gr, 1e-4)
+
+
 def test_warp_splat_gather_rejects_bad_shapes():
     xy = torch.zeros(10, 2, device=DEV)
     t = torch.zeros(10, device=DEV)
