@@ -570,7 +570,7 @@ def test_anchored_exact_fused_loss():
     vis = O.visible_fraction_dense(grid, xa, win.t, win.b, win.t, win.b, 2, H, W, 0.2)
     want, gS, _ = O.anchored_epilogue(Sv, wc, 1.0, H, W, vis=vis)
     loss = -float(np.mean(want.astype(np.float64)))
-    assert abs(float(out["loss"]) - loss) <= 1e-5 * abs(loss)
+    assert abs(float(out["loss"].detach()) - loss) <= 1e-5 * abs(loss)
     gv = O.ats_pair_bwd(gS, p, 1.0, 0.2, 3.0, win.n)
     close_rel(N(m.grid.grad), O.sample_grid_bwd(gv, idx, wts, grid.shape), 1e-4)
 
@@ -607,7 +607,7 @@ def test_anchored_exact_device_rng_full_size():
         else:
             out = obj(ev, m)
             loss = -float(np.mean(want.astype(np.float64)))
-            assert abs(float(out["loss"]) - loss) <= 1e-5 * abs(loss)
+            assert abs(float(out["loss"].detach()) - loss) <= 1e-5 * abs(loss)
             out["loss"].backward()
         close_rel(N(m.grid.grad), ggrid, 1e-4)
 
