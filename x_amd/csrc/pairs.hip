@@ -462,38 +462,107 @@ __global__ void __launch_bounds__(kBlock) k_anchor_place(PairRef a, int64_t M, c
   arec[astart[key] + slot] = rec;
 }
 
-// Forward over the binned anchors: four consecutive anchors of a wave mostly share a cell and so read the same
-// records (one set of cache lines per instruction), and neighbouring waves share L2 lines.  nb = the number of
-// binned anchors (read on the device); out and count of the anchors outside the grid are zero-filled first.
-__global__ void __launch_bounds__(kWalkBlock) k_pair_fwd_binned(PairRef a, const AnchorRec* __restrict__ arec,
-                                                                const int64_t* __restrict__ nb_ptr,
-                                                                float* __restrict__ out, int* __restrict__ count) {
-  const int64_t pos = ((int64_t)blockIdx.x * kWalkBlock + threadIdx.x) / kGroup;
-  const bool on = pos < *nb_ptr;
-  AnchorView v = no_anchor();
-  int idx = 0;
-  if (on) {
-    const AnchorRec q = arec[pos];
-    v.x = q.x;
-    v.y = q.y;
-    v.t = q.t;
-    v.id = q.id;
-    v.g = q.row / (int)a.GH;
-    v.cy = q.row - v.g * (int)a.GH;
-    v.cx = q.col;
-    v.at = q.t - a.SC[v.g % (int)a.S];
-    idx = q.idx;
+// Forward over the binned anchors, one wave per item of up to kCellAnchors anchors of one cell: the anchors of a
+// cell share their 3 x 3 neighbourhood, so the wave walks it once, lanes over 64 consecutive records per chunk,
+// and every lane evaluates each anchor of the item on its record (the record loads and list arithmetic once per
+// NA anchors).  Items per cell ceil(anchors / kCellAnchors), listed by k_cell_items / k_cell_expand.
+constexpr int kCellAnchors = 4;
+
+template <int NA>
+__device__ __forceinline__ void fwd_cell(const PairRef& a, const AnchorRec* __restrict__ arec, int64_t k0, int g,
+                                         int cx, int cy, float* __restrict__ out, int* __restrict__ count) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const float cs = a.SC[g % a.S];
+  float ax[NA], ay[NA], ta[NA], at[NA], acc[NA];
+  int id[NA], idx[NA], n[NA];
+#pragma unroll
+  for (int q = 0; q < NA; ++q) {                 // the same records on every lane
+    const AnchorRec r = arec[k0 + q];
+    ax[q] = r.x;
+    ay[q] = r.y;
+    ta[q] = r.t;
+    at[q] = r.t - cs;
+    id[q] = r.id;
+    idx[q] = r.idx;
+    acc[q] = 0.f;
+    n[q] = 0;
   }
-  float acc = 0.f;
-  int n = 0;
-  walk_group(v, a, [&](int, float, float, float, float k) {
-    acc += k;
-    ++n;
-  });
-  group_sum(acc, n);
-  if (on && (threadIdx.x & (kGroup - 1)) == 0) {
-    out[idx] = acc;
-    if (count) count[idx] = n;
+  const Rows3 r = row_ranges(a.CS, a.E, g, cy > 0 ? cy - 1 : 0, cy + 1 < a.GH ? cy + 1 : a.GH - 1,
+                             cx > 0 ? cx - 1 : 0, cx + 1 < a.GW ? cx + 1 : a.GW - 1, a.GH, a.GW);
+  const int last = (int)a.E - 1;                 // E >= 1 (the host handles an empty plan)
+  for (int base = 0; base < r.c3; base += kWave) {
+    const int p = base + lane;
+    const bool live = p < r.c3;
+    int k = list_pos(live ? p : 0, r);
+    k = k < last ? k : last;
+    const int sid = ldr((const int*)a.SID, 2u * (uint32_t)k);
+    const float st = ldr(a.ST, k);
+    const float2 sy = ldr(a.SY, k), sv = ldr(a.SV, k);
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+      const float dt = ta[q] - st;
+      const float rx = ax[q] - (sy.x + sv.x * at[q]);
+      const float ry = ay[q] - (sy.y + sv.y * at[q]);
+      const float d2 = rx * rx + ry * ry;
+      if (live && pair_hit(sid, id[q], dt, d2, a)) {
+        acc[q] += gauss(d2, a.kexp);
+        ++n[q];
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NA; ++q) {
+    acc[q] = wave_sum(acc[q]);
+    n[q] = wave_sum(n[q]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+      out[idx[q]] = acc[q];
+      if (count) count[idx[q]] = n[q];
+    }
+  }
+}
+
+// Items per cell: ceil(its binned anchors / kCellAnchors).
+__global__ void __launch_bounds__(kBlock) k_cell_items(const int64_t* __restrict__ astart, int64_t ncell,
+                                                       int* __restrict__ icnt) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= ncell) return;
+  icnt[c] = (int)((astart[c + 1] - astart[c] + kCellAnchors - 1) / kCellAnchors);
+}
+
+__global__ void __launch_bounds__(kBlock) k_cell_expand(const int* __restrict__ icnt,
+                                                        const int64_t* __restrict__ istart, int64_t ncell,
+                                                        int2* __restrict__ items) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= ncell) return;
+  const int nn = icnt[c];
+  const int64_t base = istart[c];
+  for (int i = 0; i < nn; ++i) items[base + i] = make_int2((int)c, i * kCellAnchors);
+}
+
+// nitems_ptr: the item count (read on the device); the grid covers an upper bound of it.
+__global__ void __launch_bounds__(kWalkBlock) k_pair_fwd_cell(PairRef a, const int64_t* __restrict__ astart,
+                                                              const AnchorRec* __restrict__ arec,
+                                                              const int2* __restrict__ items,
+                                                              const int64_t* __restrict__ nitems_ptr,
+                                                              float* __restrict__ out, int* __restrict__ count) {
+  const int64_t it = ((int64_t)blockIdx.x * kWalkBlock + threadIdx.x) / kWave;
+  if (it >= *nitems_ptr) return;                 // per wave: no block barriers
+  const int2 item = items[it];
+  const int64_t c = item.x;
+  const int64_t k0 = astart[c] + item.y;
+  const int64_t left = astart[c + 1] - k0;
+  const int na = (int)(left < kCellAnchors ? left : kCellAnchors);
+  const int64_t rowid = c / a.GW;
+  const int cx = (int)(c - rowid * a.GW);
+  const int g = (int)(rowid / a.GH), cy = (int)(rowid - (int64_t)g * a.GH);
+  switch (na) {
+    case 1: fwd_cell<1>(a, arec, k0, g, cx, cy, out, count); break;
+    case 2: fwd_cell<2>(a, arec, k0, g, cx, cy, out, count); break;
+    case 3: fwd_cell<3>(a, arec, k0, g, cx, cy, out, count); break;
+    default: fwd_cell<4>(a, arec, k0, g, cx, cy, out, count); break;
   }
 }
 
@@ -1036,7 +1105,10 @@ struct PairWs {
   int64_t* ustart;
   int64_t* uwork;
   int2* items;
-  int64_t units, nseg, max_items, bytes;
+  int64_t* fstart;             // the forward's items per cell: CSR starts (ncell + 1), scan totals, the items
+  int64_t* fwork;
+  int2* fitems;
+  int64_t units, nseg, max_items, max_fitems, bytes;
 };
 
 PairWs pair_ws_layout(void* base, int64_t E, int64_t ncell, int64_t M, int64_t GW) {
@@ -1059,6 +1131,10 @@ PairWs pair_ws_layout(void* base, int64_t E, int64_t ncell, int64_t M, int64_t G
   w.ustart = (int64_t*)take(8 * (w.units + 1));
   w.uwork = (int64_t*)take(8 * atl_scan_work_size(w.units));
   w.items = (int2*)take(8 * w.max_items);
+  w.max_fitems = M / kCellAnchors + (ncell < M ? ncell : M) + 1;
+  w.fstart = (int64_t*)take(8 * (ncell + 1));
+  w.fwork = (int64_t*)take(8 * atl_scan_work_size(ncell));
+  w.fitems = (int2*)take(8 * w.max_fitems);
   w.bytes = off;
   return w;
 }
@@ -1205,8 +1281,20 @@ int atl_ats_pair_fwd_ws(const float* src_y, const float* src_v, const float* src
   const PairRef a = make_ref(src_y, src_v, src_t, src_id, cell_start, E, ncell, anc_x, anc_t, anc_cell, anc_id,
                              slice_c, S, GH, GW, h, tau, cut, 0);
   if (bin_anchors(a, M, ncell, nullptr, w, stream)) return 1;
-  hipLaunchKernelGGL(k_pair_fwd_binned, dim3(grid_for(M, kWalkBlock / kGroup)), dim3(kWalkBlock), 0, stream, a,
-                     (const AnchorRec*)w.arec, (const int64_t*)(w.start + ncell), out, count);
+  // items of up to kCellAnchors anchors of one cell (the per-cell counts reuse cnt, zero after the binning)
+  hipLaunchKernelGGL(k_cell_items, dim3(grid_for(ncell)), dim3(kBlock), 0, stream, (const int64_t*)w.start, ncell,
+                     w.cnt);
+  if (atl_scan_counts(w.cnt, ncell, w.fstart, w.fwork, stream)) return 1;
+  hipLaunchKernelGGL(k_cell_expand, dim3(grid_for(ncell)), dim3(kBlock), 0, stream, (const int*)w.cnt,
+                     (const int64_t*)w.fstart, ncell, w.fitems);
+  const int64_t blocks = (w.max_fitems + kWalkBlock / kWave - 1) / (kWalkBlock / kWave);
+  if (blocks > 0x7fffffff) {
+    set_error("ats_pair_fwd_ws: %lld anchors too many", (long long)M);
+    return 1;
+  }
+  hipLaunchKernelGGL(k_pair_fwd_cell, dim3((unsigned)blocks), dim3(kWalkBlock), 0, stream, a,
+                     (const int64_t*)w.start, (const AnchorRec*)w.arec, (const int2*)w.fitems,
+                     (const int64_t*)(w.fstart + ncell), out, count);
   return check_launch("ats_pair_fwd_ws");
 }
 
