@@ -654,7 +654,6 @@ k_pair_bwd_gather(PairRef a, const int64_t* __restrict__ astart, const AnchorRec
   b0 = b0 < 0 ? 0 : b0;                               // the clamps of k_unit_chunks
   e1 = e1 > a.E ? a.E : e1;
   const int64_t e0 = b0 + (int64_t)item.y * kWave;    // item.y < the unit's chunk count, so e0 < e1
-  const Rows3 r = unit_anchors(q, astart, Mlist, a);
   const float cs = a.SC[q.g % a.S];
   const bool live = e0 + lane < e1;
   const int k = (int)(live ? e0 + lane : e1 - 1);
@@ -663,6 +662,14 @@ k_pair_bwd_gather(PairRef a, const int64_t* __restrict__ astart, const AnchorRec
   const float2 sy = ldr(a.SY, k), sv = ldr(a.SV, k);
   int ce = (int)q.cx0;                                 // the record's cell column
   for (int64_t c = q.cx0 + 1; c < q.cx1; ++c) ce = k >= a.CS[q.rowid * a.GW + c] ? (int)c : ce;
+  // the chunk's records are in cell order: its first and last lanes bound its columns, and only the anchors of
+  // the columns one beside them can pair with it (a dense unit's chunks cover one or two of its cells)
+  const int nlive = e1 - e0 < kWave ? (int)(e1 - e0) : kWave;
+  const int ca = __shfl(ce, 0), cb = __shfl(ce, nlive - 1);
+  UnitGeo qa = q;
+  qa.cx0 = ca;
+  qa.cx1 = cb + 1;
+  const Rows3 r = unit_anchors(qa, astart, Mlist, a);
   float gx = 0.f, gy = 0.f;
   bool any = false;
   for (int pb = 0; pb < r.c3; pb += kWave) {
