@@ -45,3 +45,26 @@ def test_abi_version_and_error_path(lib):
     assert rc == 1 and b"bad sizes" in L.atl_last_error()
     rc = L.atl_ats_pair_fwd(*([None] * 5), 0, 7, *([None] * 4), 0, None, 16, 3, 4, 1.0, 0.2, 3.0, None, None, None)
     assert rc == 1 and b"ats_pair_fwd" in L.atl_last_error()
+
+
+def test_workspace_and_trajectory_entries_reject_before_launch(lib):
+    """The reference-layout workspace entries and the trajectory origin entries check their arguments and
+    workspace on the host and return status 1 with a message, without a launch (no device is touched)."""
+    import ctypes
+    from x_amd.ops import _ext
+    L = _ext.load_library()
+    assert L.atl_ats_pair_ws_bytes(-1, 10, 10, 4) == -1
+    need = L.atl_ats_pair_ws_bytes(100, 48, 10, 4)
+    assert need > 0
+    fake = ctypes.c_void_p(256)                    # an aligned, never dereferenced address
+    args = (*([None] * 5), 100, 48, *([None] * 4), 10, None, 4, 3, 4, 1.0, 0.2, 3.0)
+    rc = L.atl_ats_pair_fwd_ws(*args, None, None, fake, need - 1, None)
+    assert rc == 1 and b"workspace" in L.atl_last_error()
+    rc = L.atl_ats_pair_bwd_ws(None, *args, 10, None, fake, need - 1, None)
+    assert rc == 1 and b"workspace" in L.atl_last_error()
+    rc = L.atl_ats_pair_fwd_ws(*(args[:6] + (47,) + args[7:]), None, None, fake, need, None)  # ncell % (GH GW)
+    assert rc == 1 and b"bad arguments" in L.atl_last_error()
+    rc = L.atl_traj_origin(None, 1, 6, 4, 8, 8, None, None, None, 5, 6, 0.0, 1, 2, None, 0, None, None)
+    assert rc == 1 and b"expected 2K" in L.atl_last_error()
+    rc = L.atl_traj_origin_bwd(None, 1, 8, 4, 8, 8, None, None, None, 5, 0, 1, None, None, None, None)
+    assert rc == 1 and b"traj_origin_bwd" in L.atl_last_error()
