@@ -28,6 +28,7 @@
 // backward gives each source one lane that walks the anchors of all its slices: the gradient of a source
 // is complete in registers and written once, without atomics.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "scan.h"
@@ -50,7 +51,10 @@ constexpr int kSortBlock = 512;                    // pass-2 workgroup
 constexpr int kP1Block = 1024;                     // pass-1 workgroup
 constexpr int kSrcPerBlock = 4096;                 // pass-1 sources per block (4 per thread)
 constexpr int kAncPerBlock = 8192;                 // pass-1 anchors per block (8 per thread)
-constexpr int kUnroll = 4;                         // candidates per walk step (record arrays padded by this)
+constexpr int kUnroll = 8;                         // record arrays padded by the longest walk step
+constexpr int kStep = 4;                           // candidates per walk step
+constexpr int kStepLong = 8;                       // the step of a wave whose walks are long (dense neighbourhoods)
+constexpr int kLongWalk = 256;                     // a lane's slice candidates above which its wave steps long
 constexpr int kSliceBatch = 4;                     // pass 1: slices of one source keyed and placed together
 
 constexpr int kXcd = 8;                            // XCDs: consecutive workgroups go round-robin over them
@@ -930,9 +934,12 @@ __device__ __forceinline__ float rdlanef(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-// Per-lane walk of the R-neighbourhood of (qx, qy) in plane `plane`: visit(k, e) for kUnroll consecutive
-// candidates [k, k + kUnroll) of a row ending at e (positions past e are padded records, masked by the
-// caller).  cstart offsets minus `base`.
+// Per-lane walk of the R-neighbourhood of (qx, qy) in plane `plane`: visit(k, e, Step<U>) for U consecutive
+// candidates [k, k + U) of a row ending at e (positions past e are padded records, masked by the caller; U is at
+// most kUnroll).  cstart offsets minus `base`.
+template <int U>
+using Step = std::integral_constant<int, U>;
+
 template <typename Visit>
 __device__ __forceinline__ void walk(const int* __restrict__ cstart, int base, int plane, float qx, float qy, float R,
                                      float R2, const FGeo& G, Visit&& visit) {
@@ -942,7 +949,7 @@ __device__ __forceinline__ void walk(const int* __restrict__ cstart, int base, i
     if (!row_span(r, qx, qy, R, R2, G, c0, c1)) continue;
     const int rowk = plane + r * G.GW;
     const int e = cstart[rowk + c1 + 1] - base;
-    for (int k = cstart[rowk + c0] - base; k < e; k += kUnroll) visit(k, e);
+    for (int k = cstart[rowk + c0] - base; k < e; k += kStep) visit(k, e, Step<kStep>{});
   }
 }
 
@@ -952,7 +959,9 @@ __device__ __forceinline__ void walk(const int* __restrict__ cstart, int base, i
 // in lockstep leaves most lanes idle).  Taller neighbourhoods take the row-by-row walk.
 constexpr int kRowTab = 8;
 
-template <typename Visit>
+// ADAPT: a wave in which some lane's neighbourhood holds more than kLongWalk candidates takes steps of kStepLong
+// (more loads in flight per lane on long walks; short walks keep kStep, which leaves fewer lanes masked).
+template <bool ADAPT = false, typename Visit>
 __device__ __forceinline__ void walk_flat(const int* __restrict__ cstart, int base, int plane, float qx, float qy,
                                           float R, float R2, const FGeo& G, int2* tab, Visit&& visit) {
   const int rlo = cell_walk(qy - R, G.gy0, G.gy1, G.icf, G.GH), rhi = cell_walk(qy + R, G.gy0, G.gy1, G.icf, G.GH);
@@ -975,21 +984,35 @@ __device__ __forceinline__ void walk_flat(const int* __restrict__ cstart, int ba
   }
 #pragma unroll
   for (int i = 0; i < kRowTab; ++i) tab[i * kPairBlock] = make_int2(kk[i] - base, ee[i] - base);
-  int ri = 0;                                      // row of cur; nxt holds row ri + 1 (read one row ahead)
-  int2 cur = make_int2(kk[0] - base, ee[0] - base);
-  int2 nxt = make_int2(kk[1] - base, ee[1] - base);
-  while (true) {
-    if (cur.x >= cur.y) {
-      do {
-        cur = nxt;
-        ++ri;
-        nxt = ri + 1 < nrows ? tab[(ri + 1) * kPairBlock] : make_int2(0, 0);
-      } while (cur.x >= cur.y && ri < nrows - 1);
-      if (cur.x >= cur.y) break;
+  auto steps = [&](auto step) {
+    constexpr int U = decltype(step)::value;
+    int ri = 0;                                    // row of cur; nxt holds row ri + 1 (read one row ahead)
+    int2 cur = make_int2(kk[0] - base, ee[0] - base);
+    int2 nxt = make_int2(kk[1] - base, ee[1] - base);
+    while (true) {
+      if (cur.x >= cur.y) {
+        do {
+          cur = nxt;
+          ++ri;
+          nxt = ri + 1 < nrows ? tab[(ri + 1) * kPairBlock] : make_int2(0, 0);
+        } while (cur.x >= cur.y && ri < nrows - 1);
+        if (cur.x >= cur.y) break;
+      }
+      visit(cur.x, cur.y, step);
+      cur.x += U;
     }
-    visit(cur.x, cur.y);
-    cur.x += kUnroll;
+  };
+  bool lng = false;
+  if (ADAPT) {
+    int tot = 0;
+#pragma unroll
+    for (int i = 0; i < kRowTab; ++i) tot += ee[i] - kk[i];
+    lng = __any(tot > kLongWalk);                  // uniform over the wave's walking lanes
   }
+  if (lng)
+    steps(Step<kStepLong>{});
+  else
+    steps(Step<kStep>{});
 }
 
 // Group walk: the candidates of the cells of plane `plane` that meet the R-neighbourhood of the box
@@ -1288,18 +1311,19 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
   float mgx = 0.f, mgy = 0.f;
   float4 sv;                                       // the current slice's entry (y, v) and centre
   float cs;
-  auto visit = [&](int k, int e) {
-    float4 A[kUnroll];
-    int id[kUnroll];
-    // one lane offset for the kUnroll loads, the step within the record run folded into the (scalar) base
+  auto visit = [&](int k, int e, auto step) {
+    constexpr int U = decltype(step)::value;
+    float4 A[U];
+    int id[U];
+    // one lane offset for the U loads, the step within the record run folded into the (scalar) base
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       A[u] = ld((const float4*)p.brec + u, (uint32_t)k);
       if (LOO == kLooId) id[u] = ld(aid + 8 * u, 8u * (uint32_t)k);
     }
     const int rem = e - k, self_u = sp - k;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const float at = A[u].z - cs;
       const float dt = A[u].z - tj;
       const float rx = A[u].x - (sv.x + sv.z * at);
@@ -1329,7 +1353,7 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
   for (int s = lo_l; s <= hi_l; ++s) {
     entry(s, sv, cs);
     const float qx = clampf(sv.x, G.gx0, G.gx1), qy = clampf(sv.y, G.gy0, G.gy1);
-    walk_flat(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, tab, visit);
+    walk_flat<true>(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, tab, visit);
   }
   return make_float2(mgx, mgy);
 }
@@ -1638,17 +1662,18 @@ __device__ __forceinline__ void bwd_traj_source(const FPlan& p, const FGeo& G, f
     const float cs = slice_centre(s, G.delta);
     const float qx = clampf(yx, G.gx0, G.gx1), qy = clampf(yy, G.gy0, G.gy1);
     float gyx = 0.f, gyy = 0.f, gvx = 0.f, gvy = 0.f;
-    walk_flat(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, rowtab, [&](int k, int e) {
-      float4 A[kUnroll];
-      int id[kUnroll];
+    walk_flat(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, rowtab, [&](int k, int e, auto step) {
+      constexpr int U = decltype(step)::value;
+      float4 A[U];
+      int id[U];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < U; ++u) {
         A[u] = ld((const float4*)p.brec + u, (uint32_t)k);
         if (DUP) id[u] = ld(aid + 8 * u, 8u * (uint32_t)k);
       }
       const int rem = e - k, self_u = sp - k;
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < U; ++u) {
         const float at = A[u].z - cs;
         const float dt = A[u].z - tj;
         const float rx = A[u].x - (yx + vx * at);
