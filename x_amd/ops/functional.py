@@ -864,9 +864,9 @@ def ats_pair_sums(x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, fo
 def ats_pair_sums_reference_layout(x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, anchor_xy=None):
     """The call pattern of the reference's unchanged ats_pair_sums (atl/ops/functional.py:199-207) on this
     library: the reference's plan layout built on the device (build_pair_plan, bit-exact with the reference's),
-    then the pybind-surface entry points ats_pair_fwd / ats_pair_bwd (one thread per anchor over 3 x 3 cells,
-    two global atomics per pair in the backward).  Same values as ats_pair_sums; kept to measure what a caller
-    gets without switching to the fused path."""
+    then the pybind-surface ops ats_pair_fwd / ats_pair_bwd through their workspace entries (anchors binned by
+    cell; the forward one wave per cell item, the backward source-centric without per-pair atomics).  Same values
+    as ats_pair_sums; kept to measure what a caller gets without switching to the fused path."""
     if anchors is None:
         anchors = torch.arange(x.shape[0], device=x.device)
     plan = build_pair_plan(x.detach(), t, v.detach(), b, B, H, W, anchors, h, tau, cut, n_slices,
