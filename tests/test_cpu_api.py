@@ -128,3 +128,26 @@ def test_cpu_mpcm_loss_runs_and_backprops():
     out = MotionPriorCMaxLoss(num_knn=8, t_ref=0.3)(ev, PixelTrajectories(g, K=1))
     out["loss"].backward()
     assert torch.isfinite(out["loss"]) and g.grad is not None and float(g.grad.abs().sum()) > 0
+
+
+def test_cpu_voxel_grid_normalisations():
+    """voxel_grid's normalisations (atl/ops/functional.py:229-237): "mean_std" gives each batch entry's non-zero
+    voxels mean 0 and sample standard deviation 1 (float64 check) and leaves zeros at zero; an entry with one
+    non-zero voxel keeps it minus its mean (0); "max" divides each entry by its largest magnitude."""
+    pos, _, b, t = rand_events(n=800, B=3, seed=11)
+    p = np.where(np.random.default_rng(12).random(800) < 0.5, 1.0, -1.0).astype(F32)
+    b[b == 2] = 1                                            # entry 2: empty but for one event
+    b[-1] = 2
+    pos[-1] = (5.0, 6.0)
+    t[-1] = 0.0
+    args = [torch.from_numpy(a) for a in (pos, t, p, b)]
+    raw = F.voxel_grid(*args, 3, 5, 20, 24, normalize=None).numpy().astype(np.float64)
+    got = F.voxel_grid(*args, 3, 5, 20, 24).numpy()
+    for k in range(2):
+        nz = raw[k] != 0
+        want = (raw[k][nz] - raw[k][nz].mean()) / raw[k][nz].std(ddof=1)
+        assert np.allclose(got[k][nz], want, atol=1e-5) and np.all(got[k][~nz] == 0)
+    assert (raw[2] != 0).sum() == 1 and np.all(got[2] == 0)
+    mx = F.voxel_grid(*args, 3, 5, 20, 24, normalize="max").numpy()
+    for k in range(3):
+        assert np.allclose(mx[k], raw[k] / np.abs(raw[k]).max(), atol=1e-6)

@@ -454,6 +454,157 @@ def test_traj_fp32_plan_and_pair_loops_match_fp64():
     assert np.abs(gp - wp).max() <= 1e-4 * np.abs(wp).max() and np.abs(gc - wc).max() <= 1e-4 * np.abs(wc).max()
 
 
+@pytest.mark.parametrize("tau,S,h", [(0.2, 16, 1.0), (1.0, 8, 1.5), (0.05, 4, 0.7)])
+def test_torch_plan_equals_numpy_plan(tau, S, h):
+    """build_pair_plan_torch (the reference's torch CPU op sequence, which the CPU baseline times) and the NumPy
+    restatement give the same plan bit for bit: geometry, keys, cell offsets, entries (id, position, velocity,
+    time) and anchor cells."""
+    if torch.backends.cpu.get_cpu_capability() == "DEFAULT":
+        pytest.skip("torch CPU kernels without FMA: a different rounding of the norm")
+    win, v = _dense_case(seed=20 + S)
+    rng = np.random.default_rng(S)
+    anchors = np.sort(rng.permutation(win.n)[: win.n // 2])
+    xa = (win.xy[anchors] + h * rng.standard_normal((len(anchors), 2))).astype(F32)
+    for axy in (None, xa):
+        p = O.build_pair_plan(win.xy, win.t, v, win.b, 2, 40, 48, anchors, h, tau, 3.0, S, anchor_xy=axy)
+        q = O.build_pair_plan_torch(win.xy, win.t, v, win.b, 2, 40, 48, anchors, h, tau, 3.0, S, anchor_xy=axy)
+        assert p["geometry"] == q["geometry"] and (p["GH"], p["GW"], p["S"]) == (q["GH"], q["GW"], q["S"])
+        for f in ("key", "cell_start", "src_id", "src_y", "src_v", "src_t", "anc_x", "anc_t", "anc_cell", "anc_id",
+                  "slice_c"):
+            assert p[f].dtype == q[f].dtype and np.array_equal(p[f], q[f]), f
+        assert p["key"].shape[0] > len(win.t)
+
+
+def _linear_coeff_field(rng, K, Hg, Wg, slope):
+    """A (1, 2K, Hg, Wg) coefficient field linear in the node position, c(p) = a + Bx px + By py per channel
+    (bilinear interpolation reproduces it exactly inside the grid), and its float64 parameters."""
+    a = rng.standard_normal(2 * K) * 2.0
+    bx, by = rng.standard_normal(2 * K) * slope, rng.standard_normal(2 * K) * slope
+    yy, xx = np.meshgrid(np.arange(Hg, dtype=np.float64), np.arange(Wg, dtype=np.float64), indexing="ij")
+    fld = (a[:, None, None] + bx[:, None, None] * xx + by[:, None, None] * yy)[None].astype(F32)
+    return fld, a, bx, by
+
+
+def test_traj_displacement_closed_forms():
+    """traj_displacement: (1) K = 2 B-splines are the quadratic Bernstein pair 2t(1 - t), t^2, so on a field linear
+    in the position d_x = c_x1(p) 2t(1 - t) + c_x2(p) t^2 (x channels after the y channels); (2) control points
+    v xi_k at the Greville abscissae give d = v t for K = 10 (linear precision); (3) positions outside the grid
+    take the border node's coefficients."""
+    rng = np.random.default_rng(40)
+    Hg, Wg, n = 12, 16, 400
+    fld, a, bx, by = _linear_coeff_field(rng, 2, Hg, Wg, 0.3)
+    p = np.stack([rng.uniform(0, Wg - 1, n), rng.uniform(0, Hg - 1, n)], 1).astype(F32)
+    t = rng.uniform(0, 1, n).astype(F32)
+    b = np.zeros(n, np.int64)
+    d, _, _, _ = O.traj_displacement(fld, p, t, b, 2, "bspline")
+    pd, td = p.astype(np.float64), t.astype(np.float64)
+    c = a[None] + bx[None] * pd[:, :1] + by[None] * pd[:, 1:]         # (n, 4): y1, y2, x1, x2
+    g1, g2 = 2 * td * (1 - td), td * td
+    want = np.stack([c[:, 2] * g1 + c[:, 3] * g2, c[:, 0] * g1 + c[:, 1] * g2], 1)
+    assert np.abs(d - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+    from x_amd.motion.trajectories import greville
+    K = 10
+    v = np.array([3.5, -2.25])
+    xi = greville(K)
+    uni = np.concatenate([v[1] * xi, v[0] * xi]).astype(F32)[None, :, None, None] * np.ones((1, 1, Hg, Wg), F32)
+    d, rows, _, _ = O.traj_displacement(uni, p, t, b, K, "bspline")
+    assert np.abs(d - td[:, None] * v[None]).max() <= 2e-6 * np.abs(v).max()
+    far = np.array([[-5.0, -3.0], [Wg + 7.0, Hg + 2.0]], F32)
+    _, rows, _, _ = O.traj_displacement(fld, far, np.full(2, 0.5, F32), np.zeros(2, np.int64), 2, "bspline")
+    assert np.array_equal(rows[0], fld[0, :, 0, 0]) and np.array_equal(rows[1], fld[0, :, -1, -1])
+
+
+def test_traj_origin_solves_the_inversion():
+    """traj_origin: on uniform straight trajectories p = xy - v t; on a coefficient field linear in the position
+    d(p, t) = a(t) + M(t) p, so the start solves (I + M(t)) p = xy - a(t), a 2 x 2 system per event solved in
+    float64 (the Picard steps contract by |M| <= 0.05, six of them leave < 1e-7 px)."""
+    from x_amd.motion.trajectories import greville
+    rng = np.random.default_rng(41)
+    Hg, Wg, n, K = 40, 48, 500, 10
+    xy = np.stack([rng.uniform(8, Wg - 9, n), rng.uniform(8, Hg - 9, n)], 1).astype(F32)
+    t = rng.uniform(0, 1, n).astype(F32)
+    b = np.zeros(n, np.int64)
+    v = np.array([-2.0, 4.5])
+    xi = greville(K)
+    uni = np.concatenate([v[1] * xi, v[0] * xi]).astype(F32)[None, :, None, None] * np.ones((1, 1, Hg, Wg), F32)
+    p = O.traj_origin(uni, xy, t, b, K, "bspline")
+    assert np.abs(p - (xy - t[:, None].astype(np.float64) * v)).max() <= 1e-5
+    fld, a, bx, by = _linear_coeff_field(rng, K, Hg, Wg, 0.004)
+    p = O.traj_origin(fld, xy, t, b, K, "bspline")
+    g, _ = O.traj_basis_table(t.astype(np.float64), K, "bspline")      # (n, K)
+    ax, ay = g @ a[K:], g @ a[:K]                                         # a(t): x from the x channels
+    mxx, mxy, myx, myy = g @ bx[K:], g @ by[K:], g @ bx[:K], g @ by[:K]
+    assert max(np.abs(mxx).max(), np.abs(mxy).max(), np.abs(myx).max(), np.abs(myy).max()) < 0.05
+    rx, ry = xy[:, 0] - ax, xy[:, 1] - ay
+    det = (1 + mxx) * (1 + myy) - mxy * myx
+    want = np.stack([((1 + myy) * rx - mxy * ry) / det, ((1 + mxx) * ry - myx * rx) / det], 1)
+    assert np.abs(p - want).max() <= 2e-5
+
+
+def test_traj_visible_fraction_closed_forms():
+    """traj_visible_fraction: (1) straight uniform trajectories of velocity v give the translation's closed form
+    (the anchor seen at xa + v (c_k - ta)); (2) on a field linear in the position, the starts from the float64
+    2 x 2 solve and the positions p + a(c_k) + M(c_k) p in float64 give the same weighted shares (anchors whose
+    positions come within 1e-3 px of the sensor edge are left out: fp32 may put them either side)."""
+    from x_amd.motion.trajectories import greville
+    rng = np.random.default_rng(42)
+    H, W, M, K, tau = 30, 40, 500, 10, 0.3
+    xa = np.stack([rng.uniform(-5, W + 5, M), rng.uniform(-3, H + 3, M)], 1).astype(F32)
+    ta = rng.uniform(0, 1, M).astype(F32)
+    ba = np.zeros(M, np.int64)
+    t_all = np.sort(rng.uniform(0, 1, 5000)).astype(F32)
+    b_all = np.zeros(5000, np.int64)
+    counts = np.bincount(np.clip((t_all * 16).astype(int), 0, 15), minlength=16).astype(np.float64)
+    c = (np.arange(16) + 0.5) / 16
+
+    def shares(pos_at):                       # pos_at(k) -> (M, 2) float64 positions at centre k
+        vis, tot = np.zeros(M), np.zeros(M)
+        for k in range(16):
+            y = pos_at(k)
+            ins = (y[:, 0] >= 0) & (y[:, 0] <= W - 1) & (y[:, 1] >= 0) & (y[:, 1] <= H - 1)
+            wgt = counts[k] * (np.abs(ta.astype(np.float64) - c[k]) <= tau)
+            vis += wgt * ins
+            tot += wgt
+        return np.maximum(vis / np.maximum(tot, 1), 1e-3)
+
+    def edge_clear(pos_at):
+        ok = np.ones(M, bool)
+        for k in range(16):
+            y = pos_at(k)
+            for col, hi in ((0, W - 1), (1, H - 1)):
+                ok &= (np.abs(y[:, col]) > 1e-3) & (np.abs(y[:, col] - hi) > 1e-3)
+        return ok
+
+    v = np.array([9.0, -4.0])
+    xi = greville(K)
+    uni = np.concatenate([v[1] * xi, v[0] * xi]).astype(F32)[None, :, None, None] * np.ones((1, 1, H, W), F32)
+    got = O.traj_visible_fraction(uni, xa, ta, ba, t_all, b_all, 1, H, W, tau, K, "bspline")
+    at = lambda k: xa.astype(np.float64) + v * (c[k] - ta.astype(np.float64))[:, None]
+    ok = edge_clear(at)
+    assert ok.mean() > 0.95 and np.allclose(got[ok], shares(at)[ok], atol=1e-6)
+    # a coefficient grid twice the sensor's size, so that starts stay inside it while anchors cross the sensor edge
+    fld, a, bx, by = _linear_coeff_field(rng, K, 2 * H, 2 * W, 0.004)
+    xa = np.stack([rng.uniform(8, 2 * W - 9, M), rng.uniform(8, 2 * H - 9, M)], 1).astype(F32)
+    g, _ = O.traj_basis_table(ta.astype(np.float64), K, "bspline")
+    rx, ry = xa[:, 0] - g @ a[K:], xa[:, 1] - g @ a[:K]
+    mxx, mxy, myx, myy = g @ bx[K:], g @ by[K:], g @ bx[:K], g @ by[:K]
+    det = (1 + mxx) * (1 + myy) - mxy * myx
+    p = np.stack([((1 + myy) * rx - mxy * ry) / det, ((1 + mxx) * ry - myx * rx) / det], 1)
+    gc, _ = O.traj_basis_table(c, K, "bspline")
+
+    def at_lin(k):
+        gk = gc[k]
+        cx = gk @ a[K:] + (gk @ bx[K:]) * p[:, 0] + (gk @ by[K:]) * p[:, 1]
+        cy = gk @ a[:K] + (gk @ bx[:K]) * p[:, 0] + (gk @ by[:K]) * p[:, 1]
+        return p + np.stack([cx, cy], 1)
+
+    got = O.traj_visible_fraction(fld, xa, ta, ba, t_all, b_all, 1, H, W, tau, K, "bspline")
+    ok = edge_clear(at_lin)
+    want = shares(at_lin)
+    assert ok.sum() > 100 and np.allclose(got[ok], want[ok], atol=1e-6)
+    assert (want[ok] < 1).sum() > 20                   # the case has anchors that leave the sensor
+
+
 def test_blur_impulse_response_and_mass():
     """The oracle's blur: an impulse far from the border becomes the outer product of the normalised taps (mass
     1); an image at the border loses exactly the mass that falls outside (zero padding)."""

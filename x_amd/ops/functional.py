@@ -616,44 +616,63 @@ def _build_pair_plan_hip(x, t, v, b, B, H, W, anchors, h, tau, cut, n_slices, an
                     geo)
 
 
+def _slice_span(t: torch.Tensor, tau: float, S: int):
+    """First and last slice whose centre lies within tau + delta/2 of each event time (delta = 1/S), clamped to
+    [0, S-1]: fp32 in the order (t -/+ tau -/+ delta/2) / delta - 1/2 (atl/ops/functional.py:151-152)."""
+    d = 1.0 / S
+    lo = torch.ceil((t - tau - d / 2) / d - 0.5)
+    hi = torch.floor((t + tau + d / 2) / d - 0.5)
+    return lo.clamp(0, S - 1).long(), hi.clamp(0, S - 1).long()
+
+
+def _cell_index(p: torch.Tensor, ox: float, oy: float, cell: float):
+    """Integer cell column and row of positions p (N, 2): floor((p - o) / cell) in fp32."""
+    return torch.floor((p[:, 0] - ox) / cell).long(), torch.floor((p[:, 1] - oy) / cell).long()
+
+
 def _build_pair_plan_torch(x, t, v, b, B, H, W, anchors, h, tau, cut, n_slices, anchor_xy):
-    """CPU tensors: the plan from torch ops, same arithmetic as atl/ops/functional.py:132-178."""
-    dev = x.device
+    """CPU tensors: the plan of atl/ops/functional.py:132-178 built one slice at a time.  For slice s the
+    sources whose slice span holds s are transported to the slice centre c_s, y = x + v (c_s - t) (fp32: one
+    subtraction, one product, one sum, the reference's rounding), binned, and keyed by (batch, slice, row,
+    column).  The slices' entries are then put in key order by one stable sort, which leaves the entries of a
+    cell in source order, the order the reference's stable sort of its (source, slice) list gives.  Cell offsets
+    are the positions of the cell numbers in the sorted keys."""
     S = int(n_slices)
-    delta = 1.0 / S
     with torch.no_grad():
-        vd = v.detach().float()
-        vmax = float(vd.norm(dim=1).max()) if vd.numel() else 0.0
-        xa = (x[anchors] if anchor_xy is None else anchor_xy).float()
-        bbox = (float(xa[:, 0].min()), float(xa[:, 1].min()), float(xa[:, 0].max()), float(xa[:, 1].max())) \
-            if xa.numel() else (0.0, 0.0, 0.0, 0.0)
-        geo = plan_geometry(vmax, bbox, xa.shape[0], h, tau, cut, S, W, H)
-        GW, GH, cell, ox, oy = geo["GW"], geo["GH"], geo["cell"], geo["ox"], geo["oy"]
-        s_lo = torch.ceil((t - tau - delta / 2) / delta - 0.5).clamp(0, S - 1).long()
-        s_hi = torch.floor((t + tau + delta / 2) / delta - 0.5).clamp(0, S - 1).long()
-        cnt = (s_hi - s_lo + 1).clamp(min=0)
-        rep = torch.repeat_interleave(torch.arange(t.numel(), device=dev), cnt)
-        first = torch.cumsum(cnt, 0) - cnt
-        s = s_lo[rep] + (torch.arange(rep.numel(), device=dev) - first[rep])
-        cs_all = (torch.arange(S, device=dev, dtype=torch.float32) + 0.5) * delta
-        y = x[rep].float() + vd[rep] * (cs_all[s] - t[rep])[:, None]
-        cx = torch.floor((y[:, 0] - ox) / cell).long()
-        cy = torch.floor((y[:, 1] - oy) / cell).long()
-        keep = (cx >= 0) & (cx < GW) & (cy >= 0) & (cy < GH)
-        rep, s, y, cx, cy = rep[keep], s[keep], y[keep], cx[keep], cy[keep]
-        key = ((b[rep] * S + s) * GH + cy) * GW + cx
-        order = torch.argsort(key, stable=True)
-        key, rep, y = key[order], rep[order], y[order]
-        counts = torch.bincount(key, minlength=B * S * GH * GW)
-        cell_start = torch.cat([counts.new_zeros(1), torch.cumsum(counts, 0)]).long()
+        t = t.float()
+        vel = v.detach().float()
+        anc_xy = (x[anchors] if anchor_xy is None else anchor_xy).float()
+        nrm = vel.norm(dim=1)
+        vmax = float(nrm.max()) if nrm.numel() else 0.0
+        box = ((float(anc_xy[:, 0].min()), float(anc_xy[:, 1].min()), float(anc_xy[:, 0].max()),
+                float(anc_xy[:, 1].max())) if anc_xy.numel() else (0.0, 0.0, 0.0, 0.0))
+        geo = plan_geometry(vmax, box, anc_xy.shape[0], h, tau, cut, S, W, H)
+        gw, gh, side, ox, oy = geo["GW"], geo["GH"], geo["cell"], geo["ox"], geo["oy"]
+        centres = (torch.arange(S, dtype=torch.float32) + 0.5) * (1.0 / S)
+        first, last = _slice_span(t, tau, S)
+        ids, keys = [], []
+        for s in range(S):
+            src = torch.nonzero((first <= s) & (s <= last)).flatten()
+            ys = x[src].float() + vel[src] * (centres[s] - t[src])[:, None]
+            col, row = _cell_index(ys, ox, oy, side)
+            inside = (col >= 0) & (col < gw) & (row >= 0) & (row < gh)
+            src, col, row = src[inside], col[inside], row[inside]
+            ids.append(src)
+            keys.append(((b[src] * S + s) * gh + row) * gw + col)
+        key_all = torch.cat(keys) if keys else torch.zeros(0, dtype=I64)
+        id_all = torch.cat(ids) if ids else torch.zeros(0, dtype=I64)
+        key_all, perm = torch.sort(key_all, stable=True)
+        sid = id_all[perm]
+        slc = (key_all // (gh * gw)) % S
+        y = x[sid].float() + vel[sid] * (centres[slc] - t[sid])[:, None]
+        cell_start = torch.searchsorted(key_all, torch.arange(B * S * gh * gw + 1, dtype=I64))
         ta = t[anchors]
-        sa = torch.clamp(torch.floor(ta / delta), 0, S - 1).long()
-        acx = torch.floor((xa[:, 0] - ox) / cell).long().clamp(0, GW - 1)
-        acy = torch.floor((xa[:, 1] - oy) / cell).long().clamp(0, GH - 1)
-        anc_cell = torch.stack([b[anchors] * S + sa, acx, acy], 1).contiguous()
-    return PairPlan(y.contiguous(), vd[rep].contiguous(), t[rep].float().contiguous(), rep.contiguous(), cell_start,
-                    xa.contiguous(), ta.float().contiguous(), anc_cell, anchors.long().contiguous(),
-                    cs_all.contiguous(), S, GH, GW, geo)
+        a_slice = torch.floor(ta / (1.0 / S)).clamp(0, S - 1).long()
+        a_col, a_row = _cell_index(anc_xy, ox, oy, side)
+        anc_cell = torch.stack([b[anchors] * S + a_slice, a_col.clamp(0, gw - 1), a_row.clamp(0, gh - 1)], 1)
+    return PairPlan(y.contiguous(), vel[sid].contiguous(), t[sid].contiguous(), sid.contiguous(), cell_start,
+                    anc_xy.contiguous(), ta.contiguous(), anc_cell.contiguous(), anchors.long().contiguous(),
+                    centres, S, gh, gw, geo)
 
 
 def build_pair_plan(x, t, v, b, B, H, W, anchors, h, tau, cut=3.0, n_slices=16, anchor_xy=None) -> PairPlan:
@@ -1139,6 +1158,17 @@ def anchored_score_mean(S, wc, vis, h, eps):
 
 
 # ------------------------------------------------------------------------------------------- voxel grid
+def _standardise_nonzero(rows: torch.Tensor) -> None:
+    """In place, per row: the non-zero entries minus their mean, divided by their sample standard deviation
+    (n - 1 in the denominator) when it is positive; zero entries stay zero."""
+    nz = rows != 0
+    n = nz.sum(1, keepdim=True)
+    mean = torch.where(nz, rows, 0.0).sum(1, keepdim=True) / n.clamp(min=1)
+    dev = torch.where(nz, rows - mean, 0.0)
+    sd = ((dev * dev).sum(1, keepdim=True) / (n - 1)).sqrt()      # NaN for a single non-zero entry
+    rows.copy_(torch.where(nz, dev / torch.where(sd > 0, sd, 1.0), rows))
+
+
 def voxel_grid(pos, t, p, b, B, C, H, W, normalize: str | None = "mean_std") -> torch.Tensor:
     """Trilinear polarity voxel grid (B, C, H, W), optionally normalised (atl/ops/functional.py:221-238)."""
     with torch.no_grad():
@@ -1147,15 +1177,9 @@ def voxel_grid(pos, t, p, b, B, C, H, W, normalize: str | None = "mean_std") -> 
         else:
             vox = ref.voxel_grid(pos.float(), t.float(), p.float(), b, B, C, H, W)
         if normalize == "mean_std":
-            for k in range(B):
-                vk = vox[k]
-                nz = vk != 0
-                if nz.any():
-                    m, s = vk[nz].mean(), vk[nz].std()
-                    vk[nz] = (vk[nz] - m) / s if s > 0 else vk[nz] - m
+            _standardise_nonzero(vox.view(B, -1))
         elif normalize == "max":
-            mx = vox.abs().amax(dim=(1, 2, 3), keepdim=True).clamp(min=1e-9)
-            vox = vox / mx
+            vox = vox / vox.abs().amax(dim=(1, 2, 3), keepdim=True).clamp(min=1e-9)
     return vox
 
 
