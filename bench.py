@@ -64,6 +64,10 @@ SLOTS_FWD, SLOTS_BWD = 14, 16          # VALU lane-slots per contributing pair (
 SLOTS_BWD_TRAJ = 20                    # trajectory backward: the pair recomputed (13) + k gS (1) + k gS r (2) +
                                        # position and velocity gradient sums (2 adds, 2 FMAs)
 FLOPS_FWD, FLOPS_BWD = 13, 19          # fp32 flops per contributing pair (FMA = 2, exp = 1)
+HBM_PEAK = 8.0e12                      # bytes/s
+# compulsory HBM bytes per event of the anchored step: positions 8, dequantisation 8, smoothing 8, time 4,
+# batch 8 (the flow grid and its gradient are added per call); with the splat leg: + 20 forward + 32 backward
+STEP_BYTES_PER_EVENT, SPLAT_BYTES_PER_EVENT = 36, 52
 KERNEL_OF = {"atl_fast_pair_fwd": "k_fast_fwd<false>", "atl_fast_pair_bwd": "k_fast_bwd", "atl_fast_pair_bwd_src": "k_fast_bwd",
              "atl_fast_pair_bwd_traj": "k_fast_bwd_traj<10>"}
 COUNTERS = ROOT / "profiles" / "anchored_score_1M_640x480_counters.md"
@@ -391,15 +395,18 @@ def iwe_main(a, dev):
     win, ev, motion, desc = iwe_workload(a.workload, dev)
     t_ref = 0.0 if a.workload == "iwe-plumbing" else 0.5
     cfg = IWEConfig(kernel="bilinear", sigma=0.0, mask_border=True)
+    # the loss is the sum of the gathered values; its backward is seeded with its gradient, ones, made once here:
+    # torch's many-block sum clears a semaphore buffer with a memset, which a captured graph must not hold
+    ones = torch.ones(ev.n, device=dev)
 
     def body():
         if a.workload == "iwe-composed":
             y = motion.transport(ev.xy, ev.t, t_ref, ev.b)
             img = make_iwe(ev, y, t_ref, cfg)
-            gather(img, y, ev.b).sum().backward()
+            gather(img, y, ev.b).backward(ones)
         else:
             _, vals = iwe_at_events(ev, motion, t_ref, cfg)
-            vals.sum().backward()
+            vals.backward(ones)
 
     def step():
         for p in motion.parameters():
@@ -487,11 +494,11 @@ def trajectories_main(a, dev):
 
     def step():
         coeff.grad = None
-        # a training step changes the coefficients, so their channels-last copy (kept per field version) is made
-        # again in every timed step rather than reused from the previous one
-        F._CL_CACHE.clear()
-        m = PixelTrajectories(coeff, K, "bspline", tile=1)
-        loss = obj(ev, m)["loss"] - iwe_variance(ev, m, 0.5)
+        # one layout scope per step: the coefficient grid's channels-last copy is made once per step and serves
+        # every look-up of both terms
+        with F.layout_scope():
+            m = PixelTrajectories(coeff, K, "bspline", tile=1)
+            loss = obj(ev, m)["loss"] - iwe_variance(ev, m, 0.5)
         loss.backward()
 
     for _ in range(a.warmup):
@@ -756,12 +763,11 @@ def main():
     def step():
         for prm in motion.parameters():
             prm.grad = None
-        # a training step changes the flow grid, so its interleaved copy (kept per field version) is made again in
-        # every timed step rather than reused from the previous one
-        F._CL_CACHE.clear()
-        loss = obj(ev, motion)["loss"]
-        if blobs:                                  # the splat leg of the contention config: IWE contrast at 0.5
-            loss = loss - iwe_variance(ev, motion, 0.5)
+        # one layout scope per step: the flow's interleaved copy is made once per step
+        with F.layout_scope():
+            loss = obj(ev, motion)["loss"]
+            if blobs:                              # the splat leg of the contention config: IWE contrast at 0.5
+                loss = loss - iwe_variance(ev, motion, 0.5)
         loss.backward()
 
     for _ in range(a.warmup):
@@ -798,6 +804,12 @@ def main():
     achieved = K * slots / (ms[dom] * 1e-3)
     flops = K * (FLOPS_FWD if fwd else FLOPS_BWD) / (ms[dom] * 1e-3)
     value = ev.n * a.steps / dt
+    # whole-step roofline: every contributing pair at its forward + backward slots on the VALU, plus the step's
+    # compulsory bytes at HBM peak (flow grid read and gradient written, twice 2 x 4 x Hg x Wg bytes)
+    hw = ev.height * ev.width
+    step_bytes = ev.n * (STEP_BYTES_PER_EVENT + (SPLAT_BYTES_PER_EVENT if blobs else 0)) + 16 * hw \
+        + (8 * hw if blobs else 0)
+    step_roof_s = K * (SLOTS_FWD + SLOTS_BWD) / VALU_PEAK + step_bytes / HBM_PEAK
     line = {
         "metric": ("events/s for anchored-score fwd+bwd @1M events 640x480; % HBM/VALU roofline"
                    if a.workload == "anchored" else
@@ -819,6 +831,8 @@ def main():
                      "traffic": (recorded_traffic(KERNEL_OF[dom]) if a.workload == "anchored" and a.sigma == 1.0
                                  and ev.n == 1_000_000 else None),
                      "pairs": K, "slots_per_pair": slots, "kernel_ms": ms[dom],
+                     "step_roof_ms": step_roof_s * 1e3, "step_frac": step_roof_s / (dt / a.steps),
+                     "step_bytes": step_bytes,
                      "flop_view": {"achieved": flops / 1e12, "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
                                    "frac": flops / FP32_PEAK}},
         "kernel_ms": ms,

@@ -62,9 +62,15 @@ int atl_gather_bilinear_bwd_ws(const float* gval, const float* img, const float*
  * hipMalloc).  It allocates nothing: its workspace is a 64 MiB array held by the library on every GPU it runs on
  * (until the process ends), which fits atl_tile_ws_bytes(N, B, H, W) <= 64 MiB (about 3.6M events at 640x480,
  * B = 1); larger calls fail with status 1 and a message.  img (B,H,W) is accumulated, as by the _ws form.
- * Calls that overlap on one GPU share the array and race. */
+ * The array's address on each device is resolved by atl_init (call it once after loading the library, before
+ * any capture), or else by the first call on that device.  Calls that overlap on one GPU share the array and
+ * race. */
 int atl_splat_bilinear_fwd_noalloc(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B,
                                    int64_t H, int64_t W, float* img, hipStream_t stream);
+/* Library set-up (no counterpart in the reference): resolves per-device state, the no-allocation entry point's
+ * scratch address on every visible device, with that device current; the current device is restored.  Returns 0
+ * (also with no device present) or 1 with a message.  The ctypes binding calls it once at load on a GPU host. */
+int atl_init(void);
 /* The Gaussian splat forward with the same tile engine (tiles of the rounded centres, an LDS window of
  * T + 2R pixels per tile); R <= 8.  ws: atl_splat_gauss_ws_bytes(N, B, H, W, R) bytes (-1: unsupported). */
 int64_t atl_splat_gauss_ws_bytes(int64_t N, int64_t B, int64_t H, int64_t W, int64_t R);

@@ -29,3 +29,25 @@ def rand_events(n=500, B=2, H=20, W=24, seed=0):
 @pytest.fixture
 def rng():
     return np.random.default_rng(1234)
+
+
+def assert_sums_close(got, want, rel=1e-5):
+    """Per-anchor relative bar for pair sums: a sum of positive kernel terms, each at least exp(-cut^2 / 2), so
+    every anchor is held to |got - want| <= rel * want; anchors without a contributing pair read exactly 0."""
+    g = np.asarray(got, np.float64)
+    w = np.asarray(want, np.float64)
+    assert g.shape == w.shape
+    zero = w == 0
+    assert np.all(g[zero] == 0), f"{int((g[zero] != 0).sum())} anchors without pairs read non-zero"
+    err = np.abs(g - w)
+    bad = err > rel * w
+    worst = float((err[~zero] / w[~zero]).max()) if (~zero).any() else 0.0
+    assert not bad.any(), f"{int(bad.sum())} of {w.size} sums off by more than {rel:g} relative (worst {worst:.2e})"
+
+
+def assert_logs_close(got, want, tol=1e-5):
+    """Log predictive densities: |got - want| <= tol per anchor, i.e. the densities themselves within tol
+    relative."""
+    err = np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))
+    assert float(err.max(initial=0.0)) <= tol, f"{int((err > tol).sum())} log scores off by more than {tol:g} " \
+                                               f"(worst {float(err.max()):.2e})"

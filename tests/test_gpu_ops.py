@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle as O
-from tests.conftest import rand_events
+from tests.conftest import assert_logs_close, assert_sums_close, rand_events
 from x_amd import synth
 from x_amd.ops import functional as F
 
@@ -284,12 +284,16 @@ def test_sample_flow_interleaved_same_bits(Hg, Wg, img):
         assert np.array_equal(out[ok], want) and not out[~ok].any()
 
     check(fld)
-    check(fld)                                     # the cached copy
-    if Wg >= 2:                                    # a view of the same field (detach) finds the same copy
-        assert F._interleaved(tf.detach()) is F._interleaved(tf)
-    with torch.no_grad():
-        tf.mul_(-0.5)                              # a new version of the field: a new copy
-    check(fld * np.float32(-0.5))
+    with F.layout_scope():
+        check(fld)
+        check(fld)                                 # the scope's copy
+        if Wg >= 2:                                # a view of the same field (detach) finds the same copy
+            assert F._interleaved(tf.detach()) is F._interleaved(tf)
+        with torch.no_grad():
+            tf.mul_(-0.5)                          # a new version of the field: a new copy
+        check(fld * np.float32(-0.5))
+    tf.data.mul_(-2.0)                             # no version bump: seen outside a scope (each look-up copies)
+    check(fld)
 
 
 @pytest.mark.parametrize("C,img", [(4, False), (5, False), (20, False), (7, True), (20, True)])
@@ -409,8 +413,7 @@ def test_pair_sums_match_oracle(tau, S, h):
     q = F.build_pair_plan(T(xs), T(win.t), tv, T(win.b), 2, 40, 48, T(anchors), h, tau, 3.0, S, anchor_xy=T(xa))
     Sg = F._ATSPair.apply(tv, q, h, tau, 3.0)
     assert np.array_equal(N(F.pair_counts(q, h, tau, 3.0)), wcnt)
-    close_rel(N(Sg), want, 1e-5)
-    assert np.allclose(N(Sg), want, rtol=1e-5, atol=1e-6)
+    assert_sums_close(N(Sg), want)
     gS = np.random.default_rng(3).standard_normal(len(anchors)).astype(F32)
     Sg.backward(T(gS))
     close_rel(N(tv.grad), O.ats_pair_bwd(gS, p, h, tau, 3.0, win.n), 1e-4)
@@ -449,7 +452,7 @@ def test_pair_entries_match_oracle(scene, n, tau, S, h, zero_frac):
         cnt = torch.full((len(anchors),), -7, dtype=torch.int32, device=DEV)
         got = N(e.ats_pair_fwd(*args[:-1], count=cnt, plan_order=plan_order))
         assert np.array_equal(N(cnt), want_n)
-        close_rel(got, want_s, 1e-5)
+        assert_sums_close(got, want_s)
     for atomics in (False, True):
         close_rel(N(e.ats_pair_bwd(T(gS), *args, per_pair_atomics=atomics)), want, 1e-4)
 
@@ -540,7 +543,7 @@ def test_anchored_exact_end_to_end():
     wc = O.window_counts(win.t, win.b, np.arange(win.n), 0.2)
     vis = O.visible_fraction_dense(grid, xa, win.t, win.b, win.t, win.b, 2, H, W, 0.2)
     want, gS, _ = O.anchored_epilogue(Sv, wc, 1.0, H, W, vis=vis)
-    close_rel(N(ls), want, 1e-5)
+    assert_logs_close(N(ls), want)
     gv = O.ats_pair_bwd(gS, p, 1.0, 0.2, 3.0, win.n)
     ggrid = O.sample_grid_bwd(gv, idx, wts, grid.shape)
     close_rel(N(m.grid.grad), ggrid, 1e-4)
@@ -602,7 +605,7 @@ def test_anchored_exact_device_rng_full_size():
         obj = AnchoredExact(h=1.0, tau=0.2, cut=3.0, n_slices=16, n_anchors=None, seed=0, rng="device")
         if form == "log_scores":
             ls, _ = obj.log_scores(ev, m)
-            close_rel(N(ls), want, 1e-5)
+            assert_logs_close(N(ls), want)
             (-ls.mean()).backward()
         else:
             out = obj(ev, m)

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import oracle as O
-from tests.conftest import rand_events
+from tests.conftest import assert_logs_close, assert_sums_close, rand_events
 from x_amd import synth
 from x_amd.core import EventPacket
 from x_amd.motion import PixelTrajectories, sample_grid
@@ -335,7 +335,7 @@ def check_traj_against_oracle(p, coef, tab, t, b, B, H, W, anchors, xa, h, tau, 
     plan = F.FastPairPlan(T(p), T(t), None, T(b), B, H, W, None if index_free else T(anchors), h, tau, 3.0, S, T(xa),
                           traj=(T(coef), K, T(tab)))
     assert np.array_equal(N(plan.counts()), wcnt)
-    assert np.allclose(N(plan.forward()), want, rtol=1e-5, atol=1e-6 * max(1.0, float(np.abs(want).max(initial=0))))
+    assert_sums_close(N(plan.forward()), want)
     gS = np.random.default_rng(7).standard_normal(len(anchors)).astype(F32)
     gp, gc = plan.backward_traj(T(gS))
     if fp64:
@@ -462,3 +462,222 @@ def test_anchored_trajectories_straight_equals_exact():
     mt = Translation(1, win.height, win.width, init=torch.tensor([v])).to(DEV)
     ls_e, _ = AnchoredExact(h=1.0, tau=0.3, n_anchors=None, seed=0).log_scores(ev, mt)
     close_rel(N(ls_t), N(ls_e), 1e-5)
+
+
+# ------------------------------------------------------------------------ the continuous-time objective end to end
+def _crop_c4(x0=0, y0=0, w=200, h=150):
+    """The continuous-time workload (4 windows x 500k events, 640x480, per-pixel cubic B-splines with 10 control
+    points) restricted to the events inside one 200 x 150 px box at the sensor corner: the workload's event
+    density and trajectories at about a tenth of its events, with trajectories that leave the sensor."""
+    win = synth.bspline_windows(seed=0)
+    keep = (win.xy[:, 0] >= x0) & (win.xy[:, 0] < x0 + w) & (win.xy[:, 1] >= y0) & (win.xy[:, 1] < y0 + h)
+    sub = synth.Window(xy=np.ascontiguousarray(win.xy[keep]), t=np.ascontiguousarray(win.t[keep]), p=win.p[keep],
+                       b=np.ascontiguousarray(win.b[keep]), height=win.height, width=win.width,
+                       batch_size=win.batch_size, duration=win.duration, motion=win.motion)
+    return sub
+
+
+def _bilinear64(fld, p):
+    """Border-clamped bilinear sample (float64) of a (C, Hg, Wg) field at grid positions p (n, 2): (n, C)."""
+    C, Hg, Wg = fld.shape
+    gx, gy = np.clip(p[:, 0], 0, Wg - 1), np.clip(p[:, 1], 0, Hg - 1)
+    x0, y0 = np.minimum(np.floor(gx), Wg - 2).astype(np.int64), np.minimum(np.floor(gy), Hg - 2).astype(np.int64)
+    ax, ay = (gx - x0)[:, None], (gy - y0)[:, None]
+    f = fld.transpose(1, 2, 0)
+    return (f[y0, x0] * (1 - ax) * (1 - ay) + f[y0, x0 + 1] * ax * (1 - ay) + f[y0 + 1, x0] * (1 - ax) * ay
+            + f[y0 + 1, x0 + 1] * ax * ay)
+
+
+def _disp64(fld, p, t, K):
+    g, _ = O.traj_basis_table(t, K, "bspline")
+    r = _bilinear64(fld, p)
+    return np.stack([(r[:, K:] * g).sum(1), (r[:, :K] * g).sum(1)], 1), r
+
+
+def _origin64(fld, xy, t, K, steps=6):
+    p = xy.copy()
+    for _ in range(steps):
+        p = xy - _disp64(fld, p, t, K)[0]
+    return p
+
+
+def _pair_terms64(p, rows, tj, ids, xa, ta, aid, K, h, tau, S):
+    """float64 kernel values of every (anchor, source) pair of the given sources under the trajectory pair sums'
+    definition (slice-centre linearisation, the three tests, leave-one-out): (values, count)."""
+    cs = O.slice_centres(S).astype(np.float64)
+    g, gd = O.traj_basis_table(cs, K, "bspline")
+    s_lo, s_hi = O.slice_range(tj.astype(F32), tau, S)
+    s = np.clip(np.floor(ta * S), 0, S - 1).astype(np.int64)
+    at = ta - cs[s]
+    y = p[None] + np.stack([g[s] @ rows[:, K:].T, g[s] @ rows[:, :K].T], -1)          # (m, n, 2)
+    v = np.stack([gd[s] @ rows[:, K:].T, gd[s] @ rows[:, :K].T], -1)
+    r = xa[:, None, :] - (y + v * at[:, None, None])
+    d2 = (r * r).sum(-1)
+    ok = (np.abs(ta[:, None] - tj[None]) <= tau) & (d2 <= 9 * h * h) & (aid[:, None] != ids[None])
+    ok &= (s_lo[None] <= s[:, None]) & (s[:, None] <= s_hi[None])
+    return np.where(ok, np.exp(-d2 / (2 * h * h)), 0.0).sum(1), ok.sum()
+
+
+def test_anchored_trajectories_end_to_end_against_the_oracle():
+    """AnchoredTrajectories(rng="device") and the IWE-variance leg on the continuous-time workload (a 200 x 150 px
+    crop of the 4 windows) against the oracle chain:
+    * trajectory starts of the device's fixed-point node within 2e-4 px of the oracle's (fp32, float64 basis);
+    * on those starts: per-anchor neighbour counts bit-exact (oracle plan and pair loops), window counts and
+      exposure bit-exact (anchors whose positions at a bin centre come within 1e-3 px of the sensor edge
+      excepted), log scores within 1e-5 of the oracle epilogue;
+    * the coefficient-grid gradient of -mean(log score) and of the IWE variance against float64 central
+      differences of the chain (six fixed-point steps, coefficient rows, pair sums, epilogue; transport to 0.5,
+      splat, variance) on the largest-gradient coefficients, within 2e-4;
+    * the device IWE against O.splat_bilinear_fwd at the device's transported positions, which are within 2e-4
+      px of the oracle's transport."""
+    from x_amd.objectives import iwe_variance
+    from x_amd.objectives.base import IWEConfig, make_iwe
+    print("anchored trajectories end to end vs oracle (C4 crop)", flush=True)
+    win = _crop_c4()
+    K, h, tau, S, seed = win.motion["K"], 1.0, 0.8, 16, 5
+    H, W, B = win.height, win.width, win.batch_size
+    coeffs = win.motion["coeffs"]
+    n = win.n
+    ev = EventPacket.from_window(win, DEV)
+    c = torch.tensor(coeffs, device=DEV, requires_grad=True)
+    m = PixelTrajectories(c, K, "bspline", tile=1)
+    obj = AnchoredTrajectories(h=h, tau=tau, cut=3.0, n_slices=S, n_anchors=None, seed=seed, rng="device")
+    ls_d, _ = obj.log_scores(ev, m)
+    (-ls_d.mean()).backward()
+    g_score = N(c.grad).astype(np.float64)
+    xs_d, xa_d = F.event_noise(ev.xy, seed, 0, h)                 # the objective's own first draw
+    xs, xa = N(xs_d), N(xa_d)
+    with torch.no_grad():
+        p_d = N(m.origin(xs_d, ev.t, ev.b))
+    p_o = O.traj_origin(coeffs, xs, win.t, win.b, K, "bspline")
+    assert np.abs(p_d - p_o).max() <= 2e-4
+    rows, _, _ = O.sample_grid(coeffs, p_d, win.b)
+    tab = O.traj_slice_table(K, "bspline", S)
+    anchors = np.arange(n)
+    plan = O.build_pair_plan_traj(p_d, rows, tab, win.t, win.b, B, H, W, anchors, xa, h, tau, 3.0, S)
+    S_o, cnt_o = O.ats_pair_fwd(plan, h, tau, 3.0, with_counts=True)
+    dplan = F.FastPairPlan(T(p_d), ev.t, None, ev.b, B, H, W, None, h, tau, 3.0, S, xa_d,
+                           traj=(T(rows), K, T(tab)))
+    assert np.array_equal(N(dplan.counts()), cnt_o) and cnt_o.sum() > 50 * n
+    wc = O.window_counts(win.t, win.b, anchors, tau)
+    assert np.array_equal(N(F.window_counts(ev.t, ev.b, None, tau, assume_sorted=True)), wc)
+    vis = O.traj_visible_fraction(coeffs, xa, win.t, win.b, win.t, win.b, B, H, W, tau, K, "bspline")
+    assert (vis < 1).sum() > 100                                  # the crop's trajectories leave the sensor
+    ls_o, _, D = O.anchored_epilogue(S_o, wc, h, H, W, 1e-2, vis)
+    # anchors whose trajectory position at some bin centre lies within 1e-3 px of the sensor edge: fp32 may count
+    # them inside or outside
+    pa = np.zeros((n, 2))
+    clear = np.ones(n, bool)
+    for b in range(B):
+        sel = win.b == b
+        pa[sel] = _origin64(coeffs[b].astype(np.float64), xa[sel].astype(np.float64), win.t[sel].astype(np.float64), K)
+        for k in range(16):
+            ck = (k + 0.5) / 16
+            yk = pa[sel] + _disp64(coeffs[b].astype(np.float64), pa[sel], np.full(sel.sum(), ck), K)[0]
+            near = np.zeros(sel.sum(), bool)
+            for col, hi in ((0, W - 1), (1, H - 1)):
+                near |= (np.abs(yk[:, col]) <= 1e-3) | (np.abs(yk[:, col] - hi) <= 1e-3)
+            clear[np.nonzero(sel)[0][near]] = False
+    assert clear.mean() > 0.99
+    assert_logs_close(N(ls_d)[clear], ls_o[clear])
+
+    # ---- gradient of -mean(log score): float64 central differences of the chain on the largest-gradient
+    # coefficients (a perturbation moves only the sources whose fixed-point iterates touch the node)
+    Dd = D.astype(np.float64)
+    eps = 1e-2 / (H * W)
+    checked = 0
+    for flat in np.argsort(-np.abs(g_score).ravel())[:8]:
+        b, ch, yy, xx = np.unravel_index(flat, g_score.shape)
+        sel = np.nonzero(win.b == b)[0]
+        fld = coeffs[b].astype(np.float64)
+        e = 1e-3
+        xs64, t64 = xs[sel].astype(np.float64), win.t[sel].astype(np.float64)
+        sums, counts = [], []
+        for sgn in (1, -1, 0):
+            f2 = fld.copy()
+            f2[ch, yy, xx] += sgn * e
+            p2 = _origin64(f2, xs64, t64, K)
+            sums.append((p2, _bilinear64(f2, p2)))
+        moved = np.nonzero(np.any(sums[0][0] != sums[1][0], 1) | np.any(sums[0][1] != sums[1][1], 1))[0]
+        assert 0 < moved.size < 400
+        ids = sel[moved]
+        vals = []
+        for p2, r2 in sums:
+            v, cnt = _pair_terms64(p2[moved], r2[moved], t64[moved], ids, xa[sel].astype(np.float64), t64,
+                                   sel, K, h, tau, S)
+            vals.append(v)
+            counts.append(cnt)
+        if len(set(counts)) != 1:
+            continue                                   # a pair crosses a cut-off: no derivative there
+        # the sums without the moved sources' terms (the oracle's sums hold them at the unperturbed coefficients)
+        base = S_o[sel].astype(np.float64) - vals[2]
+        lp = np.log(eps + (base + vals[0]) / Dd[sel])
+        lm = np.log(eps + (base + vals[1]) / Dd[sel])
+        fd = -(lp - lm).sum() / n / (2 * e)
+        assert abs(g_score[b, ch, yy, xx] - fd) <= 2e-4 * abs(fd), (b, ch, yy, xx, g_score[b, ch, yy, xx], fd)
+        checked += 1
+    assert checked >= 3
+
+    # ---- the IWE leg: transport to 0.5, bilinear splat with the inside mask, variance over pixels
+    c.grad = None
+    cfg = IWEConfig(kernel="bilinear", sigma=0.0)
+    y_d = m.transport(ev.xy, ev.t, 0.5, ev.b)
+    img_d = make_iwe(ev, y_d, 0.5, cfg)
+    var = img_d.var(dim=(-2, -1)).mean()
+    var.backward()
+    g_iwe = N(c.grad).astype(np.float64)
+    assert abs(float(var) - float(N(iwe_variance(ev, m, 0.5)))) <= 1e-6 * abs(float(var))
+    y = N(y_d)
+    q_o = O.traj_origin(coeffs, win.xy, win.t, win.b, K, "bspline")
+    y_o = q_o + O.traj_displacement(coeffs, q_o, np.full(n, 0.5, F32), win.b, K, "bspline")[0]
+    assert np.abs(y - y_o).max() <= 2e-4
+    w = ((y[:, 0] >= 0) & (y[:, 0] <= W - 1) & (y[:, 1] >= 0) & (y[:, 1] <= H - 1)).astype(F32)
+    img_o = O.splat_bilinear_fwd(y, w, win.b, B, H, W)
+    close_rel(N(img_d), img_o, 1e-5)
+    img64 = img_o.astype(np.float64)
+    checked = 0
+    for flat in np.argsort(-np.abs(g_iwe).ravel())[:8]:
+        b, ch, yy, xx = np.unravel_index(flat, g_iwe.shape)
+        sel = np.nonzero(win.b == b)[0]
+        fld = coeffs[b].astype(np.float64)
+        e = 1e-3
+        xy64, t64 = win.xy[sel].astype(np.float64), win.t[sel].astype(np.float64)
+        ys = []
+        for sgn in (1, -1):
+            f2 = fld.copy()
+            f2[ch, yy, xx] += sgn * e
+            q2 = _origin64(f2, xy64, t64, K)
+            ys.append(q2 + _disp64(f2, q2, np.full(sel.size, 0.5), K)[0])
+        moved = np.nonzero(np.any(ys[0] != ys[1], 1))[0]
+        inside = [((yk[moved, 0] >= 0) & (yk[moved, 0] <= W - 1) & (yk[moved, 1] >= 0) & (yk[moved, 1] <= H - 1))
+                  for yk in ys]
+        cells = [np.floor(yk[moved]) for yk in ys]
+        if not (np.array_equal(inside[0], inside[1]) and np.array_equal(cells[0], cells[1])):
+            continue                                   # a mask flip or a pixel crossing between the two sides
+        base = img64[b].copy()
+        y_base = y[sel[moved]].astype(np.float64)
+        w_base = w[sel[moved]].astype(np.float64)
+        for j in range(moved.size):                    # take the moved events out of the oracle image (fp64)
+            base -= _splat64_one(y_base[j], w_base[j], H, W)
+        vs = []
+        for k, yk in enumerate(ys):
+            im = base.copy()
+            for j in range(moved.size):
+                im += _splat64_one(yk[moved[j]], float(inside[k][j]), H, W)
+            vs.append(im.var(ddof=1))
+        fd = (vs[0] - vs[1]) / B / (2 * e)
+        assert abs(g_iwe[b, ch, yy, xx] - fd) <= 2e-4 * abs(fd), (b, ch, yy, xx, g_iwe[b, ch, yy, xx], fd)
+        checked += 1
+    assert checked >= 3
+
+
+def _splat64_one(y, w, H, W):
+    """float64 bilinear splat of one event (zero padding)."""
+    img = np.zeros((H, W))
+    x0, y0 = int(np.floor(y[0])), int(np.floor(y[1]))
+    ax, ay = y[0] - x0, y[1] - y0
+    for dx, wx in ((0, 1 - ax), (1, ax)):
+        for dy, wy in ((0, 1 - ay), (1, ay)):
+            if 0 <= x0 + dx < W and 0 <= y0 + dy < H:
+                img[y0 + dy, x0 + dx] += w * wx * wy
+    return img

@@ -167,10 +167,11 @@ def test_iwe_step_graph_replays_match_eager(kind):
     ev = EventPacket.from_window(win, DEV)
     cfg = IWEConfig(kernel="bilinear", sigma=0.0, mask_border=True)
     prm = list(m.parameters())
+    ones = torch.ones(ev.n, device=DEV)        # d sum(vals) / d vals: no reduction (and no memset) in the graph
 
     def body():
         _, vals = iwe_at_events(ev, m, 0.5, cfg)
-        vals.sum().backward()
+        vals.backward(ones)
         return vals
 
     for q in prm:
@@ -209,3 +210,27 @@ def test_warp_splat_gather_rejects_bad_shapes():
         F.warp_splat_gather(torch.zeros(1, 3, 8, 8, device=DEV), xy, t, b, 0.5, 8, 8)
     with pytest.raises(ValueError):
         F.warp_splat_gather(torch.zeros(1, 2, 8, 8, device=DEV), xy, t[:5], b, 0.5, 8, 8)
+
+
+def test_warp_splat_gather_backward_in_the_other_accumulation_form(monkeypatch):
+    """The backward reuses the forward's chunk list.  With a tile of more than 16384 events the gather form lists
+    2048-record chunks; a backward run in the scatter form (ATL_TILE_SCATTER=1 set between the two) takes them in
+    rounds, so the flow-grid gradient still matches the oracle."""
+    print("warp_splat_gather: forward gather form, backward scatter form, crowded tile", flush=True)
+    H, W, n = 40, 48, 60000
+    rng = np.random.default_rng(21)
+    xy = np.stack([rng.uniform(0, W - 1, n), rng.uniform(0, H - 1, n)], 1).astype(F32)
+    xy[: n // 2] = (np.array([20.0, 16.0]) + rng.uniform(0, 8, (n // 2, 2))).astype(F32)    # one crowded tile
+    t = np.sort(rng.random(n)).astype(F32)
+    b = np.zeros(n, np.int64)
+    grid = (rng.standard_normal((1, 2, H, W)) * 0.5).astype(F32)
+    gvals = rng.standard_normal(n).astype(F32)
+    want_img, want_vals, want_g = oracle_wsg(grid, xy, t, b, 0.5, 1, H, W, True, gvals, np.zeros((1, H, W), F32))
+    monkeypatch.setenv("ATL_TILE_SCATTER", "0")
+    tg = T(grid).requires_grad_(True)
+    img, vals = F.warp_splat_gather(tg, T(xy), T(t), T(b), 0.5, H, W)
+    close_rel(N(img), want_img, 1e-5)
+    close_rel(N(vals), want_vals, 1e-5)
+    monkeypatch.setenv("ATL_TILE_SCATTER", "1")
+    (vals * T(gvals)).sum().backward()
+    close_rel(N(tg.grad), want_g, 1e-4)

@@ -1,7 +1,8 @@
 """atl_splat_bilinear_fwd_noalloc (the splat forward without device allocation) against the workspace form
 atl_splat_bilinear_fwd_ws, both called through the C-ABI: two calls in a row, the second smaller and on another
-image shape (the library's scratch keeps the first call's contents), and a call too large for the scratch, which
-must fail before any launch."""
+image shape (the library's scratch keeps the first call's contents), a call too large for the scratch, which
+must fail before any launch, and the call recorded in a HIP graph (its scratch address resolved by atl_init at
+load), replayed with eager work between replays."""
 import numpy as np
 import pytest
 import torch
@@ -65,3 +66,29 @@ def test_noalloc_splat_rejects_sizes_beyond_its_scratch():
              torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert float(img.abs().sum()) == 0.0                   # nothing launched
+
+
+def test_noalloc_splat_under_graph_capture():
+    print("noalloc: captured call, 300k events, 480x640", flush=True)
+    lib = _ext.load_library()
+    assert lib.atl_init() == 0
+    B, H, W = 1, 480, 640
+    pos, w, b = _events(300_000, B, H, W, seed=2)
+    N = pos.shape[0]
+    nbytes = lib.atl_tile_ws_bytes(N, B, H, W)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    ref = torch.zeros(B, H, W, device=DEV)
+    call("atl_splat_bilinear_fwd_ws", ptr(pos), ptr(w), ptr(b), N, B, H, W, ptr(ref), ptr(ws), nbytes,
+         torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    img = torch.zeros(B, H, W, device=DEV)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call("atl_splat_bilinear_fwd_noalloc", ptr(pos), ptr(w), ptr(b), N, B, H, W, ptr(img),
+             torch.cuda.current_stream().cuda_stream)
+    for r in range(3):
+        img.zero_()                                        # the image is accumulated: cleared outside the graph
+        _ = torch.randn(1000, device=DEV).sum().item()     # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        _check(ref.cpu().numpy(), img.cpu().numpy())

@@ -357,9 +357,10 @@ __global__ void __launch_bounds__(kChunkScanBlock) k_tile_chunks(const int* __re
   if (threadIdx.x == 0) *nchunk = base;
 }
 
-// Accumulation: workgroup w takes chunk w (at most kAccChunk records of one tile, so a crowded tile is shared by
-// several workgroups), adds the weighted contributions of its records into an LDS copy of the pixels that tile's
-// events reach, and flushes the non-zero pixels with one global atomic each.
+// Accumulation: workgroup w takes chunk w (records of one tile, so a crowded tile is shared by several
+// workgroups), adds the weighted contributions of its records into an LDS copy of the pixels that tile's events
+// reach, in rounds of kAccChunk records (a chunk list made for the gather form holds up to kBinChunk), and flushes
+// the non-zero pixels with one global atomic each.
 template <int MODE, int C, int T>
 __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int4* __restrict__ info,
                                                           const int* __restrict__ nchunk,
@@ -387,9 +388,18 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum(const int4* __restrict
   const bool img_org = MODE == kImage || MODE == kImageG || MODE == kVoxel;
   const int ox = img_org ? tx * T - 1 : MODE == kGauss ? tx * T - 2 * g.R : tx * T;   // LDS column 0
   const int oy = img_org ? ty * T - 1 : MODE == kGauss ? ty * T - 2 * g.R : ty * T;
+  for (int base = s0; base < s1; base += kAccChunk) {
+    if (base != s0) {
 #pragma unroll
-  for (int u = 0; u < kAccItems; ++u)
-    if (s0 + u * kAccBlock + (int)threadIdx.x < s1) accum_record<MODE, C>(q[u], gout, g, ox, oy, L, acc);
+      for (int u = 0; u < kAccItems; ++u) {
+        const int k = base + u * kAccBlock + threadIdx.x;
+        if (k < s1) q[u] = rec[k];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kAccItems; ++u)
+      if (base + u * kAccBlock + (int)threadIdx.x < s1) accum_record<MODE, C>(q[u], gout, g, ox, oy, L, acc);
+  }
   __syncthreads();
   for (int a = threadIdx.x; a < L * L; a += kAccBlock) {
     const int py = oy + a / L, px = ox + a % L;
@@ -832,7 +842,8 @@ void tile_bin(const TileGeo& g, const TileLayout& L, void* ws, const float* pos,
 }
 
 // ATL_TILE_SCATTER=1 in the environment selects the scatter form of the accumulation for every mode (read at
-// every call, so that a test can compare both forms in one process).
+// every call, so that a test can compare both forms in one process).  A backward that reuses its forward's chunk
+// list may therefore run the other form on it: the scatter form takes chunks of any length, in rounds.
 bool tile_scatter_form() {
   const char* e = std::getenv("ATL_TILE_SCATTER");
   return e && e[0] == '1';
@@ -870,7 +881,9 @@ void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const flo
 // Scratch of atl_splat_bilinear_fwd_noalloc: the tile engine's workspace (counts, offsets, records) for callers
 // that cannot allocate device memory.  Every GPU the library runs on holds its own copy until the process ends.
 // Host code never passes the array's name to a kernel (on the host it is a stand-in, not a device address): the
-// address of this device's copy is looked up once per device with hipGetSymbolAddress and kept in g_scratch_ptr.
+// address of each device's copy is looked up with hipGetSymbolAddress, with that device current, by atl_init (the
+// library's set-up, for every visible device) or else by the entry point's first call on a device, and kept in
+// g_scratch_ptr.
 // Each call rewrites every byte of it that its kernels read (counts by the histogram pass, offsets by the scan,
 // records by the scatter), so nothing needs clearing; calls that overlap on one GPU share it and race.
 constexpr int64_t kNoAllocScratchBytes = 64ll << 20;
@@ -879,6 +892,19 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 void* g_scratch_ptr[kMaxDevices] = {};
 std::mutex g_scratch_mu;
 
+// The scratch address on the current device `dev`, looked up on first use (caller holds g_scratch_mu).
+int noalloc_lookup(int dev, const char* what) {
+  if (g_scratch_ptr[dev]) return 0;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) {
+    set_error("%s: hipGetSymbolAddress of the scratch array failed on device %d: %s", what, dev, hipGetErrorString(e));
+    return 1;
+  }
+  g_scratch_ptr[dev] = p;
+  return 0;
+}
+
 int noalloc_scratch(void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
@@ -886,16 +912,7 @@ int noalloc_scratch(void** out) {
     return 1;
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
-    void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !p) {
-      set_error("splat_bilinear_fwd_noalloc: hipGetSymbolAddress of the scratch array failed on device %d: %s", dev,
-                hipGetErrorString(e));
-      return 1;
-    }
-    g_scratch_ptr[dev] = p;
-  }
+  if (noalloc_lookup(dev, "splat_bilinear_fwd_noalloc") != 0) return 1;
   *out = g_scratch_ptr[dev];
   return 0;
 }
@@ -1211,6 +1228,24 @@ int atl_splat_bilinear_fwd_ws(const float* pos, const float* w, const int64_t* b
   tile_bin<kImage>(g, L, ws, pos, b, w, stream);
   tile_accum<kImage, 1>(g, L, ws, nullptr, img, stream);
   return check_launch("splat_bilinear_fwd_ws");
+}
+
+int atl_init(void) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+    (void)hipGetLastError();                       // no device: nothing to set up
+    return 0;
+  }
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) { set_error("atl_init: hipGetDevice failed"); return 1; }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  int rc = 0;
+  for (int d = 0; d < count && d < kMaxDevices && rc == 0; ++d) {
+    if (hipSetDevice(d) != hipSuccess) { set_error("atl_init: hipSetDevice(%d) failed", d); rc = 1; break; }
+    rc = noalloc_lookup(d, "atl_init");
+  }
+  if (hipSetDevice(cur) != hipSuccess && rc == 0) { set_error("atl_init: could not restore device %d", cur); rc = 1; }
+  return rc;
 }
 
 int atl_splat_bilinear_fwd_noalloc(const float* pos, const float* w, const int64_t* b, int64_t N, int64_t B,

@@ -27,7 +27,7 @@ import torch
 
 from ..core.events import EventPacket
 from ..ops import (anchored_log_scores, anchored_score_mean, ats_pair_sums, ats_pair_sums_flow, ats_pair_sums_traj,
-                   event_noise, traj_visible_fraction, visible_fraction_linear, window_counts)
+                   event_noise, layout_scope, traj_visible_fraction, visible_fraction_linear, window_counts)
 from .base import Objective
 
 
@@ -167,7 +167,8 @@ class _Anchored(Objective):
     def log_scores(self, ev: EventPacket, motion, anchors: Optional[torch.Tensor] = None):
         """Per-anchor log predictive densities log(eps + S / (W 2 pi h^2)) and the anchor indices
         (atl/objectives/ats.py:75-96)."""
-        (S, wc, vis, eps), anchors = self._terms(ev, motion, anchors)
+        with layout_scope():          # the motion's field is sampled at the sources and at the anchors
+            (S, wc, vis, eps), anchors = self._terms(ev, motion, anchors)
         if anchors is None:
             anchors = torch.arange(ev.n, device=ev.device)
         if ev.xy.is_cuda:
@@ -177,7 +178,8 @@ class _Anchored(Objective):
 
     def __call__(self, ev, motion):
         if ev.xy.is_cuda:                  # epilogue, mean and negation in one launch
-            (S, wc, vis, eps), _ = self._terms(ev, motion)
+            with layout_scope():
+                (S, wc, vis, eps), _ = self._terms(ev, motion)
             loss, score = anchored_score_mean(S, wc, vis, self.h, eps)
             return {"loss": loss, "score": score}
         s = self.log_scores(ev, motion)[0].mean()

@@ -11,7 +11,7 @@ from typing import Optional
 import torch
 
 from ..core.events import EventPacket
-from ..ops import blur, gather, splat, warp_splat_gather
+from ..ops import blur, gather, layout_scope, splat, warp_splat_gather
 
 
 class Objective:
@@ -118,5 +118,6 @@ def iwe_variance(ev: EventPacket, motion, t_ref: float, cfg: Optional[IWEConfig]
     """Contrast of the IWE at ``t_ref``: its per-image variance over the pixels, averaged over the images (the
     variance metric of the reference's contrast maximisation, atl/objectives/cmax.py:23-25)."""
     cfg = cfg or IWEConfig(kernel="bilinear", sigma=0.0)
-    img = make_iwe(ev, motion.transport(ev.xy, ev.t, t_ref, ev.b), t_ref, cfg)
+    with layout_scope():
+        img = make_iwe(ev, motion.transport(ev.xy, ev.t, t_ref, ev.b), t_ref, cfg)
     return img.var(dim=(-2, -1)).mean()

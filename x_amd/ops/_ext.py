@@ -83,6 +83,7 @@ _SIGS = {
     "atl_splat_gauss_fwd_ws": [_P, _P, _P, _I, _I, _I, _I, _D, _I, _P, _P, _I, _P],
     "atl_splat_bilinear_fwd_ws": [_P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P],
     "atl_splat_bilinear_fwd_noalloc": [_P, _P, _P, _I, _I, _I, _I, _P, _P],
+    "atl_init": [],
     "atl_gather_bilinear_bwd_ws": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P],
     "atl_grid_plan": [_I, _I, _I, _P, _P, _I, _I, _I, _P, _I, _P],
     "atl_sample_grid_bwd_planned": [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _P],
@@ -149,6 +150,8 @@ def load_library():
     for name, rt in _RESTYPE.items():
         getattr(lib, name).restype = rt
     lib.atl_last_error.argtypes = []
+    if torch.cuda.is_available() and lib.atl_init() != 0:     # per-device set-up, before any graph capture
+        raise HipLibraryError(lib.atl_last_error().decode())
     _LIB = lib
     return lib
 

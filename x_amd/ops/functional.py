@@ -13,8 +13,10 @@ semantics of :mod:`x_amd.ops.reference`, as the reference does without its exten
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
+import threading
 from dataclasses import dataclass, field
 from typing import Optional
 
@@ -133,27 +135,53 @@ def _tile_plan_ok(B, C, Hg, Wg):
     return C <= 4 or (C <= 32 and B * ((Wg + 16) // 16) * ((Hg + 16) // 16) <= 16384)
 
 
-_CL_CACHE: list = []          # [(field, its version, layout, the copy)]: the last few fields converted
+class _LayoutScope(threading.local):
+    copies: Optional[list] = None         # [(field, its version, layout, stream, the copy)] while a scope is open
+
+
+_SCOPE = _LayoutScope()
+
+
+@contextlib.contextmanager
+def layout_scope():
+    """Reuse layout copies of a field within one evaluation.  The device samplers read a field from a layout copy
+    (channels-last for wide coefficient grids, node-interleaved for two-channel flows).  Inside this scope the copy
+    made by a field's first look-up serves its later look-ups on the same stream (the trajectory model samples its
+    coefficient grid at every fixed-point step, and a flow is sampled at the sources and at the anchors), as long
+    as the field's storage, shape and in-place version are unchanged.  Outside any scope every look-up makes its own
+    copy.  The objectives open a scope around one evaluation; a caller may open one around a whole step.  Within a
+    scope, writes that leave the version counter unchanged (through ``.data``, or raw device pointers) are not
+    seen: do not update a field that way inside a scope.  Scopes nest (the outermost one holds the copies) and
+    are per thread; the copies are released when the outermost scope ends, or when the autograd graph that saved
+    them for its backward is freed."""
+    if _SCOPE.copies is not None:
+        yield
+        return
+    _SCOPE.copies = []
+    try:
+        yield
+    finally:
+        _SCOPE.copies = None
 
 
 def _cached_copy(fld: torch.Tensor, layout: str, make) -> torch.Tensor:
-    """A layout copy of a field that is sampled several times per step (the trajectory model's coefficient grid:
-    every fixed-point step, the final look-up and their backward; a flow: at the sources and at the anchors),
-    made once while the field is unchanged: the copy is kept with the field (which it holds alive) and its in-place
-    version counter, which views of it (detach()) share, and any update of the field makes a new one."""
-    ver = fld._version
-    for src, v, lay, cp in _CL_CACHE:
-        if (lay == layout and v == ver and src.data_ptr() == fld.data_ptr() and src.shape == fld.shape
+    """A layout copy of ``fld``: the open scope's copy of the same field (storage, shape, stride, dtype, version
+    and stream alike), else a new one, recorded in the scope if one is open."""
+    copies = _SCOPE.copies
+    if copies is None:
+        return make()
+    ver, st = fld._version, torch.cuda.current_stream(fld.device).cuda_stream
+    for src, v, lay, s, cp in copies:
+        if (lay == layout and v == ver and s == st and src.data_ptr() == fld.data_ptr() and src.shape == fld.shape
                 and src.stride() == fld.stride() and src.dtype == fld.dtype and src._version == ver):
             return cp
     cp = make()
-    _CL_CACHE.insert(0, (fld, ver, layout, cp))
-    del _CL_CACHE[4:]
+    copies.append((fld, ver, layout, st, cp))
     return cp
 
 
 def _channels_last(fld: torch.Tensor) -> torch.Tensor:
-    """(B, Hg, Wg, 4 ceil(C / 4)) channels-last copy of a (B, C, Hg, Wg) field (cached, _cached_copy)."""
+    """(B, Hg, Wg, 4 ceil(C / 4)) channels-last copy of a (B, C, Hg, Wg) field (reused within a layout_scope)."""
     def make():
         B, C, Hg, Wg = fld.shape
         fcl = torch.empty(B, Hg, Wg, 4 * ((C + 3) // 4), device=fld.device, dtype=F32)
@@ -164,7 +192,7 @@ def _channels_last(fld: torch.Tensor) -> torch.Tensor:
 
 
 def _interleaved(fld: torch.Tensor) -> torch.Tensor:
-    """(B, Hg, Wg, 2) node-interleaved copy of a (B, 2, Hg, Wg) flow (cached, _cached_copy)."""
+    """(B, Hg, Wg, 2) node-interleaved copy of a (B, 2, Hg, Wg) flow (reused within a layout_scope)."""
     def make():
         B, _, Hg, Wg = fld.shape
         fil = torch.empty(B, Hg, Wg, 2, device=fld.device, dtype=F32)
