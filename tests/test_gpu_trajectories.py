@@ -626,7 +626,7 @@ def test_anchored_trajectories_end_to_end_against_the_oracle():
     var = img_d.var(dim=(-2, -1)).mean()
     var.backward()
     g_iwe = N(c.grad).astype(np.float64)
-    assert abs(float(var) - float(N(iwe_variance(ev, m, 0.5)))) <= 1e-6 * abs(float(var))
+    assert abs(float(var.detach()) - float(N(iwe_variance(ev, m, 0.5)))) <= 1e-6 * abs(float(var.detach()))
     y = N(y_d)
     q_o = O.traj_origin(coeffs, win.xy, win.t, win.b, K, "bspline")
     y_o = q_o + O.traj_displacement(coeffs, q_o, np.full(n, 0.5, F32), win.b, K, "bspline")[0]

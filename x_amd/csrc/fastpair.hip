@@ -76,6 +76,8 @@ struct FGeo {
   float tau, half_delta, delta;
   float r2max, kexp, invh2;    // (cut*cut)*h*h, -log2(e)/(2 h h), 1/(h h)
   float cuth;                  // cut * h
+  int gcells;                  // forward groups: cells of one row per group
+  int stile;                   // source order: tiles of stile x stile cells (about kSrcTilePx px)
 };
 
 // Device scalars written by the plan (ordered-int encodings of non-negative floats).
@@ -206,19 +208,21 @@ __device__ __forceinline__ void traj_entry(const float (&cf)[2 * K], float px, f
   vy = uy;
 }
 
-// Sources are ordered by their own-slice cell in tile order: bands of kSrcTile cell rows, within a band tiles
-// of kSrcTile columns, within a tile row by row.  This is a bijection of the cells of a plane onto
+// Sources are ordered by their own-slice cell in tile order: bands of G.stile cell rows, within a band tiles
+// of G.stile columns, within a tile row by row.  This is a bijection of the cells of a plane onto
 // [0, GH * GW) (partial tiles at the right and bottom edges included), so the key space is the entries' and
 // the plane index is still key / (GH * GW); 64 consecutive sources then cover a compact patch rather than a
 // strip of a row, which keeps a wave's neighbourhoods (and its staged anchors) small.
-constexpr int kSrcTile = 8;
+// The tiles are about kSrcTilePx px on a side whatever the cell size: the flow adjoint accumulates a tile's
+// records in a window of 16 x 16 grid nodes, and a tile of 8 cells of 3 px (h = 2) overflowed it.
+constexpr double kSrcTilePx = 12.0;
 __device__ __forceinline__ int source_key(int key, const FGeo& G) {
-  const int pc = G.GH * G.GW;
+  const int pc = G.GH * G.GW, T = G.stile;
   const int plane = key / pc, rem = key - plane * pc;
   const int cy = rem / G.GW, cx = rem - cy * G.GW;
-  const int band = cy / kSrcTile, ly = cy - band * kSrcTile, tx = cx / kSrcTile, lx = cx - tx * kSrcTile;
-  const int hb = min(kSrcTile, G.GH - band * kSrcTile), wt = min(kSrcTile, G.GW - tx * kSrcTile);
-  return plane * pc + band * kSrcTile * G.GW + tx * kSrcTile * hb + ly * wt + lx;
+  const int band = cy / T, ly = cy - band * T, tx = cx / T, lx = cx - tx * T;
+  const int hb = min(T, G.GH - band * T), wt = min(T, G.GW - tx * T);
+  return plane * pc + band * T * G.GW + tx * T * hb + ly * wt + lx;
 }
 
 // Anchor m: slice floor(t / delta) clamped (functional.py:171), fine cell of its clamped position; the key
@@ -832,8 +836,8 @@ __device__ __forceinline__ bool pair_test(int id_a, int id_s, float ta, float ts
 
 // ------------------------------------------------------------------------------------------ walks
 // Queries come in cell order, kAnchorsPerWave (forward) or 64 (backward) to a wave.  Forward: the anchors of up
-// to kGroupCells consecutive cells of one row form a group; the group's anchors are wave-uniform and the lanes
-// take 64 candidates of the group's common neighbourhood at a time (coalesced loads, each candidate read once
+// to G.gcells consecutive cells of one row (about kGroupWidth px) form a group; the group's anchors are
+// wave-uniform and the lanes take 64 candidates of the group's common neighbourhood at a time (coalesced loads, each candidate read once
 // for the whole group); every anchor's sum is reduced across the wave after its last chunk.  A walk with one lane per anchor reads a different cache line in every
 // lane, and that is what bounds it.  Backward: one lane per source walks its own neighbourhoods (sources'
 // per-slice positions differ, so a group shares less there than it costs to set up).
@@ -842,7 +846,7 @@ constexpr int kPairBlock = 64;                     // workgroup of the pair walk
 constexpr int kBwdParts = 2;                       // backward lanes per source (each walks part of its slices)
 static_assert(kBwdParts == 1 || kBwdParts == 2 || kBwdParts == 4, "a source's parts are combined by a butterfly");
 constexpr int kGroup = 8;                          // queries evaluated per pass over a group's candidates
-constexpr int kGroupCells = 4;                     // a forward group spans up to this many cells of one row
+constexpr double kGroupWidth = 9.0;                // a forward group spans cells of one row over about this many px
 
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ float unif(float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); }
@@ -1227,8 +1231,8 @@ __global__ void __launch_bounds__(kPairBlock) k_fast_fwd(FPlan p, FGeo G, int M,
     const int cyx = rdlane(ai.w, i);               // the group's cell, packed by the plan (no divisions)
     const int cy = cyx >> 16, cx = cyx & 0xffff;
     const int plane = gkey - (cy * G.GW + cx);
-    // the group: anchors of up to kGroupCells consecutive cells of one row (lanes i .. i + gsize - 1)
-    const int span = min(kGroupCells, G.GW - cx);
+    // the group: anchors of up to G.gcells consecutive cells of one row (lanes i .. i + gsize - 1)
+    const int span = min(G.gcells, G.GW - cx);
     const uint64_t gmask = __ballot(have && key >= gkey && key - gkey < span) & todo;
     todo &= ~gmask;
     const int gsize = __popcll(gmask);
@@ -1259,8 +1263,9 @@ __device__ __forceinline__ bool bounded(float v) { return fabsf(v) < 1e30f; }
 
 // Record range of slice s of (batch b, tile (tb, tx)) in the source records.
 __device__ __forceinline__ int2 src_tile_range(const FPlan& p, const FGeo& G, int b, int s, int tb, int tx, int EA) {
-  const int hb = min(kSrcTile, G.GH - tb * kSrcTile), wt = min(kSrcTile, G.GW - tx * kSrcTile);
-  const int k0 = (b * G.S + s) * (G.GH * G.GW) + tb * kSrcTile * G.GW + tx * kSrcTile * hb;
+  const int T = G.stile;
+  const int hb = min(T, G.GH - tb * T), wt = min(T, G.GW - tx * T);
+  const int k0 = (b * G.S + s) * (G.GH * G.GW) + tb * T * G.GW + tx * T * hb;
   const int* sstart = p.start + 2 * G.ncell_pad;
   return make_int2(sstart[k0] - EA, sstart[k0 + hb * wt] - EA);
 }
@@ -1451,7 +1456,7 @@ __global__ void __launch_bounds__(kBlock) k_src_tile_counts(FPlan p, FGeo G, int
   const int q = i / SP, s = i - q * SP;
   int n = 0;
   if (q < ntiles && s < G.S) {
-    const int TXb = (G.GW + kSrcTile - 1) / kSrcTile, TYb = (G.GH + kSrcTile - 1) / kSrcTile;
+    const int TXb = (G.GW + G.stile - 1) / G.stile, TYb = (G.GH + G.stile - 1) / G.stile;
     const int b = q / (TXb * TYb), tr = q - b * TXb * TYb;
     const int tb = tr / TXb, tx = tr - tb * TXb;
     const int2 r = src_tile_range(p, G, b, s, tb, tx, p.start[2 * G.ncell_pad]);
@@ -1495,7 +1500,7 @@ __global__ void __launch_bounds__(kAdjBlock) k_src_flow_adjoint(FPlan p, FGeo G,
   if ((int)blockIdx.x >= *nchunk) return;
   const int2 ci = info[blockIdx.x];
   const int tid = threadIdx.x;
-  const int TXb = (G.GW + kSrcTile - 1) / kSrcTile, TYb = (G.GH + kSrcTile - 1) / kSrcTile;
+  const int TXb = (G.GW + G.stile - 1) / G.stile, TYb = (G.GH + G.stile - 1) / G.stile;
   const int b = ci.x / (TXb * TYb), tr = ci.x - b * TXb * TYb;
   const int tb = tr / TXb, tx = tr - tb * TXb;
   if (tid < kWave) {                               // slices s < S <= 64 of batch b: one wave
@@ -1779,6 +1784,10 @@ bool make_geo(const atl_fast_geometry* geo, FGeo& G) {
   G.kexp = (float)(-(double)inv2h2 * 1.4426950408889634);
   G.invh2 = 1.f / (float)(geo->h * geo->h);
   G.cuth = (float)(geo->cut * geo->h);
+  // groups about kGroupWidth px wide whatever the cell size: a fixed cell count made groups of 3 px at h = 0.5,
+  // where the per-pass set-up then dominates, and of 12 px at h = 2, where the box does
+  G.gcells = std::min(16, std::max(1, (int)std::lround(kGroupWidth / (double)G.cf)));
+  G.stile = std::min(16, std::max(2, (int)std::lround(kSrcTilePx / (double)G.cf)));
   return true;
 }
 
@@ -2057,7 +2066,7 @@ int atl_fast_flow_adjoint(const atl_fast_geometry* geo, void* ws, int64_t Hg, in
   F.scale = img_h > 0 && img_w > 0;
   F.sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1);
   F.syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
-  const int64_t tiles = geo->B * ((G.GW + kSrcTile - 1) / kSrcTile) * ((G.GH + kSrcTile - 1) / kSrcTile);
+  const int64_t tiles = geo->B * ((G.GW + G.stile - 1) / G.stile) * ((G.GH + G.stile - 1) / G.stile);
   const int64_t maxc = tiles + (geo->N + kAdjChunk - 1) / kAdjChunk;   // chunks, at most
   int2* info = (int2*)(at_off<char>(ws, geo->off_trec) + align256(geo->N * 8));   // after the gradients
   int* nchunk = (int*)(info + maxc);
