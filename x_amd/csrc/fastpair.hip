@@ -1830,8 +1830,16 @@ int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W
   g.version = ATL_HIP_ABI_VERSION;
   g.N = N; g.M = M; g.B = B; g.H = H; g.W = W; g.S = S;
   g.h = h; g.tau = tau; g.cut = cut;
-  double cf = 0.5 * cut * h;
-  if (cf < 0.5) cf = 0.5;
+  // Cells of about 0.6 cut h: smaller cells cut fewer candidates per walk but add rows, passes and plan cells.
+  // Measured on the 1M-event window (step time): 1.2 px beat 0.75 and 0.9 at h = 0.5, 1.8 beat 1.5 and 2.0 at
+  // h = 1, 2.1 beat 1.8, 2.4 and 3.0 at h = 2.  Denser entries (rho per px^2 and slice on average) shift the
+  // balance to the candidates: the 4M-event blobs ran 177 ms with 1.2 or 1.5 px cells and 194 ms with 1.8, so
+  // above 2 entries per px^2 the size shrinks as rho^-1/4.  At most max(2.1, 2 R / 7) with R ~ cut h + 0.7, so
+  // that a walk's rows still fit the forward's 8-row table.
+  const double rho = (double)N * std::min(1.0, 2.0 * tau + 1.0 / (double)S) / ((double)B * (double)H * (double)W);
+  const double dens = rho > 2.0 ? std::pow(2.0 / rho, 0.25) : 1.0;
+  const double cmax = std::max(2.1, 2.0 * (cut * h + 0.7) / 7.0);
+  const double cf = std::min(std::max(0.6 * cut * h * dens, 1.2), cmax);
   const double pad = 16.0;
   g.cell = (float)cf;
   g.gx0 = (float)-pad;
