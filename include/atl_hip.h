@@ -191,6 +191,18 @@ int atl_traj_visible(const float* field_cl, int64_t B, int64_t C, int64_t K, int
  * adjoint of its per-channel lookup under autograd). */
 int atl_traj_field_bwd_planned(const float* gd, const float* t, int64_t K, int64_t B, int64_t Hg, int64_t Wg,
                                int64_t N, void* ws, float* gfield, hipStream_t stream);
+/* The same coefficient-grid gradient for n_look look-ups of N events in one call, binned here (no plan): look-up
+ * r of event e at grid position pos[r N + e] (n_look, N, 2) with displacement gradient gd[r N + e] and time t[e]
+ * (t_last[e] for the last look-up when t_last is not null: PixelTrajectories.transport's look-up at the
+ * destination time), batch b[e]; gfield (B, 2K, Hg, Wg) accumulated (zero it first), 3 <= K <= 16, 16x16 tiles
+ * (at most 16384 over the batch).  Workspace: atl_traj_field_bwd_bytes(K, B, Hg, Wg, N n_look) bytes (-1 if the
+ * sizes are unsupported); calls that share a workspace must not overlap.  The products are those of
+ * atl_traj_field_bwd_planned; only the order of the float additions differs.  No counterpart in the reference
+ * (autograd's adjoint of every look-up of atl/motion/trajectories.py:68-77). */
+int64_t atl_traj_field_bwd_bytes(int64_t K, int64_t B, int64_t Hg, int64_t Wg, int64_t n_rec);
+int atl_traj_field_bwd(const float* gd, const float* pos, const float* t, const float* t_last, const int64_t* b,
+                       int64_t N, int64_t n_look, int64_t K, int64_t B, int64_t Hg, int64_t Wg, void* ws,
+                       int64_t ws_bytes, float* gfield, hipStream_t stream);
 int atl_traj_pos_bwd_cl(const float* gd, const float* t, int64_t K, const float* field_cl, int64_t B, int64_t Hg,
                         int64_t Wg, const float* gpos_in, const int64_t* b, int64_t N, float* gpos, hipStream_t stream);
 int atl_traj_gout(const float* gd, const float* t, int64_t N, int64_t K, int64_t basis, float* gout,

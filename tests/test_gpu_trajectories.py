@@ -150,6 +150,72 @@ def test_traj_bspline_backward_forms_rows_in_kernel(K):
     close_rel(N(gf_new), N(gf_old), 1e-6)
 
 
+@pytest.mark.parametrize("K,n_look,last,crowd", [(3, 1, False, 0), (10, 3, True, 0), (16, 2, False, 0),
+                                                 (10, 2, True, 20000)])
+def test_traj_field_bwd_equals_the_row_adjoint(K, n_look, last, crowd):
+    """atl_traj_field_bwd (its own binning, one accumulation over n_look look-ups per event, halo flush) against
+    the rows of atl_traj_gout (the last look-up at t_last) accumulated by the per-event sampler adjoint: equal to
+    the order of the float additions.  Positions spill past every grid edge (border clamp), some gradients are
+    zero, and with crowd a single tile holds that many records (split over several workgroups)."""
+    print(f"traj field bwd K={K} n_look={n_look} last={last} crowd={crowd}", flush=True)
+    rng = np.random.default_rng(100 + K + crowd)
+    n, B, Hg, Wg = 7000 + crowd // 2, 2, 37, 53
+    C = 2 * K
+    pos = np.stack([rng.uniform(-2, Wg + 1, (n_look, n)), rng.uniform(-2, Hg + 1, (n_look, n))], -1)
+    if crowd:                                      # one tile (nodes 16..31 x 16..31 of window 1) takes crowd records
+        sel = rng.choice(n, crowd // n_look, replace=False)
+        pos[:, sel] = rng.uniform(16.0, 31.9, (n_look, len(sel), 2))
+    b = rng.integers(0, B, n).astype(np.int64)
+    if crowd:
+        b[sel] = 1
+    t = rng.uniform(-0.1, 1.1, n).astype(F32)
+    tl = rng.uniform(0.0, 1.0, n).astype(F32) if last else None
+    gd = rng.standard_normal((n_look, n, 2)).astype(F32)
+    gd[:, rng.random(n) < 0.1] = 0.0
+    tp, tgd, tb, tt = T(pos.astype(F32)), T(gd), T(b), T(t)
+    ttl = T(tl) if last else None
+    st = F.stream_of(tp)
+    nbytes = int(F.load_library().atl_traj_field_bwd_bytes(K, B, Hg, Wg, n_look * n))
+    assert nbytes > 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    got = torch.zeros(B, C, Hg, Wg, device=DEV)
+    F.call("atl_traj_field_bwd", F.ptr(tgd), F.ptr(tp), F.ptr(tt), F.ptr(ttl), F.ptr(tb), n, n_look, K, B, Hg, Wg,
+           F.ptr(ws), nbytes, F.ptr(got), st)
+    want = torch.zeros_like(got)
+    for r in range(n_look):
+        tr = ttl if last and r == n_look - 1 else tt
+        rows = torch.empty(n, C, device=DEV)
+        F.call("atl_traj_gout", F.ptr(tgd[r]), F.ptr(tr), n, K, 2, F.ptr(rows), st)
+        F.call("atl_sample_grid_bwd", F.ptr(rows), B, C, Hg, Wg, F.ptr(tp[r]), F.ptr(tb), n, 0, 0, F.ptr(want), st)
+    close_rel(N(got), N(want), 1e-6)
+    assert torch.equal(got == 0, want == 0)
+    # a second call on the same workspace (its halo and chunk list rewritten) accumulates the same sum again
+    F.call("atl_traj_field_bwd", F.ptr(tgd), F.ptr(tp), F.ptr(tt), F.ptr(ttl), F.ptr(tb), n, n_look, K, B, Hg, Wg,
+           F.ptr(ws), nbytes, F.ptr(got), st)
+    close_rel(N(got), 2 * N(want), 1e-6)
+
+
+def test_traj_field_bwd_rejects_bad_sizes():
+    """Sizes atl_traj_field_bwd does not take are refused before any launch (workspace query -1, call status 1)."""
+    lib = F.load_library()
+    assert lib.atl_traj_field_bwd_bytes(2, 1, 16, 16, 10) == -1          # K < 3
+    assert lib.atl_traj_field_bwd_bytes(17, 1, 16, 16, 10) == -1         # 2K > 32
+    assert lib.atl_traj_field_bwd_bytes(4, 1, 16, 16, 0) > 0
+    p = torch.zeros(1, 5, 2, device=DEV)
+    t = torch.zeros(5, device=DEV)
+    b = torch.zeros(5, dtype=torch.long, device=DEV)
+    gf = torch.zeros(1, 8, 16, 16, device=DEV)
+    nbytes = int(lib.atl_traj_field_bwd_bytes(4, 1, 16, 16, 5))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    st = F.stream_of(p)
+    assert lib.atl_traj_field_bwd(F.ptr(p), F.ptr(p), F.ptr(t), None, F.ptr(b), 5, 1, 4, 1, 16, 16, F.ptr(ws),
+                                  nbytes - 256, F.ptr(gf), st) == 1
+    assert b"workspace" in lib.atl_last_error()
+    assert lib.atl_traj_field_bwd(F.ptr(p), F.ptr(p), F.ptr(t), None, F.ptr(b), 5, 0, 4, 1, 16, 16, F.ptr(ws),
+                                  nbytes, F.ptr(gf), st) == 1
+    assert not gf.any()
+
+
 def test_traj_displacement_empty_and_rejected_inputs():
     """No events: an empty (0, 2) result and zero gradients; a basis the kernel does not know and times that
     carry a gradient are refused on the host."""

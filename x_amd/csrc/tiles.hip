@@ -16,6 +16,10 @@
 //      (T+1)^2 atomics per tile segment).
 // Corner indices and weights are computed exactly as by the per-event kernels (same fp32 expressions), so the
 // set of touched pixels is identical; only the order of the float additions differs.
+// The coefficient-grid adjoint of the trajectory look-ups (atl_traj_field_bwd) bins its records with their
+// gradients and times (no gathers by event index), accumulates in registers per base node (no float atomics
+// into LDS, which are slow on this part) and flushes a tile held by one workgroup without global atomics: its
+// own nodes in place, its border row and column through a halo buffer added by a second small kernel.
 #include "common.h"
 #include "scan.h"
 #include "bilinear.h"
@@ -310,10 +314,11 @@ __device__ __forceinline__ void accum_record(const float4& q, const float* __res
   }
 }
 
-// Chunks of the tile-ordered records: every non-empty tile is cut into chunks of at most kAccChunk records, and
-// chunk w gets info[w] = (tile, first record, end record).  One workgroup; thread i takes the tiles i, i + 1024,
-// ... (a run of crowded neighbouring tiles is spread over many threads, each writing its own tile's chunks), so
-// the scan of the chunk counts runs in rounds of 1024 tiles; nchunk[0] = the number of chunks.
+// Chunks of the tile-ordered records: every non-empty tile is cut into chunks of at most `chunk` records, and
+// chunk w gets info[w] = (tile, first record, end record, 1 if the tile has more than one chunk).  One
+// workgroup; thread i takes the tiles i, i + 1024, ... (a run of crowded neighbouring tiles is spread over many
+// threads, each writing its own tile's chunks), so the scan of the chunk counts runs in rounds of 1024 tiles;
+// nchunk[0] = the number of chunks.
 constexpr int kChunkScanBlock = 1024;
 static_assert(kTileMaxKeys <= kChunkScanBlock * 16, "one scan thread handles at most 16 tiles");
 
@@ -344,13 +349,13 @@ __global__ void __launch_bounds__(kChunkScanBlock) k_tile_chunks(const int* __re
     const int c = base + block_exclusive_scan<kChunkScanBlock>(n, wsum, total);
     const bool crowded = n > kWave / 8;           // a crowded tile's chunks are written by its whole wave
     if (!crowded)
-      for (int q = 0; q < n; ++q) info[c + q] = make_int4(t, r0[k] + q * cs, min(r0[k] + (q + 1) * cs, r1[k]), 0);
+      for (int q = 0; q < n; ++q) info[c + q] = make_int4(t, r0[k] + q * cs, min(r0[k] + (q + 1) * cs, r1[k]), n > 1);
     for (uint64_t m = __ballot(crowded); m; m &= m - 1) {
       const int src = __ffsll((unsigned long long)m) - 1;
       const int tt = __shfl(t, src), cc = __shfl(c, src), a0 = __shfl(r0[k], src), a1 = __shfl(r1[k], src);
       const int nn = __shfl(n, src), ss = __shfl(cs, src);
       for (int q = threadIdx.x & (kWave - 1); q < nn; q += kWave)
-        info[cc + q] = make_int4(tt, a0 + q * ss, min(a0 + (q + 1) * ss, a1), 0);
+        info[cc + q] = make_int4(tt, a0 + q * ss, min(a0 + (q + 1) * ss, a1), nn > 1);
     }
     base += total;
   }
@@ -730,6 +735,286 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum_rows(const int4* __res
       if (v != 0.f) atomicAdd(out + ((int64_t)b * nc + ch) * pl + (int64_t)py * g.W + px, v);
     }
   }
+}
+
+// ------------------------------------------------------------ coefficient-grid adjoint of trajectory look-ups
+// The records of n_look look-ups of N events: look-up r of event e sits at grid position pos[r N + e] with the
+// displacement gradient gd[r N + e] and the time t[e] (t_last[e] for the last look-up when t_last is set, the
+// transport's look-up at the destination time).  The binning stores (x, y, gd.x, gd.y) and the time of every
+// record with a non-zero gradient in tile order, so the accumulation reads its tile's records in sequence (no
+// gathers of gradients and times by event index).  A binning block takes `per` records per thread, chosen so
+// that a call has about kTrajBinBlocks blocks: the per-block count matrix (nkeys x blocks) and its scan stay
+// small on large calls, and each block's run of a tile is longer.
+constexpr int kTrajBinBlocks = 512;
+
+inline int traj_bin_per(int64_t m) {
+  const int64_t per = (m + (int64_t)kTrajBinBlocks * kTileBinBlock - 1) / ((int64_t)kTrajBinBlocks * kTileBinBlock);
+  return (int)std::min<int64_t>(std::max<int64_t>(per, 8), 256);
+}
+
+template <bool SCATTER>
+__global__ void __launch_bounds__(kTileBinBlock) k_traj_bin(const float2* __restrict__ pos,
+                                                            const float2* __restrict__ gd,
+                                                            const float* __restrict__ t,
+                                                            const float* __restrict__ t_last,
+                                                            const int64_t* __restrict__ bidx, int N, int n_look,
+                                                            int per, TileGeo g, int* __restrict__ cnt,
+                                                            float4* __restrict__ rec, float* __restrict__ tr) {
+  extern __shared__ int hist[];
+  const int blk = blockIdx.x;
+  for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) hist[i] = SCATTER ? cnt[i * g.nblk + blk] : 0;
+  __syncthreads();
+  constexpr int U = 4;                           // records per thread in flight together
+  const int64_t j0 = (int64_t)blk * per * kTileBinBlock;
+  for (int u0 = 0; u0 < per; u0 += U) {
+    float2 d[U], p[U];
+    int e[U], r[U];
+    int64_t bj[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = j0 + (int64_t)(u0 + u) * kTileBinBlock + threadIdx.x;
+      const bool in = u0 + u < per && j < g.N;
+      r[u] = in ? (int)(j / N) : 0;
+      e[u] = in ? (int)(j - (int64_t)r[u] * N) : -1;
+      d[u] = in ? gd[j] : make_float2(0.f, 0.f);
+      p[u] = in ? pos[j] : make_float2(0.f, 0.f);
+      bj[u] = in ? bidx[e[u]] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (e[u] < 0 || (d[u].x == 0.f && d[u].y == 0.f)) continue;   // a zero gradient adds nothing
+      const int key = tile_key<kGrid>(p[u].x, p[u].y, bj[u], g);
+      if (key < 0) continue;
+      const int slot = atomicAdd(hist + key, 1);
+      if (SCATTER) {
+        rec[slot] = make_float4(p[u].x, p[u].y, d[u].x, d[u].y);
+        tr[slot] = t_last && r[u] == n_look - 1 ? t_last[e[u]] : t[e[u]];
+      }
+    }
+  }
+  if (!SCATTER) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) cnt[(int64_t)blk * g.nkeys + i] = hist[i];
+  }
+}
+
+// Window nodes past a tile's own 16 x 16: its right column (17 nodes, the last one diagonal) and its bottom row
+// (16), which belong to the tiles on its right, below and diagonally below.  Halo slot h: right column row h for
+// h <= 16, bottom row column h - 17 for h >= 17.
+constexpr int kHalo = 2 * kBinT + 1;
+
+// Accumulation of the trajectory records in the gather form.  Float atomic adds into LDS run at a small fraction
+// of the LDS rate on this part (~0.3 lane-adds per CU per cycle against ~8 for a plain read-modify-write), so no
+// record is added into shared memory: workgroup w takes chunk w of one tile (info[w] = (tile, first, end,
+// shared)) and thread c owns base node c of the tile's 16 x 16.  In rounds of kTrajRound records every thread
+// takes three records, forms their base node and fractions (grid_cell) and their B-spline basis
+// (bspline_nonzero_tab, the knots from an LDS table), ranks them by base node with one LDS integer atomic each,
+// and stores (ax, ay, gd.x, gd.y) and the dense basis row (N_{k+1} in column k, zero elsewhere) in base-node
+// order; thread c then adds, for each record of its node, fma(w gd, N, s) into registers for every corner,
+// component and column (the scatter form's corner weight times the displacement gradient, times the basis
+// value).  After the last round the window nodes sum the four base nodes that reach them (channel groups of
+// kTrajGroup through LDS) and flush without global atomics when the tile has a single chunk: its own 16 x 16
+// nodes are added in place (no other workgroup writes them in the launch) and its halo goes to the tile's
+// slots, which k_traj_halo_add adds to the neighbours afterwards; the chunks of a split tile add both with
+// atomics (halo zeroed beforehand).  KM >= K columns are held per component (rows padded with zeros).
+constexpr int kTrajRound = 768;                  // records staged per round (three per thread: 50 KB of LDS)
+constexpr int kTrajGroup = 8;                    // columns per combination pass
+
+template <int KM>
+__global__ void __launch_bounds__(kAccBlock) k_traj_tile_accum(const int4* __restrict__ info,
+                                                               const int* __restrict__ nchunk,
+                                                               const float4* __restrict__ rec,
+                                                               const float* __restrict__ tr, TileGeo g, int K,
+                                                               float* __restrict__ out, float* __restrict__ halo) {
+  constexpr int T = kBinT, L = T + 1, R = kTrajRound, U = R / kAccBlock;
+  constexpr int KP = (KM + 3) & ~3;              // basis row stride (16-byte rows)
+  constexpr int kStage = R * KP > 4 * kTrajGroup * kBins ? R * KP : 4 * kTrajGroup * kBins;
+  __shared__ int bcnt[kBins], bstart[kBins];
+  __shared__ int wsum[kAccBlock / kWave + 1];
+  __shared__ float4 sg[R];                       // (ax, ay, gd.x, gd.y) of the round's records, base-node order
+  __shared__ __align__(16) float sb[kStage];     // their basis rows; after the rounds: the corner sums
+  __shared__ float knots[kMaxChannels / 2 + 1];  // c / L, c = 0..L
+  if ((int)blockIdx.x >= *nchunk) return;
+  {
+    const int P = K < 3 ? K : 3, Lk = K + 1 - P;
+    if ((int)threadIdx.x <= Lk) knots[threadIdx.x] = (float)(int)threadIdx.x / (float)Lk;
+  }
+  const int4 ci = info[blockIdx.x];
+  const int key = ci.x, s0 = ci.y, s1 = ci.z;
+  const bool shared = ci.w != 0;
+  const int tid = threadIdx.x;
+  const int nc = 2 * K;
+  const int plane = g.TY * g.TX;
+  const int b = key / plane, rr = key - b * plane;
+  const int ty = rr / g.TX, tx = rr - ty * g.TX;
+  const int ox = tx * T, oy = ty * T;
+  float s[4][2][KM];                             // corner, component (0: gd.y channels, 1: gd.x), column
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int k = 0; k < KM; ++k) s[c][m][k] = 0.f;
+  for (int base = s0; base < s1; base += R) {
+    float4 q[U];
+    float tq[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = base + u * kAccBlock + tid;
+      if (k < s1) {
+        q[u] = rec[k];
+        tq[u] = tr[k];
+      }
+    }
+    bcnt[tid] = 0;
+    __syncthreads();                             // the previous round's readers are done
+    int bin[U], rank[U];
+    float ax[U], ay[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      bin[u] = -1;
+      if (base + u * kAccBlock + tid >= s1) continue;
+      const GridCell c = grid_cell(q[u].x, q[u].y, g.H, g.W, g.sxw, g.syh, false);
+      const int bx = c.x0 - ox, by = c.y0 - oy;
+      if ((unsigned)bx < (unsigned)T && (unsigned)by < (unsigned)T) {   // always: the binning chose this tile
+        ax[u] = c.ax;
+        ay[u] = c.ay;
+        bin[u] = by * T + bx;
+        rank[u] = atomicAdd(bcnt + bin[u], 1);
+      }
+    }
+    __syncthreads();
+    const int mine = bcnt[tid];
+    int total;
+    const int first = block_exclusive_scan<kAccBlock>(mine, wsum, total);
+    bstart[tid] = first;
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (bin[u] < 0) continue;
+      const int p = bstart[bin[u]] + rank[u];
+      sg[p] = make_float4(ax[u], ay[u], q[u].z, q[u].w);
+      float* row = sb + p * KP;
+#pragma unroll
+      for (int k = 0; k < KP; k += 4) *(float4*)(row + k) = make_float4(0.f, 0.f, 0.f, 0.f);
+      float nb[4];
+      const int j = bspline_nonzero_tab(tq[u], K, knots, nb);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int k = j - 1 + r;                 // column of nb[r] (g_k = N_{k+1})
+        if (k >= 0 && k < K) row[k] = nb[r];
+      }
+    }
+    __syncthreads();
+    for (int p = first; p < first + mine; ++p) {
+      const float4 a = sg[p];
+      const float wx0 = 1.f - a.x, wy0 = 1.f - a.y;
+      const float w[4] = {wx0 * wy0, a.x * wy0, wx0 * a.y, a.x * a.y};
+      float v[4][2];                             // corner weight times gd (channel k: gd.y, channel K + k: gd.x)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        v[c][0] = w[c] * a.w;
+        v[c][1] = w[c] * a.z;
+      }
+      const float* row = sb + p * KP;
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        const float bk = row[k];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int m = 0; m < 2; ++m) s[c][m][k] = __fmaf_rn(v[c][m], bk, s[c][m][k]);
+      }
+    }
+  }
+  __syncthreads();                               // the staging area becomes the corner-sum table
+  const int sx = g.W > 1 ? 1 : 0, sy = g.H > 1 ? 1 : 0;   // second corner: the next node, or the same one
+  const int64_t pl = (int64_t)g.H * g.W;
+  constexpr int G = kTrajGroup;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+#pragma unroll
+    for (int k0 = 0; k0 < KM; k0 += G) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int q = 0; q < G; ++q)
+          if (k0 + q < KM) sb[(c * G + q) * kBins + tid] = s[c][m][k0 + q];
+      __syncthreads();
+      for (int a = tid; a < L * L; a += kAccBlock) {   // window node a adds the base nodes that reach it
+        const int ly = a / L, lx = a - ly * L;
+        float v[G];
+#pragma unroll
+        for (int q = 0; q < G; ++q) v[q] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int cx = lx - (c & 1) * sx, cy = ly - (c >> 1) * sy;
+          if ((unsigned)cx >= (unsigned)T || (unsigned)cy >= (unsigned)T) continue;
+#pragma unroll
+          for (int q = 0; q < G; ++q) v[q] += sb[(c * G + q) * kBins + cy * T + cx];
+        }
+        const bool own = ly < T && lx < T;
+        const int py = oy + ly, px = ox + lx;
+        if (own && (py >= g.H || px >= g.W)) continue;
+#pragma unroll
+        for (int q = 0; q < G; ++q) {
+          const int k = k0 + q;
+          if (k >= K || v[q] == 0.f) continue;
+          const int ch = m * K + k;
+          float* o = own ? out + ((int64_t)b * nc + ch) * pl + (int64_t)py * g.W + px
+                         : halo + ((int64_t)key * nc + ch) * kHalo + (lx == T ? ly : T + 1 + lx);
+          if (shared)
+            atomicAdd(o, v[q]);
+          else if (own)
+            *o += v[q];
+          else
+            *o = v[q];
+        }
+      }
+      __syncthreads();                           // the table is rewritten by the next group
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kBlock) k_fill_zero_f(float* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+// Adds the halos to the nodes they belong to: thread (tile, channel, i) owns node (0, i) of the tile's left
+// column (i < 16) or node (i - 15, 0) of its top row (16 <= i < 31) and adds the halo slots that land there (the
+// left tile's right column, the upper tile's bottom row, the upper-left tile's diagonal node), one thread per node.
+__global__ void __launch_bounds__(kBlock) k_traj_halo_add(const float* __restrict__ halo, TileGeo g, int nc,
+                                                          float* __restrict__ out) {
+  constexpr int T = kBinT;
+  constexpr int kOwn = 2 * T - 1;                 // left column and top row nodes of a tile
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (int64_t)g.nkeys * nc * kOwn) return;
+  const int i = (int)(id % kOwn);
+  const int64_t kc = id / kOwn;
+  const int ch = (int)(kc % nc), key = (int)(kc / nc);
+  const int plane = g.TY * g.TX;
+  const int b = key / plane, rr = key - b * plane;
+  const int ty = rr / g.TX, tx = rr - ty * g.TX;
+  auto slot = [&](int k, int h) { return halo[((int64_t)k * nc + ch) * kHalo + h]; };
+  int lx, ly;
+  float v = 0.f;
+  if (i < T) {
+    lx = 0;
+    ly = i;
+    if (tx > 0) v += slot(key - 1, i);
+    if (i == 0 && ty > 0) {
+      v += slot(key - g.TX, T + 1);
+      if (tx > 0) v += slot(key - g.TX - 1, T);
+    }
+  } else {
+    lx = i - T + 1;
+    ly = 0;
+    if (ty > 0) v += slot(key - g.TX, T + 1 + lx);
+  }
+  const int py = ty * T + ly, px = tx * T + lx;
+  if (v == 0.f || py >= g.H || px >= g.W) return;
+  out[((int64_t)b * nc + ch) * g.H * g.W + (int64_t)py * g.W + px] += v;
 }
 
 // gpos of the bilinear gather backward (csrc/atl_cpu.cpp:151-172, the position half): per event, no atomics.
@@ -1206,6 +1491,33 @@ __global__ void __launch_bounds__(kTileBinBlock) k_wsg_grad(const float2* __rest
   for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) cnt[(int64_t)blk * gg.nkeys + i] = hist[i];
 }
 
+// Trajectory adjoint: geometry of m records on a (B, 2K, Hg, Wg) grid (16 x 16 tiles only), the block count of
+// its binning, and its workspace: the tile layout, the records' times and the halo slots.
+constexpr int kTrajChunk = 8192;                  // records per accumulation workgroup: most tiles take one
+
+bool traj_geo(int64_t K, int64_t B, int64_t Hg, int64_t Wg, int64_t m, TileGeo& g) {
+  if (K < 3 || 2 * K > kMaxChannels || !tile_geo(kGrid, B, Hg, Wg, m, 0, 0, g) || g.T != kBinT) return false;
+  g.C = (int)(2 * K);
+  const int64_t rpb = (int64_t)traj_bin_per(m) * kTileBinBlock;
+  g.nblk = (int)((m + rpb - 1) / rpb);
+  return true;
+}
+
+struct TrajLayout {
+  TileLayout t;
+  int64_t tr, halo, bytes;
+};
+
+TrajLayout traj_layout(const TileGeo& g) {
+  TrajLayout L;
+  L.t = tile_layout(g);
+  int64_t off = L.t.bytes;
+  L.tr = off;   off += align256((int64_t)g.N * 4);
+  L.halo = off; off += align256((int64_t)g.nkeys * g.C * kHalo * 4);
+  L.bytes = off;
+  return L;
+}
+
 }  // namespace
 
 // ================================================================================================ C-ABI
@@ -1435,6 +1747,70 @@ int atl_traj_field_bwd_planned(const float* gd, const float* t, int64_t K, int64
                      (const int*)nchunk, (const float4*)(w + L.rec), (const float*)nullptr, g, gfield,
                      (const float2*)gd, t);
   return check_launch("traj_field_bwd_planned");
+}
+
+int64_t atl_traj_field_bwd_bytes(int64_t K, int64_t B, int64_t Hg, int64_t Wg, int64_t n_rec) {
+  TileGeo g;
+  if (!traj_geo(K, B, Hg, Wg, n_rec, g)) return -1;
+  return traj_layout(g).bytes;
+}
+
+int atl_traj_field_bwd(const float* gd, const float* pos, const float* t, const float* t_last, const int64_t* b,
+                       int64_t N, int64_t n_look, int64_t K, int64_t B, int64_t Hg, int64_t Wg, void* ws,
+                       int64_t ws_bytes, float* gfield, hipStream_t stream) {
+  if (N < 0 || n_look < 1 || (double)N * (double)n_look >= (double)(1 << 30)) {
+    set_error("traj_field_bwd: bad record count N=%lld n_look=%lld", (long long)N, (long long)n_look);
+    return 1;
+  }
+  const int64_t m = N * n_look;
+  TileGeo g;
+  if (!traj_geo(K, B, Hg, Wg, m, g)) {
+    set_error("traj_field_bwd: bad sizes (3 <= K <= %d on grids of at most 16384 16x16 tiles)", kMaxChannels / 2);
+    return 1;
+  }
+  const TrajLayout L = traj_layout(g);
+  if (!ws || ws_bytes < L.bytes) { set_error("traj_field_bwd: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
+  if (m == 0) return 0;
+  if (!gd || !pos || !t || !b || !gfield) { set_error("traj_field_bwd: null argument"); return 1; }
+  char* w = (char*)ws;
+  int* cnt = (int*)(w + L.t.cnt);
+  int* boff = (int*)(w + L.t.boff);
+  float4* rec = (float4*)(w + L.t.rec);
+  float* tr = (float*)(w + L.tr);
+  float* halo = (float*)(w + L.halo);
+  int4* info = (int4*)(w + L.t.info);
+  int* nchunk = (int*)(w + L.t.nchunk);
+  const int per = traj_bin_per(m);
+  const size_t lds = (size_t)g.nkeys * sizeof(int);
+  hipLaunchKernelGGL(k_traj_bin<false>, dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
+                     (const float2*)gd, t, t_last, b, (int)N, (int)n_look, per, g, cnt, (float4*)nullptr,
+                     (float*)nullptr);
+  scan32t(cnt, g.nkeys, g.nblk, (int*)(w + L.t.part), boff, stream);
+  hipLaunchKernelGGL(k_traj_bin<true>, dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
+                     (const float2*)gd, t, t_last, b, (int)N, (int)n_look, per, g, boff, rec, tr);
+  hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)boff, g, kTrajChunk,
+                     kTrajChunk, info, nchunk);
+  const int64_t nh = (int64_t)g.nkeys * g.C * kHalo;
+  hipLaunchKernelGGL(k_fill_zero_f, dim3(grid_for(nh)), dim3(kBlock), 0, stream, halo, nh);
+  const int64_t nchunks = (int64_t)g.nkeys + (m + kTrajChunk - 1) / kTrajChunk;   // ceil(len / chunk) per tile
+  auto accum = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)nchunks), dim3(kAccBlock), 0, stream, (const int4*)info,
+                       (const int*)nchunk, (const float4*)rec, (const float*)tr, g, (int)K, gfield, halo);
+  };
+  if (K <= 4)
+    accum(k_traj_tile_accum<4>);
+  else if (K <= 8)
+    accum(k_traj_tile_accum<8>);
+  else if (K <= 10)
+    accum(k_traj_tile_accum<10>);
+  else if (K <= 12)
+    accum(k_traj_tile_accum<12>);
+  else
+    accum(k_traj_tile_accum<16>);
+  const int64_t nfix = (int64_t)g.nkeys * g.C * (2 * kBinT - 1);
+  hipLaunchKernelGGL(k_traj_halo_add, dim3(grid_for(nfix)), dim3(kBlock), 0, stream, (const float*)halo, g, g.C,
+                     gfield);
+  return check_launch("traj_field_bwd");
 }
 
 // Warp -> splat -> gather (the fused pipeline above).  Workspace bytes, or -1 for unsupported sizes.

@@ -352,7 +352,9 @@ class _TrajDisplacement(torch.autograd.Function):
             fcl = _channels_last(fld)
             call("atl_traj_displacement", ptr(fcl), B, C, K, Hg, Wg, ptr(gpos), ptr(b), ptr(t), N, basis, ptr(out),
                  st)
-            if plan and _tile_plan_ok(B, C, Hg, Wg):
+            bspline = basis == TRAJ_BASES["bspline"] and K >= 3 and _traj_field_ok(K, B, Hg, Wg, N) >= 0
+            ctx.bspline = bspline
+            if plan and not bspline and _tile_plan_ok(B, C, Hg, Wg):
                 nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N))
                 if nbytes >= 0:
                     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=gpos.device)
@@ -371,12 +373,10 @@ class _TrajDisplacement(torch.autograd.Function):
         gf = gp = None
         with torch.cuda.device(gpos.device):
             st = stream_of(gpos)
-            if ctx.basis == TRAJ_BASES["bspline"] and ctx.K >= 3 and ctx.plan is not None:
+            if ctx.bspline:
                 # the gradient rows are formed from gd and t inside both kernels (no (N, 2K) rows in memory)
                 if ctx.needs_input_grad[0]:
-                    gf = torch.zeros(B, C, Hg, Wg, device=gpos.device, dtype=F32)
-                    call("atl_traj_field_bwd_planned", ptr(gd), ptr(t), ctx.K, B, Hg, Wg, N, ptr(ctx.plan), ptr(gf),
-                         st)
+                    gf = _traj_field_grad(gd.view(1, N, 2), gpos.view(1, N, 2), t, None, b, ctx.K, B, Hg, Wg)
                 if ctx.needs_input_grad[1]:
                     gp = torch.empty_like(gpos)
                     call("atl_traj_pos_bwd_cl", ptr(gd), ptr(t), ctx.K, ptr(fcl), B, Hg, Wg, ptr(gpos), ptr(b), N,
@@ -436,6 +436,26 @@ def traj_displacement(fld: torch.Tensor, gpos: torch.Tensor, b: torch.Tensor, t:
     return _TrajDisplacement.apply(fld, gpos, b, t, int(K), TRAJ_BASES[basis], plan)
 
 
+def _traj_field_ok(K, B, Hg, Wg, n_rec):
+    """atl_traj_field_bwd's workspace bytes for n_rec look-ups, or -1 where it does not take the sizes."""
+    return int(load_library().atl_traj_field_bwd_bytes(int(K), B, Hg, Wg, n_rec))
+
+
+def _traj_field_grad(gD, P, t, t_last, b, K, B, Hg, Wg):
+    """Coefficient-grid gradient (B, 2K, Hg, Wg) of n look-ups of N events: look-up r of event e at grid position
+    P[r, e] with displacement gradient gD[r, e] (both (n, N, 2)) and time t[e] (t_last[e] for the last look-up
+    when t_last is given), binned and accumulated in one atl_traj_field_bwd call."""
+    n, N = P.shape[0], P.shape[1]
+    nbytes = _traj_field_ok(K, B, Hg, Wg, n * N)
+    if nbytes < 0:
+        raise HipLibraryError(f"traj field gradient: unsupported sizes K={K} B={B} {Hg}x{Wg} records={n * N}")
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=gD.device)
+    gf = torch.zeros(B, 2 * int(K), Hg, Wg, device=gD.device, dtype=F32)
+    call("atl_traj_field_bwd", ptr(gD), ptr(P), ptr(t), ptr(t_last), ptr(b), N, n, int(K), B, Hg, Wg, ptr(ws), nbytes,
+         ptr(gf), stream_of(gD))
+    return gf
+
+
 class _TrajOrigin(torch.autograd.Function):
     """PixelTrajectories.origin's n Picard steps p_{k+1} = xy - d(p_k, t), p_0 = xy, as one autograd node
     (atl/motion/trajectories.py:68-73 differentiated step by step, as autograd does there), and with ``t_dst``
@@ -493,17 +513,7 @@ class _TrajOrigin(torch.autograd.Function):
             call("atl_traj_origin_bwd", ptr(fcl), B, C, ctx.K, Hg, Wg, ptr(P), ptr(t), ptr(b), N, n, ctx.tile,
                  ptr(g), ptr(gD), ptr(gxy), st)
             if ctx.needs_input_grad[0]:
-                m = (n + int(fin)) * N
-                tt = t.repeat(n) if not fin else torch.cat([t.repeat(n), t_dst])
-                pos, bb = P.view(m, 2), b.repeat(n + int(fin))
-                nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, m))
-                if nbytes < 0:
-                    raise HipLibraryError(f"traj origin: no tile plan for {m} records")
-                ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=gy.device)
-                call("atl_grid_plan", B, Hg, Wg, ptr(pos), ptr(bb), m, 0, 0, ptr(ws), nbytes, st)
-                gf = torch.zeros(B, C, Hg, Wg, device=gy.device, dtype=F32)
-                call("atl_traj_field_bwd_planned", ptr(gD.view(m, 2)), ptr(tt), ctx.K, B, Hg, Wg, m, ptr(ws),
-                     ptr(gf), st)
+                gf = _traj_field_grad(gD, P, t, t_dst, b, ctx.K, B, Hg, Wg)
         return gf, gxy, None, None, None, None, None, None, None, None
 
 
