@@ -744,16 +744,18 @@ __global__ void __launch_bounds__(kAccBlock) k_tile_accum_rows(const int4* __res
 // record with a non-zero gradient in tile order, so the accumulation reads its tile's records in sequence (no
 // gathers of gradients and times by event index).  A binning block takes `per` records per thread, chosen so
 // that a call has about kTrajBinBlocks blocks: the per-block count matrix (nkeys x blocks) and its scan stay
-// small on large calls, and each block's run of a tile is longer.
-constexpr int kTrajBinBlocks = 512;
+// small on large calls, and each block's run of a tile is longer (14M records on 4800 tiles: the scatter took
+// 0.51 ms with 2048 blocks of 512 threads, 0.40 with 512 and 0.38 with 256 blocks of 1024).
+constexpr int kTrajBinBlocks = 256;
+constexpr int kTrajBinThreads = 1024;
 
 inline int traj_bin_per(int64_t m) {
-  const int64_t per = (m + (int64_t)kTrajBinBlocks * kTileBinBlock - 1) / ((int64_t)kTrajBinBlocks * kTileBinBlock);
+  const int64_t per = (m + (int64_t)kTrajBinBlocks * kTrajBinThreads - 1) / ((int64_t)kTrajBinBlocks * kTrajBinThreads);
   return (int)std::min<int64_t>(std::max<int64_t>(per, 8), 256);
 }
 
 template <bool SCATTER>
-__global__ void __launch_bounds__(kTileBinBlock) k_traj_bin(const float2* __restrict__ pos,
+__global__ void __launch_bounds__(kTrajBinThreads) k_traj_bin(const float2* __restrict__ pos,
                                                             const float2* __restrict__ gd,
                                                             const float* __restrict__ t,
                                                             const float* __restrict__ t_last,
@@ -765,14 +767,14 @@ __global__ void __launch_bounds__(kTileBinBlock) k_traj_bin(const float2* __rest
   for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) hist[i] = SCATTER ? cnt[i * g.nblk + blk] : 0;
   __syncthreads();
   constexpr int U = 4;                           // records per thread in flight together
-  const int64_t j0 = (int64_t)blk * per * kTileBinBlock;
+  const int64_t j0 = (int64_t)blk * per * kTrajBinThreads;
   for (int u0 = 0; u0 < per; u0 += U) {
     float2 d[U], p[U];
     int e[U], r[U];
     int64_t bj[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t j = j0 + (int64_t)(u0 + u) * kTileBinBlock + threadIdx.x;
+      const int64_t j = j0 + (int64_t)(u0 + u) * kTrajBinThreads + threadIdx.x;
       const bool in = u0 + u < per && j < g.N;
       r[u] = in ? (int)(j / N) : 0;
       e[u] = in ? (int)(j - (int64_t)r[u] * N) : -1;
@@ -1498,7 +1500,7 @@ constexpr int kTrajChunk = 8192;                  // records per accumulation wo
 bool traj_geo(int64_t K, int64_t B, int64_t Hg, int64_t Wg, int64_t m, TileGeo& g) {
   if (K < 3 || 2 * K > kMaxChannels || !tile_geo(kGrid, B, Hg, Wg, m, 0, 0, g) || g.T != kBinT) return false;
   g.C = (int)(2 * K);
-  const int64_t rpb = (int64_t)traj_bin_per(m) * kTileBinBlock;
+  const int64_t rpb = (int64_t)traj_bin_per(m) * kTrajBinThreads;
   g.nblk = (int)((m + rpb - 1) / rpb);
   return true;
 }
@@ -1782,11 +1784,11 @@ int atl_traj_field_bwd(const float* gd, const float* pos, const float* t, const 
   int* nchunk = (int*)(w + L.t.nchunk);
   const int per = traj_bin_per(m);
   const size_t lds = (size_t)g.nkeys * sizeof(int);
-  hipLaunchKernelGGL(k_traj_bin<false>, dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
+  hipLaunchKernelGGL(k_traj_bin<false>, dim3(g.nblk), dim3(kTrajBinThreads), lds, stream, (const float2*)pos,
                      (const float2*)gd, t, t_last, b, (int)N, (int)n_look, per, g, cnt, (float4*)nullptr,
                      (float*)nullptr);
   scan32t(cnt, g.nkeys, g.nblk, (int*)(w + L.t.part), boff, stream);
-  hipLaunchKernelGGL(k_traj_bin<true>, dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
+  hipLaunchKernelGGL(k_traj_bin<true>, dim3(g.nblk), dim3(kTrajBinThreads), lds, stream, (const float2*)pos,
                      (const float2*)gd, t, t_last, b, (int)N, (int)n_look, per, g, boff, rec, tr);
   hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)boff, g, kTrajChunk,
                      kTrajChunk, info, nchunk);
