@@ -202,6 +202,72 @@ def test_iwe_step_graph_replays_match_eager(kind):
             close_rel(N(q.grad), gr, 1e-4)
 
 
+def _hip_runtime():
+    """The HIP runtime this process already loaded (torch's), so the graph handles below belong to it."""
+    import ctypes
+    import os
+    with open("/proc/self/maps") as f:
+        for line in f:
+            path = line.split()[-1]
+            if os.path.basename(path).startswith("libamdhip64.so"):
+                return ctypes.CDLL(path)
+    return ctypes.CDLL("libamdhip64.so")
+
+
+def _graph_node_types(graph):
+    import ctypes
+    lib = _hip_runtime()
+    g = ctypes.c_void_p(int(graph.raw_cuda_graph()))
+    n = ctypes.c_size_t(0)
+    assert lib.hipGraphGetNodes(g, None, ctypes.byref(n)) == 0
+    nodes = (ctypes.c_void_p * max(n.value, 1))()
+    assert lib.hipGraphGetNodes(g, nodes, ctypes.byref(n)) == 0
+    types = []
+    for i in range(n.value):
+        kind = ctypes.c_int(-1)
+        assert lib.hipGraphNodeGetType(ctypes.c_void_p(nodes[i]), ctypes.byref(kind)) == 0
+        types.append(kind.value)
+    return types
+
+
+def test_iwe_step_graph_has_no_memset_node():
+    """The bench's captured IWE step (fused launches, then the backward seeded with ones) holds kernel nodes only:
+    no memset node (hipGraphNodeTypeMemset = 2), which gave wrong results on replays on these GPUs; every fill is a
+    kernel.  The graph is kept and inspected, not replayed."""
+    print("graph node types: iwe step", flush=True)
+    win = synth.small_window(seed=3, n=20000, H=40, W=48)
+    m = DenseLinearFlow(1, 40, 48, grid=(40, 48), init=torch.as_tensor(win.motion["grid"].astype(F32))).to(DEV)
+    ev = EventPacket.from_window(win, DEV)
+    cfg = IWEConfig(kernel="bilinear", sigma=0.0, mask_border=True)
+    prm = list(m.parameters())
+    ones = torch.ones(ev.n, device=DEV)
+
+    def body():
+        _, vals = iwe_at_events(ev, m, 0.5, cfg)
+        vals.backward(ones)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            for q in prm:
+                q.grad = None
+            body()
+    torch.cuda.current_stream().wait_stream(side)
+    for q in prm:
+        q.grad = None
+    graph = torch.cuda.CUDAGraph(keep_graph=True)
+    with torch.cuda.graph(graph):
+        body()
+    torch.cuda.synchronize()
+    types = _graph_node_types(graph)
+    graph.reset()
+    assert types, "no nodes captured"
+    print(f"{len(types)} nodes, types {sorted(set(types))}", flush=True)
+    assert 2 not in types, f"memset nodes in the captured step: {types.count(2)} of {len(types)}"
+    assert types.count(0) >= 8                     # the step's kernels
+
+
 def test_warp_splat_gather_rejects_bad_shapes():
     xy = torch.zeros(10, 2, device=DEV)
     t = torch.zeros(10, device=DEV)

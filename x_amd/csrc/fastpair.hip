@@ -1763,6 +1763,18 @@ __global__ void __launch_bounds__(kPairBlock) k_fast_bwd_traj(FPlan p, FGeo G, i
 // ------------------------------------------------------------------------------------------ host side
 int64_t align256(int64_t n) { return (n + 255) & ~(int64_t)255; }
 
+// Source tile edge in cells (about kSrcTilePx px) of a fine-cell size.
+inline int src_tile_cells(float cell) { return std::min(16, std::max(2, (int)std::lround(kSrcTilePx / (double)cell))); }
+
+// Bytes the flow adjoint keeps in the sort-record region: the per-source gradients, then its chunk list, chunk
+// count and tile record counts.
+inline int64_t adj_scratch_bytes(int64_t B, int64_t N, int64_t GW, int64_t GH, float cell) {
+  const int64_t st = src_tile_cells(cell);
+  const int64_t tiles = B * ((GW + st - 1) / st) * ((GH + st - 1) / st);
+  const int64_t maxc = tiles + (N + kAdjChunk - 1) / kAdjChunk;
+  return align256(N * 8) + maxc * (int64_t)sizeof(int2) + 64 * 4 + tiles * 4;
+}
+
 bool make_geo(const atl_fast_geometry* geo, FGeo& G) {
   if (!geo || geo->version != ATL_HIP_ABI_VERSION) return false;
   G.gx0 = geo->gx0; G.gy0 = geo->gy0; G.gx1 = geo->gx1; G.gy1 = geo->gy1; G.cf = geo->cell;
@@ -1787,7 +1799,7 @@ bool make_geo(const atl_fast_geometry* geo, FGeo& G) {
   // groups about kGroupWidth px wide whatever the cell size: a fixed cell count made groups of 3 px at h = 0.5,
   // where the per-pass set-up then dominates, and of 12 px at h = 2, where the box does
   G.gcells = std::min(16, std::max(1, (int)std::lround(kGroupWidth / (double)G.cf)));
-  G.stile = std::min(16, std::max(2, (int)std::lround(kSrcTilePx / (double)G.cf)));
+  G.stile = src_tile_cells(G.cf);
   return true;
 }
 
@@ -1874,7 +1886,6 @@ int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W
   g.ncell_pad = (int64_t)ncell_pad;
   g.ecap = (int64_t)ecap;
   const int64_t nbh = (int64_t)(nbuckets * nblk);
-  const int64_t ntmp = g.ecap + M + N;
   int64_t off = 0;
   // params and the bucket totals are adjacent: one fill clears both
   g.off_params = off;  off += align256(sizeof(FParams));
@@ -1882,7 +1893,11 @@ int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W
   g.off_boff = off;    off += align256((int64_t)nbuckets * 4);        // bucket positions, then bucket ends
   g.off_cnt = off;     off += align256(nbh * 4);                      // per-block histograms, block-major
   g.off_start = off;   off += align256((3 * g.ncell_pad + 1) * 4);
-  g.off_trec = off;    off += align256(ntmp * (int64_t)sizeof(Rec));
+  // the sort's records sit at their bucket positions in all three key spaces (the linear model's anchor and
+  // source records after the entries' counted places), so the region holds ecap + M + N records; after the plan
+  // it also serves the flow adjoint's scratch (per-source gradients, chunk list, tile counts)
+  g.off_trec = off;    off += align256(std::max((g.ecap + M + N) * (int64_t)sizeof(Rec),
+                                                adj_scratch_bytes(B, N, g.GW, g.GH, g.cell)));
   // the walks read up to kUnroll - 1 records past a range end: entry and anchor arrays carry that padding
   g.off_epos = off;    off += align256((g.ecap + kUnroll) * (int64_t)sizeof(float4));
   g.off_etim = off;    off += align256((g.ecap + kUnroll) * (int64_t)sizeof(float));
@@ -1963,7 +1978,7 @@ int fast_plan_impl(const atl_fast_geometry* geo, const FGeo& G, const float* x, 
     }
     auto erank = G.bshift == 10 ? k_entry_rank<10> : G.bshift == 11 ? k_entry_rank<11>
                : G.bshift == 12 ? k_entry_rank<12> : k_entry_rank<13>;
-    int2* sorted = item + geo->ecap;             // [ecap, ecap + E) of the items' space: 16 ecap <= 32 ntmp bytes
+    int2* sorted = item + geo->ecap;             // [ecap, ecap + E) of the items' space: 16 ecap <= 32 (ecap + M + N) bytes
     hipLaunchKernelGGL(erank, dim3(bpk), dim3(kSortBlock), 0, stream, (const int*)bpos, (const int*)tot,
                        (const int2*)item, sorted, out.start, G);
     const int64_t wblk = (geo->ecap + kBlock * kEntWrite - 1) / (kBlock * kEntWrite);
@@ -2075,7 +2090,7 @@ int atl_fast_flow_adjoint(const atl_fast_geometry* geo, void* ws, int64_t Hg, in
   F.sxw = (float)(img_w - 1 > 1 ? img_w - 1 : 1);
   F.syh = (float)(img_h - 1 > 1 ? img_h - 1 : 1);
   const int64_t tiles = geo->B * ((G.GW + G.stile - 1) / G.stile) * ((G.GH + G.stile - 1) / G.stile);
-  const int64_t maxc = tiles + (geo->N + kAdjChunk - 1) / kAdjChunk;   // chunks, at most
+  const int64_t maxc = tiles + (geo->N + kAdjChunk - 1) / kAdjChunk;   // chunks, at most (adj_scratch_bytes)
   int2* info = (int2*)(at_off<char>(ws, geo->off_trec) + align256(geo->N * 8));   // after the gradients
   int* nchunk = (int*)(info + maxc);
   int* tilecnt = nchunk + 64;
