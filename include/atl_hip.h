@@ -226,6 +226,15 @@ int atl_sample_grid_bwd_binned(const float* gout, int64_t B, int64_t C, int64_t 
 int atl_sample_grid_bwd_planned(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
                                 int64_t N, int64_t img_h, int64_t img_w, void* ws, float* gfield,
                                 hipStream_t stream);
+/* The field adjoint of a many-channel lookup (5 <= C <= 32, 16x16 tiles; gfield accumulated: zero it first),
+ * binned here (no plan): the records are sorted by tile, every workgroup sums its tile's records per base node in
+ * registers and writes its own nodes without global atomics (border row and column through a halo buffer in ws).
+ * ws: atl_sample_grid_bwd_rows_bytes(B, C, Hg, Wg, N) bytes (-1: unsupported).  The same corner products as
+ * atl_sample_grid_bwd (the adjoint of atl/motion/parametric.py:235-251), fused into the sums; other order. */
+int64_t atl_sample_grid_bwd_rows_bytes(int64_t B, int64_t C, int64_t Hg, int64_t Wg, int64_t N);
+int atl_sample_grid_bwd_rows(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                             const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gfield, void* ws,
+                             int64_t ws_bytes, hipStream_t stream);
 
 /* ---------------------------------------------------------------- event noise */
 

@@ -195,6 +195,38 @@ def test_traj_field_bwd_equals_the_row_adjoint(K, n_look, last, crowd):
     close_rel(N(got), 2 * N(want), 1e-6)
 
 
+@pytest.mark.parametrize("C,scale,crowd", [(5, False, 0), (12, True, 0), (20, False, 12000), (32, False, 0)])
+def test_sample_grid_bwd_rows_equals_the_per_event_adjoint(C, scale, crowd):
+    """atl_sample_grid_bwd_rows (binned in the call, per-node register sums, halo flush) against the per-event
+    atomic adjoint atl_sample_grid_bwd on the same rows: equal to the order of the float additions; positions past
+    every edge, pixel-to-grid scaling, and with crowd one tile holding that many records (several workgroups)."""
+    print(f"sample_grid_bwd_rows C={C} scale={scale} crowd={crowd}", flush=True)
+    rng = np.random.default_rng(200 + C + crowd)
+    n, B, Hg, Wg = 6000 + crowd, 2, 37, 53
+    H, W = (150, 212) if scale else (Hg, Wg)
+    pos = np.stack([rng.uniform(-3, W + 2, n), rng.uniform(-3, H + 2, n)], 1).astype(F32)
+    b = rng.integers(0, B, n).astype(np.int64)
+    if crowd:
+        pos[:crowd] = rng.uniform(16.0, 31.9, (crowd, 2))
+        b[:crowd] = 0
+    g = rng.standard_normal((n, C)).astype(F32)
+    g[rng.random(n) < 0.05] = 0.0
+    tg, tp, tb = T(g), T(pos), T(b)
+    ih, iw = (H, W) if scale else (0, 0)
+    st = F.stream_of(tp)
+    nbytes = int(F.load_library().atl_sample_grid_bwd_rows_bytes(B, C, Hg, Wg, n))
+    assert nbytes > 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    got = torch.zeros(B, C, Hg, Wg, device=DEV)
+    F.call("atl_sample_grid_bwd_rows", F.ptr(tg), B, C, Hg, Wg, F.ptr(tp), F.ptr(tb), n, ih, iw, F.ptr(got),
+           F.ptr(ws), nbytes, st)
+    want = torch.zeros_like(got)
+    F.call("atl_sample_grid_bwd", F.ptr(tg), B, C, Hg, Wg, F.ptr(tp), F.ptr(tb), n, ih, iw, F.ptr(want), st)
+    close_rel(N(got), N(want), 1e-6)
+    assert F.load_library().atl_sample_grid_bwd_rows_bytes(B, 4, Hg, Wg, n) == -1      # C <= 4: other paths
+    assert F.load_library().atl_sample_grid_bwd_rows_bytes(B, 33, Hg, Wg, n) == -1
+
+
 def test_traj_field_bwd_rejects_bad_sizes():
     """Sizes atl_traj_field_bwd does not take are refused before any launch (workspace query -1, call status 1)."""
     lib = F.load_library()

@@ -754,7 +754,9 @@ inline int traj_bin_per(int64_t m) {
   return (int)std::min<int64_t>(std::max<int64_t>(per, 8), 256);
 }
 
-template <bool SCATTER>
+// ROWS: the records of a many-channel sampler adjoint instead (one look-up per event, gd and the times unused):
+// (x, y, event index, 0), every record kept (the row is read by the accumulation).
+template <bool SCATTER, bool ROWS = false>
 __global__ void __launch_bounds__(kTrajBinThreads) k_traj_bin(const float2* __restrict__ pos,
                                                             const float2* __restrict__ gd,
                                                             const float* __restrict__ t,
@@ -778,7 +780,7 @@ __global__ void __launch_bounds__(kTrajBinThreads) k_traj_bin(const float2* __re
       const bool in = u0 + u < per && j < g.N;
       r[u] = in ? (int)(j / N) : 0;
       e[u] = in ? (int)(j - (int64_t)r[u] * N) : -1;
-      d[u] = in ? gd[j] : make_float2(0.f, 0.f);
+      d[u] = in && !ROWS ? gd[j] : make_float2(1.f, 0.f);
       p[u] = in ? pos[j] : make_float2(0.f, 0.f);
       bj[u] = in ? bidx[e[u]] : -1;
     }
@@ -788,7 +790,9 @@ __global__ void __launch_bounds__(kTrajBinThreads) k_traj_bin(const float2* __re
       const int key = tile_key<kGrid>(p[u].x, p[u].y, bj[u], g);
       if (key < 0) continue;
       const int slot = atomicAdd(hist + key, 1);
-      if (SCATTER) {
+      if (SCATTER && ROWS) {
+        rec[slot] = make_float4(p[u].x, p[u].y, __int_as_float(e[u]), 0.f);
+      } else if (SCATTER) {
         rec[slot] = make_float4(p[u].x, p[u].y, d[u].x, d[u].y);
         tr[slot] = t_last && r[u] == n_look - 1 ? t_last[e[u]] : t[e[u]];
       }
@@ -804,6 +808,25 @@ __global__ void __launch_bounds__(kTrajBinThreads) k_traj_bin(const float2* __re
 // (16), which belong to the tiles on its right, below and diagonally below.  Halo slot h: right column row h for
 // h <= 16, bottom row column h - 17 for h >= 17.
 constexpr int kHalo = 2 * kBinT + 1;
+
+// Window sums of channel group entries q at window node (lx, ly): the corner sums (table sb[(c G + q) kBins + base
+// node], corner c = 2 iy + ix) of the base nodes that reach the node (the second corner of an axis is the next
+// node, or the same one on a grid of a single column or row: sx, sy).
+template <int G>
+__device__ __forceinline__ void window_sum(const float* sb, int lx, int ly, int sx, int sy, float (&v)[G]) {
+#pragma unroll
+  for (int q = 0; q < G; ++q) v[q] = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int cx = lx - (c & 1) * sx, cy = ly - (c >> 1) * sy;
+    if ((unsigned)cx >= (unsigned)kBinT || (unsigned)cy >= (unsigned)kBinT) continue;
+#pragma unroll
+    for (int q = 0; q < G; ++q) v[q] += sb[(c * G + q) * kBins + cy * kBinT + cx];
+  }
+}
+
+// Halo slot of window node (lx, ly) past the tile's own 16 x 16 (lx == 16 or ly == 16).
+__device__ __forceinline__ int halo_slot(int lx, int ly) { return lx == kBinT ? ly : kBinT + 1 + lx; }
 
 // Accumulation of the trajectory records in the gather form.  Float atomic adds into LDS run at a small fraction
 // of the LDS rate on this part (~0.3 lane-adds per CU per cycle against ~8 for a plain read-modify-write), so no
@@ -929,9 +952,20 @@ __global__ void __launch_bounds__(kAccBlock) k_traj_tile_accum(const int4* __res
       }
     }
   }
-  __syncthreads();                               // the staging area becomes the corner-sum table
-  const int sx = g.W > 1 ? 1 : 0, sy = g.H > 1 ? 1 : 0;   // second corner: the next node, or the same one
+  // thread c adds the sums reaching its own node c (the node of base node c); threads 0..32 write the halo.
+  // A single-chunk tile reads its own nodes' previous values first, all channels in flight together.
+  const int oly = tid / T, olx = tid - oly * T;
+  const int opy = oy + oly, opx = ox + olx;
+  const bool oin = opy < g.H && opx < g.W;
   const int64_t pl = (int64_t)g.H * g.W;
+  float* const obase = out + (int64_t)b * nc * pl + (int64_t)opy * g.W + opx;
+  float prev[2][KM];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int k = 0; k < KM; ++k) prev[m][k] = !shared && oin && k < K ? obase[(int64_t)(m * K + k) * pl] : 0.f;
+  __syncthreads();                               // the staging area becomes the corner-sum table
+  const int sx = g.W > 1 ? 1 : 0, sy = g.H > 1 ? 1 : 0;
   constexpr int G = kTrajGroup;
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
@@ -943,38 +977,184 @@ __global__ void __launch_bounds__(kAccBlock) k_traj_tile_accum(const int4* __res
         for (int q = 0; q < G; ++q)
           if (k0 + q < KM) sb[(c * G + q) * kBins + tid] = s[c][m][k0 + q];
       __syncthreads();
-      for (int a = tid; a < L * L; a += kAccBlock) {   // window node a adds the base nodes that reach it
-        const int ly = a / L, lx = a - ly * L;
+      {
         float v[G];
-#pragma unroll
-        for (int q = 0; q < G; ++q) v[q] = 0.f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int cx = lx - (c & 1) * sx, cy = ly - (c >> 1) * sy;
-          if ((unsigned)cx >= (unsigned)T || (unsigned)cy >= (unsigned)T) continue;
-#pragma unroll
-          for (int q = 0; q < G; ++q) v[q] += sb[(c * G + q) * kBins + cy * T + cx];
-        }
-        const bool own = ly < T && lx < T;
-        const int py = oy + ly, px = ox + lx;
-        if (own && (py >= g.H || px >= g.W)) continue;
+        window_sum<G>(sb, olx, oly, sx, sy, v);
 #pragma unroll
         for (int q = 0; q < G; ++q) {
           const int k = k0 + q;
-          if (k >= K || v[q] == 0.f) continue;
-          const int ch = m * K + k;
-          float* o = own ? out + ((int64_t)b * nc + ch) * pl + (int64_t)py * g.W + px
-                         : halo + ((int64_t)key * nc + ch) * kHalo + (lx == T ? ly : T + 1 + lx);
+          if (k >= KM || k >= K || !oin || v[q] == 0.f) continue;
+          float* o = obase + (int64_t)(m * K + k) * pl;
           if (shared)
             atomicAdd(o, v[q]);
-          else if (own)
-            *o += v[q];
           else
-            *o = v[q];
+            *o = prev[m][k] + v[q];
+        }
+      }
+      if (tid < kHalo) {
+        const int lx = tid <= T ? T : tid - (T + 1), ly = tid <= T ? tid : T;
+        float v[G];
+        window_sum<G>(sb, lx, ly, sx, sy, v);
+#pragma unroll
+        for (int q = 0; q < G; ++q) {
+          const int k = k0 + q;
+          if (k >= KM || k >= K || v[q] == 0.f) continue;
+          float* h = halo + ((int64_t)key * nc + m * K + k) * kHalo + halo_slot(lx, ly);
+          if (shared)
+            atomicAdd(h, v[q]);
+          else
+            *h = v[q];
         }
       }
       __syncthreads();                           // the table is rewritten by the next group
     }
+  }
+}
+
+// The many-channel sampler adjoint (C in 5..32 channels, gout (N, C) rows) in the same form: thread c owns base
+// node c; per round of kRowsRound records the loading threads stage (ax, ay) and the record's gradient row
+// gout[j] in base-node order, and thread c adds fma(row, w, s) for every corner and channel of its node's records
+// (the scatter form's products go * w, fused); the window sums and the flush are k_traj_tile_accum's.
+constexpr int kRowsRound = 512;                  // records staged per round (two per thread)
+
+template <int CM>
+__global__ void __launch_bounds__(kAccBlock) k_rows_tile_accum(const int4* __restrict__ info,
+                                                               const int* __restrict__ nchunk,
+                                                               const float4* __restrict__ rec,
+                                                               const float* __restrict__ gout, TileGeo g,
+                                                               float* __restrict__ out, float* __restrict__ halo) {
+  constexpr int T = kBinT, L = T + 1, R = kRowsRound, U = R / kAccBlock;
+  constexpr int CP = (CM + 3) & ~3;              // row stride (16-byte rows)
+  constexpr int kStage = R * CP > 4 * kTrajGroup * kBins ? R * CP : 4 * kTrajGroup * kBins;
+  __shared__ int bcnt[kBins], bstart[kBins];
+  __shared__ int wsum[kAccBlock / kWave + 1];
+  __shared__ float2 sa[R];                       // (ax, ay) of the round's records, base-node order
+  __shared__ __align__(16) float sb[kStage];     // their gradient rows; after the rounds: the corner sums
+  if ((int)blockIdx.x >= *nchunk) return;
+  const int4 ci = info[blockIdx.x];
+  const int key = ci.x, s0 = ci.y, s1 = ci.z;
+  const bool shared = ci.w != 0;
+  const int tid = threadIdx.x;
+  const int nc = g.C;
+  const int plane = g.TY * g.TX;
+  const int b = key / plane, rr = key - b * plane;
+  const int ty = rr / g.TX, tx = rr - ty * g.TX;
+  const int ox = tx * T, oy = ty * T;
+  // a single-chunk tile's own node of this thread: its previous values, read now (in flight during the rounds)
+  const int oly = tid / T, olx = tid - oly * T;
+  const int opy = oy + oly, opx = ox + olx;
+  const bool oin = opy < g.H && opx < g.W;
+  const int64_t pl = (int64_t)g.H * g.W;
+  float* const obase = out + (int64_t)b * nc * pl + (int64_t)opy * g.W + opx;
+  float prev[CM];
+#pragma unroll
+  for (int k = 0; k < CM; ++k) prev[k] = !shared && oin && k < nc ? obase[(int64_t)k * pl] : 0.f;
+  float s[4][CM];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int k = 0; k < CM; ++k) s[c][k] = 0.f;
+  for (int base = s0; base < s1; base += R) {
+    float4 q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = base + u * kAccBlock + tid;
+      if (k < s1) q[u] = rec[k];
+    }
+    bcnt[tid] = 0;
+    __syncthreads();                             // the previous round's readers are done
+    int bin[U], rank[U];
+    float ax[U], ay[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      bin[u] = -1;
+      if (base + u * kAccBlock + tid >= s1) continue;
+      const GridCell c = grid_cell(q[u].x, q[u].y, g.H, g.W, g.sxw, g.syh, g.scale != 0);
+      const int bx = c.x0 - ox, by = c.y0 - oy;
+      if ((unsigned)bx < (unsigned)T && (unsigned)by < (unsigned)T) {   // always: the binning chose this tile
+        ax[u] = c.ax;
+        ay[u] = c.ay;
+        bin[u] = by * T + bx;
+        rank[u] = atomicAdd(bcnt + bin[u], 1);
+      }
+    }
+    __syncthreads();
+    const int mine = bcnt[tid];
+    int total;
+    const int first = block_exclusive_scan<kAccBlock>(mine, wsum, total);
+    bstart[tid] = first;
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (bin[u] < 0) continue;
+      const int p = bstart[bin[u]] + rank[u];
+      sa[p] = make_float2(ax[u], ay[u]);
+      const float* src = gout + (int64_t)__float_as_int(q[u].z) * nc;
+      float* row = sb + p * CP;
+      if (g.vec4) {                              // nc % 4 == 0, 16-byte aligned rows
+#pragma unroll
+        for (int k = 0; k < CP; k += 4)
+          *(float4*)(row + k) = k < nc ? *(const float4*)(src + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+#pragma unroll
+        for (int k = 0; k < CP; ++k) row[k] = k < nc ? src[k] : 0.f;
+      }
+    }
+    __syncthreads();
+    for (int p = first; p < first + mine; ++p) {
+      const float2 a = sa[p];
+      const float wx0 = 1.f - a.x, wy0 = 1.f - a.y;
+      const float w[4] = {wx0 * wy0, a.x * wy0, wx0 * a.y, a.x * a.y};
+      const float* row = sb + p * CP;
+#pragma unroll
+      for (int k = 0; k < CM; ++k) {
+        const float go = row[k];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s[c][k] = __fmaf_rn(go, w[c], s[c][k]);
+      }
+    }
+  }
+  __syncthreads();                               // the staging area becomes the corner-sum table
+  const int sx = g.W > 1 ? 1 : 0, sy = g.H > 1 ? 1 : 0;
+  constexpr int G = kTrajGroup;
+#pragma unroll
+  for (int k0 = 0; k0 < CM; k0 += G) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int q = 0; q < G; ++q)
+        if (k0 + q < CM) sb[(c * G + q) * kBins + tid] = s[c][k0 + q];
+    __syncthreads();
+    {
+      float v[G];
+      window_sum<G>(sb, olx, oly, sx, sy, v);
+#pragma unroll
+      for (int q = 0; q < G; ++q) {
+        const int ch = k0 + q;
+        if (ch >= CM || ch >= nc || !oin || v[q] == 0.f) continue;
+        float* o = obase + (int64_t)ch * pl;
+        if (shared)
+          atomicAdd(o, v[q]);
+        else
+          *o = prev[ch] + v[q];
+      }
+    }
+    if (tid < kHalo) {
+      const int lx = tid <= T ? T : tid - (T + 1), ly = tid <= T ? tid : T;
+      float v[G];
+      window_sum<G>(sb, lx, ly, sx, sy, v);
+#pragma unroll
+      for (int q = 0; q < G; ++q) {
+        const int ch = k0 + q;
+        if (ch >= CM || ch >= nc || v[q] == 0.f) continue;
+        float* h = halo + ((int64_t)key * nc + ch) * kHalo + halo_slot(lx, ly);
+        if (shared)
+          atomicAdd(h, v[q]);
+        else
+          *h = v[q];
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -1520,6 +1700,33 @@ TrajLayout traj_layout(const TileGeo& g) {
   return L;
 }
 
+// Many-channel sampler adjoint: geometry of N look-ups on a (B, C, Hg, Wg) grid, 5 <= C <= 32, 16 x 16 tiles.
+bool rows_geo(int64_t C, int64_t B, int64_t Hg, int64_t Wg, int64_t N, int64_t img_h, int64_t img_w, TileGeo& g) {
+  if (C < 5 || C > kMaxChannels || !tile_geo(kGrid, B, Hg, Wg, N, img_h, img_w, g) || g.T != kBinT) return false;
+  g.C = (int)C;
+  const int64_t rpb = (int64_t)traj_bin_per(N) * kTrajBinThreads;
+  g.nblk = (int)((N + rpb - 1) / rpb);
+  return true;
+}
+
+// Chunk list, halo clearing, accumulation and halo flush of the trajectory and many-channel adjoints.
+template <typename Accum>
+void tile_halo_accumulate(const TileGeo& g, const TrajLayout& L, char* w, int64_t m, float* gfield,
+                          hipStream_t stream, Accum accum) {
+  int4* info = (int4*)(w + L.t.info);
+  int* nchunk = (int*)(w + L.t.nchunk);
+  float* halo = (float*)(w + L.halo);
+  hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.t.boff), g,
+                     kTrajChunk, kTrajChunk, info, nchunk);
+  const int64_t nh = (int64_t)g.nkeys * g.C * kHalo;
+  hipLaunchKernelGGL(k_fill_zero_f, dim3(grid_for(nh)), dim3(kBlock), 0, stream, halo, nh);
+  const int64_t nchunks = (int64_t)g.nkeys + (m + kTrajChunk - 1) / kTrajChunk;   // ceil(len / chunk) per tile
+  accum((unsigned)nchunks, (const int4*)info, (const int*)nchunk, halo);
+  const int64_t nfix = (int64_t)g.nkeys * g.C * (2 * kBinT - 1);
+  hipLaunchKernelGGL(k_traj_halo_add, dim3(grid_for(nfix)), dim3(kBlock), 0, stream, (const float*)halo, g, g.C,
+                     gfield);
+}
+
 }  // namespace
 
 // ================================================================================================ C-ABI
@@ -1779,9 +1986,6 @@ int atl_traj_field_bwd(const float* gd, const float* pos, const float* t, const 
   int* boff = (int*)(w + L.t.boff);
   float4* rec = (float4*)(w + L.t.rec);
   float* tr = (float*)(w + L.tr);
-  float* halo = (float*)(w + L.halo);
-  int4* info = (int4*)(w + L.t.info);
-  int* nchunk = (int*)(w + L.t.nchunk);
   const int per = traj_bin_per(m);
   const size_t lds = (size_t)g.nkeys * sizeof(int);
   hipLaunchKernelGGL(k_traj_bin<false>, dim3(g.nblk), dim3(kTrajBinThreads), lds, stream, (const float2*)pos,
@@ -1790,29 +1994,76 @@ int atl_traj_field_bwd(const float* gd, const float* pos, const float* t, const 
   scan32t(cnt, g.nkeys, g.nblk, (int*)(w + L.t.part), boff, stream);
   hipLaunchKernelGGL(k_traj_bin<true>, dim3(g.nblk), dim3(kTrajBinThreads), lds, stream, (const float2*)pos,
                      (const float2*)gd, t, t_last, b, (int)N, (int)n_look, per, g, boff, rec, tr);
-  hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)boff, g, kTrajChunk,
-                     kTrajChunk, info, nchunk);
-  const int64_t nh = (int64_t)g.nkeys * g.C * kHalo;
-  hipLaunchKernelGGL(k_fill_zero_f, dim3(grid_for(nh)), dim3(kBlock), 0, stream, halo, nh);
-  const int64_t nchunks = (int64_t)g.nkeys + (m + kTrajChunk - 1) / kTrajChunk;   // ceil(len / chunk) per tile
-  auto accum = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3((unsigned)nchunks), dim3(kAccBlock), 0, stream, (const int4*)info,
-                       (const int*)nchunk, (const float4*)rec, (const float*)tr, g, (int)K, gfield, halo);
-  };
-  if (K <= 4)
-    accum(k_traj_tile_accum<4>);
-  else if (K <= 8)
-    accum(k_traj_tile_accum<8>);
-  else if (K <= 10)
-    accum(k_traj_tile_accum<10>);
-  else if (K <= 12)
-    accum(k_traj_tile_accum<12>);
-  else
-    accum(k_traj_tile_accum<16>);
-  const int64_t nfix = (int64_t)g.nkeys * g.C * (2 * kBinT - 1);
-  hipLaunchKernelGGL(k_traj_halo_add, dim3(grid_for(nfix)), dim3(kBlock), 0, stream, (const float*)halo, g, g.C,
-                     gfield);
+  tile_halo_accumulate(g, L, w, m, gfield, stream, [&](unsigned grid, const int4* info, const int* nchunk, float* halo) {
+    auto launch = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(kAccBlock), 0, stream, info, nchunk, (const float4*)rec,
+                         (const float*)tr, g, (int)K, gfield, halo);
+    };
+    if (K <= 4)
+      launch(k_traj_tile_accum<4>);
+    else if (K <= 8)
+      launch(k_traj_tile_accum<8>);
+    else if (K <= 10)
+      launch(k_traj_tile_accum<10>);
+    else if (K <= 12)
+      launch(k_traj_tile_accum<12>);
+    else
+      launch(k_traj_tile_accum<16>);
+  });
   return check_launch("traj_field_bwd");
+}
+
+int64_t atl_sample_grid_bwd_rows_bytes(int64_t B, int64_t C, int64_t Hg, int64_t Wg, int64_t N) {
+  TileGeo g;
+  if (!rows_geo(C, B, Hg, Wg, N, 0, 0, g)) return -1;
+  return traj_layout(g).bytes;
+}
+
+int atl_sample_grid_bwd_rows(const float* gout, int64_t B, int64_t C, int64_t Hg, int64_t Wg, const float* pos,
+                             const int64_t* b, int64_t N, int64_t img_h, int64_t img_w, float* gfield, void* ws,
+                             int64_t ws_bytes, hipStream_t stream) {
+  TileGeo g;
+  if (!rows_geo(C, B, Hg, Wg, N, img_h, img_w, g)) {
+    set_error("sample_grid_bwd_rows: bad sizes (5 <= C <= %d on grids of at most 16384 16x16 tiles)", kMaxChannels);
+    return 1;
+  }
+  const TrajLayout L = traj_layout(g);
+  if (!ws || ws_bytes < L.bytes) { set_error("sample_grid_bwd_rows: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
+  if (N == 0) return 0;
+  if (!gout || !pos || !b || !gfield) { set_error("sample_grid_bwd_rows: null argument"); return 1; }
+  g.vec4 = (C & 3) == 0 && (reinterpret_cast<uintptr_t>(gout) & 15) == 0;
+  char* w = (char*)ws;
+  int* cnt = (int*)(w + L.t.cnt);
+  int* boff = (int*)(w + L.t.boff);
+  float4* rec = (float4*)(w + L.t.rec);
+  const int per = traj_bin_per(N);
+  const size_t lds = (size_t)g.nkeys * sizeof(int);
+  hipLaunchKernelGGL((k_traj_bin<false, true>), dim3(g.nblk), dim3(kTrajBinThreads), lds, stream, (const float2*)pos,
+                     (const float2*)nullptr, (const float*)nullptr, (const float*)nullptr, b, (int)N, 1, per, g, cnt,
+                     (float4*)nullptr, (float*)nullptr);
+  scan32t(cnt, g.nkeys, g.nblk, (int*)(w + L.t.part), boff, stream);
+  hipLaunchKernelGGL((k_traj_bin<true, true>), dim3(g.nblk), dim3(kTrajBinThreads), lds, stream, (const float2*)pos,
+                     (const float2*)nullptr, (const float*)nullptr, (const float*)nullptr, b, (int)N, 1, per, g, boff,
+                     rec, (float*)nullptr);
+  tile_halo_accumulate(g, L, w, N, gfield, stream, [&](unsigned grid, const int4* info, const int* nchunk, float* halo) {
+    auto launch = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(kAccBlock), 0, stream, info, nchunk, (const float4*)rec, gout, g,
+                         gfield, halo);
+    };
+    if (C <= 8)
+      launch(k_rows_tile_accum<8>);
+    else if (C <= 12)
+      launch(k_rows_tile_accum<12>);
+    else if (C <= 16)
+      launch(k_rows_tile_accum<16>);
+    else if (C <= 20)
+      launch(k_rows_tile_accum<20>);
+    else if (C <= 24)
+      launch(k_rows_tile_accum<24>);
+    else
+      launch(k_rows_tile_accum<32>);
+  });
+  return check_launch("sample_grid_bwd_rows");
 }
 
 // Warp -> splat -> gather (the fused pipeline above).  Workspace bytes, or -1 for unsupported sizes.

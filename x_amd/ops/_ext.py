@@ -46,6 +46,8 @@ _SIGS = {
     "atl_traj_origin_bwd": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P],
     "atl_traj_field_bwd_planned": [_P, _P, _I, _I, _I, _I, _I, _P, _P, _P],
     "atl_traj_field_bwd_bytes": [_I, _I, _I, _I, _I],
+    "atl_sample_grid_bwd_rows_bytes": [_I, _I, _I, _I, _I],
+    "atl_sample_grid_bwd_rows": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _P],
     "atl_traj_field_bwd": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P],
     "atl_traj_pos_bwd_cl": [_P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _P],
     "atl_traj_gout": [_P, _P, _I, _I, _I, _P, _P],
@@ -112,6 +114,7 @@ _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.
             "atl_anchored_score_mean_scratch_bytes": ctypes.c_int64, "atl_knn_ws_bytes": ctypes.c_int64,
             "atl_voxel_ws_bytes": ctypes.c_int64, "atl_warp_splat_gather_ws_bytes": ctypes.c_int64,
             "atl_ats_pair_ws_bytes": ctypes.c_int64, "atl_traj_field_bwd_bytes": ctypes.c_int64,
+            "atl_sample_grid_bwd_rows_bytes": ctypes.c_int64,
 "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):
@@ -167,7 +170,7 @@ _EVERY = {"n": 1, "calls": {}}   # time one call in n of each entry point
 # position of the event count N in the arguments of the entry points whose calls are sized by it
 _NARG = {"atl_sample_grid_fwd": 7, "atl_sample_grid_bwd_planned": 6, "atl_sample_grid_bwd_binned": 7, "atl_sample_grid_bwd_pos": 8,
          "atl_sample_grid_fwd_cl": 7, "atl_sample_flow_il": 6, "atl_sample_grid_bwd_pos_cl": 8, "atl_traj_displacement": 9,
-         "atl_traj_gout": 2, "atl_traj_field_bwd_planned": 6, "atl_traj_field_bwd": 5, "atl_traj_origin": 9, "atl_traj_origin_bwd": 9, "atl_traj_pos_bwd_cl": 9,
+         "atl_traj_gout": 2, "atl_traj_field_bwd_planned": 6, "atl_traj_field_bwd": 5, "atl_sample_grid_bwd_rows": 7, "atl_traj_origin": 9, "atl_traj_origin_bwd": 9, "atl_traj_pos_bwd_cl": 9,
          "atl_splat_gauss_fwd": 3, "atl_splat_gauss_bwd": 4, "atl_splat_gauss_fwd_ws": 3,
          "atl_gather_bilinear_fwd": 3, "atl_gather_bilinear_bwd_ws": 4, "atl_splat_bilinear_fwd_ws": 3,
          "atl_splat_bilinear_bwd": 4, "atl_voxel_grid_ws": 4, "atl_voxel_grid": 4,

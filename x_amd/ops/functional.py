@@ -240,7 +240,9 @@ class _SampleGrid(torch.autograd.Function):
                      ptr(out), st)
             ctx.cl = cl
             ctx.binned = bool(plan) and C <= 2 and int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N)) >= 0
-            if plan and not ctx.binned and _tile_plan_ok(B, C, Hg, Wg):
+            # many channels: binned in the backward (records sorted by tile, per-node sums, halo flush)
+            ctx.rows = bool(plan) and C > 4 and int(load_library().atl_sample_grid_bwd_rows_bytes(B, C, Hg, Wg, N)) >= 0
+            if plan and not ctx.binned and not ctx.rows and _tile_plan_ok(B, C, Hg, Wg):
                 nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N))
                 if nbytes >= 0:
                     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=pos.device)
@@ -259,7 +261,13 @@ class _SampleGrid(torch.autograd.Function):
         with torch.cuda.device(pos.device):
             if ctx.needs_input_grad[0]:
                 gf = torch.zeros(B, C, Hg, Wg, device=pos.device, dtype=F32)
-                if ctx.binned:
+                if ctx.rows:
+                    N = pos.shape[0]
+                    nbytes = int(load_library().atl_sample_grid_bwd_rows_bytes(B, C, Hg, Wg, N))
+                    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=pos.device)
+                    call("atl_sample_grid_bwd_rows", ptr(g), B, C, Hg, Wg, ptr(pos), ptr(b), N, ctx.img[0],
+                         ctx.img[1], ptr(gf), ptr(ws), nbytes, stream_of(pos))
+                elif ctx.binned:
                     N = pos.shape[0]
                     nbytes = int(load_library().atl_grid_plan_bytes(B, Hg, Wg, N))
                     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=pos.device)
