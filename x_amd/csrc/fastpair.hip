@@ -78,7 +78,12 @@ struct FGeo {
   float cuth;                  // cut * h
   int gcells;                  // forward groups: cells of one row per group
   int stile;                   // source order: tiles of stile x stile cells (about kSrcTilePx px)
+  int vplanes;                 // B * S <= kMaxPlanes: the plan keeps every (batch, slice) plane's max ||v||
 };
+
+// Planes (batch, slice) whose largest entry velocity the plan keeps (after FParams in the workspace): the
+// forward's walks around anchors of plane (b, s) then use that plane's bound instead of the global one.
+constexpr int kMaxPlanes = 1024;
 
 // Device scalars written by the plan (ordered-int encodings of non-negative floats).
 struct FParams {
@@ -87,8 +92,11 @@ struct FParams {
   int dup;                     // non-zero if an event occurs more than once among the anchors
   int unique;                  // non-zero if the anchors are every event in order (no index array): no repeats
   int nonfinite;               // non-zero if a backward record (anchor position, time or gS) is not finite
-  int pad[3];
-};
+  int planes;                  // non-zero if the per-plane maxima below were written (trajectory plans)
+  int pad[2];
+};                             // followed by B * S ints (ordered): each plane's max ||v|| when `planes`
+
+__device__ __forceinline__ int* plane_vmax(const FParams* P) { return (int*)(P + 1) ; }
 
 // One 32-byte record per sorted item, written with a single scattered line (separate arrays would cost one
 // scattered cache line each, and scattered lines are what the sort pays for):
@@ -278,8 +286,14 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
                                                        const float* __restrict__ tab) {
   extern __shared__ int hist[];
   __shared__ int red[kP1Block / kWave];
+  __shared__ int vpl[kMaxPlanes];                // the block's max ||v|| per (batch, slice) plane (count pass)
   int vm = 0;                                    // this thread's max ||v|| (sources) or max |at| (anchors)
   const int blk = blockIdx.x;
+  // the trajectory model's velocities differ by slice and trajectory (the fastest few set the global bound); the
+  // linear model's per-plane maxima bought nothing measurable and cost the count pass contended LDS atomics
+  const int nplanes = !SCATTER && K > 0 && G.vplanes ? (int)G.B * G.S : 0;
+  for (int i = threadIdx.x; i < nplanes; i += blockDim.x) vpl[i] = 0;
+  if (nplanes && blk == 0 && threadIdx.x == 0) P->planes = 1;
   int* __restrict__ mycnt = cnt + (int64_t)blk * G.nbuckets;
   const int bpk = G.ncell_pad >> G.bshift;       // buckets per key space (the entries' buckets come first)
   for (int i = threadIdx.x; i < G.nbuckets; i += blockDim.x) {
@@ -319,7 +333,11 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
       for (int s = lo; s <= hi; ++s) {
         float yx, yy, vx, vy;
         traj_entry<KK>(cf, pj.x, pj.y, tab, s, yx, yy, vx, vy);
-        if (!SCATTER) vm = max(vm, float_to_ordered(sqrtf(vx * vx + vy * vy)));
+        if (!SCATTER) {
+          const int vo = float_to_ordered(sqrtf(vx * vx + vy * vy));
+          vm = max(vm, vo);
+          if (nplanes) atomicMax(vpl + (int)bj * G.S + s, vo);
+        }
         const int key = entry_key_at(yx, yy, (int)bj, s, G);
         const int slot = atomicAdd(hist + (key >> G.bshift), 1);
         int sslot = -1, skey = -1;
@@ -477,6 +495,9 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
       for (int w = 1; w < kP1Block / kWave; ++w) vm = max(vm, red[w]);
       if (vm > 0) atomicMax(src_blk ? &P->vmax : &P->atmax, vm);
     }
+    if (src_blk)
+      for (int i = threadIdx.x; i < nplanes; i += blockDim.x)
+        if (vpl[i] > 0) atomicMax(plane_vmax(P) + i, vpl[i]);
   }
 }
 
@@ -1214,6 +1235,8 @@ __global__ void __launch_bounds__(kPairBlock) k_fast_fwd(FPlan p, FGeo G, int M,
   R = unif(R);
   R2 = unif(R2);
   const float vmax = unif(ordered_to_float(p.P->vmax));
+  const int* vpl = plane_vmax(p.P);
+  const bool planes = G.vplanes && uni(p.P->planes) != 0;
   const bool have = lane < n;
   const int q = wbase + min(lane, n - 1);
   const Rec AR = p.arec[q];
@@ -1231,6 +1254,8 @@ __global__ void __launch_bounds__(kPairBlock) k_fast_fwd(FPlan p, FGeo G, int M,
     const int cyx = rdlane(ai.w, i);               // the group's cell, packed by the plan (no divisions)
     const int cy = cyx >> 16, cx = cyx & 0xffff;
     const int plane = gkey - (cy * G.GW + cx);
+    // the plane's own velocity bound (its entries only are candidates); NaN keeps the global one
+    const float vg = planes ? fminf(vmax, ordered_to_float(vpl[plane / plane_cells])) : vmax;
     // the group: anchors of up to G.gcells consecutive cells of one row (lanes i .. i + gsize - 1)
     const int span = min(G.gcells, G.GW - cx);
     const uint64_t gmask = __ballot(have && key >= gkey && key - gkey < span) & todo;
@@ -1239,17 +1264,17 @@ __global__ void __launch_bounds__(kPairBlock) k_fast_fwd(FPlan p, FGeo G, int M,
     for (int a0 = 0; a0 < gsize; a0 += kGroup) {
       const int na = min(kGroup, gsize - a0);
       if (na == 1)
-        fwd_pass<1, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<1, COUNT>(p, G, plane, R, R2, vg, A, es, i + a0, na, lane, mine, mine_n);
       else if (na == 2)
-        fwd_pass<2, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<2, COUNT>(p, G, plane, R, R2, vg, A, es, i + a0, na, lane, mine, mine_n);
       else if (na == 3)
-        fwd_pass<3, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<3, COUNT>(p, G, plane, R, R2, vg, A, es, i + a0, na, lane, mine, mine_n);
       else if (na == 4)
-        fwd_pass<4, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<4, COUNT>(p, G, plane, R, R2, vg, A, es, i + a0, na, lane, mine, mine_n);
       else if (na <= 6)
-        fwd_pass<6, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<6, COUNT>(p, G, plane, R, R2, vg, A, es, i + a0, na, lane, mine, mine_n);
       else
-        fwd_pass<kGroup, COUNT>(p, G, plane, R, R2, vmax, A, es, i + a0, na, lane, mine, mine_n);
+        fwd_pass<kGroup, COUNT>(p, G, plane, R, R2, vg, A, es, i + a0, na, lane, mine, mine_n);
     }
   }
   if (have) {
@@ -1644,7 +1669,7 @@ __global__ void __launch_bounds__(kAdjBlock) k_src_flow_adjoint(FPlan p, FGeo G,
 // gcoef[j, k] = sum_s (Gy_s g_k(c_s) + Gv_s g_k'(c_s)) per axis (channels [y_1..y_K, x_1..x_K]).  Each source's
 // gradients are complete in its lanes and written once, without atomics.
 template <int K, bool DUP>
-__device__ __forceinline__ void bwd_traj_source(const FPlan& p, const FGeo& G, float R, float R2, float px,
+__device__ __forceinline__ void bwd_traj_source(const FPlan& p, const FGeo& G, float R, float R2, float atmax, float px,
                                                 float py, const float (&cf)[2 * K], const float* __restrict__ tab,
                                                 int sid, float tj, int key, int sp, int part, int2* rowtab,
                                                 float (&gc)[2 * K], float& gpx, float& gpy) {
@@ -1666,8 +1691,18 @@ __device__ __forceinline__ void bwd_traj_source(const FPlan& p, const FGeo& G, f
     traj_entry<K>(cf, px, py, tab, s, yx, yy, vx, vy);
     const float cs = slice_centre(s, G.delta);
     const float qx = clampf(yx, G.gx0, G.gx1), qy = clampf(yy, G.gy0, G.gy1);
+    // this entry's own search radius: its pairs lie within cut h + |v_s| max|at| of y_s (the global R takes the
+    // largest velocity of all entries); the same slack as search_radius
+    float Rs = R, R2s = R2;
+    {
+      const float rs = G.cuth * 1.000001f + sqrtf(vx * vx + vy * vy) * atmax * 1.000001f + 0.01f;
+      if (rs < R) {                                // false for NaN / inf velocities: keep the global walk
+        Rs = rs;
+        R2s = rs * rs;
+      }
+    }
     float gyx = 0.f, gyy = 0.f, gvx = 0.f, gvy = 0.f;
-    walk_flat(astart, E, (bj * G.S + s) * plane_cells, qx, qy, R, R2, G, rowtab, [&](int k, int e, auto step) {
+    walk_flat(astart, E, (bj * G.S + s) * plane_cells, qx, qy, Rs, R2s, G, rowtab, [&](int k, int e, auto step) {
       constexpr int U = decltype(step)::value;
       float4 A[U];
       int id[U];
@@ -1739,12 +1774,13 @@ __global__ void __launch_bounds__(kPairBlock) k_fast_bwd_traj(FPlan p, FGeo G, i
   const int sp = p.self[si.y];
   float gpx = 0.f, gpy = 0.f;
   if (have) {
+    const float atmax = unif(ordered_to_float(p.P->atmax));
     if (uni(p.P->dup))
-      bwd_traj_source<K, true>(p, G, R, R2, SR.f.x, SR.f.y, cf, tab, si.y, tj, si.z, sp, part, rowtab + threadIdx.x,
-                               gc, gpx, gpy);
+      bwd_traj_source<K, true>(p, G, R, R2, atmax, SR.f.x, SR.f.y, cf, tab, si.y, tj, si.z, sp, part,
+                               rowtab + threadIdx.x, gc, gpx, gpy);
     else
-      bwd_traj_source<K, false>(p, G, R, R2, SR.f.x, SR.f.y, cf, tab, si.y, tj, si.z, sp, part, rowtab + threadIdx.x,
-                                gc, gpx, gpy);
+      bwd_traj_source<K, false>(p, G, R, R2, atmax, SR.f.x, SR.f.y, cf, tab, si.y, tj, si.z, sp, part,
+                                rowtab + threadIdx.x, gc, gpx, gpy);
   }
 #pragma unroll
   for (int o = kSrcPerWave; o < kWave; o <<= 1) {  // the parts of a source sit kSrcPerWave lanes apart
@@ -1800,6 +1836,7 @@ bool make_geo(const atl_fast_geometry* geo, FGeo& G) {
   // where the per-pass set-up then dominates, and of 12 px at h = 2, where the box does
   G.gcells = std::min(16, std::max(1, (int)std::lround(kGroupWidth / (double)G.cf)));
   G.stile = src_tile_cells(G.cf);
+  G.vplanes = geo->B * geo->S <= kMaxPlanes;
   return true;
 }
 
@@ -1888,7 +1925,7 @@ int atl_fast_geometry_init(int64_t N, int64_t M, int64_t B, int64_t H, int64_t W
   const int64_t nbh = (int64_t)(nbuckets * nblk);
   int64_t off = 0;
   // params and the bucket totals are adjacent: one fill clears both
-  g.off_params = off;  off += align256(sizeof(FParams));
+  g.off_params = off;  off += align256(sizeof(FParams) + (B * S <= kMaxPlanes ? B * S * 4 : 0));
   g.off_part = off;    off += align256((int64_t)nbuckets * 4);        // bucket totals
   g.off_boff = off;    off += align256((int64_t)nbuckets * 4);        // bucket positions, then bucket ends
   g.off_cnt = off;     off += align256(nbh * 4);                      // per-block histograms, block-major
