@@ -267,6 +267,16 @@ int atl_plan_fill(const float* x, const float* t, const float* v, const int64_t*
                   double ox, double oy, double cell, double tau, int64_t S, int64_t GH, int64_t GW,
                   const int64_t* start, int* cursor, float* src_y, float* src_v, float* src_t, int64_t* src_id,
                   hipStream_t stream);
+/* The plan's entries and CSR offsets (functional.py:149-168) in one call, by a two-level counting sort (no
+ * per-entry global atomics): start (ncell+1) int64 and the entries src_y (,2), src_v (,2), src_t, src_id written at
+ * [0, E), E = start[ncell]; the entry arrays hold ecap >= N * (floor((2 tau + 1/S) S) + 2, at most S) entries.
+ * The same keys, slice positions and offsets as atl_plan_count + atl_scan_counts + atl_plan_fill; entry order
+ * inside one cell unspecified.  ws: atl_plan_sort_bytes(N, ecap, ncell) bytes (-1: unsupported sizes). */
+int64_t atl_plan_sort_bytes(int64_t N, int64_t ecap, int64_t ncell);
+int atl_plan_sort(const float* x, const float* t, const float* v, const int64_t* b, int64_t N, int64_t B, double ox,
+                  double oy, double cell, double tau, int64_t S, int64_t GH, int64_t GW, int64_t ecap,
+                  int64_t* start, float* src_y, float* src_v, float* src_t, int64_t* src_id, void* ws,
+                  int64_t ws_bytes, hipStream_t stream);
 /* Anchor fields of the plan (functional.py:169-177): anc_x (M,2), anc_t (M), anc_cell (M,3), anc_id (M).
  * anchor_xy may be null (positions x[anchors]). */
 int atl_plan_anchors(const float* x, const float* t, const int64_t* b, const int64_t* anchors,

@@ -404,6 +404,54 @@ def test_plan_bit_exact(tau, S, h):
         assert np.array_equal(N(getattr(q, f)), p[f]), f
 
 
+@pytest.mark.parametrize("n,B,H,W,tau,S", [(20000, 2, 40, 48, 0.2, 16), (30000, 4, 480, 640, 0.05, 96),
+                                            (7, 1, 40, 48, 0.3, 8)])
+def test_sorted_plan_equals_the_atomic_plan(n, B, H, W, tau, S):
+    """atl_plan_sort (bucketed counting sort, one call) against atl_plan_count + atl_scan_counts + atl_plan_fill
+    (per-entry atomics) on the same geometry: cell_start bit for bit, the same (cell, source) entries with the same
+    slice positions, velocities and times; events of an absent batch and positions leaving the grid are dropped by
+    both.  The second case has about 9M cells (buckets of 1024 keys), the third seven events."""
+    print(f"sorted plan n={n} B={B} {H}x{W} tau={tau} S={S}", flush=True)
+    rng = np.random.default_rng(n + S)
+    x = np.stack([rng.uniform(-30, W + 30, n), rng.uniform(-30, H + 30, n)], 1).astype(F32)
+    t = np.sort(rng.uniform(0, 1, n)).astype(F32)
+    v = rng.normal(0, 15, (n, 2)).astype(F32)
+    b = rng.integers(0, B, n).astype(np.int64)
+    b[::97] = B                                    # absent batch
+    tx, tt, tv, tb = T(x), T(t), T(v), T(b)
+    cell, ox, oy = 3.2, -5.0, -4.0
+    GW, GH = int(np.ceil((W + 10) / cell)) + 1, int(np.ceil((H + 8) / cell)) + 1
+    ncell = B * S * GH * GW
+    lib = F.load_library()
+    st = F.stream_of(tx)
+    ecap = n * min(int(np.floor((2 * tau + 1 / S) * S)) + 2, S)
+    nbytes = int(lib.atl_plan_sort_bytes(n, ecap, ncell))
+    assert nbytes > 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    cs1 = torch.empty(ncell + 1, dtype=torch.int64, device=DEV)
+    out1 = [torch.empty(ecap, 2, device=DEV), torch.empty(ecap, 2, device=DEV), torch.empty(ecap, device=DEV),
+            torch.empty(ecap, dtype=torch.int64, device=DEV)]
+    F.call("atl_plan_sort", F.ptr(tx), F.ptr(tt), F.ptr(tv), F.ptr(tb), n, B, ox, oy, cell, tau, S, GH, GW, ecap,
+           F.ptr(cs1), *[F.ptr(a) for a in out1], F.ptr(ws), nbytes, st)
+    counts = torch.zeros(ncell, dtype=torch.int32, device=DEV)
+    F.call("atl_plan_count", F.ptr(tx), F.ptr(tt), F.ptr(tv), F.ptr(tb), n, B, ox, oy, cell, tau, S, GH, GW,
+           F.ptr(counts), st)
+    cs2 = F._scan(counts)
+    E = int(cs2[-1])
+    assert torch.equal(cs1, cs2) and E > 0
+    out2 = [torch.empty(E, 2, device=DEV), torch.empty(E, 2, device=DEV), torch.empty(E, device=DEV),
+            torch.empty(E, dtype=torch.int64, device=DEV)]
+    counts.zero_()
+    F.call("atl_plan_fill", F.ptr(tx), F.ptr(tt), F.ptr(tv), F.ptr(tb), n, B, ox, oy, cell, tau, S, GH, GW,
+           F.ptr(cs2), F.ptr(counts), *[F.ptr(a) for a in out2], st)
+    key = np.repeat(np.arange(ncell), np.diff(N(cs2)))
+    k1, i1, o1 = _cellwise_sorted(key, N(out1[3][:E]))
+    k2, i2, o2 = _cellwise_sorted(key, N(out2[3]))
+    assert np.array_equal(i1, i2)
+    for a1, a2 in zip(out1[:3], out2[:3]):
+        assert np.array_equal(N(a1[:E])[o1], N(a2)[o2])
+
+
 @pytest.mark.parametrize("tau,S,h", [(0.2, 16, 1.0), (1.0, 8, 1.5), (0.05, 4, 0.5)])
 def test_pair_sums_match_oracle(tau, S, h):
     win, xs, v, anchors, xa = _pair_case(seed=2, h=h)

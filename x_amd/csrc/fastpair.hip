@@ -336,7 +336,8 @@ __global__ void __launch_bounds__(kP1Block) k_sort_pass1(const float2* __restric
         if (!SCATTER) {
           const int vo = float_to_ordered(sqrtf(vx * vx + vy * vy));
           vm = max(vm, vo);
-          if (nplanes) atomicMax(vpl + (int)bj * G.S + s, vo);
+          // the lanes of a wave mostly share a plane: the atomic only where the running maximum is exceeded
+          if (nplanes && vo > vpl[(int)bj * G.S + s]) atomicMax(vpl + (int)bj * G.S + s, vo);
         }
         const int key = entry_key_at(yx, yy, (int)bj, s, G);
         const int slot = atomicAdd(hist + (key >> G.bshift), 1);

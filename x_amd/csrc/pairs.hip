@@ -146,6 +146,181 @@ __global__ void __launch_bounds__(kBlock) k_plan_fill(const float2* __restrict__
   }
 }
 
+// The same plan by a two-level counting sort instead of one global atomic per entry for the counts and another
+// for the cursor (k_plan_count, k_plan_fill: about 25 G scattered atomics/s on this part).  Buckets of 2^shift
+// consecutive cell keys.  Pass A (COUNT): every block of kPsPer * kPsBlock sources counts its entries per bucket
+// in LDS, writes the row (cnt, block-major) and adds its non-zero counts into the bucket totals; one workgroup
+// scans the totals into bucket positions.  Pass A (SCATTER): the block reserves its run of every bucket it feeds
+// with one atomic add on the bucket's position (which ends as the bucket's end) and writes one 32-byte record per
+// entry, (y, v | key, source, t): y = x + v (c_s - t) as source_cell computes it, so pass B gathers nothing.
+// Pass B: one workgroup per bucket counts its records per cell in LDS, scans them into the bucket's part of
+// cell_start (the CSR offsets of the old path, bit for bit) and writes every entry at its cell's next slot.
+// Entry order within a cell is arrival order, unspecified as before.
+constexpr int kPsBlock = 512;
+constexpr int kPsPer = 8;                          // sources per thread and pass-A block
+constexpr int kPsScanBlock = 1024;
+constexpr int kPsMaxBuckets = 16 * kPsScanBlock;
+constexpr int kPsMinShift = 7;                     // 128 cells per bucket at least: many pass-B workgroups
+constexpr int kPsMaxShift = 12;                    // pass B: at most 4096 cells per bucket (16 KB of LDS)
+constexpr int kPsItems = 4;                        // pass B: records per thread in flight together
+
+struct PsRec {
+  float4 f;                                        // y.x, y.y, v.x, v.y
+  int4 i;                                          // key, source, t bits, 0
+};
+
+template <bool SCATTER>
+__global__ void __launch_bounds__(kPsBlock) k_psort_pass_a(const float2* __restrict__ x, const float* __restrict__ t,
+                                                         const float2* __restrict__ v,
+                                                         const int64_t* __restrict__ b, int64_t N, PlanGeo g,
+                                                         int shift, int nbuckets, int* __restrict__ cnt,
+                                                         int* __restrict__ tot_or_pos, PsRec* __restrict__ rec) {
+  extern __shared__ int hist[];
+  const int blk = blockIdx.x;
+  int* mycnt = cnt + (int64_t)blk * nbuckets;
+  for (int i = threadIdx.x; i < nbuckets; i += blockDim.x) {
+    int h = 0;
+    if (SCATTER) {
+      const int c = mycnt[i];
+      if (c > 0) h = atomicAdd(tot_or_pos + i, c);  // this block's run of bucket i
+    }
+    hist[i] = h;
+  }
+  __syncthreads();
+  const int64_t j0 = (int64_t)blk * (kPsPer * kPsBlock) + threadIdx.x;
+  for (int u = 0; u < kPsPer; ++u) {
+    const int64_t j = j0 + (int64_t)u * kPsBlock;
+    if (j >= N) break;
+    const int64_t bj = b[j];
+    if (bj < 0 || bj >= g.B) continue;
+    const float tj = t[j];
+    const float2 xj = x[j], vj = v[j];
+    int lo, hi;
+    slice_range(tj, g, lo, hi);
+    for (int s = lo; s <= hi; ++s) {
+      float2 y;
+      int cx, cy;
+      if (!source_cell(xj, vj, tj, slice_centre(s, g.delta), g, y, cx, cy)) continue;
+      const int key = (int)((((int)bj * g.S + s) * (int64_t)g.GH + cy) * g.GW + cx);
+      const int slot = atomicAdd(hist + (key >> shift), 1);
+      if (SCATTER) {
+        PsRec r;
+        r.f = make_float4(y.x, y.y, vj.x, vj.y);
+        r.i = make_int4(key, (int)j, __float_as_int(tj), 0);
+        rec[slot] = r;
+      }
+    }
+  }
+  if (!SCATTER) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < nbuckets; i += blockDim.x) {
+      const int c = hist[i];
+      mycnt[i] = c;
+      if (c > 0) atomicAdd(tot_or_pos + i, c);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kPsBlock) k_psort_pass_b(const PsRec* __restrict__ rec, const int* __restrict__ bend,
+                                                         const int* __restrict__ tot, int shift, int64_t ncell,
+                                                         int nbuckets, int64_t* __restrict__ start,
+                                                         float2* __restrict__ src_y, float2* __restrict__ src_v,
+                                                         float* __restrict__ src_t, int64_t* __restrict__ src_id) {
+  __shared__ int cur[1 << kPsMaxShift];
+  __shared__ int wsum[kPsBlock / kWave + 1];
+  const int bk = blockIdx.x;
+  const int nk = 1 << shift;                       // cells of a bucket
+  const int hi = bend[bk], lo = hi - tot[bk];
+  const int base = bk << shift;
+  const int4* tki = (const int4*)rec;              // int half of record p: tki[2 p + 1]
+  for (int i = threadIdx.x; i < nk; i += kPsBlock) cur[i] = 0;
+  __syncthreads();
+  for (int k = lo + (int)threadIdx.x; k < hi; k += kPsBlock) atomicAdd(cur + (tki[2 * k + 1].x - base), 1);
+  __syncthreads();
+  const int per = nk > kPsBlock ? nk / kPsBlock : 1;   // cells per thread in the scan
+  const int c0 = threadIdx.x * per;
+  int sum = 0;
+  for (int q = 0; q < per; ++q) sum += c0 + q < nk ? cur[c0 + q] : 0;
+  int total;
+  int run = block_exclusive_scan<kPsBlock>(sum, wsum, total);
+  for (int q = 0; q < per; ++q) {
+    const int c = c0 + q;
+    if (c >= nk) break;
+    const int n = cur[c];
+    cur[c] = lo + run;                             // the cell's next slot
+    if ((int64_t)base + c < ncell) start[(int64_t)base + c] = lo + run;
+    run += n;
+  }
+  if (bk == nbuckets - 1 && threadIdx.x == 0) start[ncell] = hi;
+  __syncthreads();
+  for (int k0 = lo; k0 < hi; k0 += kPsItems * kPsBlock) {
+    PsRec r[kPsItems];
+    int at[kPsItems];
+#pragma unroll
+    for (int u = 0; u < kPsItems; ++u) {
+      const int k = k0 + u * kPsBlock + (int)threadIdx.x;
+      if (k < hi) r[u] = rec[k];
+    }
+#pragma unroll
+    for (int u = 0; u < kPsItems; ++u)
+      if (k0 + u * kPsBlock + (int)threadIdx.x < hi) at[u] = atomicAdd(cur + (r[u].i.x - base), 1);
+#pragma unroll
+    for (int u = 0; u < kPsItems; ++u) {
+      if (k0 + u * kPsBlock + (int)threadIdx.x >= hi) continue;
+      src_y[at[u]] = make_float2(r[u].f.x, r[u].f.y);
+      src_v[at[u]] = make_float2(r[u].f.z, r[u].f.w);
+      src_t[at[u]] = __int_as_float(r[u].i.z);
+      src_id[at[u]] = r[u].i.y;
+    }
+  }
+}
+
+// Exclusive scan of the bucket totals into their positions: one workgroup, 16 totals per thread.
+__global__ void __launch_bounds__(kPsScanBlock) k_psort_scan(const int* __restrict__ tot, int n, int* __restrict__ pos) {
+  __shared__ int wsum[kPsScanBlock / kWave + 1];
+  constexpr int kPer = kPsMaxBuckets / kPsScanBlock;
+  int v[kPer];
+  int sum = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = threadIdx.x * kPer + k;
+    v[k] = i < n ? tot[i] : 0;
+    sum += v[k];
+  }
+  int total;
+  int run = block_exclusive_scan<kPsScanBlock>(sum, wsum, total);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = threadIdx.x * kPer + k;
+    if (i < n) pos[i] = run;
+    run += v[k];
+  }
+}
+
+struct PsortLayout {
+  int shift, nbuckets, nblk;
+  int64_t cnt, tot, pos, item, bytes;
+};
+
+// Bucket size and workspace of the sorted plan build; false if the grid or the entry capacity is out of range.
+bool psort_layout(int64_t N, int64_t ecap, int64_t ncell, PsortLayout& L) {
+  if (N < 0 || ecap < 0 || ncell < 1 || ecap >= ((int64_t)1 << 31) || N >= ((int64_t)1 << 31)) return false;
+  int shift = kPsMinShift;
+  while (shift <= kPsMaxShift && ((ncell + ((int64_t)1 << shift) - 1) >> shift) > kPsMaxBuckets) ++shift;
+  if (shift > kPsMaxShift) return false;
+  L.shift = shift;
+  L.nbuckets = (int)((ncell + ((int64_t)1 << shift) - 1) >> shift);
+  L.nblk = (int)((N + kPsPer * kPsBlock - 1) / (kPsPer * kPsBlock));
+  auto a256 = [](int64_t n) { return (n + 255) & ~(int64_t)255; };
+  int64_t off = 0;
+  L.cnt = off;  off += a256((int64_t)L.nblk * L.nbuckets * 4);
+  L.tot = off;  off += a256((int64_t)L.nbuckets * 4);
+  L.pos = off;  off += a256((int64_t)L.nbuckets * 4);
+  L.item = off; off += a256(ecap * (int64_t)sizeof(PsRec));
+  L.bytes = off;
+  return true;
+}
+
 // Anchors: slice floor(t / delta), cells clamped into the grid, functional.py:170-175.
 __global__ void __launch_bounds__(kBlock) k_plan_anchors(const float2* __restrict__ x, const float* __restrict__ t,
                                                          const int64_t* __restrict__ b,
@@ -1226,6 +1401,45 @@ int atl_plan_fill(const float* x, const float* t, const float* v, const int64_t*
   hipLaunchKernelGGL(k_plan_fill, dim3(grid_for(N)), dim3(kBlock), 0, stream, (const float2*)x, t,
                      (const float2*)v, b, N, g, start, cursor, (float2*)src_y, (float2*)src_v, src_t, src_id);
   return check_launch("plan_fill");
+}
+
+int64_t atl_plan_sort_bytes(int64_t N, int64_t ecap, int64_t ncell) {
+  PsortLayout L;
+  if (!psort_layout(N, ecap, ncell, L)) return -1;
+  return L.bytes;
+}
+
+int atl_plan_sort(const float* x, const float* t, const float* v, const int64_t* b, int64_t N, int64_t B, double ox,
+                  double oy, double cell, double tau, int64_t S, int64_t GH, int64_t GW, int64_t ecap,
+                  int64_t* start, float* src_y, float* src_v, float* src_t, int64_t* src_id, void* ws,
+                  int64_t ws_bytes, hipStream_t stream) {
+  if (N < 0 || !geo_ok(S, GH, GW, B) || !(cell > 0)) { set_error("plan_sort: bad geometry"); return 1; }
+  const int64_t ncell = B * S * GH * GW;
+  PsortLayout L;
+  if (ncell < 1 || !psort_layout(N, ecap, ncell, L)) { set_error("plan_sort: unsupported sizes (N=%lld ecap=%lld ncell=%lld)", (long long)N, (long long)ecap, (long long)ncell); return 1; }
+  if (!ws || ws_bytes < L.bytes) { set_error("plan_sort: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
+  if (!start || (N > 0 && (!x || !t || !v || !b))) { set_error("plan_sort: null argument"); return 1; }
+  const int64_t ms = std::min<int64_t>((int64_t)std::floor((2.0 * tau + 1.0 / (double)S) * (double)S) + 2, S);
+  if (ecap < N * ms) { set_error("plan_sort: ecap %lld below N * max slices (%lld)", (long long)ecap, (long long)(N * ms)); return 1; }
+  const PlanGeo g = make_geo(ox, oy, cell, tau, S, GH, GW, B);
+  char* w = (char*)ws;
+  int* cnt = (int*)(w + L.cnt);
+  int* tot = (int*)(w + L.tot);
+  int* pos = (int*)(w + L.pos);
+  PsRec* rec = (PsRec*)(w + L.item);
+  hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(L.nbuckets)), dim3(kBlock), 0, stream, tot, (int64_t)L.nbuckets, 0);
+  const size_t lds = (size_t)L.nbuckets * sizeof(int);
+  if (L.nblk > 0)
+    hipLaunchKernelGGL(k_psort_pass_a<false>, dim3(L.nblk), dim3(kPsBlock), lds, stream, (const float2*)x, t,
+                       (const float2*)v, b, N, g, L.shift, L.nbuckets, cnt, tot, (PsRec*)nullptr);
+  hipLaunchKernelGGL(k_psort_scan, dim3(1), dim3(kPsScanBlock), 0, stream, (const int*)tot, L.nbuckets, pos);
+  if (L.nblk > 0)
+    hipLaunchKernelGGL(k_psort_pass_a<true>, dim3(L.nblk), dim3(kPsBlock), lds, stream, (const float2*)x, t,
+                       (const float2*)v, b, N, g, L.shift, L.nbuckets, cnt, pos, rec);
+  hipLaunchKernelGGL(k_psort_pass_b, dim3(L.nbuckets), dim3(kPsBlock), 0, stream, (const PsRec*)rec,
+                     (const int*)pos, (const int*)tot, L.shift, ncell, L.nbuckets, start, (float2*)src_y,
+                     (float2*)src_v, src_t, src_id);
+  return check_launch("plan_sort");
 }
 
 int atl_plan_anchors(const float* x, const float* t, const int64_t* b, const int64_t* anchors,

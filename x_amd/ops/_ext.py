@@ -47,6 +47,8 @@ _SIGS = {
     "atl_traj_field_bwd_planned": [_P, _P, _I, _I, _I, _I, _I, _P, _P, _P],
     "atl_traj_field_bwd_bytes": [_I, _I, _I, _I, _I],
     "atl_sample_grid_bwd_rows_bytes": [_I, _I, _I, _I, _I],
+    "atl_plan_sort_bytes": [_I, _I, _I],
+    "atl_plan_sort": [_P, _P, _P, _P, _I, _I, _D, _D, _D, _D, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P],
     "atl_sample_grid_bwd_rows": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _P],
     "atl_traj_field_bwd": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P],
     "atl_traj_pos_bwd_cl": [_P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _P, _P],
@@ -114,7 +116,7 @@ _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.
             "atl_anchored_score_mean_scratch_bytes": ctypes.c_int64, "atl_knn_ws_bytes": ctypes.c_int64,
             "atl_voxel_ws_bytes": ctypes.c_int64, "atl_warp_splat_gather_ws_bytes": ctypes.c_int64,
             "atl_ats_pair_ws_bytes": ctypes.c_int64, "atl_traj_field_bwd_bytes": ctypes.c_int64,
-            "atl_sample_grid_bwd_rows_bytes": ctypes.c_int64,
+            "atl_sample_grid_bwd_rows_bytes": ctypes.c_int64, "atl_plan_sort_bytes": ctypes.c_int64,
 "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):

@@ -638,18 +638,33 @@ def _build_pair_plan_hip(x, t, v, b, B, H, W, anchors, h, tau, cut, n_slices, an
         if ncell >= 2 ** 31:
             raise ValueError(f"pair plan grid too large ({ncell} cells)")
         st = stream_of(x)
-        counts = torch.zeros(ncell, dtype=torch.int32, device=dev)
-        call("atl_plan_count", ptr(x), ptr(t), ptr(vd), ptr(b), N, B, ox, oy, cell, float(tau), S, GH, GW,
-             ptr(counts), st)
-        cell_start = _scan(counts)
-        E = int(cell_start[-1])
-        src_y = torch.empty(E, 2, dtype=F32, device=dev)
-        src_v = torch.empty(E, 2, dtype=F32, device=dev)
-        src_t = torch.empty(E, dtype=F32, device=dev)
-        src_id = torch.empty(E, dtype=I64, device=dev)
-        counts.zero_()
-        call("atl_plan_fill", ptr(x), ptr(t), ptr(vd), ptr(b), N, B, ox, oy, cell, float(tau), S, GH, GW,
-             ptr(cell_start), ptr(counts), ptr(src_y), ptr(src_v), ptr(src_t), ptr(src_id), st)
+        lib = load_library()
+        ecap = N * min(int(math.floor((2.0 * float(tau) + 1.0 / S) * S)) + 2, S)   # entries per source, at most
+        nbytes = int(lib.atl_plan_sort_bytes(N, ecap, ncell))
+        if nbytes >= 0:                            # counting sort: no per-entry atomics, one synchronisation
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+            cell_start = torch.empty(ncell + 1, dtype=I64, device=dev)
+            src_y = torch.empty(ecap, 2, dtype=F32, device=dev)
+            src_v = torch.empty(ecap, 2, dtype=F32, device=dev)
+            src_t = torch.empty(ecap, dtype=F32, device=dev)
+            src_id = torch.empty(ecap, dtype=I64, device=dev)
+            call("atl_plan_sort", ptr(x), ptr(t), ptr(vd), ptr(b), N, B, ox, oy, cell, float(tau), S, GH, GW, ecap,
+                 ptr(cell_start), ptr(src_y), ptr(src_v), ptr(src_t), ptr(src_id), ptr(ws), nbytes, st)
+            E = int(cell_start[-1])
+            src_y, src_v, src_t, src_id = src_y[:E], src_v[:E], src_t[:E], src_id[:E]
+        else:
+            counts = torch.zeros(ncell, dtype=torch.int32, device=dev)
+            call("atl_plan_count", ptr(x), ptr(t), ptr(vd), ptr(b), N, B, ox, oy, cell, float(tau), S, GH, GW,
+                 ptr(counts), st)
+            cell_start = _scan(counts)
+            E = int(cell_start[-1])
+            src_y = torch.empty(E, 2, dtype=F32, device=dev)
+            src_v = torch.empty(E, 2, dtype=F32, device=dev)
+            src_t = torch.empty(E, dtype=F32, device=dev)
+            src_id = torch.empty(E, dtype=I64, device=dev)
+            counts.zero_()
+            call("atl_plan_fill", ptr(x), ptr(t), ptr(vd), ptr(b), N, B, ox, oy, cell, float(tau), S, GH, GW,
+                 ptr(cell_start), ptr(counts), ptr(src_y), ptr(src_v), ptr(src_t), ptr(src_id), st)
         anc_x = torch.empty(M, 2, dtype=F32, device=dev)
         anc_t = torch.empty(M, dtype=F32, device=dev)
         anc_cell = torch.empty(M, 3, dtype=I64, device=dev)
