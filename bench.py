@@ -775,7 +775,7 @@ def main():
     torch.cuda.synchronize()
     # the pair kernels first (the roofline's candidates); the objective's dense flow takes the flow path, whose
     # backward is the pair backward (atl_fast_pair_bwd_src) and then the flow-grid adjoint
-    kernels = (["atl_ats_pair_fwd_ws", "atl_ats_pair_bwd_ws"] if reflayout else
+    kernels = (["atl_ats_pair_fwd_ws", "atl_ats_pair_bwd_ws_binned"] if reflayout else
                ["atl_fast_pair_fwd", "atl_fast_pair_bwd_src", "atl_fast_flow_adjoint"]) + (
         ["atl_splat_bilinear_fwd_ws", "atl_splat_bilinear_bwd"] if blobs else [])
     rec = _ext.time_kernels(kernels, every=4)      # every bracket delays the next launch: sample the steps
@@ -799,7 +799,7 @@ def main():
             pairs.append(int(plan.counts().sum()))
     K = float(np.mean(pairs))
     dom = max(kernels, key=lambda k: ms[k])
-    fwd = dom.endswith("fwd")
+    fwd = "_fwd" in dom
     slots = SLOTS_FWD if fwd else SLOTS_BWD
     achieved = K * slots / (ms[dom] * 1e-3)
     flops = K * (FLOPS_FWD if fwd else FLOPS_BWD) / (ms[dom] * 1e-3)

@@ -322,6 +322,16 @@ int atl_ats_pair_bwd_ws(const float* gS, const float* src_y, const float* src_v,
                         const float* anc_x, const float* anc_t, const int64_t* anc_cell, const int64_t* anc_id,
                         int64_t M, const float* slice_c, int64_t S, int64_t GH, int64_t GW, double h, double tau,
                         double cut, int64_t N, float* gv, void* ws, int64_t ws_bytes, hipStream_t stream);
+/* atl_ats_pair_bwd_ws over the anchors binned by the atl_ats_pair_fwd_ws call that ran in this ws on the same plan
+ * and anchors (ws untouched since): the binning is not repeated, every binned anchor takes its gS (anchors of
+ * gS = 0 included, adding zero terms as the reference's loop does).  No counterpart in the reference, whose
+ * forward and backward are separate calls (csrc/atl_ops.h:31-47). */
+int atl_ats_pair_bwd_ws_binned(const float* gS, const float* src_y, const float* src_v, const float* src_t,
+                               const int64_t* src_id, const int64_t* cell_start, int64_t E, int64_t ncell,
+                               const float* anc_x, const float* anc_t, const int64_t* anc_cell,
+                               const int64_t* anc_id, int64_t M, const float* slice_c, int64_t S, int64_t GH,
+                               int64_t GW, double h, double tau, double cut, int64_t N, float* gv, void* ws,
+                               int64_t ws_bytes, hipStream_t stream);
 
 /* ---------------------------------------------------------------- fused pair sums (no host synchronisation)
  *

@@ -637,6 +637,15 @@ __global__ void __launch_bounds__(kBlock) k_anchor_place(PairRef a, int64_t M, c
   arec[astart[key] + slot] = rec;
 }
 
+// The backward over a forward's binning: every binned record takes its anchor's gS (the forward binned every
+// anchor with g = 0; an anchor of gS = 0 then adds exact zeros for finite terms, as in the reference's loop).
+__global__ void __launch_bounds__(kBlock) k_anchor_set_g(const int64_t* __restrict__ astart, int64_t ncell, int64_t M,
+                                                         const float* __restrict__ gS, AnchorRec* __restrict__ arec) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= M || p >= astart[ncell]) return;
+  arec[p].g = gS[arec[p].idx];
+}
+
 // Forward over the binned anchors, one wave per item of up to kCellAnchors anchors of one cell: the anchors of a
 // cell share their 3 x 3 neighbourhood, so the wave walks it once, lanes over 64 consecutive records per chunk,
 // and every lane evaluates each anchor of the item on its record (the record loads and list arithmetic once per
@@ -1537,11 +1546,14 @@ int atl_ats_pair_bwd(const float* gS, const float* src_y, const float* src_v, co
   return check_launch("ats_pair_bwd");
 }
 
-int atl_ats_pair_bwd_ws(const float* gS, const float* src_y, const float* src_v, const float* src_t,
-                        const int64_t* src_id, const int64_t* cell_start, int64_t E, int64_t ncell,
-                        const float* anc_x, const float* anc_t, const int64_t* anc_cell, const int64_t* anc_id,
-                        int64_t M, const float* slice_c, int64_t S, int64_t GH, int64_t GW, double h, double tau,
-                        double cut, int64_t N, float* gv, void* ws, int64_t ws_bytes, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+int pair_bwd_ws(const float* gS, const float* src_y, const float* src_v, const float* src_t, const int64_t* src_id,
+                const int64_t* cell_start, int64_t E, int64_t ncell, const float* anc_x, const float* anc_t,
+                const int64_t* anc_cell, const int64_t* anc_id, int64_t M, const float* slice_c, int64_t S,
+                int64_t GH, int64_t GW, double h, double tau, double cut, int64_t N, float* gv, void* ws,
+                int64_t ws_bytes, bool binned, hipStream_t stream) {
   if (!pair_args_ok(E, ncell, M, S, GH, GW, h, N)) {
     set_error("ats_pair_bwd_ws: bad arguments");
     return 1;
@@ -1558,7 +1570,11 @@ int atl_ats_pair_bwd_ws(const float* gS, const float* src_y, const float* src_v,
   const PairRef a = make_ref(src_y, src_v, src_t, src_id, cell_start, E, ncell, anc_x, anc_t, anc_cell, anc_id,
                              slice_c, S, GH, GW, h, tau, cut, N);
   const float invh2 = 1.f / (float)(h * h);
-  if (bin_anchors(a, M, ncell, gS, w, stream)) return 1;
+  if (binned)
+    hipLaunchKernelGGL(k_anchor_set_g, dim3(grid_for(M)), dim3(kBlock), 0, stream, (const int64_t*)w.start, ncell, M,
+                       gS, w.arec);
+  else if (bin_anchors(a, M, ncell, gS, w, stream))
+    return 1;
   hipLaunchKernelGGL(k_unit_chunks, dim3(grid_for(w.units)), dim3(kBlock), 0, stream, a, (const int64_t*)w.start, M,
                      w.nseg, w.units, w.ucnt);
   if (atl_scan_counts(w.ucnt, w.units, w.ustart, w.uwork, stream)) return 1;
@@ -1567,7 +1583,29 @@ int atl_ats_pair_bwd_ws(const float* gS, const float* src_y, const float* src_v,
   hipLaunchKernelGGL(k_pair_bwd_gather, dim3((unsigned)blocks), dim3(kGatherWaves * kWave), 0, stream, a,
                      (const int64_t*)w.start, (const AnchorRec*)w.arec, M, (const int2*)w.items,
                      (const int64_t*)(w.ustart + w.units), w.max_items, invh2, w.nseg, gv);
-  return check_launch("ats_pair_bwd_ws");
+  return check_launch(binned ? "ats_pair_bwd_ws_binned" : "ats_pair_bwd_ws");
+}
+}  // namespace
+
+extern "C" {
+
+int atl_ats_pair_bwd_ws(const float* gS, const float* src_y, const float* src_v, const float* src_t,
+                        const int64_t* src_id, const int64_t* cell_start, int64_t E, int64_t ncell,
+                        const float* anc_x, const float* anc_t, const int64_t* anc_cell, const int64_t* anc_id,
+                        int64_t M, const float* slice_c, int64_t S, int64_t GH, int64_t GW, double h, double tau,
+                        double cut, int64_t N, float* gv, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  return pair_bwd_ws(gS, src_y, src_v, src_t, src_id, cell_start, E, ncell, anc_x, anc_t, anc_cell, anc_id, M,
+                     slice_c, S, GH, GW, h, tau, cut, N, gv, ws, ws_bytes, false, stream);
+}
+
+int atl_ats_pair_bwd_ws_binned(const float* gS, const float* src_y, const float* src_v, const float* src_t,
+                               const int64_t* src_id, const int64_t* cell_start, int64_t E, int64_t ncell,
+                               const float* anc_x, const float* anc_t, const int64_t* anc_cell,
+                               const int64_t* anc_id, int64_t M, const float* slice_c, int64_t S, int64_t GH,
+                               int64_t GW, double h, double tau, double cut, int64_t N, float* gv, void* ws,
+                               int64_t ws_bytes, hipStream_t stream) {
+  return pair_bwd_ws(gS, src_y, src_v, src_t, src_id, cell_start, E, ncell, anc_x, anc_t, anc_cell, anc_id, M,
+                     slice_c, S, GH, GW, h, tau, cut, N, gv, ws, ws_bytes, true, stream);
 }
 
 int atl_window_counts(const float* t, const int64_t* b, int64_t N, const int64_t* idx, int64_t M, double tau,

@@ -71,6 +71,8 @@ _SIGS = {
                             _I, _P],
     "atl_ats_pair_bwd_ws": [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _D, _D, _D, _I,
                             _P, _P, _I, _P],
+    "atl_ats_pair_bwd_ws_binned": [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _D, _D, _D, _I,
+                            _P, _P, _I, _P],
     "atl_window_counts": [_P, _P, _I, _P, _I, _D, _P, _P],
     "atl_check_sorted": [_P, _P, _I, _P, _P],
     "atl_bin_counts": [_P, _P, _I, _I, _I, _P, _P],
@@ -373,9 +375,10 @@ class HipOps:
         return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev), nbytes
 
     def ats_pair_fwd(self, sy, sv, st, sid, cs, ax, at, ac, aid, sc, S, GH, GW, h, tau, cut, count=None,
-                     plan_order=False):
+                     plan_order=False, keep_ws=False):
         """S (M,).  By default over a workspace allocated here with the output (atl_ats_pair_fwd_ws, anchors
-        walked in cell order); ``plan_order`` selects the workspace-free entry."""
+        walked in cell order); ``plan_order`` selects the workspace-free entry.  ``keep_ws`` returns (S, ws):
+        the workspace holds the binned anchors, which ats_pair_bwd(..., ws=ws) then reuses."""
         E, M, ncell = self._pair_args(sy, sv, st, sid, cs, ax, at, ac, aid, sc)
         out = torch.empty(M, device=ax.device, dtype=F32)
         args = (ptr(sy), ptr(sv), ptr(st), ptr(sid), ptr(cs), E, ncell, ptr(ax), ptr(at), ptr(ac), ptr(aid), M,
@@ -386,12 +389,15 @@ class HipOps:
             else:
                 ws, nbytes = self._pair_ws(E, ncell, M, GW, ax.device)
                 call("atl_ats_pair_fwd_ws", *args, ptr(ws), nbytes, stream_of(ax))
+                if keep_ws:
+                    return out, ws
         return out
 
     def ats_pair_bwd(self, g, sy, sv, st, sid, cs, ax, at, ac, aid, sc, S, GH, GW, h, tau, cut, N,
-                     per_pair_atomics=False):
+                     per_pair_atomics=False, ws=None):
         """gv (N, 2).  By default the source-centric backward over a workspace allocated here with the output
-        (atl_ats_pair_bwd_ws); ``per_pair_atomics`` selects the workspace-free entry (two atomics per pair)."""
+        (atl_ats_pair_bwd_ws); ``per_pair_atomics`` selects the workspace-free entry (two atomics per pair);
+        ``ws`` (from ats_pair_fwd(..., keep_ws=True) on the same plan) reuses the forward's anchor binning."""
         E, M, ncell = self._pair_args(sy, sv, st, sid, cs, ax, at, ac, aid, sc)
         _need(g, "gS", F32, ax.device, (M,))
         gv = torch.zeros(int(N), 2, device=ax.device, dtype=F32)
@@ -400,6 +406,8 @@ class HipOps:
         with torch.cuda.device(ax.device):
             if per_pair_atomics:
                 call("atl_ats_pair_bwd", *args, stream_of(ax))
+            elif ws is not None:
+                call("atl_ats_pair_bwd_ws_binned", *args, ptr(ws), ws.numel(), stream_of(ax))
             else:
                 ws, nbytes = self._pair_ws(E, ncell, M, GW, ax.device)
                 call("atl_ats_pair_bwd_ws", *args, ptr(ws), nbytes, stream_of(ax))

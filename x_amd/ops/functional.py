@@ -758,15 +758,17 @@ class _ATSPair(torch.autograd.Function):
         e = get_ext()
         ctx.plan, ctx.args, ctx.n = plan, (float(h), float(tau), float(cut)), v.shape[0]
         p = plan
-        return e.ats_pair_fwd(p.src_y, p.src_v, p.src_t, p.src_id, p.cell_start, p.anc_x, p.anc_t, p.anc_cell,
-                              p.anc_id, p.slice_c, p.S, p.GH, p.GW, *ctx.args)
+        # the workspace keeps the anchors binned by the forward for the backward (one binning per step)
+        out, ctx.ws = e.ats_pair_fwd(p.src_y, p.src_v, p.src_t, p.src_id, p.cell_start, p.anc_x, p.anc_t,
+                                     p.anc_cell, p.anc_id, p.slice_c, p.S, p.GH, p.GW, *ctx.args, keep_ws=True)
+        return out
 
     @staticmethod
     def backward(ctx, g):
         p = ctx.plan
         gv = get_ext().ats_pair_bwd(g.contiguous().float(), p.src_y, p.src_v, p.src_t, p.src_id, p.cell_start,
                                     p.anc_x, p.anc_t, p.anc_cell, p.anc_id, p.slice_c, p.S, p.GH, p.GW,
-                                    *ctx.args, ctx.n)
+                                    *ctx.args, ctx.n, ws=ctx.ws)
         return gv, None, None, None, None
 
 
