@@ -59,7 +59,9 @@ def check_against_oracle(xs, t, v, b, B, H, W, anchors, xa, h, tau, S, seed=0, i
     return wcnt
 
 
-@pytest.mark.parametrize("tau,S,h", [(0.2, 16, 1.0), (1.0, 8, 1.5), (0.05, 4, 0.5), (0.2, 16, 2.0)])
+# at most 8, 9, 12 and 16 slices per source (the entry passes keep up to 12 in registers, more take two passes)
+@pytest.mark.parametrize("tau,S,h", [(0.2, 16, 1.0), (1.0, 8, 1.5), (0.05, 4, 0.5), (0.2, 16, 2.0), (0.3, 16, 1.0),
+                                     (0.6, 16, 1.0)])
 def test_fast_matches_oracle(tau, S, h):
     win, xs, v, xa = _case(seed=11, h=h)
     cnt = check_against_oracle(xs, win.t, v, win.b, 2, 40, 48, np.arange(win.n), xa, h, tau, S)

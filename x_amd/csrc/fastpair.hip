@@ -708,6 +708,63 @@ __global__ void __launch_bounds__(kEntBlock) k_entry_pass(const Rec* __restrict_
   }
 }
 
+// Passes E1 and E2 in one launch, for sources of at most MAXE slices: each entry's key and its rank in the
+// block's run of its bucket (a returning LDS atomic) stay in registers, the block then reserves its runs with one
+// global atomic per bucket it feeds, and every entry is written at run start + rank.  No count matrix, and the
+// source records and keys are read and formed once.
+template <int MAXE>
+__global__ void __launch_bounds__(kEntBlock) k_entry_scatter(const Rec* __restrict__ srec,
+                                                          const int* __restrict__ start, FGeo G,
+                                                          int* __restrict__ bpos, int2* __restrict__ item) {
+  extern __shared__ int hist[];
+  const int nb0 = G.ncell_pad >> G.bshift;
+  const int EA = start[2 * G.ncell_pad];
+  const int Nv = start[3 * G.ncell_pad] - EA;
+  const int q0 = blockIdx.x * kEntSrcPerBlock;
+  if (q0 >= Nv) return;
+  for (int i = threadIdx.x; i < nb0; i += blockDim.x) hist[i] = 0;
+  const int scells = G.S * G.GH * G.GW;
+  constexpr int per = kEntSrcPerBlock / kEntBlock;
+  Rec r[per];
+#pragma unroll
+  for (int u = 0; u < per; ++u) r[u] = srec[min(q0 + u * kEntBlock + (int)threadIdx.x, Nv - 1)];
+  __syncthreads();                               // the histogram is cleared
+  int key[per][MAXE], rank[per][MAXE];
+#pragma unroll
+  for (int u = 0; u < per; ++u) {
+    const int q = q0 + u * kEntBlock + threadIdx.x;
+    const float tj = __int_as_float(r[u].i.x);
+    const float2 xj = make_float2(r[u].f.x, r[u].f.y), vj = make_float2(r[u].f.z, r[u].f.w);
+    const int bj = r[u].i.z / scells;
+    int lo, hi;
+    slice_range(tj, G, lo, hi);
+    if (q >= Nv) hi = lo - 1;                    // no entries
+#pragma unroll
+    for (int k = 0; k < MAXE; ++k) {
+      key[u][k] = -1;
+      rank[u][k] = 0;
+      if (lo + k <= hi) {                        // never past G.MS slices: whole waves skip the tail
+        float yx, yy;
+        key[u][k] = entry_key(xj, vj, tj, bj, lo + k, G, yx, yy);
+        rank[u][k] = atomicAdd(hist + (key[u][k] >> G.bshift), 1);
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nb0; i += blockDim.x) {
+    const int c = hist[i];
+    hist[i] = c > 0 ? atomicAdd(bpos + i, c) : 0;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < per; ++u) {
+    const int q = q0 + u * kEntBlock + threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < MAXE; ++k)
+      if (key[u][k] >= 0) item[hist[key[u][k] >> G.bshift] + rank[u][k]] = make_int2(q, key[u][k]);
+  }
+}
+
 // Pass E3: workgroup `bucket` (an entry bucket) orders its items by cell, as k_sort_pass2 orders records, into
 // `sorted` (items at their final positions) and writes the CSR of its keys.  bend: the bucket ends after pass E2,
 // tot: the bucket totals.  Up to kSortBlock * kEntItems items are read once and ranked as they arrive; larger
@@ -2008,7 +2065,10 @@ int fast_plan_impl(const atl_fast_geometry* geo, const FGeo& G, const float* x, 
     // per-block counts: (N / kEntSrcPerBlock) * bpk <= nblk * nbuckets ints (kEntSrcPerBlock = kSrcPerBlock / 2)
     static_assert(2 * kEntSrcPerBlock >= kSrcPerBlock, "the entry passes' counts fit the plan's count array");
     const unsigned eblk = (unsigned)((N + kEntSrcPerBlock - 1) / kEntSrcPerBlock);
-    if (eblk > 0) {
+    if (eblk > 0 && G.MS <= 12) {                // keys and ranks in registers
+      auto scatter = G.MS <= 8 ? k_entry_scatter<8> : k_entry_scatter<12>;
+      hipLaunchKernelGGL(scatter, dim3(eblk), dim3(kEntBlock), elds, stream, srec, start, G, bpos, item);
+    } else if (eblk > 0) {
       hipLaunchKernelGGL(k_entry_pass<false>, dim3(eblk), dim3(kEntBlock), elds, stream, srec, start, G, cnt,
                          bpos, item);
       hipLaunchKernelGGL(k_entry_pass<true>, dim3(eblk), dim3(kEntBlock), elds, stream, srec, start, G, cnt,
