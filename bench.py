@@ -322,7 +322,7 @@ IWE_COUNTERS = ROOT / "profiles" / "iwe_1M_640x480_counters.md"
 IWE_KERNELS = {
     "atl_warp_splat_gather_fwd": ["k_wsg_warp", "k_tile_bin<0, true, false>", "k_tile_accum_bins<0, 1>",
                                   "k_wsg_gather"],
-    "atl_warp_splat_gather_bwd": ["k_wsg_pack", "k_tile_accum_bins<5, 1>", "k_wsg_grad", "k_tile_bin<4, true, true>",
+    "atl_warp_splat_gather_bwd": ["k_wsg_pack", "k_tile_accum_bins<5, 1>", "k_wsg_grad<true>",
                                   "k_tile_accum_bins<4, 2>"],
 }
 IWE_BYTES = {

@@ -74,6 +74,28 @@ def test_warp_splat_gather_matches_oracle(B, H, W, vmax, mask):
     close_rel(N(tg.grad), want_g, 1e-4)
 
 
+@pytest.mark.parametrize("B,H,W,Hg,Wg", [(2, 40, 48, 9, 14), (8, 480, 640, 480, 640)])
+def test_warp_splat_gather_grid_shapes(B, H, W, Hg, Wg):
+    """A coarse flow grid, and eight full-sensor windows: their image and flow-grid tile histograms together
+    exceed one workgroup's histogram, so the backward counts the flow-grid tiles itself.  Outputs are written,
+    not accumulated: the buffers the wrapper allocates hold whatever was there before."""
+    print(f"warp_splat_gather grid shape B={B} {H}x{W} grid {Hg}x{Wg}", flush=True)
+    win = synth.small_window(seed=B, n=2500, H=H, W=W, vmax=10.0, B=B)
+    rng = np.random.default_rng(Hg)
+    grid = rng.uniform(-10.0, 10.0, (B, 2, Hg, Wg)).astype(F32)
+    gvals = rng.standard_normal(win.n).astype(F32)
+    gimg = rng.standard_normal((B, H, W)).astype(F32)
+    want_img, want_vals, want_g = oracle_wsg(grid, win.xy, win.t, win.b, 0.5, B, H, W, True, gvals, gimg)
+    stale = torch.full((B * H * W * 4,), float("nan"), device=DEV)
+    del stale                                                    # NaNs left in the allocator's free blocks
+    tg = T(grid).requires_grad_(True)
+    img, vals = F.warp_splat_gather(tg, T(win.xy), T(win.t), T(win.b), 0.5, H, W, True)
+    close_rel(N(img), want_img, 1e-5)
+    close_rel(N(vals), want_vals, 1e-5)
+    ((vals * T(gvals)).sum() + (img * T(gimg)).sum()).backward()
+    close_rel(N(tg.grad), want_g, 1e-4)
+
+
 def test_warp_splat_gather_values_only_and_image_only():
     """Gradients through one output at a time (the other's gradient absent)."""
     win = synth.small_window(seed=5, n=5000, H=30, W=44, vmax=8.0, B=2)

@@ -142,19 +142,78 @@ __device__ __forceinline__ int tile_key(float x, float y, int64_t b, const TileG
   return ((int)b * g.TY + ty) * g.TX + tx;
 }
 
+// Chunks of the tile-ordered records: every non-empty tile is cut into chunks of at most `chunk` records, and
+// chunk w gets info[w] = (tile, first record, end record, 1 if the tile has more than one chunk); crowded tiles
+// (more than 32 * chunk records, where the flushes of many chunks would pile up on the same pixels) take chunks
+// of `crowd` records; nchunk[0] = the number of chunks.  One workgroup of NT threads: thread i takes the tiles
+// i, i + NT, ... (a run of crowded neighbouring tiles is spread over many threads, each writing its own tile's
+// chunks), so the scan of the chunk counts runs in rounds of NT tiles.  It runs as a launch of its own
+// (k_tile_chunks) or as one extra workgroup of the pass that places the records (after the scan that fixed the
+// tiles' offsets, so the list is ready when the records are).
+struct ChunkList {
+  int4* info;
+  int* nchunk;
+  int chunk, crowd;
+};
+
+template <int NT>
+__device__ __forceinline__ void tile_chunks_body(const int* __restrict__ boff, const TileGeo& g, ChunkList cl) {
+  static_assert(kTileMaxKeys % NT == 0, "whole rounds of tiles");
+  __shared__ int wsum[NT / kWave + 1];
+  constexpr int kPer = kTileMaxKeys / NT;
+  const int rounds = (g.nkeys + NT - 1) / NT;
+  int r0[kPer], r1[kPer];                         // record range of this thread's tile of every round
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int t = k * NT + threadIdx.x;
+    r0[k] = k < rounds ? boff[min(t, g.nkeys) * g.nblk] : 0;
+    r1[k] = k < rounds ? boff[min(t + 1, g.nkeys) * g.nblk] : 0;
+  }
+  int base = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    if (k >= rounds) break;
+    const int t = k * NT + threadIdx.x;
+    const int len = r1[k] - r0[k];
+    const int cs = len > 32 * cl.chunk ? cl.crowd : cl.chunk;
+    const int n = t < g.nkeys ? (len + cs - 1) / cs : 0;
+    int total;
+    const int c = base + block_exclusive_scan<NT>(n, wsum, total);
+    const bool crowded = n > kWave / 8;           // a crowded tile's chunks are written by its whole wave
+    if (!crowded)
+      for (int q = 0; q < n; ++q)
+        cl.info[c + q] = make_int4(t, r0[k] + q * cs, min(r0[k] + (q + 1) * cs, r1[k]), n > 1);
+    for (uint64_t m = __ballot(crowded); m; m &= m - 1) {
+      const int src = __ffsll((unsigned long long)m) - 1;
+      const int tt = __shfl(t, src), cc = __shfl(c, src), a0 = __shfl(r0[k], src), a1 = __shfl(r1[k], src);
+      const int nn = __shfl(n, src), ss = __shfl(cs, src);
+      for (int q = threadIdx.x & (kWave - 1); q < nn; q += kWave)
+        cl.info[cc + q] = make_int4(tt, a0 + q * ss, min(a0 + (q + 1) * ss, a1), nn > 1);
+    }
+    base += total;
+  }
+  if (threadIdx.x == 0) *cl.nchunk = base;
+}
+
 // Binning.  SCATTER = false: per-block tile histogram into cnt[block * nkeys + key] (rows written coalesced; the
 // scan reads them transposed, key-major).  SCATTER = true: the block's scanned offsets (boff[key * nblk + block])
 // are loaded into LDS and every event writes (x, y, value, index) to its slot; kVoxel
 // writes (x, y, polarity, t * (C - 1)) (aux = t) and skips events whose time bins both miss [0, C).  Events of
 // value zero are skipped unless SKIP_ZERO is false (records whose index also serves a second accumulation).
+// SCATTER with a launch of nblk + 1 workgroups: the last one writes the chunk list `cl` instead.
 template <int MODE, bool SCATTER, bool SKIP_ZERO = true>
 __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __restrict__ pos,
                                                             const int64_t* __restrict__ bidx,
                                                             const float* __restrict__ val, TileGeo g,
                                                             int* __restrict__ cnt, float4* __restrict__ rec,
-                                                            const float* __restrict__ aux = nullptr) {
+                                                            const float* __restrict__ aux = nullptr,
+                                                            ChunkList cl = ChunkList{}) {
   extern __shared__ int hist[];
   const int blk = blockIdx.x;
+  if (SCATTER && blk == g.nblk) {                 // the extra workgroup: cnt holds the scanned offsets
+    tile_chunks_body<kTileBinBlock>(cnt, g, cl);
+    return;
+  }
   for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) hist[i] = SCATTER ? cnt[i * g.nblk + blk] : 0;
   __syncthreads();
   constexpr int per = tile_per_block(MODE) / kTileBinBlock;
@@ -170,7 +229,7 @@ __global__ void __launch_bounds__(kTileBinBlock) k_tile_bin(const float2* __rest
     v2[u] = 0.f;
     if (j < g.N) {
       p[u] = pos[j];
-      if (MODE == kGridVal) {                     // the gradient row (C = 1 or 2): its values ride in the record
+      if (MODE == kGridVal && val) {              // the gradient row (C = 1 or 2): its values ride in the record
         vj[u] = val[(int64_t)j * g.C];
         if (g.C == 2) v2[u] = val[(int64_t)j * 2 + 1];
       } else if (val) {
@@ -314,52 +373,12 @@ __device__ __forceinline__ void accum_record(const float4& q, const float* __res
   }
 }
 
-// Chunks of the tile-ordered records: every non-empty tile is cut into chunks of at most `chunk` records, and
-// chunk w gets info[w] = (tile, first record, end record, 1 if the tile has more than one chunk).  One
-// workgroup; thread i takes the tiles i, i + 1024, ... (a run of crowded neighbouring tiles is spread over many
-// threads, each writing its own tile's chunks), so the scan of the chunk counts runs in rounds of 1024 tiles;
-// nchunk[0] = the number of chunks.
+// The chunk list of the tile-ordered records (tile_chunks_body) as a launch of its own: one workgroup.
 constexpr int kChunkScanBlock = 1024;
-static_assert(kTileMaxKeys <= kChunkScanBlock * 16, "one scan thread handles at most 16 tiles");
-
 __global__ void __launch_bounds__(kChunkScanBlock) k_tile_chunks(const int* __restrict__ boff, TileGeo g, int chunk,
                                                                  int crowd, int4* __restrict__ info,
                                                                  int* __restrict__ nchunk) {
-  __shared__ int wsum[kChunkScanBlock / kWave + 1];
-  constexpr int kPer = kTileMaxKeys / kChunkScanBlock;
-  const int rounds = (g.nkeys + kChunkScanBlock - 1) / kChunkScanBlock;
-  int r0[kPer], r1[kPer];                         // record range of this thread's tile of every round
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int t = k * kChunkScanBlock + threadIdx.x;
-    r0[k] = k < rounds ? boff[min(t, g.nkeys) * g.nblk] : 0;
-    r1[k] = k < rounds ? boff[min(t + 1, g.nkeys) * g.nblk] : 0;
-  }
-  int base = 0;
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    if (k >= rounds) break;
-    const int t = k * kChunkScanBlock + threadIdx.x;
-    // chunk: records per chunk; crowded tiles (more than 32 * chunk records, where the flushes of many chunks
-    // would pile up on the same pixels) take chunks of `crowd` records
-    const int len = r1[k] - r0[k];
-    const int cs = len > 32 * chunk ? crowd : chunk;
-    const int n = t < g.nkeys ? (len + cs - 1) / cs : 0;
-    int total;
-    const int c = base + block_exclusive_scan<kChunkScanBlock>(n, wsum, total);
-    const bool crowded = n > kWave / 8;           // a crowded tile's chunks are written by its whole wave
-    if (!crowded)
-      for (int q = 0; q < n; ++q) info[c + q] = make_int4(t, r0[k] + q * cs, min(r0[k] + (q + 1) * cs, r1[k]), n > 1);
-    for (uint64_t m = __ballot(crowded); m; m &= m - 1) {
-      const int src = __ffsll((unsigned long long)m) - 1;
-      const int tt = __shfl(t, src), cc = __shfl(c, src), a0 = __shfl(r0[k], src), a1 = __shfl(r1[k], src);
-      const int nn = __shfl(n, src), ss = __shfl(cs, src);
-      for (int q = threadIdx.x & (kWave - 1); q < nn; q += kWave)
-        info[cc + q] = make_int4(tt, a0 + q * ss, min(a0 + (q + 1) * ss, a1), nn > 1);
-    }
-    base += total;
-  }
-  if (threadIdx.x == 0) *nchunk = base;
+  tile_chunks_body<kChunkScanBlock>(boff, g, ChunkList{info, nchunk, chunk, crowd});
 }
 
 // Accumulation: workgroup w takes chunk w (records of one tile, so a crowded tile is shared by several
@@ -755,7 +774,8 @@ inline int traj_bin_per(int64_t m) {
 }
 
 // ROWS: the records of a many-channel sampler adjoint instead (one look-up per event, gd and the times unused):
-// (x, y, event index, 0), every record kept (the row is read by the accumulation).
+// (x, y, event index, 0), every record kept (the row is read by the accumulation).  SCATTER also prepares the
+// accumulation: its nblk workgroups clear the nh halo floats, and one more workgroup writes the chunk list cl.
 template <bool SCATTER, bool ROWS = false>
 __global__ void __launch_bounds__(kTrajBinThreads) k_traj_bin(const float2* __restrict__ pos,
                                                             const float2* __restrict__ gd,
@@ -763,9 +783,18 @@ __global__ void __launch_bounds__(kTrajBinThreads) k_traj_bin(const float2* __re
                                                             const float* __restrict__ t_last,
                                                             const int64_t* __restrict__ bidx, int N, int n_look,
                                                             int per, TileGeo g, int* __restrict__ cnt,
-                                                            float4* __restrict__ rec, float* __restrict__ tr) {
+                                                            float4* __restrict__ rec, float* __restrict__ tr,
+                                                            ChunkList cl, float* __restrict__ halo, int64_t nh) {
   extern __shared__ int hist[];
   const int blk = blockIdx.x;
+  if (SCATTER) {
+    if (blk == g.nblk) {                         // the extra workgroup: cnt holds the scanned offsets
+      tile_chunks_body<kTrajBinThreads>(cnt, g, cl);
+      return;
+    }
+    for (int64_t k = (int64_t)blk * blockDim.x + threadIdx.x; k < nh; k += (int64_t)g.nblk * blockDim.x)
+      halo[k] = 0.f;
+  }
   for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) hist[i] = SCATTER ? cnt[i * g.nblk + blk] : 0;
   __syncthreads();
   constexpr int U = 4;                           // records per thread in flight together
@@ -1290,9 +1319,36 @@ TileLayout tile_layout(const TileGeo& g) {
 
 __global__ void k_tile_zero1(int* p) { p[0] = 0; }
 
+// ATL_TILE_SCATTER=1 in the environment selects the scatter form of the accumulation for every mode (read at
+// every call, so that a test can compare both forms in one process).  A backward that reuses its forward's chunk
+// list may therefore run the other form on it: the scatter form takes chunks of any length, in rounds.
+bool tile_scatter_form() {
+  const char* e = std::getenv("ATL_TILE_SCATTER");
+  return e && e[0] == '1';
+}
+
+// The accumulation form of tile_accum<MODE, C> on geometry g (gather: one thread per pixel of a 16 x 16 tile)
+// and the chunk list it runs on: chunks of kAccChunk records, crowded tiles in chunks of kBinChunk for the gather
+// form.
+template <int MODE, int C>
+bool tile_gather(const TileGeo& g) {
+  constexpr bool kGatherForm =
+      MODE == kImage || MODE == kImageG || MODE == kGridVal || (MODE == kGrid && C >= 1 && C <= 4);
+  return kGatherForm && g.T == kBinT && !tile_scatter_form();
+}
+
+template <int MODE, int C>
+ChunkList tile_chunk_list(const TileGeo& g, const TileLayout& L, void* ws) {
+  char* w = (char*)ws;
+  return ChunkList{(int4*)(w + L.info), (int*)(w + L.nchunk), kAccChunk,
+                   tile_gather<MODE, C>(g) ? kBinChunk : kAccChunk};
+}
+
+// Histogram, scan and scatter of the records; with cl, the scatter launch's extra workgroup writes that chunk
+// list (then the accumulation runs with listed = true).
 template <int MODE>
 void tile_bin(const TileGeo& g, const TileLayout& L, void* ws, const float* pos, const int64_t* b, const float* val,
-              hipStream_t stream, const float* aux = nullptr) {
+              hipStream_t stream, const float* aux = nullptr, const ChunkList* cl = nullptr) {
   char* w = (char*)ws;
   int* cnt = (int*)(w + L.cnt);
   int* boff = (int*)(w + L.boff);
@@ -1302,18 +1358,10 @@ void tile_bin(const TileGeo& g, const TileLayout& L, void* ws, const float* pos,
   }
   const size_t lds = (size_t)g.nkeys * sizeof(int);
   hipLaunchKernelGGL((k_tile_bin<MODE, false>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
-                     b, val, g, cnt, (float4*)nullptr, aux);
+                     b, val, g, cnt, (float4*)nullptr, aux, ChunkList{});
   scan32t(cnt, g.nkeys, g.nblk, (int*)(w + L.part), boff, stream);
-  hipLaunchKernelGGL((k_tile_bin<MODE, true>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream, (const float2*)pos,
-                     b, val, g, boff, (float4*)(w + L.rec), aux);
-}
-
-// ATL_TILE_SCATTER=1 in the environment selects the scatter form of the accumulation for every mode (read at
-// every call, so that a test can compare both forms in one process).  A backward that reuses its forward's chunk
-// list may therefore run the other form on it: the scatter form takes chunks of any length, in rounds.
-bool tile_scatter_form() {
-  const char* e = std::getenv("ATL_TILE_SCATTER");
-  return e && e[0] == '1';
+  hipLaunchKernelGGL((k_tile_bin<MODE, true>), dim3(g.nblk + (cl ? 1 : 0)), dim3(kTileBinBlock), lds, stream,
+                     (const float2*)pos, b, val, g, boff, (float4*)(w + L.rec), aux, cl ? *cl : ChunkList{});
 }
 
 // listed: the chunk list in ws is already that of this form (an earlier accumulation on the same records).
@@ -1326,10 +1374,12 @@ void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const flo
   int* nchunk = (int*)(w + L.nchunk);
   constexpr bool kGatherForm =
       MODE == kImage || MODE == kImageG || MODE == kGridVal || (MODE == kGrid && C >= 1 && C <= 4);
-  const bool gather = kGatherForm && g.T == kBinT && !tile_scatter_form();
-  if (!listed)
+  const bool gather = tile_gather<MODE, C>(g);
+  if (!listed) {
+    const ChunkList cl = tile_chunk_list<MODE, C>(g, L, w);
     hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.boff), g,
-                       kAccChunk, gather ? kBinChunk : kAccChunk, info, nchunk);
+                       cl.chunk, cl.crowd, info, nchunk);
+  }
   const unsigned grid = (unsigned)max_chunks(g);  // workgroups past the chunk count return at once
   const int nc = C > 0 ? C : g.C;
   const size_t edge = MODE == kGauss ? (size_t)(g.T + 2 * g.R) : (size_t)(g.T + 1);
@@ -1343,6 +1393,15 @@ void tile_accum(const TileGeo& g, const TileLayout& L, const void* ws, const flo
   else
     hipLaunchKernelGGL((k_tile_accum<MODE, C, 32>), dim3(grid), dim3(kAccBlock), lds, stream, (const int4*)info,
                        (const int*)nchunk, (const float4*)(w + L.rec), gout, g, out);
+}
+
+// Binning and accumulation of one set of records, the chunk list written by the binning's scatter launch.
+template <int MODE, int C>
+void tile_bin_accum(const TileGeo& g, const TileLayout& L, void* ws, const float* pos, const int64_t* b,
+                    const float* val, float* out, hipStream_t stream, const float* aux = nullptr) {
+  const ChunkList cl = tile_chunk_list<MODE, C>(g, L, ws);
+  tile_bin<MODE>(g, L, ws, pos, b, val, stream, aux, &cl);
+  tile_accum<MODE, C>(g, L, ws, nullptr, out, stream, true);
 }
 
 // Scratch of atl_splat_bilinear_fwd_noalloc: the tile engine's workspace (counts, offsets, records) for callers
@@ -1390,18 +1449,25 @@ int noalloc_scratch(void** out) {
 // atl/ops/functional.py:67-87 with the flow of parametric.py:212-216):
 //   v_j = sample(grid, x_j), y_j = x_j + v_j (t_ref - t_j), w_j = [y_j inside the sensor] (or 1),
 //   img = splat(y, w), vals_j = gather(img, y_j).
-// The forward bins the warped events by image tile (the histogram is taken by the warp kernel itself) and keeps
-// y, w and the records for the backward, which splats the value gradient on those records, forms each event's
-// position gradient and flow gradient in one per-event kernel (with the flow grid's tile histogram), and
-// accumulates the flow-grid adjoint on the tile engine.  Every per-event expression is the composed path's, in
-// its fp32 order.
+// The forward bins the warped events by image tile (the histogram is taken by the warp kernel itself, with the
+// flow-grid tile histogram of the events' own positions beside it) and keeps y, w and the records for the
+// backward, which splats the value gradient on those records, forms each event's flow gradient in one per-event
+// kernel that writes it straight into its flow-grid tile slot, and accumulates the flow-grid adjoint on the tile
+// engine.  The image (forward) and the flow-grid gradient (backward) are written, not accumulated: the first
+// kernel of each clears them.  Every per-event expression is the composed path's, in its fp32 order.
 struct WsgLayout {
   TileGeo gi, gg;              // image tiles (kImage / kImageG), flow-grid tiles (kGridVal, 2 channels)
   TileLayout Li, Lg;
   int64_t ai, ag;              // byte offsets of the two tile-engine regions
-  int64_t y, w, gv, G, bytes;  // warped positions (N float2), weights (N), flow gradients (N float2), and the
-                               // (image, image gradient) pairs (B H W float2)
+  int64_t y, w, gv, G, bytes;  // warped positions (N float2), weights (N), flow gradients (N float2, one-node
+                               // grids only), and the (image, image gradient) pairs (B H W float2)
 };
+
+// One-node grids (Hg = Wg = 1, a translation) of at most kOneNodeMaxB windows: the adjoint is a sum per window.
+constexpr int kOneNodeMaxB = 64;
+constexpr int kOneNodeBlocks = 256;
+
+bool wsg_one_node(int64_t B, int64_t Hg, int64_t Wg) { return Hg == 1 && Wg == 1 && B <= kOneNodeMaxB; }
 
 bool wsg_layout(int64_t N, int64_t B, int64_t H, int64_t W, int64_t Hg, int64_t Wg, WsgLayout& L) {
   if (N < 1 || B < 1 || H < 1 || W < 1 || Hg < 1 || Wg < 1) return false;
@@ -1418,21 +1484,39 @@ bool wsg_layout(int64_t N, int64_t B, int64_t H, int64_t W, int64_t Hg, int64_t 
   L.gv = off; off += align256(N * 8);
   L.G = off;  off += align256(B * H * W * 8);
   L.bytes = off;
-  return true;
+  return L.gi.nblk == L.gg.nblk;                  // one block partition for both histograms
+}
+
+// Where the flow-grid adjoint's tile counts are made: in the forward's k_wsg_warp when both histograms fit its
+// LDS, else by a counting pass in the backward; none for one-node grids.
+enum WsgCount { kCountNone, kCountWarp, kCountBwd };
+WsgCount wsg_count(const WsgLayout& L, int64_t B, int64_t Hg, int64_t Wg) {
+  if (wsg_one_node(B, Hg, Wg)) return kCountNone;
+  return L.gi.nkeys + L.gg.nkeys <= kTileMaxKeys ? kCountWarp : kCountBwd;
 }
 
 // Warp, weight and the image-tile histogram, with the block partition of k_tile_bin (4096 events per block) so
 // that its scatter pass finds the same per-block counts.  Every event with an in-image base corner is counted,
-// masked ones (w = 0) included: the value gradient of the gather reaches them.
+// masked ones (w = 0) included: the value gradient of the gather reaches them.  With cntg, the flow-grid tile
+// histogram of the events' own positions too (every event of a valid window: the backward's k_wsg_grad places
+// its gradient rows by it, over the same partition).  The threads also clear the nz floats of `zero` (the image,
+// which the splat then accumulates).  WIDE (Wg >= 2): each row's two corners are adjacent and load as one 8-byte
+// pair per channel; a single kernel with both forms compiled to four separate 4-byte loads per row.
+template <bool WIDE>
 __global__ void __launch_bounds__(kTileBinBlock) k_wsg_warp(const float* __restrict__ grid, int Hg, int Wg,
                                                             float sxw, float syh, const float2* __restrict__ xy,
                                                             const float* __restrict__ t,
                                                             const int64_t* __restrict__ bidx, float t_ref, int mask,
                                                             TileGeo g, float2* __restrict__ y, float* __restrict__ w,
-                                                            int* __restrict__ cnt) {
+                                                            int* __restrict__ cnt, TileGeo gg, int* __restrict__ cntg,
+                                                            float* __restrict__ zero, int64_t nz) {
   extern __shared__ int hist[];
+  int* histg = hist + g.nkeys;
   const int blk = blockIdx.x;
   for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) hist[i] = 0;
+  if (cntg)
+    for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) histg[i] = 0;
+  for (int64_t k = (int64_t)blk * blockDim.x + threadIdx.x; k < nz; k += (int64_t)gridDim.x * blockDim.x) zero[k] = 0.f;
   constexpr int per = kTilePerBlock / kTileBinBlock;
   const int j0 = blk * kTilePerBlock;
   const int64_t plane = (int64_t)Hg * Wg;
@@ -1455,7 +1539,7 @@ __global__ void __launch_bounds__(kTileBinBlock) k_wsg_warp(const float* __restr
     ra[u] = rb[u] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (!batch_ok(bj[u], g.B)) continue;          // sample_grid of an event outside the batch: zero
     const float* f = grid + bj[u] * 2 * plane;
-    if (Wg >= 2) {                                // o01 = o00 + 1, o11 = o10 + 1: one 8-byte load per row
+    if (WIDE) {                                   // o01 = o00 + 1, o11 = o10 + 1: one 8-byte load per row
       float2 r0, r1, q0, q1;
       __builtin_memcpy(&r0, f + c[u].o00, sizeof(float2));
       __builtin_memcpy(&r1, f + c[u].o10, sizeof(float2));
@@ -1489,9 +1573,15 @@ __global__ void __launch_bounds__(kTileBinBlock) k_wsg_warp(const float* __restr
     w[j] = wj;
     const int key = tile_key<kImage>(yx, yy, bj[u], g);
     if (key >= 0) atomicAdd(hist + key, 1);
+    if (cntg) {
+      const int kg = tile_key<kGridVal>(p[u].x, p[u].y, bj[u], gg);
+      if (kg >= 0) atomicAdd(histg + kg, 1);
+    }
   }
   __syncthreads();
   for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) cnt[(int64_t)blk * g.nkeys + i] = hist[i];
+  if (cntg)
+    for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) cntg[(int64_t)blk * gg.nkeys + i] = histg[i];
 }
 
 // vals_j = gather(img, y_j): csrc/atl_cpu.cpp:134-149.
@@ -1533,8 +1623,6 @@ __global__ void __launch_bounds__(kBlock) k_wsg_gather(const float* __restrict__
 // 1, so the node's gradient is the sum of its batch's per-event rows gv (N, 2); B <= kOneNodeMaxB windows.  Per
 // block: a wave whose lanes share one window adds its rows across the wave first; partial sums per window in LDS,
 // then one global atomic per window and channel (ggrid accumulated, as the tile adjoint accumulates).
-constexpr int kOneNodeMaxB = 64;
-constexpr int kOneNodeBlocks = 256;
 
 __global__ void __launch_bounds__(kBlock) k_one_node_adjoint(const float2* __restrict__ gv,
                                                              const int64_t* __restrict__ bidx, int64_t N, int B,
@@ -1571,17 +1659,23 @@ __global__ void __launch_bounds__(kBlock) k_one_node_adjoint(const float2* __res
 }
 
 // The backward's image pair: ig[p] = (img[p], gimg[p] or 0); the value gradient's splat is then added into the
-// second slots, and the per-event gradient reads both images of a corner row with one 16-byte load.
+// second slots, and the per-event gradient reads both images of a corner row with one 16-byte load.  The same
+// threads clear the nz floats of `zero` (the flow-grid gradient, which the adjoint then accumulates).
 __global__ void __launch_bounds__(kBlock) k_wsg_pack(const float* __restrict__ img, const float* __restrict__ gimg,
-                                                     int64_t n, float2* __restrict__ ig) {
+                                                     int64_t n, float2* __restrict__ ig, float* __restrict__ zero,
+                                                     int64_t nz) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) ig[i] = make_float2(img[i], gimg ? gimg[i] : 0.f);
+  for (int64_t k = i; k < nz; k += (int64_t)gridDim.x * blockDim.x) zero[k] = 0.f;
 }
 
 // Per-event gradient: the position gradient of the gather (gvals_j * grad img(y_j), csrc/atl_cpu.cpp:151-172) plus
 // that of the splat (w_j * grad G(y_j), csrc/atl_cpu.cpp:58-76, G the image gradient), times (t_ref - t_j) for the
-// flow sampled at x_j; and the flow-grid tile histogram of those rows (zero rows skipped, as k_tile_bin<kGridVal>
-// skips them), with k_tile_bin's block partition.
+// flow sampled at x_j.  RECS: every row goes straight to its slot in the flow-grid tile order as the record
+// (x, y, gv.x, gv.y), the slots counted by the forward's k_wsg_warp over the same block partition and scanned
+// (boff; a zero row adds nothing and keeps its slot); otherwise the rows are written to gv (one-node grids).
+// RECS with nblk + 1 workgroups: the last one writes the chunk list `cl` of the records.
+template <bool RECS>
 __global__ void __launch_bounds__(kTileBinBlock) k_wsg_grad(const float2* __restrict__ ig,
                                                             const float* __restrict__ gvals,
                                                             const float2* __restrict__ y, const float* __restrict__ w,
@@ -1589,10 +1683,16 @@ __global__ void __launch_bounds__(kTileBinBlock) k_wsg_grad(const float2* __rest
                                                             const float* __restrict__ t,
                                                             const int64_t* __restrict__ bidx, float t_ref,
                                                             int H, int W, TileGeo gg, float2* __restrict__ gv,
-                                                            int* __restrict__ cnt) {
+                                                            const int* __restrict__ boff, float4* __restrict__ rec,
+                                                            ChunkList cl) {
   extern __shared__ int hist[];
   const int blk = blockIdx.x;
-  for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) hist[i] = 0;
+  if (RECS && blk == gg.nblk) {
+    tile_chunks_body<kTileBinBlock>(boff, gg, cl);
+    return;
+  }
+  if (RECS)
+    for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) hist[i] = boff[i * gg.nblk + blk];
   constexpr int per = kTilePerBlock / kTileBinBlock;
   const int j0 = blk * kTilePerBlock;
   const int64_t pl = (int64_t)H * W;
@@ -1625,7 +1725,7 @@ __global__ void __launch_bounds__(kTileBinBlock) k_wsg_grad(const float2* __rest
       }
     }
   }
-  __syncthreads();                                // the histogram is cleared
+  __syncthreads();                                // the run starts are loaded
 #pragma unroll
   for (int u = 0; u < per; ++u) {
     const int j = j0 + u * kTileBinBlock + threadIdx.x;
@@ -1663,14 +1763,14 @@ __global__ void __launch_bounds__(kTileBinBlock) k_wsg_grad(const float2* __rest
     const float gx = g * s1x + wj * s2x, gy = g * s1y + wj * s2y;
     const float step = t_ref - t[j];
     const float vx = gx * step, vy = gy * step;
-    gv[j] = make_float2(vx, vy);
-    if (vx == 0.f && vy == 0.f) continue;
+    if (!RECS) {
+      gv[j] = make_float2(vx, vy);
+      continue;
+    }
     const float2 x = xy[j];
     const int key = tile_key<kGridVal>(x.x, x.y, bj[u], gg);
-    if (key >= 0) atomicAdd(hist + key, 1);
+    if (key >= 0) rec[atomicAdd(hist + key, 1)] = make_float4(x.x, x.y, vx, vy);
   }
-  __syncthreads();
-  for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) cnt[(int64_t)blk * gg.nkeys + i] = hist[i];
 }
 
 // Trajectory adjoint: geometry of m records on a (B, 2K, Hg, Wg) grid (16 x 16 tiles only), the block count of
@@ -1709,17 +1809,26 @@ bool rows_geo(int64_t C, int64_t B, int64_t Hg, int64_t Wg, int64_t N, int64_t i
   return true;
 }
 
-// Chunk list, halo clearing, accumulation and halo flush of the trajectory and many-channel adjoints.
+// The scatter launch of the trajectory and many-channel adjoints' records (k_traj_bin<true, ROWS>), which also
+// clears the halo slots and writes the chunk list; then tile_halo_accumulate runs the accumulation and the halo
+// flush.
+template <bool ROWS>
+void traj_scatter(const TileGeo& g, const TrajLayout& L, char* w, const float* pos, const float* gd, const float* t,
+                  const float* t_last, const int64_t* b, int64_t N, int n_look, int per, hipStream_t stream) {
+  const ChunkList cl{(int4*)(w + L.t.info), (int*)(w + L.t.nchunk), kTrajChunk, kTrajChunk};
+  hipLaunchKernelGGL((k_traj_bin<true, ROWS>), dim3(g.nblk + 1), dim3(kTrajBinThreads),
+                     (size_t)g.nkeys * sizeof(int), stream, (const float2*)pos, (const float2*)gd, t, t_last, b,
+                     (int)N, n_look, per, g, (int*)(w + L.t.boff), (float4*)(w + L.t.rec),
+                     ROWS ? (float*)nullptr : (float*)(w + L.tr), cl,
+                     (float*)(w + L.halo), (int64_t)g.nkeys * g.C * kHalo);
+}
+
 template <typename Accum>
 void tile_halo_accumulate(const TileGeo& g, const TrajLayout& L, char* w, int64_t m, float* gfield,
                           hipStream_t stream, Accum accum) {
   int4* info = (int4*)(w + L.t.info);
   int* nchunk = (int*)(w + L.t.nchunk);
   float* halo = (float*)(w + L.halo);
-  hipLaunchKernelGGL(k_tile_chunks, dim3(1), dim3(kChunkScanBlock), 0, stream, (const int*)(w + L.t.boff), g,
-                     kTrajChunk, kTrajChunk, info, nchunk);
-  const int64_t nh = (int64_t)g.nkeys * g.C * kHalo;
-  hipLaunchKernelGGL(k_fill_zero_f, dim3(grid_for(nh)), dim3(kBlock), 0, stream, halo, nh);
   const int64_t nchunks = (int64_t)g.nkeys + (m + kTrajChunk - 1) / kTrajChunk;   // ceil(len / chunk) per tile
   accum((unsigned)nchunks, (const int4*)info, (const int*)nchunk, halo);
   const int64_t nfix = (int64_t)g.nkeys * g.C * (2 * kBinT - 1);
@@ -1746,8 +1855,7 @@ int atl_splat_bilinear_fwd_ws(const float* pos, const float* w, const int64_t* b
   const TileLayout L = tile_layout(g);
   if (!ws || ws_bytes < L.bytes) { set_error("splat_bilinear_fwd_ws: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
   if (!pos || !w || !b || !img) { set_error("splat_bilinear_fwd_ws: null argument"); return 1; }
-  tile_bin<kImage>(g, L, ws, pos, b, w, stream);
-  tile_accum<kImage, 1>(g, L, ws, nullptr, img, stream);
+  tile_bin_accum<kImage, 1>(g, L, ws, pos, b, w, img, stream);
   return check_launch("splat_bilinear_fwd_ws");
 }
 
@@ -1785,8 +1893,7 @@ int atl_splat_bilinear_fwd_noalloc(const float* pos, const float* w, const int64
   if (!pos || !w || !b || !img) { set_error("splat_bilinear_fwd_noalloc: null argument"); return 1; }
   void* ws = nullptr;
   if (noalloc_scratch(&ws) != 0) return 1;
-  tile_bin<kImage>(g, L, ws, pos, b, w, stream);
-  tile_accum<kImage, 1>(g, L, ws, nullptr, img, stream);
+  tile_bin_accum<kImage, 1>(g, L, ws, pos, b, w, img, stream);
   return check_launch("splat_bilinear_fwd_noalloc");
 }
 
@@ -1814,8 +1921,7 @@ int atl_voxel_grid_ws(const float* pos, const float* t, const float* p, const in
   const TileLayout L = tile_layout(g);
   if (!ws || ws_bytes < L.bytes) { set_error("voxel_grid_ws: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
   if (!pos || !t || !p || !b || !vox) { set_error("voxel_grid_ws: null argument"); return 1; }
-  tile_bin<kVoxel>(g, L, ws, pos, b, p, stream, t);
-  tile_accum<kVoxel, 0>(g, L, ws, nullptr, vox, stream);
+  tile_bin_accum<kVoxel, 0>(g, L, ws, pos, b, p, vox, stream, t);
   return check_launch("voxel_grid_ws");
 }
 
@@ -1830,8 +1936,7 @@ int atl_gather_bilinear_bwd_ws(const float* gval, const float* img, const float*
   if (!gval || !img || !pos || !b || !gimg || !gpos) { set_error("gather_bilinear_bwd_ws: null argument"); return 1; }
   hipLaunchKernelGGL(k_gather_bwd_pos, dim3(grid_for(N)), dim3(kBlock), 0, stream, gval, img, (const float2*)pos, b,
                      N, B, (int)H, (int)W, (float2*)gpos);
-  tile_bin<kImage>(g, L, ws, pos, b, gval, stream);
-  tile_accum<kImage, 1>(g, L, ws, nullptr, gimg, stream);
+  tile_bin_accum<kImage, 1>(g, L, ws, pos, b, gval, gimg, stream);
   return check_launch("gather_bilinear_bwd_ws");
 }
 
@@ -1853,8 +1958,7 @@ int atl_splat_gauss_fwd_ws(const float* pos, const float* w, const int64_t* b, i
   const float s2 = (float)(sigma * sigma);        // the per-event kernel's constants, same fp32 expressions
   g.inv2s2 = 1.f / (2.f * s2);
   g.norm = 1.f / (2.f * (float)M_PI * s2);
-  tile_bin<kGauss>(g, L, ws, pos, b, w, stream);
-  tile_accum<kGauss, 1>(g, L, ws, nullptr, img, stream);
+  tile_bin_accum<kGauss, 1>(g, L, ws, pos, b, w, img, stream);
   return check_launch("splat_gauss_fwd_ws");
 }
 
@@ -1887,11 +1991,10 @@ int atl_sample_grid_bwd_binned(const float* gout, int64_t B, int64_t C, int64_t 
   if (!ws || ws_bytes < L.bytes) { set_error("sample_grid_bwd_binned: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
   if (N == 0) return 0;
   if (!gout || !pos || !b || !gfield) { set_error("sample_grid_bwd_binned: null argument"); return 1; }
-  tile_bin<kGridVal>(g, L, ws, pos, b, gout, stream);
   if (C == 1)
-    tile_accum<kGridVal, 1>(g, L, ws, nullptr, gfield, stream);
+    tile_bin_accum<kGridVal, 1>(g, L, ws, pos, b, gout, gfield, stream);
   else
-    tile_accum<kGridVal, 2>(g, L, ws, nullptr, gfield, stream);
+    tile_bin_accum<kGridVal, 2>(g, L, ws, pos, b, gout, gfield, stream);
   return check_launch("sample_grid_bwd_binned");
 }
 
@@ -1990,10 +2093,9 @@ int atl_traj_field_bwd(const float* gd, const float* pos, const float* t, const 
   const size_t lds = (size_t)g.nkeys * sizeof(int);
   hipLaunchKernelGGL(k_traj_bin<false>, dim3(g.nblk), dim3(kTrajBinThreads), lds, stream, (const float2*)pos,
                      (const float2*)gd, t, t_last, b, (int)N, (int)n_look, per, g, cnt, (float4*)nullptr,
-                     (float*)nullptr);
+                     (float*)nullptr, ChunkList{}, (float*)nullptr, (int64_t)0);
   scan32t(cnt, g.nkeys, g.nblk, (int*)(w + L.t.part), boff, stream);
-  hipLaunchKernelGGL(k_traj_bin<true>, dim3(g.nblk), dim3(kTrajBinThreads), lds, stream, (const float2*)pos,
-                     (const float2*)gd, t, t_last, b, (int)N, (int)n_look, per, g, boff, rec, tr);
+  traj_scatter<false>(g, L, w, pos, gd, t, t_last, b, N, (int)n_look, per, stream);
   tile_halo_accumulate(g, L, w, m, gfield, stream, [&](unsigned grid, const int4* info, const int* nchunk, float* halo) {
     auto launch = [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(grid), dim3(kAccBlock), 0, stream, info, nchunk, (const float4*)rec,
@@ -2040,11 +2142,9 @@ int atl_sample_grid_bwd_rows(const float* gout, int64_t B, int64_t C, int64_t Hg
   const size_t lds = (size_t)g.nkeys * sizeof(int);
   hipLaunchKernelGGL((k_traj_bin<false, true>), dim3(g.nblk), dim3(kTrajBinThreads), lds, stream, (const float2*)pos,
                      (const float2*)nullptr, (const float*)nullptr, (const float*)nullptr, b, (int)N, 1, per, g, cnt,
-                     (float4*)nullptr, (float*)nullptr);
+                     (float4*)nullptr, (float*)nullptr, ChunkList{}, (float*)nullptr, (int64_t)0);
   scan32t(cnt, g.nkeys, g.nblk, (int*)(w + L.t.part), boff, stream);
-  hipLaunchKernelGGL((k_traj_bin<true, true>), dim3(g.nblk), dim3(kTrajBinThreads), lds, stream, (const float2*)pos,
-                     (const float2*)nullptr, (const float*)nullptr, (const float*)nullptr, b, (int)N, 1, per, g, boff,
-                     rec, (float*)nullptr);
+  traj_scatter<true>(g, L, w, pos, nullptr, nullptr, nullptr, b, N, 1, per, stream);
   tile_halo_accumulate(g, L, w, N, gfield, stream, [&](unsigned grid, const int4* info, const int* nchunk, float* halo) {
     auto launch = [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(grid), dim3(kAccBlock), 0, stream, info, nchunk, (const float4*)rec, gout, g,
@@ -2075,7 +2175,12 @@ int64_t atl_warp_splat_gather_ws_bytes(int64_t N, int64_t B, int64_t H, int64_t 
 int atl_warp_splat_gather_fwd(const float* grid, int64_t B, int64_t Hg, int64_t Wg, const float* xy, const float* t,
                               const int64_t* b, int64_t N, int64_t H, int64_t W, double t_ref, int64_t mask_border,
                               float* img, float* vals, void* ws, int64_t ws_bytes, hipStream_t stream) {
-  if (N == 0) return 0;
+  if (N == 0) {                                   // img is written: all zero
+    if (!img) { set_error("warp_splat_gather_fwd: null argument"); return 1; }
+    if (B * H * W > 0)
+      hipLaunchKernelGGL(k_fill_zero_f, dim3(grid_for(B * H * W)), dim3(kBlock), 0, stream, img, B * H * W);
+    return check_launch("warp_splat_gather_fwd");
+  }
   WsgLayout L;
   if (!wsg_layout(N, B, H, W, Hg, Wg, L)) { set_error("warp_splat_gather_fwd: unsupported sizes N=%lld B=%lld H=%lld W=%lld Hg=%lld Wg=%lld", (long long)N, (long long)B, (long long)H, (long long)W, (long long)Hg, (long long)Wg); return 1; }
   if (!ws || ws_bytes < L.bytes) { set_error("warp_splat_gather_fwd: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
@@ -2087,13 +2192,17 @@ int atl_warp_splat_gather_fwd(const float* grid, int64_t B, int64_t Hg, int64_t 
   float* wt = (float*)(w + L.w);
   const float sxw = (float)(W - 1 > 1 ? W - 1 : 1), syh = (float)(H - 1 > 1 ? H - 1 : 1);
   const size_t lds = (size_t)g.nkeys * sizeof(int);
-  hipLaunchKernelGGL(k_wsg_warp, dim3(g.nblk), dim3(kTileBinBlock), lds, stream, grid, (int)Hg, (int)Wg, sxw, syh,
-                     (const float2*)xy, t, b, (float)t_ref, (int)(mask_border != 0), g, y, wt, (int*)(wi + L.Li.cnt));
+  // the flow-grid adjoint's counts (not for one-node grids, whose adjoint is a sum per window)
+  int* cntg = wsg_count(L, B, Hg, Wg) == kCountWarp ? (int*)(w + L.ag + L.Lg.cnt) : nullptr;
+  const size_t wlds = lds + (cntg ? (size_t)L.gg.nkeys * sizeof(int) : 0);
+  hipLaunchKernelGGL(Wg >= 2 ? k_wsg_warp<true> : k_wsg_warp<false>, dim3(g.nblk), dim3(kTileBinBlock), wlds,
+                     stream, grid, (int)Hg, (int)Wg, sxw, syh, (const float2*)xy, t, b, (float)t_ref,
+                     (int)(mask_border != 0), g, y, wt, (int*)(wi + L.Li.cnt), L.gg, cntg, img, B * H * W);
   scan32t((int*)(wi + L.Li.cnt), g.nkeys, g.nblk, (int*)(wi + L.Li.part), (int*)(wi + L.Li.boff), stream);
-  hipLaunchKernelGGL((k_tile_bin<kImage, true, false>), dim3(g.nblk), dim3(kTileBinBlock), lds, stream,
+  hipLaunchKernelGGL((k_tile_bin<kImage, true, false>), dim3(g.nblk + 1), dim3(kTileBinBlock), lds, stream,
                      (const float2*)y, b, (const float*)wt, g, (int*)(wi + L.Li.boff), (float4*)(wi + L.Li.rec),
-                     (const float*)nullptr);
-  tile_accum<kImage, 1>(g, L.Li, wi, nullptr, img, stream);
+                     (const float*)nullptr, tile_chunk_list<kImage, 1>(g, L.Li, wi));
+  tile_accum<kImage, 1>(g, L.Li, wi, nullptr, img, stream, true);
   if (vals)
     hipLaunchKernelGGL(k_wsg_gather, dim3(grid_for(N)), dim3(kBlock), 0, stream, (const float*)img,
                        (const float2*)y, b, N, B, (int)H, (int)W, vals);
@@ -2104,7 +2213,13 @@ int atl_warp_splat_gather_bwd(const float* img, const float* gvals, const float*
                               const float* t, const int64_t* b, int64_t N, int64_t B, int64_t H, int64_t W,
                               int64_t Hg, int64_t Wg, double t_ref, float* ggrid, void* ws, int64_t ws_bytes,
                               hipStream_t stream) {
-  if (N == 0) return 0;
+  if (N == 0) {                                   // ggrid is written: all zero
+    if (!ggrid) { set_error("warp_splat_gather_bwd: null argument"); return 1; }
+    if (B * 2 * Hg * Wg > 0)
+      hipLaunchKernelGGL(k_fill_zero_f, dim3(grid_for(B * 2 * Hg * Wg)), dim3(kBlock), 0, stream, ggrid,
+                         B * 2 * Hg * Wg);
+    return check_launch("warp_splat_gather_bwd");
+  }
   WsgLayout L;
   if (!wsg_layout(N, B, H, W, Hg, Wg, L)) { set_error("warp_splat_gather_bwd: unsupported sizes"); return 1; }
   if (!ws || ws_bytes < L.bytes) { set_error("warp_splat_gather_bwd: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
@@ -2115,27 +2230,35 @@ int atl_warp_splat_gather_bwd(const float* img, const float* gvals, const float*
   float2* ig = (float2*)(w + L.G);
   const int64_t npix = B * H * W;
   // (img, G) with G = gimg + splat(y, gvals), the image gradient, accumulated on the forward's records
-  hipLaunchKernelGGL(k_wsg_pack, dim3(grid_for(npix)), dim3(kBlock), 0, stream, img, gimg, npix, ig);
+  hipLaunchKernelGGL(k_wsg_pack, dim3(grid_for(npix)), dim3(kBlock), 0, stream, img, gimg, npix, ig, ggrid,
+                     B * 2 * Hg * Wg);
   if (gvals) {
     TileGeo gi = L.gi;
     gi.ilv = 2;
     tile_accum<kImageG, 1>(gi, L.Li, wi, gvals, (float*)ig, stream, true);
   }
   const TileGeo& gg = L.gg;
-  hipLaunchKernelGGL(k_wsg_grad, dim3(gg.nblk), dim3(kTileBinBlock), (size_t)gg.nkeys * sizeof(int), stream,
-                     (const float2*)ig, gvals, (const float2*)(w + L.y), (const float*)(w + L.w), (const float2*)xy,
-                     t, b, (float)t_ref, (int)H, (int)W, gg, (float2*)(w + L.gv), (int*)(wg + L.Lg.cnt));
-  if (Hg == 1 && Wg == 1 && B <= kOneNodeMaxB) {   // a translation: the adjoint is a sum per window
+  if (wsg_one_node(B, Hg, Wg)) {                  // a translation: the adjoint is a sum per window
+    hipLaunchKernelGGL(k_wsg_grad<false>, dim3(gg.nblk), dim3(kTileBinBlock), 0, stream, (const float2*)ig, gvals,
+                       (const float2*)(w + L.y), (const float*)(w + L.w), (const float2*)xy, t, b, (float)t_ref,
+                       (int)H, (int)W, gg, (float2*)(w + L.gv), (const int*)nullptr, (float4*)nullptr, ChunkList{});
     const unsigned nb = std::min<unsigned>(grid_for(N), kOneNodeBlocks);
     hipLaunchKernelGGL(k_one_node_adjoint, dim3(nb), dim3(kBlock), 0, stream, (const float2*)(w + L.gv), b, N,
                        (int)B, ggrid);
     return check_launch("warp_splat_gather_bwd");
   }
+  // the rows' flow-grid tiles are counted by the forward's k_wsg_warp (or here), and k_wsg_grad writes the records
+  // in place
+  if (wsg_count(L, B, Hg, Wg) == kCountBwd)
+    hipLaunchKernelGGL((k_tile_bin<kGridVal, false, false>), dim3(gg.nblk), dim3(kTileBinBlock),
+                       (size_t)gg.nkeys * sizeof(int), stream, (const float2*)xy, b, (const float*)nullptr, gg,
+                       (int*)(wg + L.Lg.cnt), (float4*)nullptr, (const float*)nullptr);
   scan32t((int*)(wg + L.Lg.cnt), gg.nkeys, gg.nblk, (int*)(wg + L.Lg.part), (int*)(wg + L.Lg.boff), stream);
-  hipLaunchKernelGGL((k_tile_bin<kGridVal, true>), dim3(gg.nblk), dim3(kTileBinBlock),
-                     (size_t)gg.nkeys * sizeof(int), stream, (const float2*)xy, b, (const float*)(w + L.gv), gg,
-                     (int*)(wg + L.Lg.boff), (float4*)(wg + L.Lg.rec), (const float*)nullptr);
-  tile_accum<kGridVal, 2>(gg, L.Lg, wg, nullptr, ggrid, stream);
+  hipLaunchKernelGGL(k_wsg_grad<true>, dim3(gg.nblk + 1), dim3(kTileBinBlock), (size_t)gg.nkeys * sizeof(int),
+                     stream, (const float2*)ig, gvals, (const float2*)(w + L.y), (const float*)(w + L.w),
+                     (const float2*)xy, t, b, (float)t_ref, (int)H, (int)W, gg, (float2*)nullptr,
+                     (const int*)(wg + L.Lg.boff), (float4*)(wg + L.Lg.rec), tile_chunk_list<kGridVal, 2>(gg, L.Lg, wg));
+  tile_accum<kGridVal, 2>(gg, L.Lg, wg, nullptr, ggrid, stream, true);
   return check_launch("warp_splat_gather_bwd");
 }
 

@@ -301,7 +301,7 @@ class _WarpSplatGather(torch.autograd.Function):
         nbytes = int(lib.atl_warp_splat_gather_ws_bytes(N, B, H, W, Hg, Wg))
         if nbytes < 0:
             raise ValueError(f"warp_splat_gather: unsupported sizes N={N} B={B} {H}x{W}, grid {Hg}x{Wg}")
-        img = torch.zeros(B, H, W, device=xy.device, dtype=F32)
+        img = torch.empty(B, H, W, device=xy.device, dtype=F32)          # written by the launch
         vals = torch.empty(N, device=xy.device, dtype=F32)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=xy.device)
         with torch.cuda.device(xy.device):
@@ -318,7 +318,7 @@ class _WarpSplatGather(torch.autograd.Function):
         B, H, W, Hg, Wg = ctx.shape
         if not ctx.needs_input_grad[0] or (gimg is None and gvals is None):
             return (None,) * 8
-        ggrid = torch.zeros(B, 2, Hg, Wg, device=xy.device, dtype=F32)
+        ggrid = torch.empty(B, 2, Hg, Wg, device=xy.device, dtype=F32)   # written by the launch
         gimg = None if gimg is None else gimg.contiguous().float()
         gvals = None if gvals is None else gvals.contiguous().float()
         with torch.cuda.device(xy.device):
