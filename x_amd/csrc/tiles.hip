@@ -36,7 +36,7 @@ using namespace atlhip;
 namespace {
 
 constexpr int kTilePerBlock = 4096;              // binning: events per block
-constexpr int kTileBinBlock = 512;               // binning: threads per block (8 events each)
+constexpr int kTileBinBlock = 1024;              // binning: threads per block (4 events each)
 constexpr int kTileMaxKeys = 16384;              // LDS histogram capacity (tiles over all batches)
 constexpr int kAccBlock = 256;                   // accumulation: threads per tile
 constexpr int kMaxChannels = 32;                 // field channels of the tile adjoint (LDS: C x 17 x 17 floats)
@@ -1455,13 +1455,10 @@ int noalloc_scratch(void** out) {
 // kernel that writes it straight into its flow-grid tile slot, and accumulates the flow-grid adjoint on the tile
 // engine.  The image (forward) and the flow-grid gradient (backward) are written, not accumulated: the first
 // kernel of each clears them.  Every per-event expression is the composed path's, in its fp32 order.
-struct WsgLayout {
-  TileGeo gi, gg;              // image tiles (kImage / kImageG), flow-grid tiles (kGridVal, 2 channels)
-  TileLayout Li, Lg;
-  int64_t ai, ag;              // byte offsets of the two tile-engine regions
-  int64_t y, w, gv, G, bytes;  // warped positions (N float2), weights (N), flow gradients (N float2, one-node
-                               // grids only), and the (image, image gradient) pairs (B H W float2)
-};
+// The per-event kernels of the pipeline (k_wsg_warp, k_wsg_grad) take k_tile_bin's 4096 events per block in
+// 1024 threads of 4 events: 16 waves per CU hide their gathers' latency better than 8 waves of 8 events.
+constexpr int kWsgBlock = 1024;
+static_assert(kTilePerBlock % kWsgBlock == 0, "whole events per thread");
 
 // One-node grids (Hg = Wg = 1, a translation) of at most kOneNodeMaxB windows: the adjoint is a sum per window.
 constexpr int kOneNodeMaxB = 64;
@@ -1469,55 +1466,80 @@ constexpr int kOneNodeBlocks = 256;
 
 bool wsg_one_node(int64_t B, int64_t Hg, int64_t Wg) { return Hg == 1 && Wg == 1 && B <= kOneNodeMaxB; }
 
+// Where the flow-grid adjoint's tile counts are made: in the forward's k_wsg_warp when both histograms fit its
+// LDS (kCountWarp: one count matrix over both key spaces, one scan), else by a counting pass and a scan of their
+// own in the backward (kCountBwd); none for one-node grids.
+enum WsgCount { kCountNone, kCountWarp, kCountBwd };
+
+struct WsgLayout {
+  TileGeo gi, gg;              // image tiles (kImage / kImageG), flow-grid tiles (kGridVal, 2 channels)
+  TileLayout Li, Lg;           // views (offsets from the workspace base) into one count matrix, one offset array
+                               // and one record array, with a chunk list each
+  WsgCount count;
+  int nkc;                     // count matrix columns (keys): gi.nkeys + gg.nkeys with kCountWarp, else gi.nkeys
+  int64_t y, w, gv, G, bytes;  // warped positions (N float2), weights (N), flow gradients (N float2, one-node
+                               // grids only), and the (image, image gradient) pairs (B H W float2)
+};
+
+// With kCountWarp the joint scan puts the image records at [0, Ni) and the flow-grid records at [Ni, Ni + Ng) of
+// the record array (the grid's offsets follow the image's); otherwise the grid's records have their own scan and
+// the array's second half.
 bool wsg_layout(int64_t N, int64_t B, int64_t H, int64_t W, int64_t Hg, int64_t Wg, WsgLayout& L) {
   if (N < 1 || B < 1 || H < 1 || W < 1 || Hg < 1 || Wg < 1) return false;
   if (!tile_geo(kImage, B, H, W, N, 0, 0, L.gi) || !tile_geo(kGridVal, B, Hg, Wg, N, H, W, L.gg)) return false;
   if (B * H * W >= ((int64_t)1 << 31) || B * 2 * Hg * Wg >= ((int64_t)1 << 31)) return false;
+  if (L.gi.nblk != L.gg.nblk) return false;       // one block partition for both histograms
   L.gg.C = 2;
-  L.Li = tile_layout(L.gi);
-  L.Lg = tile_layout(L.gg);
+  L.count = wsg_one_node(B, Hg, Wg) ? kCountNone : L.gi.nkeys + L.gg.nkeys <= kTileMaxKeys ? kCountWarp : kCountBwd;
+  L.nkc = L.count == kCountWarp ? L.gi.nkeys + L.gg.nkeys : L.gi.nkeys;
+  const int64_t nblk = L.gi.nblk, nbh = (int64_t)(L.gi.nkeys + L.gg.nkeys) * nblk;
   int64_t off = 0;
-  L.ai = off; off += align256(L.Li.bytes);
-  L.ag = off; off += align256(L.Lg.bytes);
+  const int64_t cnt = off;  off += align256(nbh * 4);
+  const int64_t boff = off; off += align256((nbh + 1) * 4);
+  const int64_t part = off; off += align256((scan_tiles(nbh) + 1) * 4);
+  const int64_t rec = off;  off += align256(2 * N * 16);
+  L.Li.info = off;   off += align256(max_chunks(L.gi) * 16);
+  L.Li.nchunk = off; off += 256;
+  L.Lg.info = off;   off += align256(max_chunks(L.gg) * 16);
+  L.Lg.nchunk = off; off += 256;
+  L.Li.cnt = L.Lg.cnt = cnt;
+  L.Li.part = L.Lg.part = part;
+  L.Li.boff = boff;
+  L.Lg.boff = boff + (int64_t)L.gi.nkeys * nblk * 4;
+  L.Li.rec = rec;
+  L.Lg.rec = L.count == kCountWarp ? rec : rec + N * 16;
   L.y = off;  off += align256(N * 8);
   L.w = off;  off += align256(N * 4);
   L.gv = off; off += align256(N * 8);
   L.G = off;  off += align256(B * H * W * 8);
-  L.bytes = off;
-  return L.gi.nblk == L.gg.nblk;                  // one block partition for both histograms
-}
-
-// Where the flow-grid adjoint's tile counts are made: in the forward's k_wsg_warp when both histograms fit its
-// LDS, else by a counting pass in the backward; none for one-node grids.
-enum WsgCount { kCountNone, kCountWarp, kCountBwd };
-WsgCount wsg_count(const WsgLayout& L, int64_t B, int64_t Hg, int64_t Wg) {
-  if (wsg_one_node(B, Hg, Wg)) return kCountNone;
-  return L.gi.nkeys + L.gg.nkeys <= kTileMaxKeys ? kCountWarp : kCountBwd;
+  L.bytes = L.Li.bytes = L.Lg.bytes = off;
+  return true;
 }
 
 // Warp, weight and the image-tile histogram, with the block partition of k_tile_bin (4096 events per block) so
 // that its scatter pass finds the same per-block counts.  Every event with an in-image base corner is counted,
-// masked ones (w = 0) included: the value gradient of the gather reaches them.  With cntg, the flow-grid tile
-// histogram of the events' own positions too (every event of a valid window: the backward's k_wsg_grad places
-// its gradient rows by it, over the same partition).  The threads also clear the nz floats of `zero` (the image,
+// masked ones (w = 0) included: the value gradient of the gather reaches them.  Counts go to cnt[block * cstride
+// + key]; with countg, the flow-grid tile histogram of the events' own positions too, at columns g.nkeys + key
+// (every event of a valid window: the backward's k_wsg_grad places its gradient rows by it, over the same
+// partition).  The threads also clear the nz floats of `zero` (the image,
 // which the splat then accumulates).  WIDE (Wg >= 2): each row's two corners are adjacent and load as one 8-byte
 // pair per channel; a single kernel with both forms compiled to four separate 4-byte loads per row.
 template <bool WIDE>
-__global__ void __launch_bounds__(kTileBinBlock) k_wsg_warp(const float* __restrict__ grid, int Hg, int Wg,
+__global__ void __launch_bounds__(kWsgBlock) k_wsg_warp(const float* __restrict__ grid, int Hg, int Wg,
                                                             float sxw, float syh, const float2* __restrict__ xy,
                                                             const float* __restrict__ t,
                                                             const int64_t* __restrict__ bidx, float t_ref, int mask,
                                                             TileGeo g, float2* __restrict__ y, float* __restrict__ w,
-                                                            int* __restrict__ cnt, TileGeo gg, int* __restrict__ cntg,
-                                                            float* __restrict__ zero, int64_t nz) {
+                                                            int* __restrict__ cnt, int cstride, TileGeo gg,
+                                                            bool countg, float* __restrict__ zero, int64_t nz) {
   extern __shared__ int hist[];
   int* histg = hist + g.nkeys;
   const int blk = blockIdx.x;
   for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) hist[i] = 0;
-  if (cntg)
+  if (countg)
     for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) histg[i] = 0;
   for (int64_t k = (int64_t)blk * blockDim.x + threadIdx.x; k < nz; k += (int64_t)gridDim.x * blockDim.x) zero[k] = 0.f;
-  constexpr int per = kTilePerBlock / kTileBinBlock;
+  constexpr int per = kTilePerBlock / kWsgBlock;
   const int j0 = blk * kTilePerBlock;
   const int64_t plane = (int64_t)Hg * Wg;
   const float wmax = (float)(g.W - 1), hmax = (float)(g.H - 1);
@@ -1526,7 +1548,7 @@ __global__ void __launch_bounds__(kTileBinBlock) k_wsg_warp(const float* __restr
   int64_t bj[per];
 #pragma unroll
   for (int u = 0; u < per; ++u) {                 // every event's inputs first, then every flow row
-    const int j = j0 + u * kTileBinBlock + threadIdx.x;
+    const int j = j0 + u * kWsgBlock + threadIdx.x;
     bj[u] = j < g.N ? bidx[j] : -1;
     p[u] = j < g.N ? xy[j] : make_float2(0.f, 0.f);
     tj[u] = j < g.N ? t[j] : 0.f;
@@ -1555,7 +1577,7 @@ __global__ void __launch_bounds__(kTileBinBlock) k_wsg_warp(const float* __restr
   __syncthreads();                                // the histogram is cleared
 #pragma unroll
   for (int u = 0; u < per; ++u) {
-    const int j = j0 + u * kTileBinBlock + threadIdx.x;
+    const int j = j0 + u * kWsgBlock + threadIdx.x;
     if (j >= g.N) continue;
     float vx = ra[u].x * c[u].w00;                // atl/motion/parametric.py:235-251, the device sampler's order
     vx = vx + ra[u].y * c[u].w01;
@@ -1573,15 +1595,16 @@ __global__ void __launch_bounds__(kTileBinBlock) k_wsg_warp(const float* __restr
     w[j] = wj;
     const int key = tile_key<kImage>(yx, yy, bj[u], g);
     if (key >= 0) atomicAdd(hist + key, 1);
-    if (cntg) {
+    if (countg) {
       const int kg = tile_key<kGridVal>(p[u].x, p[u].y, bj[u], gg);
       if (kg >= 0) atomicAdd(histg + kg, 1);
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) cnt[(int64_t)blk * g.nkeys + i] = hist[i];
-  if (cntg)
-    for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) cntg[(int64_t)blk * gg.nkeys + i] = histg[i];
+  int* __restrict__ row = cnt + (int64_t)blk * cstride;
+  for (int i = threadIdx.x; i < g.nkeys; i += blockDim.x) row[i] = hist[i];
+  if (countg)
+    for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) row[g.nkeys + i] = histg[i];
 }
 
 // vals_j = gather(img, y_j): csrc/atl_cpu.cpp:134-149.
@@ -1676,7 +1699,7 @@ __global__ void __launch_bounds__(kBlock) k_wsg_pack(const float* __restrict__ i
 // (boff; a zero row adds nothing and keeps its slot); otherwise the rows are written to gv (one-node grids).
 // RECS with nblk + 1 workgroups: the last one writes the chunk list `cl` of the records.
 template <bool RECS>
-__global__ void __launch_bounds__(kTileBinBlock) k_wsg_grad(const float2* __restrict__ ig,
+__global__ void __launch_bounds__(kWsgBlock) k_wsg_grad(const float2* __restrict__ ig,
                                                             const float* __restrict__ gvals,
                                                             const float2* __restrict__ y, const float* __restrict__ w,
                                                             const float2* __restrict__ xy,
@@ -1688,19 +1711,19 @@ __global__ void __launch_bounds__(kTileBinBlock) k_wsg_grad(const float2* __rest
   extern __shared__ int hist[];
   const int blk = blockIdx.x;
   if (RECS && blk == gg.nblk) {
-    tile_chunks_body<kTileBinBlock>(boff, gg, cl);
+    tile_chunks_body<kWsgBlock>(boff, gg, cl);
     return;
   }
   if (RECS)
     for (int i = threadIdx.x; i < gg.nkeys; i += blockDim.x) hist[i] = boff[i * gg.nblk + blk];
-  constexpr int per = kTilePerBlock / kTileBinBlock;
+  constexpr int per = kTilePerBlock / kWsgBlock;
   const int j0 = blk * kTilePerBlock;
   const int64_t pl = (int64_t)H * W;
   float2 p[per];
   int64_t bj[per];
 #pragma unroll
   for (int u = 0; u < per; ++u) {                 // positions first, then every corner row of every event
-    const int j = j0 + u * kTileBinBlock + threadIdx.x;
+    const int j = j0 + u * kWsgBlock + threadIdx.x;
     bj[u] = j < gg.N ? bidx[j] : -1;
     p[u] = j < gg.N ? y[j] : make_float2(0.f, 0.f);
   }
@@ -1728,7 +1751,7 @@ __global__ void __launch_bounds__(kTileBinBlock) k_wsg_grad(const float2* __rest
   __syncthreads();                                // the run starts are loaded
 #pragma unroll
   for (int u = 0; u < per; ++u) {
-    const int j = j0 + u * kTileBinBlock + threadIdx.x;
+    const int j = j0 + u * kWsgBlock + threadIdx.x;
     if (j >= gg.N) continue;
     float s1x = 0.f, s1y = 0.f, s2x = 0.f, s2y = 0.f;
     const float fx = floorf(p[u].x), fy = floorf(p[u].y);
@@ -2186,23 +2209,22 @@ int atl_warp_splat_gather_fwd(const float* grid, int64_t B, int64_t Hg, int64_t 
   if (!ws || ws_bytes < L.bytes) { set_error("warp_splat_gather_fwd: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
   if (!grid || !xy || !t || !b || !img) { set_error("warp_splat_gather_fwd: null argument"); return 1; }
   char* w = (char*)ws;
-  char* wi = w + L.ai;
   const TileGeo& g = L.gi;
   float2* y = (float2*)(w + L.y);
   float* wt = (float*)(w + L.w);
   const float sxw = (float)(W - 1 > 1 ? W - 1 : 1), syh = (float)(H - 1 > 1 ? H - 1 : 1);
   const size_t lds = (size_t)g.nkeys * sizeof(int);
-  // the flow-grid adjoint's counts (not for one-node grids, whose adjoint is a sum per window)
-  int* cntg = wsg_count(L, B, Hg, Wg) == kCountWarp ? (int*)(w + L.ag + L.Lg.cnt) : nullptr;
-  const size_t wlds = lds + (cntg ? (size_t)L.gg.nkeys * sizeof(int) : 0);
-  hipLaunchKernelGGL(Wg >= 2 ? k_wsg_warp<true> : k_wsg_warp<false>, dim3(g.nblk), dim3(kTileBinBlock), wlds,
+  // with kCountWarp, the flow-grid adjoint's counts too, and one scan over both key spaces
+  const bool joint = L.count == kCountWarp;
+  const size_t wlds = lds + (joint ? (size_t)L.gg.nkeys * sizeof(int) : 0);
+  hipLaunchKernelGGL(Wg >= 2 ? k_wsg_warp<true> : k_wsg_warp<false>, dim3(g.nblk), dim3(kWsgBlock), wlds,
                      stream, grid, (int)Hg, (int)Wg, sxw, syh, (const float2*)xy, t, b, (float)t_ref,
-                     (int)(mask_border != 0), g, y, wt, (int*)(wi + L.Li.cnt), L.gg, cntg, img, B * H * W);
-  scan32t((int*)(wi + L.Li.cnt), g.nkeys, g.nblk, (int*)(wi + L.Li.part), (int*)(wi + L.Li.boff), stream);
+                     (int)(mask_border != 0), g, y, wt, (int*)(w + L.Li.cnt), L.nkc, L.gg, joint, img, B * H * W);
+  scan32t((int*)(w + L.Li.cnt), L.nkc, g.nblk, (int*)(w + L.Li.part), (int*)(w + L.Li.boff), stream);
   hipLaunchKernelGGL((k_tile_bin<kImage, true, false>), dim3(g.nblk + 1), dim3(kTileBinBlock), lds, stream,
-                     (const float2*)y, b, (const float*)wt, g, (int*)(wi + L.Li.boff), (float4*)(wi + L.Li.rec),
-                     (const float*)nullptr, tile_chunk_list<kImage, 1>(g, L.Li, wi));
-  tile_accum<kImage, 1>(g, L.Li, wi, nullptr, img, stream, true);
+                     (const float2*)y, b, (const float*)wt, g, (int*)(w + L.Li.boff), (float4*)(w + L.Li.rec),
+                     (const float*)nullptr, tile_chunk_list<kImage, 1>(g, L.Li, w));
+  tile_accum<kImage, 1>(g, L.Li, w, nullptr, img, stream, true);
   if (vals)
     hipLaunchKernelGGL(k_wsg_gather, dim3(grid_for(N)), dim3(kBlock), 0, stream, (const float*)img,
                        (const float2*)y, b, N, B, (int)H, (int)W, vals);
@@ -2225,8 +2247,6 @@ int atl_warp_splat_gather_bwd(const float* img, const float* gvals, const float*
   if (!ws || ws_bytes < L.bytes) { set_error("warp_splat_gather_bwd: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)L.bytes); return 1; }
   if (!img || !xy || !t || !b || !ggrid) { set_error("warp_splat_gather_bwd: null argument"); return 1; }
   char* w = (char*)ws;
-  char* wi = w + L.ai;
-  char* wg = w + L.ag;
   float2* ig = (float2*)(w + L.G);
   const int64_t npix = B * H * W;
   // (img, G) with G = gimg + splat(y, gvals), the image gradient, accumulated on the forward's records
@@ -2235,11 +2255,11 @@ int atl_warp_splat_gather_bwd(const float* img, const float* gvals, const float*
   if (gvals) {
     TileGeo gi = L.gi;
     gi.ilv = 2;
-    tile_accum<kImageG, 1>(gi, L.Li, wi, gvals, (float*)ig, stream, true);
+    tile_accum<kImageG, 1>(gi, L.Li, w, gvals, (float*)ig, stream, true);
   }
   const TileGeo& gg = L.gg;
-  if (wsg_one_node(B, Hg, Wg)) {                  // a translation: the adjoint is a sum per window
-    hipLaunchKernelGGL(k_wsg_grad<false>, dim3(gg.nblk), dim3(kTileBinBlock), 0, stream, (const float2*)ig, gvals,
+  if (L.count == kCountNone) {                    // a translation: the adjoint is a sum per window
+    hipLaunchKernelGGL(k_wsg_grad<false>, dim3(gg.nblk), dim3(kWsgBlock), 0, stream, (const float2*)ig, gvals,
                        (const float2*)(w + L.y), (const float*)(w + L.w), (const float2*)xy, t, b, (float)t_ref,
                        (int)H, (int)W, gg, (float2*)(w + L.gv), (const int*)nullptr, (float4*)nullptr, ChunkList{});
     const unsigned nb = std::min<unsigned>(grid_for(N), kOneNodeBlocks);
@@ -2247,18 +2267,19 @@ int atl_warp_splat_gather_bwd(const float* img, const float* gvals, const float*
                        (int)B, ggrid);
     return check_launch("warp_splat_gather_bwd");
   }
-  // the rows' flow-grid tiles are counted by the forward's k_wsg_warp (or here), and k_wsg_grad writes the records
-  // in place
-  if (wsg_count(L, B, Hg, Wg) == kCountBwd)
+  // the rows' flow-grid tiles were counted and scanned by the forward (kCountWarp) or are here (kCountBwd), and
+  // k_wsg_grad writes the records in place
+  if (L.count == kCountBwd) {
     hipLaunchKernelGGL((k_tile_bin<kGridVal, false, false>), dim3(gg.nblk), dim3(kTileBinBlock),
                        (size_t)gg.nkeys * sizeof(int), stream, (const float2*)xy, b, (const float*)nullptr, gg,
-                       (int*)(wg + L.Lg.cnt), (float4*)nullptr, (const float*)nullptr);
-  scan32t((int*)(wg + L.Lg.cnt), gg.nkeys, gg.nblk, (int*)(wg + L.Lg.part), (int*)(wg + L.Lg.boff), stream);
-  hipLaunchKernelGGL(k_wsg_grad<true>, dim3(gg.nblk + 1), dim3(kTileBinBlock), (size_t)gg.nkeys * sizeof(int),
+                       (int*)(w + L.Lg.cnt), (float4*)nullptr, (const float*)nullptr, ChunkList{});
+    scan32t((int*)(w + L.Lg.cnt), gg.nkeys, gg.nblk, (int*)(w + L.Lg.part), (int*)(w + L.Lg.boff), stream);
+  }
+  hipLaunchKernelGGL(k_wsg_grad<true>, dim3(gg.nblk + 1), dim3(kWsgBlock), (size_t)gg.nkeys * sizeof(int),
                      stream, (const float2*)ig, gvals, (const float2*)(w + L.y), (const float*)(w + L.w),
                      (const float2*)xy, t, b, (float)t_ref, (int)H, (int)W, gg, (float2*)nullptr,
-                     (const int*)(wg + L.Lg.boff), (float4*)(wg + L.Lg.rec), tile_chunk_list<kGridVal, 2>(gg, L.Lg, wg));
-  tile_accum<kGridVal, 2>(gg, L.Lg, wg, nullptr, ggrid, stream, true);
+                     (const int*)(w + L.Lg.boff), (float4*)(w + L.Lg.rec), tile_chunk_list<kGridVal, 2>(gg, L.Lg, w));
+  tile_accum<kGridVal, 2>(gg, L.Lg, w, nullptr, ggrid, stream, true);
   return check_launch("warp_splat_gather_bwd");
 }
 
