@@ -95,6 +95,9 @@ def parse():
     ap.add_argument("--copy-mb", type=float, default=0.0)
     ap.add_argument("--calibration", nargs="*", default=[], metavar="DIR",
                     help="counter runs of --calibrate-copy (FETCH_SIZE, WRITE_SIZE)")
+    ap.add_argument("--pairs", type=float, default=0.0,
+                    help="--summarize: contributing pairs K per launch of the pair kernels (the bench line's "
+                         "roofline.pairs), for their VALU lane-slots per pair")
     return ap.parse_args()
 
 
@@ -118,9 +121,10 @@ def _counters(dirs):
     return agg
 
 
-def summarize(dirs, out, title, command, copy_mb, cal_dirs=()):
+def summarize(dirs, out, title, command, copy_mb, cal_dirs=(), pairs=0.0):
     """Markdown summary of rocprofv3 csv output (kernel stats and counters), with the per-launch HBM traffic
-    of every kernel when a calibration copy of copy_mb MiB is among the counter runs."""
+    of every kernel when a calibration copy of copy_mb MiB is among the counter runs, and the VALU lane-slots
+    per contributing pair (SQ_INSTS_VALU x 64 / K) of the pair kernels when K is given."""
     lines = [f"# {title}", "", "Command (repo root, on the MI355X):", "", f"    {command}", ""]
     for f in sorted(sum((glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True) for d in dirs), [])):
         rows = list(csv.DictReader(open(f)))
@@ -154,6 +158,19 @@ def summarize(dirs, out, title, command, copy_mb, cal_dirs=()):
                 write = sum(agg[k]["WRITE_SIZE"]) / len(agg[k]["WRITE_SIZE"]) * scale["WRITE_SIZE"]
                 traffic[k] = (fetch + write) * 1024.0
         lines.append("")
+    if pairs > 0:
+        rows = [(k, agg[k]) for k in sorted(agg) if k.startswith("k_fast_") and "SQ_INSTS_VALU" in agg[k]]
+        if rows:
+            lines += [f"VALU lane-slots per contributing pair (SQ_INSTS_VALU x 64 / K, K = {pairs:.4g} pairs per "
+                      f"launch):", ""]
+            for k, cs in rows:
+                v = sum(cs["SQ_INSTS_VALU"]) / len(cs["SQ_INSTS_VALU"])
+                act = ""
+                if "SQ_THREAD_CYCLES_VALU" in cs:
+                    tc = sum(cs["SQ_THREAD_CYCLES_VALU"]) / len(cs["SQ_THREAD_CYCLES_VALU"])
+                    act = f"; active lanes {tc / (64.0 * v):.2f} (SQ_THREAD_CYCLES_VALU / 64 SQ_INSTS_VALU)"
+                lines.append(f"- {k}: {v * 64.0 / pairs:.1f}{act}")
+            lines.append("")
     if traffic:
         lines += ["HBM traffic per launch (calibrated FETCH_SIZE + WRITE_SIZE):", ""]
         lines += [f"- {k}: {v / 1e6:.1f} MB" for k, v in sorted(traffic.items())]
@@ -727,7 +744,7 @@ def mpcm_lut_main(a, dev):
 def main():
     a = parse()
     if a.summarize:
-        summarize(a.summarize, a.out, a.title, a.command, a.copy_mb, a.calibration)
+        summarize(a.summarize, a.out, a.title, a.command, a.copy_mb, a.calibration, a.pairs)
         return
     if a.calibrate_copy > 0:
         calibrate_copy(a.calibrate_copy)

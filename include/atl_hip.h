@@ -237,6 +237,16 @@ int atl_sample_grid_bwd_rows(const float* gout, int64_t B, int64_t C, int64_t Hg
 
 /* ---------------------------------------------------------------- event noise */
 
+/* Per-image mean and unbiased variance of B images of n pixels each (the IWE contrast of
+ * atl/objectives/cmax.py:23-25, iwe.var(dim=(-2, -1))): mean (B) and var (B) written, var = NaN for n = 1.  Sums in
+ * fp64 over fixed chunks of pixels, added in a fixed order.  ws: atl_image_variance_ws_bytes(B, n) bytes (-1: bad
+ * sizes).  The backward writes gimg (B, n) = gvar[b] * 2 (img - mean[b]) / (n - 1), torch.var's gradient. */
+int64_t atl_image_variance_ws_bytes(int64_t B, int64_t n);
+int atl_image_variance(const float* img, int64_t B, int64_t n, float* mean, float* var, void* ws, int64_t ws_bytes,
+                       hipStream_t stream);
+int atl_image_variance_bwd(const float* img, const float* mean, const float* gvar, int64_t B, int64_t n, float* gimg,
+                           hipStream_t stream);
+
 /* Dequantisation and smoothing noise of AnchoredExact (atl/objectives/ats.py:79-84, where torch.rand - 0.5 and
  * h * torch.randn are drawn on a CPU generator and added): xs (N,2) = xy + U(-1/2, 1/2) per coordinate when
  * dequantize != 0 (else a copy of xy); xa (N,2) = xs + h N(0, 1) per coordinate when xa is not null.  Philox4x32-10

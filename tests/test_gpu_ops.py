@@ -750,3 +750,26 @@ def test_blur_matches_oracle_and_keeps_interior_mass():
     img[0, 10:30, 12:28] = rng.random((20, 16))
     out = N(F.blur(T(img), 2.0))
     assert abs(float(out.sum()) - float(img.sum())) <= 1e-5 * float(img.sum())
+
+
+@pytest.mark.parametrize("shape", [(4, 480, 640), (1, 37, 53), (2, 3, 5, 7), (3, 1, 1)])
+def test_image_variance_matches_fp64(shape):
+    """The IWE contrast's per-image variance (atl/objectives/cmax.py:23-25, iwe.var(dim=(-2, -1))) and its
+    gradient against torch's float64 var on the same images: an IWE-like image (counts plus a constant offset,
+    where the one-pass sum of squares cancels most), a small odd size, extra leading dimensions, and one-pixel
+    images (NaN, as torch.var)."""
+    print(f"image_variance shape={shape}", flush=True)
+    rng = np.random.default_rng(len(shape) + shape[-1])
+    img = (rng.poisson(2.0, shape) + 50.0 + rng.uniform(0, 1, shape)).astype(F32)
+    g = rng.standard_normal(shape[:-2]).astype(F32)
+    x = T(img).requires_grad_(True)
+    v = F.image_variance(x)
+    if shape[-1] * shape[-2] == 1:
+        assert torch.isnan(v).all()
+        return
+    x64 = torch.as_tensor(img.astype(np.float64)).requires_grad_(True)
+    v64 = x64.var(dim=(-2, -1))
+    close_rel(N(v), v64.detach().numpy(), 1e-6)
+    (v * T(g)).sum().backward()
+    (v64 * torch.as_tensor(g.astype(np.float64))).sum().backward()
+    close_rel(N(x.grad), x64.grad.numpy(), 1e-5)

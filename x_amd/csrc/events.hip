@@ -1006,6 +1006,81 @@ __global__ void __launch_bounds__(kBlock) k_event_noise(const float2* __restrict
   }
 }
 
+
+// Per-image mean and unbiased variance of B images of n pixels each: the IWE contrast of
+// atl/objectives/cmax.py:23-25, iwe.var(dim=(-2, -1)), whose library reduction over 4 outputs of 307k pixels
+// each ran in one workgroup per output.  Pass 1: workgroup (image b, chunk c) sums x and x^2 over its kVarChunk
+// pixels in fp64 into part[2 (b nch + c) + {0, 1}]; pass 2: one wave per image adds its chunks' sums in a fixed
+// order and writes mean = S1 / n and var = max(S2 - S1 mean, 0) / (n - 1) (NaN for n = 1, as torch.var).
+constexpr int kVarItems = 16;
+constexpr int kVarChunk = kVarItems * kBlock;   // pixels per workgroup of pass 1
+
+__global__ void __launch_bounds__(kBlock) k_image_var_part(const float* __restrict__ img, int64_t n, int nch,
+                                                           double* __restrict__ part) {
+  __shared__ double red[2][kBlock / kWave];
+  const int b = blockIdx.x / nch, c = blockIdx.x - b * nch;
+  const float* __restrict__ x = img + (int64_t)b * n;
+  const int64_t p0 = (int64_t)c * kVarChunk + threadIdx.x;
+  float v[kVarItems];
+#pragma unroll
+  for (int k = 0; k < kVarItems; ++k) {            // all loads in flight
+    const int64_t p = p0 + (int64_t)k * kBlock;
+    v[k] = p < n ? x[p] : 0.f;
+  }
+  double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+  for (int k = 0; k < kVarItems; ++k) {
+    const double d = v[k];
+    s1 += d;
+    s2 += d * d;
+  }
+  s1 = wave_sum(s1);
+  s2 = wave_sum(s2);
+  const int w = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    red[0][w] = s1;
+    red[1][w] = s2;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t1 = 0.0, t2 = 0.0;
+    for (int i = 0; i < kBlock / kWave; ++i) {
+      t1 += red[0][i];
+      t2 += red[1][i];
+    }
+    part[2 * (int64_t)blockIdx.x] = t1;
+    part[2 * (int64_t)blockIdx.x + 1] = t2;
+  }
+}
+
+__global__ void __launch_bounds__(kWave) k_image_var_fin(const double* __restrict__ part, int nch, int64_t n,
+                                                         float* __restrict__ mean, float* __restrict__ var) {
+  const int64_t base = 2 * (int64_t)blockIdx.x * nch;
+  double s1 = 0.0, s2 = 0.0;
+  for (int c = threadIdx.x; c < nch; c += kWave) {
+    s1 += part[base + 2 * c];
+    s2 += part[base + 2 * c + 1];
+  }
+  s1 = wave_sum(s1);
+  s2 = wave_sum(s2);
+  if (threadIdx.x == 0) {
+    const double m = s1 / (double)n;
+    mean[blockIdx.x] = (float)m;
+    var[blockIdx.x] = n > 1 ? (float)(fmax(s2 - s1 * m, 0.0) / (double)(n - 1)) : __builtin_nanf("");
+  }
+}
+
+// Its backward (the autograd of torch.var): gimg[b, p] = gvar[b] * 2 (img[b, p] - mean[b]) / (n - 1).
+__global__ void __launch_bounds__(kBlock) k_image_var_bwd(const float* __restrict__ img,
+                                                          const float* __restrict__ mean,
+                                                          const float* __restrict__ gvar, int64_t n, int64_t total,
+                                                          float* __restrict__ gimg) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int64_t b = i / n;
+  gimg[i] = gvar[b] * (2.f / (float)(n - 1)) * (img[i] - mean[b]);
+}
+
 }  // namespace
 
 // ================================================================================================ C-ABI
@@ -1344,6 +1419,33 @@ int atl_event_noise(const float* xy, int64_t N, uint64_t seed, uint64_t offset, 
                      (uint32_t)seed, (uint32_t)(seed >> 32), (uint32_t)offset, (uint32_t)(offset >> 32), (float)h,
                      dequantize, (float2*)xs, (float2*)xa);
   return check_launch("event_noise");
+}
+
+int64_t atl_image_variance_ws_bytes(int64_t B, int64_t n) {
+  if (B < 0 || n < 1) return -1;
+  return B * ((n + kVarChunk - 1) / kVarChunk) * 2 * (int64_t)sizeof(double);
+}
+
+int atl_image_variance(const float* img, int64_t B, int64_t n, float* mean, float* var, void* ws, int64_t ws_bytes,
+                       hipStream_t stream) {
+  const int64_t need = atl_image_variance_ws_bytes(B, n);
+  if (need < 0 || B * ((n + kVarChunk - 1) / kVarChunk) >= ((int64_t)1 << 31)) { set_error("image_variance: bad sizes B=%lld n=%lld", (long long)B, (long long)n); return 1; }
+  if (B == 0) return 0;
+  if (!img || !mean || !var || !ws) { set_error("image_variance: null argument"); return 1; }
+  if (ws_bytes < need) { set_error("image_variance: workspace of %lld bytes, need %lld", (long long)ws_bytes, (long long)need); return 1; }
+  const int nch = (int)((n + kVarChunk - 1) / kVarChunk);
+  hipLaunchKernelGGL(k_image_var_part, dim3((unsigned)(B * nch)), dim3(kBlock), 0, stream, img, n, nch, (double*)ws);
+  hipLaunchKernelGGL(k_image_var_fin, dim3((unsigned)B), dim3(kWave), 0, stream, (const double*)ws, nch, n, mean, var);
+  return check_launch("image_variance");
+}
+
+int atl_image_variance_bwd(const float* img, const float* mean, const float* gvar, int64_t B, int64_t n, float* gimg,
+                           hipStream_t stream) {
+  if (B < 0 || n < 1) { set_error("image_variance_bwd: bad sizes B=%lld n=%lld", (long long)B, (long long)n); return 1; }
+  if (B == 0) return 0;
+  if (!img || !mean || !gvar || !gimg) { set_error("image_variance_bwd: null argument"); return 1; }
+  hipLaunchKernelGGL(k_image_var_bwd, dim3(grid_for(B * n)), dim3(kBlock), 0, stream, img, mean, gvar, n, B * n, gimg);
+  return check_launch("image_variance_bwd");
 }
 
 }  // extern "C"

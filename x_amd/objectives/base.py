@@ -11,7 +11,7 @@ from typing import Optional
 import torch
 
 from ..core.events import EventPacket
-from ..ops import blur, gather, layout_scope, splat, warp_splat_gather
+from ..ops import blur, gather, image_variance, layout_scope, splat, warp_splat_gather
 
 
 class Objective:
@@ -120,4 +120,4 @@ def iwe_variance(ev: EventPacket, motion, t_ref: float, cfg: Optional[IWEConfig]
     cfg = cfg or IWEConfig(kernel="bilinear", sigma=0.0)
     with layout_scope():
         img = make_iwe(ev, motion.transport(ev.xy, ev.t, t_ref, ev.b), t_ref, cfg)
-    return img.var(dim=(-2, -1)).mean()
+    return image_variance(img).mean()

@@ -56,6 +56,9 @@ _SIGS = {
     "atl_sample_grid_fwd_cl": [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_sample_grid_bwd_pos_cl": [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P],
     "atl_event_noise": [_P, _I, ctypes.c_uint64, ctypes.c_uint64, _D, _C, _P, _P, _P],
+    "atl_image_variance_ws_bytes": [_I, _I],
+    "atl_image_variance": [_P, _I, _I, _P, _P, _P, _I, _P],
+    "atl_image_variance_bwd": [_P, _P, _P, _I, _I, _P, _P],
     "atl_plan_stats": [_P, _I, _P, _I, _P, _P],
     "atl_plan_count": [_P, _P, _P, _P, _I, _I, _D, _D, _D, _D, _I, _I, _I, _P, _P],
     "atl_scan_counts": [_P, _I, _P, _P, _P],
@@ -119,6 +122,7 @@ _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.
             "atl_voxel_ws_bytes": ctypes.c_int64, "atl_warp_splat_gather_ws_bytes": ctypes.c_int64,
             "atl_ats_pair_ws_bytes": ctypes.c_int64, "atl_traj_field_bwd_bytes": ctypes.c_int64,
             "atl_sample_grid_bwd_rows_bytes": ctypes.c_int64, "atl_plan_sort_bytes": ctypes.c_int64,
+            "atl_image_variance_ws_bytes": ctypes.c_int64,
 "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
 
 class FastGeometry(ctypes.Structure):

@@ -341,6 +341,50 @@ def warp_splat_gather(grid: torch.Tensor, xy: torch.Tensor, t: torch.Tensor, b: 
     return _WarpSplatGather.apply(grid, xy, t, b, float(t_ref), int(H), int(W), bool(mask_border))
 
 
+class _ImageVariance(torch.autograd.Function):
+    """Per-image unbiased variance over the last two dimensions (atl/objectives/cmax.py:23-25, the IWE contrast
+    iwe.var(dim=(-2, -1))) on the device: fp64 sums over fixed pixel chunks in two launches, and torch.var's
+    gradient in one."""
+
+    @staticmethod
+    def forward(ctx, img):
+        x = _f32(img)
+        lead, n = x.shape[:-2], x.shape[-2] * x.shape[-1]
+        B = x.numel() // max(n, 1)
+        mean = torch.empty(B, device=x.device, dtype=F32)
+        var = torch.empty(B, device=x.device, dtype=F32)
+        lib = load_library()
+        nbytes = int(lib.atl_image_variance_ws_bytes(B, n))
+        if nbytes < 0:
+            raise ValueError(f"image_variance: unsupported sizes {tuple(x.shape)}")
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+        with torch.cuda.device(x.device):
+            call("atl_image_variance", ptr(x), B, n, ptr(mean), ptr(var), ptr(ws), nbytes, stream_of(x))
+        ctx.save_for_backward(x, mean)
+        ctx.shape = (B, n)
+        return var.view(lead)
+
+    @staticmethod
+    def backward(ctx, gvar):
+        x, mean = ctx.saved_tensors
+        B, n = ctx.shape
+        g = gvar.contiguous().float().view(B)
+        gimg = torch.empty_like(x)
+        with torch.cuda.device(x.device):
+            call("atl_image_variance_bwd", ptr(x), ptr(mean), ptr(g), B, n, ptr(gimg), stream_of(x))
+        return gimg
+
+
+def image_variance(img: torch.Tensor) -> torch.Tensor:
+    """``img.var(dim=(-2, -1))`` (unbiased, over each image's pixels), differentiable; device tensors run the HIP
+    kernels, host tensors torch's reduction."""
+    if img.dim() < 2 or img.shape[-2] * img.shape[-1] < 1:
+        raise ValueError(f"image_variance needs images of at least one pixel, got {tuple(img.shape)}")
+    if not img.is_cuda:
+        return img.var(dim=(-2, -1))
+    return _ImageVariance.apply(img)
+
+
 class _TrajDisplacement(torch.autograd.Function):
     """PixelTrajectories.displacement in one kernel (atl/motion/trajectories.py: d = sum_k c_k(p) g_k(t), the
     coefficients c_k the border-clamped bilinear sample of a (B, 2K, Hg, Wg) grid at grid coordinates p).
