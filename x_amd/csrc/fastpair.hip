@@ -1277,8 +1277,14 @@ __device__ __forceinline__ void fwd_pass(const FPlan& p, const FGeo& G, int plan
 constexpr int kAnchorsPerWave = 16;
 constexpr int kAnchorsPerBlock = kPairBlock / kWave * kAnchorsPerWave;
 
+// Register budgets (amdgpu_waves_per_eu: the compiler keeps the kernel within the registers of that many waves
+// per SIMD): the forward fits 8 waves without spills (53 VGPRs, 69 unconstrained), the backward 6 (80 VGPRs, three
+// spills outside its walk loop; 88 unconstrained), the trajectory backward 4 at K = 10 (128 VGPRs, 135
+// unconstrained).  Same code, more waves to hide the candidate loads: C3 forward 0.329 -> 0.322 ms, backward
+// 0.446 -> 0.435 ms, C4 trajectory backward 1.89 -> 1.67 ms (alternating runs on one box).  Tighter budgets spill
+// inside the walks (backward at 7 waves: 13 spills; trajectory backward at 5: 42).
 template <bool COUNT>
-__global__ void __launch_bounds__(kPairBlock) k_fast_fwd(FPlan p, FGeo G, int M, float* __restrict__ out,
+__global__ void __launch_bounds__(kPairBlock) __attribute__((amdgpu_waves_per_eu(8))) k_fast_fwd(FPlan p, FGeo G, int M, float* __restrict__ out,
                                                      int* __restrict__ count) {
   const int lb = xcd_block((M + kAnchorsPerBlock - 1) / kAnchorsPerBlock);
   if (lb < 0) return;
@@ -1449,7 +1455,7 @@ __device__ __forceinline__ float2 bwd_source(const FPlan& p, const FGeo& G, floa
 // Backward: every source (one lane each, own-slice tile order) sums, over the anchors of each slice of its
 // range within R of its slice-centre position, gS_i * k * dt / h^2 * r (csrc/atl_cpu.cpp:240-248);
 // gv[j] = the total (each source has one record: no atomics).
-__global__ void __launch_bounds__(kPairBlock) k_fast_bwd(FPlan p, FGeo G, int N, float2* __restrict__ gv,
+__global__ void __launch_bounds__(kPairBlock) __attribute__((amdgpu_waves_per_eu(6))) k_fast_bwd(FPlan p, FGeo G, int N, float2* __restrict__ gv,
                                                       float2* __restrict__ gvr) {
   __shared__ int2 tab[kRowTab * kPairBlock];           // per-lane row spans of the current slice (column threadIdx.x)
   constexpr int kSrcPerWave = kWave / kBwdParts;
@@ -1801,7 +1807,7 @@ __device__ __forceinline__ void bwd_traj_source(const FPlan& p, const FGeo& G, f
 }
 
 template <int K>
-__global__ void __launch_bounds__(kPairBlock) k_fast_bwd_traj(FPlan p, FGeo G, int N, const float* __restrict__ coef,
+__global__ void __launch_bounds__(kPairBlock) __attribute__((amdgpu_waves_per_eu(4))) k_fast_bwd_traj(FPlan p, FGeo G, int N, const float* __restrict__ coef,
                                                              const float* __restrict__ tab, float2* __restrict__ gp,
                                                              float* __restrict__ gcoef) {
   __shared__ int2 rowtab[kRowTab * kPairBlock];
