@@ -1477,8 +1477,10 @@ struct WsgLayout {
                                // and one record array, with a chunk list each
   WsgCount count;
   int nkc;                     // count matrix columns (keys): gi.nkeys + gg.nkeys with kCountWarp, else gi.nkeys
-  int64_t y, w, gv, G, bytes;  // warped positions (N float2), weights (N), flow gradients (N float2, one-node
-                               // grids only), and the (image, image gradient) pairs (B H W float2)
+  int64_t y, w, gv, G, fil;    // warped positions (N float2), weights (N), flow gradients (N float2, one-node
+                               // grids only), the (image, image gradient) pairs (B H W float2), the flow's
+                               // node-interleaved copy (B Hg Wg float2)
+  int64_t bytes;
 };
 
 // With kCountWarp the joint scan puts the image records at [0, Ni) and the flow-grid records at [Ni, Ni + Ng) of
@@ -1512,6 +1514,7 @@ bool wsg_layout(int64_t N, int64_t B, int64_t H, int64_t W, int64_t Hg, int64_t 
   L.w = off;  off += align256(N * 4);
   L.gv = off; off += align256(N * 8);
   L.G = off;  off += align256(B * H * W * 8);
+  L.fil = off; off += align256(B * Hg * Wg * 8);
   L.bytes = L.Li.bytes = L.Lg.bytes = off;
   return true;
 }
@@ -1522,10 +1525,13 @@ bool wsg_layout(int64_t N, int64_t B, int64_t H, int64_t W, int64_t Hg, int64_t 
 // + key]; with countg, the flow-grid tile histogram of the events' own positions too, at columns g.nkeys + key
 // (every event of a valid window: the backward's k_wsg_grad places its gradient rows by it, over the same
 // partition).  The threads also clear the nz floats of `zero` (the image,
-// which the splat then accumulates).  WIDE (Wg >= 2): each row's two corners are adjacent and load as one 8-byte
-// pair per channel; a single kernel with both forms compiled to four separate 4-byte loads per row.
+// which the splat then accumulates).  WIDE (Wg >= 2): the flow is read from its node-interleaved copy fil
+// (B, Hg, Wg, 2; atl_flow_interleave), where a row's two corners with both channels are 16 contiguous bytes, so an
+// event reads two pieces instead of four (the sums are the planar ones, bit for bit); a single kernel with both
+// forms compiled to separate 4-byte loads.
 template <bool WIDE>
-__global__ void __launch_bounds__(kWsgBlock) k_wsg_warp(const float* __restrict__ grid, int Hg, int Wg,
+__global__ void __launch_bounds__(kWsgBlock) k_wsg_warp(const float* __restrict__ grid,
+                                                        const float* __restrict__ fil, int Hg, int Wg,
                                                             float sxw, float syh, const float2* __restrict__ xy,
                                                             const float* __restrict__ t,
                                                             const int64_t* __restrict__ bidx, float t_ref, int mask,
@@ -1561,14 +1567,13 @@ __global__ void __launch_bounds__(kWsgBlock) k_wsg_warp(const float* __restrict_
     ra[u] = rb[u] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (!batch_ok(bj[u], g.B)) continue;          // sample_grid of an event outside the batch: zero
     const float* f = grid + bj[u] * 2 * plane;
-    if (WIDE) {                                   // o01 = o00 + 1, o11 = o10 + 1: one 8-byte load per row
-      float2 r0, r1, q0, q1;
-      __builtin_memcpy(&r0, f + c[u].o00, sizeof(float2));
-      __builtin_memcpy(&r1, f + c[u].o10, sizeof(float2));
-      __builtin_memcpy(&q0, f + plane + c[u].o00, sizeof(float2));
-      __builtin_memcpy(&q1, f + plane + c[u].o10, sizeof(float2));
-      ra[u] = make_float4(r0.x, r0.y, r1.x, r1.y);
-      rb[u] = make_float4(q0.x, q0.y, q1.x, q1.y);
+    if (WIDE) {                                   // o01 = o00 + 1, o11 = o10 + 1: one 16-byte piece per row
+      const float* fi = fil + bj[u] * 2 * plane;
+      float4 r0, r1;                              // (c0, c1) of corner x0, then of x0 + 1: 8-byte aligned
+      __builtin_memcpy(&r0, fi + 2 * (int64_t)c[u].o00, sizeof(float4));
+      __builtin_memcpy(&r1, fi + 2 * (int64_t)c[u].o10, sizeof(float4));
+      ra[u] = make_float4(r0.x, r0.z, r1.x, r1.z);
+      rb[u] = make_float4(r0.y, r0.w, r1.y, r1.w);
     } else {
       ra[u] = make_float4(f[c[u].o00], f[c[u].o01], f[c[u].o10], f[c[u].o11]);
       rb[u] = make_float4(f[plane + c[u].o00], f[plane + c[u].o01], f[plane + c[u].o10], f[plane + c[u].o11]);
@@ -2217,8 +2222,10 @@ int atl_warp_splat_gather_fwd(const float* grid, int64_t B, int64_t Hg, int64_t 
   // with kCountWarp, the flow-grid adjoint's counts too, and one scan over both key spaces
   const bool joint = L.count == kCountWarp;
   const size_t wlds = lds + (joint ? (size_t)L.gg.nkeys * sizeof(int) : 0);
+  float* fil = (float*)(w + L.fil);
+  if (Wg >= 2 && atl_flow_interleave(grid, B, Hg, Wg, fil, stream) != 0) return 1;
   hipLaunchKernelGGL(Wg >= 2 ? k_wsg_warp<true> : k_wsg_warp<false>, dim3(g.nblk), dim3(kWsgBlock), wlds,
-                     stream, grid, (int)Hg, (int)Wg, sxw, syh, (const float2*)xy, t, b, (float)t_ref,
+                     stream, grid, (const float*)fil, (int)Hg, (int)Wg, sxw, syh, (const float2*)xy, t, b, (float)t_ref,
                      (int)(mask_border != 0), g, y, wt, (int*)(w + L.Li.cnt), L.nkc, L.gg, joint, img, B * H * W);
   scan32t((int*)(w + L.Li.cnt), L.nkc, g.nblk, (int*)(w + L.Li.part), (int*)(w + L.Li.boff), stream);
   hipLaunchKernelGGL((k_tile_bin<kImage, true, false>), dim3(g.nblk + 1), dim3(kTileBinBlock), lds, stream,
