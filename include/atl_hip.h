@@ -93,7 +93,7 @@ int atl_voxel_grid_ws(const float* pos, const float* t, const float* p, const in
  * reference runs as separate ops.  Forward: y = x + v(x) (t_ref - t) with v the border-clamped sample of the flow
  * grid (B,2,Hg,Wg) at pixel x, w = [y inside the sensor] if mask_border else 1, img (B,H,W) = splat(y, w)
  * (written), vals (N) = gather(img, y) (written; may be null).  Backward: ggrid (B,2,Hg,Wg) written with the
- * flow-grid gradient of <gvals, vals> + <gimg, img> (either may be null), from the forward's ws.  ws: atl_warp_splat_gather_ws_bytes bytes (-1: sizes unsupported). */
+ * flow-grid gradient of <gvals, vals> + <gimg, img> (either may be null), from the forward's ws.  ws: atl_warp_splat_gather_ws_bytes bytes (-1: sizes unsupported; 0 for N = 0, whose outputs are zeros). */
 int64_t atl_warp_splat_gather_ws_bytes(int64_t N, int64_t B, int64_t H, int64_t W, int64_t Hg, int64_t Wg);
 int atl_warp_splat_gather_fwd(const float* grid, int64_t B, int64_t Hg, int64_t Wg, const float* xy, const float* t,
                               const int64_t* b, int64_t N, int64_t H, int64_t W, double t_ref, int64_t mask_border,

@@ -290,6 +290,21 @@ def test_iwe_step_graph_has_no_memset_node():
     assert types.count(0) >= 8                     # the step's kernels
 
 
+def test_warp_splat_gather_no_events():
+    """No events: the image and the flow-grid gradient are still written (zeros), though the wrapper allocates
+    both uninitialised, with NaNs left in the allocator's free blocks."""
+    stale = torch.full((4 * 2 * 30 * 44,), float("nan"), device=DEV)
+    del stale
+    tg = torch.ones(2, 2, 30, 44, device=DEV, requires_grad=True)
+    xy = torch.zeros(0, 2, device=DEV)
+    img, vals = F.warp_splat_gather(tg, xy, torch.zeros(0, device=DEV), torch.zeros(0, dtype=torch.long, device=DEV),
+                                    0.5, 30, 44)
+    assert img.shape == (2, 30, 44) and vals.shape == (0,)
+    assert torch.count_nonzero(img).item() == 0 and not torch.isnan(img).any()
+    (img * torch.randn_like(img)).sum().backward()
+    assert torch.count_nonzero(tg.grad).item() == 0 and not torch.isnan(tg.grad).any()
+
+
 def test_warp_splat_gather_rejects_bad_shapes():
     xy = torch.zeros(10, 2, device=DEV)
     t = torch.zeros(10, device=DEV)

@@ -2197,6 +2197,8 @@ int atl_sample_grid_bwd_rows(const float* gout, int64_t B, int64_t C, int64_t Hg
 // Warp -> splat -> gather (the fused pipeline above).  Workspace bytes, or -1 for unsupported sizes.
 int64_t atl_warp_splat_gather_ws_bytes(int64_t N, int64_t B, int64_t H, int64_t W, int64_t Hg, int64_t Wg) {
   WsgLayout L;
+  if (N == 0)                                     // no events: the outputs are zeros, no workspace is read
+    return B >= 1 && H >= 1 && W >= 1 && Hg >= 1 && Wg >= 1 && wsg_layout(1, B, H, W, Hg, Wg, L) ? 0 : -1;
   return wsg_layout(N, B, H, W, Hg, Wg, L) ? L.bytes : -1;
 }
 
