@@ -337,8 +337,8 @@ def cpu_baseline(win, sigma, budget, splat_leg=False):
 IWE_COUNTERS = ROOT / "profiles" / "iwe_1M_640x480_counters.md"
 # the kernels of the fused entry points whose HBM counters the IWE counter summary holds
 IWE_KERNELS = {
-    "atl_warp_splat_gather_fwd": ["k_wsg_warp<true>", "k_tile_bin<0, true, false>", "k_tile_accum_bins<0, 1>",
-                                  "k_wsg_gather"],
+    "atl_warp_splat_gather_fwd": ["k_flow_interleave", "k_wsg_warp<true>", "k_tile_bin<0, true, false>",
+                                  "k_tile_accum_bins<0, 1>", "k_wsg_gather"],
     "atl_warp_splat_gather_bwd": ["k_wsg_pack", "k_tile_accum_bins<5, 1>", "k_wsg_grad<true>",
                                   "k_tile_accum_bins<4, 2>"],
 }
