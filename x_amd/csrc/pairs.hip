@@ -163,6 +163,7 @@ constexpr int kPsMaxBuckets = 16 * kPsScanBlock;
 constexpr int kPsMinShift = 7;                     // 128 cells per bucket at least: many pass-B workgroups
 constexpr int kPsMaxShift = 12;                    // pass B: at most 4096 cells per bucket (16 KB of LDS)
 constexpr int kPsItems = 4;                        // pass B: records per thread in flight together
+constexpr int kPsOne = 8;                          // pass B: buckets of up to kPsOne * kPsBlock records are read once
 
 struct PsRec {
   float4 f;                                        // y.x, y.y, v.x, v.y
@@ -188,13 +189,26 @@ __global__ void __launch_bounds__(kPsBlock) k_psort_pass_a(const float2* __restr
   }
   __syncthreads();
   const int64_t j0 = (int64_t)blk * (kPsPer * kPsBlock) + threadIdx.x;
+  // the thread's sources are read before any is binned, so that all their loads are in flight together
+  int64_t bb[kPsPer];
+  float tt[kPsPer];
+  float2 xx[kPsPer], vv[kPsPer];
+#pragma unroll
+  for (int u = 0; u < kPsPer; ++u) {
+    const int64_t j = min(j0 + (int64_t)u * kPsBlock, N - 1);
+    bb[u] = b[j];
+    tt[u] = t[j];
+    xx[u] = x[j];
+    vv[u] = v[j];
+  }
+#pragma unroll
   for (int u = 0; u < kPsPer; ++u) {
     const int64_t j = j0 + (int64_t)u * kPsBlock;
     if (j >= N) break;
-    const int64_t bj = b[j];
+    const int64_t bj = bb[u];
     if (bj < 0 || bj >= g.B) continue;
-    const float tj = t[j];
-    const float2 xj = x[j], vj = v[j];
+    const float tj = tt[u];
+    const float2 xj = xx[u], vj = vv[u];
     int lo, hi;
     slice_range(tj, g, lo, hi);
     for (int s = lo; s <= hi; ++s) {
@@ -235,7 +249,20 @@ __global__ void __launch_bounds__(kPsBlock) k_psort_pass_b(const PsRec* __restri
   const int4* tki = (const int4*)rec;              // int half of record p: tki[2 p + 1]
   for (int i = threadIdx.x; i < nk; i += kPsBlock) cur[i] = 0;
   __syncthreads();
-  for (int k = lo + (int)threadIdx.x; k < hi; k += kPsBlock) atomicAdd(cur + (tki[2 * k + 1].x - base), 1);
+  // a bucket of up to kPsOne * kPsBlock records is read once: the records stay in registers with their rank
+  // among the records of their cell (the count's return value), and are written after the scan
+  const bool one = hi - lo <= kPsOne * kPsBlock;
+  PsRec r1[kPsOne];
+  int rk[kPsOne];
+  if (one && hi > lo) {                            // positions clamped into the bucket: every load in flight at once
+#pragma unroll
+    for (int u = 0; u < kPsOne; ++u) r1[u] = rec[min(lo + u * kPsBlock + (int)threadIdx.x, hi - 1)];
+#pragma unroll
+    for (int u = 0; u < kPsOne; ++u)
+      rk[u] = lo + u * kPsBlock + (int)threadIdx.x < hi ? atomicAdd(cur + (r1[u].i.x - base), 1) : 0;
+  } else if (!one) {
+    for (int k = lo + (int)threadIdx.x; k < hi; k += kPsBlock) atomicAdd(cur + (tki[2 * k + 1].x - base), 1);
+  }
   __syncthreads();
   const int per = nk > kPsBlock ? nk / kPsBlock : 1;   // cells per thread in the scan
   const int c0 = threadIdx.x * per;
@@ -253,6 +280,18 @@ __global__ void __launch_bounds__(kPsBlock) k_psort_pass_b(const PsRec* __restri
   }
   if (bk == nbuckets - 1 && threadIdx.x == 0) start[ncell] = hi;
   __syncthreads();
+  if (one) {
+#pragma unroll
+    for (int u = 0; u < kPsOne; ++u) {
+      if (lo + u * kPsBlock + (int)threadIdx.x >= hi) continue;
+      const int at = cur[r1[u].i.x - base] + rk[u];
+      src_y[at] = make_float2(r1[u].f.x, r1[u].f.y);
+      src_v[at] = make_float2(r1[u].f.z, r1[u].f.w);
+      src_t[at] = __int_as_float(r1[u].i.z);
+      src_id[at] = r1[u].i.y;
+    }
+    return;
+  }
   for (int k0 = lo; k0 < hi; k0 += kPsItems * kPsBlock) {
     PsRec r[kPsItems];
     int at[kPsItems];
@@ -613,6 +652,20 @@ __global__ void __launch_bounds__(kBlock) k_anchor_count(PairRef a, int64_t M, c
   if (key >= 0) atomicAdd(cnt + key, 1);
 }
 
+__device__ __forceinline__ AnchorRec anchor_rec(const PairRef& a, int64_t i, int64_t key, float gi) {
+  const float2 xi = a.AX[i];
+  AnchorRec rec;
+  rec.x = xi.x;
+  rec.y = xi.y;
+  rec.t = a.AT[i];
+  rec.g = gi;
+  rec.id = (int)a.AID[i];
+  rec.col = (int)a.AC[3 * i + 1];
+  rec.row = (int)(key / a.GW);
+  rec.idx = (int)i;
+  return rec;
+}
+
 // Writes each anchor's record into its cell's run, filled from the run's end (the counts run down to zero).
 __global__ void __launch_bounds__(kBlock) k_anchor_place(PairRef a, int64_t M, const float* __restrict__ gS,
                                                          const int64_t* __restrict__ astart, int* __restrict__ cnt,
@@ -624,17 +677,113 @@ __global__ void __launch_bounds__(kBlock) k_anchor_place(PairRef a, int64_t M, c
   const int64_t key = anchor_key(i, a);
   if (key < 0) return;
   const int slot = atomicSub(cnt + key, 1) - 1;
-  const float2 xi = a.AX[i];
-  AnchorRec rec;
-  rec.x = xi.x;
-  rec.y = xi.y;
-  rec.t = a.AT[i];
-  rec.g = gi;
-  rec.id = (int)a.AID[i];
-  rec.col = (int)a.AC[3 * i + 1];
-  rec.row = (int)(key / a.GW);
-  rec.idx = (int)i;
-  arec[astart[key] + slot] = rec;
+  arec[astart[key] + slot] = anchor_rec(a, i, key, gi);
+}
+
+// The same binning by a two-level counting sort (the plan's scheme: buckets of 2^shift consecutive cells): pass
+// A counts the anchors of every block of kAbPer * kAbBlock per bucket in LDS (one block-major row of counts,
+// added into the bucket totals), one workgroup scans the totals, and pass A again reserves the block's run of
+// each bucket with one atomic add on the bucket's position and writes the anchors' records there; pass B ranks
+// each bucket's records by cell in LDS, writes the cells' CSR starts and the records at their final places.
+// Within a cell the records follow their arrival in the bucket.  No global atomic per anchor.
+constexpr int kAbBlock = 512;
+constexpr int kAbPer = 8;                          // anchors per thread of pass A, records per thread of pass B
+
+template <bool SCATTER>
+__global__ void __launch_bounds__(kAbBlock) k_abin_a(PairRef a, int64_t M, const float* __restrict__ gS, int shift,
+                                                     int nbuckets, int* __restrict__ cnt,
+                                                     int* __restrict__ tot_or_pos, AnchorRec* __restrict__ tmp) {
+  extern __shared__ int hist[];
+  int* mycnt = cnt + (int64_t)blockIdx.x * nbuckets;
+  for (int i = threadIdx.x; i < nbuckets; i += kAbBlock) {
+    int h = 0;
+    if (SCATTER) {
+      const int c = mycnt[i];
+      if (c > 0) h = atomicAdd(tot_or_pos + i, c);  // this block's run of bucket i
+    }
+    hist[i] = h;
+  }
+  __syncthreads();
+  const int64_t i0 = (int64_t)blockIdx.x * (kAbPer * kAbBlock) + threadIdx.x;
+  int key[kAbPer];
+  float gi[kAbPer];
+#pragma unroll
+  for (int u = 0; u < kAbPer; ++u) {
+    const int64_t i = i0 + (int64_t)u * kAbBlock;
+    key[u] = -1;
+    gi[u] = 0.f;
+    if (i < M) {
+      gi[u] = gS ? gS[i] : 0.f;
+      if (!(gS && gi[u] == 0.f)) key[u] = (int)anchor_key(i, a);   // -1 outside the grid
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kAbPer; ++u) {
+    if (key[u] < 0) continue;
+    const int slot = atomicAdd(hist + (key[u] >> shift), 1);
+    if (SCATTER) tmp[slot] = anchor_rec(a, i0 + (int64_t)u * kAbBlock, key[u], gi[u]);
+  }
+  if (!SCATTER) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < nbuckets; i += kAbBlock) {
+      const int c = hist[i];
+      mycnt[i] = c;
+      if (c > 0) atomicAdd(tot_or_pos + i, c);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kAbBlock) k_abin_b(const AnchorRec* __restrict__ tmp, const int* __restrict__ bend,
+                                                     const int* __restrict__ tot, int shift, int64_t ncell,
+                                                     int nbuckets, int GW, int64_t* __restrict__ start,
+                                                     AnchorRec* __restrict__ arec) {
+  __shared__ int cur[1 << kPsMaxShift];
+  __shared__ int wsum[kAbBlock / kWave + 1];
+  const int bk = blockIdx.x;
+  const int nk = 1 << shift;
+  const int hi = bend[bk], lo = hi - tot[bk];
+  const int base = bk << shift;
+  for (int i = threadIdx.x; i < nk; i += kAbBlock) cur[i] = 0;
+  __syncthreads();
+  const bool one = hi - lo <= kAbPer * kAbBlock;  // the bucket's records stay in registers with their ranks
+  AnchorRec r1[kAbPer];
+  int rk[kAbPer];
+  if (one && hi > lo) {
+#pragma unroll
+    for (int u = 0; u < kAbPer; ++u) r1[u] = tmp[min(lo + u * kAbBlock + (int)threadIdx.x, hi - 1)];
+#pragma unroll
+    for (int u = 0; u < kAbPer; ++u)
+      rk[u] = lo + u * kAbBlock + (int)threadIdx.x < hi ? atomicAdd(cur + (r1[u].row * GW + r1[u].col - base), 1) : 0;
+  } else if (!one) {
+    for (int k = lo + (int)threadIdx.x; k < hi; k += kAbBlock) atomicAdd(cur + (tmp[k].row * GW + tmp[k].col - base), 1);
+  }
+  __syncthreads();
+  const int per = nk > kAbBlock ? nk / kAbBlock : 1;   // cells per thread in the scan
+  const int c0 = threadIdx.x * per;
+  int sum = 0;
+  for (int q = 0; q < per; ++q) sum += c0 + q < nk ? cur[c0 + q] : 0;
+  int total;
+  int run = block_exclusive_scan<kAbBlock>(sum, wsum, total);
+  for (int q = 0; q < per; ++q) {
+    const int c = c0 + q;
+    if (c >= nk) break;
+    const int n = cur[c];
+    cur[c] = lo + run;                             // the cell's next slot
+    if ((int64_t)base + c < ncell) start[(int64_t)base + c] = lo + run;
+    run += n;
+  }
+  if (bk == nbuckets - 1 && threadIdx.x == 0) start[ncell] = hi;
+  __syncthreads();
+  if (one) {
+#pragma unroll
+    for (int u = 0; u < kAbPer; ++u)
+      if (lo + u * kAbBlock + (int)threadIdx.x < hi) arec[cur[r1[u].row * GW + r1[u].col - base] + rk[u]] = r1[u];
+    return;
+  }
+  for (int k = lo + (int)threadIdx.x; k < hi; k += kAbBlock) {
+    const AnchorRec r = tmp[k];
+    arec[atomicAdd(cur + (r.row * GW + r.col - base), 1)] = r;
+  }
 }
 
 // The backward over a forward's binning: every binned record takes its anchor's gS (the forward binned every
@@ -1299,6 +1448,11 @@ struct PairWs {
   int64_t* fstart;             // the forward's items per cell: CSR starts (ncell + 1), scan totals, the items
   int64_t* fwork;
   int2* fitems;
+  int* abcnt;                  // the anchors' counting sort: block-major bucket counts, bucket totals and
+  int* abtot;                  // positions, the records in bucket order (ab_shift < 0: grids of more buckets
+  int* abpos;                  // than one workgroup scans take the atomic binning)
+  AnchorRec* abtmp;
+  int ab_shift, ab_nbuckets, ab_nblk;
   int64_t units, nseg, max_items, max_fitems, bytes;
 };
 
@@ -1326,6 +1480,23 @@ PairWs pair_ws_layout(void* base, int64_t E, int64_t ncell, int64_t M, int64_t G
   w.fstart = (int64_t*)take(8 * (ncell + 1));
   w.fwork = (int64_t*)take(8 * atl_scan_work_size(ncell));
   w.fitems = (int2*)take(8 * w.max_fitems);
+  // buckets of about kAbPer * kAbBlock / 2 anchors on average (pass B's workgroups hold up to twice that in
+  // registers), at least kPsMinShift and at most kPsMaxShift cells, and few enough for one scan workgroup
+  w.ab_shift = -1;
+  for (int s = kPsMinShift; s <= kPsMaxShift; ++s)
+    if (((ncell + ((int64_t)1 << s) - 1) >> s) <= kPsMaxBuckets &&
+        (s == kPsMaxShift || (M << s) >= ncell * (int64_t)(kAbPer * kAbBlock / 2))) {
+      w.ab_shift = s;
+      break;
+    }
+  w.ab_nbuckets = w.ab_shift < 0 ? 0 : (int)((ncell + ((int64_t)1 << w.ab_shift) - 1) >> w.ab_shift);
+  w.ab_nblk = (int)((M + kAbPer * kAbBlock - 1) / (kAbPer * kAbBlock));
+  if (w.ab_shift >= 0) {
+    w.abcnt = (int*)take(4 * (int64_t)w.ab_nblk * w.ab_nbuckets);
+    w.abtot = (int*)take(4 * (int64_t)w.ab_nbuckets);
+    w.abpos = (int*)take(4 * (int64_t)w.ab_nbuckets);
+    w.abtmp = (AnchorRec*)take((int64_t)sizeof(AnchorRec) * M);
+  }
   w.bytes = off;
   return w;
 }
@@ -1341,6 +1512,21 @@ bool pair_ws_ok(const PairWs& w, void* ws, int64_t ws_bytes, const char* what) {
 
 // Bins the anchors (all inside the grid, or those with gS != 0) into w.arec by cell.
 int bin_anchors(const PairRef& a, int64_t M, int64_t ncell, const float* gS, const PairWs& w, hipStream_t stream) {
+  if (w.ab_shift >= 0 && M > 0) {
+    const size_t lds = (size_t)w.ab_nbuckets * sizeof(int);
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(w.ab_nbuckets)), dim3(kBlock), 0, stream, w.abtot,
+                       (int64_t)w.ab_nbuckets, 0);
+    hipLaunchKernelGGL(k_abin_a<false>, dim3(w.ab_nblk), dim3(kAbBlock), lds, stream, a, M, gS, w.ab_shift,
+                       w.ab_nbuckets, w.abcnt, w.abtot, (AnchorRec*)nullptr);
+    hipLaunchKernelGGL(k_psort_scan, dim3(1), dim3(kPsScanBlock), 0, stream, (const int*)w.abtot, w.ab_nbuckets,
+                       w.abpos);
+    hipLaunchKernelGGL(k_abin_a<true>, dim3(w.ab_nblk), dim3(kAbBlock), lds, stream, a, M, gS, w.ab_shift,
+                       w.ab_nbuckets, w.abcnt, w.abpos, w.abtmp);
+    hipLaunchKernelGGL(k_abin_b, dim3(w.ab_nbuckets), dim3(kAbBlock), 0, stream, (const AnchorRec*)w.abtmp,
+                       (const int*)w.abpos, (const int*)w.abtot, w.ab_shift, ncell, w.ab_nbuckets, (int)a.GW,
+                       w.start, w.arec);
+    return 0;
+  }
   hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(ncell)), dim3(kBlock), 0, stream, w.cnt, ncell, 0);
   hipLaunchKernelGGL(k_anchor_count, dim3(grid_for(M)), dim3(kBlock), 0, stream, a, M, gS, w.cnt);
   if (atl_scan_counts(w.cnt, ncell, w.start, w.work, stream)) return 1;
