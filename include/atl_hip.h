@@ -319,8 +319,12 @@ int atl_ats_pair_bwd(const float* gS, const float* src_y, const float* src_v, co
  * one cell, which walks the cell's 3 x 3 neighbourhood once for all of them.  atl_ats_pair_bwd_ws, source-centric: each chunk of 64 plan entries
  * of a run of four cells of a row gathers over the binned anchors (gS != 0) around it and adds every entry's
  * sum to gv once (two atomics per entry instead of two per pair); the same visited pairs and terms as
- * atl_ats_pair_bwd, gv (N,2) accumulated. */
+ * atl_ats_pair_bwd, gv (N,2) accumulated.  A workspace of atl_ats_pair_bwd_ws_bytes(E, ncell, M, GW, N, S)
+ * bytes (the same regions, then N * S float2) lets the backward write each entry's sum to its own
+ * (source, slice) slot instead, a plan holding one entry per source and slice, and add every source's slots in
+ * slice order: no atomics.  Either size serves either call; -1 for unsupported sizes (S > 4096). */
 int64_t atl_ats_pair_ws_bytes(int64_t E, int64_t ncell, int64_t M, int64_t GW);
+int64_t atl_ats_pair_bwd_ws_bytes(int64_t E, int64_t ncell, int64_t M, int64_t GW, int64_t N, int64_t S);
 int atl_ats_pair_fwd_ws(const float* src_y, const float* src_v, const float* src_t, const int64_t* src_id,
                         const int64_t* cell_start, int64_t E, int64_t ncell, const float* anc_x, const float* anc_t,
                         const int64_t* anc_cell, const int64_t* anc_id, int64_t M, const float* slice_c, int64_t S,

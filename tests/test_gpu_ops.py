@@ -473,7 +473,8 @@ def test_pair_sums_match_oracle(tau, S, h):
                                                        ("blobs", 40000, 0.2, 16, 1.0, 0.5)])
 def test_pair_entries_match_oracle(scene, n, tau, S, h, zero_frac):
     """Both forward entry points over the reference-layout plan (binned anchors over a workspace; the plan's
-    anchor order) and both backward ones (source-centric over a workspace; per-pair atomics) against the oracle:
+    anchor order) and the backward ones (source-centric over a workspace, with per-entry atomics or
+    per-(source, slice) slots; per-pair atomics) against the oracle:
     counts bit-exact, S within 1e-5, gv within 1e-4, with a share of the anchors' gS exactly zero (skipped by
     both backwards, or kept with their zero terms by the backward over the forward's binning).
     The anchors sit h * N(0, 1) off the events, so records two cells from an anchor pass the distance test and
@@ -503,9 +504,11 @@ def test_pair_entries_match_oracle(scene, n, tau, S, h, zero_frac):
         assert_sums_close(got, want_s)
     for atomics in (False, True):
         close_rel(N(e.ats_pair_bwd(T(gS), *args, per_pair_atomics=atomics)), want, 1e-4)
-    # the backward over the forward's anchor binning (the workspace kept from the forward)
-    _, ws = e.ats_pair_fwd(*args[:-1], keep_ws=True)
-    close_rel(N(e.ats_pair_bwd(T(gS), *args, ws=ws)), want, 1e-4)
+    # the backward over the forward's anchor binning (the workspace kept from the forward): two atomics per
+    # entry, or (the workspace sized with the source count) one slot per source and slice, added per source
+    for n_src in (None, win.n):
+        _, ws = e.ats_pair_fwd(*args[:-1], keep_ws=True, n_src=n_src)
+        close_rel(N(e.ats_pair_bwd(T(gS), *args, ws=ws)), want, 1e-4)
 
 
 def test_ats_pair_sums_api_matches_bruteforce():

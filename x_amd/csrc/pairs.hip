@@ -32,16 +32,26 @@ __global__ void __launch_bounds__(kBlock) k_stats(const float2* __restrict__ v, 
   int vm = float_to_ordered(0.f);
   int mnx = float_to_ordered(INFINITY), mny = mnx, nmx = mnx, nmy = mnx;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < N; j += stride) {
-    const float2 q = v[j];
-    vm = max(vm, float_to_ordered(sqrtf(fmaf(q.y, q.y, q.x * q.x))));
+  const int64_t j0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  constexpr int U = 4;                             // loads in flight per thread
+  for (int64_t j = j0; j < N; j += U * stride) {
+    float2 q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) q[u] = v[min(j + u * stride, N - 1)];   // repeats of v[N - 1] change no max
+#pragma unroll
+    for (int u = 0; u < U; ++u) vm = max(vm, float_to_ordered(sqrtf(fmaf(q[u].y, q[u].y, q[u].x * q[u].x))));
   }
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < M; i += stride) {
-    const float2 p = xa[i];
-    mnx = min(mnx, float_to_ordered(p.x));
-    mny = min(mny, float_to_ordered(p.y));
-    nmx = min(nmx, float_to_ordered(-p.x));
-    nmy = min(nmy, float_to_ordered(-p.y));
+  for (int64_t i = j0; i < M; i += U * stride) {
+    float2 p[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) p[u] = xa[min(i + u * stride, M - 1)];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      mnx = min(mnx, float_to_ordered(p[u].x));
+      mny = min(mny, float_to_ordered(p[u].y));
+      nmx = min(nmx, float_to_ordered(-p[u].x));
+      nmy = min(nmy, float_to_ordered(-p[u].y));
+    }
   }
   vm = wave_max_i(vm);
   mnx = wave_min_i(mnx);
@@ -424,10 +434,28 @@ __global__ void __launch_bounds__(kBlock) k_scan_parts(int64_t* __restrict__ par
   }
 }
 
-template <typename T>
+// PRE: part holds the tile totals themselves, and each block adds up those of the tiles before its own (up to
+// kScanPreTiles tiles: cheaper than the launch of k_scan_parts); otherwise part holds their exclusive scan.
+constexpr int64_t kScanPreTiles = 2048;
+
+template <typename T, bool PRE>
 __global__ void __launch_bounds__(kBlock) k_scan_write(const int* __restrict__ in, int64_t n,
                                                        const int64_t* __restrict__ part, T* __restrict__ out) {
   __shared__ int lds[kBlock / kWave + 1];
+  __shared__ int64_t pre_lds[kBlock / kWave];
+  int64_t offset = 0;
+  if (PRE) {
+    int64_t s = 0;
+    for (int64_t i = threadIdx.x; i < (int64_t)blockIdx.x; i += kBlock) s += part[i];
+#pragma unroll
+    for (int d = kWave / 2; d >= 1; d >>= 1) s += __shfl_xor(s, d);
+    if ((threadIdx.x & (kWave - 1)) == 0) pre_lds[threadIdx.x / kWave] = s;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kBlock / kWave; ++k) offset += pre_lds[k];
+  } else {
+    offset = part[blockIdx.x];
+  }
   const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
   int vals[kScanItems];
   int s = 0;
@@ -438,7 +466,7 @@ __global__ void __launch_bounds__(kBlock) k_scan_write(const int* __restrict__ i
   }
   int total;
   const int excl = block_exclusive_scan<kBlock>(s, lds, total);
-  int64_t run = part[blockIdx.x] + excl;
+  int64_t run = offset + excl;
 #pragma unroll
   for (int k = 0; k < kScanItems; ++k) {
     run += vals[k];
@@ -969,11 +997,17 @@ __device__ __forceinline__ int64_t xcd_unit(int64_t nblocks) {
 // the compiler barrier plus the wait for the writes).
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// max_items bounds the item count (the grid); the count itself is read on the device (nitems_ptr).
+// max_items bounds the item count (the grid); the count itself is read on the device (nitems_ptr).  SLOTS: each
+// record's sum goes to its own slot, slots[k * N + source] with k = slice - the first slice of the source's
+// range (a plan holds one record per source and slice of its range, so k < ms; k-major, so that the records of
+// one plane write into few N-slot rows; a record outside that range adds its sum with atomics),
+// and k_slots_reduce adds every source's slots into gv afterwards; otherwise two atomics per record add it to gv.
+template <bool SLOTS>
 __global__ void __launch_bounds__(kGatherWaves * kWave)
 k_pair_bwd_gather(PairRef a, const int64_t* __restrict__ astart, const AnchorRec* __restrict__ arec, int64_t Mlist,
                   const int2* __restrict__ items, const int64_t* __restrict__ nitems_ptr, int64_t max_items,
-                  float invh2, int64_t nseg, float* __restrict__ gv) {
+                  float invh2, int64_t nseg, float* __restrict__ gv, float2* __restrict__ slots, PlanGeo sg,
+                  int ms) {
   __shared__ float4 sa[kGatherWaves][kWave];   // anchor x, y, t, gS
   __shared__ int4 sb[kGatherWaves][kWave];     // at = t - slice centre (bits), anchor id, anchor cell column
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
@@ -1037,9 +1071,35 @@ k_pair_bwd_gather(PairRef a, const int64_t* __restrict__ astart, const AnchorRec
     wave_lds_sync();
   }
   if (live && any && sid >= 0 && sid < a.N) {
-    atomicAdd(gv + 2 * (int64_t)sid, gx);
-    atomicAdd(gv + 2 * (int64_t)sid + 1, gy);
+    int kk = -1;
+    if (SLOTS) {
+      int lo, hi;
+      slice_range(st, sg, lo, hi);
+      kk = (int)(q.g % a.S) - lo;
+    }
+    if (SLOTS && kk >= 0 && kk < ms) {
+      slots[(int64_t)kk * a.N + sid] = make_float2(gx, gy);
+    } else {
+      atomicAdd(gv + 2 * (int64_t)sid, gx);
+      atomicAdd(gv + 2 * (int64_t)sid + 1, gy);
+    }
   }
+}
+
+// gv[j] += the sum of source j's ms slots, in slice order (cleared slots of slices without a record add zero).
+__global__ void __launch_bounds__(kBlock) k_slots_reduce(const float2* __restrict__ slots, int64_t N, int S,
+                                                         float* __restrict__ gv) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= N) return;
+  float sx = 0.f, sy = 0.f;
+  for (int s = 0; s < S; ++s) {
+    const float2 v = slots[s * N + j];
+    sx += v.x;
+    sy += v.y;
+  }
+  float2* g = (float2*)gv + j;
+  const float2 old = *g;
+  *g = make_float2(old.x + sx, old.y + sy);
 }
 
 // ------------------------------------------------------------------------------------------ window counts
@@ -1452,11 +1512,12 @@ struct PairWs {
   int* abtot;                  // positions, the records in bucket order (ab_shift < 0: grids of more buckets
   int* abpos;                  // than one workgroup scans take the atomic binning)
   AnchorRec* abtmp;
+  float2* slots;               // the backward's per-(source, slice) sums (N * S), when the workspace holds them
   int ab_shift, ab_nbuckets, ab_nblk;
   int64_t units, nseg, max_items, max_fitems, bytes;
 };
 
-PairWs pair_ws_layout(void* base, int64_t E, int64_t ncell, int64_t M, int64_t GW) {
+PairWs pair_ws_layout(void* base, int64_t E, int64_t ncell, int64_t M, int64_t GW, int64_t N = 0, int64_t S = 0) {
   PairWs w;
   w.nseg = (GW + kSegCells - 1) / kSegCells;
   w.units = ncell / GW * w.nseg;
@@ -1497,6 +1558,7 @@ PairWs pair_ws_layout(void* base, int64_t E, int64_t ncell, int64_t M, int64_t G
     w.abpos = (int*)take(4 * (int64_t)w.ab_nbuckets);
     w.abtmp = (AnchorRec*)take((int64_t)sizeof(AnchorRec) * M);
   }
+  w.slots = N > 0 && S > 0 ? (float2*)take(8 * N * S) : nullptr;   // last: the regions above keep their offsets
   w.bytes = off;
   return w;
 }
@@ -1545,7 +1607,7 @@ int atl_plan_stats(const float* v, int64_t N, const float* xa, int64_t M, int* s
   hipLaunchKernelGGL(k_stats_init, dim3(1), dim3(64), 0, stream, stats);
   const int64_t n = N > M ? N : M;
   if (n > 0) {
-    unsigned grid = grid_for(n);
+    unsigned grid = grid_for(n, 4 * kBlock);
     if (grid > 256) grid = 256;                   // few blocks: their same-address atomics serialise
     hipLaunchKernelGGL(k_stats, dim3(grid), dim3(kBlock), 0, stream, (const float2*)v, N, (const float2*)xa, M,
                        stats);
@@ -1572,8 +1634,13 @@ int atl_scan_counts(const int* counts, int64_t n, int64_t* start, int64_t* work,
     return check_launch("scan_counts");
   }
   hipLaunchKernelGGL(k_scan_reduce, dim3((unsigned)tiles), dim3(kBlock), 0, stream, counts, n, work);
+  if (tiles <= kScanPreTiles) {
+    hipLaunchKernelGGL((k_scan_write<int64_t, true>), dim3((unsigned)tiles), dim3(kBlock), 0, stream, counts, n,
+                       (const int64_t*)work, start);
+    return check_launch("scan_counts");
+  }
   hipLaunchKernelGGL(k_scan_parts, dim3(1), dim3(kBlock), 0, stream, work, tiles);
-  hipLaunchKernelGGL(k_scan_write<int64_t>, dim3((unsigned)tiles), dim3(kBlock), 0, stream, counts, n,
+  hipLaunchKernelGGL((k_scan_write<int64_t, false>), dim3((unsigned)tiles), dim3(kBlock), 0, stream, counts, n,
                      (const int64_t*)work, start);
   return check_launch("scan_counts");
 }
@@ -1678,6 +1745,11 @@ int64_t atl_ats_pair_ws_bytes(int64_t E, int64_t ncell, int64_t M, int64_t GW) {
   return pair_ws_layout(nullptr, E, ncell, M, GW).bytes;
 }
 
+int64_t atl_ats_pair_bwd_ws_bytes(int64_t E, int64_t ncell, int64_t M, int64_t GW, int64_t N, int64_t S) {
+  if (E < 0 || ncell < 0 || M < 0 || GW < 1 || N < 0 || S < 1 || N >= kMaxRecords || S > 4096) return -1;
+  return pair_ws_layout(nullptr, E, ncell, M, GW, N, S).bytes;
+}
+
 int atl_ats_pair_fwd_ws(const float* src_y, const float* src_v, const float* src_t, const int64_t* src_id,
                         const int64_t* cell_start, int64_t E, int64_t ncell, const float* anc_x, const float* anc_t,
                         const int64_t* anc_cell, const int64_t* anc_id, int64_t M, const float* slice_c, int64_t S,
@@ -1744,7 +1816,13 @@ int pair_bwd_ws(const float* gS, const float* src_y, const float* src_v, const f
     set_error("ats_pair_bwd_ws: bad arguments");
     return 1;
   }
-  const PairWs w = pair_ws_layout(ws, E, ncell, M, GW);
+  // a workspace of atl_ats_pair_bwd_ws_bytes holds the per-(source, slice) sums: no atomics
+  const PairWs ws_slots = pair_ws_layout(ws, E, ncell, M, GW, N, S);
+  const bool slots = N > 0 && S <= 4096 && ws_bytes >= ws_slots.bytes;
+  // slices per source (the plan's bound): the slots of the first ms rows are used
+  const int ms = (int)std::min<int64_t>((int64_t)std::floor((2.0 * tau + 1.0 / (double)S) * (double)S) + 2, S);
+  const PlanGeo sg = make_geo(0.0, 0.0, 1.0, tau, S, 1, 1, 1);
+  const PairWs w = slots ? ws_slots : pair_ws_layout(ws, E, ncell, M, GW);
   if (!pair_ws_ok(w, ws, ws_bytes, "ats_pair_bwd_ws")) return 1;
   if (M == 0 || N == 0 || E == 0 || ncell == 0) return 0;
   const int64_t grp = kXcds * kXcdRun;
@@ -1756,6 +1834,9 @@ int pair_bwd_ws(const float* gS, const float* src_y, const float* src_v, const f
   const PairRef a = make_ref(src_y, src_v, src_t, src_id, cell_start, E, ncell, anc_x, anc_t, anc_cell, anc_id,
                              slice_c, S, GH, GW, h, tau, cut, N);
   const float invh2 = 1.f / (float)(h * h);
+  if (slots)
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(2 * N * ms)), dim3(kBlock), 0, stream, (int*)w.slots, 2 * N * ms,
+                       0);
   if (binned)
     hipLaunchKernelGGL(k_anchor_set_g, dim3(grid_for(M)), dim3(kBlock), 0, stream, (const int64_t*)w.start, ncell, M,
                        gS, w.arec);
@@ -1766,9 +1847,13 @@ int pair_bwd_ws(const float* gS, const float* src_y, const float* src_v, const f
   if (atl_scan_counts(w.ucnt, w.units, w.ustart, w.uwork, stream)) return 1;
   hipLaunchKernelGGL(k_unit_items, dim3(grid_for(w.units)), dim3(kBlock), 0, stream, (const int*)w.ucnt,
                      (const int64_t*)w.ustart, w.units, w.items);
-  hipLaunchKernelGGL(k_pair_bwd_gather, dim3((unsigned)blocks), dim3(kGatherWaves * kWave), 0, stream, a,
-                     (const int64_t*)w.start, (const AnchorRec*)w.arec, M, (const int2*)w.items,
-                     (const int64_t*)(w.ustart + w.units), w.max_items, invh2, w.nseg, gv);
+  hipLaunchKernelGGL(slots ? k_pair_bwd_gather<true> : k_pair_bwd_gather<false>, dim3((unsigned)blocks),
+                     dim3(kGatherWaves * kWave), 0, stream, a, (const int64_t*)w.start, (const AnchorRec*)w.arec, M,
+                     (const int2*)w.items, (const int64_t*)(w.ustart + w.units), w.max_items, invh2, w.nseg, gv,
+                     w.slots, sg, ms);
+  if (slots)
+    hipLaunchKernelGGL(k_slots_reduce, dim3(grid_for(N)), dim3(kBlock), 0, stream, (const float2*)w.slots, N, ms,
+                       gv);
   return check_launch(binned ? "ats_pair_bwd_ws_binned" : "ats_pair_bwd_ws");
 }
 }  // namespace

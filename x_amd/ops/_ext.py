@@ -70,6 +70,7 @@ _SIGS = {
     "atl_ats_pair_bwd": [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _D, _D, _D, _I, _P,
                          _P],
     "atl_ats_pair_ws_bytes": [_I, _I, _I, _I],
+    "atl_ats_pair_bwd_ws_bytes": [_I, _I, _I, _I, _I, _I],
     "atl_ats_pair_fwd_ws": [_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _D, _D, _D, _P, _P, _P,
                             _I, _P],
     "atl_ats_pair_bwd_ws": [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _D, _D, _D, _I,
@@ -120,7 +121,7 @@ _RESTYPE = {"atl_scan_work_size": ctypes.c_int64, "atl_grid_plan_bytes": ctypes.
             "atl_tile_ws_bytes": ctypes.c_int64, "atl_splat_gauss_ws_bytes": ctypes.c_int64,
             "atl_anchored_score_mean_scratch_bytes": ctypes.c_int64, "atl_knn_ws_bytes": ctypes.c_int64,
             "atl_voxel_ws_bytes": ctypes.c_int64, "atl_warp_splat_gather_ws_bytes": ctypes.c_int64,
-            "atl_ats_pair_ws_bytes": ctypes.c_int64, "atl_traj_field_bwd_bytes": ctypes.c_int64,
+            "atl_ats_pair_ws_bytes": ctypes.c_int64, "atl_ats_pair_bwd_ws_bytes": ctypes.c_int64, "atl_traj_field_bwd_bytes": ctypes.c_int64,
             "atl_sample_grid_bwd_rows_bytes": ctypes.c_int64, "atl_plan_sort_bytes": ctypes.c_int64,
             "atl_image_variance_ws_bytes": ctypes.c_int64,
 "atl_last_error": ctypes.c_char_p, "atl_abi_version": ctypes.c_int}
@@ -372,17 +373,25 @@ class HipOps:
         _need(aid, "anc_id", I64, dev, (M,)); _need(sc, "slice_c", F32, dev)
         return E, M, cs.shape[0] - 1
 
-    def _pair_ws(self, E, ncell, M, GW, dev):
-        nbytes = load_library().atl_ats_pair_ws_bytes(E, ncell, M, int(GW))
+    def _pair_ws(self, E, ncell, M, GW, dev, N=None, S=None):
+        """Workspace of the pair entries; with the source count N and the slices S it also holds the backward's
+        per-(source, slice) sums (the backward then adds no atomics)."""
+        lib = load_library()
+        nbytes = -1
+        if N is not None and S is not None:
+            nbytes = lib.atl_ats_pair_bwd_ws_bytes(E, ncell, M, int(GW), int(N), int(S))
+        if nbytes < 0:
+            nbytes = lib.atl_ats_pair_ws_bytes(E, ncell, M, int(GW))
         if nbytes < 0:
             raise HipLibraryError(f"ats_pair: no workspace size for E={E} ncell={ncell} M={M} GW={GW}")
         return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev), nbytes
 
     def ats_pair_fwd(self, sy, sv, st, sid, cs, ax, at, ac, aid, sc, S, GH, GW, h, tau, cut, count=None,
-                     plan_order=False, keep_ws=False):
+                     plan_order=False, keep_ws=False, n_src=None):
         """S (M,).  By default over a workspace allocated here with the output (atl_ats_pair_fwd_ws, anchors
         walked in cell order); ``plan_order`` selects the workspace-free entry.  ``keep_ws`` returns (S, ws):
-        the workspace holds the binned anchors, which ats_pair_bwd(..., ws=ws) then reuses."""
+        the workspace holds the binned anchors, which ats_pair_bwd(..., ws=ws) then reuses; with ``n_src`` (the
+        backward's N) it is sized for the backward's per-(source, slice) sums too."""
         E, M, ncell = self._pair_args(sy, sv, st, sid, cs, ax, at, ac, aid, sc)
         out = torch.empty(M, device=ax.device, dtype=F32)
         args = (ptr(sy), ptr(sv), ptr(st), ptr(sid), ptr(cs), E, ncell, ptr(ax), ptr(at), ptr(ac), ptr(aid), M,
@@ -391,7 +400,7 @@ class HipOps:
             if plan_order:
                 call("atl_ats_pair_fwd", *args, stream_of(ax))
             else:
-                ws, nbytes = self._pair_ws(E, ncell, M, GW, ax.device)
+                ws, nbytes = self._pair_ws(E, ncell, M, GW, ax.device, n_src if keep_ws else None, S)
                 call("atl_ats_pair_fwd_ws", *args, ptr(ws), nbytes, stream_of(ax))
                 if keep_ws:
                     return out, ws
@@ -413,7 +422,7 @@ class HipOps:
             elif ws is not None:
                 call("atl_ats_pair_bwd_ws_binned", *args, ptr(ws), ws.numel(), stream_of(ax))
             else:
-                ws, nbytes = self._pair_ws(E, ncell, M, GW, ax.device)
+                ws, nbytes = self._pair_ws(E, ncell, M, GW, ax.device, N, S)
                 call("atl_ats_pair_bwd_ws", *args, ptr(ws), nbytes, stream_of(ax))
         return gv
 

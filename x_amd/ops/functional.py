@@ -804,7 +804,8 @@ class _ATSPair(torch.autograd.Function):
         p = plan
         # the workspace keeps the anchors binned by the forward for the backward (one binning per step)
         out, ctx.ws = e.ats_pair_fwd(p.src_y, p.src_v, p.src_t, p.src_id, p.cell_start, p.anc_x, p.anc_t,
-                                     p.anc_cell, p.anc_id, p.slice_c, p.S, p.GH, p.GW, *ctx.args, keep_ws=True)
+                                     p.anc_cell, p.anc_id, p.slice_c, p.S, p.GH, p.GW, *ctx.args, keep_ws=True,
+                                     n_src=ctx.n)
         return out
 
     @staticmethod
