@@ -662,7 +662,7 @@ __global__ void __launch_bounds__(kWalkBlock) k_pair_bwd_group(PairRef a, int64_
 // with gS != 0, as the reference's backward skips the others) gets a record in its cell's run of the list.
 // Within a cell the order follows the atomics; the forward's sums do not depend on it.
 struct __align__(16) AnchorRec {
-  float x, y, t, g;     // position, time, gS (0 in the forward)
+  float x, y, t, g;     // position, time, gS (0 in the forward; the backward reads gS by idx)
   int id, col, row, idx;  // event id (low word), cell column, plane row g * GH + cy, anchor index
 };
 
@@ -812,15 +812,6 @@ __global__ void __launch_bounds__(kAbBlock) k_abin_b(const AnchorRec* __restrict
     const AnchorRec r = tmp[k];
     arec[atomicAdd(cur + (r.row * GW + r.col - base), 1)] = r;
   }
-}
-
-// The backward over a forward's binning: every binned record takes its anchor's gS (the forward binned every
-// anchor with g = 0; an anchor of gS = 0 then adds exact zeros for finite terms, as in the reference's loop).
-__global__ void __launch_bounds__(kBlock) k_anchor_set_g(const int64_t* __restrict__ astart, int64_t ncell, int64_t M,
-                                                         const float* __restrict__ gS, AnchorRec* __restrict__ arec) {
-  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (p >= M || p >= astart[ncell]) return;
-  arec[p].g = gS[arec[p].idx];
 }
 
 // Forward over the binned anchors, one wave per item of up to kCellAnchors anchors of one cell: the anchors of a
@@ -1007,7 +998,7 @@ __global__ void __launch_bounds__(kGatherWaves * kWave)
 k_pair_bwd_gather(PairRef a, const int64_t* __restrict__ astart, const AnchorRec* __restrict__ arec, int64_t Mlist,
                   const int2* __restrict__ items, const int64_t* __restrict__ nitems_ptr, int64_t max_items,
                   float invh2, int64_t nseg, float* __restrict__ gv, float2* __restrict__ slots, PlanGeo sg,
-                  int ms) {
+                  int ms, const float* __restrict__ gS) {
   __shared__ float4 sa[kGatherWaves][kWave];   // anchor x, y, t, gS
   __shared__ int4 sb[kGatherWaves][kWave];     // at = t - slice centre (bits), anchor id, anchor cell column
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
@@ -1043,7 +1034,7 @@ k_pair_bwd_gather(PairRef a, const int64_t* __restrict__ astart, const AnchorRec
     const int p = pb + lane;
     if (p < r.c3) {
       const AnchorRec an = arec[list_pos(p, r)];
-      sa[w][lane] = make_float4(an.x, an.y, an.t, an.g);
+      sa[w][lane] = make_float4(an.x, an.y, an.t, gS[an.idx]);
       sb[w][lane] = make_int4(__float_as_int(an.t - cs), an.id, an.col, 0);
     } else {
       sa[w][lane] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1837,11 +1828,8 @@ int pair_bwd_ws(const float* gS, const float* src_y, const float* src_v, const f
   if (slots)
     hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(2 * N * ms)), dim3(kBlock), 0, stream, (int*)w.slots, 2 * N * ms,
                        0);
-  if (binned)
-    hipLaunchKernelGGL(k_anchor_set_g, dim3(grid_for(M)), dim3(kBlock), 0, stream, (const int64_t*)w.start, ncell, M,
-                       gS, w.arec);
-  else if (bin_anchors(a, M, ncell, gS, w, stream))
-    return 1;
+  // the gather reads each staged anchor's gS by its index: the forward's binning serves as it is
+  if (!binned && bin_anchors(a, M, ncell, gS, w, stream)) return 1;
   hipLaunchKernelGGL(k_unit_chunks, dim3(grid_for(w.units)), dim3(kBlock), 0, stream, a, (const int64_t*)w.start, M,
                      w.nseg, w.units, w.ucnt);
   if (atl_scan_counts(w.ucnt, w.units, w.ustart, w.uwork, stream)) return 1;
@@ -1850,7 +1838,7 @@ int pair_bwd_ws(const float* gS, const float* src_y, const float* src_v, const f
   hipLaunchKernelGGL(slots ? k_pair_bwd_gather<true> : k_pair_bwd_gather<false>, dim3((unsigned)blocks),
                      dim3(kGatherWaves * kWave), 0, stream, a, (const int64_t*)w.start, (const AnchorRec*)w.arec, M,
                      (const int2*)w.items, (const int64_t*)(w.ustart + w.units), w.max_items, invh2, w.nseg, gv,
-                     w.slots, sg, ms);
+                     w.slots, sg, ms, gS);
   if (slots)
     hipLaunchKernelGGL(k_slots_reduce, dim3(grid_for(N)), dim3(kBlock), 0, stream, (const float2*)w.slots, N, ms,
                        gv);
