@@ -467,11 +467,12 @@ def test_pair_sums_match_oracle(tau, S, h):
     close_rel(N(tv.grad), O.ats_pair_bwd(gS, p, h, tau, 3.0, win.n), 1e-4)
 
 
-@pytest.mark.parametrize("scene,n,tau,S,h,zero_frac", [("segments", 6000, 0.2, 16, 1.0, 0.0),
-                                                       ("segments", 6000, 1.0, 8, 1.5, 0.7),
-                                                       ("segments", 6000, 0.05, 4, 0.5, 0.3),
-                                                       ("blobs", 40000, 0.2, 16, 1.0, 0.5)])
-def test_pair_entries_match_oracle(scene, n, tau, S, h, zero_frac):
+@pytest.mark.parametrize("scene,n,tau,S,h,zero_frac,B", [("segments", 6000, 0.2, 16, 1.0, 0.0, 1),
+                                                         ("segments", 6000, 1.0, 8, 1.5, 0.7, 1),
+                                                         ("segments", 6000, 0.05, 4, 0.5, 0.3, 1),
+                                                         ("segments", 3000, 0.2, 8, 1.0, 0.2, 3),
+                                                         ("blobs", 40000, 0.2, 16, 1.0, 0.5, 1)])
+def test_pair_entries_match_oracle(scene, n, tau, S, h, zero_frac, B):
     """Both forward entry points over the reference-layout plan (binned anchors over a workspace; the plan's
     anchor order) and the backward ones (source-centric over a workspace, with per-entry atomics or
     per-(source, slice) slots; per-pair atomics) against the oracle:
@@ -480,14 +481,14 @@ def test_pair_entries_match_oracle(scene, n, tau, S, h, zero_frac):
     The anchors sit h * N(0, 1) off the events, so records two cells from an anchor pass the distance test and
     only the neighbourhood test keeps them out; the blob case fills cells with hundreds of records and
     anchors (several 64-wide chunks on both sides)."""
-    win = synth.small_window(seed=4, n=n, H=40, W=48, B=1, scene=scene)
+    win = synth.small_window(seed=4, n=n, H=40, W=48, B=B, scene=scene)
     v, _, _ = O.dense_velocity(win.motion["grid"], win.xy, win.b, 40, 48)
     rng = np.random.default_rng(104)
     xs = (win.xy + rng.uniform(-0.5, 0.5, win.xy.shape)).astype(F32)
     anchors = np.arange(win.n)
     xa = (xs + h * rng.standard_normal(xs.shape)).astype(F32)
-    p = O.build_pair_plan(xs, win.t, v, win.b, 1, 40, 48, anchors, h, tau, 3.0, S, anchor_xy=xa)
-    q = F.build_pair_plan(T(xs), T(win.t), T(v), T(win.b), 1, 40, 48, T(anchors), h, tau, 3.0, S, anchor_xy=T(xa))
+    p = O.build_pair_plan(xs, win.t, v, win.b, B, 40, 48, anchors, h, tau, 3.0, S, anchor_xy=xa)
+    q = F.build_pair_plan(T(xs), T(win.t), T(v), T(win.b), B, 40, 48, T(anchors), h, tau, 3.0, S, anchor_xy=T(xa))
     gS = rng.standard_normal(len(anchors)).astype(F32)
     gS[rng.random(len(anchors)) < zero_frac] = 0
     want = O.ats_pair_bwd(gS, p, h, tau, 3.0, win.n)
