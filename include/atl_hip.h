@@ -315,7 +315,7 @@ int atl_ats_pair_bwd(const float* gS, const float* src_y, const float* src_v, co
 /* Workspace entries of the same two ops (csrc/atl_ops.h:31-47), for a binding that allocates a workspace
  * with its outputs: ws is atl_ats_pair_ws_bytes(E, ncell, M, GW) bytes of device memory, 256-byte aligned,
  * contents on entry ignored, and serves either call.  Both bin the anchors by cell first.
- * atl_ats_pair_fwd_ws: the same out and count as atl_ats_pair_fwd, one wave per item of up to four anchors of
+ * atl_ats_pair_fwd_ws: the same out and count as atl_ats_pair_fwd, one wave per item of up to five anchors of
  * one cell, which walks the cell's 3 x 3 neighbourhood once for all of them.  atl_ats_pair_bwd_ws, source-centric: each chunk of 64 plan entries
  * of a run of four cells of a row gathers over the binned anchors (gS != 0) around it and adds every entry's
  * sum to gv once (two atomics per entry instead of two per pair); the same visited pairs and terms as

@@ -818,7 +818,7 @@ __global__ void __launch_bounds__(kAbBlock) k_abin_b(const AnchorRec* __restrict
 // cell share their 3 x 3 neighbourhood, so the wave walks it once, lanes over 64 consecutive records per chunk,
 // and every lane evaluates each anchor of the item on its record (the record loads and list arithmetic once per
 // NA anchors).  Items per cell ceil(anchors / kCellAnchors), listed by k_cell_items / k_cell_expand.
-constexpr int kCellAnchors = 4;
+constexpr int kCellAnchors = 5;
 
 template <int NA>
 __device__ __forceinline__ void fwd_cell(const PairRef& a, const AnchorRec* __restrict__ arec, int64_t k0, int g,
@@ -914,7 +914,8 @@ __global__ void __launch_bounds__(kWalkBlock) k_pair_fwd_cell(PairRef a, const i
     case 1: fwd_cell<1>(a, arec, k0, g, cx, cy, out, count); break;
     case 2: fwd_cell<2>(a, arec, k0, g, cx, cy, out, count); break;
     case 3: fwd_cell<3>(a, arec, k0, g, cx, cy, out, count); break;
-    default: fwd_cell<4>(a, arec, k0, g, cx, cy, out, count); break;
+    case 4: fwd_cell<4>(a, arec, k0, g, cx, cy, out, count); break;
+    default: fwd_cell<5>(a, arec, k0, g, cx, cy, out, count); break;
   }
 }
 
