@@ -317,7 +317,7 @@ int atl_ats_pair_bwd(const float* gS, const float* src_y, const float* src_v, co
  * contents on entry ignored, and serves either call.  Both bin the anchors by cell first.
  * atl_ats_pair_fwd_ws: the same out and count as atl_ats_pair_fwd, one wave per item of up to five anchors of
  * one cell, which walks the cell's 3 x 3 neighbourhood once for all of them.  atl_ats_pair_bwd_ws, source-centric: each chunk of 64 plan entries
- * of a run of four cells of a row gathers over the binned anchors (gS != 0) around it and adds every entry's
+ * of a run of six cells of a row gathers over the binned anchors (gS != 0) around it and adds every entry's
  * sum to gv once (two atomics per entry instead of two per pair); the same visited pairs and terms as
  * atl_ats_pair_bwd, gv (N,2) accumulated.  A workspace of atl_ats_pair_bwd_ws_bytes(E, ncell, M, GW, N, S)
  * bytes (the same regions, then N * S float2) lets the backward write each entry's sum to its own

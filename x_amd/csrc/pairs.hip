@@ -926,8 +926,8 @@ __global__ void __launch_bounds__(kWalkBlock) k_pair_fwd_cell(PairRef a, const i
 // iff |c - c'| <= 1 in both coordinates of the same plane (the column test is explicit: the unit's anchors
 // span kSegCells + 2 columns), the reference's neighbourhood seen from the record's side, and the tests are
 // the same, so the visited pairs are the reference's.
-constexpr int kSegCells = 4;       // source cells of a row per unit (~4 x 16 records at the 1M-event density)
-constexpr int kGatherWaves = 4;    // waves per workgroup, each on its own item
+constexpr int kSegCells = 6;       // source cells of a row per unit (~6 x 19 records at the 1M-event density)
+constexpr int kGatherWaves = 1;    // waves per workgroup, each on its own item
 constexpr int kXcds = 8, kXcdRun = 64;
 constexpr int kNoCol = -(1 << 29); // column of a padding slot: never within one of a record's column
 
