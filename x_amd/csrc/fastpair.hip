@@ -1529,7 +1529,7 @@ struct FlowGeo {
 
 constexpr int kAdjBlock = 256;
 constexpr int kAdjT = 16;                        // window of base nodes
-constexpr int kAdjItems = 4;
+constexpr int kAdjItems = 2;
 constexpr int kAdjChunk = kAdjBlock * kAdjItems; // records per chunk (one workgroup)
 constexpr int kAdjListBlock = 1024;
 constexpr int kAdjMaxSlices = 64;
